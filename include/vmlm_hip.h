@@ -1,0 +1,271 @@
+/*
+ * vmlm_hip.h -- C ABI of libvmlm_hip.so, the MI355X (gfx950) backend for the
+ * inference hot path of VMLM (shouzugzs-AI/Sparrow).
+ *
+ * Plain C: pointers, sizes, status codes. No HIP or torch types cross this
+ * boundary (streams travel as `void *`, a hipStream_t; NULL = the library's
+ * own stream).
+ *
+ * Three layers:
+ *  1. vmlm_*        Host-pointer kernels with the exact parameter lists of the
+ *                   reference's vmlm-ops functions (cited per entry). They
+ *                   copy in, run on the GPU, copy out and synchronise: a
+ *                   drop-in for the Rust FFI crate that replaces
+ *                   `vmlm_ops::kernels::*`.
+ *  2. vmlm_hip_*    Device-pointer variants (same arguments + stream), async.
+ *  3. vmlm_decoder_*, vmlm_b1_stack_*
+ *                   Device-resident sessions for the MiniCPM-shaped decoder
+ *                   program (tools/p12_build_minicpm.py, p14_gen_build.py)
+ *                   and the B1 layer stack (models/src/b1.rs:108-150).
+ *
+ * Error convention. The reference kernels never validate; the interpreter
+ * validates and exits the process (core/src/interp.rs:2357-2376). Here every
+ * entry point validates and returns a status code equal to the reference's
+ * exit code, with a message from vmlm_hip_last_error():
+ *   0 ok, 2 device/runtime failure, 5 unimplemented, 9 guard violation.
+ * All entry points are thread-safe; host-pointer calls serialise.
+ */
+#ifndef VMLM_HIP_H
+#define VMLM_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VMLM_OK 0
+#define VMLM_ERR_DEVICE 2
+#define VMLM_ERR_UNIMPL 5
+#define VMLM_ERR_GUARD 9
+
+/* Activation kinds and elementwise opcodes: core/src/format.rs:98-103,
+ * tensor/src/act_op.rs:9-12 (same numeric values). */
+#define VMLM_ACT_RELU 0
+#define VMLM_ACT_GELU 1
+#define VMLM_ACT_SILU 2
+#define VMLM_ACT_SIGMOID 3
+#define VMLM_ACT_TANH 4
+#define VMLM_ACT_RELU2 5
+#define VMLM_OP_EWADD 20
+#define VMLM_OP_EWMUL 21
+#define VMLM_OP_EWSUB 22
+#define VMLM_OP_EWDIV 23
+
+/* ---------------------------------------------------------------- library */
+int vmlm_hip_init(int device);         /* optional; first call does it */
+const char *vmlm_hip_last_error(void); /* message of the last non-zero status */
+const char *vmlm_hip_version(void);
+int vmlm_hip_sync(void);               /* wait for the library stream */
+int vmlm_hip_malloc(void **dptr, size_t bytes);
+int vmlm_hip_free(void *dptr);
+int vmlm_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int vmlm_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int vmlm_hip_memset(void *dptr, int value, size_t bytes);
+/* Event timing on a stream (NULL = library stream): returns an opaque id. */
+int vmlm_hip_event_record(void *stream, int *event_id);
+int vmlm_hip_event_elapsed_ms(int start_id, int end_id, float *ms);
+int vmlm_hip_event_release_all(void);
+
+/* B1 connection block, field for field ops/src/conn.rs:8-53 SparseConnW
+ * (the Rust struct is not repr(C); the FFI shim fills this one). The GPU
+ * kernels read `w` and `src_u32`; `src` / `act` are not read. */
+typedef struct vmlm_sparse_conn_w {
+    size_t e;
+    size_t k0;
+    uint32_t layer;
+    uint32_t n_neurons;
+    float *w;
+    float *src;
+    uint32_t *src_u32;
+    float *act;
+} vmlm_sparse_conn_w;
+
+/* ================================================================ layer 1
+ * Host pointers, synchronous. Each replaces the vmlm-ops function cited. */
+
+/* ops/src/kernels.rs:1258 gemm_nt_int8(a,q,scale,c,m,n,k):
+ * C[m,n] = (A[m,k] . Q[n,k]^T) * scale[n], overwrite. */
+int vmlm_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c,
+                      size_t m, size_t n, size_t k);
+/* ops/src/kernels.rs:1202 gemm_nt_bf16(a,b,c,m,n,k): C = A . B^T, B bf16 [n,k]. */
+int vmlm_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
+                      size_t k);
+/* ops/src/kernels.rs:987 gemm_nt(a,b,c,m,n,k,acc): C (+)= A[m,k] . B[n,k]^T. */
+int vmlm_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                 bool acc);
+/* ops/src/kernels.rs:407 gemm(a,b,c,m,n,k,acc): C (+)= A[m,k] . B[k,n]. */
+int vmlm_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+              bool acc);
+/* ops/src/kernels.rs:1346 rmsnorm(dst,src,g,rows,cols,eps). */
+int vmlm_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
+                 float eps);
+/* ops/src/kernels.rs:1389 softmax(p,rows,cols,causal), in place. */
+int vmlm_softmax(float *p, size_t rows, size_t cols, bool causal);
+/* ops/src/kernels.rs:1146 act_avx2(dst,n,kind), in place. */
+int vmlm_act(float *dst, size_t n, uint16_t kind);
+/* ops/src/kernels.rs:1117 ew_op(dst,x,y,n,op). */
+int vmlm_ew_op(float *dst, const float *x, const float *y, size_t n, uint8_t op);
+/* core/src/interp.rs:1225-1235 OP_SCALE: dst = src * s. */
+int vmlm_scale(float *dst, const float *src, size_t n, float s);
+/* core/src/interp.rs:1159-1223 OP_ROPE over [rows, hd], positions pos0+row;
+ * dst may equal src. */
+int vmlm_rope(float *dst, const float *src, size_t rows, size_t hd, float theta,
+              uint16_t pos0);
+/* core/src/interp.rs:1351-1436 OP_EMB: one row of a bf16 / f32 table. */
+int vmlm_emb_bf16(float *dst, const uint16_t *table, size_t rows, size_t cols, float rowf);
+int vmlm_emb_f32(float *dst, const float *table, size_t rows, size_t cols, float rowf);
+/* core/src/interp.rs:1649-1681 OP_TOPK_IDX: argmax of row 0 as f32. */
+int vmlm_topk_idx(const float *src, size_t rows, size_t cols, float *dst);
+/* ops/src/b1_pure.rs:151 b1_forward(sc,x,y) -> macs. */
+int vmlm_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y, size_t *macs);
+/* ops/src/b1_pure.rs:271 b1_forward_t8(sc,xt,t8,n_tokens,yt) -> macs. */
+int vmlm_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
+                       size_t n_tokens, float *yt, size_t *macs);
+/* ops/src/kernels.rs:1881 transpose_t8_avx2(x,t,d,xt,t8). */
+int vmlm_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8);
+/* ops/src/kernels.rs:3307 transpose_t8_back_avx2(a,rows,cols,out,os,in_stride). */
+int vmlm_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out, size_t os,
+                           size_t in_stride);
+/* ops/src/kernels.rs:1017-1033 jit_gemm_nt(a,b,c,dims),
+ * dims = m | n<<16 | k<<32 | acc<<48. */
+int vmlm_jit_gemm_nt(const float *a, const float *b, float *c, uint64_t dims);
+
+/* Attention as tools/p12_build_minicpm.py:770-781 composes it (SLICE, ROPE,
+ * GEMM NT, SCALE, SOFTMAX causal, GEMM NN, WRITECOL), fused.
+ * q,k,v,out: [S, n_heads*head_dim] f32. */
+int vmlm_attention_prefill(const float *q, const float *k, const float *v, float *out,
+                           size_t S, size_t n_heads, size_t head_dim, float theta,
+                           uint16_t pos0, float scale, bool causal);
+/* One decode token (tools/p12_build_minicpm.py:941-967): rotate k_new at
+ * `pos` and append it with v_new to the caches ([n_heads][cap][head_dim]
+ * f32, updated in place), then attend q (rotated at pos) over [0, pos]. */
+int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new,
+                          float *kcache, float *vcache, float *out, size_t n_heads,
+                          size_t head_dim, size_t cap, size_t pos, float theta,
+                          float scale);
+
+/* ================================================================ layer 2
+ * Device pointers, asynchronous on `stream`. Same semantics as layer 1. */
+int vmlm_hip_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c,
+                          size_t m, size_t n, size_t k, void *stream);
+int vmlm_hip_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
+                          size_t k, void *stream);
+/* bf16 x bf16 -> f32 (the dense training shape): C = A[m,k] . B[n,k]^T. */
+int vmlm_hip_gemm_nt_bf16bf16(const uint16_t *a, const uint16_t *b, float *c, size_t m,
+                              size_t n, size_t k, void *stream);
+int vmlm_hip_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n,
+                     size_t k, bool acc, void *stream);
+int vmlm_hip_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                  bool acc, void *stream);
+int vmlm_hip_rmsnorm(float *dst, const float *src, const float *g, size_t rows,
+                     size_t cols, float eps, void *stream);
+int vmlm_hip_softmax(float *p, size_t rows, size_t cols, bool causal, void *stream);
+int vmlm_hip_act(float *dst, size_t n, uint16_t kind, void *stream);
+int vmlm_hip_ew_op(float *dst, const float *x, const float *y, size_t n, uint8_t op,
+                   void *stream);
+int vmlm_hip_scale(float *dst, const float *src, size_t n, float s, void *stream);
+int vmlm_hip_rope(float *dst, const float *src, size_t rows, size_t hd, float theta,
+                  uint16_t pos0, void *stream);
+/* Row index guards are checked on the device; a violation is reported by
+ * the next vmlm_hip_check_guards() as status 9. */
+int vmlm_hip_emb_bf16(float *dst, const uint16_t *table, size_t rows, size_t cols,
+                      const float *rowf, void *stream);
+int vmlm_hip_topk_idx(const float *src, size_t rows, size_t cols, float *dst, void *stream);
+int vmlm_hip_check_guards(void);
+int vmlm_hip_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y,
+                        size_t n_tokens, void *stream);
+int vmlm_hip_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
+                           size_t n_tokens, float *yt, void *stream);
+int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8,
+                          void *stream);
+int vmlm_hip_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out,
+                               size_t os, size_t in_stride, void *stream);
+int vmlm_hip_attention_prefill(const float *q, const float *k, const float *v, float *out,
+                               size_t S, size_t n_heads, size_t head_dim, float theta,
+                               uint16_t pos0, float scale, bool causal, void *stream);
+int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v_new,
+                              float *kcache, float *vcache, float *out, size_t n_heads,
+                              size_t head_dim, size_t cap, size_t pos, float theta,
+                              float scale, void *stream);
+
+/* ================================================================ layer 3 */
+
+/* MiniCPM-shaped decoder session (config: MHA, SiLU-gated MLP, int8 weights
+ * with per-output-row f32 scales, bf16 embedding and LM head). Weights and
+ * the f32 KV cache ([layer][seq][head][cap][head_dim]) live in HBM. */
+typedef struct vmlm_decoder_cfg {
+    uint32_t n_layers, hidden, n_heads, head_dim, inter, vocab;
+    uint32_t batch; /* independent sequences decoded together */
+    uint32_t cap;   /* KV capacity in positions */
+    float eps, theta, attn_scale;
+} vmlm_decoder_cfg;
+typedef struct vmlm_decoder vmlm_decoder;
+
+int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out);
+int vmlm_decoder_destroy(vmlm_decoder *dec);
+/* Host weights of one layer, [N,K] row-major, as the program's constants
+ * L{l}_{q,k,v,o,gate,up,down} with their _sc scales and the two norms. */
+int vmlm_decoder_load_layer(vmlm_decoder *dec, uint32_t layer, const int8_t *wq,
+                            const float *sq, const int8_t *wk, const float *sk,
+                            const int8_t *wv, const float *sv, const int8_t *wo,
+                            const float *so, const int8_t *wg, const float *sg,
+                            const int8_t *wu, const float *su, const int8_t *wd,
+                            const float *sd, const float *in_ln, const float *post_ln);
+int vmlm_decoder_load_globals(vmlm_decoder *dec, const uint16_t *embed,
+                              const uint16_t *lm_head, const float *final_norm);
+/* Prefill `S` prompt tokens per sequence (tokens [batch][S]); writes the
+ * greedy first token of each sequence (argmax of row S-1) and optionally the
+ * row-(S-1) logits [batch][vocab]. Resets the session position to S. */
+int vmlm_decoder_prefill(vmlm_decoder *dec, const int32_t *tokens, uint32_t S,
+                         int32_t *first_tokens, float *logits_last);
+/* `n_steps` greedy decode steps (p14_gen_build.py:470-560): each step feeds
+ * the previous argmax, appends to the KV cache and takes the argmax of the
+ * new logits. tokens_out [n_steps][batch] (optional), logits_last
+ * [batch][vocab] of the final step (optional). */
+int vmlm_decoder_decode(vmlm_decoder *dec, uint32_t n_steps, int32_t *tokens_out,
+                        float *logits_last);
+int vmlm_decoder_position(const vmlm_decoder *dec, uint32_t *pos);
+/* 1 = replay one captured HIP graph per step (default), 0 = launch eagerly. */
+int vmlm_decoder_set_graph(vmlm_decoder *dec, int enable);
+void *vmlm_decoder_stream(vmlm_decoder *dec);
+/* Times `iters` launches of one decode-step GEMV of every layer in turn
+ * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head) on the session stream;
+ * writes the mean per-launch duration (HIP events) and its algorithmic
+ * HBM bytes (weights + scales + activations in + outputs). */
+int vmlm_decoder_time_gemv(vmlm_decoder *dec, int which, uint32_t iters, float *avg_us,
+                           double *bytes_per_launch);
+
+/* B1 layer stack (models/src/b1.rs:108-150 with the t8 contract of
+ * ops/src/b1_pure.rs:271): y = act(gather-dot) per layer over source-major
+ * activations. act: VMLM_ACT_* or 0xFFFF for none. */
+int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers,
+                          const float *x, float *y, size_t n_tokens, uint16_t act,
+                          void *stream);
+
+/* The backend function table (sys/src/lib.rs:24-72 defines the reference's
+ * `#[repr(C)] Backend` as the cross-language backend form; this is the
+ * kernel-level table of this backend). */
+typedef struct vmlm_hip_backend_t {
+    const char *name;
+    int (*gemm_nt_int8)(const float *, const int8_t *, const float *, float *, size_t,
+                        size_t, size_t);
+    int (*gemm_nt_bf16)(const float *, const uint16_t *, float *, size_t, size_t, size_t);
+    int (*gemm_nt)(const float *, const float *, float *, size_t, size_t, size_t, bool);
+    int (*gemm)(const float *, const float *, float *, size_t, size_t, size_t, bool);
+    int (*rmsnorm)(float *, const float *, const float *, size_t, size_t, float);
+    int (*softmax)(float *, size_t, size_t, bool);
+    int (*act)(float *, size_t, uint16_t);
+    int (*ew_op)(float *, const float *, const float *, size_t, uint8_t);
+    int (*b1_forward)(const vmlm_sparse_conn_w *, const float *, float *, size_t *);
+    int (*b1_forward_t8)(const vmlm_sparse_conn_w *, const float *, size_t, size_t, float *,
+                         size_t *);
+} vmlm_hip_backend_t;
+const vmlm_hip_backend_t *vmlm_hip_backend(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

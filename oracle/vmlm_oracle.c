@@ -252,13 +252,60 @@ static inline float dot_int8(const float *ar, const int8_t *qr, size_t k) {
     return s;
 }
 
+/* Same per-element arithmetic as dot_int8 with the weight row converted to
+ * f32 once ((float)q is exact) and four activation rows sharing it. */
+static inline void dot_rowf_x4(const float *a0, const float *a1, const float *a2,
+                               const float *a3, const float *wf, size_t k, float out[4]) {
+    float c0[8] = {0}, c1[8] = {0}, c2[8] = {0}, c3[8] = {0};
+    size_t kk = 0;
+    for (; kk + 8 <= k; kk += 8)
+        for (int l = 0; l < 8; ++l) {
+            float w = wf[kk + l];
+            c0[l] = fmaf(a0[kk + l], w, c0[l]);
+            c1[l] = fmaf(a1[kk + l], w, c1[l]);
+            c2[l] = fmaf(a2[kk + l], w, c2[l]);
+            c3[l] = fmaf(a3[kk + l], w, c3[l]);
+        }
+    float s0 = fold8(c0), s1 = fold8(c1), s2 = fold8(c2), s3 = fold8(c3);
+    for (; kk < k; ++kk) {
+        s0 += a0[kk] * wf[kk];
+        s1 += a1[kk] * wf[kk];
+        s2 += a2[kk] * wf[kk];
+        s3 += a3[kk] * wf[kk];
+    }
+    out[0] = s0;
+    out[1] = s1;
+    out[2] = s2;
+    out[3] = s3;
+}
+
 void vo_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c,
                      size_t m, size_t n, size_t k) {
     long nn = (long)n;
+    if (m < 4) {
 #pragma omp parallel for schedule(static) num_threads(g_threads)
-    for (long j = 0; j < nn; ++j) {
-        const int8_t *qr = q + (size_t)j * k;
-        for (size_t i = 0; i < m; ++i) c[i * n + j] = dot_int8(a + i * k, qr, k) * scale[j];
+        for (long j = 0; j < nn; ++j) {
+            const int8_t *qr = q + (size_t)j * k;
+            for (size_t i = 0; i < m; ++i) c[i * n + j] = dot_int8(a + i * k, qr, k) * scale[j];
+        }
+        return;
+    }
+#pragma omp parallel num_threads(g_threads)
+    {
+        float *wf = malloc(k * sizeof(float));
+#pragma omp for schedule(static)
+        for (long j = 0; j < nn; ++j) {
+            const int8_t *qr = q + (size_t)j * k;
+            for (size_t p = 0; p < k; ++p) wf[p] = (float)qr[p];
+            size_t i = 0;
+            for (; i + 4 <= m; i += 4) {
+                float o[4];
+                dot_rowf_x4(a + i * k, a + (i + 1) * k, a + (i + 2) * k, a + (i + 3) * k, wf, k, o);
+                for (int r = 0; r < 4; ++r) c[(i + r) * n + j] = o[r] * scale[j];
+            }
+            for (; i < m; ++i) c[i * n + j] = dot_int8(a + i * k, qr, k) * scale[j];
+        }
+        free(wf);
     }
 }
 

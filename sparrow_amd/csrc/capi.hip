@@ -1,0 +1,820 @@
+// capi.hip -- the extern "C" boundary of libvmlm_hip.so (include/vmlm_hip.h).
+//
+// Layer 1 (vmlm_*): host pointers, exact vmlm-ops parameter lists; each call
+// stages its operands in stream-ordered device memory, runs, copies back and
+// synchronises (serialised by a mutex). Layer 2 (vmlm_hip_*): device pointers,
+// asynchronous. Both validate like the reference interpreter's guards and
+// return its exit codes instead of exiting.
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace vmlm {
+
+// ------------------------------------------------------------------ errors
+static thread_local char g_err[1024] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(VMLM_ERR_DEVICE, "HIP error %d (%s) in %s", (int)e, hipGetErrorString(e), what);
+}
+
+// ------------------------------------------------------------------ init
+static std::once_flag g_once;
+static int g_init_status = -1;
+static hipStream_t g_stream = nullptr;
+static int *g_guard = nullptr;
+static std::mutex g_host_mutex;
+static std::mutex g_event_mutex;
+static std::vector<hipEvent_t> g_events;
+
+static void do_init(int device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        g_init_status = fail(VMLM_ERR_DEVICE, "no HIP device available (%s)",
+                             e == hipSuccess ? "count 0" : hipGetErrorString(e));
+        return;
+    }
+    if ((e = hipSetDevice(device)) != hipSuccess) {
+        g_init_status = hip_fail(e, "hipSetDevice");
+        return;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) {
+        g_init_status = hip_fail(e, "hipGetDeviceProperties");
+        return;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_init_status = fail(VMLM_ERR_DEVICE, "libvmlm_hip is built for gfx950, device is %s",
+                             prop.gcnArchName);
+        return;
+    }
+    if ((e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking)) != hipSuccess) {
+        g_init_status = hip_fail(e, "hipStreamCreate");
+        return;
+    }
+    if ((e = hipMalloc(&g_guard, sizeof(int))) != hipSuccess ||
+        (e = hipMemset(g_guard, 0, sizeof(int))) != hipSuccess) {
+        g_init_status = hip_fail(e, "guard flag");
+        return;
+    }
+    g_init_status = VMLM_OK;
+}
+
+int ensure_init() {
+    std::call_once(g_once, do_init, 0);
+    if (g_init_status != VMLM_OK) return fail(VMLM_ERR_DEVICE, "%s", g_err[0] ? g_err : "init failed");
+    return VMLM_OK;
+}
+hipStream_t lib_stream() { return g_stream; }
+int *guard_flag_ptr() { return g_guard; }
+
+// ops/src/kernels.rs:240-255, host side
+float host_ln_f(float x) {
+    if (x <= 0.0f) return -88.0f;
+    uint32_t bits;
+    std::memcpy(&bits, &x, 4);
+    int e = (int)((bits >> 23) & 0xffu) - 127;
+    uint32_t mb = (bits & 0x007fffffu) | 0x3f800000u;
+    float m;
+    std::memcpy(&m, &mb, 4);
+    if (m > 1.4142136f) {
+        m *= 0.5f;
+        e += 1;
+    }
+    float t = (m - 1.0f) / (m + 1.0f);
+    float t2 = t * t;
+    float p = 2.0f * t * (1.0f + t2 * (0.33333334f + t2 * (0.2f + t2 * 0.14285715f)));
+    return p + (float)e * 0.69314718f;
+}
+
+// ------------------------------------------------------------------ staging
+// Stream-ordered device buffers freed when the scope ends (after the stream
+// work that uses them is enqueued).
+struct Stage {
+    hipStream_t st;
+    std::vector<void *> bufs;
+    int status = VMLM_OK;
+    explicit Stage(hipStream_t s) : st(s) {}
+    ~Stage() {
+        for (void *p : bufs) (void)hipFreeAsync(p, st);
+    }
+    template <typename T>
+    T *alloc(size_t count) {
+        if (count == 0) count = 1;
+        void *p = nullptr;
+        hipError_t e = hipMallocAsync(&p, count * sizeof(T), st);
+        if (e != hipSuccess) {
+            status = hip_fail(e, "hipMallocAsync");
+            return nullptr;
+        }
+        bufs.push_back(p);
+        return (T *)p;
+    }
+    template <typename T>
+    T *upload(const T *host, size_t count) {
+        T *d = alloc<T>(count);
+        if (!d) return nullptr;
+        if (count) {
+            hipError_t e = hipMemcpyAsync(d, host, count * sizeof(T), hipMemcpyHostToDevice, st);
+            if (e != hipSuccess) {
+                status = hip_fail(e, "upload");
+                return nullptr;
+            }
+        }
+        return d;
+    }
+};
+
+static int download(void *host, const void *dev, size_t bytes, hipStream_t st) {
+    if (bytes) VMLM_HIP_CHECK(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, st));
+    return VMLM_OK;
+}
+
+#define STAGE_OK(stg) \
+    do {              \
+        if ((stg).status) return (stg).status; \
+    } while (0)
+
+static inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// int8 / bf16 weight GEMM on device operands: C[m,n] = A[m,k] . W[n,k]^T (* scale).
+// Pads K to a multiple of 64 when needed, splits A into 3 bf16 terms, then the
+// GEMV kernel (m <= 16) or the tiled MFMA GEMM.
+static int q_matmul(const float *a, const void *W, bool wi8, const float *scale, float *c,
+                    size_t m, size_t n, size_t k, hipStream_t st) {
+    if (m == 0 || n == 0) return VMLM_OK;
+    const size_t esz = wi8 ? 1 : 2;
+    const size_t Kp = round_up(k == 0 ? 1 : k, 64);
+    Stage stg(st);
+    const void *Wd = W;
+    if (Kp != k || ((uintptr_t)W & 15)) {
+        uint8_t *wp = stg.alloc<uint8_t>(n * Kp * esz);
+        STAGE_OK(stg);
+        VMLM_HIP_CHECK(hipMemsetAsync(wp, 0, n * Kp * esz, st));
+        if (k) VMLM_HIP_CHECK(hipMemcpy2DAsync(wp, Kp * esz, W, k * esz, k * esz, n,
+                                               hipMemcpyDeviceToDevice, st));
+        Wd = wp;
+    }
+    const int T = 3;
+    uint16_t *terms = stg.alloc<uint16_t>((size_t)T * m * Kp);
+    STAGE_OK(stg);
+    int rc = launch_split_terms(a, k, (int)m, (int)k, T, terms, (int)Kp, st);
+    if (rc) return rc;
+    if (m > 16) {
+        GemmArgs g;
+        g.W = Wd;
+        g.w_int8 = wi8;
+        g.scale = scale;
+        g.A = terms;
+        g.T = T;
+        g.lda = (int)Kp;
+        g.M = (int)m;
+        g.N = (int)n;
+        g.K = (int)Kp;
+        g.C = c;
+        g.ldc = (int)n;
+        return launch_gemm(g, st);
+    }
+    GemvArgs g;
+    g.W = Wd;
+    g.w_int8 = wi8;
+    g.scale = scale;
+    g.A = terms;
+    g.T = T;
+    g.lda = (int)Kp;
+    g.M = (int)m;
+    g.N = (int)n;
+    g.K = (int)Kp;
+    g.Y = c;
+    g.ldy = (int)n;
+    return launch_gemv(g, st);
+}
+
+}  // namespace vmlm
+
+using namespace vmlm;
+
+#define INIT_OR_RETURN()              \
+    do {                              \
+        int _rc = ensure_init();      \
+        if (_rc) return _rc;          \
+    } while (0)
+
+#define HOST_CALL_BEGIN()                                 \
+    INIT_OR_RETURN();                                     \
+    std::lock_guard<std::mutex> _lk(g_host_mutex);        \
+    hipStream_t st = lib_stream()
+
+#define FINISH(st_)                                       \
+    do {                                                  \
+        VMLM_HIP_CHECK(hipStreamSynchronize(st_));        \
+        return vmlm_hip_check_guards();                   \
+    } while (0)
+
+extern "C" {
+
+// ================================================================ library
+int vmlm_hip_init(int device) {
+    std::call_once(g_once, do_init, device);
+    if (g_init_status != VMLM_OK) return fail(VMLM_ERR_DEVICE, "%s", g_err);
+    return VMLM_OK;
+}
+
+const char *vmlm_hip_last_error(void) { return g_err; }
+const char *vmlm_hip_version(void) { return "vmlm_hip 0.1 gfx950"; }
+
+int vmlm_hip_sync(void) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipStreamSynchronize(lib_stream()));
+    return VMLM_OK;
+}
+
+int vmlm_hip_malloc(void **dptr, size_t bytes) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipMalloc(dptr, bytes ? bytes : 1));
+    return VMLM_OK;
+}
+int vmlm_hip_free(void *dptr) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipFree(dptr));
+    return VMLM_OK;
+}
+int vmlm_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return VMLM_OK;
+}
+int vmlm_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipStreamSynchronize(lib_stream()));
+    VMLM_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return VMLM_OK;
+}
+int vmlm_hip_memset(void *dptr, int value, size_t bytes) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipMemset(dptr, value, bytes));
+    return VMLM_OK;
+}
+
+int vmlm_hip_event_record(void *stream, int *event_id) {
+    INIT_OR_RETURN();
+    hipEvent_t ev;
+    VMLM_HIP_CHECK(hipEventCreate(&ev));
+    VMLM_HIP_CHECK(hipEventRecord(ev, as_stream(stream)));
+    std::lock_guard<std::mutex> lk(g_event_mutex);
+    g_events.push_back(ev);
+    *event_id = (int)g_events.size() - 1;
+    return VMLM_OK;
+}
+int vmlm_hip_event_elapsed_ms(int a, int b, float *ms) {
+    INIT_OR_RETURN();
+    std::lock_guard<std::mutex> lk(g_event_mutex);
+    VMLM_GUARD(a >= 0 && b >= 0 && a < (int)g_events.size() && b < (int)g_events.size(),
+               "event id out of range");
+    VMLM_HIP_CHECK(hipEventSynchronize(g_events[b]));
+    VMLM_HIP_CHECK(hipEventElapsedTime(ms, g_events[a], g_events[b]));
+    return VMLM_OK;
+}
+int vmlm_hip_event_release_all(void) {
+    INIT_OR_RETURN();
+    std::lock_guard<std::mutex> lk(g_event_mutex);
+    for (auto &e : g_events) (void)hipEventDestroy(e);
+    g_events.clear();
+    return VMLM_OK;
+}
+
+int vmlm_hip_check_guards(void) {
+    INIT_OR_RETURN();
+    int v = 0;
+    VMLM_HIP_CHECK(hipMemcpy(&v, guard_flag_ptr(), sizeof(int), hipMemcpyDeviceToHost));
+    if (v) {
+        VMLM_HIP_CHECK(hipMemset(guard_flag_ptr(), 0, sizeof(int)));
+        return fail(VMLM_ERR_GUARD, "device guard tripped (code %d): row/source index out of range",
+                    v);
+    }
+    return VMLM_OK;
+}
+
+// ================================================================ layer 2
+int vmlm_hip_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c,
+                          size_t m, size_t n, size_t k, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(scale != nullptr, "int8 gemm: scale slot must be f32 (null)");
+    return q_matmul(a, q, true, scale, c, m, n, k, as_stream(stream));
+}
+int vmlm_hip_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
+                          size_t k, void *stream) {
+    INIT_OR_RETURN();
+    return q_matmul(a, b, false, nullptr, c, m, n, k, as_stream(stream));
+}
+int vmlm_hip_gemm_nt_bf16bf16(const uint16_t *a, const uint16_t *b, float *c, size_t m,
+                              size_t n, size_t k, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(k % 64 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0,
+               "bf16 x bf16 gemm: k %% 64 == 0 and 16-byte aligned operands required");
+    if (m <= 16) {
+        GemvArgs g;
+        g.W = b;
+        g.w_int8 = false;
+        g.A = a;
+        g.T = 1;
+        g.lda = (int)k;
+        g.M = (int)m;
+        g.N = (int)n;
+        g.K = (int)k;
+        g.Y = c;
+        g.ldy = (int)n;
+        return launch_gemv(g, as_stream(stream));
+    }
+    GemmArgs g;
+    g.W = b;
+    g.w_int8 = false;
+    g.A = a;
+    g.T = 1;
+    g.lda = (int)k;
+    g.M = (int)m;
+    g.N = (int)n;
+    g.K = (int)k;
+    g.C = c;
+    g.ldc = (int)n;
+    return launch_gemm(g, as_stream(stream));
+}
+int vmlm_hip_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                     bool acc, void *stream) {
+    INIT_OR_RETURN();
+    return launch_gemm_f32(a, b, c, m, n, k, acc, true, as_stream(stream));
+}
+int vmlm_hip_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                  bool acc, void *stream) {
+    INIT_OR_RETURN();
+    return launch_gemm_f32(a, b, c, m, n, k, acc, false, as_stream(stream));
+}
+int vmlm_hip_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
+                     float eps, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(cols > 0 || rows == 0, "RMSNORM: zero columns");
+    return launch_rmsnorm(dst, src, g, rows, cols, eps, nullptr, 0, 0, as_stream(stream));
+}
+int vmlm_hip_softmax(float *p, size_t rows, size_t cols, bool causal, void *stream) {
+    INIT_OR_RETURN();
+    return launch_softmax(p, rows, cols, causal, as_stream(stream));
+}
+int vmlm_hip_act(float *dst, size_t n, uint16_t kind, void *stream) {
+    INIT_OR_RETURN();
+    return launch_act(dst, n, kind, as_stream(stream));
+}
+int vmlm_hip_ew_op(float *dst, const float *x, const float *y, size_t n, uint8_t op,
+                   void *stream) {
+    INIT_OR_RETURN();
+    return launch_ew(dst, x, y, n, op, as_stream(stream));
+}
+int vmlm_hip_scale(float *dst, const float *src, size_t n, float s, void *stream) {
+    INIT_OR_RETURN();
+    return launch_scale(dst, src, n, s, as_stream(stream));
+}
+int vmlm_hip_rope(float *dst, const float *src, size_t rows, size_t hd, float theta,
+                  uint16_t pos0, void *stream) {
+    INIT_OR_RETURN();
+    return launch_rope(dst, src, rows, hd, hd, theta, (float)pos0, 1, as_stream(stream));
+}
+int vmlm_hip_emb_bf16(float *dst, const uint16_t *table, size_t rows, size_t cols,
+                      const float *rowf, void *stream) {
+    INIT_OR_RETURN();
+    return launch_emb_bf16(dst, cols, table, rows, cols, rowf, nullptr, 1, as_stream(stream));
+}
+int vmlm_hip_topk_idx(const float *src, size_t rows, size_t cols, float *dst, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(rows > 0 && cols > 0, "TOPK_IDX: src or dst slot has width 0");
+    return launch_argmax(src, 1, cols, cols, dst, nullptr, as_stream(stream));
+}
+
+static int check_conn(const vmlm_sparse_conn_w *sc) {
+    VMLM_GUARD(sc != nullptr, "B1: null SparseConnW");
+    VMLM_GUARD(sc->e == (size_t)sc->n_neurons * sc->k0,
+               "CONN_TRAIN: SparseConnW geometry inconsistent: e=%zu but n_neurons*k0=%zu",
+               sc->e, (size_t)sc->n_neurons * sc->k0);
+    VMLM_GUARD(sc->k0 <= 1024, "B1: k0 exceeds the safe stack bound k0=%zu bound=1024", sc->k0);
+    return VMLM_OK;
+}
+
+int vmlm_hip_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y,
+                        size_t n_tokens, void *stream) {
+    INIT_OR_RETURN();
+    int rc = check_conn(sc);
+    if (rc) return rc;
+    // x, y: source-major [n][n_tokens] (n_tokens == 1: a plain vector)
+    return launch_b1_forward(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, x, n_tokens,
+                             (int)n_tokens, y, 1, -1, as_stream(stream));
+}
+int vmlm_hip_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
+                           size_t n_tokens, float *yt, void *stream) {
+    INIT_OR_RETURN();
+    int rc = check_conn(sc);
+    if (rc) return rc;
+    VMLM_GUARD(t8 >= n_tokens, "B1_T8: row stride t8 < n_tokens");
+    return launch_b1_forward(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, xt, t8,
+                             (int)n_tokens, yt, 0, -1, as_stream(stream));
+}
+int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8,
+                          void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(t8 >= t, "transpose_t8: t8 < t");
+    return launch_transpose_t8(x, t, d, xt, t8, as_stream(stream));
+}
+int vmlm_hip_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out,
+                               size_t os, size_t in_stride, void *stream) {
+    INIT_OR_RETURN();
+    return launch_transpose_back(a, rows, cols, out, os, in_stride, as_stream(stream));
+}
+
+int vmlm_hip_attention_prefill(const float *q, const float *k, const float *v, float *out,
+                               size_t S, size_t n_heads, size_t head_dim, float theta,
+                               uint16_t pos0, float scale, bool causal, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(head_dim == 64, "attention: head_dim %zu unsupported (64 only)", head_dim);
+    VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
+    if (S == 0 || n_heads == 0) return VMLM_OK;
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    const size_t W = n_heads * head_dim;
+    float *qr = stg.alloc<float>(S * W), *kr = stg.alloc<float>(S * W);
+    STAGE_OK(stg);
+    int rc = launch_rope(qr, q, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
+    if (!rc) rc = launch_rope(kr, k, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
+    if (!rc) rc = launch_attention_prefill(qr, kr, v, out, (int)S, (int)n_heads, (int)W,
+                                           (int)W, scale, causal, st);
+    return rc;
+}
+
+int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v_new,
+                              float *kcache, float *vcache, float *out, size_t n_heads,
+                              size_t head_dim, size_t cap, size_t pos, float theta,
+                              float scale, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(head_dim == 64, "attention: head_dim %zu unsupported (64 only)", head_dim);
+    VMLM_GUARD(pos < cap, "WRITECOL: column %zu beyond cache capacity %zu", pos, cap);
+    VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    const int NS = (int)((pos + 1 + 63) / 64);
+    DecodeArgs a;
+    a.q = q;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.ldq = (int)(n_heads * head_dim);
+    a.kc = kcache;
+    a.vc = vcache;
+    a.cap = (int)cap;
+    a.H = (int)n_heads;
+    a.posp = nullptr;
+    a.pos = (int)pos;
+    a.step = -2.0f / (float)head_dim * host_ln_f(theta);
+    a.scale = scale;
+    a.part = stg.alloc<float>((size_t)n_heads * NS * 66);
+    a.NS = NS;
+    STAGE_OK(stg);
+    return launch_attention_decode(a, 1, out, (int)(n_heads * head_dim), nullptr, 0, 0, st);
+}
+
+// ================================================================ layer 1
+int vmlm_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c, size_t m,
+                      size_t n, size_t k) {
+    HOST_CALL_BEGIN();
+    VMLM_GUARD(scale != nullptr, "int8 gemm: scale slot must be f32 (null)");
+    if (m == 0 || n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *da = stg.upload(a, m * k);
+        int8_t *dq = stg.upload(q, n * k);
+        float *ds = stg.upload(scale, n);
+        float *dc = stg.alloc<float>(m * n);
+        STAGE_OK(stg);
+        int rc = q_matmul(da, dq, true, ds, dc, m, n, k, st);
+        if (rc) return rc;
+        rc = download(c, dc, m * n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
+                      size_t k) {
+    HOST_CALL_BEGIN();
+    if (m == 0 || n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *da = stg.upload(a, m * k);
+        uint16_t *db = stg.upload(b, n * k);
+        float *dc = stg.alloc<float>(m * n);
+        STAGE_OK(stg);
+        int rc = q_matmul(da, db, false, nullptr, dc, m, n, k, st);
+        if (rc) return rc;
+        rc = download(c, dc, m * n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+static int host_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                         bool acc, bool nt) {
+    HOST_CALL_BEGIN();
+    if (m == 0 || n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *da = stg.upload(a, m * k);
+        float *db = stg.upload(b, n * k);
+        float *dc = acc ? stg.upload((const float *)c, m * n) : stg.alloc<float>(m * n);
+        STAGE_OK(stg);
+        int rc = launch_gemm_f32(da, db, dc, m, n, k, acc, nt, st);
+        if (rc) return rc;
+        rc = download(c, dc, m * n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                 bool acc) {
+    return host_gemm_f32(a, b, c, m, n, k, acc, true);
+}
+int vmlm_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+              bool acc) {
+    return host_gemm_f32(a, b, c, m, n, k, acc, false);
+}
+
+int vmlm_jit_gemm_nt(const float *a, const float *b, float *c, uint64_t dims) {
+    size_t m = dims & 0xFFFF, n = (dims >> 16) & 0xFFFF, k = (dims >> 32) & 0xFFFF;
+    bool acc = ((dims >> 48) & 1) != 0;
+    return vmlm_gemm_nt(a, b, c, m, n, k, acc);
+}
+
+int vmlm_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
+                 float eps) {
+    HOST_CALL_BEGIN();
+    if (rows == 0) return VMLM_OK;
+    VMLM_GUARD(cols > 0, "RMSNORM: zero columns");
+    {
+        Stage stg(st);
+        float *ds = stg.upload(src, rows * cols);
+        float *dg = stg.upload(g, cols);
+        float *dd = stg.alloc<float>(rows * cols);
+        STAGE_OK(stg);
+        int rc = launch_rmsnorm(dd, ds, dg, rows, cols, eps, nullptr, 0, 0, st);
+        if (!rc) rc = download(dst, dd, rows * cols * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_softmax(float *p, size_t rows, size_t cols, bool causal) {
+    HOST_CALL_BEGIN();
+    if (rows == 0 || cols == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dp = stg.upload((const float *)p, rows * cols);
+        STAGE_OK(stg);
+        int rc = launch_softmax(dp, rows, cols, causal, st);
+        if (!rc) rc = download(p, dp, rows * cols * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_act(float *dst, size_t n, uint16_t kind) {
+    HOST_CALL_BEGIN();
+    if (n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dd = stg.upload((const float *)dst, n);
+        STAGE_OK(stg);
+        int rc = launch_act(dd, n, kind, st);
+        if (!rc) rc = download(dst, dd, n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_ew_op(float *dst, const float *x, const float *y, size_t n, uint8_t op) {
+    HOST_CALL_BEGIN();
+    if (n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dx = stg.upload(x, n), *dy = stg.upload(y, n), *dd = stg.alloc<float>(n);
+        STAGE_OK(stg);
+        int rc = launch_ew(dd, dx, dy, n, op, st);
+        if (!rc) rc = download(dst, dd, n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_scale(float *dst, const float *src, size_t n, float s) {
+    HOST_CALL_BEGIN();
+    if (n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *ds = stg.upload(src, n), *dd = stg.alloc<float>(n);
+        STAGE_OK(stg);
+        int rc = launch_scale(dd, ds, n, s, st);
+        if (!rc) rc = download(dst, dd, n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_rope(float *dst, const float *src, size_t rows, size_t hd, float theta,
+              uint16_t pos0) {
+    HOST_CALL_BEGIN();
+    VMLM_GUARD(hd >= 2 && (hd & 1) == 0, "ROPE: hd must be even >= 2");
+    VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
+    if (rows == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *ds = stg.upload(src, rows * hd), *dd = stg.alloc<float>(rows * hd);
+        STAGE_OK(stg);
+        int rc = launch_rope(dd, ds, rows, hd, hd, theta, (float)pos0, 1, st);
+        if (!rc) rc = download(dst, dd, rows * hd * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+static int emb_guard(float rowf, size_t rows, size_t *row) {
+    if (!(rowf >= 0.0f) || rowf >= (float)rows)
+        return fail(VMLM_ERR_GUARD, "EMB: row index out of range row=%g table_rows=%zu",
+                    (double)rowf, rows);
+    size_t r = (size_t)rowf;
+    if ((float)r != rowf)
+        return fail(VMLM_ERR_GUARD, "EMB: row index is not an integer row=%g", (double)rowf);
+    *row = r;
+    return VMLM_OK;
+}
+
+int vmlm_emb_bf16(float *dst, const uint16_t *table, size_t rows, size_t cols, float rowf) {
+    size_t row = 0;
+    int rc = emb_guard(rowf, rows, &row);
+    if (rc) return rc;
+    HOST_CALL_BEGIN();
+    {
+        Stage stg(st);
+        uint16_t *dt = stg.upload(table + row * cols, cols);
+        float *dd = stg.alloc<float>(cols);
+        int32_t zero = 0;
+        int32_t *di = stg.upload(&zero, 1);
+        STAGE_OK(stg);
+        rc = launch_emb_bf16(dd, cols, dt, 1, cols, nullptr, di, 1, st);
+        if (!rc) rc = download(dst, dd, cols * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_emb_f32(float *dst, const float *table, size_t rows, size_t cols, float rowf) {
+    size_t row = 0;
+    int rc = emb_guard(rowf, rows, &row);
+    if (rc) return rc;
+    std::memcpy(dst, table + row * cols, cols * sizeof(float));
+    return VMLM_OK;
+}
+
+int vmlm_topk_idx(const float *src, size_t rows, size_t cols, float *dst) {
+    VMLM_GUARD(rows > 0 && cols > 0, "TOPK_IDX: src or dst slot has width 0");
+    HOST_CALL_BEGIN();
+    {
+        Stage stg(st);
+        float *ds = stg.upload(src, cols), *dd = stg.alloc<float>(1);
+        STAGE_OK(stg);
+        int rc = launch_argmax(ds, 1, cols, cols, dd, nullptr, st);
+        if (!rc) rc = download(dst, dd, sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+static int host_b1(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8, size_t n_tokens,
+                   float *yt, size_t *macs, int mode) {
+    int rc = check_conn(sc);
+    if (rc) return rc;
+    const size_t n = sc->n_neurons, e = sc->e;
+    for (size_t t = 0; t < e; ++t)
+        VMLM_GUARD(sc->src_u32[t] < n, "B1: src_u32[%zu]=%u >= n_neurons=%zu", t, sc->src_u32[t],
+                   n);
+    HOST_CALL_BEGIN();
+    {
+        Stage stg(st);
+        float *dw = stg.upload(sc->w, e);
+        uint32_t *ds = stg.upload(sc->src_u32, e);
+        float *dx = stg.upload(xt, n * t8);
+        float *dy = stg.upload((const float *)yt, n * t8);
+        STAGE_OK(stg);
+        rc = launch_b1_forward(dw, ds, (int)n, (int)sc->k0, dx, t8, (int)n_tokens, dy, mode, -1,
+                               st);
+        if (!rc) rc = download(yt, dy, n * t8 * sizeof(float), st);
+        if (rc) return rc;
+    }
+    if (macs) *macs = n * sc->k0;
+    FINISH(st);
+}
+
+int vmlm_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y, size_t *macs) {
+    return host_b1(sc, x, 1, 1, y, macs, 1);
+}
+int vmlm_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
+                       size_t n_tokens, float *yt, size_t *macs) {
+    VMLM_GUARD(t8 >= n_tokens, "B1_T8: row stride t8 < n_tokens");
+    return host_b1(sc, xt, t8, n_tokens, yt, macs, 0);
+}
+
+int vmlm_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8) {
+    VMLM_GUARD(t8 >= t, "transpose_t8: t8 < t");
+    HOST_CALL_BEGIN();
+    {
+        Stage stg(st);
+        float *dx = stg.upload(x, t * d), *dxt = stg.alloc<float>(d * t8);
+        STAGE_OK(stg);
+        int rc = launch_transpose_t8(dx, t, d, dxt, t8, st);
+        if (!rc) rc = download(xt, dxt, d * t8 * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out, size_t os,
+                           size_t in_stride) {
+    VMLM_GUARD(os >= rows && in_stride >= cols, "transpose_t8_back: stride too small");
+    HOST_CALL_BEGIN();
+    if (rows == 0 || cols == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *da = stg.upload(a, rows * in_stride);
+        float *dout = stg.upload((const float *)out, cols * os);
+        STAGE_OK(stg);
+        int rc = launch_transpose_back(da, rows, cols, dout, os, in_stride, st);
+        if (!rc) rc = download(out, dout, cols * os * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_attention_prefill(const float *q, const float *k, const float *v, float *out,
+                           size_t S, size_t n_heads, size_t head_dim, float theta,
+                           uint16_t pos0, float scale, bool causal) {
+    HOST_CALL_BEGIN();
+    const size_t n = S * n_heads * head_dim;
+    if (n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dq = stg.upload(q, n), *dk = stg.upload(k, n), *dv = stg.upload(v, n);
+        float *dout = stg.alloc<float>(n);
+        STAGE_OK(stg);
+        int rc = vmlm_hip_attention_prefill(dq, dk, dv, dout, S, n_heads, head_dim, theta,
+                                            pos0, scale, causal, st);
+        if (!rc) rc = download(out, dout, n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new,
+                          float *kcache, float *vcache, float *out, size_t n_heads,
+                          size_t head_dim, size_t cap, size_t pos, float theta, float scale) {
+    HOST_CALL_BEGIN();
+    const size_t w = n_heads * head_dim, cn = n_heads * cap * head_dim;
+    {
+        Stage stg(st);
+        float *dq = stg.upload(q, w), *dk = stg.upload(k_new, w), *dv = stg.upload(v_new, w);
+        float *dkc = stg.upload((const float *)kcache, cn);
+        float *dvc = stg.upload((const float *)vcache, cn);
+        float *dout = stg.alloc<float>(w);
+        STAGE_OK(stg);
+        int rc = vmlm_hip_attention_decode(dq, dk, dv, dkc, dvc, dout, n_heads, head_dim, cap,
+                                           pos, theta, scale, st);
+        if (!rc) rc = download(out, dout, w * sizeof(float), st);
+        if (!rc) rc = download(kcache, dkc, cn * sizeof(float), st);
+        if (!rc) rc = download(vcache, dvc, cn * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+// ================================================================ backend table
+static const vmlm_hip_backend_t g_backend = {
+    "hip_gfx950",      vmlm_gemm_nt_int8, vmlm_gemm_nt_bf16, vmlm_gemm_nt,
+    vmlm_gemm,         vmlm_rmsnorm,      vmlm_softmax,      vmlm_act,
+    vmlm_ew_op,        vmlm_b1_forward,   vmlm_b1_forward_t8,
+};
+const vmlm_hip_backend_t *vmlm_hip_backend(void) { return &g_backend; }
+
+}  // extern "C"

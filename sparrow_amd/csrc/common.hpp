@@ -1,0 +1,230 @@
+// common.hpp -- shared definitions of libvmlm_hip.so (gfx950 only).
+//
+// Everything here compiles with -ffp-contract=off: device float expressions
+// round after every operation exactly like the reference's Rust code, and
+// FMAs appear only where written as __builtin_fmaf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/vmlm_hip.h"
+
+namespace vmlm {
+
+// ------------------------------------------------------------------ status
+// Sets the thread's last-error message and returns `code`.
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+#define VMLM_HIP_CHECK(expr)                                   \
+    do {                                                       \
+        hipError_t _e = (expr);                                \
+        if (_e != hipSuccess) return ::vmlm::hip_fail(_e, #expr); \
+    } while (0)
+
+#define VMLM_GUARD(cond, ...)                                  \
+    do {                                                       \
+        if (!(cond)) return ::vmlm::fail(VMLM_ERR_GUARD, __VA_ARGS__); \
+    } while (0)
+
+// Library stream (created on first use, default priority) and device init.
+int ensure_init();
+hipStream_t lib_stream();
+inline hipStream_t as_stream(void *s) { return s ? (hipStream_t)s : lib_stream(); }
+
+// Device-side guard flag (set by kernels that validate indices on the GPU).
+int *guard_flag_ptr();
+
+// ------------------------------------------------------------------ types
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+// ------------------------------------------------------------------ bf16
+// bf16 bits of f32, round to nearest even (tensor/src/dtype.rs:40-46).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
+    uint32_t u = __float_as_uint(v);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+// Splits f32 x into up to three bf16 terms hi + mid + lo whose sum equals x
+// to within 2^-24 |x| (each residual is exact in f32). Products of a bf16
+// term with a bf16 (or small-integer) weight are exact in f32, so an MFMA
+// over the terms reproduces f32 x . w up to the order of f32 accumulation.
+template <int T>
+__device__ __forceinline__ void split_bf16(float x, uint32_t (&t)[T]) {
+    float r = x;
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        t[i] = bf16_rne_bits(r);
+        r = r - bf16_bits_to_f32(t[i]);
+    }
+}
+
+// 16 int8 (one 16-byte load) -> 16 bf16 in two 16-byte vectors, element order
+// kept. Exact: |q| <= 128 has at most 8 significant bits; the bf16 is the high
+// half of the f32 conversion, packed two per dword with v_perm_b32.
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+__device__ __forceinline__ void i8x16_to_bf16(u32x4 w, u32x4 &lo, u32x4 &hi) {
+    uint32_t d[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t x = w[q];
+        const float f0 = (float)(int)(int8_t)(x & 0xffu);
+        const float f1 = (float)(int)(int8_t)((x >> 8) & 0xffu);
+        const float f2 = (float)(int)(int8_t)((x >> 16) & 0xffu);
+        const float f3 = (float)(int)(int8_t)(x >> 24);
+        d[2 * q] = pack_hi16(f0, f1);
+        d[2 * q + 1] = pack_hi16(f2, f3);
+    }
+    lo = u32x4{d[0], d[1], d[2], d[3]};
+    hi = u32x4{d[4], d[5], d[6], d[7]};
+}
+
+// ------------------------------------------------------------------ math
+// Device ports of the reference's scalar math, operation for operation, so
+// that elementwise kernels are bitwise equal to the CPU kernels.
+
+// sys/src/math/mod.rs:68-71
+__device__ __forceinline__ float round_f32(float v) {
+    const float MAGIC = 12582912.0f;
+    return (v + MAGIC) - MAGIC;
+}
+
+// sys/src/math/mod.rs:74-140
+__device__ __forceinline__ float exp_f(float x) {
+    x = x < -88.0f ? -88.0f : (x > 88.0f ? 88.0f : x);
+    const float LOG2E = 1.4426950f;
+    const float LN2_HI = 0.69314575f;
+    const float LN2_LO = 1.4286068e-6f;
+    float n = round_f32(x * LOG2E);
+    float r = (x - n * LN2_HI) - n * LN2_LO;
+    float r2 = r * r;
+    float p = 1.9875691e-4f;
+    p = p * r + 1.3981999e-3f;
+    p = p * r + 8.333452e-3f;
+    p = p * r + 4.1665797e-2f;
+    p = p * r + 1.6666665e-1f;
+    p = p * r + 0.5f;
+    p = p * r2 + r + 1.0f;
+    int ni = (int)n;
+    if (ni >= -126) return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+    if (ni >= -149) return p * __uint_as_float(1u << (ni + 149));
+    return 0.0f;
+}
+
+// ops/src/kernels.rs:240-255
+__device__ __forceinline__ float ln_f(float x) {
+    if (x <= 0.0f) return -88.0f;
+    uint32_t bits = __float_as_uint(x);
+    int e = (int)((bits >> 23) & 0xffu) - 127;
+    float m = __uint_as_float((bits & 0x007fffffu) | 0x3f800000u);
+    if (m > 1.4142136f) {
+        m *= 0.5f;
+        e += 1;
+    }
+    float t = (m - 1.0f) / (m + 1.0f);
+    float t2 = t * t;
+    float p = 2.0f * t * (1.0f + t2 * (0.33333334f + t2 * (0.2f + t2 * 0.14285715f)));
+    return p + (float)e * 0.69314718f;
+}
+
+// ops/src/kernels.rs:113-232 (reduction, quadrant select, polynomials)
+__device__ __forceinline__ void sincos_f(float x, float *s_out, float *c_out) {
+    const float PI2_HI = 1.57079637f;
+    const float PI2_MID = -4.3711388e-8f;
+    const float PI2_LO = -1.7151245e-15f;
+    const float TWO_OVER_PI = 0.6366198f;
+    x = x > 1.0e7f ? 1.0e7f : (x < -1.0e7f ? -1.0e7f : x);
+    float n = round_f32(x * TWO_OVER_PI);
+    float r = ((x - n * PI2_HI) - n * PI2_MID) - n * PI2_LO;
+    float r2 = r * r;
+    float q = 2.7269829e-6f;
+    q = q * r2 - 1.9840246e-4f;
+    q = q * r2 + 8.3333322e-3f;
+    q = q * r2 - 1.6666667e-1f;
+    float sp = r * (1.0f + r2 * q);
+    float p = 2.4410573e-5f;
+    p = p * r2 - 1.3886977e-3f;
+    p = p * r2 + 4.1666630e-2f;
+    p = p * r2 - 5.0e-1f;
+    float cp = r2 * p + 1.0f;
+    switch (((int)n) & 3) {
+    case 0: *s_out = sp; *c_out = cp; break;
+    case 1: *s_out = cp; *c_out = -sp; break;
+    case 2: *s_out = -sp; *c_out = -cp; break;
+    default: *s_out = -cp; *c_out = sp; break;
+    }
+}
+
+// ops/src/kernels.rs:216-223
+__device__ __forceinline__ float floor_f(float x) {
+    float t = (float)(long long)x;
+    return t > x ? t - 1.0f : t;
+}
+
+// ops/src/kernels.rs:58-67
+__device__ __forceinline__ float tanh_f(float x) {
+    if (x > 15.0f) return 1.0f;
+    if (x < -15.0f) return -1.0f;
+    float e = exp_f(2.0f * x);
+    return (e - 1.0f) / (e + 1.0f);
+}
+
+// ops/src/kernels.rs:27-52
+__device__ __forceinline__ float act_scalar(float x, int kind) {
+    switch (kind) {
+    case VMLM_ACT_RELU: return x > 0.0f ? x : 0.0f;
+    case VMLM_ACT_GELU:
+        return 0.5f * x * (1.0f + tanh_f(0.7978846f * (x + 0.044715f * x * x * x)));
+    case VMLM_ACT_SILU: return x / (1.0f + exp_f(-x));
+    case VMLM_ACT_SIGMOID: return 1.0f / (1.0f + exp_f(-x));
+    case VMLM_ACT_TANH: return tanh_f(x);
+    case VMLM_ACT_RELU2: {
+        float r = x > 0.0f ? x : 0.0f;
+        return r * r;
+    }
+    default: return x;
+    }
+}
+
+// core/src/interp.rs:1183-1221: one RoPE pair at position `pos`, component i.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float pos, int i, float step,
+                                          float *y1, float *y2) {
+    const float TWO_PI = 6.2831855f;
+    float inv = exp_f((float)i * step);
+    float period = TWO_PI / inv;
+    float pr = period >= 1.0e6f ? pos : pos - period * floor_f(pos / period);
+    float ang = pr * inv;
+    float si, co;
+    sincos_f(ang, &si, &co);
+    *y1 = x1 * co - x2 * si;
+    *y2 = x1 * si + x2 * co;
+}
+
+// ------------------------------------------------------------------ wave ops
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace vmlm

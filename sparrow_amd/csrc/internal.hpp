@@ -1,0 +1,104 @@
+// internal.hpp -- launchers shared between translation units of libvmlm_hip.so.
+#pragma once
+
+#include "common.hpp"
+
+namespace vmlm {
+
+// Host restatement of ln_f (ops/src/kernels.rs:240-255) for RoPE's step
+// constant -2/hd * ln_f(theta), computed once per launch.
+float host_ln_f(float x);
+
+// Activation operand of the MFMA GEMV / GEMM: T planes of bf16 bits
+// [T][rows][ld] (ld a multiple of 64, zero padded) whose sum is the f32
+// activation (see split_bf16).
+int launch_split_terms(const float *x, size_t ldx, int rows, int K, int T, uint16_t *out,
+                       int ld_out, hipStream_t st);
+
+enum GemvEpi {
+    EPI_STORE = 0,    // Y = acc * scale
+    EPI_RESIDUAL = 1, // Y = R + acc * scale              (OP_GEMM then OP_EWADD)
+    EPI_SILU_MUL = 2, // pairs of 16-row tiles (gate, up): Y = silu(g) * u and its terms
+};
+
+struct GemvArgs {
+    const void *W = nullptr; // [N][K] int8 or bf16 bits, rows 16-byte aligned
+    bool w_int8 = true;
+    const float *scale = nullptr; // [N] per-row scale (int8) or null
+    const uint16_t *A = nullptr;  // terms [T][.][lda], plane stride a_tstride
+    int T = 3;
+    int lda = 0;
+    size_t a_tstride = 0;    // elements between term planes (0: M * lda)
+    int M = 1, N = 0, K = 0; // K % 64 == 0, M <= 16
+    float *Y = nullptr;
+    int ldy = 0;
+    const float *R = nullptr; // residual (EPI_RESIDUAL), [M][ldr]
+    int ldr = 0;
+    int epi = EPI_STORE;
+    uint16_t *Aout = nullptr; // EPI_SILU_MUL: terms of Y, [T][M][ldaout]
+    int ldaout = 0;
+    int Tout = 3;
+};
+int launch_gemv(const GemvArgs &a, hipStream_t st);
+
+// Tiled MFMA GEMM for M > 16: C[M,N] = A[M,K] . W[N,K]^T (* scale[n]).
+struct GemmArgs {
+    const void *W = nullptr;
+    bool w_int8 = true;
+    const float *scale = nullptr;
+    const uint16_t *A = nullptr; // terms [T][M][lda]
+    int T = 3;
+    int lda = 0;
+    int M = 0, N = 0, K = 0; // K % 64 == 0
+    float *C = nullptr;
+    int ldc = 0;
+};
+int launch_gemm(const GemmArgs &a, hipStream_t st);
+
+// f32 GEMMs (NT and NN) with optional accumulate.
+int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                    bool acc, bool b_is_nt, hipStream_t st);
+
+// Row / elementwise ops.
+int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
+                   float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st);
+int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t st);
+int launch_act(float *dst, size_t n, int kind, hipStream_t st);
+int launch_ew(float *dst, const float *x, const float *y, size_t n, int op, hipStream_t st);
+int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st);
+// RoPE over `rows` positions (pos0 + row) x `heads` heads of width hd,
+// head h at column h*hd of a row of stride ld.
+int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld, float theta,
+                float pos0, int heads, hipStream_t st);
+int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
+                    const float *rowf, const int32_t *rowi, int n, hipStream_t st);
+int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float *dst_f,
+                  int32_t *dst_i, hipStream_t st);
+
+// Attention (head_dim 64). Prefill takes rotated Q and K.
+int launch_attention_prefill(const float *qrot, const float *krot, const float *v, float *out,
+                             int S, int H, int ld, int ldo, float scale, bool causal,
+                             hipStream_t st);
+struct DecodeArgs {
+    const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
+    int ldq;
+    float *kc, *vc;  // [B][H][cap][64]
+    int cap, H;
+    const int *posp;  // device position (graph replay) or null -> `pos`
+    int pos;
+    float step, scale;  // RoPE step -2/64*ln_f(theta); score scale
+    float *part;        // [B][H][NS][66] split partials
+    int NS;             // splits of 64 positions (>= ceil((pos+1)/64))
+};
+int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
+                            int T, int ldt, hipStream_t st);
+
+// B1 gather forward over source-major activations.
+int launch_b1_forward(const float *w, const uint32_t *src, int n, int k0, const float *xt,
+                      size_t t8, int n_tokens, float *yt, int mode, int act, hipStream_t st);
+int launch_transpose_t8(const float *x, size_t T, size_t d, float *xt, size_t t8,
+                        hipStream_t st);
+int launch_transpose_back(const float *a, size_t rows, size_t cols, float *out, size_t os,
+                          size_t in_stride, hipStream_t st);
+
+}  // namespace vmlm

@@ -1,0 +1,283 @@
+// k_rowops.hip -- row and elementwise kernels of the VM opcode set.
+//
+// Elementwise kernels (act, ew_op, scale, RoPE, EMB) perform the same
+// operations in the same order as the reference and are bitwise equal to
+// it. Row reductions (RMSNORM sum of squares, SOFTMAX sum) are tree sums
+// across a workgroup instead of the reference's left-to-right loop; the max
+// and every per-element operation remain exact.
+#include "internal.hpp"
+
+namespace vmlm {
+
+// Block-wide sum for 256 threads (4 wavefronts).
+__device__ __forceinline__ float block_sum256(float v, float *sh) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) sh[w] = v;
+    __syncthreads();
+    float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ float block_max256(float v, float *sh) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) sh[w] = v;
+    __syncthreads();
+    float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return r;
+}
+
+// ops/src/kernels.rs:1346-1368 -- y = (x * inv) * g, inv = 1/sqrt(mean(x^2)+eps).
+// Optionally also writes the T bf16 terms of y (GEMV activation operand).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ dst,
+                                                      const float *__restrict__ src,
+                                                      const float *__restrict__ g, int cols,
+                                                      float eps, uint16_t *__restrict__ terms,
+                                                      int T, int ld_terms, int rows) {
+    __shared__ float sh[4];
+    const int row = blockIdx.x;
+    const float *p = src + (size_t)row * cols;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += 256) ss += p[i] * p[i];
+    ss = block_sum256(ss, sh);
+    ss = ss / (float)cols;
+    const float inv = 1.0f / sqrtf(ss + eps);
+    float *q = dst ? dst + (size_t)row * cols : nullptr;
+    for (int i = threadIdx.x; i < cols; i += 256) {
+        float y = p[i] * inv * g[i];
+        if (q) q[i] = y;
+        if (terms) {
+            for (int t = 0; t < T; ++t) {
+                uint32_t h = bf16_rne_bits(y);
+                y = y - bf16_bits_to_f32(h);
+                terms[((size_t)t * rows + row) * ld_terms + i] = (uint16_t)h;
+            }
+        }
+    }
+    if (terms) {  // zero the K padding of the terms
+        for (int i = cols + threadIdx.x; i < ld_terms; i += 256)
+            for (int t = 0; t < T; ++t) terms[((size_t)t * rows + row) * ld_terms + i] = 0;
+    }
+}
+
+int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
+                   float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st) {
+    if (rows == 0) return VMLM_OK;
+    rmsnorm_kernel<<<(unsigned)rows, 256, 0, st>>>(dst, src, g, (int)cols, eps, terms, T,
+                                                   ld_terms, (int)rows);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// ops/src/kernels.rs:1388-1414 -- max, exp_f(x-max), sum, * (1/sum), causal tail 0.
+__global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ p, int cols,
+                                                      int causal) {
+    __shared__ float sh[4];
+    const int r = blockIdx.x;
+    float *row = p + (size_t)r * cols;
+    int lim = causal ? (r + 1 < cols ? r + 1 : cols) : cols;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < lim; i += 256) mx = fmaxf(mx, row[i]);
+    mx = block_max256(mx, sh);
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < lim; i += 256) {
+        float e = exp_f(row[i] - mx);
+        row[i] = e;
+        s += e;
+    }
+    s = block_sum256(s, sh);
+    const float inv = 1.0f / s;
+    for (int i = threadIdx.x; i < lim; i += 256) row[i] *= inv;
+    for (int i = lim + threadIdx.x; i < cols; i += 256) row[i] = 0.0f;
+}
+
+int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t st) {
+    if (rows == 0 || cols == 0) return VMLM_OK;
+    softmax_kernel<<<(unsigned)rows, 256, 0, st>>>(p, (int)cols, causal ? 1 : 0);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// ops/src/kernels.rs:1144-1167 -- RELU: maxps(v,0) on the 8-wide body
+// (returns 0 unless v > 0), `if x < 0 {0}` on the tail; others act_scalar.
+__global__ void act_kernel(float *__restrict__ d, size_t n, int kind) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float x = d[i];
+    if (kind == VMLM_ACT_RELU) {
+        size_t n8 = n / 8 * 8;
+        if (i < n8) {
+            d[i] = x > 0.0f ? x : 0.0f;
+        } else if (x < 0.0f) {
+            d[i] = 0.0f;
+        }
+        return;
+    }
+    d[i] = act_scalar(x, kind);
+}
+
+int launch_act(float *dst, size_t n, int kind, hipStream_t st) {
+    if (n == 0) return VMLM_OK;
+    act_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, n, kind);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// ops/src/kernels.rs:1115-1142
+__global__ void ew_kernel(float *__restrict__ d, const float *__restrict__ x,
+                          const float *__restrict__ y, size_t n, int op) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float a = x[i], b = y[i];
+    float r;
+    switch (op) {
+    case VMLM_OP_EWADD: r = a + b; break;
+    case VMLM_OP_EWMUL: r = a * b; break;
+    case VMLM_OP_EWSUB: r = a - b; break;
+    default: r = a / b; break;
+    }
+    d[i] = r;
+}
+
+int launch_ew(float *dst, const float *x, const float *y, size_t n, int op, hipStream_t st) {
+    if (n == 0) return VMLM_OK;
+    ew_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, x, y, n, op);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// core/src/interp.rs:1225-1235
+__global__ void scale_kernel(float *__restrict__ d, const float *__restrict__ s, size_t n,
+                             float a) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = s[i] * a;
+}
+
+int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st) {
+    if (n == 0) return VMLM_OK;
+    scale_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, src, n, s);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// core/src/interp.rs:1159-1223 -- one thread per (row, pair).
+__global__ void rope_kernel(float *__restrict__ dst, const float *__restrict__ src, int rows,
+                            int hd, size_t ld, float step, float pos0, int heads) {
+    const int half = hd / 2;
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * heads * half) return;
+    const int i = (int)(idx % half);
+    const int h = (int)((idx / half) % heads);
+    const int row = (int)(idx / ((size_t)half * heads));
+    const float pos = pos0 + (float)row;
+    const float *sr = src + (size_t)row * ld + (size_t)h * hd;
+    float *dr = dst + (size_t)row * ld + (size_t)h * hd;
+    float y1, y2;
+    rope_pair(sr[i], sr[i + half], pos, i, step, &y1, &y2);
+    dr[i] = y1;
+    dr[i + half] = y2;
+}
+
+int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld, float theta,
+                float pos0, int heads, hipStream_t st) {
+    VMLM_GUARD(hd >= 2 && (hd & 1) == 0, "ROPE: hd must be even >= 2 (hd=%zu)", hd);
+    VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
+    if (rows == 0) return VMLM_OK;
+    // step = -2/hd * ln_f(theta), evaluated on the host with the same operations
+    float step = -2.0f / (float)hd * host_ln_f(theta);
+    size_t n = rows * heads * (hd / 2);
+    rope_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, src, (int)rows, (int)hd, ld, step, pos0,
+                                              heads);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// core/src/interp.rs:1351-1436 -- validate the f32 row index, then widen.
+// `rowf` (f32 indices) or `rowi` (int32 ids) per output row.
+__global__ void emb_bf16_kernel(float *__restrict__ dst, size_t ldd,
+                                const uint16_t *__restrict__ table, size_t rows, int cols,
+                                const float *__restrict__ rowf,
+                                const int32_t *__restrict__ rowi, int *guard) {
+    const int r = blockIdx.x;
+    float f = rowf ? rowf[r] : (float)rowi[r];
+    bool bad = !(f >= 0.0f) || f >= (float)rows;
+    size_t row = 0;
+    if (!bad) {
+        row = (size_t)f;
+        bad = (float)row != f;
+    }
+    if (bad) {
+        if (threadIdx.x == 0) atomicOr(guard, 1);
+        return;
+    }
+    const uint16_t *s = table + row * cols;
+    float *d = dst + (size_t)r * ldd;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) d[i] = bf16_bits_to_f32(s[i]);
+}
+
+int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
+                    const float *rowf, const int32_t *rowi, int n, hipStream_t st) {
+    if (n == 0) return VMLM_OK;
+    emb_bf16_kernel<<<n, 256, 0, st>>>(dst, ldd, table, rows, (int)cols, rowf, rowi,
+                                       guard_flag_ptr());
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// core/src/interp.rs:1649-1681 -- argmax with the scan's semantics: a larger
+// value wins, equal values keep the lower index, NaN never wins except that
+// a NaN at index 0 blocks every candidate (nothing compares > NaN).
+__device__ __forceinline__ void am_merge(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ src, int cols,
+                                                     size_t lds, float *dst_f,
+                                                     int32_t *dst_i) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int r = blockIdx.x;
+    const float *row = src + (size_t)r * lds;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < cols; i += 256) {
+        float v = row[i];
+        if (v == v) am_merge(bv, bi, v, i);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, 64);
+        int oi = __shfl_xor(bi, o, 64);
+        am_merge(bv, bi, ov, oi);
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) {
+        sv[w] = bv;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bv = sv[0];
+        bi = si[0];
+        for (int k = 1; k < 4; ++k) am_merge(bv, bi, sv[k], si[k]);
+        float x0 = row[0];
+        if (x0 != x0 || bi == 0x7fffffff) bi = 0;  // NaN at 0, or all NaN
+        if (dst_f) dst_f[r] = (float)bi;
+        if (dst_i) dst_i[r] = bi;
+    }
+}
+
+int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float *dst_f,
+                  int32_t *dst_i, hipStream_t st) {
+    if (rows == 0) return VMLM_OK;
+    argmax_kernel<<<(unsigned)rows, 256, 0, st>>>(src, (int)cols, lds, dst_f, dst_i);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+}  // namespace vmlm

@@ -1,0 +1,670 @@
+// sessions.hip -- device-resident sessions: the MiniCPM-shaped decoder program
+// (tools/p12_build_minicpm.py:766-981 + tools/p14_gen_build.py:470-560) and
+// the B1 layer stack (models/src/b1.rs:108-150).
+//
+// Decoder layout in HBM (one allocation each):
+//   weights per layer  [Wqkv 3H x H | Wo H x H | Wgu 2I x H | Wd H x I] int8
+//                      Wqkv = rows of q, k, v concatenated; Wgu interleaves
+//                      16-row blocks of gate and up so one GEMV workgroup owns
+//                      the gate and up rows of the same 16 outputs.
+//   scales per layer   [sqkv 3H | so H | sgu 2I (same interleave) | sd H] f32
+//   norms per layer    [in_ln H | post_ln H] f32
+//   KV cache           [layer][seq][head][cap][64] f32, rotated K and raw V
+//                      (the program's [HD, PMAX] state slots, position-major so
+//                      one lane streams one 256-byte row)
+// A decode step is captured once as a HIP graph; the position and the greedy
+// tokens live in device memory, so replays need no host round trip -- the
+// same closed loop the reference runs inside one Vm::run.
+#include <cstring>
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace vmlm {
+
+// tok[b] -> h[b] = bf16 row of embed (OP_EMB with its index guards) happens in
+// launch_emb_bf16; after the LM head, argmax writes tok[b]; this kernel then
+// records tok into tokens_out[step] and advances step and position.
+__global__ void advance_kernel(const int32_t *__restrict__ tok, int32_t *__restrict__ out,
+                               int B, int max_steps, int *step, int *pos, int *guard) {
+    const int s = *step;
+    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+        if (s < max_steps) out[(size_t)s * B + b] = tok[b];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (s >= max_steps) atomicOr(guard, 2);
+        *step = s + 1;
+        *pos = *pos + 1;
+    }
+}
+
+// Scatter rotated K / raw V of prefill rows [b*S + s][...] into the cache.
+__global__ void kv_fill_kernel(const float *__restrict__ qkv, int ldq, int H, int NH, int S,
+                               float *__restrict__ kc, float *__restrict__ vc, int cap, int B) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t total = (size_t)B * S * NH * 64;
+    if (idx >= total) return;
+    const int d = idx % 64;
+    const int h = (idx / 64) % NH;
+    const int s = (idx / (64 * NH)) % S;
+    const int b = idx / ((size_t)64 * NH * S);
+    const float *row = qkv + ((size_t)b * S + s) * ldq;
+    const size_t o = (((size_t)b * NH + h) * cap + s) * 64 + d;
+    kc[o] = row[H + h * 64 + d];
+    vc[o] = row[2 * H + h * 64 + d];
+}
+
+// Prefill MLP: act = silu(gate) * up from the interleaved GEMM output, plus
+// its bf16 terms (same element operations as ACT silu then EWMUL).
+__global__ void silu_mul_kernel(const float *__restrict__ gu, int I, int M,
+                                float *__restrict__ act, uint16_t *__restrict__ terms, int T) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)M * I) return;
+    const int m = idx / I, j = idx % I;
+    const int pg = (j / 16) * 32 + (j % 16);
+    const float gate = gu[(size_t)m * 2 * I + pg];
+    const float up = gu[(size_t)m * 2 * I + pg + 16];
+    float a = (gate / (1.0f + exp_f(-gate))) * up;
+    act[idx] = a;
+    for (int t = 0; t < T; ++t) {
+        uint32_t hb = bf16_rne_bits(a);
+        a = a - bf16_bits_to_f32(hb);
+        terms[((size_t)t * M + m) * I + j] = (uint16_t)hb;
+    }
+}
+
+}  // namespace vmlm
+
+using namespace vmlm;
+
+struct vmlm_decoder {
+    vmlm_decoder_cfg c{};
+    hipStream_t st = nullptr;
+    size_t H = 0, I = 0, NH = 0, V = 0, B = 0, cap = 0, L = 0;
+    size_t w_layer = 0, s_layer = 0;  // per-layer element counts
+    int8_t *w = nullptr;
+    float *s = nullptr, *norms = nullptr;
+    uint16_t *embed = nullptr, *lm_head = nullptr;
+    float *final_norm = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+    // decode activations
+    float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
+    float *part = nullptr, *logits = nullptr;
+    uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
+    int32_t *tok = nullptr, *tokens_out = nullptr;
+    int *pos = nullptr, *step = nullptr;
+    int NS = 0;
+    float rope_step = 0.0f;
+    uint32_t pos_host = 0, step_host = 0;
+    bool loaded_globals = false;
+    std::vector<bool> loaded;
+    bool use_graph = true;
+    hipGraphExec_t graph = nullptr;
+    std::vector<void *> allocs;
+
+    const int8_t *Wqkv(size_t l) const { return w + l * w_layer; }
+    const int8_t *Wo(size_t l) const { return Wqkv(l) + 3 * H * H; }
+    const int8_t *Wgu(size_t l) const { return Wo(l) + H * H; }
+    const int8_t *Wd(size_t l) const { return Wgu(l) + 2 * I * H; }
+    const float *Sqkv(size_t l) const { return s + l * s_layer; }
+    const float *So(size_t l) const { return Sqkv(l) + 3 * H; }
+    const float *Sgu(size_t l) const { return So(l) + H; }
+    const float *Sd(size_t l) const { return Sgu(l) + 2 * I; }
+    const float *InLn(size_t l) const { return norms + l * 2 * H; }
+    const float *PostLn(size_t l) const { return InLn(l) + H; }
+    float *Kc(size_t l) const { return kc + l * B * NH * cap * 64; }
+    float *Vc(size_t l) const { return vc + l * B * NH * cap * 64; }
+};
+
+namespace {
+
+template <typename T>
+int dalloc(vmlm_decoder *d, T **p, size_t count) {
+    void *q = nullptr;
+    VMLM_HIP_CHECK(hipMalloc(&q, (count ? count : 1) * sizeof(T)));
+    d->allocs.push_back(q);
+    *p = (T *)q;
+    return VMLM_OK;
+}
+
+// One decode step over the B sequences (all launches on d->st).
+int enqueue_step(vmlm_decoder *d) {
+    hipStream_t st = d->st;
+    const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
+    const int T = 3;
+    int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
+    if (rc) return rc;
+    for (size_t l = 0; l < d->L; ++l) {
+        rc = launch_rmsnorm(nullptr, d->h, d->InLn(l), B, H, d->c.eps, d->t_x, T, H, st);
+        if (rc) return rc;
+        GemvArgs g;
+        g.W = d->Wqkv(l);
+        g.scale = d->Sqkv(l);
+        g.A = d->t_x;
+        g.T = T;
+        g.lda = H;
+        g.M = B;
+        g.N = 3 * H;
+        g.K = H;
+        g.Y = d->qkv;
+        g.ldy = 3 * H;
+        if ((rc = launch_gemv(g, st))) return rc;
+        DecodeArgs a;
+        a.q = d->qkv;
+        a.k_new = d->qkv + H;
+        a.v_new = d->qkv + 2 * H;
+        a.ldq = 3 * H;
+        a.kc = d->Kc(l);
+        a.vc = d->Vc(l);
+        a.cap = (int)d->cap;
+        a.H = (int)d->NH;
+        a.posp = d->pos;
+        a.pos = 0;
+        a.step = d->rope_step;
+        a.scale = d->c.attn_scale;
+        a.part = d->part;
+        a.NS = d->NS;
+        if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
+        GemvArgs o;
+        o.W = d->Wo(l);
+        o.scale = d->So(l);
+        o.A = d->t_att;
+        o.T = T;
+        o.lda = H;
+        o.M = B;
+        o.N = H;
+        o.K = H;
+        o.Y = d->h2;
+        o.ldy = H;
+        o.epi = EPI_RESIDUAL;
+        o.R = d->h;
+        o.ldr = H;
+        if ((rc = launch_gemv(o, st))) return rc;
+        if ((rc = launch_rmsnorm(nullptr, d->h2, d->PostLn(l), B, H, d->c.eps, d->t_x, T, H, st)))
+            return rc;
+        GemvArgs gu;
+        gu.W = d->Wgu(l);
+        gu.scale = d->Sgu(l);
+        gu.A = d->t_x;
+        gu.T = T;
+        gu.lda = H;
+        gu.M = B;
+        gu.N = 2 * I;
+        gu.K = H;
+        gu.Y = d->act;
+        gu.ldy = I;
+        gu.epi = EPI_SILU_MUL;
+        gu.Aout = d->t_act;
+        gu.ldaout = I;
+        gu.Tout = T;
+        if ((rc = launch_gemv(gu, st))) return rc;
+        GemvArgs dn;
+        dn.W = d->Wd(l);
+        dn.scale = d->Sd(l);
+        dn.A = d->t_act;
+        dn.T = T;
+        dn.lda = I;
+        dn.M = B;
+        dn.N = H;
+        dn.K = I;
+        dn.Y = d->h;
+        dn.ldy = H;
+        dn.epi = EPI_RESIDUAL;
+        dn.R = d->h2;
+        dn.ldr = H;
+        if ((rc = launch_gemv(dn, st))) return rc;
+    }
+    if ((rc = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, T, H, st)))
+        return rc;
+    GemvArgs lm;
+    lm.W = d->lm_head;
+    lm.w_int8 = false;
+    lm.A = d->t_x;
+    lm.T = T;
+    lm.lda = H;
+    lm.M = B;
+    lm.N = (int)d->V;
+    lm.K = H;
+    lm.Y = d->logits;
+    lm.ldy = (int)d->V;
+    if ((rc = launch_gemv(lm, st))) return rc;
+    if ((rc = launch_argmax(d->logits, B, d->V, d->V, nullptr, d->tok, st))) return rc;
+    advance_kernel<<<1, 64, 0, st>>>(d->tok, d->tokens_out, B, (int)d->cap, d->step, d->pos,
+                                     guard_flag_ptr());
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+int ensure_graph(vmlm_decoder *d) {
+    if (d->graph) return VMLM_OK;
+    hipGraph_t g = nullptr;
+    VMLM_HIP_CHECK(hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(d);
+    hipError_t e = hipStreamEndCapture(d->st, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&d->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    return VMLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    VMLM_GUARD(cfg && out, "decoder: null argument");
+    const vmlm_decoder_cfg &c = *cfg;
+    VMLM_GUARD(c.head_dim == 64, "decoder: head_dim %u unsupported (64 only)", c.head_dim);
+    VMLM_GUARD(c.n_heads * c.head_dim == c.hidden, "decoder: hidden != n_heads * head_dim");
+    VMLM_GUARD(c.hidden % 64 == 0 && c.inter % 64 == 0, "decoder: hidden and inter must be multiples of 64");
+    VMLM_GUARD(c.batch >= 1 && c.batch <= 16, "decoder: batch %u outside 1..16", c.batch);
+    VMLM_GUARD(c.cap >= 2 && c.vocab >= 1 && c.n_layers >= 1, "decoder: empty shape");
+    VMLM_GUARD(c.theta > 0.0f, "ROPE: theta must be > 0");
+    vmlm_decoder *d = new vmlm_decoder();
+    d->c = c;
+    d->H = c.hidden;
+    d->I = c.inter;
+    d->NH = c.n_heads;
+    d->V = c.vocab;
+    d->B = c.batch;
+    d->cap = c.cap;
+    d->L = c.n_layers;
+    d->w_layer = 4 * d->H * d->H + 3 * d->I * d->H;
+    d->s_layer = 5 * d->H + 2 * d->I;
+    d->NS = (int)((d->cap + 63) / 64);
+    d->rope_step = -2.0f / 64.0f * host_ln_f(c.theta);
+    d->loaded.assign(d->L, false);
+    auto cleanup = [&](int code) {
+        vmlm_decoder_destroy(d);
+        return code;
+    };
+    hipError_t e = hipStreamCreateWithFlags(&d->st, hipStreamNonBlocking);
+    if (e != hipSuccess) return cleanup(hip_fail(e, "decoder stream"));
+    const size_t kvn = d->L * d->B * d->NH * d->cap * 64;
+    if ((rc = dalloc(d, &d->w, d->L * d->w_layer)) || (rc = dalloc(d, &d->s, d->L * d->s_layer)) ||
+        (rc = dalloc(d, &d->norms, d->L * 2 * d->H)) || (rc = dalloc(d, &d->embed, d->V * d->H)) ||
+        (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
+        (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
+        (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
+        (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
+        (rc = dalloc(d, &d->act, d->B * d->I)) ||
+        (rc = dalloc(d, &d->part, d->B * d->NH * d->NS * 66)) ||
+        (rc = dalloc(d, &d->logits, d->B * d->V)) || (rc = dalloc(d, &d->t_x, 3 * d->B * d->H)) ||
+        (rc = dalloc(d, &d->t_att, 3 * d->B * d->H)) ||
+        (rc = dalloc(d, &d->t_act, 3 * d->B * d->I)) || (rc = dalloc(d, &d->tok, d->B)) ||
+        (rc = dalloc(d, &d->tokens_out, d->cap * d->B)) || (rc = dalloc(d, &d->pos, 1)) ||
+        (rc = dalloc(d, &d->step, 1)))
+        return cleanup(rc);
+    if ((e = hipMemsetAsync(d->kc, 0, kvn * 4, d->st)) != hipSuccess ||
+        (e = hipMemsetAsync(d->vc, 0, kvn * 4, d->st)) != hipSuccess ||
+        (e = hipMemsetAsync(d->pos, 0, 4, d->st)) != hipSuccess ||
+        (e = hipMemsetAsync(d->step, 0, 4, d->st)) != hipSuccess ||
+        (e = hipStreamSynchronize(d->st)) != hipSuccess)
+        return cleanup(hip_fail(e, "decoder init"));
+    *out = d;
+    return VMLM_OK;
+}
+
+int vmlm_decoder_destroy(vmlm_decoder *d) {
+    if (!d) return VMLM_OK;
+    if (d->st) (void)hipStreamSynchronize(d->st);
+    if (d->graph) (void)hipGraphExecDestroy(d->graph);
+    for (void *p : d->allocs) (void)hipFree(p);
+    if (d->st) (void)hipStreamDestroy(d->st);
+    delete d;
+    return VMLM_OK;
+}
+
+int vmlm_decoder_load_layer(vmlm_decoder *d, uint32_t layer, const int8_t *wq, const float *sq,
+                            const int8_t *wk, const float *sk, const int8_t *wv,
+                            const float *sv, const int8_t *wo, const float *so,
+                            const int8_t *wg, const float *sg, const int8_t *wu,
+                            const float *su, const int8_t *wd, const float *sd,
+                            const float *in_ln, const float *post_ln) {
+    VMLM_GUARD(d && layer < d->L, "decoder: layer %u out of range", layer);
+    const size_t H = d->H, I = d->I, l = layer;
+    int8_t *W = d->w + l * d->w_layer;
+    float *S = d->s + l * d->s_layer;
+    hipStream_t st = d->st;
+    auto h2d = [&](void *dst, const void *src, size_t bytes) {
+        return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
+    };
+    hipError_t e;
+#define H2D(dst, src, bytes)                                         \
+    if ((e = h2d(dst, src, bytes)) != hipSuccess) return hip_fail(e, "load_layer");
+    H2D(W, wq, H * H);
+    H2D(W + H * H, wk, H * H);
+    H2D(W + 2 * H * H, wv, H * H);
+    H2D(W + 3 * H * H, wo, H * H);
+    int8_t *Wgu = W + 4 * H * H;
+    // 16-row blocks: gate block b -> rows [32b, 32b+16), up block b -> [32b+16, 32b+32)
+    if ((e = hipMemcpy2DAsync(Wgu, 32 * H, wg, 16 * H, 16 * H, I / 16, hipMemcpyHostToDevice,
+                              st)) != hipSuccess ||
+        (e = hipMemcpy2DAsync(Wgu + 16 * H, 32 * H, wu, 16 * H, 16 * H, I / 16,
+                              hipMemcpyHostToDevice, st)) != hipSuccess)
+        return hip_fail(e, "load_layer gate/up");
+    H2D(Wgu + 2 * I * H, wd, H * I);
+    H2D(S, sq, H * 4);
+    H2D(S + H, sk, H * 4);
+    H2D(S + 2 * H, sv, H * 4);
+    H2D(S + 3 * H, so, H * 4);
+    float *Sgu = S + 4 * H;
+    if ((e = hipMemcpy2DAsync(Sgu, 32 * 4, sg, 16 * 4, 16 * 4, I / 16, hipMemcpyHostToDevice,
+                              st)) != hipSuccess ||
+        (e = hipMemcpy2DAsync(Sgu + 16, 32 * 4, su, 16 * 4, 16 * 4, I / 16,
+                              hipMemcpyHostToDevice, st)) != hipSuccess)
+        return hip_fail(e, "load_layer gate/up scales");
+    H2D(Sgu + 2 * I, sd, H * 4);
+    H2D(d->norms + l * 2 * H, in_ln, H * 4);
+    H2D(d->norms + l * 2 * H + H, post_ln, H * 4);
+#undef H2D
+    VMLM_HIP_CHECK(hipStreamSynchronize(st));
+    d->loaded[l] = true;
+    return VMLM_OK;
+}
+
+int vmlm_decoder_load_globals(vmlm_decoder *d, const uint16_t *embed, const uint16_t *lm_head,
+                              const float *final_norm) {
+    VMLM_GUARD(d, "decoder: null");
+    VMLM_HIP_CHECK(hipMemcpyAsync(d->embed, embed, d->V * d->H * 2, hipMemcpyHostToDevice, d->st));
+    VMLM_HIP_CHECK(
+        hipMemcpyAsync(d->lm_head, lm_head, d->V * d->H * 2, hipMemcpyHostToDevice, d->st));
+    VMLM_HIP_CHECK(
+        hipMemcpyAsync(d->final_norm, final_norm, d->H * 4, hipMemcpyHostToDevice, d->st));
+    VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
+    d->loaded_globals = true;
+    return VMLM_OK;
+}
+
+static int check_loaded(vmlm_decoder *d) {
+    VMLM_GUARD(d, "decoder: null");
+    VMLM_GUARD(d->loaded_globals, "decoder: embedding / LM head not loaded");
+    for (size_t l = 0; l < d->L; ++l) VMLM_GUARD(d->loaded[l], "decoder: layer %zu not loaded", l);
+    return VMLM_OK;
+}
+
+int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
+                         int32_t *first_tokens, float *logits_last) {
+    int rc = check_loaded(d);
+    if (rc) return rc;
+    VMLM_GUARD(S >= 1 && S < d->cap, "decoder: prompt length %u outside 1..cap-1", S);
+    hipStream_t st = d->st;
+    const size_t B = d->B, H = d->H, I = d->I, NH = d->NH, M = B * S;
+    const int T = 3;
+    // per-prefill buffers
+    float *h, *h2, *qkv, *att, *o, *gu, *act;
+    uint16_t *terms;
+    int32_t *toks;
+    std::vector<void *> tmp;
+    auto get = [&](auto **p, size_t bytes) -> int {
+        void *q = nullptr;
+        hipError_t e = hipMallocAsync(&q, bytes ? bytes : 1, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill buffers");
+        tmp.push_back(q);
+        *p = (std::remove_reference_t<decltype(*p)>)q;
+        return VMLM_OK;
+    };
+    auto release = [&]() {
+        for (void *p : tmp) (void)hipFreeAsync(p, st);
+    };
+    if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
+        (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) || (rc = get(&gu, M * 2 * I * 4)) ||
+        (rc = get(&act, M * I * 4)) || (rc = get(&terms, (size_t)T * M * I * 2)) ||
+        (rc = get(&toks, M * 4))) {
+        release();
+        return rc;
+    }
+    auto run = [&]() -> int {
+        VMLM_HIP_CHECK(hipMemcpyAsync(toks, tokens, M * 4, hipMemcpyHostToDevice, st));
+        int r = launch_emb_bf16(h, H, d->embed, d->V, H, nullptr, toks, (int)M, st);
+        if (r) return r;
+        for (size_t l = 0; l < d->L; ++l) {
+            if ((r = launch_rmsnorm(nullptr, h, d->InLn(l), M, H, d->c.eps, terms, T, (int)H, st)))
+                return r;
+            GemmArgs g;
+            g.W = d->Wqkv(l);
+            g.scale = d->Sqkv(l);
+            g.A = terms;
+            g.T = T;
+            g.lda = (int)H;
+            g.M = (int)M;
+            g.N = (int)(3 * H);
+            g.K = (int)H;
+            g.C = qkv;
+            g.ldc = (int)(3 * H);
+            if ((r = launch_gemm(g, st))) return r;
+            for (size_t b = 0; b < B; ++b) {  // RoPE q and k in place at positions 0..S-1
+                float *rowq = qkv + b * S * 3 * H;
+                if ((r = launch_rope(rowq, rowq, S, 64, 3 * H, d->c.theta, 0.0f, (int)NH, st)))
+                    return r;
+                if ((r = launch_rope(rowq + H, rowq + H, S, 64, 3 * H, d->c.theta, 0.0f, (int)NH,
+                                     st)))
+                    return r;
+            }
+            size_t nkv = M * NH * 64;
+            kv_fill_kernel<<<cdiv(nkv, 256), 256, 0, st>>>(qkv, (int)(3 * H), (int)H, (int)NH,
+                                                           (int)S, d->Kc(l), d->Vc(l),
+                                                           (int)d->cap, (int)B);
+            VMLM_HIP_CHECK(hipGetLastError());
+            for (size_t b = 0; b < B; ++b) {
+                const float *base = qkv + b * S * 3 * H;
+                if ((r = launch_attention_prefill(base, base + H, base + 2 * H, att + b * S * H,
+                                                  (int)S, (int)NH, (int)(3 * H), (int)H,
+                                                  d->c.attn_scale, true, st)))
+                    return r;
+            }
+            if ((r = launch_split_terms(att, H, (int)M, (int)H, T, terms, (int)H, st))) return r;
+            GemmArgs go = g;
+            go.W = d->Wo(l);
+            go.scale = d->So(l);
+            go.N = (int)H;
+            go.C = o;
+            go.ldc = (int)H;
+            if ((r = launch_gemm(go, st))) return r;
+            if ((r = launch_ew(h2, h, o, M * H, VMLM_OP_EWADD, st))) return r;
+            if ((r = launch_rmsnorm(nullptr, h2, d->PostLn(l), M, H, d->c.eps, terms, T, (int)H,
+                                    st)))
+                return r;
+            GemmArgs ggu = g;
+            ggu.W = d->Wgu(l);
+            ggu.scale = d->Sgu(l);
+            ggu.N = (int)(2 * I);
+            ggu.C = gu;
+            ggu.ldc = (int)(2 * I);
+            if ((r = launch_gemm(ggu, st))) return r;
+            silu_mul_kernel<<<cdiv(M * I, 256), 256, 0, st>>>(gu, (int)I, (int)M, act, terms, T);
+            VMLM_HIP_CHECK(hipGetLastError());
+            GemmArgs gd = g;
+            gd.W = d->Wd(l);
+            gd.scale = d->Sd(l);
+            gd.lda = (int)I;
+            gd.K = (int)I;
+            gd.N = (int)H;
+            gd.C = o;
+            gd.ldc = (int)H;
+            if ((r = launch_gemm(gd, st))) return r;
+            if ((r = launch_ew(h, h2, o, M * H, VMLM_OP_EWADD, st))) return r;
+        }
+        // last row of every sequence -> decode buffers, then the shared tail
+        VMLM_HIP_CHECK(hipMemcpy2DAsync(d->h, H * 4, h + (S - 1) * H, S * H * 4, H * 4, B,
+                                        hipMemcpyDeviceToDevice, st));
+        if ((r = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, T, (int)H,
+                                st)))
+            return r;
+        GemvArgs lm;
+        lm.W = d->lm_head;
+        lm.w_int8 = false;
+        lm.A = d->t_x;
+        lm.T = T;
+        lm.lda = (int)H;
+        lm.M = (int)B;
+        lm.N = (int)d->V;
+        lm.K = (int)H;
+        lm.Y = d->logits;
+        lm.ldy = (int)d->V;
+        if ((r = launch_gemv(lm, st))) return r;
+        if ((r = launch_argmax(d->logits, B, d->V, d->V, nullptr, d->tok, st))) return r;
+        int zero = 0, p = (int)S;
+        VMLM_HIP_CHECK(hipMemcpyAsync(d->step, &zero, 4, hipMemcpyHostToDevice, st));
+        VMLM_HIP_CHECK(hipMemcpyAsync(d->pos, &p, 4, hipMemcpyHostToDevice, st));
+        if (first_tokens)
+            VMLM_HIP_CHECK(hipMemcpyAsync(first_tokens, d->tok, B * 4, hipMemcpyDeviceToHost, st));
+        if (logits_last)
+            VMLM_HIP_CHECK(
+                hipMemcpyAsync(logits_last, d->logits, B * d->V * 4, hipMemcpyDeviceToHost, st));
+        return VMLM_OK;
+    };
+    rc = run();
+    release();
+    VMLM_HIP_CHECK(hipStreamSynchronize(st));
+    if (rc) return rc;
+    d->pos_host = S;
+    d->step_host = 0;
+    return vmlm_hip_check_guards();
+}
+
+int vmlm_decoder_decode(vmlm_decoder *d, uint32_t n_steps, int32_t *tokens_out,
+                        float *logits_last) {
+    int rc = check_loaded(d);
+    if (rc) return rc;
+    VMLM_GUARD(d->pos_host >= 1, "decoder: decode before prefill");
+    VMLM_GUARD((size_t)d->pos_host + n_steps <= d->cap,
+               "WRITECOL: decode would write position %zu beyond capacity %zu",
+               (size_t)d->pos_host + n_steps - 1, d->cap);
+    VMLM_GUARD((size_t)d->step_host + n_steps <= d->cap, "decoder: token log full");
+    if (d->use_graph && (rc = ensure_graph(d))) return rc;
+    for (uint32_t i = 0; i < n_steps; ++i) {
+        if (d->use_graph) {
+            VMLM_HIP_CHECK(hipGraphLaunch(d->graph, d->st));
+        } else if ((rc = enqueue_step(d))) {
+            return rc;
+        }
+    }
+    const uint32_t first = d->step_host;
+    if (tokens_out && n_steps)
+        VMLM_HIP_CHECK(hipMemcpyAsync(tokens_out, d->tokens_out + (size_t)first * d->B,
+                                      (size_t)n_steps * d->B * 4, hipMemcpyDeviceToHost, d->st));
+    if (logits_last)
+        VMLM_HIP_CHECK(hipMemcpyAsync(logits_last, d->logits, d->B * d->V * 4,
+                                      hipMemcpyDeviceToHost, d->st));
+    VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
+    d->pos_host += n_steps;
+    d->step_host += n_steps;
+    return vmlm_hip_check_guards();
+}
+
+int vmlm_decoder_position(const vmlm_decoder *d, uint32_t *pos) {
+    VMLM_GUARD(d && pos, "decoder: null");
+    *pos = d->pos_host;
+    return VMLM_OK;
+}
+
+int vmlm_decoder_set_graph(vmlm_decoder *d, int enable) {
+    VMLM_GUARD(d, "decoder: null");
+    d->use_graph = enable != 0;
+    return VMLM_OK;
+}
+
+void *vmlm_decoder_stream(vmlm_decoder *d) { return d ? (void *)d->st : nullptr; }
+
+int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *avg_us,
+                           double *bytes_per_launch) {
+    int rc = check_loaded(d);
+    if (rc) return rc;
+    VMLM_GUARD(which >= 0 && which <= 4 && iters >= 1, "time_gemv: which 0..4, iters >= 1");
+    const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
+    auto make = [&](size_t l) {
+        GemvArgs g;
+        g.T = 3;
+        g.M = B;
+        g.lda = H;
+        g.K = H;
+        g.A = d->t_x;
+        switch (which) {
+        case 0: g.W = d->Wqkv(l); g.scale = d->Sqkv(l); g.N = 3 * H; g.Y = d->qkv; g.ldy = 3 * H; break;
+        case 1:
+            g.W = d->Wo(l); g.scale = d->So(l); g.A = d->t_att; g.N = H; g.Y = d->h2; g.ldy = H;
+            g.epi = EPI_RESIDUAL; g.R = d->h; g.ldr = H; break;
+        case 2:
+            g.W = d->Wgu(l); g.scale = d->Sgu(l); g.N = 2 * I; g.Y = d->act; g.ldy = I;
+            g.epi = EPI_SILU_MUL; g.Aout = d->t_act; g.ldaout = I; g.Tout = 3; break;
+        case 3:
+            g.W = d->Wd(l); g.scale = d->Sd(l); g.A = d->t_act; g.lda = I; g.K = I; g.N = H;
+            g.Y = d->att; g.ldy = H; g.epi = EPI_RESIDUAL; g.R = d->h2; g.ldr = H; break;
+        default:
+            g.W = d->lm_head; g.w_int8 = false; g.N = (int)d->V; g.Y = d->logits;
+            g.ldy = (int)d->V; break;
+        }
+        return g;
+    };
+    hipEvent_t e0, e1;
+    VMLM_HIP_CHECK(hipEventCreate(&e0));
+    VMLM_HIP_CHECK(hipEventCreate(&e1));
+    // warm-up pass over every layer
+    for (size_t l = 0; l < (which == 4 ? 1 : d->L); ++l)
+        if ((rc = launch_gemv(make(l), d->st))) return rc;
+    VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
+    for (uint32_t i = 0; i < iters; ++i)
+        if ((rc = launch_gemv(make(which == 4 ? 0 : i % d->L), d->st))) return rc;
+    VMLM_HIP_CHECK(hipEventRecord(e1, d->st));
+    VMLM_HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    VMLM_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_us = ms * 1000.0f / (float)iters;
+    GemvArgs g = make(0);
+    const double wbytes = (double)g.N * g.K * (g.w_int8 ? 1 : 2);
+    const double sbytes = g.scale ? (double)g.N * 4 : 0.0;
+    const double xbytes = (double)B * g.K * 4;
+    const double ybytes = (double)B * (which == 2 ? I : g.N) * 4;
+    const double rbytes = g.epi == EPI_RESIDUAL ? (double)B * g.N * 4 : 0.0;
+    *bytes_per_launch = wbytes + sbytes + xbytes + ybytes + rbytes;
+    return VMLM_OK;
+}
+
+// B1 layer stack: x [T][d] -> transpose -> n_layers x (gather-dot, act) ->
+// transpose back into y [T][d]. Connection arrays are device pointers.
+int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers, const float *x,
+                          float *y, size_t n_tokens, uint16_t act, void *stream) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    VMLM_GUARD(layers && n_layers >= 1, "b1 stack: no layers");
+    const size_t d = layers[0].n_neurons;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const vmlm_sparse_conn_w &sc = layers[l];
+        VMLM_GUARD(sc.n_neurons == d, "b1 stack: layer %u width %u != %zu", l, sc.n_neurons, d);
+        VMLM_GUARD(sc.e == (size_t)sc.n_neurons * sc.k0,
+                   "CONN_TRAIN: SparseConnW geometry inconsistent at layer %u", l);
+        VMLM_GUARD(sc.k0 <= 1024, "B1: k0 exceeds the safe stack bound");
+    }
+    if (n_tokens == 0) return VMLM_OK;
+    hipStream_t st = as_stream(stream);
+    const size_t t8 = (n_tokens + 63) / 64 * 64;
+    float *a = nullptr, *b = nullptr;
+    VMLM_HIP_CHECK(hipMallocAsync((void **)&a, d * t8 * 4, st));
+    VMLM_HIP_CHECK(hipMallocAsync((void **)&b, d * t8 * 4, st));
+    rc = launch_transpose_t8(x, n_tokens, d, a, t8, st);
+    const int actk = act == 0xFFFF ? -1 : (int)act;
+    for (uint32_t l = 0; l < n_layers && !rc; ++l) {
+        rc = launch_b1_forward(layers[l].w, layers[l].src_u32, (int)d, (int)layers[l].k0, a, t8,
+                               (int)n_tokens, b, 0, actk, st);
+        std::swap(a, b);
+    }
+    if (!rc) rc = launch_transpose_back(a, d, n_tokens, y, d, t8, st);
+    (void)hipFreeAsync(a, st);
+    (void)hipFreeAsync(b, st);
+    return rc;
+}
+
+}  // extern "C"

@@ -51,37 +51,66 @@ def bf16_rne(x: np.ndarray) -> np.ndarray:
     return ((u + np.uint32(0x7FFF) + lsb) >> np.uint32(16)).astype(np.uint16)
 
 
+def uniform_int8(rng: np.random.Generator, shape) -> np.ndarray:
+    """Uniform integers in [-127, 127]: random bytes u in [0, 254] shifted by
+    -127; the byte value 255 is redrawn (exact uniformity, ~1/256 redraws)."""
+    n = int(np.prod(shape))
+
+    def raw_bytes(count):
+        return rng.bit_generator.random_raw((count + 7) // 8).view(np.uint8)[:count]
+
+    u = raw_bytes(n)
+    bad = np.flatnonzero(u == 255)
+    while bad.size:
+        u[bad] = raw_bytes(bad.size)
+        bad = bad[u[bad] == 255]
+    u -= np.uint8(127)  # wraps: 0..126 -> 129..255 (= -127..-1), 127..254 -> 0..127
+    return u.view(np.int8).reshape(shape)
+
+
 def q8_weight(rng: np.random.Generator, n: int, k: int):
-    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    q = uniform_int8(rng, (n, k))
     s = (np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)) / np.float32(127)
          + np.float32(1e-6)).astype(np.float32)
     return q, s
 
 
-def make_weights(cfg: dict, seed: int = 3) -> dict:
-    """Seeded host weights; layer arrays are [N, K] row-major (nn.Linear)."""
-    rng = np.random.default_rng(seed)
+def make_weights(cfg: dict, seed: int = 3, threads: int = 8) -> dict:
+    """Seeded host weights; layer arrays are [N, K] row-major (nn.Linear).
+
+    Every layer and every 8192-row block of the two bf16 tables draws from its
+    own child of SeedSequence(seed), so the values depend only on the seed and
+    the shapes, not on the thread count used to fill them."""
+    from concurrent.futures import ThreadPoolExecutor
     H, I, V = cfg["hidden"], cfg["inter"], cfg["vocab"]
-    layers = []
-    for _ in range(cfg["n_layers"]):
+    nl = cfg["n_layers"]
+    step = 8192
+    nblk = (V + step - 1) // step
+    kids = np.random.SeedSequence(seed).spawn(nl + 2 * nblk)
+
+    def layer(li):
+        rng = np.random.default_rng(kids[li])
         L = {}
         for name, (n, k) in (("q", (H, H)), ("k", (H, H)), ("v", (H, H)), ("o", (H, H)),
                              ("g", (I, H)), ("u", (I, H)), ("d", (H, I))):
             L["w" + name], L["s" + name] = q8_weight(rng, n, k)
         L["in_ln"] = np.ones(H, np.float32)
         L["post_ln"] = np.ones(H, np.float32)
-        layers.append(L)
+        return L
 
-    def bf16_table():
-        out = np.empty((V, H), np.uint16)
-        step = 8192
-        for r in range(0, V, step):
-            blk = rng.standard_normal((min(step, V - r), H), dtype=np.float32) * np.float32(0.02)
-            out[r:r + blk.shape[0]] = bf16_rne(blk)
-        return out
+    embed = np.empty((V, H), np.uint16)
+    lm_head = np.empty((V, H), np.uint16)
 
-    embed = bf16_table()
-    lm_head = bf16_table()
+    def table_block(t, b):
+        rng = np.random.default_rng(kids[nl + t * nblk + b])
+        r0 = b * step
+        rows = min(step, V - r0)
+        blk = rng.standard_normal((rows, H), dtype=np.float32) * np.float32(0.02)
+        (embed if t == 0 else lm_head)[r0:r0 + rows] = bf16_rne(blk)
+
+    with ThreadPoolExecutor(max(1, threads)) as ex:
+        layers = list(ex.map(layer, range(nl)))
+        list(ex.map(lambda tb: table_block(*tb), [(t, b) for t in (0, 1) for b in range(nblk)]))
     return dict(layers=layers, embed=embed, lm_head=lm_head,
                 final_norm=np.ones(H, np.float32))
 

@@ -1,0 +1,228 @@
+"""GPU parity of the vmlm-ops kernels against the CPU oracle, through the
+host-pointer C ABI (sparrow_amd.ops).
+
+Bars: integer / index / elementwise work bit-exact;
+f32-accumulated outputs within max|d| <= 1e-4 * RMS(reference)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def rms(x):
+    return float(np.sqrt(np.mean(np.asarray(x, np.float64) ** 2)))
+
+
+def assert_close_rms(got, ref, tol=TOL):
+    err = float(np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64)).max())
+    assert err <= tol * max(rms(ref), 1e-30), f"max|d|={err:.3e} rms={rms(ref):.3e}"
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ops(hip):
+    from sparrow_amd import ops
+    return ops
+
+
+def q8_case(rng, m, n, k):
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)) / np.float32(127)
+         + np.float32(1e-6)).astype(np.float32)
+    return a, q, s
+
+
+def test_q8_kat(ops):
+    """tools/p13_q8_check.py:42-47 -> [[-1, -1]] exactly."""
+    c = ops.gemm_nt_int8(np.float32([[1, 2, 3, 4]]), np.int8([[1, 0, -1, 0], [0, 2, 0, -2]]),
+                         np.float32([0.5, 0.25]))
+    assert np.array_equal(c, np.float32([[-1, -1]]))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 2304, 2304), (1, 2304, 2304), (1, 5760, 2304),
+                                   (4, 2304, 5760), (3, 17, 100), (40, 300, 256),
+                                   (128, 512, 2304)])
+def test_gemm_nt_int8(ops, oracle, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a, q, s = q8_case(rng, m, n, k)
+    assert_close_rms(ops.gemm_nt_int8(a, q, s), oracle.gemm_nt_int8(a, q, s))
+
+
+def test_gemm_nt_int8_exact_case(ops):
+    """Integer activations and power-of-two scales: every term and partial
+    sum is exact, so the result is exact."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(-3, 4, size=(5, 640)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(48, 640), dtype=np.int8)
+    s = np.full(48, 1 / 64, np.float32)
+    ref = (a.astype(np.float64) @ q.astype(np.float64).T) / 64
+    assert np.array_equal(ops.gemm_nt_int8(a, q, s).astype(np.float64), ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 5000, 2304), (16, 1000, 2304), (2, 33, 70),
+                                   (64, 256, 512)])
+def test_gemm_nt_bf16(ops, oracle, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = oracle.f32_to_bf16(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    assert_close_rms(ops.gemm_nt_bf16(a, b), oracle.gemm_nt_bf16(a, b))
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 8, 8), (1, 1, 64), (17, 23, 31), (512, 512, 64),
+                                   (16, 16, 1), (64, 64, 64)])
+def test_gemm_nt_f32_and_nn(ops, oracle, m, n, k):
+    rng = np.random.default_rng(m * n + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = rng.standard_normal((n, k), dtype=np.float32)
+    c0 = rng.standard_normal((m, n), dtype=np.float32)
+    assert_close_rms(ops.gemm_nt(a, b), oracle.gemm_nt(a, b))
+    assert_close_rms(ops.gemm_nt(a, b, c0, acc=True), oracle.gemm_nt(a, b, c0, acc=True))
+    bn = np.ascontiguousarray(b.T)
+    assert_close_rms(ops.gemm(a, bn), oracle.gemm(a, bn))
+
+
+def test_rmsnorm_softmax(ops, oracle):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((9, 2304), dtype=np.float32) * 3
+    g = rng.uniform(0.5, 1.5, 2304).astype(np.float32)
+    assert_close_rms(ops.rmsnorm(x, g, 1e-5), oracle.rmsnorm(x, g, 1e-5), 1e-6)
+    p = rng.standard_normal((37, 300), dtype=np.float32) * 4
+    for causal in (False, True):
+        got, ref = ops.softmax(p, causal), oracle.softmax(p, causal)
+        assert np.abs(got - ref).max() <= 1e-6
+        if causal:
+            assert np.all(got[np.triu_indices(37, 1, 300)] == 0)
+
+
+@pytest.mark.parametrize("kind", range(6))
+def test_act_bitwise(ops, oracle, kind):
+    rng = np.random.default_rng(kind)
+    x = (rng.standard_normal(1003, dtype=np.float32) * 6).astype(np.float32)
+    x[:4] = [0.0, -0.0, 20.0, -20.0]
+    assert np.array_equal(bits(ops.act(x, kind)), bits(oracle.act(x, kind)))
+
+
+@pytest.mark.parametrize("op", [20, 21, 22, 23])
+def test_ew_scale_bitwise(ops, oracle, op):
+    rng = np.random.default_rng(op)
+    x = rng.standard_normal(777, dtype=np.float32)
+    y = rng.standard_normal(777, dtype=np.float32) + np.float32(0.1)
+    assert np.array_equal(bits(ops.ew_op(x, y, op)), bits(oracle.ew_op(x, y, op)))
+    assert np.array_equal(bits(ops.scale(x, 0.125)), bits(oracle.scale(x, 0.125)))
+
+
+@pytest.mark.parametrize("pos0", [0, 1, 127, 1000, 65000])
+def test_rope_bitwise(ops, oracle, pos0):
+    rng = np.random.default_rng(pos0)
+    x = rng.standard_normal((33, 64), dtype=np.float32)
+    assert np.array_equal(bits(ops.rope(x, 10000.0, pos0)), bits(oracle.rope(x, 10000.0, pos0)))
+    x = rng.standard_normal((5, 128), dtype=np.float32)
+    assert np.array_equal(bits(ops.rope(x, 500000.0, pos0)),
+                          bits(oracle.rope(x, 500000.0, pos0)))
+
+
+def test_rope_guards(ops):
+    from sparrow_amd import VmlmError
+    with pytest.raises(VmlmError) as e:
+        ops.rope(np.zeros((2, 63), np.float32), 10000.0, 0)
+    assert e.value.code == 9
+
+
+def test_emb_and_guards(ops, oracle):
+    from sparrow_amd import VmlmError
+    rng = np.random.default_rng(8)
+    tab = oracle.f32_to_bf16(rng.standard_normal((50, 2304), dtype=np.float32))
+    for r in (0, 17, 49):
+        assert np.array_equal(bits(ops.emb_bf16(tab, float(r))),
+                              bits(oracle.emb_bf16(tab, float(r))[1]))
+    for bad in (-1.0, float("nan"), 50.0, 2.5):
+        with pytest.raises(VmlmError) as e:
+            ops.emb_bf16(tab, bad)
+        assert e.value.code == 9
+
+
+def test_topk_idx_bitexact(ops, oracle):
+    rng = np.random.default_rng(9)
+    for n in (1, 7, 122753):
+        x = rng.standard_normal(n, dtype=np.float32)
+        assert ops.topk_idx(x) == oracle.topk_idx(x)[1]
+    x = np.zeros(5000, np.float32)
+    x[[17, 300, 4999]] = 3.0  # ties: lowest index wins
+    assert ops.topk_idx(x) == 17.0
+    x = rng.standard_normal(1000, dtype=np.float32)
+    x[0] = np.nan  # nothing compares > NaN: the scan keeps index 0
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 0.0
+
+
+@pytest.mark.parametrize("k0", [1, 4, 8, 20, 32, 37])
+def test_b1_forward_bitwise(ops, oracle, k0):
+    rng = np.random.default_rng(k0)
+    n = 200
+    w = rng.standard_normal((n, k0), dtype=np.float32)
+    src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
+    x = rng.standard_normal(n, dtype=np.float32)
+    y, macs = ops.b1_forward(w, src, x)
+    assert macs == n * k0
+    assert np.array_equal(bits(y), bits(oracle.b1_forward(w, src, x)))
+
+
+@pytest.mark.parametrize("k0,T,t8", [(32, 1024, 1024), (20, 37, 40), (1, 5, 8), (0, 3, 8)])
+def test_b1_forward_t8_bitwise(ops, oracle, k0, T, t8):
+    rng = np.random.default_rng(k0 + T)
+    n = 96
+    w = rng.standard_normal((n, k0), dtype=np.float32)
+    src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
+    x = rng.standard_normal((T, n), dtype=np.float32)
+    xt = ops.transpose_t8(x, t8)
+    assert np.array_equal(xt, oracle.transpose_t8(x, t8))
+    yt, _ = ops.b1_forward_t8(w, src, xt, T)
+    ref = oracle.b1_forward_t8(w, src, xt, T)
+    assert np.array_equal(bits(yt[:, :T]), bits(ref[:, :T]))
+    back = ops.transpose_t8_back(yt, T)
+    assert np.array_equal(back, oracle.transpose_t8_back(yt, T))
+
+
+def test_b1_guards(ops):
+    from sparrow_amd import VmlmError
+    w = np.ones((8, 4), np.float32)
+    src = np.zeros((8, 4), np.uint32)
+    src[3, 2] = 8  # out of range
+    with pytest.raises(VmlmError) as e:
+        ops.b1_forward(w, src, np.ones(8, np.float32))
+    assert e.value.code == 9
+
+
+@pytest.mark.parametrize("S,H", [(128, 4), (512, 36), (77, 2)])
+def test_attention_prefill(ops, oracle, S, H):
+    rng = np.random.default_rng(S + H)
+    q, k, v = (rng.standard_normal((S, H * 64), dtype=np.float32) for _ in range(3))
+    got = ops.attention_prefill(q, k, v, H)
+    ref = oracle.attention_prefill(q, k, v, H)
+    assert_close_rms(got, ref)
+    assert np.array_equal(got[0], v[0]) or np.abs(got[0] - v[0]).max() <= 1e-6
+
+
+def test_attention_decode_cfg2(ops, oracle):
+    """Config 2 decode: 1 query against a KV cache of length 1024."""
+    rng = np.random.default_rng(2)
+    H, hd, cap = 36, 64, 1024
+    pos = cap - 1
+    kc = np.zeros((H, cap, hd), np.float32)
+    vc = np.zeros((H, cap, hd), np.float32)
+    kraw = rng.standard_normal((pos, H * hd), dtype=np.float32)
+    for h in range(H):  # rotated keys at their positions 0..pos-1, raw values
+        kc[h, :pos, :] = oracle.rope(kraw[:, h * hd:(h + 1) * hd], 10000.0, 0)
+    vc[:, :pos, :] = rng.standard_normal((H, pos, hd), dtype=np.float32)
+    q, kn, vn = (rng.standard_normal(H * hd, dtype=np.float32) for _ in range(3))
+    kc2, vc2 = kc.copy(), vc.copy()
+    got = ops.attention_decode(q, kn, vn, kc, vc, pos)
+    ref = oracle.attention_decode(q, kn, vn, kc2, vc2, pos)
+    assert_close_rms(got, ref)
+    assert np.array_equal(bits(kc[:, pos]), bits(kc2[:, pos]))  # appended rotated k, bitwise
+    assert np.array_equal(vc[:, pos], vc2[:, pos])
