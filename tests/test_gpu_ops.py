@@ -91,7 +91,9 @@ def test_rmsnorm_softmax(ops, oracle):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((9, 2304), dtype=np.float32) * 3
     g = rng.uniform(0.5, 1.5, 2304).astype(np.float32)
-    assert_close_rms(ops.rmsnorm(x, g, 1e-5), oracle.rmsnorm(x, g, 1e-5), 1e-6)
+    # the sum of squares is a tree sum instead of the reference's left-to-right
+    # loop: ~sqrt(cols) * 2^-24 relative in the row scale
+    assert_close_rms(ops.rmsnorm(x, g, 1e-5), oracle.rmsnorm(x, g, 1e-5), 1e-5)
     p = rng.standard_normal((37, 300), dtype=np.float32) * 4
     for causal in (False, True):
         got, ref = ops.softmax(p, causal), oracle.softmax(p, causal)
