@@ -19,7 +19,22 @@ enum GemvEpi {
     EPI_STORE = 0,    // Y = acc * scale
     EPI_RESIDUAL = 1, // Y = R + acc * scale              (OP_GEMM then OP_EWADD)
     EPI_SILU_MUL = 2, // pairs of 16-row tiles (gate, up): Y = silu(g) * u and its terms
+    EPI_ARGMAX = 3,   // Y = acc (* scale), plus the row argmax folded into keys[M]
 };
+
+// Argmax keys: (order-preserving bits of the value << 32) | (0xffffffff - index),
+// combined with 64-bit atomicMax -> the largest value, lowest index on ties
+// (the strict `>` scan of OP_TOPK_IDX). 0 = empty.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t u = __float_as_uint(v);
+    uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xffffffffu - idx);
+}
+__device__ __forceinline__ int32_t argmax_key_index(unsigned long long k) {
+    return (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+}
+constexpr unsigned long long ARGMAX_NAN0_KEY = 0xffffffffffffffffull;  // NaN at index 0
+constexpr int KEY_SLOTS = 64;  // argmax slots per row (spreads the atomics)
 
 struct GemvArgs {
     const void *W = nullptr; // [N][K] int8 or bf16 bits, rows 16-byte aligned
@@ -38,6 +53,7 @@ struct GemvArgs {
     uint16_t *Aout = nullptr; // EPI_SILU_MUL: terms of Y, [T][M][ldaout]
     int ldaout = 0;
     int Tout = 3;
+    unsigned long long *keys = nullptr; // EPI_ARGMAX: [M], zeroed before the launch
 };
 int launch_gemv(const GemvArgs &a, hipStream_t st);
 

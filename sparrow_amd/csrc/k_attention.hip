@@ -9,9 +9,10 @@
 //
 // Decode (tools/p12_build_minicpm.py:941-967): per (sequence, head, 64-
 // position split) one wavefront rotates q and the new k at `pos`, appends the
-// rotated k and raw v to the f32 cache, scores its positions (one lane per
-// position, each lane streaming its 256-byte K row), and accumulates its
-// share of p.V; a combine kernel merges the splits (flash-decoding).
+// rotated k and raw v to the f32 cache, scores its positions (16 lanes per
+// 256-byte K row, four rows per coalesced load instruction, all loads of
+// the split in flight together), and accumulates its share of p.V; a
+// combine kernel merges the splits (flash-decoding).
 //
 // Both change the order of the reference's sums (E contract: 1e-4 of the
 // output RMS); RoPE, the scale multiply and every exp_f are bitwise.
@@ -213,16 +214,15 @@ int launch_attention_prefill(const float *qrot, const float *krot, const float *
 }
 
 // ---------------------------------------------------------------- decode
-// One wavefront per (sequence b, head h, split s of 64 positions).
-// q/k_new/v_new: rows of [B][ldq]; head h at column h*64 (k, v via their own
-// base pointers). Cache for sequence b, head h: kc + ((b*H + h)*cap)*64.
-
-
+// One wavefront per (sequence b, head h, split s of 64 positions). Lane =
+// (group grp = lane/16, dim quad q = lane%16): a K or V row (64 f32 = 256 B)
+// is read by the 16 lanes of a group as float4s, four rows per load
+// instruction; the 16 row loads of the split are issued before use.
 __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeArgs a) {
     __shared__ float qs[64], kn[64], vn[64];
     __shared__ float es[64];
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x, grp = lane >> 4, q = lane & 15;
     const int pos = a.posp ? *a.posp : a.pos;
     const int live = pos + 1;
     float *part = a.part + (((size_t)b * a.H + h) * a.NS + s) * 66;
@@ -233,6 +233,16 @@ __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeArgs a) {
             part[1] = 0.0f;
         }
         return;
+    }
+    const float *kc = a.kc + ((size_t)b * a.H + h) * a.cap * 64;
+    const float *vc = a.vc + ((size_t)b * a.H + h) * a.cap * 64;
+    // K rows of this split (positions < pos come from the cache)
+    float4 kv[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int p = p0 + it * 4 + grp;
+        kv[it] = p < pos ? *(const float4 *)(kc + (size_t)p * 64 + 4 * q)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const float *qr = a.q + (size_t)b * a.ldq + h * 64;
     const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
@@ -249,68 +259,104 @@ __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeArgs a) {
     }
     vn[lane] = vr[lane];
     __syncthreads();
-    float *kc = a.kc + ((size_t)b * a.H + h) * a.cap * 64;
-    float *vc = a.vc + ((size_t)b * a.H + h) * a.cap * 64;
     if (pos >= p0 && pos < p0 + 64) {  // this split owns the new position
-        kc[(size_t)pos * 64 + lane] = kn[lane];
-        vc[(size_t)pos * 64 + lane] = vn[lane];
+        float *kw = a.kc + ((size_t)b * a.H + h) * a.cap * 64;
+        float *vw = a.vc + ((size_t)b * a.H + h) * a.cap * 64;
+        kw[(size_t)pos * 64 + lane] = kn[lane];
+        vw[(size_t)pos * 64 + lane] = vn[lane];
     }
-    // scores: lane = position
-    const int p = p0 + lane;
-    float sc = -INFINITY;
-    if (p < pos) {
-        const float4 *kp = (const float4 *)(kc + (size_t)p * 64);
-        float acc = 0.0f;
+    // V rows, issued before the scores are reduced
+    float4 vv[16];
 #pragma unroll
-        for (int d4 = 0; d4 < 16; ++d4) {
-            float4 kv = kp[d4];
-            acc = __builtin_fmaf(qs[d4 * 4 + 0], kv.x, acc);
-            acc = __builtin_fmaf(qs[d4 * 4 + 1], kv.y, acc);
-            acc = __builtin_fmaf(qs[d4 * 4 + 2], kv.z, acc);
-            acc = __builtin_fmaf(qs[d4 * 4 + 3], kv.w, acc);
-        }
-        sc = acc * a.scale;
-    } else if (p == pos) {
-        float acc = 0.0f;
-        for (int d = 0; d < 64; ++d) acc = __builtin_fmaf(qs[d], kn[d], acc);
-        sc = acc * a.scale;
+    for (int it = 0; it < 16; ++it) {
+        const int p = p0 + it * 4 + grp;
+        vv[it] = p < pos ? *(const float4 *)(vc + (size_t)p * 64 + 4 * q)
+                         : (p == pos ? make_float4(vn[4 * q], vn[4 * q + 1], vn[4 * q + 2],
+                                                   vn[4 * q + 3])
+                                     : make_float4(0.f, 0.f, 0.f, 0.f));
     }
-    const float mx = wave_max(sc);
-    const float e = (sc == -INFINITY) ? 0.0f : exp_f(sc - mx);
+    const float4 qv = make_float4(qs[4 * q], qs[4 * q + 1], qs[4 * q + 2], qs[4 * q + 3]);
+    const float4 kq = make_float4(kn[4 * q], kn[4 * q + 1], kn[4 * q + 2], kn[4 * q + 3]);
+    float myscore = -INFINITY;
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int p = p0 + it * 4 + grp;
+        const float4 k4 = p == pos ? kq : kv[it];
+        float d = qv.x * k4.x;
+        d = __builtin_fmaf(qv.y, k4.y, d);
+        d = __builtin_fmaf(qv.z, k4.z, d);
+        d = __builtin_fmaf(qv.w, k4.w, d);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) d += __shfl_xor(d, o, 64);
+        if (q == it) myscore = p <= pos ? d * a.scale : -INFINITY;  // lane (grp, it) keeps row it*4+grp
+    }
+    // lane (grp, q) now holds the score of position p0 + q*4 + grp
+    const float mx = wave_max(myscore);
+    const float e = (myscore == -INFINITY) ? 0.0f : exp_f(myscore - mx);
     const float l = wave_sum(e);
-    es[lane] = e;
+    es[q * 4 + grp] = e;
     __syncthreads();
-    // context: lane = dimension
-    const int np = (live - p0) < 64 ? (live - p0) : 64;
-    float o = 0.0f;
-    for (int j = 0; j < np; ++j) {
-        const int pp = p0 + j;
-        const float v = (pp == pos) ? vn[lane] : vc[(size_t)pp * 64 + lane];
-        o = __builtin_fmaf(es[j], v, o);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const float w = es[it * 4 + grp];
+        o.x = __builtin_fmaf(w, vv[it].x, o.x);
+        o.y = __builtin_fmaf(w, vv[it].y, o.y);
+        o.z = __builtin_fmaf(w, vv[it].z, o.z);
+        o.w = __builtin_fmaf(w, vv[it].w, o.w);
+    }
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+        o.x += __shfl_xor(o.x, off, 64);
+        o.y += __shfl_xor(o.y, off, 64);
+        o.z += __shfl_xor(o.z, off, 64);
+        o.w += __shfl_xor(o.w, off, 64);
     }
     if (lane == 0) {
         part[0] = mx;
         part[1] = l;
     }
-    part[2 + lane] = o;
+    if (grp == 0) {
+        part[2 + 4 * q + 0] = o.x;
+        part[2 + 4 * q + 1] = o.y;
+        part[2 + 4 * q + 2] = o.z;
+        part[2 + 4 * q + 3] = o.w;
+    }
 }
 
 // Merge the splits of (b, h): out = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M};
 // also writes the bf16 terms of the output row (operand of the o-projection).
+// The partials of up to 16 splits are loaded in one batch.
 __global__ __launch_bounds__(64) void attn_decode_combine_kernel(
     const float *__restrict__ part, int NS, int H, float *__restrict__ out, int ldo,
     uint16_t *__restrict__ terms, int T, int ldt, int B) {
     const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     const float *pb = part + ((size_t)b * H + h) * NS * 66;
-    float M = -INFINITY;
-    for (int s = 0; s < NS; ++s) M = fmaxf(M, pb[s * 66]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < NS; ++s) {
-        const float ms = pb[s * 66];
-        if (ms == -INFINITY) continue;
-        const float w = exp_f(ms - M);
-        L = __builtin_fmaf(pb[s * 66 + 1], w, L);
-        O = __builtin_fmaf(pb[s * 66 + 2 + lane], w, O);
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < NS; s0 += 16) {
+        float ms[16], ls[16], os[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int s = s0 + i;
+            ms[i] = s < NS ? pb[s * 66] : -INFINITY;
+            ls[i] = s < NS ? pb[s * 66 + 1] : 0.0f;
+            os[i] = s < NS ? pb[s * 66 + 2 + lane] : 0.0f;
+        }
+        float Mn = M;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Mn = fmaxf(Mn, ms[i]);
+        if (Mn == -INFINITY) continue;
+        const float c = (M == -INFINITY) ? 0.0f : exp_f(M - Mn);
+        L *= c;
+        O *= c;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (ms[i] == -INFINITY) continue;
+            const float w = exp_f(ms[i] - Mn);
+            L = __builtin_fmaf(ls[i], w, L);
+            O = __builtin_fmaf(os[i], w, O);
+        }
+        M = Mn;
     }
     float y = O / L;
     const int col = h * 64 + lane;

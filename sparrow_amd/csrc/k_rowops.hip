@@ -62,9 +62,86 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ dst,
     }
 }
 
+// Same operations for cols % 4 == 0, cols <= 4096: the row is read once into
+// registers (float4 per thread, all loads issued together), so the kernel
+// costs one memory round trip; terms are stored 4 bf16 (8 bytes) at a time.
+template <int U>
+__global__ __launch_bounds__(256) void rmsnorm_v4_kernel(float *__restrict__ dst,
+                                                         const float *__restrict__ src,
+                                                         const float *__restrict__ g, int cols,
+                                                         float eps, uint16_t *__restrict__ terms,
+                                                         int T, int ld_terms, int rows) {
+    __shared__ float sh[4];
+    const int row = blockIdx.x, n4 = cols >> 2;
+    const float4 *p = (const float4 *)(src + (size_t)row * cols);
+    const float4 *g4 = (const float4 *)g;
+    float4 x[U], gg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c = threadIdx.x + u * 256;
+        x[u] = c < n4 ? p[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        gg[u] = c < n4 ? g4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        ss += x[u].x * x[u].x;
+        ss += x[u].y * x[u].y;
+        ss += x[u].z * x[u].z;
+        ss += x[u].w * x[u].w;
+    }
+    ss = block_sum256(ss, sh);
+    ss = ss / (float)cols;
+    const float inv = 1.0f / sqrtf(ss + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c = threadIdx.x + u * 256;
+        if (c >= n4) continue;
+        float y[4] = {x[u].x * inv * gg[u].x, x[u].y * inv * gg[u].y, x[u].z * inv * gg[u].z,
+                      x[u].w * inv * gg[u].w};
+        if (dst) ((float4 *)(dst + (size_t)row * cols))[c] = make_float4(y[0], y[1], y[2], y[3]);
+        if (terms) {
+            for (int t = 0; t < T; ++t) {
+                uint32_t h[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    h[q] = bf16_rne_bits(y[q]);
+                    y[q] = y[q] - bf16_bits_to_f32(h[q]);
+                }
+                uint2 pk = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                *(uint2 *)(terms + ((size_t)t * rows + row) * ld_terms + 4 * c) = pk;
+            }
+        }
+    }
+    if (terms) {
+        for (int i = cols + threadIdx.x; i < ld_terms; i += 256)
+            for (int t = 0; t < T; ++t) terms[((size_t)t * rows + row) * ld_terms + i] = 0;
+    }
+}
+
 int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
                    float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st) {
     if (rows == 0) return VMLM_OK;
+    const bool aligned = cols % 4 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)g & 15) == 0 &&
+                         (!dst || ((uintptr_t)dst & 15) == 0) &&
+                         (!terms || (((uintptr_t)terms & 7) == 0 && ld_terms % 4 == 0));
+    const size_t u = (cols / 4 + 255) / 256;
+    if (aligned && u >= 1 && u <= 4) {
+        switch (u) {
+#define RMS_CASE(U)                                                                            \
+    case U:                                                                                    \
+        rmsnorm_v4_kernel<U><<<(unsigned)rows, 256, 0, st>>>(dst, src, g, (int)cols, eps,     \
+                                                              terms, T, ld_terms, (int)rows); \
+        break;
+            RMS_CASE(1)
+            RMS_CASE(2)
+            RMS_CASE(3)
+            RMS_CASE(4)
+#undef RMS_CASE
+        }
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     rmsnorm_kernel<<<(unsigned)rows, 256, 0, st>>>(dst, src, g, (int)cols, eps, terms, T,
                                                    ld_terms, (int)rows);
     VMLM_HIP_CHECK(hipGetLastError());

@@ -24,21 +24,33 @@
 
 namespace vmlm {
 
-// tok[b] -> h[b] = bf16 row of embed (OP_EMB with its index guards) happens in
-// launch_emb_bf16; after the LM head, argmax writes tok[b]; this kernel then
-// records tok into tokens_out[step] and advances step and position.
-__global__ void advance_kernel(const int32_t *__restrict__ tok, int32_t *__restrict__ out,
-                               int B, int max_steps, int *step, int *pos, int *guard) {
+// Folds the LM head's argmax slots of each sequence into tok[b] (the
+// TOPK_IDX result fed to the next step's EMB), clears the slots for the next
+// step, and -- when `out` is given -- records tok into tokens_out[step] and
+// advances step and position. One wavefront per sequence.
+__global__ __launch_bounds__(64) void argmax_advance_kernel(
+    unsigned long long *__restrict__ keys, int32_t *__restrict__ tok, int32_t *__restrict__ out,
+    int B, int max_steps, int *step, int *pos, int *guard) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    unsigned long long k = keys[(size_t)b * KEY_SLOTS + lane];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned long long ok = __shfl_xor(k, o, 64);
+        k = ok > k ? ok : k;
+    }
+    keys[(size_t)b * KEY_SLOTS + lane] = 0ull;
+    if (lane != 0) return;
+    const int32_t t = k ? argmax_key_index(k) : 0;  // all-NaN row: the scan keeps index 0
+    tok[b] = t;
+    if (!out) return;
     const int s = *step;
-    for (int b = threadIdx.x; b < B; b += blockDim.x) {
-        if (s < max_steps) out[(size_t)s * B + b] = tok[b];
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        if (s >= max_steps) atomicOr(guard, 2);
-        *step = s + 1;
-        *pos = *pos + 1;
-    }
+    if (s < max_steps) out[(size_t)s * B + b] = t;
+    else atomicOr(guard, 2);
+}
+
+__global__ void step_advance_kernel(int *step, int *pos) {
+    *step = *step + 1;
+    *pos = *pos + 1;
 }
 
 // Scatter rotated K / raw V of prefill rows [b*S + s][...] into the cache.
@@ -95,6 +107,7 @@ struct vmlm_decoder {
     float *part = nullptr, *logits = nullptr;
     uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
     int32_t *tok = nullptr, *tokens_out = nullptr;
+    unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     int *pos = nullptr, *step = nullptr;
     int NS = 0;
     float rope_step = 0.0f;
@@ -127,6 +140,31 @@ int dalloc(vmlm_decoder *d, T **p, size_t count) {
     VMLM_HIP_CHECK(hipMalloc(&q, (count ? count : 1) * sizeof(T)));
     d->allocs.push_back(q);
     *p = (T *)q;
+    return VMLM_OK;
+}
+
+// LM head over the final-normed terms in d->t_x with the argmax folded into
+// its epilogue, then the argmax slots -> d->tok (and tokens_out when recording).
+int enqueue_head(vmlm_decoder *d, bool record) {
+    GemvArgs lm;
+    lm.W = d->lm_head;
+    lm.w_int8 = false;
+    lm.A = d->t_x;
+    lm.T = 3;
+    lm.lda = (int)d->H;
+    lm.M = (int)d->B;
+    lm.N = (int)d->V;
+    lm.K = (int)d->H;
+    lm.Y = d->logits;
+    lm.ldy = (int)d->V;
+    lm.epi = EPI_ARGMAX;
+    lm.keys = d->keys;
+    int rc = launch_gemv(lm, d->st);
+    if (rc) return rc;
+    argmax_advance_kernel<<<(unsigned)d->B, 64, 0, d->st>>>(
+        d->keys, d->tok, record ? d->tokens_out : nullptr, (int)d->B, (int)d->cap, d->step,
+        d->pos, guard_flag_ptr());
+    VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
 
@@ -219,21 +257,8 @@ int enqueue_step(vmlm_decoder *d) {
     }
     if ((rc = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, T, H, st)))
         return rc;
-    GemvArgs lm;
-    lm.W = d->lm_head;
-    lm.w_int8 = false;
-    lm.A = d->t_x;
-    lm.T = T;
-    lm.lda = H;
-    lm.M = B;
-    lm.N = (int)d->V;
-    lm.K = H;
-    lm.Y = d->logits;
-    lm.ldy = (int)d->V;
-    if ((rc = launch_gemv(lm, st))) return rc;
-    if ((rc = launch_argmax(d->logits, B, d->V, d->V, nullptr, d->tok, st))) return rc;
-    advance_kernel<<<1, 64, 0, st>>>(d->tok, d->tokens_out, B, (int)d->cap, d->step, d->pos,
-                                     guard_flag_ptr());
+    if ((rc = enqueue_head(d, true))) return rc;
+    step_advance_kernel<<<1, 1, 0, st>>>(d->step, d->pos);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -303,9 +328,10 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->t_att, 3 * d->B * d->H)) ||
         (rc = dalloc(d, &d->t_act, 3 * d->B * d->I)) || (rc = dalloc(d, &d->tok, d->B)) ||
         (rc = dalloc(d, &d->tokens_out, d->cap * d->B)) || (rc = dalloc(d, &d->pos, 1)) ||
-        (rc = dalloc(d, &d->step, 1)))
+        (rc = dalloc(d, &d->step, 1)) || (rc = dalloc(d, &d->keys, d->B * KEY_SLOTS)))
         return cleanup(rc);
-    if ((e = hipMemsetAsync(d->kc, 0, kvn * 4, d->st)) != hipSuccess ||
+    if ((e = hipMemsetAsync(d->keys, 0, d->B * KEY_SLOTS * 8, d->st)) != hipSuccess ||
+        (e = hipMemsetAsync(d->kc, 0, kvn * 4, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->vc, 0, kvn * 4, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->pos, 0, 4, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->step, 0, 4, d->st)) != hipSuccess ||
@@ -501,19 +527,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         if ((r = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, T, (int)H,
                                 st)))
             return r;
-        GemvArgs lm;
-        lm.W = d->lm_head;
-        lm.w_int8 = false;
-        lm.A = d->t_x;
-        lm.T = T;
-        lm.lda = (int)H;
-        lm.M = (int)B;
-        lm.N = (int)d->V;
-        lm.K = (int)H;
-        lm.Y = d->logits;
-        lm.ldy = (int)d->V;
-        if ((r = launch_gemv(lm, st))) return r;
-        if ((r = launch_argmax(d->logits, B, d->V, d->V, nullptr, d->tok, st))) return r;
+        if ((r = enqueue_head(d, false))) return r;
         int zero = 0, p = (int)S;
         VMLM_HIP_CHECK(hipMemcpyAsync(d->step, &zero, 4, hipMemcpyHostToDevice, st));
         VMLM_HIP_CHECK(hipMemcpyAsync(d->pos, &p, 4, hipMemcpyHostToDevice, st));
