@@ -135,9 +135,12 @@ def main():
     log(f"q8 GEMV: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     dec.close()
 
-    dec1, wall1, ev1, _, _ = run_decode(cfg, W, 1, args.steps, args.warmup)
-    dec1.close()
-    log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
+    if args.batch == 1:
+        wall1 = wall
+    else:
+        dec1, wall1, _, _, _ = run_decode(cfg, W, 1, args.steps, args.warmup)
+        dec1.close()
+        log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
 
     cpu = None
     if not args.no_cpu:

@@ -156,7 +156,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
                     size_t m, size_t n, size_t k, hipStream_t st) {
     if (m == 0 || n == 0) return VMLM_OK;
     const size_t esz = wi8 ? 1 : 2;
-    const size_t Kp = round_up(k == 0 ? 1 : k, 64);
+    const size_t Kp = round_up(k == 0 ? 1 : k, 128);  // one 128-byte GEMV chunk covers 128 k
     Stage stg(st);
     const void *Wd = W;
     if (Kp != k || ((uintptr_t)W & 15)) {
@@ -467,8 +467,6 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
     VMLM_GUARD(pos < cap, "WRITECOL: column %zu beyond cache capacity %zu", pos, cap);
     VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
     hipStream_t st = as_stream(stream);
-    Stage stg(st);
-    const int NS = (int)((pos + 1 + 63) / 64);
     DecodeArgs a;
     a.q = q;
     a.k_new = k_new;
@@ -482,9 +480,6 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
     a.pos = (int)pos;
     a.step = -2.0f / (float)head_dim * host_ln_f(theta);
     a.scale = scale;
-    a.part = stg.alloc<float>((size_t)n_heads * NS * 66);
-    a.NS = NS;
-    STAGE_OK(stg);
     return launch_attention_decode(a, 1, out, (int)(n_heads * head_dim), nullptr, 0, 0, st);
 }
 

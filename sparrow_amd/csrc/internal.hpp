@@ -103,8 +103,6 @@ struct DecodeArgs {
     const int *posp;  // device position (graph replay) or null -> `pos`
     int pos;
     float step, scale;  // RoPE step -2/64*ln_f(theta); score scale
-    float *part;        // [B][H][NS][66] split partials
-    int NS;             // splits of 64 positions (>= ceil((pos+1)/64))
 };
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st);

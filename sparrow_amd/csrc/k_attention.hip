@@ -214,156 +214,208 @@ int launch_attention_prefill(const float *qrot, const float *krot, const float *
 }
 
 // ---------------------------------------------------------------- decode
-// One wavefront per (sequence b, head h, split s of 64 positions). Lane =
-// (group grp = lane/16, dim quad q = lane%16): a K or V row (64 f32 = 256 B)
-// is read by the 16 lanes of a group as float4s, four rows per load
-// instruction; the 16 row loads of the split are issued before use.
-__global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeArgs a) {
-    __shared__ float qs[64], kn[64], vn[64];
-    __shared__ float es[64];
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x, grp = lane >> 4, q = lane & 15;
-    const int pos = a.posp ? *a.posp : a.pos;
-    const int live = pos + 1;
-    float *part = a.part + (((size_t)b * a.H + h) * a.NS + s) * 66;
-    const int p0 = s * 64;
-    if (p0 >= live) {
-        if (lane == 0) {
-            part[0] = -INFINITY;
-            part[1] = 0.0f;
-        }
-        return;
-    }
-    const float *kc = a.kc + ((size_t)b * a.H + h) * a.cap * 64;
-    const float *vc = a.vc + ((size_t)b * a.H + h) * a.cap * 64;
-    // K rows of this split (positions < pos come from the cache)
-    float4 kv[16];
+// Decode attention, one workgroup per (head, sequence): the new query and key
+// are rotated once, the new key/value row is appended to the cache, and the
+// AD_NW waves stride over the positions in chunks of 64 (wave w takes chunks
+// w, w + AD_NW, ...). Each chunk leaves (m_c, l_c, o_c) = (max score,
+// sum e^{s - m_c}, sum e^{s - m_c} v) in LDS; after a barrier they are merged
+// in chunk order,
+//   out = sum_c o_c e^{m_c - M} / sum_c l_c e^{m_c - M},
+// so the result does not depend on the wave count.
+// Lane (grp, q) of a wave holds dims 4q..4q+3 of positions p0 + 4*it + grp
+// (it = 0..15): one load instruction covers 4 consecutive 256-byte rows.
+// All 32 row loads of a chunk are issued together, unconditionally.
+// AD_NW is 8 when the (head, sequence) pairs are fewer than the CUs (one
+// workgroup per CU), else 4 with a register budget for three workgroups per
+// CU so that all of them are resident at once.
+constexpr int BUF_RSRC_WORD3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
+
+// DPP lane moves inside a row of 16 lanes (row_mirror: lane i <- 15 - i;
+// row_half_mirror: i <- 7 - i within each 8; quad_perm [3,2,1,0] and
+// [1,0,3,2]): partners that differ in bit 3, 2, 1, 0 of the lane index.
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_QUAD_REV = 0x1B, DPP_QUAD_SWAP = 0xB1;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// One stage of the transposing butterfly: N values per lane become N/2 sums;
+// the lane with `up` keeps the upper half and sends the lower.
+template <int N, int CTRL>
+__device__ __forceinline__ void bfly_stage(float (&d)[16], bool up) {
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int p = p0 + it * 4 + grp;
-        kv[it] = p < pos ? *(const float4 *)(kc + (size_t)p * 64 + 4 * q)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const float *qr = a.q + (size_t)b * a.ldq + h * 64;
-    const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
-    const float *vr = a.v_new + (size_t)b * a.ldq + h * 64;
-    const float fpos = (float)pos;
-    if (lane < 32) {
-        float y1, y2;
-        rope_pair(qr[lane], qr[lane + 32], fpos, lane, a.step, &y1, &y2);
-        qs[lane] = y1;
-        qs[lane + 32] = y2;
-        rope_pair(kr[lane], kr[lane + 32], fpos, lane, a.step, &y1, &y2);
-        kn[lane] = y1;
-        kn[lane + 32] = y2;
-    }
-    vn[lane] = vr[lane];
-    __syncthreads();
-    if (pos >= p0 && pos < p0 + 64) {  // this split owns the new position
-        float *kw = a.kc + ((size_t)b * a.H + h) * a.cap * 64;
-        float *vw = a.vc + ((size_t)b * a.H + h) * a.cap * 64;
-        kw[(size_t)pos * 64 + lane] = kn[lane];
-        vw[(size_t)pos * 64 + lane] = vn[lane];
-    }
-    // V rows, issued before the scores are reduced
-    float4 vv[16];
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int p = p0 + it * 4 + grp;
-        vv[it] = p < pos ? *(const float4 *)(vc + (size_t)p * 64 + 4 * q)
-                         : (p == pos ? make_float4(vn[4 * q], vn[4 * q + 1], vn[4 * q + 2],
-                                                   vn[4 * q + 3])
-                                     : make_float4(0.f, 0.f, 0.f, 0.f));
-    }
-    const float4 qv = make_float4(qs[4 * q], qs[4 * q + 1], qs[4 * q + 2], qs[4 * q + 3]);
-    const float4 kq = make_float4(kn[4 * q], kn[4 * q + 1], kn[4 * q + 2], kn[4 * q + 3]);
-    float myscore = -INFINITY;
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int p = p0 + it * 4 + grp;
-        const float4 k4 = p == pos ? kq : kv[it];
-        float d = qv.x * k4.x;
-        d = __builtin_fmaf(qv.y, k4.y, d);
-        d = __builtin_fmaf(qv.z, k4.z, d);
-        d = __builtin_fmaf(qv.w, k4.w, d);
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) d += __shfl_xor(d, o, 64);
-        if (q == it) myscore = p <= pos ? d * a.scale : -INFINITY;  // lane (grp, it) keeps row it*4+grp
-    }
-    // lane (grp, q) now holds the score of position p0 + q*4 + grp
-    const float mx = wave_max(myscore);
-    const float e = (myscore == -INFINITY) ? 0.0f : exp_f(myscore - mx);
-    const float l = wave_sum(e);
-    es[q * 4 + grp] = e;
-    __syncthreads();
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const float w = es[it * 4 + grp];
-        o.x = __builtin_fmaf(w, vv[it].x, o.x);
-        o.y = __builtin_fmaf(w, vv[it].y, o.y);
-        o.z = __builtin_fmaf(w, vv[it].z, o.z);
-        o.w = __builtin_fmaf(w, vv[it].w, o.w);
-    }
-#pragma unroll
-    for (int off = 16; off < 64; off <<= 1) {
-        o.x += __shfl_xor(o.x, off, 64);
-        o.y += __shfl_xor(o.y, off, 64);
-        o.z += __shfl_xor(o.z, off, 64);
-        o.w += __shfl_xor(o.w, off, 64);
-    }
-    if (lane == 0) {
-        part[0] = mx;
-        part[1] = l;
-    }
-    if (grp == 0) {
-        part[2 + 4 * q + 0] = o.x;
-        part[2 + 4 * q + 1] = o.y;
-        part[2 + 4 * q + 2] = o.z;
-        part[2 + 4 * q + 3] = o.w;
+    for (int j = 0; j < N / 2; ++j) {
+        const float send = up ? d[j] : d[j + N / 2];
+        const float keep = up ? d[j + N / 2] : d[j];
+        d[j] = keep + dpp_f<CTRL>(send);
     }
 }
 
-// Merge the splits of (b, h): out = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M};
-// also writes the bf16 terms of the output row (operand of the o-projection).
-// The partials of up to 16 splits are loaded in one batch.
-__global__ __launch_bounds__(64) void attn_decode_combine_kernel(
-    const float *__restrict__ part, int NS, int H, float *__restrict__ out, int ldo,
-    uint16_t *__restrict__ terms, int T, int ldt, int B) {
-    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const float *pb = part + ((size_t)b * H + h) * NS * 66;
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int s0 = 0; s0 < NS; s0 += 16) {
-        float ms[16], ls[16], os[16];
+// Max and sum over the 64 lanes as wave-uniform values: DPP inside each
+// row, then the four row results read out in a fixed order.
+__device__ __forceinline__ float rows_to_uniform_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_REV>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_SWAP>(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float rows_to_uniform_sum(float v) {
+    v += dpp_f<DPP_ROW_MIRROR>(v);
+    v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_f<DPP_QUAD_REV>(v);
+    v += dpp_f<DPP_QUAD_SWAP>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+constexpr int AD_PART = 68;                 // floats per chunk partial: m, l, pad, o[64]
+
+template <int AD_NW>
+__global__ __launch_bounds__(AD_NW * 64) __attribute__((amdgpu_waves_per_eu(AD_NW == 4 ? 3 : 2)))
+void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int T, int ldt,
+                        int B) {
+    extern __shared__ float cpart[];  // [ceil(cap / 64)][AD_PART]
+    __shared__ float qs[64], kn[64], vn[64];
+    __shared__ float es[AD_NW][64];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = lane >> 4, q = lane & 15;
+    const int pos = a.posp ? *a.posp : a.pos;
+    const int nch = (pos + 1 + 63) / 64;
+    const size_t head = ((size_t)b * a.H + h) * a.cap * 64;
+
+    // Cache rows through buffer loads whose range ends at row `pos`: rows at
+    // or past it (the new row, unused rows, chunks past the last) read as
+    // zero without a memory access, so every wave issues its first chunk
+    // unconditionally and the memory counter waits stay exact.
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(a.kc + head), 0, pos * 256, BUF_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + head), 0, pos * 256, BUF_RSRC_WORD3);
+    float4 kv[16], vv[16];
+    auto load_chunk = [&](int c) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int s = s0 + i;
-            ms[i] = s < NS ? pb[s * 66] : -INFINITY;
-            ls[i] = s < NS ? pb[s * 66 + 1] : 0.0f;
-            os[i] = s < NS ? pb[s * 66 + 2 + lane] : 0.0f;
+        for (int it = 0; it < 16; ++it) {
+            const int off = (c * 64 + it * 4 + grp) * 256 + 16 * q;
+            kv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+            vv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
         }
-        float Mn = M;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) Mn = fmaxf(Mn, ms[i]);
-        if (Mn == -INFINITY) continue;
-        const float c = (M == -INFINITY) ? 0.0f : exp_f(M - Mn);
-        L *= c;
-        O *= c;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (ms[i] == -INFINITY) continue;
-            const float w = exp_f(ms[i] - Mn);
-            L = __builtin_fmaf(ls[i], w, L);
-            O = __builtin_fmaf(os[i], w, O);
+    };
+    // the new q/k/v values first (every lane, unconditionally), then the
+    // chunk rows; the scheduling barriers keep that issue order so the
+    // rotation below waits only for the former
+    const int l32 = lane & 31;
+    const float *qr = a.q + (size_t)b * a.ldq + h * 64;
+    const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
+    const float q1 = qr[l32], q2 = qr[l32 + 32], k1 = kr[l32], k2 = kr[l32 + 32];
+    const float vnew = a.v_new[(size_t)b * a.ldq + h * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave == 0) {
+        if (lane < 32) {
+            const float fpos = (float)pos;
+            float y1, y2;
+            rope_pair(q1, q2, fpos, lane, a.step, &y1, &y2);
+            qs[lane] = y1;
+            qs[lane + 32] = y2;
+            rope_pair(k1, k2, fpos, lane, a.step, &y1, &y2);
+            kn[lane] = y1;
+            kn[lane + 32] = y2;
         }
-        M = Mn;
+        vn[lane] = vnew;
+    }
+    __syncthreads();
+    if (tid < 64) {  // append the new row (no wave reads row `pos` from the cache)
+        a.kc[head + (size_t)pos * 64 + tid] = kn[tid];
+        a.vc[head + (size_t)pos * 64 + tid] = vn[tid];
+    }
+    const float4 qv = make_float4(qs[4 * q], qs[4 * q + 1], qs[4 * q + 2], qs[4 * q + 3]);
+    const float4 kq = make_float4(kn[4 * q], kn[4 * q + 1], kn[4 * q + 2], kn[4 * q + 3]);
+    const float4 vq = make_float4(vn[4 * q], vn[4 * q + 1], vn[4 * q + 2], vn[4 * q + 3]);
+
+    for (int c = wave; c < nch; c += AD_NW) {
+        if (c != wave) load_chunk(c);
+        const int p0 = c * 64;
+        // partial dots (4 dims per lane), then a transposing butterfly over
+        // the 16 lanes of a group: lane (grp, q) ends with position
+        // p0 + 4q + grp (15 DPP exchanges for 16 sums)
+        float d[16];
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int p = p0 + it * 4 + grp;
+            const float4 k4 = p == pos ? kq : kv[it];
+            float t = qv.x * k4.x;
+            t = __builtin_fmaf(qv.y, k4.y, t);
+            t = __builtin_fmaf(qv.z, k4.z, t);
+            d[it] = __builtin_fmaf(qv.w, k4.w, t);
+        }
+        bfly_stage<16, DPP_ROW_MIRROR>(d, (q & 8) != 0);
+        bfly_stage<8, DPP_ROW_HALF_MIRROR>(d, (q & 4) != 0);
+        bfly_stage<4, DPP_QUAD_REV>(d, (q & 2) != 0);
+        bfly_stage<2, DPP_QUAD_SWAP>(d, (q & 1) != 0);
+        const float sc = p0 + 4 * q + grp <= pos ? d[0] * a.scale : -INFINITY;
+        const float mc = rows_to_uniform_max(sc);  // chunk c holds position p0 <= pos: finite
+        const float e = sc == -INFINITY ? 0.0f : exp_f(sc - mc);
+        const float lc = rows_to_uniform_sum(e);
+        es[wave][4 * q + grp] = e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const float w = es[wave][it * 4 + grp];
+            const float4 v4 = p0 + it * 4 + grp == pos ? vq : vv[it];
+            o.x = __builtin_fmaf(w, v4.x, o.x);
+            o.y = __builtin_fmaf(w, v4.y, o.y);
+            o.z = __builtin_fmaf(w, v4.z, o.z);
+            o.w = __builtin_fmaf(w, v4.w, o.w);
+        }
+#pragma unroll
+        for (int off = 16; off < 64; off <<= 1) {
+            o.x += __shfl_xor(o.x, off, 64);
+            o.y += __shfl_xor(o.y, off, 64);
+            o.z += __shfl_xor(o.z, off, 64);
+            o.w += __shfl_xor(o.w, off, 64);
+        }
+        float *pc = cpart + (size_t)c * AD_PART;
+        if (lane == 0) {
+            pc[0] = mc;
+            pc[1] = lc;
+        }
+        if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+    float M = cpart[0];
+    for (int c = 1; c < nch; ++c) M = fmaxf(M, cpart[c * AD_PART]);
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        const float f = exp_f(cpart[c * AD_PART] - M);
+        L = __builtin_fmaf(cpart[c * AD_PART + 1], f, L);
+        O = __builtin_fmaf(cpart[c * AD_PART + 4 + tid], f, O);
     }
     float y = O / L;
-    const int col = h * 64 + lane;
+    const int col = h * 64 + tid;
     out[(size_t)b * ldo + col] = y;
     if (terms) {
         for (int t = 0; t < T; ++t) {
-            uint32_t hb = bf16_rne_bits(y);
+            const uint32_t hb = bf16_rne_bits(y);
             y = y - bf16_bits_to_f32(hb);
             terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
         }
@@ -372,11 +424,15 @@ __global__ __launch_bounds__(64) void attn_decode_combine_kernel(
 
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st) {
-    dim3 grid(a.NS, a.H, B);
-    attn_decode_split_kernel<<<grid, 64, 0, st>>>(a);
-    VMLM_HIP_CHECK(hipGetLastError());
-    attn_decode_combine_kernel<<<dim3(a.H, B), 64, 0, st>>>(a.part, a.NS, a.H, out, ldo,
-                                                            terms, T, ldt, B);
+    VMLM_GUARD(a.cap >= 1 && a.H >= 1 && B >= 1, "attention decode: empty shape");
+    const size_t lds = (size_t)((a.cap + 63) / 64) * AD_PART * sizeof(float);
+    VMLM_GUARD(lds <= 96 * 1024, "attention decode: cache capacity %d beyond %d positions",
+               a.cap, 96 * 1024 / (AD_PART * 4) * 64);
+    VMLM_GUARD((size_t)a.cap * 256 <= 0x7fffffffu, "attention decode: cache row range too large");
+    if (a.H * B < 256)
+        attn_decode_kernel<8><<<dim3(a.H, B), 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+    else
+        attn_decode_kernel<4><<<dim3(a.H, B), 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

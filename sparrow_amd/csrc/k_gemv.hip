@@ -6,16 +6,18 @@
 //
 // Design (gfx950):
 //  * One workgroup = 8 wavefronts on one 16-row output tile (or a gate/up
-//    pair of tiles). The waves split K; each wave issues ALL of its weight
-//    loads (16 bytes per lane per 64-wide K step, a wave reading 16 rows x
-//    64 B per instruction) before it consumes any, so a launch costs one HBM
-//    round trip plus streaming time; the waves meet in LDS.
+//    pair of tiles); the waves split K into 128-byte chunks and meet in LDS.
+//  * Loads are shaped for full cache lines: a chunk (16 rows x 128 B) is two
+//    load instructions of 8 rows x 128 B, every lane 16 B. Each wave issues
+//    all of its chunk loads before consuming any (one HBM round trip per
+//    launch), then passes each chunk through a 2.3 KB per-wave LDS buffer to
+//    the MFMA operand layout (lane (g, r) <- row r, bytes 32g..32g+31).
 //  * The dot products run on v_mfma_f32_16x16x32_bf16. int8 weights convert
 //    to bf16 exactly (|q| <= 127 needs 8 significant bits); the f32
 //    activations arrive pre-split into T bf16 terms (hi+mid+lo, split_bf16),
 //    each an exact product with the weight, accumulated in f32 by the MFMA.
 //    With T*M <= 16 the (term, batch) pairs are the MFMA's A rows (one A
-//    fragment per step, the terms summed in the epilogue); otherwise the
+//    fragment per MFMA, the terms summed in the epilogue); otherwise the
 //    batch rows are the A rows and each term is a separate MFMA.
 //  * Epilogues fuse the scale multiply and the adjacent elementwise ops of
 //    the VM program (EWADD residual; ACT silu + EWMUL with the up
@@ -47,33 +49,59 @@ __device__ __forceinline__ u32x4 ldg16(const void *p) {
 }
 __device__ __forceinline__ u32x4 ldg16_cached(const void *p) { return *(const u32x4 *)p; }
 
-constexpr int GEMV_NW = 8;     // wavefronts per workgroup (split of K)
-constexpr int GEMV_MAXS = 12;  // 64-wide K steps per wave per pass (all loads in flight)
+// Orders one wavefront's LDS writes before its following LDS reads (other
+// lanes' data); LDS operations of a wavefront execute in order.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int GEMV_NW = 8;    // wavefronts per workgroup (split of K)
+#ifndef GEMV_MAXC_DEF
+#define GEMV_MAXC_DEF 3
+#endif
+#ifndef GEMV_AR_DEF
+#define GEMV_AR_DEF 3
+#endif
+constexpr int GEMV_MAXC = GEMV_MAXC_DEF;  // 128-byte chunks per wave per pass (all loads in flight)
+constexpr int GEMV_AR = GEMV_AR_DEF;      // activation chunks in flight (ring)
+constexpr int CH_BYTES = 128; // chunk width per row
+constexpr int CH_LD = CH_BYTES + 16;  // padded LDS row
+
+static_assert(GEMV_NW * 64 >= 2 * 16 * 16, "epilogue maps one output per thread");
 
 template <bool WI8, int T, int R, bool BT>
 __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
-    constexpr int TA = BT ? 1 : T;  // A fragment sets per 32-wide half step
-    constexpr int WB = WI8 ? 64 : 128;  // weight bytes per 64-wide K step and row
-    constexpr int WL = WI8 ? 1 : 2;     // 16-byte loads per lane per step
+    constexpr int TA = BT ? 1 : T;            // A fragment sets per MFMA
+    constexpr int KC = WI8 ? 128 : 64;        // k per 128-byte chunk
+    constexpr int NF = KC / 32;               // MFMAs (k-slices of 32) per chunk
+    constexpr int ESZ = WI8 ? 1 : 2;
     __shared__ f32x4 red[GEMV_NW][R][64];
-    __shared__ float ys[R][16][17];
     __shared__ float ssc[R][16];
+    __shared__ __attribute__((aligned(16))) uint8_t wbuf[GEMV_NW][R][16][CH_LD];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    // wave index as a scalar: chunk counts and branches below are wave-uniform
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, rr = lane & 15;
-    const int S = p.K >> 6;
+    const int lrow = lane >> 3, lcol = (lane & 7) * 16;  // load layout: 8 rows x 128 B
+    const int NCH = p.K / KC;
+    // A rows past the live ones re-read row 0: their MFMA output rows are
+    // never read, and unconditional loads keep the memory counters exact
     const int arows = BT ? T * p.M : p.M;
-    const bool arow = rr < arows;
-    const uint16_t *abase = p.A + (size_t)(arow ? rr : 0) * p.lda + g * 16;
+    const uint16_t *abase = p.A + (size_t)(rr < arows ? rr : 0) * p.lda + g * (KC / 4);
 
-    const uint8_t *wrow[R];
+    const uint8_t *wrow[R][2];
 #pragma unroll
-    for (int t = 0; t < R; ++t) {
-        int j = (blockIdx.x * R + t) * 16 + rr;
-        j = j < p.N ? j : p.N - 1;
-        wrow[t] = p.W + (size_t)j * p.K * (WI8 ? 1 : 2) + g * (WB / 4);
-    }
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int j = (blockIdx.x * R + t) * 16 + lrow + 8 * h;
+            j = j < p.N ? j : p.N - 1;
+            wrow[t][h] = p.W + (size_t)j * p.K * ESZ + lcol;
+        }
     if (tid < R * 16) {  // scales for the epilogue, fetched while the weights stream
         const int t = tid >> 4, c = tid & 15;
         int j = (blockIdx.x * R + t) * 16 + c;
@@ -85,121 +113,139 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int base = 0; base < S; base += GEMV_NW * GEMV_MAXS) {
-        const int Sp = (S - base) < GEMV_NW * GEMV_MAXS ? (S - base) : GEMV_NW * GEMV_MAXS;
-        const int s0 = base + (Sp * wave) / GEMV_NW;
-        const int n = base + (Sp * (wave + 1)) / GEMV_NW - s0;
-        u32x4 wv[GEMV_MAXS][R][WL];
-#pragma unroll
-        for (int i = 0; i < GEMV_MAXS; ++i)
-            if (i < n) {
-#pragma unroll
-                for (int t = 0; t < R; ++t)
-#pragma unroll
-                    for (int l = 0; l < WL; ++l)
-                        wv[i][t][l] = ldg16(wrow[t] + (size_t)(s0 + i) * WB + l * 16);
-            }
-        u32x4 av[3][TA][2];
-        auto load_a = [&](int i, u32x4 (&dst)[TA][2]) {
-#pragma unroll
-            for (int tt = 0; tt < TA; ++tt) {
-                if (arow) {
-                    const uint16_t *ap = abase + (BT ? 0 : tt * p.tstride) + (size_t)(s0 + i) * 64;
-                    dst[tt][0] = ldg16_cached(ap);
-                    dst[tt][1] = ldg16_cached(ap + 8);
-                } else {
-                    dst[tt][0] = u32x4{0u, 0u, 0u, 0u};
-                    dst[tt][1] = u32x4{0u, 0u, 0u, 0u};
-                }
-            }
+    for (int base = 0; base < NCH; base += GEMV_NW * GEMV_MAXC) {
+        const int Cp = (NCH - base) < GEMV_NW * GEMV_MAXC ? (NCH - base) : GEMV_NW * GEMV_MAXC;
+        const int c0 = base + (Cp * wave) / GEMV_NW;
+        const int n = base + (Cp * (wave + 1)) / GEMV_NW - c0;
+        // every load below is issued unconditionally (slots past this wave's
+        // n chunks re-read a valid chunk and are not consumed): a load under
+        // a branch makes the compiler drain the whole memory queue before the
+        // next one, serialising the stream into one round trip per chunk
+        auto chunk = [&](int i) {
+            const int c = c0 + i;
+            return c < NCH ? c : NCH - 1;
         };
-        if (n > 0) load_a(0, av[0]);
-        if (n > 1) load_a(1, av[1]);
+        u32x4 av[GEMV_AR][TA][NF];
+        auto load_a = [&](int i, u32x4 (&dst)[TA][NF]) {
+            const uint16_t *ap = abase + (size_t)chunk(i) * KC;
 #pragma unroll
-        for (int i = 0; i < GEMV_MAXS; ++i) {
+            for (int tt = 0; tt < TA; ++tt)
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    dst[tt][f] = ldg16_cached(ap + (BT ? 0 : tt * p.tstride) + 8 * f);
+        };
+        // activation fragments of the first chunks go out first: the memory
+        // counter retires in order, so they must not queue behind the weights
+#pragma unroll
+        for (int i = 0; i < GEMV_AR; ++i) load_a(i, av[i]);
+        u32x4 wv[GEMV_MAXC][R][2];
+#pragma unroll
+        for (int i = 0; i < GEMV_MAXC; ++i)
+#pragma unroll
+            for (int t = 0; t < R; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    wv[i][t][h] = ldg16(wrow[t][h] + (size_t)chunk(i) * CH_BYTES);
+#pragma unroll
+        for (int i = 0; i < GEMV_MAXC; ++i) {
+            u32x4 cur[TA][NF];
+#pragma unroll
+            for (int tt = 0; tt < TA; ++tt)
+#pragma unroll
+                for (int f = 0; f < NF; ++f) cur[tt][f] = av[i % GEMV_AR][tt][f];
+            if (i + GEMV_AR < GEMV_MAXC) load_a(i + GEMV_AR, av[i % GEMV_AR]);
             if (i < n) {
-                if (i + 2 < n) load_a(i + 2, av[(i + 2) % 3]);
 #pragma unroll
                 for (int t = 0; t < R; ++t) {
-                    u32x4 b0, b1;
+                    uint8_t(*buf)[CH_LD] = wbuf[wave][t];
+                    *(u32x4 *)&buf[lrow][lcol] = wv[i][t][0];
+                    *(u32x4 *)&buf[lrow + 8][lcol] = wv[i][t][1];
+                    wave_lds_sync();
+                    const u32x4 r0 = *(const u32x4 *)&buf[rr][g * 32];
+                    const u32x4 r1 = *(const u32x4 *)&buf[rr][g * 32 + 16];
+                    wave_lds_sync();
+                    u32x4 bfr[NF];
                     if constexpr (WI8) {
-                        i8x16_to_bf16(wv[i][t][0], b0, b1);
+                        i8x16_to_bf16(r0, bfr[0], bfr[1]);
+                        i8x16_to_bf16(r1, bfr[2], bfr[3]);
                     } else {
-                        b0 = wv[i][t][0];
-                        b1 = wv[i][t][1];
+                        bfr[0] = r0;
+                        bfr[1] = r1;
                     }
 #pragma unroll
-                    for (int tt = 0; tt < TA; ++tt) {
-                        acc[t] = mfma_bf16(av[i % 3][tt][0], b0, acc[t]);
-                        acc[t] = mfma_bf16(av[i % 3][tt][1], b1, acc[t]);
-                    }
+                    for (int f = 0; f < NF; ++f)
+#pragma unroll
+                        for (int tt = 0; tt < TA; ++tt)
+                            acc[t] = mfma_bf16(cur[tt][f], bfr[f], acc[t]);
                 }
             }
         }
     }
 
-    // ---- cross-wave reduction: D[row = 4g+i][col = rr] of each tile
+    // ---- cross-wave reduction, fused with the epilogue: D[row = 4g+i][col =
+    // rr] of tile t sits in red[*][t][(row / 4) * 16 + col][row % 4]; each
+    // output sums its accumulator row over the waves, then (term, batch) rows
+    // over the terms, in that fixed order
 #pragma unroll
     for (int t = 0; t < R; ++t) red[wave][t][lane] = acc[t];
+    // one output per thread (R * M * 16 <= 512): the residual operand is
+    // fetched before the barrier so its latency overlaps the reduction
+    const bool live = tid < (p.epi == EPI_SILU_MUL ? 1 : R) * p.M * 16;
+    const int et = tid / (p.M * 16), eb = (tid >> 4) % p.M, ecol = tid & 15;
+    const int ej = (blockIdx.x * R + et) * 16 + ecol;
+    const bool ein = live && ej < p.N;
+    float resid = 0.0f;
+    if (ein && p.epi == EPI_RESIDUAL) resid = p.Rr[(size_t)eb * p.ldr + ej];
     __syncthreads();
-    for (int e = tid; e < R * 256; e += GEMV_NW * 64) {
-        const int t = e >> 8, row = (e >> 4) & 15, col = e & 15;
+    auto dsum = [&](int t, int row, int col) {
         const int ln = (row >> 2) * 16 + col, i = row & 3;
         float v = red[0][t][ln][i];
+#pragma unroll
         for (int w = 1; w < GEMV_NW; ++w) v += red[w][t][ln][i];
-        ys[t][row][col] = v;
-    }
-    __syncthreads();
-
-    // ---- epilogue over (tile, batch row, column)
+        return v;
+    };
     auto rowval = [&](int t, int b, int col) {
         if constexpr (BT) {
-            float v = ys[t][b][col];
+            float v = dsum(t, b, col);
 #pragma unroll
-            for (int tt = 1; tt < T; ++tt) v += ys[t][tt * p.M + b][col];
+            for (int tt = 1; tt < T; ++tt) v += dsum(t, tt * p.M + b, col);
             return v;
         } else {
-            return ys[t][b][col];
+            return dsum(t, b, col);
         }
     };
+    if (!live) return;
     if (p.epi == EPI_SILU_MUL) {  // tile 0 = gate rows, tile 1 = up rows
-        for (int e = tid; e < p.M * 16; e += GEMV_NW * 64) {
-            const int b = e >> 4, col = e & 15;
-            const int jo = blockIdx.x * 16 + col;
-            const float gate = rowval(0, b, col) * ssc[0][col];
-            const float up = rowval(R - 1, b, col) * ssc[R - 1][col];
-            float a = (gate / (1.0f + exp_f(-gate))) * up;
-            p.Y[(size_t)b * p.ldy + jo] = a;
-            for (int tt = 0; tt < p.Tout; ++tt) {
-                const uint32_t h = bf16_rne_bits(a);
-                a = a - bf16_bits_to_f32(h);
-                p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
-            }
+        const int jo = blockIdx.x * 16 + ecol;
+        const float gate = rowval(0, eb, ecol) * ssc[0][ecol];
+        const float up = rowval(R - 1, eb, ecol) * ssc[R - 1][ecol];
+        float a = (gate / (1.0f + exp_f(-gate))) * up;
+        p.Y[(size_t)eb * p.ldy + jo] = a;
+        for (int tt = 0; tt < p.Tout; ++tt) {
+            const uint32_t h = bf16_rne_bits(a);
+            a = a - bf16_bits_to_f32(h);
+            p.Aout[((size_t)tt * p.M + eb) * p.ldaout + jo] = (uint16_t)h;
         }
         return;
     }
-    for (int e = tid; e < R * p.M * 16; e += GEMV_NW * 64) {
-        const int t = e / (p.M * 16), b = (e >> 4) % p.M, col = e & 15;
-        const int j = (blockIdx.x * R + t) * 16 + col;
-        float y = 0.0f;
-        const bool in = j < p.N;
-        if (in) {
-            y = p.scale ? rowval(t, b, col) * ssc[t][col] : rowval(t, b, col);
-            if (p.epi == EPI_RESIDUAL) y = p.Rr[(size_t)b * p.ldr + j] + y;
-            p.Y[(size_t)b * p.ldy + j] = y;
-        }
-        if (p.epi == EPI_ARGMAX) {
-            // 16 consecutive threads hold the 16 columns of row b: reduce keys
-            unsigned long long k = 0;
-            if (in && y == y) k = argmax_key(y, (uint32_t)j);
-            if (in && j == 0 && y != y) k = ARGMAX_NAN0_KEY;
+    float y = 0.0f;
+    if (ein) {
+        y = p.scale ? rowval(et, eb, ecol) * ssc[et][ecol] : rowval(et, eb, ecol);
+        if (p.epi == EPI_RESIDUAL) y = resid + y;
+        p.Y[(size_t)eb * p.ldy + ej] = y;
+    }
+    if (p.epi == EPI_ARGMAX) {
+        // 16 consecutive threads hold the 16 columns of row eb: reduce keys
+        unsigned long long k = 0;
+        if (ein && y == y) k = argmax_key(y, (uint32_t)ej);
+        if (ein && ej == 0 && y != y) k = ARGMAX_NAN0_KEY;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                unsigned long long ok = __shfl_xor(k, o, 64);
-                k = ok > k ? ok : k;
-            }
-            if (col == 0 && k) atomicMax(p.keys + (size_t)b * KEY_SLOTS + (blockIdx.x & (KEY_SLOTS - 1)), k);
+        for (int o = 1; o < 16; o <<= 1) {
+            unsigned long long ok = __shfl_xor(k, o, 64);
+            k = ok > k ? ok : k;
         }
+        if (ecol == 0 && k)
+            atomicMax(p.keys + (size_t)eb * KEY_SLOTS + (blockIdx.x & (KEY_SLOTS - 1)), k);
     }
 }
 
@@ -247,7 +293,8 @@ static int launch_r(const GemvParams &p, int T, bool bt, hipStream_t st) {
 
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.M <= 16, "gemv: M=%d outside 1..16", a.M);
-    VMLM_GUARD(a.K > 0 && a.K % 64 == 0, "gemv: K=%d not a positive multiple of 64", a.K);
+    VMLM_GUARD(a.K > 0 && a.K % (a.w_int8 ? 128 : 64) == 0,
+               "gemv: K=%d not a positive multiple of %d", a.K, a.w_int8 ? 128 : 64);
     VMLM_GUARD(a.N > 0, "gemv: N=%d", a.N);
     VMLM_GUARD(((uintptr_t)a.W & 15) == 0 && ((uintptr_t)a.A & 15) == 0 && a.lda % 64 == 0,
                "gemv: operands must be 16-byte aligned with lda %% 64 == 0");

@@ -104,12 +104,11 @@ struct vmlm_decoder {
     float *kc = nullptr, *vc = nullptr;
     // decode activations
     float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
-    float *part = nullptr, *logits = nullptr;
+    float *logits = nullptr;
     uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     int *pos = nullptr, *step = nullptr;
-    int NS = 0;
     float rope_step = 0.0f;
     uint32_t pos_host = 0, step_host = 0;
     bool loaded_globals = false;
@@ -203,8 +202,6 @@ int enqueue_step(vmlm_decoder *d) {
         a.pos = 0;
         a.step = d->rope_step;
         a.scale = d->c.attn_scale;
-        a.part = d->part;
-        a.NS = d->NS;
         if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
         GemvArgs o;
         o.W = d->Wo(l);
@@ -291,7 +288,8 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     const vmlm_decoder_cfg &c = *cfg;
     VMLM_GUARD(c.head_dim == 64, "decoder: head_dim %u unsupported (64 only)", c.head_dim);
     VMLM_GUARD(c.n_heads * c.head_dim == c.hidden, "decoder: hidden != n_heads * head_dim");
-    VMLM_GUARD(c.hidden % 64 == 0 && c.inter % 64 == 0, "decoder: hidden and inter must be multiples of 64");
+    VMLM_GUARD(c.hidden % 128 == 0 && c.inter % 128 == 0,
+               "decoder: hidden and inter must be multiples of 128");
     VMLM_GUARD(c.batch >= 1 && c.batch <= 16, "decoder: batch %u outside 1..16", c.batch);
     VMLM_GUARD(c.cap >= 2 && c.vocab >= 1 && c.n_layers >= 1, "decoder: empty shape");
     VMLM_GUARD(c.theta > 0.0f, "ROPE: theta must be > 0");
@@ -306,7 +304,6 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     d->L = c.n_layers;
     d->w_layer = 4 * d->H * d->H + 3 * d->I * d->H;
     d->s_layer = 5 * d->H + 2 * d->I;
-    d->NS = (int)((d->cap + 63) / 64);
     d->rope_step = -2.0f / 64.0f * host_ln_f(c.theta);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
@@ -323,7 +320,6 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
         (rc = dalloc(d, &d->act, d->B * d->I)) ||
-        (rc = dalloc(d, &d->part, d->B * d->NH * d->NS * 66)) ||
         (rc = dalloc(d, &d->logits, d->B * d->V)) || (rc = dalloc(d, &d->t_x, 3 * d->B * d->H)) ||
         (rc = dalloc(d, &d->t_att, 3 * d->B * d->H)) ||
         (rc = dalloc(d, &d->t_act, 3 * d->B * d->I)) || (rc = dalloc(d, &d->tok, d->B)) ||
