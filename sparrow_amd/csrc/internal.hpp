@@ -20,6 +20,7 @@ enum GemvEpi {
     EPI_RESIDUAL = 1, // Y = R + acc * scale              (OP_GEMM then OP_EWADD)
     EPI_SILU_MUL = 2, // pairs of 16-row tiles (gate, up): Y = silu(g) * u and its terms
     EPI_ARGMAX = 3,   // Y = acc (* scale), plus the row argmax folded into keys[M]
+    EPI_PARTIAL = 4,  // Y[ks][M][ldy] = raw sums of k-slice ks (no scale); consumer reduces
 };
 
 // Argmax keys: (order-preserving bits of the value << 32) | (0xffffffff - index),
@@ -54,6 +55,8 @@ struct GemvArgs {
     int ldaout = 0;
     int Tout = 3;
     unsigned long long *keys = nullptr; // EPI_ARGMAX: [M], zeroed before the launch
+    int tiles = 0; // 16-row tiles per workgroup (1, 2, 4; SiLU: 2, 4); 0 = chosen by shape
+    int ksplit = 1; // k-slices (workgroup rows) for EPI_PARTIAL
 };
 int launch_gemv(const GemvArgs &a, hipStream_t st);
 
@@ -78,6 +81,15 @@ int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n
 // Row / elementwise ops.
 int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
                    float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st);
+// x = base + (sum of ks k-slice partials [ks][rows][ldp]) * scale -> resid;
+// RMSNorm(x) * g -> T bf16 terms [T][rows][cols].
+int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
+                         const float *scale, float *resid, size_t rows, size_t cols,
+                         const float *g, float eps, uint16_t *terms, int T, int ld_terms,
+                         hipStream_t st);
+// SiLU(gate) * up from the partials of the interleaved gate/up projection.
+int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
+                       uint16_t *terms, int T, hipStream_t st);
 int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t st);
 int launch_act(float *dst, size_t n, int kind, hipStream_t st);
 int launch_ew(float *dst, const float *x, const float *y, size_t n, int op, hipStream_t st);
@@ -103,6 +115,11 @@ struct DecodeArgs {
     const int *posp;  // device position (graph replay) or null -> `pos`
     int pos;
     float step, scale;  // RoPE step -2/64*ln_f(theta); score scale
+    // optional: q/k/v as ks k-slice partials [ks][B][ldp] of the q/k/v
+    // projection (q at column 0, k at H*64, v at 2*H*64) times wscale
+    const float *part = nullptr;
+    int ks = 0, ldp = 0;
+    const float *wscale = nullptr;
 };
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st);

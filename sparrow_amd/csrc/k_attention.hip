@@ -279,14 +279,16 @@ __device__ __forceinline__ float rows_to_uniform_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 constexpr int AD_PART = 68;                 // floats per chunk partial: m, l, pad, o[64]
+constexpr int PART_KS_MAX = 16;             // k-slices of partial q/k/v read up front
 
-template <int AD_NW>
+template <int AD_NW, bool PART>
 __global__ __launch_bounds__(AD_NW * 64) __attribute__((amdgpu_waves_per_eu(AD_NW == 4 ? 3 : 2)))
 void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int T, int ldt,
                         int B) {
     extern __shared__ float cpart[];  // [ceil(cap / 64)][AD_PART]
     __shared__ float qs[64], kn[64], vn[64];
     __shared__ float es[AD_NW][64];
+    __shared__ float qkv_s[PART ? 192 : 1];
     const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -316,13 +318,41 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     // chunk rows; the scheduling barriers keep that issue order so the
     // rotation below waits only for the former
     const int l32 = lane & 31;
-    const float *qr = a.q + (size_t)b * a.ldq + h * 64;
-    const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
-    const float q1 = qr[l32], q2 = qr[l32 + 32], k1 = kr[l32], k2 = kr[l32 + 32];
-    const float vnew = a.v_new[(size_t)b * a.ldq + h * 64 + lane];
+    float q1 = 0.f, q2 = 0.f, k1 = 0.f, k2 = 0.f, vnew = 0.f;
+    float pv[PART ? PART_KS_MAX : 1];
+    float wsc = 0.f;
+    if constexpr (PART) {
+        // threads 0..191 each own one of the head's q/k/v columns and load
+        // every k-slice partial of it (index clamped) before the chunk rows
+        const int c = tid < 192 ? tid : 191;
+        const int pcol = (c >> 6) * a.H * 64 + h * 64 + (c & 63);
+        const float *pp = a.part + (size_t)b * a.ldp + pcol;
+        wsc = a.wscale[pcol];
+        const size_t pst = (size_t)B * a.ldp;
+#pragma unroll
+        for (int k = 0; k < PART_KS_MAX; ++k) pv[k] = pp[(k < a.ks ? k : a.ks - 1) * pst];
+    } else {
+        const float *qr = a.q + (size_t)b * a.ldq + h * 64;
+        const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
+        q1 = qr[l32], q2 = qr[l32 + 32], k1 = kr[l32], k2 = kr[l32 + 32];
+        vnew = a.v_new[(size_t)b * a.ldq + h * 64 + lane];
+    }
     __builtin_amdgcn_sched_barrier(0);
     load_chunk(wave);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PART) {  // slices summed in order, then the row scale
+        float v = pv[0];
+#pragma unroll
+        for (int k = 1; k < PART_KS_MAX; ++k)
+            if (k < a.ks) v += pv[k];
+        if (tid < 192) qkv_s[tid] = v * wsc;
+        __syncthreads();
+        q1 = qkv_s[l32];
+        q2 = qkv_s[l32 + 32];
+        k1 = qkv_s[64 + l32];
+        k2 = qkv_s[96 + l32];
+        vnew = qkv_s[128 + lane];
+    }
     if (wave == 0) {
         if (lane < 32) {
             const float fpos = (float)pos;
@@ -429,10 +459,20 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
     VMLM_GUARD(lds <= 96 * 1024, "attention decode: cache capacity %d beyond %d positions",
                a.cap, 96 * 1024 / (AD_PART * 4) * 64);
     VMLM_GUARD((size_t)a.cap * 256 <= 0x7fffffffu, "attention decode: cache row range too large");
-    if (a.H * B < 256)
-        attn_decode_kernel<8><<<dim3(a.H, B), 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
-    else
-        attn_decode_kernel<4><<<dim3(a.H, B), 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+    VMLM_GUARD(!a.part || (a.ks >= 1 && a.ks <= PART_KS_MAX && a.wscale && a.ldp >= 3 * a.H * 64),
+               "attention decode: partial q/k/v need ks, ldp and scales");
+    const dim3 grid(a.H, B);
+    if (a.H * B < 256) {
+        if (a.part)
+            attn_decode_kernel<8, true><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+        else
+            attn_decode_kernel<8, false><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+    } else {
+        if (a.part)
+            attn_decode_kernel<4, true><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+        else
+            attn_decode_kernel<4, false><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+    }
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

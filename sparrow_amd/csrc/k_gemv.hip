@@ -36,7 +36,7 @@ struct GemvParams {
     uint16_t *Aout;
     unsigned long long *keys;
     size_t tstride;
-    int lda, M, N, K, ldy, ldr, ldaout, Tout, epi;
+    int lda, M, N, K, ldy, ldr, ldaout, Tout, epi, ks;
 };
 
 __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
@@ -58,28 +58,27 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 constexpr int GEMV_NW = 8;    // wavefronts per workgroup (split of K)
-#ifndef GEMV_MAXC_DEF
-#define GEMV_MAXC_DEF 3
-#endif
-#ifndef GEMV_AR_DEF
-#define GEMV_AR_DEF 3
-#endif
-constexpr int GEMV_MAXC = GEMV_MAXC_DEF;  // 128-byte chunks per wave per pass (all loads in flight)
-constexpr int GEMV_AR = GEMV_AR_DEF;      // activation chunks in flight (ring)
 constexpr int CH_BYTES = 128; // chunk width per row
 constexpr int CH_LD = CH_BYTES + 16;  // padded LDS row
 
-static_assert(GEMV_NW * 64 >= 2 * 16 * 16, "epilogue maps one output per thread");
-
-template <bool WI8, int T, int R, bool BT>
+// MAXC: 128-byte chunks per wave per pass, all loads in flight; AR:
+// activation chunks in flight (ring); R: 16-row tiles sharing the activation
+// fragments (SiLU: R/2 gate/up pairs).
+template <bool WI8, int T, int R, bool BT, int MAXC, int AR>
 __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
     constexpr int TA = BT ? 1 : T;            // A fragment sets per MFMA
     constexpr int KC = WI8 ? 128 : 64;        // k per 128-byte chunk
     constexpr int NF = KC / 32;               // MFMAs (k-slices of 32) per chunk
     constexpr int ESZ = WI8 ? 1 : 2;
-    __shared__ f32x4 red[GEMV_NW][R][64];
+    // one transpose buffer per wave (tiles pass through it in turn); the
+    // cross-wave reduction reuses the same bytes after a barrier
+    constexpr int WBUF_BYTES = GEMV_NW * 16 * CH_LD;
+    constexpr int RED_BYTES = GEMV_NW * R * 64 * 16;
+    __shared__ __attribute__((aligned(16)))
+    uint8_t smem[WBUF_BYTES > RED_BYTES ? WBUF_BYTES : RED_BYTES];
     __shared__ float ssc[R][16];
-    __shared__ __attribute__((aligned(16))) uint8_t wbuf[GEMV_NW][R][16][CH_LD];
+    auto wbuf = reinterpret_cast<uint8_t(*)[16][CH_LD]>(smem);
+    auto red = reinterpret_cast<f32x4(*)[R][64]>(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -87,7 +86,9 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, rr = lane & 15;
     const int lrow = lane >> 3, lcol = (lane & 7) * 16;  // load layout: 8 rows x 128 B
-    const int NCH = p.K / KC;
+    // split K: workgroup row blockIdx.y takes k-slice [ks * K / KS, ...)
+    const int NCH = p.K / KC / gridDim.y;
+    const int ch0 = blockIdx.y * NCH;
     // A rows past the live ones re-read row 0: their MFMA output rows are
     // never read, and unconditional loads keep the memory counters exact
     const int arows = BT ? T * p.M : p.M;
@@ -113,8 +114,8 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int base = 0; base < NCH; base += GEMV_NW * GEMV_MAXC) {
-        const int Cp = (NCH - base) < GEMV_NW * GEMV_MAXC ? (NCH - base) : GEMV_NW * GEMV_MAXC;
+    for (int base = 0; base < NCH; base += GEMV_NW * MAXC) {
+        const int Cp = (NCH - base) < GEMV_NW * MAXC ? (NCH - base) : GEMV_NW * MAXC;
         const int c0 = base + (Cp * wave) / GEMV_NW;
         const int n = base + (Cp * (wave + 1)) / GEMV_NW - c0;
         // every load below is issued unconditionally (slots past this wave's
@@ -123,9 +124,9 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
         // next one, serialising the stream into one round trip per chunk
         auto chunk = [&](int i) {
             const int c = c0 + i;
-            return c < NCH ? c : NCH - 1;
+            return ch0 + (c < NCH ? c : NCH - 1);
         };
-        u32x4 av[GEMV_AR][TA][NF];
+        u32x4 av[AR][TA][NF];
         auto load_a = [&](int i, u32x4 (&dst)[TA][NF]) {
             const uint16_t *ap = abase + (size_t)chunk(i) * KC;
 #pragma unroll
@@ -137,27 +138,27 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
         // activation fragments of the first chunks go out first: the memory
         // counter retires in order, so they must not queue behind the weights
 #pragma unroll
-        for (int i = 0; i < GEMV_AR; ++i) load_a(i, av[i]);
-        u32x4 wv[GEMV_MAXC][R][2];
+        for (int i = 0; i < AR; ++i) load_a(i, av[i]);
+        u32x4 wv[MAXC][R][2];
 #pragma unroll
-        for (int i = 0; i < GEMV_MAXC; ++i)
+        for (int i = 0; i < MAXC; ++i)
 #pragma unroll
             for (int t = 0; t < R; ++t)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
                     wv[i][t][h] = ldg16(wrow[t][h] + (size_t)chunk(i) * CH_BYTES);
 #pragma unroll
-        for (int i = 0; i < GEMV_MAXC; ++i) {
+        for (int i = 0; i < MAXC; ++i) {
             u32x4 cur[TA][NF];
 #pragma unroll
             for (int tt = 0; tt < TA; ++tt)
 #pragma unroll
-                for (int f = 0; f < NF; ++f) cur[tt][f] = av[i % GEMV_AR][tt][f];
-            if (i + GEMV_AR < GEMV_MAXC) load_a(i + GEMV_AR, av[i % GEMV_AR]);
+                for (int f = 0; f < NF; ++f) cur[tt][f] = av[i % AR][tt][f];
+            if (i + AR < MAXC) load_a(i + AR, av[i % AR]);
             if (i < n) {
 #pragma unroll
                 for (int t = 0; t < R; ++t) {
-                    uint8_t(*buf)[CH_LD] = wbuf[wave][t];
+                    uint8_t(*buf)[CH_LD] = wbuf[wave];
                     *(u32x4 *)&buf[lrow][lcol] = wv[i][t][0];
                     *(u32x4 *)&buf[lrow + 8][lcol] = wv[i][t][1];
                     wave_lds_sync();
@@ -186,16 +187,26 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
     // rr] of tile t sits in red[*][t][(row / 4) * 16 + col][row % 4]; each
     // output sums its accumulator row over the waves, then (term, batch) rows
     // over the terms, in that fixed order
+    __syncthreads();  // every wave is done with its transpose buffer
 #pragma unroll
     for (int t = 0; t < R; ++t) red[wave][t][lane] = acc[t];
-    // one output per thread (R * M * 16 <= 512): the residual operand is
-    // fetched before the barrier so its latency overlaps the reduction
-    const bool live = tid < (p.epi == EPI_SILU_MUL ? 1 : R) * p.M * 16;
-    const int et = tid / (p.M * 16), eb = (tid >> 4) % p.M, ecol = tid & 15;
-    const int ej = (blockIdx.x * R + et) * 16 + ecol;
-    const bool ein = live && ej < p.N;
-    float resid = 0.0f;
-    if (ein && p.epi == EPI_RESIDUAL) resid = p.Rr[(size_t)eb * p.ldr + ej];
+    // outputs (tile or pair, batch row, column); the first pass's residual
+    // operand is fetched before the barrier so its latency overlaps the
+    // reduction
+    const bool silu = p.epi == EPI_SILU_MUL;
+    const int nout = (silu ? R / 2 : R) * p.M * 16;
+    auto coords = [&](int e, int &t, int &b, int &col) {
+        t = e / (p.M * 16);
+        b = (e >> 4) % p.M;
+        col = e & 15;
+    };
+    float resid0 = 0.0f;
+    if (p.epi == EPI_RESIDUAL && tid < nout) {
+        int t, b, col;
+        coords(tid, t, b, col);
+        const int j = (blockIdx.x * R + t) * 16 + col;
+        if (j < p.N) resid0 = p.Rr[(size_t)b * p.ldr + j];
+    }
     __syncthreads();
     auto dsum = [&](int t, int row, int col) {
         const int ln = (row >> 2) * 16 + col, i = row & 3;
@@ -214,39 +225,191 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
             return dsum(t, b, col);
         }
     };
-    if (!live) return;
-    if (p.epi == EPI_SILU_MUL) {  // tile 0 = gate rows, tile 1 = up rows
-        const int jo = blockIdx.x * 16 + ecol;
-        const float gate = rowval(0, eb, ecol) * ssc[0][ecol];
-        const float up = rowval(R - 1, eb, ecol) * ssc[R - 1][ecol];
-        float a = (gate / (1.0f + exp_f(-gate))) * up;
-        p.Y[(size_t)eb * p.ldy + jo] = a;
-        for (int tt = 0; tt < p.Tout; ++tt) {
-            const uint32_t h = bf16_rne_bits(a);
-            a = a - bf16_bits_to_f32(h);
-            p.Aout[((size_t)tt * p.M + eb) * p.ldaout + jo] = (uint16_t)h;
+    for (int e = tid; e < nout; e += GEMV_NW * 64) {
+        int t, b, col;
+        coords(e, t, b, col);
+        if (silu) {  // pair t: tile 2t = gate rows, tile 2t + 1 = up rows
+            const int jo = (blockIdx.x * (R / 2) + t) * 16 + col;
+            const float gate = rowval(2 * t, b, col) * ssc[2 * t][col];
+            const float up = rowval(2 * t + 1, b, col) * ssc[2 * t + 1][col];
+            float a = (gate / (1.0f + exp_f(-gate))) * up;
+            p.Y[(size_t)b * p.ldy + jo] = a;
+            for (int tt = 0; tt < p.Tout; ++tt) {
+                const uint32_t h = bf16_rne_bits(a);
+                a = a - bf16_bits_to_f32(h);
+                p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
+            }
+            continue;
+        }
+        const int j = (blockIdx.x * R + t) * 16 + col;
+        const bool in = j < p.N;
+        if (p.epi == EPI_PARTIAL) {  // raw k-slice sums, reduced by the consumer
+            if (in) p.Y[((size_t)blockIdx.y * p.M + b) * p.ldy + j] = rowval(t, b, col);
+            continue;
+        }
+        float y = 0.0f;
+        if (in) {
+            y = p.scale ? rowval(t, b, col) * ssc[t][col] : rowval(t, b, col);
+            if (p.epi == EPI_RESIDUAL)
+                y = (e == tid ? resid0 : p.Rr[(size_t)b * p.ldr + j]) + y;
+            p.Y[(size_t)b * p.ldy + j] = y;
+        }
+        if (p.epi == EPI_ARGMAX) {
+            // 16 consecutive threads hold the 16 columns of row b: reduce keys
+            unsigned long long k = 0;
+            if (in && y == y) k = argmax_key(y, (uint32_t)j);
+            if (in && j == 0 && y != y) k = ARGMAX_NAN0_KEY;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                unsigned long long ok = __shfl_xor(k, o, 64);
+                k = ok > k ? ok : k;
+            }
+            if (col == 0 && k)
+                atomicMax(p.keys + (size_t)b * KEY_SLOTS + (blockIdx.x & (KEY_SLOTS - 1)), k);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wide variant for int8 weights: the 8 waves of a workgroup own 8 different
+// 16-row tiles (128 rows) over one k-slice of NC chunks (blockIdx.y), and
+// share that slice of the activation terms, loaded once into LDS. Activation
+// bytes from L2 per weight byte drop from M*T*2/16 (one tile per workgroup)
+// to M*T*2/128. All weight chunks of a wave and the activation slice are in
+// flight together (one memory round trip); the workgroup's k-slice sums go
+// out raw (EPI_PARTIAL, reduced in a fixed order by the consumer) or, with a
+// single slice, through the usual epilogues.
+template <int T, bool BT, int NC>
+__global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
+    constexpr int TA = BT ? 1 : T;
+    constexpr int KW = NC * 128;  // k of the slice
+    constexpr int ALD = KW + 8;   // LDS row of the activation slice (+16 B)
+    __shared__ __attribute__((aligned(16))) uint16_t as[TA][16][ALD];
+    __shared__ __attribute__((aligned(16))) uint8_t wbuf[8][16][CH_LD];
+    __shared__ float dwave[8][16][17];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, rr = lane & 15;
+    const int lrow = lane >> 3, lcol = (lane & 7) * 16;
+    const int tile = blockIdx.x * 8 + wave;
+    const int k0 = blockIdx.y * KW;
+
+    // this wave's weight rows, every chunk of the slice (rows clamped)
+    u32x4 wv[NC][2];
+    {
+        int j0 = tile * 16 + lrow, j1 = j0 + 8;
+        j0 = j0 < p.N ? j0 : p.N - 1;
+        j1 = j1 < p.N ? j1 : p.N - 1;
+        const uint8_t *w0 = p.W + (size_t)j0 * p.K + k0 + lcol;
+        const uint8_t *w1 = p.W + (size_t)j1 * p.K + k0 + lcol;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            wv[c][0] = ldg16(w0 + c * CH_BYTES);
+            wv[c][1] = ldg16(w1 + c * CH_BYTES);
+        }
+    }
+    // the activation slice [TA][16 rows][KW] -> LDS in 16-byte pieces; rows
+    // past the live ones repeat row 0 (their outputs are never read)
+    const int arows = BT ? T * p.M : p.M;
+    constexpr int PIECES = TA * 16 * (KW / 8);
+    constexpr int PER = (PIECES + 511) / 512;
+    u32x4 ap[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        int e = tid + i * 512;
+        e = e < PIECES ? e : PIECES - 1;
+        const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+        const int rs = r < arows ? r : 0;
+        ap[i] = ldg16_cached(p.A + (BT ? 0 : tt * p.tstride) + (size_t)rs * p.lda + k0 + c8 * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        int e = tid + i * 512;
+        e = e < PIECES ? e : PIECES - 1;
+        const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+        *(u32x4 *)&as[tt][r][c8 * 8] = ap[i];
+    }
+    __syncthreads();
+
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        uint8_t(*buf)[CH_LD] = wbuf[wave];
+        *(u32x4 *)&buf[lrow][lcol] = wv[c][0];
+        *(u32x4 *)&buf[lrow + 8][lcol] = wv[c][1];
+        wave_lds_sync();
+        const u32x4 r0 = *(const u32x4 *)&buf[rr][g * 32];
+        const u32x4 r1 = *(const u32x4 *)&buf[rr][g * 32 + 16];
+        wave_lds_sync();
+        u32x4 bfr[4];
+        i8x16_to_bf16(r0, bfr[0], bfr[1]);
+        i8x16_to_bf16(r1, bfr[2], bfr[3]);
+        // fragment f of lane (g, r): k = c*128 + 32g + 8f .. +7 (as the B side)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int tt = 0; tt < TA; ++tt)
+                acc = mfma_bf16(*(const u32x4 *)&as[tt][rr][c * 128 + g * 32 + 8 * f], bfr[f], acc);
+    }
+
+    // D[row = 4g + i][col = rr]: rows are (term, batch) or batch rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dwave[wave][4 * g + i][rr] = acc[i];
+    if (p.epi == EPI_SILU_MUL) __syncthreads();  // pairs read the partner wave's tile
+    else wave_lds_sync();
+    auto val = [&](int w, int b, int col) {
+        float v = dwave[w][b][col];
+        if constexpr (BT) {
+#pragma unroll
+            for (int tt = 1; tt < T; ++tt) v += dwave[w][tt * p.M + b][col];
+        }
+        return v;
+    };
+    if (p.epi == EPI_SILU_MUL) {  // wave 2q: gate tile, wave 2q + 1: up tile
+        if (wave & 1) return;
+        const int pt = blockIdx.x * 4 + (wave >> 1);
+        for (int e = lane; e < p.M * 16; e += 64) {
+            const int b = e >> 4, col = e & 15;
+            const int jg = tile * 16 + col, ju = jg + 16, jo = pt * 16 + col;
+            const float gate = val(wave, b, col) * p.scale[jg];
+            const float up = val(wave + 1, b, col) * p.scale[ju];
+            float a = (gate / (1.0f + exp_f(-gate))) * up;
+            p.Y[(size_t)b * p.ldy + jo] = a;
+            for (int tt = 0; tt < p.Tout; ++tt) {
+                const uint32_t h = bf16_rne_bits(a);
+                a = a - bf16_bits_to_f32(h);
+                p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
+            }
         }
         return;
     }
-    float y = 0.0f;
-    if (ein) {
-        y = p.scale ? rowval(et, eb, ecol) * ssc[et][ecol] : rowval(et, eb, ecol);
-        if (p.epi == EPI_RESIDUAL) y = resid + y;
-        p.Y[(size_t)eb * p.ldy + ej] = y;
-    }
-    if (p.epi == EPI_ARGMAX) {
-        // 16 consecutive threads hold the 16 columns of row eb: reduce keys
-        unsigned long long k = 0;
-        if (ein && y == y) k = argmax_key(y, (uint32_t)ej);
-        if (ein && ej == 0 && y != y) k = ARGMAX_NAN0_KEY;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            unsigned long long ok = __shfl_xor(k, o, 64);
-            k = ok > k ? ok : k;
+    for (int e = lane; e < p.M * 16; e += 64) {
+        const int b = e >> 4, col = e & 15;
+        const int j = tile * 16 + col;
+        if (j >= p.N) continue;
+        const float v = val(wave, b, col);
+        if (p.epi == EPI_PARTIAL) {
+            p.Y[((size_t)blockIdx.y * p.M + b) * p.ldy + j] = v;
+        } else {
+            float y = p.scale ? v * p.scale[j] : v;
+            if (p.epi == EPI_RESIDUAL) y = p.Rr[(size_t)b * p.ldr + j] + y;
+            p.Y[(size_t)b * p.ldy + j] = y;
         }
-        if (ecol == 0 && k)
-            atomicMax(p.keys + (size_t)eb * KEY_SLOTS + (blockIdx.x & (KEY_SLOTS - 1)), k);
     }
+}
+
+template <int T, bool BT>
+static int launch_wide_t(const GemvParams &p, int nc, hipStream_t st) {
+    const dim3 grid((p.N + 127) / 128, p.ks);
+    switch (nc) {
+    case 1: gemv_wide_kernel<T, BT, 1><<<grid, 512, 0, st>>>(p); break;
+    case 2: gemv_wide_kernel<T, BT, 2><<<grid, 512, 0, st>>>(p); break;
+    case 3: gemv_wide_kernel<T, BT, 3><<<grid, 512, 0, st>>>(p); break;
+    default: return fail(VMLM_ERR_UNIMPL, "gemv wide: %d chunks per slice", nc);
+    }
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
 }
 
 __global__ void split_terms_kernel(const float *__restrict__ x, size_t ldx, int rows, int K,
@@ -274,9 +437,13 @@ int launch_split_terms(const float *x, size_t ldx, int rows, int K, int T, uint1
 
 template <bool WI8, int T, int R, bool BT>
 static int launch_t(const GemvParams &p, hipStream_t st) {
-    int tiles = (p.N + 16 * R - 1) / (16 * R);
-    if (p.epi == EPI_SILU_MUL) tiles = p.N / 32;
-    gemv_kernel<WI8, T, R, BT><<<tiles, GEMV_NW * 64, 0, st>>>(p);
+    // chunk depth / activation ring per tile count, from measurements: one
+    // tile keeps three chunks and their activation fragments in flight; more
+    // tiles share one activation chunk at a time (register budget)
+    constexpr int MAXC = 3, AR = R == 1 ? 3 : 1;
+    int wgs = (p.N + 16 * R - 1) / (16 * R);
+    if (p.epi == EPI_SILU_MUL) wgs = p.N / (16 * R);
+    gemv_kernel<WI8, T, R, BT, MAXC, AR><<<dim3(wgs, p.ks), GEMV_NW * 64, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -317,14 +484,53 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     p.ldaout = a.ldaout;
     p.Tout = a.Tout;
     p.epi = a.epi;
+    p.ks = a.ksplit > 0 ? a.ksplit : 1;
+    VMLM_GUARD(p.ks == 1 || (a.epi == EPI_PARTIAL && (a.K / (a.w_int8 ? 128 : 64)) % p.ks == 0) ||
+                   (a.tiles == 8 && a.epi == EPI_PARTIAL),
+               "gemv: k-split %d needs EPI_PARTIAL and whole chunks per slice", p.ks);
     // (term, batch) rows need the planes contiguous: row r = buffer row r
     const bool bt = a.T > 1 && a.T * a.M <= 16 && p.tstride == (size_t)a.M * a.lda;
-    if (a.epi == EPI_SILU_MUL) {
-        VMLM_GUARD(a.N % 32 == 0 && a.scale && a.Aout && a.w_int8,
-                   "gemv silu: int8 weights, N %% 32, scale, Aout");
-        return launch_r<true, 2>(p, a.T, bt, st);
+    // Tiles per workgroup: the activation fragments a wave loads serve R
+    // tiles, so R trades activation traffic (M * T * 2 bytes per k per
+    // workgroup) against workgroup count. One tile while the activation is a
+    // few (term, batch) rows; with a full 16-row batch, 4 tiles where that
+    // still leaves a workgroup for most CUs.
+    int R = a.tiles;
+    if (R == 8) {  // wide: 128 rows per workgroup, activation slice in LDS
+        const int nch = a.K / 128;
+        VMLM_GUARD(a.w_int8 && nch % p.ks == 0 && nch / p.ks <= 3,
+                   "gemv wide: int8, k-slices of 1..3 whole chunks");
+        VMLM_GUARD(a.epi != EPI_ARGMAX, "gemv wide: no argmax epilogue");
+        VMLM_GUARD(a.epi != EPI_SILU_MUL || (p.ks == 1 && a.N % 128 == 0 && a.scale && a.Aout),
+                   "gemv wide silu: one k-slice, N %% 128, scale, Aout");
+        const int nc = nch / p.ks;
+        switch (a.T) {
+        case 1: return launch_wide_t<1, false>(p, nc, st);
+        case 2: return bt ? launch_wide_t<2, true>(p, nc, st) : launch_wide_t<2, false>(p, nc, st);
+        case 3: return bt ? launch_wide_t<3, true>(p, nc, st) : launch_wide_t<3, false>(p, nc, st);
+        default: return fail(VMLM_ERR_UNIMPL, "gemv: %d activation terms unsupported", a.T);
+        }
     }
-    return a.w_int8 ? launch_r<true, 1>(p, a.T, bt, st) : launch_r<false, 1>(p, a.T, bt, st);
+    if (R == 0) {
+        const int tiles16 = a.N / 16;
+        if (a.epi == EPI_SILU_MUL) R = (!bt && tiles16 / 4 >= 128) ? 4 : 2;
+        else R = (a.w_int8 && !bt && tiles16 / 4 >= 96) ? 4 : 1;
+    }
+    if (a.epi == EPI_SILU_MUL) {
+        VMLM_GUARD(a.w_int8 && a.scale && a.Aout && (R == 2 || R == 4) && a.N % (16 * R) == 0,
+                   "gemv silu: int8 weights, scale, Aout, 2 or 4 tiles dividing N");
+        return R == 4 ? launch_r<true, 4>(p, a.T, bt, st) : launch_r<true, 2>(p, a.T, bt, st);
+    }
+    VMLM_GUARD(R == 1 || R == 2 || R == 4, "gemv: %d tiles per workgroup unsupported", R);
+    if (!a.w_int8) {
+        VMLM_GUARD(R == 1, "gemv bf16: one tile per workgroup");
+        return launch_r<false, 1>(p, a.T, bt, st);
+    }
+    switch (R) {
+    case 1: return launch_r<true, 1>(p, a.T, bt, st);
+    case 2: return launch_r<true, 2>(p, a.T, bt, st);
+    default: return launch_r<true, 4>(p, a.T, bt, st);
+    }
 }
 
 }  // namespace vmlm

@@ -148,6 +148,135 @@ int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, si
     return VMLM_OK;
 }
 
+// Residual add of a k-split projection fused with the RMSNorm that follows
+// it (OP_GEMM + OP_EWADD + OP_RMSNORM of the decoder program): per row,
+//   x = base + (sum_ks part[ks]) * scale      (slices summed in order)
+//   resid = x;  y = x * (1 / sqrt(mean(x^2) + eps)) * g  -> T bf16 terms.
+// One thread per 4 columns (cols <= 4096); every slice of a column is loaded
+// up front (index clamped, KS_MAX slots) so the reads take one round trip.
+constexpr int KS_MAX = 16;
+
+__global__ __launch_bounds__(1024) void rmsnorm_resid_kernel(
+    const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
+    const float *__restrict__ scale, float *__restrict__ resid, const float *__restrict__ g,
+    int cols, float eps, uint16_t *__restrict__ terms, int T, int ld_terms, int rows) {
+    __shared__ float sh[16];
+    const int row = blockIdx.x, n4 = cols >> 2;
+    const int c = threadIdx.x < n4 ? threadIdx.x : n4 - 1;
+    float4 pv[KS_MAX];
+#pragma unroll
+    for (int k = 0; k < KS_MAX; ++k) {
+        const int kk = k < ks ? k : ks - 1;
+        pv[k] = ((const float4 *)(part + ((size_t)kk * rows + row) * ldp))[c];
+    }
+    const float4 sc = ((const float4 *)scale)[c];
+    const float4 bb = ((const float4 *)(base + (size_t)row * cols))[c];
+    const float4 gg = ((const float4 *)g)[c];
+    float4 acc = pv[0];
+#pragma unroll
+    for (int k = 1; k < KS_MAX; ++k) {
+        if (k < ks) {
+            acc.x += pv[k].x;
+            acc.y += pv[k].y;
+            acc.z += pv[k].z;
+            acc.w += pv[k].w;
+        }
+    }
+    const float4 x = make_float4(bb.x + acc.x * sc.x, bb.y + acc.y * sc.y, bb.z + acc.z * sc.z,
+                                 bb.w + acc.w * sc.w);
+    const bool live = threadIdx.x < n4;
+    float ss = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.0f;
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) ss += sh[w];
+    ss = ss / (float)cols;
+    const float inv = 1.0f / sqrtf(ss + eps);
+    if (!live) return;
+    ((float4 *)(resid + (size_t)row * cols))[c] = x;
+    float y[4] = {x.x * inv * gg.x, x.y * inv * gg.y, x.z * inv * gg.z, x.w * inv * gg.w};
+    for (int t = 0; t < T; ++t) {
+        uint32_t h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h[q] = bf16_rne_bits(y[q]);
+            y[q] = y[q] - bf16_bits_to_f32(h[q]);
+        }
+        *(uint2 *)(terms + ((size_t)t * rows + row) * ld_terms + 4 * c) =
+            make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    }
+}
+
+int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
+                         const float *scale, float *resid, size_t rows, size_t cols,
+                         const float *g, float eps, uint16_t *terms, int T, int ld_terms,
+                         hipStream_t st) {
+    if (rows == 0) return VMLM_OK;
+    VMLM_GUARD(cols % 4 == 0 && cols <= 4096 && ldp % 4 == 0 && ks >= 1 && ks <= KS_MAX &&
+                   (int)cols == ld_terms,
+               "rmsnorm_resid: cols %% 4 (<= 4096), ldp %% 4, 1 <= ks <= %d, ld_terms == cols",
+               KS_MAX);
+    const unsigned threads = (unsigned)((cols / 4 + 63) / 64 * 64);
+    rmsnorm_resid_kernel<<<(unsigned)rows, threads, 0, st>>>(base, part, ks, ldp, scale, resid,
+                                                             g, (int)cols, eps, terms, T,
+                                                             ld_terms, (int)rows);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// SiLU(gate) * up from the k-slice partials of the interleaved gate/up
+// projection (16-row blocks: rows 32t..32t+15 gate and 32t+16..32t+31 up
+// of output columns 16t..16t+15), written as T bf16 terms [T][rows][I]:
+//   gate = (sum_ks P) * sg, up = (sum_ks P) * su, a = gate / (1 + exp_f(-gate)) * up.
+// One output per thread, every slice loaded up front.
+__global__ __launch_bounds__(256) void silu_reduce_kernel(const float *__restrict__ part, int ks,
+                                                          int ldp, const float *__restrict__ sgu,
+                                                          int rows, int I,
+                                                          uint16_t *__restrict__ terms, int T) {
+    const int n = rows * I;
+    int i = blockIdx.x * 256 + threadIdx.x;
+    const bool live = i < n;
+    i = live ? i : n - 1;
+    const int row = i / I, jo = i % I;
+    const int jg = (jo >> 4) * 32 + (jo & 15), ju = jg + 16;
+    float gv[KS_MAX], uv[KS_MAX];
+#pragma unroll
+    for (int k = 0; k < KS_MAX; ++k) {
+        const int kk = k < ks ? k : ks - 1;
+        const float *pr = part + ((size_t)kk * rows + row) * ldp;
+        gv[k] = pr[jg];
+        uv[k] = pr[ju];
+    }
+    const float sg = sgu[jg], su = sgu[ju];
+    float ga = gv[0], ua = uv[0];
+#pragma unroll
+    for (int k = 1; k < KS_MAX; ++k) {
+        if (k < ks) {
+            ga += gv[k];
+            ua += uv[k];
+        }
+    }
+    if (!live) return;
+    const float gate = ga * sg, up = ua * su;
+    float y = (gate / (1.0f + exp_f(-gate))) * up;
+    for (int t = 0; t < T; ++t) {
+        const uint32_t h = bf16_rne_bits(y);
+        y = y - bf16_bits_to_f32(h);
+        terms[((size_t)t * rows + row) * I + jo] = (uint16_t)h;
+    }
+}
+
+int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
+                       uint16_t *terms, int T, hipStream_t st) {
+    VMLM_GUARD(I % 16 == 0 && ks >= 1 && ks <= KS_MAX && rows >= 1,
+               "silu_reduce: I %% 16, 1 <= ks <= %d", KS_MAX);
+    const size_t n = (size_t)rows * I;
+    silu_reduce_kernel<<<cdiv(n, 256), 256, 0, st>>>(part, ks, ldp, sgu, rows, I, terms, T);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 // ops/src/kernels.rs:1388-1414 -- max, exp_f(x-max), sum, * (1/sum), causal tail 0.
 __global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ p, int cols,
                                                       int causal) {

@@ -108,6 +108,8 @@ struct vmlm_decoder {
     uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
+    float *part = nullptr;               // k-slice partial sums of the decode GEMVs
+    int ks_h = 1, ks_i = 1;              // k-slices of the K=H and K=I projections
     int *pos = nullptr, *step = nullptr;
     float rope_step = 0.0f;
     uint32_t pos_host = 0, step_host = 0;
@@ -167,32 +169,41 @@ int enqueue_head(vmlm_decoder *d, bool record) {
     return VMLM_OK;
 }
 
-// One decode step over the B sequences (all launches on d->st).
+// Decode GEMV of the step: the wide kernel (8 tiles of 16 rows per
+// workgroup, activation slice shared through LDS) over k-slices, raw slice
+// sums to d->part; the consumer (attention, residual RMSNorm, SiLU) reduces
+// them in slice order and applies the row scales.
+GemvArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int K, int ks) {
+    GemvArgs g;
+    g.W = W;
+    g.A = A;
+    g.T = 3;
+    g.lda = K;
+    g.M = (int)d->B;
+    g.N = N;
+    g.K = K;
+    g.Y = d->part;
+    g.ldy = N;
+    g.epi = EPI_PARTIAL;
+    g.tiles = 8;
+    g.ksplit = ks;
+    return g;
+}
+
+// One decode step over the B sequences (all launches on d->st). Layer l's
+// input norm is produced by the previous layer's closing residual RMSNorm.
 int enqueue_step(vmlm_decoder *d) {
     hipStream_t st = d->st;
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     const int T = 3;
     int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
     if (rc) return rc;
+    if ((rc = launch_rmsnorm(nullptr, d->h, d->InLn(0), B, H, d->c.eps, d->t_x, T, H, st)))
+        return rc;
     for (size_t l = 0; l < d->L; ++l) {
-        rc = launch_rmsnorm(nullptr, d->h, d->InLn(l), B, H, d->c.eps, d->t_x, T, H, st);
-        if (rc) return rc;
-        GemvArgs g;
-        g.W = d->Wqkv(l);
-        g.scale = d->Sqkv(l);
-        g.A = d->t_x;
-        g.T = T;
-        g.lda = H;
-        g.M = B;
-        g.N = 3 * H;
-        g.K = H;
-        g.Y = d->qkv;
-        g.ldy = 3 * H;
-        if ((rc = launch_gemv(g, st))) return rc;
+        if ((rc = launch_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H, d->ks_h), st))) return rc;
         DecodeArgs a;
-        a.q = d->qkv;
-        a.k_new = d->qkv + H;
-        a.v_new = d->qkv + 2 * H;
+        a.q = a.k_new = a.v_new = nullptr;
         a.ldq = 3 * H;
         a.kc = d->Kc(l);
         a.vc = d->Vc(l);
@@ -202,58 +213,24 @@ int enqueue_step(vmlm_decoder *d) {
         a.pos = 0;
         a.step = d->rope_step;
         a.scale = d->c.attn_scale;
+        a.part = d->part;
+        a.ks = d->ks_h;
+        a.ldp = 3 * H;
+        a.wscale = d->Sqkv(l);
         if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
-        GemvArgs o;
-        o.W = d->Wo(l);
-        o.scale = d->So(l);
-        o.A = d->t_att;
-        o.T = T;
-        o.lda = H;
-        o.M = B;
-        o.N = H;
-        o.K = H;
-        o.Y = d->h2;
-        o.ldy = H;
-        o.epi = EPI_RESIDUAL;
-        o.R = d->h;
-        o.ldr = H;
-        if ((rc = launch_gemv(o, st))) return rc;
-        if ((rc = launch_rmsnorm(nullptr, d->h2, d->PostLn(l), B, H, d->c.eps, d->t_x, T, H, st)))
+        if ((rc = launch_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H, d->ks_h), st))) return rc;
+        if ((rc = launch_rmsnorm_resid(d->h, d->part, d->ks_h, H, d->So(l), d->h2, B, H,
+                                       d->PostLn(l), d->c.eps, d->t_x, T, H, st)))
             return rc;
-        GemvArgs gu;
-        gu.W = d->Wgu(l);
-        gu.scale = d->Sgu(l);
-        gu.A = d->t_x;
-        gu.T = T;
-        gu.lda = H;
-        gu.M = B;
-        gu.N = 2 * I;
-        gu.K = H;
-        gu.Y = d->act;
-        gu.ldy = I;
-        gu.epi = EPI_SILU_MUL;
-        gu.Aout = d->t_act;
-        gu.ldaout = I;
-        gu.Tout = T;
-        if ((rc = launch_gemv(gu, st))) return rc;
-        GemvArgs dn;
-        dn.W = d->Wd(l);
-        dn.scale = d->Sd(l);
-        dn.A = d->t_act;
-        dn.T = T;
-        dn.lda = I;
-        dn.M = B;
-        dn.N = H;
-        dn.K = I;
-        dn.Y = d->h;
-        dn.ldy = H;
-        dn.epi = EPI_RESIDUAL;
-        dn.R = d->h2;
-        dn.ldr = H;
-        if ((rc = launch_gemv(dn, st))) return rc;
+        if ((rc = launch_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H, d->ks_h), st))) return rc;
+        if ((rc = launch_silu_reduce(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->t_act, T, st)))
+            return rc;
+        if ((rc = launch_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I, d->ks_i), st))) return rc;
+        const float *g_next = l + 1 < d->L ? d->InLn(l + 1) : d->final_norm;
+        if ((rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H, g_next,
+                                       d->c.eps, d->t_x, T, H, st)))
+            return rc;
     }
-    if ((rc = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, T, H, st)))
-        return rc;
     if ((rc = enqueue_head(d, true))) return rc;
     step_advance_kernel<<<1, 1, 0, st>>>(d->step, d->pos);
     VMLM_HIP_CHECK(hipGetLastError());
@@ -305,6 +282,16 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     d->w_layer = 4 * d->H * d->H + 3 * d->I * d->H;
     d->s_layer = 5 * d->H + 2 * d->I;
     d->rope_step = -2.0f / 64.0f * host_ln_f(c.theta);
+    // k-slices: 2 chunks (256 k) per slice for K = hidden, 3 for K = inter,
+    // else the largest of 3, 2, 1 chunks that divides the chunk count
+    auto pick_ks = [](size_t K, int want) {
+        const int nch = (int)(K / 128);
+        for (int nc = want; nc > 1; --nc)
+            if (nch % nc == 0) return nch / nc;
+        return nch;
+    };
+    d->ks_h = pick_ks(d->H, 2);
+    d->ks_i = pick_ks(d->I, 3);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
         vmlm_decoder_destroy(d);
@@ -324,7 +311,10 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->t_att, 3 * d->B * d->H)) ||
         (rc = dalloc(d, &d->t_act, 3 * d->B * d->I)) || (rc = dalloc(d, &d->tok, d->B)) ||
         (rc = dalloc(d, &d->tokens_out, d->cap * d->B)) || (rc = dalloc(d, &d->pos, 1)) ||
-        (rc = dalloc(d, &d->step, 1)) || (rc = dalloc(d, &d->keys, d->B * KEY_SLOTS)))
+        (rc = dalloc(d, &d->step, 1)) || (rc = dalloc(d, &d->keys, d->B * KEY_SLOTS)) ||
+        (rc = dalloc(d, &d->part, d->B * std::max({(size_t)d->ks_h * 3 * d->H,
+                                                   (size_t)d->ks_h * 2 * d->I,
+                                                   (size_t)d->ks_i * d->H}))))
         return cleanup(rc);
     if ((e = hipMemsetAsync(d->keys, 0, d->B * KEY_SLOTS * 8, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->kc, 0, kvn * 4, d->st)) != hipSuccess ||
@@ -593,29 +583,28 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     if (rc) return rc;
     VMLM_GUARD(which >= 0 && which <= 4 && iters >= 1, "time_gemv: which 0..4, iters >= 1");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
+    // the launches of the decode step (k-split wide GEMVs; LM head bf16)
     auto make = [&](size_t l) {
-        GemvArgs g;
-        g.T = 3;
-        g.M = B;
-        g.lda = H;
-        g.K = H;
-        g.A = d->t_x;
         switch (which) {
-        case 0: g.W = d->Wqkv(l); g.scale = d->Sqkv(l); g.N = 3 * H; g.Y = d->qkv; g.ldy = 3 * H; break;
-        case 1:
-            g.W = d->Wo(l); g.scale = d->So(l); g.A = d->t_att; g.N = H; g.Y = d->h2; g.ldy = H;
-            g.epi = EPI_RESIDUAL; g.R = d->h; g.ldr = H; break;
-        case 2:
-            g.W = d->Wgu(l); g.scale = d->Sgu(l); g.N = 2 * I; g.Y = d->act; g.ldy = I;
-            g.epi = EPI_SILU_MUL; g.Aout = d->t_act; g.ldaout = I; g.Tout = 3; break;
-        case 3:
-            g.W = d->Wd(l); g.scale = d->Sd(l); g.A = d->t_act; g.lda = I; g.K = I; g.N = H;
-            g.Y = d->att; g.ldy = H; g.epi = EPI_RESIDUAL; g.R = d->h2; g.ldr = H; break;
-        default:
-            g.W = d->lm_head; g.w_int8 = false; g.N = (int)d->V; g.Y = d->logits;
-            g.ldy = (int)d->V; break;
+        case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H, d->ks_h);
+        case 1: return step_gemv(d, d->Wo(l), d->t_att, H, H, d->ks_h);
+        case 2: return step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H, d->ks_h);
+        case 3: return step_gemv(d, d->Wd(l), d->t_act, H, I, d->ks_i);
+        default: {
+            GemvArgs g;
+            g.T = 3;
+            g.M = B;
+            g.lda = H;
+            g.K = H;
+            g.A = d->t_x;
+            g.W = d->lm_head;
+            g.w_int8 = false;
+            g.N = (int)d->V;
+            g.Y = d->logits;
+            g.ldy = (int)d->V;
+            return g;
         }
-        return g;
+        }
     };
     hipEvent_t e0, e1;
     VMLM_HIP_CHECK(hipEventCreate(&e0));
@@ -633,13 +622,15 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     *avg_us = ms * 1000.0f / (float)iters;
+    // algorithmic bytes of the projection: weights, row scales (int8), the
+    // f32 activation in and the f32 result out (the partial sums and the
+    // bf16 term planes are this implementation's, not the algorithm's)
     GemvArgs g = make(0);
     const double wbytes = (double)g.N * g.K * (g.w_int8 ? 1 : 2);
-    const double sbytes = g.scale ? (double)g.N * 4 : 0.0;
+    const double sbytes = g.w_int8 ? (double)g.N * 4 : 0.0;
     const double xbytes = (double)B * g.K * 4;
-    const double ybytes = (double)B * (which == 2 ? I : g.N) * 4;
-    const double rbytes = g.epi == EPI_RESIDUAL ? (double)B * g.N * 4 : 0.0;
-    *bytes_per_launch = wbytes + sbytes + xbytes + ybytes + rbytes;
+    const double ybytes = (double)B * g.N * 4;
+    *bytes_per_launch = wbytes + sbytes + xbytes + ybytes;
     return VMLM_OK;
 }
 
