@@ -46,7 +46,7 @@ def gemv_roofline(dec, iters):
     achieved = tot_b / tot_t / 1e3  # GB/s
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": "gemv_kernel<int8,T=3> (q/k/v, o, gate+up, down)",
+            "traffic": None, "kernel": "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)",
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "per_shape": per}
 

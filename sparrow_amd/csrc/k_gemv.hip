@@ -399,6 +399,192 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
     }
 }
 
+// Wide variant with a k-loop, for full-K workgroups (the LM head, and any
+// projection whose k-slice spans more than three chunks): the 8 waves own 8
+// row tiles; the k-range advances in steps of SC chunks. Per step the
+// activation slice is staged through a double-buffered LDS area (loaded one
+// step ahead), and each wave keeps the weight chunks of the next two steps
+// in flight in a 3-slot register ring (the loop is unrolled by 3 so every
+// slot is a fixed set of registers).
+template <bool WI8, int T, bool BT, int SC>
+__global__ __launch_bounds__(512) void gemv_wloop_kernel(GemvParams p) {
+    constexpr int TA = BT ? 1 : T;
+    constexpr int KC = WI8 ? 128 : 64;  // k per 128-byte chunk
+    constexpr int NF = KC / 32;
+    constexpr int ESZ = WI8 ? 1 : 2;
+    constexpr int KW = SC * KC;         // k per step
+    constexpr int ALD = KW + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t as[2][TA][16][ALD];
+    __shared__ __attribute__((aligned(16))) uint8_t wbuf[8][16][CH_LD];
+    __shared__ float dwave[8][16][17];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, rr = lane & 15;
+    const int lrow = lane >> 3, lcol = (lane & 7) * 16;
+    const int tile = blockIdx.x * 8 + wave;
+    const int nsteps = p.K / KW / (int)gridDim.y;
+    const int kslice = blockIdx.y * nsteps * KW;
+
+    int j0 = tile * 16 + lrow, j1 = j0 + 8;
+    j0 = j0 < p.N ? j0 : p.N - 1;
+    j1 = j1 < p.N ? j1 : p.N - 1;
+    const uint8_t *w0 = p.W + ((size_t)j0 * p.K + kslice) * ESZ + lcol;
+    const uint8_t *w1 = p.W + ((size_t)j1 * p.K + kslice) * ESZ + lcol;
+    auto load_w = [&](int s, u32x4 (&dst)[SC][2]) {
+        s = s < nsteps ? s : nsteps - 1;
+#pragma unroll
+        for (int c = 0; c < SC; ++c) {
+            const size_t off = ((size_t)s * SC + c) * CH_BYTES;
+            dst[c][0] = ldg16(w0 + off);
+            dst[c][1] = ldg16(w1 + off);
+        }
+    };
+    const int arows = BT ? T * p.M : p.M;
+    constexpr int PIECES = TA * 16 * (KW / 8);
+    constexpr int PER = (PIECES + 511) / 512;
+    auto load_a = [&](int s, u32x4 (&dst)[PER]) {
+        s = s < nsteps ? s : nsteps - 1;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int e = tid + i * 512;
+            e = e < PIECES ? e : PIECES - 1;
+            const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+            const int rs = r < arows ? r : 0;
+            dst[i] = ldg16_cached(p.A + (BT ? 0 : tt * p.tstride) + (size_t)rs * p.lda + kslice +
+                                  (size_t)s * KW + c8 * 8);
+        }
+    };
+    auto store_a = [&](int buf, const u32x4 (&src)[PER]) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int e = tid + i * 512;
+            e = e < PIECES ? e : PIECES - 1;
+            const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+            *(u32x4 *)&as[buf][tt][r][c8 * 8] = src[i];
+        }
+    };
+
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf, const u32x4 (&w)[SC][2]) {
+#pragma unroll
+        for (int c = 0; c < SC; ++c) {
+            uint8_t(*bw)[CH_LD] = wbuf[wave];
+            *(u32x4 *)&bw[lrow][lcol] = w[c][0];
+            *(u32x4 *)&bw[lrow + 8][lcol] = w[c][1];
+            wave_lds_sync();
+            const u32x4 r0 = *(const u32x4 *)&bw[rr][g * 32];
+            const u32x4 r1 = *(const u32x4 *)&bw[rr][g * 32 + 16];
+            wave_lds_sync();
+            u32x4 bfr[NF];
+            if constexpr (WI8) {
+                i8x16_to_bf16(r0, bfr[0], bfr[1]);
+                i8x16_to_bf16(r1, bfr[2], bfr[3]);
+            } else {
+                bfr[0] = r0;
+                bfr[1] = r1;
+            }
+            // fragment f of lane (g, r): k = c*KC + (KC/4)*g + 8f .. +7
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int tt = 0; tt < TA; ++tt)
+                    acc = mfma_bf16(
+                        *(const u32x4 *)&as[buf][tt][rr][c * KC + g * (KC / 4) + 8 * f], bfr[f],
+                        acc);
+        }
+    };
+
+    u32x4 wa[SC][2], wb[SC][2], wc[SC][2];
+    u32x4 ap[PER];
+    load_a(0, ap);
+    load_w(0, wa);
+    load_w(1, wb);
+    store_a(0, ap);
+    load_a(1, ap);
+    __syncthreads();
+    // step s: weights of s in the ring slot s % 3, activation of s in LDS
+    // buffer s & 1, activation of s + 1 in registers
+    auto step = [&](int s, u32x4 (&wcur)[SC][2], u32x4 (&wnext2)[SC][2]) {
+        load_w(s + 2, wnext2);
+        compute(s & 1, wcur);
+        store_a((s + 1) & 1, ap);
+        load_a(s + 2, ap);
+        __syncthreads();
+    };
+    for (int s = 0; s < nsteps; s += 3) {
+        step(s, wa, wc);
+        if (s + 1 < nsteps) step(s + 1, wb, wa);
+        if (s + 2 < nsteps) step(s + 2, wc, wb);
+    }
+
+    // D[row = 4g + i][col = rr]: rows are (term, batch) or batch rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dwave[wave][4 * g + i][rr] = acc[i];
+    if (p.epi == EPI_SILU_MUL) __syncthreads();
+    else wave_lds_sync();
+    auto val = [&](int w, int b, int col) {
+        float v = dwave[w][b][col];
+        if constexpr (BT) {
+#pragma unroll
+            for (int tt = 1; tt < T; ++tt) v += dwave[w][tt * p.M + b][col];
+        }
+        return v;
+    };
+    if (p.epi == EPI_SILU_MUL) {  // wave 2q: gate tile, wave 2q + 1: up tile
+        if (wave & 1) return;
+        const int pt = blockIdx.x * 4 + (wave >> 1);
+        for (int e = lane; e < p.M * 16; e += 64) {
+            const int b = e >> 4, col = e & 15;
+            const int jg = tile * 16 + col, ju = jg + 16, jo = pt * 16 + col;
+            const float gate = val(wave, b, col) * p.scale[jg];
+            const float up = val(wave + 1, b, col) * p.scale[ju];
+            float a = (gate / (1.0f + exp_f(-gate))) * up;
+            p.Y[(size_t)b * p.ldy + jo] = a;
+            for (int tt = 0; tt < p.Tout; ++tt) {
+                const uint32_t h = bf16_rne_bits(a);
+                a = a - bf16_bits_to_f32(h);
+                p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
+            }
+        }
+        return;
+    }
+    for (int e = lane; e < p.M * 16; e += 64) {
+        const int b = e >> 4, col = e & 15;
+        const int j = tile * 16 + col;
+        const bool in = j < p.N;
+        const float v = val(wave, b, col);
+        if (p.epi == EPI_PARTIAL) {
+            if (in) p.Y[((size_t)blockIdx.y * p.M + b) * p.ldy + j] = v;
+            continue;
+        }
+        float y = p.scale ? v * p.scale[in ? j : 0] : v;
+        if (in && p.epi == EPI_RESIDUAL) y = p.Rr[(size_t)b * p.ldr + j] + y;
+        if (in) p.Y[(size_t)b * p.ldy + j] = y;
+        if (p.epi == EPI_ARGMAX) {
+            // 16 consecutive lanes hold the 16 columns of row b
+            unsigned long long k = 0;
+            if (in && y == y) k = argmax_key(y, (uint32_t)j);
+            if (in && j == 0 && y != y) k = ARGMAX_NAN0_KEY;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const unsigned long long ok = __shfl_xor(k, o, 64);
+                k = ok > k ? ok : k;
+            }
+            if (col == 0 && k)
+                atomicMax(p.keys + (size_t)b * KEY_SLOTS + (tile & (KEY_SLOTS - 1)), k);
+        }
+    }
+}
+
+template <bool WI8, int T, bool BT>
+static int launch_wloop_t(const GemvParams &p, hipStream_t st) {
+    const dim3 grid((p.N + 127) / 128, p.ks);
+    gemv_wloop_kernel<WI8, T, BT, WI8 ? 1 : 2><<<grid, 512, 0, st>>>(p);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 template <int T, bool BT>
 static int launch_wide_t(const GemvParams &p, int nc, hipStream_t st) {
     const dim3 grid((p.N + 127) / 128, p.ks);
@@ -486,7 +672,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     p.epi = a.epi;
     p.ks = a.ksplit > 0 ? a.ksplit : 1;
     VMLM_GUARD(p.ks == 1 || (a.epi == EPI_PARTIAL && (a.K / (a.w_int8 ? 128 : 64)) % p.ks == 0) ||
-                   (a.tiles == 8 && a.epi == EPI_PARTIAL),
+                   (a.tiles >= 8 && a.epi == EPI_PARTIAL),
                "gemv: k-split %d needs EPI_PARTIAL and whole chunks per slice", p.ks);
     // (term, batch) rows need the planes contiguous: row r = buffer row r
     const bool bt = a.T > 1 && a.T * a.M <= 16 && p.tstride == (size_t)a.M * a.lda;
@@ -496,6 +682,28 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     // few (term, batch) rows; with a full 16-row batch, 4 tiles where that
     // still leaves a workgroup for most CUs.
     int R = a.tiles;
+    if (R == 9) {  // wide with a k-loop: 128 rows per workgroup, any k-slice length
+        const int kstep = 128;  // int8: one chunk per step; bf16: two
+        VMLM_GUARD(a.K % kstep == 0 && (a.K / kstep) % p.ks == 0,
+                   "gemv wide loop: K %% 128 and whole steps per k-slice");
+        VMLM_GUARD(p.ks == 1 || a.epi == EPI_PARTIAL, "gemv wide loop: k-slices need EPI_PARTIAL");
+        VMLM_GUARD(a.epi != EPI_SILU_MUL || (a.N % 128 == 0 && a.scale && a.Aout && a.w_int8),
+                   "gemv wide loop silu: int8, N %% 128, scale, Aout");
+        if (a.w_int8) {
+            switch (a.T) {
+            case 1: return launch_wloop_t<true, 1, false>(p, st);
+            case 2: return bt ? launch_wloop_t<true, 2, true>(p, st) : launch_wloop_t<true, 2, false>(p, st);
+            case 3: return bt ? launch_wloop_t<true, 3, true>(p, st) : launch_wloop_t<true, 3, false>(p, st);
+            default: return fail(VMLM_ERR_UNIMPL, "gemv: %d activation terms unsupported", a.T);
+            }
+        }
+        switch (a.T) {
+        case 1: return launch_wloop_t<false, 1, false>(p, st);
+        case 2: return bt ? launch_wloop_t<false, 2, true>(p, st) : launch_wloop_t<false, 2, false>(p, st);
+        case 3: return bt ? launch_wloop_t<false, 3, true>(p, st) : launch_wloop_t<false, 3, false>(p, st);
+        default: return fail(VMLM_ERR_UNIMPL, "gemv: %d activation terms unsupported", a.T);
+        }
+    }
     if (R == 8) {  // wide: 128 rows per workgroup, activation slice in LDS
         const int nch = a.K / 128;
         VMLM_GUARD(a.w_int8 && nch % p.ks == 0 && nch / p.ks <= 3,

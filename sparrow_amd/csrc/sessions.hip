@@ -160,6 +160,7 @@ int enqueue_head(vmlm_decoder *d, bool record) {
     lm.ldy = (int)d->V;
     lm.epi = EPI_ARGMAX;
     lm.keys = d->keys;
+    lm.tiles = 9;  // 128 rows per workgroup over the full K, activation through LDS
     int rc = launch_gemv(lm, d->st);
     if (rc) return rc;
     argmax_advance_kernel<<<(unsigned)d->B, 64, 0, d->st>>>(
@@ -602,6 +603,7 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
             g.N = (int)d->V;
             g.Y = d->logits;
             g.ldy = (int)d->V;
+            g.tiles = 9;
             return g;
         }
         }
