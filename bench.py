@@ -78,6 +78,134 @@ def cpu_baseline(cfg, W, steps, threads):
                       f"(AVX2 restatement of ops/src/kernels.rs), {threads} OpenMP threads"}
 
 
+PEAK_BF16_TFLOPS = 2500.0   # dense MFMA bf16
+PEAK_FP32_TFLOPS = 157.3    # FP32
+
+
+def _timed(L, fn, iters):
+    """Mean GPU time per call from HIP events on the library stream around
+    `iters` back-to-back calls (after 3 warm-up calls), and the host wall
+    time per call (equal when the host issue rate is the limit)."""
+    import ctypes as C
+    from sparrow_amd import check
+    for _ in range(3):
+        check(fn())
+    check(L.vmlm_hip_sync())
+    e0, e1 = C.c_int(), C.c_int()
+    check(L.vmlm_hip_event_record(None, C.byref(e0)))
+    t = time.perf_counter()
+    for _ in range(iters):
+        check(fn())
+    check(L.vmlm_hip_event_record(None, C.byref(e1)))
+    check(L.vmlm_hip_sync())
+    wall = (time.perf_counter() - t) / iters * 1e6
+    ms = C.c_float()
+    check(L.vmlm_hip_event_elapsed_ms(e0.value, e1.value, C.byref(ms)))
+    return ms.value * 1e3 / iters, wall
+
+
+def run_suite(iters):
+    """The other BASELINE configs through the device-pointer API, inputs
+    resident in HBM: per-call time and the achieved fraction of the roofline
+    that bounds each (HBM 8 TB/s, bf16 MFMA 2.5 PF, FP32 157.3 TF)."""
+    import ctypes as C
+    from sparrow_amd import check, conn, lib
+    L = lib()
+    ptrs = []
+
+    def up(a):
+        a = np.ascontiguousarray(a)
+        p = C.c_void_p()
+        check(L.vmlm_hip_malloc(C.byref(p), a.nbytes))
+        check(L.vmlm_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes))
+        ptrs.append(p)
+        return p
+
+    def zeros(nbytes):
+        p = C.c_void_p()
+        check(L.vmlm_hip_malloc(C.byref(p), nbytes))
+        check(L.vmlm_hip_memset(p, 0, nbytes))
+        ptrs.append(p)
+        return p
+
+    def bf16(x):
+        u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    out = {}
+    # config 0: q8 GEMM X f32[16,2304] . (W i8[2304,2304] * scale)^T (+ the M=1 GEMV)
+    rng = np.random.default_rng(0)
+    n = k = 2304
+    x = rng.standard_normal((16, k), dtype=np.float32)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sc = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
+    dx, dq, ds, dy = up(x), up(q), up(sc), zeros(16 * n * 4)
+    cfg0 = {}
+    for m, nbytes in ((16, 5612544), (1, 5336064)):
+        us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt_int8(dx, dq, ds, dy, m, n, k, None), iters)
+        gbs = nbytes / us / 1e3
+        cfg0[f"M{m}"] = {"us": round(us, 2), "host_us": round(wall, 2), "bytes": nbytes,
+                         "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    out["cfg0_q8_gemm"] = cfg0
+    # config 1: bf16 A[1024,512] . B[512,2048] (B passed as its [2048,512] transpose)
+    rng = np.random.default_rng(1)
+    a = bf16(rng.standard_normal((1024, 512), dtype=np.float32))
+    bt = bf16((rng.standard_normal((512, 2048), dtype=np.float32) / np.sqrt(512)).T)
+    da, db, dc = up(a), up(bt), zeros(1024 * 2048 * 4)
+    us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, 1024, 2048, 512, None),
+                      iters)
+    tf = 2147483648 / us / 1e6
+    out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2),
+                             "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    # config 2: causal attention prefill [512, 36, 64] and one decode token vs 1024 positions
+    rng = np.random.default_rng(2)
+    S, H = 512, 36
+    qkv = [up(rng.standard_normal((S, H * 64), dtype=np.float32)) for _ in range(3)]
+    do = zeros(S * H * 64 * 4)
+    us, wall = _timed(L, lambda: L.vmlm_hip_attention_prefill(qkv[0], qkv[1], qkv[2], do, S, H, 64,
+                                                             C.c_float(10000.0), 0,
+                                                             C.c_float(0.125), True, None),
+                      max(8, iters // 4))
+    tf = 1210318848 / us / 1e6
+    cap = 1024
+    kc = up(rng.standard_normal((H, cap, 64), dtype=np.float32))
+    vc = up(rng.standard_normal((H, cap, 64), dtype=np.float32))
+    qd, kd, vd = (up(rng.standard_normal(H * 64, dtype=np.float32)) for _ in range(3))
+    dod = zeros(H * 64 * 4)
+    usd, walld = _timed(L, lambda: L.vmlm_hip_attention_decode(qd, kd, vd, kc, vc, dod, H, 64, cap,
+                                                              cap - 1, C.c_float(10000.0),
+                                                              C.c_float(0.125), None), iters)
+    gbs = (18874368 + 18432) / usd / 1e3
+    out["cfg2_attention"] = {
+        "prefill": {"us": round(us, 2), "host_us": round(wall, 2), "TFLOPs": round(tf, 2),
+                    "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)},
+        "decode": {"us": round(usd, 2), "host_us": round(walld, 2), "GBps": round(gbs, 1),
+                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}}
+    # config 4: B1 stack, 8 layers, d = 1536, k0 = 32, 1024 tokens, tanh
+    rng = np.random.default_rng(4)
+    d, k0, T = 1536, 32, 1024
+    layers = []
+    for li in range(8):
+        w, src = conn.make_block_aligned(rng, d, k0)
+        layers.append(conn.DeviceConn(w, src, layer=li))
+    xb = up(rng.standard_normal((T, d), dtype=np.float32))
+    yb = zeros(T * d * 4)
+    arr = (type(layers[0].struct) * 8)(*[l.struct for l in layers])
+    us, wall = _timed(L, lambda: L.vmlm_b1_stack_forward(arr, 8, xb, yb, T, 4, None),
+                      max(8, iters // 4))
+    layer_bytes = 12976128
+    gbs = 8 * layer_bytes / us / 1e3
+    out["cfg4_b1_stack"] = {"us": round(us, 2), "host_us": round(wall, 2),
+                            "us_per_layer": round(us / 8, 2), "GBps_unique": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                            "note": "includes the two transposes of the stack"}
+    for l in layers:
+        l.free()
+    for p in ptrs:
+        L.vmlm_hip_free(p)
+    return out
+
+
 def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
     from sparrow_amd import model as M
     from sparrow_amd.decoder import Decoder
@@ -112,6 +240,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-iters", type=int, default=400)
+    ap.add_argument("--suite-iters", type=int, default=100)
+    ap.add_argument("--no-suite", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -141,6 +271,11 @@ def main():
         dec1, wall1, _, _, _ = run_decode(cfg, W, 1, args.steps, args.warmup)
         dec1.close()
         log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
+
+    suite = None
+    if not args.no_suite:
+        suite = run_suite(args.suite_iters)
+        log(f"suite: {json.dumps(suite)}")
 
     cpu = None
     if not args.no_cpu:
@@ -174,6 +309,7 @@ def main():
         "event_ms_per_step": round(ev_s / args.steps * 1e3, 4),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "other_configs": suite,
         "tokens_checksum": int(np.asarray(toks, np.int64).sum()),
     }
     print(json.dumps(out))
