@@ -1,13 +1,16 @@
 // capi.hip -- the extern "C" boundary of libvmlm_hip.so (include/vmlm_hip.h).
 //
 // Layer 1 (vmlm_*): host pointers, exact vmlm-ops parameter lists; each call
-// stages its operands in stream-ordered device memory, runs, copies back and
+// stages its operands in a per-stream device workspace, runs, copies back and
 // synchronises (serialised by a mutex). Layer 2 (vmlm_hip_*): device pointers,
 // asynchronous. Both validate like the reference interpreter's guards and
 // return its exit codes instead of exiting.
 #include <cstdarg>
 #include <cstring>
+#include <memory>
 #include <mutex>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "internal.hpp"
@@ -102,24 +105,77 @@ float host_ln_f(float x) {
 // ------------------------------------------------------------------ staging
 // Stream-ordered device buffers freed when the scope ends (after the stream
 // work that uses them is enqueued).
+// Temporaries of an entry point come from a per-stream arena of persistent
+// device blocks, bump-allocated for the duration of the call and reused by
+// the next call on the same stream (stream order keeps the uses apart); the
+// arena's lock is held while the call enqueues its work. Requests above
+// ARENA_BIG go to the stream-ordered allocator instead and are freed after.
+constexpr size_t ARENA_BIG = (size_t)1 << 30;
+struct Arena {
+    std::recursive_mutex mu;  // an entry point may call another on the same stream
+    std::vector<std::pair<char *, size_t>> blocks;
+    size_t blk = 0, off = 0;
+    int depth = 0;  // nested calls keep bumping; the outermost one resets
+};
+static std::mutex g_arena_map_mutex;
+static std::unordered_map<hipStream_t, std::unique_ptr<Arena>> g_arenas;
+
+static Arena &arena_for(hipStream_t st) {
+    std::lock_guard<std::mutex> lk(g_arena_map_mutex);
+    std::unique_ptr<Arena> &a = g_arenas[st];
+    if (!a) a.reset(new Arena);
+    return *a;
+}
+
 struct Stage {
     hipStream_t st;
-    std::vector<void *> bufs;
+    Arena &ar;
+    std::unique_lock<std::recursive_mutex> lk;
+    std::vector<void *> big;
     int status = VMLM_OK;
-    explicit Stage(hipStream_t s) : st(s) {}
+    explicit Stage(hipStream_t s) : st(s), ar(arena_for(s)), lk(ar.mu) {
+        if (ar.depth++ == 0) {
+            ar.blk = 0;
+            ar.off = 0;
+        }
+    }
     ~Stage() {
-        for (void *p : bufs) (void)hipFreeAsync(p, st);
+        for (void *p : big) (void)hipFreeAsync(p, st);
+        --ar.depth;
     }
     template <typename T>
     T *alloc(size_t count) {
-        if (count == 0) count = 1;
+        const size_t bytes = ((count ? count : 1) * sizeof(T) + 255) / 256 * 256;
+        if (bytes > ARENA_BIG) {
+            void *p = nullptr;
+            hipError_t e = hipMallocAsync(&p, bytes, st);
+            if (e != hipSuccess) {
+                status = hip_fail(e, "hipMallocAsync");
+                return nullptr;
+            }
+            big.push_back(p);
+            return (T *)p;
+        }
+        while (ar.blk < ar.blocks.size()) {
+            if (ar.off + bytes <= ar.blocks[ar.blk].second) {
+                char *p = ar.blocks[ar.blk].first + ar.off;
+                ar.off += bytes;
+                return (T *)p;
+            }
+            ++ar.blk;
+            ar.off = 0;
+        }
+        size_t sz = ar.blocks.empty() ? ((size_t)16 << 20) : ar.blocks.back().second * 2;
+        if (sz < bytes) sz = bytes;
         void *p = nullptr;
-        hipError_t e = hipMallocAsync(&p, count * sizeof(T), st);
+        hipError_t e = hipMalloc(&p, sz);
         if (e != hipSuccess) {
-            status = hip_fail(e, "hipMallocAsync");
+            status = hip_fail(e, "hipMalloc (workspace)");
             return nullptr;
         }
-        bufs.push_back(p);
+        ar.blocks.emplace_back((char *)p, sz);
+        ar.blk = ar.blocks.size() - 1;
+        ar.off = bytes;
         return (T *)p;
     }
     template <typename T>
@@ -449,12 +505,14 @@ int vmlm_hip_attention_prefill(const float *q, const float *k, const float *v, f
     hipStream_t st = as_stream(stream);
     Stage stg(st);
     const size_t W = n_heads * head_dim;
-    float *qr = stg.alloc<float>(S * W), *kr = stg.alloc<float>(S * W);
+    float *kr = stg.alloc<float>(S * W);
     STAGE_OK(stg);
-    int rc = launch_rope(qr, q, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
-    if (!rc) rc = launch_rope(kr, k, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
-    if (!rc) rc = launch_attention_prefill(qr, kr, v, out, (int)S, (int)n_heads, (int)W,
-                                           (int)W, scale, causal, st);
+    // K rotated once into the workspace; Q rotated as the attention loads it
+    int rc = launch_rope(kr, k, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
+    if (!rc)
+        rc = launch_attention_prefill(q, kr, v, out, (int)S, (int)n_heads, (int)W, (int)W, scale,
+                                      causal, st, true, -2.0f / (float)head_dim * host_ln_f(theta),
+                                      (float)pos0);
     return rc;
 }
 

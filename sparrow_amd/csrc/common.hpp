@@ -48,9 +48,18 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 
 // ------------------------------------------------------------------ bf16
 // bf16 bits of f32, round to nearest even (tensor/src/dtype.rs:40-46).
+// f32 -> bf16 bits, round to nearest even: v_cvt_pk_bf16_f32, which equals
+// (u + 0x7fff + ((u >> 16) & 1)) >> 16 on every non-NaN input (checked on
+// all 2^28 strided f32 patterns) and keeps NaNs NaN.
+typedef __bf16 hw_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float hw_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
-    uint32_t u = __float_as_uint(v);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v);
+}
+// two values packed (lo = a, hi = b) in one conversion
+__device__ __forceinline__ uint32_t bf16x2_rne_bits(float a, float b) {
+    const hw_f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, hw_bf16x2));
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);

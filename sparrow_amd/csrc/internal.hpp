@@ -103,10 +103,13 @@ int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, 
 int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float *dst_f,
                   int32_t *dst_i, hipStream_t st);
 
-// Attention (head_dim 64). Prefill takes rotated Q and K.
-int launch_attention_prefill(const float *qrot, const float *krot, const float *v, float *out,
+// Attention (head_dim 64). Prefill takes rotated K, and Q rotated (rope_q
+// false) or raw (rope_q: rotated on load with the step -2/64*ln_f(theta),
+// row positions pos0 + row).
+int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
                              int S, int H, int ld, int ldo, float scale, bool causal,
-                             hipStream_t st);
+                             hipStream_t st, bool rope_q = false, float rope_step = 0.0f,
+                             float pos0 = 0.0f);
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;

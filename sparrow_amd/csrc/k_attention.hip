@@ -94,121 +94,276 @@ int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n
 
 // ---------------------------------------------------------------- prefill
 // Q, K already rotated; all [S][ld] with head h at columns h*64.
-constexpr int AT_B = 64;  // query / key block
+//
+// Flash attention on the bf16 matrix cores. Q, K and the probabilities are
+// carried as two bf16 terms x0 = bf16(x), x1 = bf16(x - x0) (|x - x0 - x1|
+// <= 2^-17 |x|), V as three (exact); a product is the sum of the term
+// products (q0k0 + q0k1 + q1k0 + q1k1; p0v0 + p0v1 + p0v2 + p1v0 + p1v1),
+// each exact, accumulated in f32 by v_mfma_f32_16x16x32_bf16: relative error
+// ~2^-16, well inside the 1e-4 * RMS contract of the attention composition,
+// and a one-key softmax row returns its V row exactly. A workgroup owns 64
+// queries of one head (wave w: queries 16w..16w+15) and walks the key blocks
+// of 64 up to the diagonal: K is staged as [key][dim] terms, V transposed as
+// [dim][key] terms, the probabilities go back through LDS as terms, and the
+// running max / sum are per query row (rows 4g..4g+3 of lane (g, r), reduced
+// over the 16 lanes r of a DPP row).
+constexpr int AT_B = 64;   // query / key block
+constexpr int AT_LD = 72;  // bf16 elements per LDS row (64 + 8)
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+// DPP lane moves inside a row of 16 lanes (row_mirror: lane i <- 15 - i;
+// row_half_mirror: i <- 7 - i within each 8; quad_perm [3,2,1,0] and
+// [1,0,3,2]): partners that differ in bit 3, 2, 1, 0 of the lane index.
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_QUAD_REV = 0x1B, DPP_QUAD_SWAP = 0xB1;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_REV>(v));
+    return fmaxf(v, dpp_f<DPP_QUAD_SWAP>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<DPP_ROW_MIRROR>(v);
+    v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_f<DPP_QUAD_REV>(v);
+    return v + dpp_f<DPP_QUAD_SWAP>(v);
+}
+
+__device__ __forceinline__ f32x4 mfma_b(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 8 f32 -> two bf16 term fragments
+__device__ __forceinline__ float bf16_lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+__device__ __forceinline__ void split8(const float (&x)[8], u32x4 &t0, u32x4 &t1) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float a = x[2 * q], b = x[2 * q + 1];
+        const uint32_t h = bf16x2_rne_bits(a, b);
+        t0[q] = h;
+        t1[q] = bf16x2_rne_bits(a - bf16_lo_f32(h), b - bf16_hi_f32(h));
+    }
+}
+
+// 8 f32 -> three bf16 term fragments (their sum is x exactly)
+__device__ __forceinline__ void split8x3(const float (&x)[8], u32x4 &t0, u32x4 &t1, u32x4 &t2) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float a = x[2 * q], b = x[2 * q + 1];
+        const uint32_t h = bf16x2_rne_bits(a, b);
+        const float ra = a - bf16_lo_f32(h), rb = b - bf16_hi_f32(h);
+        const uint32_t m = bf16x2_rne_bits(ra, rb);
+        t0[q] = h;
+        t1[q] = m;
+        t2[q] = bf16x2_rne_bits(ra - bf16_lo_f32(m), rb - bf16_hi_f32(m));
+    }
+}
+
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
-    float *__restrict__ O, int S, int ld, int ldo, float scale, int causal) {
-    __shared__ float Qs[64][AT_B + 1];   // [d][q]
-    __shared__ float KPs[AT_B][AT_B + 1];  // K as [d][key], then P as [q][key]
-    __shared__ float Vs[AT_B][64 + 4];   // [key][d]
-    const int h = blockIdx.y, qb = blockIdx.x;
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int q0 = qb * AT_B;
+    float *__restrict__ O, int S, int ld, int ldo, float scale, int causal, int rope_q,
+    float rope_step, float pos0) {
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
+    __shared__ __attribute__((aligned(16))) uint16_t Ps[4][2][16][AT_LD];  // [wave][term][q][key]
+    // causal work grows with the query block: dispatch the longest first
+    const int h = blockIdx.y, qb = causal ? (int)gridDim.x - 1 - (int)blockIdx.x : blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r = lane & 15;
+    const int q0 = qb * AT_B + wave * 16;
     const float *Qh = Q + h * 64, *Kh = K + h * 64, *Vh = V + h * 64;
 
-    for (int e = threadIdx.x; e < AT_B * 64; e += 256) {
-        int q = e >> 6, d = e & 63;
-        Qs[d][q] = (q0 + q < S) ? Qh[(size_t)(q0 + q) * ld + d] : 0.0f;
+    // this lane's query fragments: row q0 + r, dims 32s + 8g .. +7, two terms;
+    // the lane holds both members (i, i + 32) of its RoPE pairs, so an
+    // unrotated Q is rotated here (position pos0 + row)
+    u32x4 aq[2][2];  // [slice][term]
+    {
+        const int qr = q0 + r < S ? q0 + r : S - 1;
+        float x[2][8];
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+            const float4 *src = (const float4 *)(Qh + (size_t)qr * ld + sl * 32 + g * 8);
+            const float4 x0 = src[0], x1 = src[1];
+            x[sl][0] = x0.x, x[sl][1] = x0.y, x[sl][2] = x0.z, x[sl][3] = x0.w;
+            x[sl][4] = x1.x, x[sl][5] = x1.y, x[sl][6] = x1.z, x[sl][7] = x1.w;
+        }
+        if (rope_q) {
+            const float fpos = pos0 + (float)qr;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                rope_pair(x[0][e], x[1][e], fpos, g * 8 + e, rope_step, &x[0][e], &x[1][e]);
+        }
+        split8(x[0], aq[0][0], aq[0][1]);
+        split8(x[1], aq[1][0], aq[1][1]);
     }
-    float m[4], l[4], o[4][4];
+    float m[4], l[4];
+    f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         m[i] = -INFINITY;
         l[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[i][j] = 0.0f;
+        o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const int nkb = causal ? qb + 1 : (S + AT_B - 1) / AT_B;
-    for (int kb = 0; kb < nkb; ++kb) {
+    // staging roles: K rows (key tid/4, dims 16*(tid%4) ..), V columns (dim
+    // tid%64, keys 16*(tid/64) ..)
+    const int kkey = tid >> 2, kd0 = (tid & 3) * 16;
+    const int vd = tid & 63, vk0 = (tid >> 6) * 16;
+    // the next key block's K / V are loaded into registers while the current
+    // one is consumed (the last block reloads itself)
+    float kx[16], vx[16];
+    auto load_kv = [&](int kb) {
         const int k0 = kb * AT_B;
-        __syncthreads();
-        for (int e = threadIdx.x; e < AT_B * 64; e += 256) {
-            int kk = e >> 6, d = e & 63;
-            bool in = k0 + kk < S;
-            KPs[d][kk] = in ? Kh[(size_t)(k0 + kk) * ld + d] : 0.0f;
-            Vs[kk][d] = in ? Vh[(size_t)(k0 + kk) * ld + d] : 0.0f;
-        }
-        __syncthreads();
-        float s[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) s[i][j] = 0.0f;
-        for (int d = 0; d < 64; ++d) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = Qs[d][ty * 4 + i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = KPs[d][tx * 4 + j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) s[i][j] = __builtin_fmaf(a[i], b[j], s[i][j]);
-        }
-        float pm[4];
+        const int kr = k0 + kkey < S ? k0 + kkey : S - 1;
+        const float4 *src = (const float4 *)(Kh + (size_t)kr * ld + kd0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int q = q0 + ty * 4 + i;
+            const float4 v = src[i];
+            kx[4 * i] = v.x;
+            kx[4 * i + 1] = v.y;
+            kx[4 * i + 2] = v.z;
+            kx[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int vr = k0 + vk0 + i < S ? k0 + vk0 + i : S - 1;
+            vx[i] = Vh[(size_t)vr * ld + vd];
+        }
+    };
+    load_kv(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * AT_B;
+        __syncthreads();  // the previous block's K / V are no longer read
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float x[8], y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x[i] = k0 + kkey < S ? kx[8 * half + i] : 0.0f;
+                y[i] = k0 + vk0 + 8 * half + i < S ? vx[8 * half + i] : 0.0f;
+            }
+            u32x4 t0, t1, t2;
+            split8(x, t0, t1);
+            *(u32x4 *)&Ks[0][kkey][kd0 + 8 * half] = t0;
+            *(u32x4 *)&Ks[1][kkey][kd0 + 8 * half] = t1;
+            split8x3(y, t0, t1, t2);
+            *(u32x4 *)&Vt[0][vd][vk0 + 8 * half] = t0;
+            *(u32x4 *)&Vt[1][vd][vk0 + 8 * half] = t1;
+            *(u32x4 *)&Vt[2][vd][vk0 + 8 * half] = t2;
+        }
+        __syncthreads();
+        load_kv(kb + 1 < nkb ? kb + 1 : kb);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // scores: block j = keys 16j..16j+15; lane (g, r): queries 4g+i, key 16j+r
+        f32x4 sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) {
+                const u32x4 b0 = *(const u32x4 *)&Ks[0][16 * j + r][sl * 32 + g * 8];
+                const u32x4 b1 = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
+                acc = mfma_b(aq[sl][0], b0, acc);
+                acc = mfma_b(aq[sl][0], b1, acc);
+                acc = mfma_b(aq[sl][1], b0, acc);
+                acc = mfma_b(aq[sl][1], b1, acc);
+            }
+            sc[j] = acc;
+        }
+        float rmax[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qa = q0 + 4 * g + i;
             float mx = -INFINITY;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int kk = k0 + tx * 4 + j;
-                bool valid = kk < S && (!causal || kk <= q);
-                s[i][j] = valid ? s[i][j] * scale : -INFINITY;
-                mx = fmaxf(mx, s[i][j]);
+                const int ka = k0 + 16 * j + r;
+                const bool valid = ka < S && (!causal || ka <= qa);
+                sc[j][i] = valid ? sc[j][i] * scale : -INFINITY;
+                mx = fmaxf(mx, sc[j][i]);
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            pm[i] = fmaxf(m[i], mx);
+            rmax[i] = row16_max(mx);
         }
-        __syncthreads();  // K no longer needed; reuse its LDS for P
+        float p[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float corr = (m[i] == -INFINITY) ? 0.0f : exp_f(m[i] - pm[i]);
+            const float mn = fmaxf(m[i], rmax[i]);
+            const float alpha = m[i] == -INFINITY ? 0.0f : __expf(m[i] - mn);
             float rs = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float p = (s[i][j] == -INFINITY) ? 0.0f : exp_f(s[i][j] - pm[i]);
-                KPs[ty * 4 + i][tx * 4 + j] = p;
-                rs += p;
+                p[j][i] = sc[j][i] == -INFINITY ? 0.0f : __expf(sc[j][i] - mn);
+                rs += p[j][i];
             }
+            rs = row16_sum(rs);
+            l[i] = l[i] * alpha + rs;
+            m[i] = mn;
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
-            l[i] = l[i] * corr + rs;
-            m[i] = pm[i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) o[i][j] *= corr;
+            for (int jd = 0; jd < 4; ++jd) o[jd][i] *= alpha;
         }
-        __syncthreads();
-        for (int kk = 0; kk < AT_B; ++kk) {
-            float p[4], v[4];
+        // P terms -> LDS as [q][key] rows of this wave
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = KPs[ty * 4 + i][kk];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = Vs[kk][tx * 4 + j];
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t hb = bf16_rne_bits(p[j][i]);
+                const uint32_t lb = bf16_rne_bits(p[j][i] - bf16_bits_to_f32(hb));
+                Ps[wave][0][4 * g + i][16 * j + r] = (uint16_t)hb;
+                Ps[wave][1][4 * g + i][16 * j + r] = (uint16_t)lb;
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // O[q][d] += P[q][key] V[key][d]: A = P rows, B = V^T rows (dims)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int sl = 0; sl < 2; ++sl) {
+            const u32x4 p0 = *(const u32x4 *)&Ps[wave][0][r][sl * 32 + g * 8];
+            const u32x4 p1 = *(const u32x4 *)&Ps[wave][1][r][sl * 32 + g * 8];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[i][j] = __builtin_fmaf(p[i], v[j], o[i][j]);
+            for (int jd = 0; jd < 4; ++jd) {
+                const u32x4 v0 = *(const u32x4 *)&Vt[0][16 * jd + r][sl * 32 + g * 8];
+                const u32x4 v1 = *(const u32x4 *)&Vt[1][16 * jd + r][sl * 32 + g * 8];
+                const u32x4 v2 = *(const u32x4 *)&Vt[2][16 * jd + r][sl * 32 + g * 8];
+                o[jd] = mfma_b(p0, v0, o[jd]);
+                o[jd] = mfma_b(p0, v1, o[jd]);
+                o[jd] = mfma_b(p0, v2, o[jd]);
+                o[jd] = mfma_b(p1, v0, o[jd]);
+                o[jd] = mfma_b(p1, v1, o[jd]);
+            }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    // lane (g, r) of block jd: queries 4g+i, dim 16jd + r
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int q = q0 + ty * 4 + i;
-        if (q >= S) continue;
+        const int qa = q0 + 4 * g + i;
+        if (qa >= S) continue;
         const float inv = 1.0f / l[i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) O[(size_t)q * ldo + h * 64 + tx * 4 + j] = o[i][j] * inv;
+        for (int jd = 0; jd < 4; ++jd) O[(size_t)qa * ldo + h * 64 + 16 * jd + r] = o[jd][i] * inv;
     }
 }
 
-int launch_attention_prefill(const float *qrot, const float *krot, const float *v, float *out,
+int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
                              int S, int H, int ld, int ldo, float scale, bool causal,
-                             hipStream_t st) {
+                             hipStream_t st, bool rope_q, float rope_step, float pos0) {
+    VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)krot & 15) == 0,
+               "attention prefill: 16-byte aligned rows required");
     dim3 grid(cdiv(S, AT_B), H);
-    attn_prefill_kernel<<<grid, 256, 0, st>>>(qrot, krot, v, out, S, ld, ldo, scale,
-                                              causal ? 1 : 0);
+    attn_prefill_kernel<<<grid, 256, 0, st>>>(q, krot, v, out, S, ld, ldo, scale,
+                                              causal ? 1 : 0, rope_q ? 1 : 0, rope_step, pos0);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -230,17 +385,6 @@ int launch_attention_prefill(const float *qrot, const float *krot, const float *
 // CU so that all of them are resident at once.
 constexpr int BUF_RSRC_WORD3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 
-// DPP lane moves inside a row of 16 lanes (row_mirror: lane i <- 15 - i;
-// row_half_mirror: i <- 7 - i within each 8; quad_perm [3,2,1,0] and
-// [1,0,3,2]): partners that differ in bit 3, 2, 1, 0 of the lane index.
-constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141;
-constexpr int DPP_QUAD_REV = 0x1B, DPP_QUAD_SWAP = 0xB1;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
 
 // One stage of the transposing butterfly: N values per lane become N/2 sums;
 // the lane with `up` keeps the upper half and sends the lower.
