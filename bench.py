@@ -28,6 +28,23 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wide_decode_minicpm2b_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode GEMV from the committed counter
+    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
+    a plain copy's reading; the command is in the file), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch_mean:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def gemv_roofline(dec, iters):
     """q8 GEMV (the int8 projections of a decode step): mean launch duration
     per shape from HIP events on the session stream, and the step-mix
@@ -46,7 +63,9 @@ def gemv_roofline(dec, iters):
     achieved = tot_b / tot_t / 1e3  # GB/s
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)",
+            "traffic": measured_traffic(),
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
+            "kernel": "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)",
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "per_shape": per}
 
@@ -231,6 +250,35 @@ def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
     return dec, wall, ms.value / 1e3, t0, toks
 
 
+def traffic_probe(iters):
+    """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` runs: a plain device copy
+    of 256 MiB (the calibration: its bytes are known) three times, then the
+    four decode GEMV shapes of the batch-16 session `iters` times each."""
+    import ctypes as C
+    from sparrow_amd import check, lib
+    from sparrow_amd import model as M
+    from sparrow_amd.decoder import Decoder
+    L = lib()
+    nbytes = 256 << 20
+    a, b = C.c_void_p(), C.c_void_p()
+    check(L.vmlm_hip_malloc(C.byref(a), nbytes))
+    check(L.vmlm_hip_malloc(C.byref(b), nbytes))
+    check(L.vmlm_hip_memset(a, 1, nbytes))
+    for _ in range(3):
+        check(L.vmlm_hip_memcpy_d2d(b, a, nbytes))
+    check(L.vmlm_hip_free(a))
+    check(L.vmlm_hip_free(b))
+    cfg = M.minicpm_2b_config()
+    W = M.make_weights(cfg, seed=3, threads=16)
+    dec = Decoder(cfg, batch=16, cap=1024)
+    dec.load(W)
+    dec.prefill(M.make_prompts(cfg, 16, 128, seed=3))
+    for which in range(4):
+        dec.time_gemv(which, iters)
+    dec.close()
+    print(json.dumps({"probe": "traffic", "copy_bytes": nbytes, "gemv_iters": iters}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +290,8 @@ def main():
     ap.add_argument("--gemv-iters", type=int, default=400)
     ap.add_argument("--suite-iters", type=int, default=100)
     ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only the copy + GEMV launches that the counter runs measure")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -253,6 +303,9 @@ def main():
     import sparrow_amd
     from sparrow_amd import model as M
     sparrow_amd.init(0)
+    if args.traffic_probe:
+        traffic_probe(20)
+        return
     cfg = M.minicpm_2b_config()
     t = time.time()
     W = M.make_weights(cfg, seed=3, threads=16)

@@ -63,6 +63,9 @@ int vmlm_hip_malloc(void **dptr, size_t bytes);
 int vmlm_hip_free(void *dptr);
 int vmlm_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int vmlm_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+/* device -> device on the library stream (synchronous); also the plain copy
+ * of known size that calibrates the HBM traffic counters */
+int vmlm_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int vmlm_hip_memset(void *dptr, int value, size_t bytes);
 /* Event timing on a stream (NULL = library stream): returns an opaque id. */
 int vmlm_hip_event_record(void *stream, int *event_id);

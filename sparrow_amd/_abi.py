@@ -36,6 +36,7 @@ SIGNATURES = {
     "vmlm_hip_free": (I, [P]),
     "vmlm_hip_memcpy_h2d": (I, [P, P, SZ]),
     "vmlm_hip_memcpy_d2h": (I, [P, P, SZ]),
+    "vmlm_hip_memcpy_d2d": (I, [P, P, SZ]),
     "vmlm_hip_memset": (I, [P, I, SZ]),
     "vmlm_hip_event_record": (I, [P, C.POINTER(I)]),
     "vmlm_hip_event_elapsed_ms": (I, [I, I, C.POINTER(F)]),

@@ -318,6 +318,12 @@ int vmlm_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
     VMLM_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return VMLM_OK;
 }
+int vmlm_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, lib_stream()));
+    VMLM_HIP_CHECK(hipStreamSynchronize(lib_stream()));
+    return VMLM_OK;
+}
 int vmlm_hip_memset(void *dptr, int value, size_t bytes) {
     INIT_OR_RETURN();
     VMLM_HIP_CHECK(hipMemset(dptr, value, bytes));

@@ -608,11 +608,13 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
         }
         }
     };
+    // one event pair around `iters` back-to-back launches (the mean launch
+    // duration, launch gaps included); successive launches walk the layers
+    // so that no weight is re-read from cache
     hipEvent_t e0, e1;
     VMLM_HIP_CHECK(hipEventCreate(&e0));
     VMLM_HIP_CHECK(hipEventCreate(&e1));
-    // warm-up pass over every layer
-    for (size_t l = 0; l < (which == 4 ? 1 : d->L); ++l)
+    for (size_t l = 0; l < (which == 4 ? 1 : d->L); ++l)  // warm-up pass over every layer
         if ((rc = launch_gemv(make(l), d->st))) return rc;
     VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
     for (uint32_t i = 0; i < iters; ++i)

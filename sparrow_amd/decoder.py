@@ -96,7 +96,7 @@ class Decoder:
     def time_gemv(self, which: int, iters: int):
         """Mean per-launch duration (us, HIP events on the session stream) of
         one decode-step GEMV over every layer in turn, and its algorithmic
-        bytes. which: 0 qkv, 1 o, 2 gate/up (+SiLU*up), 3 down, 4 LM head."""
+        bytes. which: 0 qkv, 1 o, 2 gate/up, 3 down (k-slice partials), 4 LM head."""
         us = C.c_float()
         nbytes = C.c_double()
         check(lib().vmlm_decoder_time_gemv(self._h, int(which), int(iters), C.byref(us),
