@@ -271,28 +271,29 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide variant for int8 weights: the 8 waves of a workgroup own 8 different
-// 16-row tiles (128 rows) over one k-slice of NC chunks (blockIdx.y), and
+// Wide variant for int8 weights: the NWV (8 or 16) waves of a workgroup own
+// NWV different 16-row tiles over one k-slice of NC chunks (blockIdx.y), and
 // share that slice of the activation terms, loaded once into LDS. Activation
 // bytes from L2 per weight byte drop from M*T*2/16 (one tile per workgroup)
-// to M*T*2/128. All weight chunks of a wave and the activation slice are in
+// to M*T*2/(16*NWV). All weight chunks of a wave and the activation slice are in
 // flight together (one memory round trip); the workgroup's k-slice sums go
 // out raw (EPI_PARTIAL, reduced in a fixed order by the consumer) or, with a
 // single slice, through the usual epilogues.
-template <int T, bool BT, int NC>
-__global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
+template <int T, bool BT, int NC, int NWV>
+__global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
+    constexpr int NTH = NWV * 64;
     constexpr int TA = BT ? 1 : T;
     constexpr int KW = NC * 128;  // k of the slice
     constexpr int ALD = KW + 8;   // LDS row of the activation slice (+16 B)
     __shared__ __attribute__((aligned(16))) uint16_t as[TA][16][ALD];
-    __shared__ __attribute__((aligned(16))) uint8_t wbuf[8][16][CH_LD];
-    __shared__ float dwave[8][16][17];
+    __shared__ __attribute__((aligned(16))) uint8_t wbuf[NWV][16][CH_LD];
+    __shared__ float dwave[NWV][16][17];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, rr = lane & 15;
     const int lrow = lane >> 3, lcol = (lane & 7) * 16;
-    const int tile = blockIdx.x * 8 + wave;
+    const int tile = blockIdx.x * NWV + wave;
     const int k0 = blockIdx.y * KW;
 
     // this wave's weight rows, every chunk of the slice (rows clamped)
@@ -313,11 +314,11 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
     // past the live ones repeat row 0 (their outputs are never read)
     const int arows = BT ? T * p.M : p.M;
     constexpr int PIECES = TA * 16 * (KW / 8);
-    constexpr int PER = (PIECES + 511) / 512;
+    constexpr int PER = (PIECES + NTH - 1) / NTH;
     u32x4 ap[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        int e = tid + i * 512;
+        int e = tid + i * NTH;
         e = e < PIECES ? e : PIECES - 1;
         const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
         const int rs = r < arows ? r : 0;
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        int e = tid + i * 512;
+        int e = tid + i * NTH;
         e = e < PIECES ? e : PIECES - 1;
         const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
         *(u32x4 *)&as[tt][r][c8 * 8] = ap[i];
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(GemvParams p) {
     };
     if (p.epi == EPI_SILU_MUL) {  // wave 2q: gate tile, wave 2q + 1: up tile
         if (wave & 1) return;
-        const int pt = blockIdx.x * 4 + (wave >> 1);
+        const int pt = blockIdx.x * (NWV / 2) + (wave >> 1);
         for (int e = lane; e < p.M * 16; e += 64) {
             const int b = e >> 4, col = e & 15;
             const int jg = tile * 16 + col, ju = jg + 16, jo = pt * 16 + col;
@@ -585,17 +586,45 @@ static int launch_wloop_t(const GemvParams &p, hipStream_t st) {
     return VMLM_OK;
 }
 
-template <int T, bool BT>
-static int launch_wide_t(const GemvParams &p, int nc, hipStream_t st) {
-    const dim3 grid((p.N + 127) / 128, p.ks);
-    switch (nc) {
-    case 1: gemv_wide_kernel<T, BT, 1><<<grid, 512, 0, st>>>(p); break;
-    case 2: gemv_wide_kernel<T, BT, 2><<<grid, 512, 0, st>>>(p); break;
-    case 3: gemv_wide_kernel<T, BT, 3><<<grid, 512, 0, st>>>(p); break;
-    default: return fail(VMLM_ERR_UNIMPL, "gemv wide: %d chunks per slice", nc);
+// Workgroups of one wide-kernel variant resident on the device at once.
+template <int T, bool BT, int NC, int NWV>
+static int wide_slots() {
+    static int slots = -1;
+    if (slots < 0) {
+        int per_cu = 0, dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, (const void *)gemv_wide_kernel<T, BT, NC, NWV>, NWV * 64, 0) != hipSuccess)
+            return 0;
+        slots = per_cu * cus;
+    }
+    return slots;
+}
+
+// 8 waves (128 rows) per workgroup while the grid fits on the device in one
+// round; 16 waves (256 rows, half the workgroups) when it would spill into a
+// second round and the rows split evenly.
+template <int T, bool BT, int NC>
+static int launch_wide_nc(const GemvParams &p, hipStream_t st) {
+    const int wgs8 = (p.N + 127) / 128 * p.ks;
+    if (p.N % 256 == 0 && wgs8 > wide_slots<T, BT, NC, 8>()) {
+        gemv_wide_kernel<T, BT, NC, 16><<<dim3(p.N / 256, p.ks), 1024, 0, st>>>(p);
+    } else {
+        gemv_wide_kernel<T, BT, NC, 8><<<dim3((p.N + 127) / 128, p.ks), 512, 0, st>>>(p);
     }
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
+}
+
+template <int T, bool BT>
+static int launch_wide_t(const GemvParams &p, int nc, hipStream_t st) {
+    switch (nc) {
+    case 1: return launch_wide_nc<T, BT, 1>(p, st);
+    case 2: return launch_wide_nc<T, BT, 2>(p, st);
+    case 3: return launch_wide_nc<T, BT, 3>(p, st);
+    default: return fail(VMLM_ERR_UNIMPL, "gemv wide: %d chunks per slice", nc);
+    }
 }
 
 __global__ void split_terms_kernel(const float *__restrict__ x, size_t ldx, int rows, int K,
