@@ -71,6 +71,8 @@ struct GemmArgs {
     int M = 0, N = 0, K = 0; // K % 64 == 0
     float *C = nullptr;
     int ldc = 0;
+    int bm = 0;      // tile rows (64, 128); 0 = chosen by shape
+    int stages = 0;  // LDS stages of the copy pipeline (2..4); 0 = chosen by shape
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
 

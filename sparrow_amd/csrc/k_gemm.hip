@@ -1,7 +1,8 @@
 // k_gemm.hip -- LDS-tiled MFMA GEMM for M > 16 (prefill, dense bf16 shape).
 //
-// C[M,N] = A[M,K] . W[N,K]^T (* scale[n]) with W int8 (converted exactly to
-// bf16 when staged into LDS) or bf16, and A given as T bf16 term planes
+// C[M,N] = A[M,K] . W[N,K]^T (* scale[n]) with W int8 (kept int8 in LDS and
+// converted exactly to bf16 per MFMA fragment) or bf16, and A given as T bf16
+// term planes
 // (T = 1 for bf16 activations, 3 for f32 activations; see split_bf16).
 // Replaces gemm_nt_int8 / gemm_nt_bf16 (ops/src/kernels.rs:1199-1287) for
 // multi-row activations; f32 accumulation in the MFMA, order differs from the
@@ -25,76 +26,116 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-constexpr int G_BK = 64;
-constexpr int G_LDK = G_BK + 8;  // padded LDS row (bf16 elements)
+// s_waitcnt immediate (gfx9 encoding) that waits for the vector-memory
+// counter to drop to n and leaves the other counters unconstrained.
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
-// Workgroup tile BM x BN (A rows x W rows) x 64 k, 4 wavefronts as 2 x 2,
-// each (BM/2) x (BN/2) of 16x16 MFMA blocks. Per k-step every thread loads
-// its share of the next tile into registers (unconditionally: rows clamped,
-// the last step reloads itself) while the current tile is consumed from LDS.
-template <bool WI8, int T, int BM, int BN>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmParams p) {
-    constexpr int WM = BM / 2, WN = BN / 2;    // per-wave tile
-    constexpr int TM = WM / 16, TN = WN / 16;  // MFMA blocks per wave
-    __shared__ __attribute__((aligned(16))) uint16_t As[T][BM][G_LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[BN][G_LDK];
+// One 16-byte-per-lane copy from global memory into LDS: lane i's 16 bytes
+// at gptr land at LDS byte address lds_base + 16 * i (lds_base wave-uniform).
+// Issued as inline assembly so that the compiler does not order every later
+// LDS read behind it; the callers wait for the copies with explicit vmcnt
+// waits and publish them with barriers. m0 is not used by anything else in
+// these kernels.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; nothing else here uses it
+__device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t *)p;
+}
+
+// 8 int8 weights -> 8 bf16 (exact).
+__device__ __forceinline__ u32x4 i8x8_to_bf16(uint32_t w0, uint32_t w1) {
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t x = q ? w1 : w0;
+        d[2 * q] = pack_hi16((float)(int)(int8_t)(x & 0xffu), (float)(int)(int8_t)((x >> 8) & 0xffu));
+        d[2 * q + 1] = pack_hi16((float)(int)(int8_t)((x >> 16) & 0xffu), (float)(int)(int8_t)(x >> 24));
+    }
+    return u32x4{d[0], d[1], d[2], d[3]};
+}
+
+// GEMM with the tiles copied straight from global memory into LDS
+// (global_load_lds_dwordx4: no register staging) through an NS-stage ring:
+// the copy of k-step kt + NS - 1 is issued while step kt is consumed, and one
+// barrier per step both publishes step kt and retires the reads of step
+// kt - 1, whose stage the new copy overwrites. Copies past the last step
+// re-read it into a stage that is never consumed again, so every step waits
+// for the same number of outstanding copies.
+//
+// LDS rows hold 64 k: A (bf16 terms) and bf16 W 128 bytes, int8 W 64 bytes.
+// The 16-byte pieces of a row are XOR-swizzled (piece c of row R sits in
+// slot c ^ (R & 7); int8: c ^ ((R >> 1) & 3)) so that the 16 rows of an MFMA
+// fragment read spread over the banks. Each copy instruction fills 1 KB of
+// consecutive LDS (8 rows of 128 B or 16 of 64 B); the swizzle is applied by
+// choosing which global piece each lane fetches.
+//
+// The epilogue stages each wave's 16-row slabs through LDS so that rows go
+// out as 16-byte stores.
+template <bool WI8, int T, int BM, int BN, int NS>
+__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    constexpr int A_ROW = 128, B_ROW = WI8 ? 64 : 128;
+    constexpr int A_BYTES = T * BM * A_ROW, B_BYTES = BN * B_ROW;
+    constexpr int STAGE = A_BYTES + B_BYTES;
+    constexpr int C_LD = WN + 4;
+    constexpr int C_BYTES = 4 * 16 * C_LD * 4;
+    constexpr int SMEM = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
+    constexpr int A_INS = A_BYTES / 1024 / 4, B_INS = B_BYTES / 1024 / 4;  // per wave per step
+    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copy instructions per wave");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int g = lane >> 4, r = lane & 15;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int nk = p.K / 64;
 
-    // 16-byte pieces per k-step: A: T*BM rows x 8; W: BN rows x 4 (int8) or 8
-    constexpr int A_CHUNKS = T * BM * 8;
-    static_assert(A_CHUNKS % 256 == 0, "A tile pieces per thread");
-    constexpr int A_PER = A_CHUNKS / 256;
-    constexpr int CPR = WI8 ? 4 : 8;
-    constexpr int B_CHUNKS = BN * CPR;
-    static_assert(B_CHUNKS % 256 == 0, "W tile pieces per thread");
-    constexpr int B_PER = B_CHUNKS / 256;
-    const uint16_t *asrc[A_PER];
-    const uint8_t *bsrc[B_PER];
+    // copy plan: global source of this lane (k-step 0) per instruction
+    const uint8_t *a_src[A_INS];
+    const uint8_t *b_src[B_INS];
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-        const int c = tid + i * 256, t = c / (BM * 8), rem = c % (BM * 8);
-        int gm = m0 + rem / 8;
+    for (int q = 0; q < A_INS; ++q) {
+        const int rowg = (q * 4 + wave) * 8 + (lane >> 3);  // over the T*BM rows
+        const int t = rowg / BM, R = rowg % BM;
+        const int c = (lane & 7) ^ (R & 7);
+        int gm = m0 + R;
         gm = gm < p.M ? gm : p.M - 1;
-        asrc[i] = p.A + t * p.tstride + (size_t)gm * p.lda + (rem % 8) * 8;
+        a_src[q] = (const uint8_t *)(p.A + t * p.tstride + (size_t)gm * p.lda) + c * 16;
     }
 #pragma unroll
-    for (int i = 0; i < B_PER; ++i) {
-        const int c = tid + i * 256;
-        int gn = n0 + c / CPR;
+    for (int q = 0; q < B_INS; ++q) {
+        int R, c;
+        if constexpr (WI8) {
+            R = (q * 4 + wave) * 16 + (lane >> 2);
+            c = (lane & 3) ^ ((R >> 1) & 3);
+        } else {
+            R = (q * 4 + wave) * 8 + (lane >> 3);
+            c = (lane & 7) ^ (R & 7);
+        }
+        int gn = n0 + R;
         gn = gn < p.N ? gn : p.N - 1;
-        bsrc[i] = p.W + (size_t)gn * p.K * (WI8 ? 1 : 2) + (c % CPR) * 16;
+        b_src[q] = p.W + (size_t)gn * p.K * (WI8 ? 1 : 2) + c * 16;
     }
-    u32x4 ra[A_PER], rb[B_PER];
-    auto load_tile = [&](int k0) {
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+    auto issue = [&](int kt) {
+        const int kc = kt < nk ? kt : nk - 1;
+        const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
 #pragma unroll
-        for (int i = 0; i < A_PER; ++i) ra[i] = *(const u32x4 *)(asrc[i] + k0);
+        for (int q = 0; q < A_INS; ++q)
+            dma16(a_src[q] + (size_t)kc * A_ROW, sb + (q * 4 + wave) * 1024);
 #pragma unroll
-        for (int i = 0; i < B_PER; ++i)
-            rb[i] = __builtin_nontemporal_load((const u32x4 *)(bsrc[i] + (size_t)k0 * (WI8 ? 1 : 2)));
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_PER; ++i) {
-            const int c = tid + i * 256, t = c / (BM * 8), rem = c % (BM * 8);
-            *(u32x4 *)&As[t][rem / 8][(rem % 8) * 8] = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER; ++i) {
-            const int c = tid + i * 256;
-            if constexpr (WI8) {
-                u32x4 lo, hi;
-                i8x16_to_bf16(rb[i], lo, hi);
-                *(u32x4 *)&Bs[c / 4][(c % 4) * 16] = lo;
-                *(u32x4 *)&Bs[c / 4][(c % 4) * 16 + 8] = hi;
-            } else {
-                *(u32x4 *)&Bs[c / 8][(c % 8) * 8] = rb[i];
-            }
-        }
+        for (int q = 0; q < B_INS; ++q)
+            dma16(b_src[q] + (size_t)kc * B_ROW, sb + A_BYTES + (q * 4 + wave) * 1024);
     };
 
     f32x4 acc[TM][TN];
@@ -103,64 +144,123 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = p.K / G_BK;
-    load_tile(0);
-    for (int kt = 0; kt < nk; ++kt) {
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        load_tile((kt + 1 < nk ? kt + 1 : kt) * G_BK);
-        __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out before the MFMAs
+    auto compute = [&](const uint8_t *sA) {
+        const uint8_t *sB = sA + A_BYTES;
 #pragma unroll
-        for (int ks = 0; ks < G_BK / 32; ++ks) {
+        for (int ks = 0; ks < 2; ++ks) {
             u32x4 bf[TN];
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[j] = *(const u32x4 *)&Bs[wn * WN + j * 16 + r][ks * 32 + g * 8];
+            for (int j = 0; j < TN; ++j) {
+                const int R = wn * WN + j * 16 + r;
+                if constexpr (WI8) {
+                    const int c = ks * 2 + (g >> 1);
+                    const uint2 v = *(const uint2 *)(sB + R * 64 + ((c ^ ((R >> 1) & 3)) * 16) +
+                                                     (g & 1) * 8);
+                    bf[j] = i8x8_to_bf16(v.x, v.y);
+                } else {
+                    const int c = ks * 4 + g;
+                    bf[j] = *(const u32x4 *)(sB + R * 128 + ((c ^ (R & 7)) * 16));
+                }
+            }
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
+            for (int t = 0; t < T; ++t)
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    const u32x4 af = *(const u32x4 *)&As[t][wm * WM + i * 16 + r][ks * 32 + g * 8];
+                    const int R = wm * WM + i * 16 + r;
+                    const int c = ks * 4 + g;
+                    const u32x4 af =
+                        *(const u32x4 *)(sA + (t * BM + R) * 128 + ((c ^ (R & 7)) * 16));
 #pragma unroll
                     for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(af, bf[j], acc[i][j]);
                 }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * (A_INS + B_INS)));
+        __syncthreads();
+        issue(kt + NS - 1);
+        compute(smem + (kt % NS) * STAGE);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // copies past the end land before reuse
+    __syncthreads();
+
+    // epilogue: 16-row slabs of this wave's tile through LDS, 16-byte stores
+    float *cs = (float *)smem + wave * 16 * C_LD;
+    const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.C & 15) == 0;
+    constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cs[(g * 4 + q) * C_LD + j * 16 + r] = acc[i][j][q];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's slab is in LDS
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int pass = 0; pass < 16 / RPP; ++pass) {
+            const int rr_ = pass * RPP + lane / LPR, c4 = (lane % LPR) * 4;
+            float4 v = *(const float4 *)&cs[rr_ * C_LD + c4];
+            const int row = m0 + wm * WM + i * 16 + rr_, col = n0 + wn * WN + c4;
+            if (row >= p.M || col >= p.N) continue;
+            float y[4] = {v.x, v.y, v.z, v.w};
+            if (p.scale) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = y[e] * p.scale[col + e < p.N ? col + e : col];
+            }
+            float *dst = p.C + (size_t)row * p.ldc + col;
+            if (vec && col + 3 < p.N) {
+                *(float4 *)dst = make_float4(y[0], y[1], y[2], y[3]);
+            } else {
+                for (int e = 0; e < 4 && col + e < p.N; ++e) dst[e] = y[e];
             }
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
     }
+}
 
-    // D layout: lane (g, r) holds rows 4g..4g+3 of the A block, column r
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 16 + r;
-        if (col >= p.N) continue;
-        const float sc = p.scale ? p.scale[col] : 1.0f;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int row = m0 + wm * WM + i * 16 + g * 4 + q;
-                if (row < p.M) {
-                    const float v = acc[i][j][q];
-                    p.C[(size_t)row * p.ldc + col] = p.scale ? v * sc : v;
-                }
-            }
+constexpr int DMA_LDS_MAX = 160 * 1024;
+constexpr int dma_stage_bytes(bool wi8, int T, int BM, int BN) {
+    return T * BM * 128 + BN * (wi8 ? 64 : 128);
+}
+
+template <bool WI8, int T, int BM, int BN, int NS>
+static int launch_dma_ns(const GemmParams &p, hipStream_t st) {
+    if constexpr (NS * dma_stage_bytes(WI8, T, BM, BN) <= DMA_LDS_MAX) {
+        const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
+        gemm_dma_kernel<WI8, T, BM, BN, NS><<<grid, 256, 0, st>>>(p);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    } else {
+        return fail(VMLM_ERR_UNIMPL, "gemm: %d LDS stages exceed the LDS", NS);
+    }
+}
+
+template <bool WI8, int T, int BM, int BN>
+static int launch_dma(const GemmParams &p, int ns, hipStream_t st) {
+    switch (ns) {
+    case 2: return launch_dma_ns<WI8, T, BM, BN, 2>(p, st);
+    case 3: return launch_dma_ns<WI8, T, BM, BN, 3>(p, st);
+    case 4: return launch_dma_ns<WI8, T, BM, BN, 4>(p, st);
+    default: return fail(VMLM_ERR_UNIMPL, "gemm: %d LDS stages", ns);
     }
 }
 
 template <bool WI8, int T>
-static int launch_g(const GemmParams &p, hipStream_t st) {
-    // 128 x 128 tiles, or 64 x 128 when that leaves fewer workgroups than CUs
-    const int n_blocks = (p.N + 127) / 128;
-    if (((p.M + 127) / 128) * n_blocks >= 256) {
-        const dim3 grid(n_blocks, (p.M + 127) / 128);
-        gemm_kernel<WI8, T, 128, 128><<<grid, 256, 0, st>>>(p);
-    } else {
-        const dim3 grid(n_blocks, (p.M + 63) / 64);
-        gemm_kernel<WI8, T, 64, 128><<<grid, 256, 0, st>>>(p);
-    }
-    VMLM_HIP_CHECK(hipGetLastError());
-    return VMLM_OK;
+static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
+    // Tiles: 128 x 128 for single-term (bf16) activations when that still
+    // gives two workgroups per CU (512 on this device), else 64 x 128 (and
+    // always with three terms, whose 128-row stage would leave one workgroup
+    // per CU). Two LDS stages keep two workgroups resident per CU.
+    if (bm == 0) bm = T == 1 && ((p.M + 127) / 128) * ((p.N + 127) / 128) >= 512 ? 128 : 64;
+    VMLM_GUARD(bm == 64 || bm == 128, "gemm: tile rows %d (64 or 128)", bm);
+    if (ns == 0) ns = 2;
+    VMLM_GUARD(ns >= 2 && ns <= 4 && ns * dma_stage_bytes(WI8, T, bm, 128) <= DMA_LDS_MAX,
+               "gemm: %d LDS stages of %d bytes", ns, dma_stage_bytes(WI8, T, bm, 128));
+    return bm == 128 ? launch_dma<WI8, T, 128, 128>(p, ns, st) : launch_dma<WI8, T, 64, 128>(p, ns, st);
 }
 
 int launch_gemm(const GemmArgs &a, hipStream_t st) {
@@ -181,15 +281,15 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
     p.ldc = a.ldc;
     if (a.w_int8) {
         switch (a.T) {
-        case 1: return launch_g<true, 1>(p, st);
-        case 2: return launch_g<true, 2>(p, st);
-        case 3: return launch_g<true, 3>(p, st);
+        case 1: return launch_g<true, 1>(p, a.bm, a.stages, st);
+        case 2: return launch_g<true, 2>(p, a.bm, a.stages, st);
+        case 3: return launch_g<true, 3>(p, a.bm, a.stages, st);
         }
     } else {
         switch (a.T) {
-        case 1: return launch_g<false, 1>(p, st);
-        case 2: return launch_g<false, 2>(p, st);
-        case 3: return launch_g<false, 3>(p, st);
+        case 1: return launch_g<false, 1>(p, a.bm, a.stages, st);
+        case 2: return launch_g<false, 2>(p, a.bm, a.stages, st);
+        case 3: return launch_g<false, 3>(p, a.bm, a.stages, st);
         }
     }
     return fail(VMLM_ERR_UNIMPL, "gemm: %d activation terms unsupported", a.T);

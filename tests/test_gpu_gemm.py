@@ -1,0 +1,104 @@
+"""Prefill GEMM (M > 16) through the device-pointer API.
+
+The kernel copies its tiles straight from global memory into a two-stage LDS
+ring and writes C through an LDS-staged epilogue; these cases cover both tile
+heights (64 rows, and 128 rows once the grid gives two workgroups per CU),
+ragged M / N edges (the scalar store tail when rows are not 16-byte
+multiples), short and long k-loops, and three-term (f32) activations with
+int8 weights. The reference is float64 over the same bf16 / int8 operands:
+every product is exact in f32, only the summation order differs, so the
+bound is the 1e-4 x RMS contract of gemm_nt_bf16 / gemm_nt_int8
+(ops/src/kernels.rs:1199-1287).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def bf16_bits(x):
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_value(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_close_rms(got, ref, tol=TOL):
+    ref = np.asarray(ref, np.float64)
+    err = float(np.abs(np.asarray(got, np.float64) - ref).max())
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    assert err <= tol * max(rms, 1e-30), f"max|d|={err:.3e} rms={rms:.3e}"
+
+
+class Device:
+    def __init__(self, lib):
+        self.lib, self.ptrs = lib, []
+
+    def check(self, rc):
+        assert rc == 0, self.lib.vmlm_hip_last_error().decode()
+
+    def up(self, a):
+        a = np.ascontiguousarray(a)
+        p = C.c_void_p()
+        self.check(self.lib.vmlm_hip_malloc(C.byref(p), a.nbytes))
+        self.check(self.lib.vmlm_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes))
+        self.ptrs.append(p)
+        return p
+
+    def empty(self, nbytes):
+        p = C.c_void_p()
+        self.check(self.lib.vmlm_hip_malloc(C.byref(p), nbytes))
+        self.ptrs.append(p)
+        return p
+
+    def down(self, p, shape, dtype):
+        out = np.empty(shape, dtype)
+        self.check(self.lib.vmlm_hip_sync())
+        self.check(self.lib.vmlm_hip_memcpy_d2h(out.ctypes.data, p, out.nbytes))
+        return out
+
+    def free(self):
+        for p in self.ptrs:
+            self.lib.vmlm_hip_free(p)
+
+
+@pytest.fixture
+def dev(hip):
+    d = Device(hip)
+    yield d
+    d.free()
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 2048, 512),   # config 1
+                                   (2048, 4096, 128),   # 128-row tiles
+                                   (130, 201, 192),     # ragged, odd row stride
+                                   (17, 128, 64)])      # one k-step, one spare row
+def test_gemm_bf16_bf16(dev, m, n, k):
+    rng = np.random.default_rng(m * 3 + n + k)
+    a = bf16_bits(rng.standard_normal((m, k), dtype=np.float32))
+    b = bf16_bits(rng.standard_normal((n, k), dtype=np.float32) / np.float32(np.sqrt(k)))
+    da, db, dc = dev.up(a), dev.up(b), dev.empty(m * n * 4)
+    dev.check(dev.lib.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, m, n, k, None))
+    got = dev.down(dc, (m, n), np.float32)
+    ref = bf16_value(a).astype(np.float64) @ bf16_value(b).astype(np.float64).T
+    assert_close_rms(got, ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 2304, 5760),   # down projection, 90 k-steps
+                                   (2048, 384, 256)])   # many row tiles
+def test_gemm_int8_three_terms(dev, oracle, m, n, k):
+    rng = np.random.default_rng(m + n * 5 + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
+    da, dq, ds, dc = dev.up(a), dev.up(q), dev.up(s), dev.empty(m * n * 4)
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, dc, m, n, k, None))
+    got = dev.down(dc, (m, n), np.float32)
+    ref = (a.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    assert_close_rms(got, ref)
+    assert_close_rms(got, oracle.gemm_nt_int8(a, q, s))
