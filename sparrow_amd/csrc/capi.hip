@@ -224,6 +224,40 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         Wd = wp;
     }
     const int T = 3;
+    // int8 weights, a few rows: the wide k-split GEMV splits the f32 rows
+    // into terms while staging them, then the slices are reduced in order
+    const size_t nch = Kp / 128;
+    const int nc = nch % 2 == 0 ? 2 : nch % 3 == 0 ? 3 : 1;
+    if (wi8 && m <= 16 && Wd == W && k % 4 == 0 && ((uintptr_t)a & 15) == 0 &&
+        nch / nc <= 16) {
+        const int ks = (int)(nch / nc);
+        float *part = ks > 1 ? stg.alloc<float>((size_t)ks * m * n) : nullptr;
+        STAGE_OK(stg);
+        GemvArgs g;
+        g.W = Wd;
+        g.w_int8 = true;
+        g.scale = scale;
+        g.X = a;
+        g.ldx = (int)k;
+        g.T = T;
+        g.lda = (int)Kp;
+        g.M = (int)m;
+        g.N = (int)n;
+        g.K = (int)Kp;
+        g.tiles = 8;
+        g.ksplit = ks;
+        if (ks == 1) {
+            g.Y = c;
+            g.ldy = (int)n;
+            return launch_gemv(g, st);
+        }
+        g.Y = part;
+        g.ldy = (int)n;
+        g.epi = EPI_PARTIAL;
+        int rc = launch_gemv(g, st);
+        if (rc) return rc;
+        return launch_gemv_reduce(part, ks, (int)m, (int)n, scale, c, (int)n, st);
+    }
     uint16_t *terms = stg.alloc<uint16_t>((size_t)T * m * Kp);
     STAGE_OK(stg);
     int rc = launch_split_terms(a, k, (int)m, (int)k, T, terms, (int)Kp, st);

@@ -57,8 +57,13 @@ struct GemvArgs {
     unsigned long long *keys = nullptr; // EPI_ARGMAX: [M], zeroed before the launch
     int tiles = 0; // 16-row tiles per workgroup (1, 2, 4; SiLU: 2, 4); 0 = chosen by shape
     int ksplit = 1; // k-slices (workgroup rows) for EPI_PARTIAL
+    const float *X = nullptr; // tiles == 8: f32 activation rows [M][ldx] instead of A
+    int ldx = 0;
 };
 int launch_gemv(const GemvArgs &a, hipStream_t st);
+// C = (in-order sum of ks k-slice partials [ks][M][N]) * scale (per column, or none).
+int launch_gemv_reduce(const float *part, int ks, int M, int N, const float *scale, float *C,
+                       int ldc, hipStream_t st);
 
 // Tiled MFMA GEMM for M > 16: C[M,N] = A[M,K] . W[N,K]^T (* scale[n]).
 struct GemmArgs {

@@ -37,6 +37,8 @@ struct GemvParams {
     unsigned long long *keys;
     size_t tstride;
     int lda, M, N, K, ldy, ldr, ldaout, Tout, epi, ks;
+    const float *X;  // wide kernel: f32 activation rows [M][ldx], split while staged
+    int ldx;
 };
 
 __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
 // flight together (one memory round trip); the workgroup's k-slice sums go
 // out raw (EPI_PARTIAL, reduced in a fixed order by the consumer) or, with a
 // single slice, through the usual epilogues.
-template <int T, bool BT, int NC, int NWV>
+template <int T, bool BT, int NC, int NWV, bool XF32>
 __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
     constexpr int NTH = NWV * 64;
     constexpr int TA = BT ? 1 : T;
@@ -311,25 +313,61 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
         }
     }
     // the activation slice [TA][16 rows][KW] -> LDS in 16-byte pieces; rows
-    // past the live ones repeat row 0 (their outputs are never read)
+    // past the live ones repeat row 0 (their outputs are never read). From
+    // f32 rows (p.X) each thread splits 8 values into the T terms.
     const int arows = BT ? T * p.M : p.M;
-    constexpr int PIECES = TA * 16 * (KW / 8);
-    constexpr int PER = (PIECES + NTH - 1) / NTH;
-    u32x4 ap[PER];
+    if constexpr (XF32) {
+        constexpr int UNITS = 16 * (KW / 8);
+        constexpr int UPER = (UNITS + NTH - 1) / NTH;
+        float4 xv[UPER][2];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        int e = tid + i * NTH;
-        e = e < PIECES ? e : PIECES - 1;
-        const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
-        const int rs = r < arows ? r : 0;
-        ap[i] = ldg16_cached(p.A + (BT ? 0 : tt * p.tstride) + (size_t)rs * p.lda + k0 + c8 * 8);
-    }
+        for (int i = 0; i < UPER; ++i) {
+            int e = tid + i * NTH;
+            e = e < UNITS ? e : UNITS - 1;
+            const int r = e / (KW / 8), c8 = e % (KW / 8);
+            const float *xr = p.X + (size_t)(r < p.M ? r : 0) * p.ldx + k0 + c8 * 8;
+            xv[i][0] = *(const float4 *)xr;
+            xv[i][1] = *(const float4 *)(xr + 4);
+        }
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        int e = tid + i * NTH;
-        e = e < PIECES ? e : PIECES - 1;
-        const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
-        *(u32x4 *)&as[tt][r][c8 * 8] = ap[i];
+        for (int i = 0; i < UPER; ++i) {
+            const int e = tid + i * NTH;
+            const int r = e / (KW / 8), c8 = e % (KW / 8);
+            float y[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                          xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) {
+                uint32_t hb[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    hb[q] = bf16_rne_bits(y[q]);
+                    y[q] = y[q] - bf16_bits_to_f32(hb[q]);
+                }
+                const u32x4 pk = u32x4{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16),
+                                       hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16)};
+                if (e < UNITS && (!BT || r < p.M))
+                    *(u32x4 *)&as[BT ? 0 : tt][BT ? tt * p.M + r : r][c8 * 8] = pk;
+            }
+        }
+    } else {
+        constexpr int PIECES = TA * 16 * (KW / 8);
+        constexpr int PER = (PIECES + NTH - 1) / NTH;
+        u32x4 ap[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int e = tid + i * NTH;
+            e = e < PIECES ? e : PIECES - 1;
+            const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+            const int rs = r < arows ? r : 0;
+            ap[i] = ldg16_cached(p.A + (BT ? 0 : tt * p.tstride) + (size_t)rs * p.lda + k0 + c8 * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int e = tid + i * NTH;
+            e = e < PIECES ? e : PIECES - 1;
+            const int tt = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+            *(u32x4 *)&as[tt][r][c8 * 8] = ap[i];
+        }
     }
     __syncthreads();
 
@@ -595,11 +633,20 @@ static int wide_slots() {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, (const void *)gemv_wide_kernel<T, BT, NC, NWV>, NWV * 64, 0) != hipSuccess)
+                &per_cu, (const void *)gemv_wide_kernel<T, BT, NC, NWV, false>, NWV * 64, 0) !=
+                hipSuccess)
             return 0;
         slots = per_cu * cus;
     }
     return slots;
+}
+
+template <int T, bool BT, int NC, bool XF32>
+static void launch_wide_x(const GemvParams &p, bool wide16, hipStream_t st) {
+    if (wide16)
+        gemv_wide_kernel<T, BT, NC, 16, XF32><<<dim3(p.N / 256, p.ks), 1024, 0, st>>>(p);
+    else
+        gemv_wide_kernel<T, BT, NC, 8, XF32><<<dim3((p.N + 127) / 128, p.ks), 512, 0, st>>>(p);
 }
 
 // 8 waves (128 rows) per workgroup while the grid fits on the device in one
@@ -608,11 +655,11 @@ static int wide_slots() {
 template <int T, bool BT, int NC>
 static int launch_wide_nc(const GemvParams &p, hipStream_t st) {
     const int wgs8 = (p.N + 127) / 128 * p.ks;
-    if (p.N % 256 == 0 && wgs8 > wide_slots<T, BT, NC, 8>()) {
-        gemv_wide_kernel<T, BT, NC, 16><<<dim3(p.N / 256, p.ks), 1024, 0, st>>>(p);
-    } else {
-        gemv_wide_kernel<T, BT, NC, 8><<<dim3((p.N + 127) / 128, p.ks), 512, 0, st>>>(p);
-    }
+    const bool wide16 = p.N % 256 == 0 && wgs8 > wide_slots<T, BT, NC, 8>();
+    if (p.X)
+        launch_wide_x<T, BT, NC, true>(p, wide16, st);
+    else
+        launch_wide_x<T, BT, NC, false>(p, wide16, st);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -673,6 +720,39 @@ static int launch_r(const GemvParams &p, int T, bool bt, hipStream_t st) {
     }
 }
 
+// C[b][j] = (sum over the ks k-slices of part[s][b][j], in slice order) * scale[j];
+// every slice of an output is loaded up front (index clamped).
+constexpr int RED_KS_MAX = 16;
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float *__restrict__ part, int ks,
+                                                          int M, int N,
+                                                          const float *__restrict__ scale,
+                                                          float *__restrict__ C, int ldc) {
+    const int n = M * N;
+    int i = blockIdx.x * 256 + threadIdx.x;
+    const bool live = i < n;
+    i = live ? i : n - 1;
+    float v[RED_KS_MAX];
+#pragma unroll
+    for (int s = 0; s < RED_KS_MAX; ++s) v[s] = part[(size_t)(s < ks ? s : ks - 1) * n + i];
+    float acc = v[0];
+#pragma unroll
+    for (int s = 1; s < RED_KS_MAX; ++s)
+        if (s < ks) acc += v[s];
+    if (!live) return;
+    const int b = i / N, j = i % N;
+    C[(size_t)b * ldc + j] = scale ? acc * scale[j] : acc;
+}
+
+int launch_gemv_reduce(const float *part, int ks, int M, int N, const float *scale, float *C,
+                       int ldc, hipStream_t st) {
+    VMLM_GUARD(ks >= 1 && ks <= RED_KS_MAX && M >= 1 && N >= 1,
+               "gemv reduce: 1 <= ks <= %d k-slices", RED_KS_MAX);
+    const size_t n = (size_t)M * N;
+    gemv_reduce_kernel<<<cdiv(n, 256), 256, 0, st>>>(part, ks, M, N, scale, C, ldc);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.M <= 16, "gemv: M=%d outside 1..16", a.M);
     VMLM_GUARD(a.K > 0 && a.K % (a.w_int8 ? 128 : 64) == 0,
@@ -680,6 +760,8 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     VMLM_GUARD(a.N > 0, "gemv: N=%d", a.N);
     VMLM_GUARD(((uintptr_t)a.W & 15) == 0 && ((uintptr_t)a.A & 15) == 0 && a.lda % 64 == 0,
                "gemv: operands must be 16-byte aligned with lda %% 64 == 0");
+    VMLM_GUARD(!a.X || (a.tiles == 8 && ((uintptr_t)a.X & 15) == 0 && a.ldx % 4 == 0),
+               "gemv: f32 activation rows need the wide kernel and 16-byte aligned rows");
     VMLM_GUARD(a.epi != EPI_ARGMAX || a.keys, "gemv argmax: keys buffer required");
     GemvParams p;
     p.W = (const uint8_t *)a.W;
@@ -700,6 +782,8 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     p.Tout = a.Tout;
     p.epi = a.epi;
     p.ks = a.ksplit > 0 ? a.ksplit : 1;
+    p.X = a.X;
+    p.ldx = a.ldx;
     VMLM_GUARD(p.ks == 1 || (a.epi == EPI_PARTIAL && (a.K / (a.w_int8 ? 128 : 64)) % p.ks == 0) ||
                    (a.tiles >= 8 && a.epi == EPI_PARTIAL),
                "gemv: k-split %d needs EPI_PARTIAL and whole chunks per slice", p.ks);
