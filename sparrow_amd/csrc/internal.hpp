@@ -113,10 +113,12 @@ int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float 
 // Attention (head_dim 64). Prefill takes rotated K, and Q rotated (rope_q
 // false) or raw (rope_q: rotated on load with the step -2/64*ln_f(theta),
 // row positions pos0 + row).
+// nseq sequences (one launch, grid z) at strides sin (q/k/v) and sout (out)
+// elements.
 int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
                              int S, int H, int ld, int ldo, float scale, bool causal,
                              hipStream_t st, bool rope_q = false, float rope_step = 0.0f,
-                             float pos0 = 0.0f);
+                             float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0);
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;

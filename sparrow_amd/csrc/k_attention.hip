@@ -167,20 +167,30 @@ __device__ __forceinline__ void split8x3(const float (&x)[8], u32x4 &t0, u32x4 &
     }
 }
 
-__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
-    const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
-    float *__restrict__ O, int S, int ld, int ldo, float scale, int causal, int rope_q,
-    float rope_step, float pos0) {
+// One workgroup per (query block, head, sequence); sequences at strides
+// sin / sout (elements) along grid z. The longest causal rows go first.
+struct PrefillParams {
+    const float *Q, *K, *V;
+    float *O;
+    size_t sin, sout;
+    int S, ld, ldo, causal, rope_q, nqb;
+    float scale, rope_step, pos0;
+};
+
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
     __shared__ __attribute__((aligned(16))) uint16_t Ps[4][2][16][AT_LD];  // [wave][term][q][key]
-    // causal work grows with the query block: dispatch the longest first
-    const int h = blockIdx.y, qb = causal ? (int)gridDim.x - 1 - (int)blockIdx.x : blockIdx.x;
+    const int S = P.S, ld = P.ld, causal = P.causal;
+    const int h = blockIdx.y, z = blockIdx.z;
+    const int qb = causal ? P.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int kb0 = 0, kb1 = causal ? qb + 1 : (S + AT_B - 1) / AT_B;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r = lane & 15;
     const int q0 = qb * AT_B + wave * 16;
-    const float *Qh = Q + h * 64, *Kh = K + h * 64, *Vh = V + h * 64;
+    const float *Qh = P.Q + z * P.sin + h * 64, *Kh = P.K + z * P.sin + h * 64,
+                *Vh = P.V + z * P.sin + h * 64;
 
     // this lane's query fragments: row q0 + r, dims 32s + 8g .. +7, two terms;
     // the lane holds both members (i, i + 32) of its RoPE pairs, so an
@@ -196,11 +206,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
             x[sl][0] = x0.x, x[sl][1] = x0.y, x[sl][2] = x0.z, x[sl][3] = x0.w;
             x[sl][4] = x1.x, x[sl][5] = x1.y, x[sl][6] = x1.z, x[sl][7] = x1.w;
         }
-        if (rope_q) {
-            const float fpos = pos0 + (float)qr;
+        if (P.rope_q) {
+            const float fpos = P.pos0 + (float)qr;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                rope_pair(x[0][e], x[1][e], fpos, g * 8 + e, rope_step, &x[0][e], &x[1][e]);
+                rope_pair(x[0][e], x[1][e], fpos, g * 8 + e, P.rope_step, &x[0][e], &x[1][e]);
         }
         split8(x[0], aq[0][0], aq[0][1]);
         split8(x[1], aq[1][0], aq[1][1]);
@@ -213,7 +223,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         l[i] = 0.0f;
         o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const int nkb = causal ? qb + 1 : (S + AT_B - 1) / AT_B;
     // staging roles: K rows (key tid/4, dims 16*(tid%4) ..), V columns (dim
     // tid%64, keys 16*(tid/64) ..)
     const int kkey = tid >> 2, kd0 = (tid & 3) * 16;
@@ -239,8 +248,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
             vx[i] = Vh[(size_t)vr * ld + vd];
         }
     };
-    load_kv(0);
-    for (int kb = 0; kb < nkb; ++kb) {
+    load_kv(kb0);
+    for (int kb = kb0; kb < kb1; ++kb) {
         const int k0 = kb * AT_B;
         __syncthreads();  // the previous block's K / V are no longer read
 #pragma unroll
@@ -261,24 +270,31 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
             *(u32x4 *)&Vt[2][vd][vk0 + 8 * half] = t2;
         }
         __syncthreads();
-        load_kv(kb + 1 < nkb ? kb + 1 : kb);
+        load_kv(kb + 1 < kb1 ? kb + 1 : kb);
         __builtin_amdgcn_sched_barrier(0);
 
-        // scores: block j = keys 16j..16j+15; lane (g, r): queries 4g+i, key 16j+r
+        // scores: block j = keys 16j..16j+15; lane (g, r): queries 4g+i, key
+        // 16j+r. The four blocks' MFMA chains are interleaved (each block's
+        // own term order is q0k0, q0k1, q1k0, q1k1 per 32-dim slice).
         f32x4 sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int sl = 0; sl < 2; ++sl) {
-                const u32x4 b0 = *(const u32x4 *)&Ks[0][16 * j + r][sl * 32 + g * 8];
-                const u32x4 b1 = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
-                acc = mfma_b(aq[sl][0], b0, acc);
-                acc = mfma_b(aq[sl][0], b1, acc);
-                acc = mfma_b(aq[sl][1], b0, acc);
-                acc = mfma_b(aq[sl][1], b1, acc);
+        for (int sl = 0; sl < 2; ++sl) {
+            u32x4 b0[4], b1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                b0[j] = *(const u32x4 *)&Ks[0][16 * j + r][sl * 32 + g * 8];
+                b1[j] = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
             }
-            sc[j] = acc;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][0], b0[j], sc[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][0], b1[j], sc[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][1], b0[j], sc[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][1], b1[j], sc[j]);
         }
         float rmax[4];
 #pragma unroll
@@ -289,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
             for (int j = 0; j < 4; ++j) {
                 const int ka = k0 + 16 * j + r;
                 const bool valid = ka < S && (!causal || ka <= qa);
-                sc[j][i] = valid ? sc[j][i] * scale : -INFINITY;
+                sc[j][i] = valid ? sc[j][i] * P.scale : -INFINITY;
                 mx = fmaxf(mx, sc[j][i]);
             }
             rmax[i] = row16_max(mx);
@@ -324,46 +340,74 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O[q][d] += P[q][key] V[key][d]: A = P rows, B = V^T rows (dims)
+        // O[q][d] += P[q][key] V[key][d]: A = P rows, B = V^T rows (dims);
+        // the four dim blocks' chains interleaved, each in the term order
+        // p0v0, p0v1, p0v2, p1v0, p1v1
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
             const u32x4 p0 = *(const u32x4 *)&Ps[wave][0][r][sl * 32 + g * 8];
             const u32x4 p1 = *(const u32x4 *)&Ps[wave][1][r][sl * 32 + g * 8];
+            u32x4 v0[4], v1[4], v2[4];
 #pragma unroll
             for (int jd = 0; jd < 4; ++jd) {
-                const u32x4 v0 = *(const u32x4 *)&Vt[0][16 * jd + r][sl * 32 + g * 8];
-                const u32x4 v1 = *(const u32x4 *)&Vt[1][16 * jd + r][sl * 32 + g * 8];
-                const u32x4 v2 = *(const u32x4 *)&Vt[2][16 * jd + r][sl * 32 + g * 8];
-                o[jd] = mfma_b(p0, v0, o[jd]);
-                o[jd] = mfma_b(p0, v1, o[jd]);
-                o[jd] = mfma_b(p0, v2, o[jd]);
-                o[jd] = mfma_b(p1, v0, o[jd]);
-                o[jd] = mfma_b(p1, v1, o[jd]);
+                v0[jd] = *(const u32x4 *)&Vt[0][16 * jd + r][sl * 32 + g * 8];
+                v1[jd] = *(const u32x4 *)&Vt[1][16 * jd + r][sl * 32 + g * 8];
+                v2[jd] = *(const u32x4 *)&Vt[2][16 * jd + r][sl * 32 + g * 8];
             }
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v0[jd], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v1[jd], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v2[jd], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p1, v0[jd], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p1, v1[jd], o[jd]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     // lane (g, r) of block jd: queries 4g+i, dim 16jd + r
+    float *Oz = P.O + z * P.sout;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int qa = q0 + 4 * g + i;
         if (qa >= S) continue;
         const float inv = 1.0f / l[i];
 #pragma unroll
-        for (int jd = 0; jd < 4; ++jd) O[(size_t)qa * ldo + h * 64 + 16 * jd + r] = o[jd][i] * inv;
+        for (int jd = 0; jd < 4; ++jd)
+            Oz[(size_t)qa * P.ldo + h * 64 + 16 * jd + r] = o[jd][i] * inv;
     }
 }
 
 int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
                              int S, int H, int ld, int ldo, float scale, bool causal,
-                             hipStream_t st, bool rope_q, float rope_step, float pos0) {
-    VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)krot & 15) == 0,
+                             hipStream_t st, bool rope_q, float rope_step, float pos0, int nseq,
+                             size_t sin, size_t sout) {
+    VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)krot & 15) == 0 &&
+                   (nseq == 1 || sin % 4 == 0),
                "attention prefill: 16-byte aligned rows required");
-    dim3 grid(cdiv(S, AT_B), H);
-    attn_prefill_kernel<<<grid, 256, 0, st>>>(q, krot, v, out, S, ld, ldo, scale,
-                                              causal ? 1 : 0, rope_q ? 1 : 0, rope_step, pos0);
+    VMLM_GUARD(nseq >= 1 && nseq <= 65535 && H <= 65535, "attention prefill: grid too large");
+    if (S <= 0) return VMLM_OK;
+    PrefillParams P;
+    P.Q = q;
+    P.K = krot;
+    P.V = v;
+    P.O = out;
+    P.sin = sin;
+    P.sout = sout;
+    P.S = S;
+    P.ld = ld;
+    P.ldo = ldo;
+    P.causal = causal ? 1 : 0;
+    P.rope_q = rope_q ? 1 : 0;
+    P.nqb = cdiv(S, AT_B);
+    P.scale = scale;
+    P.rope_step = rope_step;
+    P.pos0 = pos0;
+    attn_prefill_kernel<<<dim3(P.nqb, H, nseq), 256, 0, st>>>(P);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

@@ -469,13 +469,10 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
                                                            (int)S, d->Kc(l), d->Vc(l),
                                                            (int)d->cap, (int)B);
             VMLM_HIP_CHECK(hipGetLastError());
-            for (size_t b = 0; b < B; ++b) {
-                const float *base = qkv + b * S * 3 * H;
-                if ((r = launch_attention_prefill(base, base + H, base + 2 * H, att + b * S * H,
-                                                  (int)S, (int)NH, (int)(3 * H), (int)H,
-                                                  d->c.attn_scale, true, st)))
-                    return r;
-            }
+            if ((r = launch_attention_prefill(qkv, qkv + H, qkv + 2 * H, att, (int)S, (int)NH,
+                                              (int)(3 * H), (int)H, d->c.attn_scale, true, st,
+                                              false, 0.0f, 0.0f, (int)B, S * 3 * H, S * H)))
+                return r;
             if ((r = launch_split_terms(att, H, (int)M, (int)H, T, terms, (int)H, st))) return r;
             GemmArgs go = g;
             go.W = d->Wo(l);
