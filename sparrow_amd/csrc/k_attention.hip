@@ -502,6 +502,20 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
             vv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
         }
     };
+    // a wave's next chunk: its keys as soon as the scores are out of kv, its
+    // values once the weighted sum is out of vv (chunks past the last read as 0)
+    auto load_k = [&](int c) {
+#pragma unroll
+        for (int it = 0; it < 16; ++it)
+            kv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    krs, (c * 64 + it * 4 + grp) * 256 + 16 * q, 0, 0));
+    };
+    auto load_v = [&](int c) {
+#pragma unroll
+        for (int it = 0; it < 16; ++it)
+            vv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    vrs, (c * 64 + it * 4 + grp) * 256 + 16 * q, 0, 0));
+    };
     // the new q/k/v values first (every lane, unconditionally), then the
     // chunk rows; the scheduling barriers keep that issue order so the
     // rotation below waits only for the former
@@ -563,8 +577,11 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     const float4 kq = make_float4(kn[4 * q], kn[4 * q + 1], kn[4 * q + 2], kn[4 * q + 3]);
     const float4 vq = make_float4(vn[4 * q], vn[4 * q + 1], vn[4 * q + 2], vn[4 * q + 3]);
 
+    // 8 waves (few workgroups, long rows per wave): a wave's next chunk is
+    // loaded while the current one is consumed; 4 waves: loaded at the top
+    constexpr bool PIPE = AD_NW == 8;
     for (int c = wave; c < nch; c += AD_NW) {
-        if (c != wave) load_chunk(c);
+        if (!PIPE && c != wave) load_chunk(c);
         const int p0 = c * 64;
         // partial dots (4 dims per lane), then a transposing butterfly over
         // the 16 lanes of a group: lane (grp, q) ends with position
@@ -583,6 +600,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
         bfly_stage<8, DPP_ROW_HALF_MIRROR>(d, (q & 4) != 0);
         bfly_stage<4, DPP_QUAD_REV>(d, (q & 2) != 0);
         bfly_stage<2, DPP_QUAD_SWAP>(d, (q & 1) != 0);
+        if constexpr (PIPE) load_k(c + AD_NW);
         const float sc = p0 + 4 * q + grp <= pos ? d[0] * a.scale : -INFINITY;
         const float mc = rows_to_uniform_max(sc);  // chunk c holds position p0 <= pos: finite
         const float e = sc == -INFINITY ? 0.0f : exp_f(sc - mc);
@@ -601,6 +619,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
             o.z = __builtin_fmaf(w, v4.z, o.z);
             o.w = __builtin_fmaf(w, v4.w, o.w);
         }
+        if constexpr (PIPE) load_v(c + AD_NW);
 #pragma unroll
         for (int off = 16; off < 64; off <<= 1) {
             o.x += __shfl_xor(o.x, off, 64);
@@ -619,12 +638,16 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     __syncthreads();
-    if (tid >= 64) return;
+    // each chunk's weight e^{m_c - M} once (into the chunk's spare slot),
+    // then every output dim sums over the chunks in order
     float M = cpart[0];
     for (int c = 1; c < nch; ++c) M = fmaxf(M, cpart[c * AD_PART]);
+    for (int c = tid; c < nch; c += AD_NW * 64) cpart[c * AD_PART + 2] = exp_f(cpart[c * AD_PART] - M);
+    __syncthreads();
+    if (tid >= 64) return;
     float L = 0.0f, O = 0.0f;
     for (int c = 0; c < nch; ++c) {
-        const float f = exp_f(cpart[c * AD_PART] - M);
+        const float f = cpart[c * AD_PART + 2];
         L = __builtin_fmaf(cpart[c * AD_PART + 1], f, L);
         O = __builtin_fmaf(cpart[c * AD_PART + 4 + tid], f, O);
     }
