@@ -139,6 +139,11 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
 // B1 gather forward over source-major activations.
 int launch_b1_forward(const float *w, const uint32_t *src, int n, int k0, const float *xt,
                       size_t t8, int n_tokens, float *yt, int mode, int act, hipStream_t st);
+// T8 layer over d source rows (indices clamped to d - 1) with the sources of
+// each 16-token block staged in LDS; other shapes take launch_b1_forward.
+int launch_b1_t8_layer(const float *w, const uint32_t *src, int n, int k0, int d,
+                       const float *xt, size_t t8, int n_tokens, float *yt, int act,
+                       hipStream_t st);
 int launch_transpose_t8(const float *x, size_t T, size_t d, float *xt, size_t t8,
                         hipStream_t st);
 int launch_transpose_back(const float *a, size_t rows, size_t cols, float *out, size_t os,

@@ -95,6 +95,104 @@ int launch_b1_forward(const float *w, const uint32_t *src, int n, int k0, const 
     return VMLM_OK;
 }
 
+// T8 layer with the sources staged in LDS: a workgroup owns 16 tokens and a
+// group of neurons. The 16-token slice of every source row (d rows, 64 bytes
+// each) is copied into LDS once, so a source row is fetched once per 16 tokens
+// and workgroup rather than once per connection; then thread (slot, token)
+// computes neurons slot, slot + 64, ... of the group with the T8 contract
+// (j ascending, first product assigned, multiply then add). Indices are
+// clamped to the staged rows.
+constexpr int B1S_TB = 16;
+constexpr int B1S_PIECES = 9;  // 16-byte staging pieces per thread: d <= 2304
+__global__ __launch_bounds__(1024) void b1_t8_staged_kernel(const float *__restrict__ w,
+                                                            const uint32_t *__restrict__ src,
+                                                            int n, int k0, int d,
+                                                            const float *__restrict__ xt,
+                                                            size_t t8, int n_tokens,
+                                                            float *__restrict__ yt, int act,
+                                                            int group) {
+    extern __shared__ float4 xs4[];  // [d][4] float4 = [d][16] floats
+    const float *xs = (const float *)xs4;
+    const int t0 = blockIdx.x * B1S_TB;
+    {
+        // every staging load of the thread goes out before any is stored;
+        // pieces past d * 4 re-read the last one and store it again (same
+        // value, same place), so neither the loads nor the stores branch
+        float4 stg[B1S_PIECES];
+        int pcs[B1S_PIECES];
+#pragma unroll
+        for (int k = 0; k < B1S_PIECES; ++k) {
+            const int pc = threadIdx.x + k * 1024;
+            pcs[k] = pc < d * 4 ? pc : d * 4 - 1;
+            stg[k] = *(const float4 *)(xt + (size_t)(pcs[k] >> 2) * t8 + t0 + (pcs[k] & 3) * 4);
+        }
+#pragma unroll
+        for (int k = 0; k < B1S_PIECES; ++k) xs4[pcs[k]] = stg[k];
+    }
+    __syncthreads();
+    const int tok = threadIdx.x & 15, slot = threadIdx.x >> 4;
+    const int t = t0 + tok;
+    const int i_end = (int)blockIdx.y * group + group < n ? (int)blockIdx.y * group + group : n;
+    for (int i = (int)blockIdx.y * group + slot; i < i_end; i += 64) {
+        const float *wi = w + (size_t)i * k0;
+        const uint32_t *si = src + (size_t)i * k0;
+        float acc = 0.0f;
+        // batches of 32 connections: indices and weights loaded together
+        // (clamped past k0), then the in-order sum; a full batch has no branch
+        for (int j0 = 0; j0 < k0; j0 += 32) {
+            uint32_t sv[32];
+            float wv[32];
+#pragma unroll
+            for (int jj = 0; jj < 32; ++jj) {
+                const int j = j0 + jj < k0 ? j0 + jj : k0 - 1;
+                sv[jj] = si[j];
+                wv[jj] = wi[j];
+            }
+            if (j0 + 32 <= k0) {
+#pragma unroll
+                for (int jj = 0; jj < 32; ++jj) {
+                    const uint32_t srow = sv[jj] < (uint32_t)d ? sv[jj] : (uint32_t)(d - 1);
+                    const float p = wv[jj] * xs[srow * B1S_TB + tok];
+                    acc = j0 + jj == 0 ? p : acc + p;
+                }
+            } else {
+                for (int jj = 0; j0 + jj < k0; ++jj) {
+                    const uint32_t srow = sv[jj] < (uint32_t)d ? sv[jj] : (uint32_t)(d - 1);
+                    const float p = wv[jj] * xs[srow * B1S_TB + tok];
+                    acc = j0 + jj == 0 ? p : acc + p;
+                }
+            }
+        }
+        if (act >= 0) acc = act_scalar(acc, act);
+        if (t < n_tokens) yt[(size_t)i * t8 + t] = acc;
+    }
+}
+
+int launch_b1_t8_layer(const float *w, const uint32_t *src, int n, int k0, int d,
+                       const float *xt, size_t t8, int n_tokens, float *yt, int act,
+                       hipStream_t st) {
+    const size_t lds = (size_t)d * B1S_TB * sizeof(float);
+    if (n == 0 || n_tokens == 0) return VMLM_OK;
+    if (k0 == 0 || d == 0 || d * 4 > B1S_PIECES * 1024 || t8 % B1S_TB)
+        return launch_b1_forward(w, src, n, k0, xt, t8, n_tokens, yt, B1_T8, act, st);
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    // about one workgroup per CU: token blocks x neuron groups
+    const int ntb = (int)((size_t)(n_tokens + B1S_TB - 1) / B1S_TB);
+    int groups = cus / ntb;
+    groups = groups < 1 ? 1 : groups > (n + 63) / 64 ? (n + 63) / 64 : groups;
+    const int group = (n + groups - 1) / groups;
+    b1_t8_staged_kernel<<<dim3(ntb, (n + group - 1) / group), 1024, lds, st>>>(
+        w, src, n, k0, d, xt, t8, n_tokens, yt, act, group);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 // xt[s*t8 + t] = x[t*d + s] for t < T, 0 for T <= t < t8 (32x32 LDS tiles).
 __global__ __launch_bounds__(256) void transpose_t8_kernel(const float *__restrict__ x, int T,
                                                            int d, float *__restrict__ xt,

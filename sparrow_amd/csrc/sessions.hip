@@ -659,8 +659,8 @@ int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers, c
     rc = launch_transpose_t8(x, n_tokens, d, a, t8, st);
     const int actk = act == 0xFFFF ? -1 : (int)act;
     for (uint32_t l = 0; l < n_layers && !rc; ++l) {
-        rc = launch_b1_forward(layers[l].w, layers[l].src_u32, (int)d, (int)layers[l].k0, a, t8,
-                               (int)n_tokens, b, 0, actk, st);
+        rc = launch_b1_t8_layer(layers[l].w, layers[l].src_u32, (int)d, (int)layers[l].k0,
+                                (int)d, a, t8, (int)n_tokens, b, actk, st);
         std::swap(a, b);
     }
     if (!rc) rc = launch_transpose_back(a, d, n_tokens, y, d, t8, st);
