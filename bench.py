@@ -123,14 +123,33 @@ def _timed(L, fn, iters):
     return ms.value * 1e3 / iters, wall
 
 
-def run_suite(iters):
+def _cpu_us(fn, budget_s=0.5):
+    """Mean host time of the oracle call `fn` (reported beside the GPU figure,
+    never the product path): at least one call, more while under budget_s."""
+    t = time.perf_counter()
+    fn()
+    n, el = 1, time.perf_counter() - t
+    while el < budget_s and n < 20:
+        fn()
+        n += 1
+        el = time.perf_counter() - t
+    return round(el / n * 1e6, 1)
+
+
+def run_suite(iters, cpu=True):
     """The other BASELINE configs through the device-pointer API, inputs
     resident in HBM: per-call time and the achieved fraction of the roofline
-    that bounds each (HBM 8 TB/s, bf16 MFMA 2.5 PF, FP32 157.3 TF)."""
+    that bounds each (HBM 8 TB/s, bf16 MFMA 2.5 PF, FP32 157.3 TF). With
+    `cpu`, the oracle (C restatement of the reference kernels, OpenMP) is timed
+    on the same inputs on the host and reported as cpu_us."""
     import ctypes as C
     from sparrow_amd import check, conn, lib
     L = lib()
     ptrs = []
+    orc = None
+    if cpu:
+        from oracle import oracle as orc
+        orc.lib()
 
     def up(a):
         a = np.ascontiguousarray(a)
@@ -165,6 +184,9 @@ def run_suite(iters):
         gbs = nbytes / us / 1e3
         cfg0[f"M{m}"] = {"us": round(us, 2), "host_us": round(wall, 2), "bytes": nbytes,
                          "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    if orc:
+        cfg0["cpu_us_M16"] = _cpu_us(lambda: orc.gemm_nt_int8(x, q, sc))
+        cfg0["cpu_threads"] = orc.get_threads()
     out["cfg0_q8_gemm"] = cfg0
     # config 1: bf16 A[1024,512] . B[512,2048] (B passed as its [2048,512] transpose)
     rng = np.random.default_rng(1)
@@ -176,10 +198,14 @@ def run_suite(iters):
     tf = 2147483648 / us / 1e6
     out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2),
                              "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    if orc:
+        af = orc.bf16_to_f32(a)
+        out["cfg1_bf16_gemm"]["cpu_us"] = _cpu_us(lambda: orc.gemm_nt_bf16(af, bt))
     # config 2: causal attention prefill [512, 36, 64] and one decode token vs 1024 positions
     rng = np.random.default_rng(2)
     S, H = 512, 36
-    qkv = [up(rng.standard_normal((S, H * 64), dtype=np.float32)) for _ in range(3)]
+    qkv_h = [rng.standard_normal((S, H * 64), dtype=np.float32) for _ in range(3)]
+    qkv = [up(t) for t in qkv_h]
     do = zeros(S * H * 64 * 4)
     us, wall = _timed(L, lambda: L.vmlm_hip_attention_prefill(qkv[0], qkv[1], qkv[2], do, S, H, 64,
                                                              C.c_float(10000.0), 0,
@@ -200,6 +226,10 @@ def run_suite(iters):
                     "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)},
         "decode": {"us": round(usd, 2), "host_us": round(walld, 2), "GBps": round(gbs, 1),
                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}}
+    if orc:
+        out["cfg2_attention"]["prefill"]["cpu_us"] = _cpu_us(
+            lambda: orc.attention_prefill(qkv_h[0], qkv_h[1], qkv_h[2], H, 10000.0, 0, 0.125,
+                                          True))
     # config 4: B1 stack, 8 layers, d = 1536, k0 = 32, 1024 tokens, tanh
     rng = np.random.default_rng(4)
     d, k0, T = 1536, 32, 1024
@@ -218,11 +248,96 @@ def run_suite(iters):
                             "us_per_layer": round(us / 8, 2), "GBps_unique": round(gbs, 1),
                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                             "note": "includes the two transposes of the stack"}
+    if orc:  # one layer of the stack on the host (the t8 contract), per layer
+        w0, s0 = conn.make_block_aligned(np.random.default_rng(4), d, k0)
+        xt_h = orc.transpose_t8(np.random.default_rng(5).standard_normal((T, d), dtype=np.float32),
+                                T)
+        out["cfg4_b1_stack"]["cpu_us_per_layer"] = _cpu_us(
+            lambda: orc.b1_forward_t8(w0, s0, xt_h, T))
+    out["ops"] = run_ops(L, up, zeros, iters, orc)
     for l in layers:
         l.free()
     for p in ptrs:
         L.vmlm_hip_free(p)
     return out
+
+
+def run_ops(L, up, zeros, iters, orc):
+    """The per-op kernels of the VM path (RMSNorm, softmax, RoPE, activation,
+    elementwise, scale, EMB, TOPK_IDX, f32 GEMM NT / NN) through the device
+    API at decoder-sized shapes: time per call, algorithmic bytes (or flops)
+    and the fraction of the roofline that bounds each; the oracle on the same
+    inputs beside it."""
+    import ctypes as C
+    rng = np.random.default_rng(7)
+    ops = {}
+
+    def rec(name, us, wall, nbytes=None, flops=None, cpu=None):
+        e = {"us": round(us, 2), "host_us": round(wall, 2)}
+        if nbytes is not None:
+            gbs = nbytes / us / 1e3
+            e.update({"bytes": int(nbytes), "GBps": round(gbs, 1),
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        if flops is not None:
+            tf = flops / us / 1e6
+            e.update({"flops": int(flops), "TFLOPs": round(tf, 2),
+                      "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)})
+        if cpu is not None:
+            e["cpu_us"] = cpu
+        ops[name] = e
+
+    R, Hd = 2048, 2304  # prefill activations: 16 sequences x 128 tokens
+    x = rng.standard_normal((R, Hd), dtype=np.float32)
+    y = rng.standard_normal((R, Hd), dtype=np.float32)
+    g = rng.standard_normal(Hd, dtype=np.float32)
+    dx, dy, dg, dd = up(x), up(y), up(g), zeros(x.nbytes)
+    us, wall = _timed(L, lambda: L.vmlm_hip_rmsnorm(dd, dx, dg, R, Hd, C.c_float(1e-5), None), iters)
+    rec("rmsnorm_2048x2304", us, wall, nbytes=2 * x.nbytes + g.nbytes,
+        cpu=_cpu_us(lambda: orc.rmsnorm(x, g, 1e-5)) if orc else None)
+    EWADD, SILU = 20, 2  # VMLM_OP_EWADD, VMLM_ACT_SILU
+    us, wall = _timed(L, lambda: L.vmlm_hip_ew_op(dd, dx, dy, R * Hd, EWADD, None), iters)
+    rec("ew_add_2048x2304", us, wall, nbytes=3 * x.nbytes,
+        cpu=_cpu_us(lambda: orc.ew_op(x, y, EWADD)) if orc else None)
+    us, wall = _timed(L, lambda: L.vmlm_hip_scale(dd, dx, R * Hd, C.c_float(0.125), None), iters)
+    rec("scale_2048x2304", us, wall, nbytes=2 * x.nbytes,
+        cpu=_cpu_us(lambda: orc.scale(x, 0.125)) if orc else None)
+    a = rng.standard_normal((R, 5760), dtype=np.float32)
+    da = up(a)
+    us, wall = _timed(L, lambda: L.vmlm_hip_act(da, R * 5760, SILU, None), iters)
+    rec("act_silu_2048x5760", us, wall, nbytes=2 * a.nbytes,
+        cpu=_cpu_us(lambda: orc.act(a, SILU)) if orc else None)
+    # softmax over the scores of 36 heads x 512 queries (rows of 512)
+    p = rng.standard_normal((36 * 512, 512), dtype=np.float32)
+    dp = up(p)
+    us, wall = _timed(L, lambda: L.vmlm_hip_softmax(dp, 36 * 512, 512, False, None), iters)
+    rec("softmax_18432x512", us, wall, nbytes=2 * p.nbytes,
+        cpu=_cpu_us(lambda: orc.softmax(p, False)) if orc else None)
+    # RoPE of 512 positions x 36 heads (rows of 64)
+    r = rng.standard_normal((512 * 36, 64), dtype=np.float32)
+    dr, dro = up(r), zeros(r.nbytes)
+    us, wall = _timed(L, lambda: L.vmlm_hip_rope(dro, dr, 512 * 36, 64, C.c_float(10000.0), 0,
+                                                 None), iters)
+    rec("rope_18432x64", us, wall, nbytes=2 * r.nbytes,
+        cpu=_cpu_us(lambda: orc.rope(r, 10000.0, 0)) if orc else None)
+    # TOPK_IDX over one row of LM-head logits (the op scans the first row)
+    lg = rng.standard_normal((1, 122753), dtype=np.float32)
+    dl, di = up(lg), zeros(4)
+    us, wall = _timed(L, lambda: L.vmlm_hip_topk_idx(dl, 1, 122753, di, None), iters)
+    rec("topk_idx_122753", us, wall, nbytes=lg.nbytes,
+        cpu=_cpu_us(lambda: orc.topk_idx(lg)) if orc else None)
+    # f32 GEMMs of the VM's attention composition (one head): scores Q K^T
+    # 512x512x64 (NT) and P V 512x64x512 (NN)
+    qh = rng.standard_normal((512, 64), dtype=np.float32)
+    kh = rng.standard_normal((512, 64), dtype=np.float32)
+    ph = rng.standard_normal((512, 512), dtype=np.float32)
+    dq, dk, dph, ds_, do_ = up(qh), up(kh), up(ph), zeros(512 * 512 * 4), zeros(512 * 64 * 4)
+    us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt(dq, dk, ds_, 512, 512, 64, False, None), iters)
+    rec("gemm_nt_f32_512x512x64", us, wall, flops=2 * 512 * 512 * 64,
+        cpu=_cpu_us(lambda: orc.gemm_nt(qh, kh)) if orc else None)
+    us, wall = _timed(L, lambda: L.vmlm_hip_gemm(dph, dk, do_, 512, 64, 512, False, None), iters)
+    rec("gemm_nn_f32_512x64x512", us, wall, flops=2 * 512 * 64 * 512,
+        cpu=_cpu_us(lambda: orc.gemm(ph, kh)) if orc else None)
+    return ops
 
 
 def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
@@ -327,7 +442,7 @@ def main():
 
     suite = None
     if not args.no_suite:
-        suite = run_suite(args.suite_iters)
+        suite = run_suite(args.suite_iters, cpu=not args.no_cpu)
         log(f"suite: {json.dumps(suite)}")
 
     cpu = None

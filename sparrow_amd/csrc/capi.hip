@@ -447,15 +447,23 @@ int vmlm_hip_gemm_nt_bf16bf16(const uint16_t *a, const uint16_t *b, float *c, si
     g.ldc = (int)n;
     return launch_gemm(g, as_stream(stream));
 }
+static int dev_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                        bool acc, bool nt, hipStream_t st) {
+    Stage stg(st);
+    const size_t wf = gemm_f32_work_floats(m, n, k);
+    float *work = wf ? stg.alloc<float>(wf) : nullptr;
+    STAGE_OK(stg);
+    return launch_gemm_f32(a, b, c, m, n, k, acc, nt, st, work);
+}
 int vmlm_hip_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
                      bool acc, void *stream) {
     INIT_OR_RETURN();
-    return launch_gemm_f32(a, b, c, m, n, k, acc, true, as_stream(stream));
+    return dev_gemm_f32(a, b, c, m, n, k, acc, true, as_stream(stream));
 }
 int vmlm_hip_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
                   bool acc, void *stream) {
     INIT_OR_RETURN();
-    return launch_gemm_f32(a, b, c, m, n, k, acc, false, as_stream(stream));
+    return dev_gemm_f32(a, b, c, m, n, k, acc, false, as_stream(stream));
 }
 int vmlm_hip_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
                      float eps, void *stream) {
@@ -493,7 +501,11 @@ int vmlm_hip_emb_bf16(float *dst, const uint16_t *table, size_t rows, size_t col
 int vmlm_hip_topk_idx(const float *src, size_t rows, size_t cols, float *dst, void *stream) {
     INIT_OR_RETURN();
     VMLM_GUARD(rows > 0 && cols > 0, "TOPK_IDX: src or dst slot has width 0");
-    return launch_argmax(src, 1, cols, cols, dst, nullptr, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    unsigned long long *keys = stg.alloc<unsigned long long>(1);
+    STAGE_OK(stg);
+    return launch_argmax(src, cols, dst, nullptr, keys, st);
 }
 
 static int check_conn(const vmlm_sparse_conn_w *sc) {
@@ -629,8 +641,10 @@ static int host_gemm_f32(const float *a, const float *b, float *c, size_t m, siz
         float *da = stg.upload(a, m * k);
         float *db = stg.upload(b, n * k);
         float *dc = acc ? stg.upload((const float *)c, m * n) : stg.alloc<float>(m * n);
+        const size_t wf = gemm_f32_work_floats(m, n, k);
+        float *work = wf ? stg.alloc<float>(wf) : nullptr;
         STAGE_OK(stg);
-        int rc = launch_gemm_f32(da, db, dc, m, n, k, acc, nt, st);
+        int rc = launch_gemm_f32(da, db, dc, m, n, k, acc, nt, st, work);
         if (rc) return rc;
         rc = download(c, dc, m * n * sizeof(float), st);
         if (rc) return rc;
@@ -788,8 +802,9 @@ int vmlm_topk_idx(const float *src, size_t rows, size_t cols, float *dst) {
     {
         Stage stg(st);
         float *ds = stg.upload(src, cols), *dd = stg.alloc<float>(1);
+        unsigned long long *keys = stg.alloc<unsigned long long>(1);
         STAGE_OK(stg);
-        int rc = launch_argmax(ds, 1, cols, cols, dd, nullptr, st);
+        int rc = launch_argmax(ds, cols, dd, nullptr, keys, st);
         if (!rc) rc = download(dst, dd, sizeof(float), st);
         if (rc) return rc;
     }

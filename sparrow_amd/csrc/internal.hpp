@@ -27,6 +27,7 @@ enum GemvEpi {
 // combined with 64-bit atomicMax -> the largest value, lowest index on ties
 // (the strict `>` scan of OP_TOPK_IDX). 0 = empty.
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal under `>`: one key, lowest index wins
     uint32_t u = __float_as_uint(v);
     uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)o << 32) | (0xffffffffu - idx);
@@ -82,8 +83,10 @@ struct GemmArgs {
 int launch_gemm(const GemmArgs &a, hipStream_t st);
 
 // f32 GEMMs (NT and NN) with optional accumulate.
+// work: gemm_f32_work_floats() floats (narrow outputs are split over k; null: no split).
 int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
-                    bool acc, bool b_is_nt, hipStream_t st);
+                    bool acc, bool b_is_nt, hipStream_t st, float *work = nullptr);
+size_t gemm_f32_work_floats(size_t m, size_t n, size_t k);
 
 // Row / elementwise ops.
 int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
@@ -107,8 +110,11 @@ int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld,
                 float pos0, int heads, hipStream_t st);
 int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
                     const float *rowf, const int32_t *rowi, int n, hipStream_t st);
-int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float *dst_f,
-                  int32_t *dst_i, hipStream_t st);
+// OP_TOPK_IDX over one row of cols values: index of the largest non-NaN value,
+// lowest index on ties, 0 when x[0] is NaN or every value is; keys: one
+// 64-bit device word of workspace.
+int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
+                  unsigned long long *keys, hipStream_t st);
 
 // Attention (head_dim 64). Prefill takes rotated K, and Q rotated (rope_q
 // false) or raw (rope_q: rotated on load with the step -2/64*ln_f(theta),

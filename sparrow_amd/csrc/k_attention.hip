@@ -22,73 +22,181 @@ namespace vmlm {
 
 // ---------------------------------------------------------------- f32 GEMM
 // C[m,n] (+)= A[m,k] . op(B), op(B) = B[n,k]^T (nt) or B[k,n].
+// 64x64 tiles, 256 threads of 4x4 outputs, 64-deep k-steps through LDS
+// (As[k][row], Bs[k][col]); the next step's tiles are loaded into registers
+// while the current one is consumed. With VEC the rows are read as float4
+// (k, or n for an NN B, a multiple of 4 and 16-byte aligned operands).
+// A narrow output is split over k (grid z): each slice writes its partial
+// tile to `part` [ks][m][n] and gemm_f32_reduce_kernel sums the slices in
+// order (deterministic).
+constexpr int GF_T = 64, GF_K = 64, GF_LD = 68;
+
+template <bool NT, bool VEC>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float *__restrict__ A,
                                                        const float *__restrict__ B,
-                                                       float *__restrict__ C, int m, int n,
-                                                       int k, int acc, int nt) {
-    __shared__ float As[16][68];
-    __shared__ float Bs[16][68];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
+                                                       float *__restrict__ C, int m, int n, int k,
+                                                       int acc, int kslice,
+                                                       float *__restrict__ part) {
+    __shared__ __attribute__((aligned(16))) float As[GF_K][GF_LD];
+    __shared__ __attribute__((aligned(16))) float Bs[GF_K][GF_LD];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int row0 = blockIdx.y * GF_T, col0 = blockIdx.x * GF_T;
+    const int kb = blockIdx.z * kslice;
+    const int ke = kb + kslice < k ? kb + kslice : k;
+    // loader roles: A (and an NT B) as 64 rows x 16 float4 of k; an NN B as
+    // 64 k-rows x 16 float4 of n; 4 pieces per thread
+    float4 ra[4], rb[4];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = tid + q * 256, r = e >> 4, c4 = (e & 15) * 4;
+            const int gk = k0 + c4;
+            {
+                const int gr = row0 + r;
+                const float *pa = A + (size_t)(gr < m ? gr : 0) * k + gk;
+                if constexpr (VEC) {
+                    ra[q] = gr < m && gk < ke ? *(const float4 *)pa : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    ra[q].x = gr < m && gk < ke ? pa[0] : 0.f;
+                    ra[q].y = gr < m && gk + 1 < ke ? pa[1] : 0.f;
+                    ra[q].z = gr < m && gk + 2 < ke ? pa[2] : 0.f;
+                    ra[q].w = gr < m && gk + 3 < ke ? pa[3] : 0.f;
+                }
+            }
+            if constexpr (NT) {
+                const int gc = col0 + r;
+                const float *pb = B + (size_t)(gc < n ? gc : 0) * k + gk;
+                if constexpr (VEC) {
+                    rb[q] = gc < n && gk < ke ? *(const float4 *)pb : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    rb[q].x = gc < n && gk < ke ? pb[0] : 0.f;
+                    rb[q].y = gc < n && gk + 1 < ke ? pb[1] : 0.f;
+                    rb[q].z = gc < n && gk + 2 < ke ? pb[2] : 0.f;
+                    rb[q].w = gc < n && gk + 3 < ke ? pb[3] : 0.f;
+                }
+            } else {
+                const int gkr = k0 + r, gc = col0 + c4;
+                const float *pb = B + (size_t)(gkr < ke ? gkr : kb) * n + gc;
+                if constexpr (VEC) {
+                    rb[q] = gkr < ke && gc < n ? *(const float4 *)pb : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    rb[q].x = gkr < ke && gc < n ? pb[0] : 0.f;
+                    rb[q].y = gkr < ke && gc + 1 < n ? pb[1] : 0.f;
+                    rb[q].z = gkr < ke && gc + 2 < n ? pb[2] : 0.f;
+                    rb[q].w = gkr < ke && gc + 3 < n ? pb[3] : 0.f;
+                }
+            }
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = tid + q * 256, r = e >> 4, c4 = (e & 15) * 4;
+            As[c4][r] = ra[q].x;
+            As[c4 + 1][r] = ra[q].y;
+            As[c4 + 2][r] = ra[q].z;
+            As[c4 + 3][r] = ra[q].w;
+            if constexpr (NT) {
+                Bs[c4][r] = rb[q].x;
+                Bs[c4 + 1][r] = rb[q].y;
+                Bs[c4 + 2][r] = rb[q].z;
+                Bs[c4 + 3][r] = rb[q].w;
+            } else {
+                *(float4 *)&Bs[r][c4] = rb[q];
+            }
+        }
+    };
     float c[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) c[i][j] = 0.0f;
-    for (int k0 = 0; k0 < k; k0 += 16) {
-        for (int e = threadIdx.x; e < 1024; e += 256) {
-            int r = e >> 4, kk = e & 15;
-            int gr = row0 + r, gk = k0 + kk;
-            As[kk][r] = (gr < m && gk < k) ? A[(size_t)gr * k + gk] : 0.0f;
-            if (nt) {
-                int gc = col0 + r;
-                Bs[kk][r] = (gc < n && gk < k) ? B[(size_t)gc * k + gk] : 0.0f;
-            } else {
-                int kk2 = e >> 6, cc = e & 63;
-                int gk2 = k0 + kk2, gc = col0 + cc;
-                Bs[kk2][cc] = (gc < n && gk2 < k) ? B[(size_t)gk2 * n + gc] : 0.0f;
-            }
-        }
+    load(kb);
+    for (int k0 = kb; k0 < ke; k0 += GF_K) {
         __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+        store();
+        __syncthreads();
+        if (k0 + GF_K < ke) load(k0 + GF_K);
+#pragma unroll 16
+        for (int kk = 0; kk < GF_K; ++kk) {
+            const float4 a = *(const float4 *)&As[kk][ty * 4];
+            const float4 b = *(const float4 *)&Bs[kk][tx * 4];
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) c[i][j] = __builtin_fmaf(a[i], b[j], c[i][j]);
+                for (int j = 0; j < 4; ++j) c[i][j] = __builtin_fmaf(av[i], bv[j], c[i][j]);
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        int gr = row0 + ty * 4 + i;
+        const int gr = row0 + ty * 4 + i;
         if (gr >= m) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            int gc = col0 + tx * 4 + j;
+            const int gc = col0 + tx * 4 + j;
             if (gc >= n) continue;
-            float *o = C + (size_t)gr * n + gc;
-            *o = acc ? *o + c[i][j] : c[i][j];
+            if (part) {
+                part[((size_t)blockIdx.z * m + gr) * n + gc] = c[i][j];
+            } else {
+                float *o = C + (size_t)gr * n + gc;
+                *o = acc ? *o + c[i][j] : c[i][j];
+            }
         }
     }
 }
 
+__global__ __launch_bounds__(256) void gemm_f32_reduce_kernel(const float *__restrict__ part,
+                                                              int ks, size_t mn,
+                                                              float *__restrict__ C, int acc) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float v = part[i];
+    for (int z = 1; z < ks; ++z) v += part[(size_t)z * mn + i];
+    C[i] = acc ? C[i] + v : v;
+}
+
+size_t gemm_f32_work_floats(size_t m, size_t n, size_t k) {
+    const size_t tiles = cdiv(m, (size_t)GF_T) * cdiv(n, (size_t)GF_T);
+    if (tiles >= 128 || k < 2 * GF_K) return 0;
+    size_t ks = cdiv((size_t)256, tiles);
+    const size_t steps = cdiv(k, (size_t)GF_K);
+    ks = ks < steps ? ks : steps;
+    return ks > 1 ? ks * m * n : 0;
+}
+
 int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
-                    bool acc, bool b_is_nt, hipStream_t st) {
+                    bool acc, bool b_is_nt, hipStream_t st, float *work) {
     if (m == 0 || n == 0) return VMLM_OK;
     if (k == 0) {
         if (!acc) VMLM_HIP_CHECK(hipMemsetAsync(c, 0, m * n * sizeof(float), st));
         return VMLM_OK;
     }
-    dim3 grid(cdiv(n, 64), cdiv(m, 64));
-    gemm_f32_kernel<<<grid, 256, 0, st>>>(a, b, c, (int)m, (int)n, (int)k, acc ? 1 : 0,
-                                          b_is_nt ? 1 : 0);
+    VMLM_GUARD(m <= 0x7fffffffu && n <= 0x7fffffffu && k <= 0x7fffffffu, "gemm f32: shape too large");
+    // split k when the output is narrow (and the caller gave the workspace)
+    const size_t wf = gemm_f32_work_floats(m, n, k);
+    int ks = 1;
+    if (wf && work) ks = (int)(wf / (m * n));
+    const size_t steps = cdiv(k, (size_t)GF_K);
+    const int kslice = (int)(cdiv(steps, (size_t)ks) * GF_K);
+    ks = (int)cdiv(k, (size_t)kslice);
+    const bool vec = k % 4 == 0 && (b_is_nt || n % 4 == 0) && ((uintptr_t)a & 15) == 0 &&
+                     ((uintptr_t)b & 15) == 0;
+    float *part = ks > 1 ? work : nullptr;
+    dim3 grid(cdiv(n, (size_t)GF_T), cdiv(m, (size_t)GF_T), ks);
+    const int ia = acc ? 1 : 0, ik = (int)k;
+    if (b_is_nt) {
+        if (vec) gemm_f32_kernel<true, true><<<grid, 256, 0, st>>>(a, b, c, (int)m, (int)n, ik, ia, kslice, part);
+        else gemm_f32_kernel<true, false><<<grid, 256, 0, st>>>(a, b, c, (int)m, (int)n, ik, ia, kslice, part);
+    } else {
+        if (vec) gemm_f32_kernel<false, true><<<grid, 256, 0, st>>>(a, b, c, (int)m, (int)n, ik, ia, kslice, part);
+        else gemm_f32_kernel<false, false><<<grid, 256, 0, st>>>(a, b, c, (int)m, (int)n, ik, ia, kslice, part);
+    }
     VMLM_HIP_CHECK(hipGetLastError());
+    if (part) {
+        gemm_f32_reduce_kernel<<<cdiv(m * n, (size_t)256), 256, 0, st>>>(part, ks, m * n, c, ia);
+        VMLM_HIP_CHECK(hipGetLastError());
+    }
     return VMLM_OK;
 }
 

@@ -442,46 +442,59 @@ __device__ __forceinline__ void am_merge(float &bv, int &bi, float v, int i) {
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ src, int cols,
-                                                     size_t lds, float *dst_f,
-                                                     int32_t *dst_i) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int r = blockIdx.x;
-    const float *row = src + (size_t)r * lds;
+// The row is split over many workgroups: each thread scans AM_E values
+// (loads issued together, index clamped), the wave reduces (value, index)
+// pairs with the strict-`>` / lowest-index rule, and one 64-bit atomicMax per
+// wave folds the order-preserving key into keys[0] (max is order-independent,
+// so the result is deterministic). A single-thread kernel clears the key
+// before and turns it into the index after.
+constexpr int AM_E = 8;
+
+__global__ void argmax_clear_kernel(unsigned long long *keys) { keys[0] = 0ull; }
+
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restrict__ src, int cols,
+                                                          unsigned long long *keys) {
+    const int stride = gridDim.x * 256;
+    const int i0 = blockIdx.x * 256 + threadIdx.x;
+    float v[AM_E];
+#pragma unroll
+    for (int e = 0; e < AM_E; ++e) {
+        const int i = i0 + e * stride;
+        v[e] = src[i < cols ? i : cols - 1];
+    }
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < cols; i += 256) {
-        float v = row[i];
-        if (v == v) am_merge(bv, bi, v, i);
+#pragma unroll
+    for (int e = 0; e < AM_E; ++e) {
+        const int i = i0 + e * stride;
+        if (i < cols && v[e] == v[e]) am_merge(bv, bi, v[e], i);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(bv, o, 64);
-        int oi = __shfl_xor(bi, o, 64);
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
         am_merge(bv, bi, ov, oi);
     }
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0) {
-        sv[w] = bv;
-        si[w] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        bv = sv[0];
-        bi = si[0];
-        for (int k = 1; k < 4; ++k) am_merge(bv, bi, sv[k], si[k]);
-        float x0 = row[0];
-        if (x0 != x0 || bi == 0x7fffffff) bi = 0;  // NaN at 0, or all NaN
-        if (dst_f) dst_f[r] = (float)bi;
-        if (dst_i) dst_i[r] = bi;
-    }
+    if ((threadIdx.x & 63) == 0 && bi != 0x7fffffff) atomicMax(keys, argmax_key(bv, (uint32_t)bi));
 }
 
-int launch_argmax(const float *src, size_t rows, size_t cols, size_t lds, float *dst_f,
-                  int32_t *dst_i, hipStream_t st) {
-    if (rows == 0) return VMLM_OK;
-    argmax_kernel<<<(unsigned)rows, 256, 0, st>>>(src, (int)cols, lds, dst_f, dst_i);
+__global__ void argmax_final_kernel(const float *__restrict__ src,
+                                    const unsigned long long *__restrict__ keys, float *dst_f,
+                                    int32_t *dst_i) {
+    const unsigned long long k = keys[0];
+    const float x0 = src[0];
+    const int bi = (x0 != x0 || k == 0ull) ? 0 : argmax_key_index(k);  // NaN at 0, or all NaN
+    if (dst_f) dst_f[0] = (float)bi;
+    if (dst_i) dst_i[0] = bi;
+}
+
+int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
+                  unsigned long long *keys, hipStream_t st) {
+    VMLM_GUARD(cols >= 1 && cols <= 0x7fffffffu, "TOPK_IDX: %zu values", cols);
+    const unsigned nwg = (unsigned)cdiv(cols, (size_t)256 * AM_E);
+    argmax_clear_kernel<<<1, 1, 0, st>>>(keys);
+    argmax_keys_kernel<<<nwg, 256, 0, st>>>(src, (int)cols, keys);
+    argmax_final_kernel<<<1, 1, 0, st>>>(src, keys, dst_f, dst_i);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

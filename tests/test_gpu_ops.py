@@ -75,7 +75,9 @@ def test_gemm_nt_bf16(ops, oracle, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(4, 8, 8), (1, 1, 64), (17, 23, 31), (512, 512, 64),
-                                   (16, 16, 1), (64, 64, 64)])
+                                   (16, 16, 1), (64, 64, 64),
+                                   # narrow outputs split over k (in-order slice sum)
+                                   (512, 64, 512), (64, 64, 1024), (70, 33, 300)])
 def test_gemm_nt_f32_and_nn(ops, oracle, m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = rng.standard_normal((m, k), dtype=np.float32)
@@ -160,6 +162,25 @@ def test_topk_idx_bitexact(ops, oracle):
     x = rng.standard_normal(1000, dtype=np.float32)
     x[0] = np.nan  # nothing compares > NaN: the scan keeps index 0
     assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 0.0
+
+
+def test_topk_idx_edges(ops, oracle):
+    """Cases the strict-`>` scan (core/src/interp.rs:1649-1681) fixes: -0.0
+    and +0.0 tie (lowest index), NaN after index 0 is skipped, all-NaN gives
+    0, -inf rows, and ties split across the workgroups of a long row."""
+    x = np.array([-0.0, 0.0, -1.0], np.float32)
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 0.0
+    x = np.array([-1.0, 0.0, -0.0], np.float32)
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 1.0
+    x = np.array([1.0, np.nan, 2.0, np.nan], np.float32)
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 2.0
+    x = np.full(4097, np.nan, np.float32)
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 0.0
+    x = np.full(3000, -np.inf, np.float32)
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 0.0
+    x = np.zeros(122753, np.float32)
+    x[[120000, 5000, 70001]] = 7.5  # ties in different workgroups: lowest index
+    assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 5000.0
 
 
 @pytest.mark.parametrize("k0", [1, 4, 8, 20, 32, 37])
