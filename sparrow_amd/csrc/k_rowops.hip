@@ -299,9 +299,52 @@ __global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ p, int
     for (int i = lim + threadIdx.x; i < cols; i += 256) row[i] = 0.0f;
 }
 
+// Rows of at most 64 * SM_R values: one wavefront per row (four rows per
+// workgroup), the row read once into registers (lane l holds l, l + 64, ...),
+// max and sum reduced across the wave without barriers, written once.
+constexpr int SM_R = 16;
+__global__ __launch_bounds__(256) void softmax_wave_kernel(float *__restrict__ p, int rows,
+                                                           int cols, int causal) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float *row = p + (size_t)r * cols;
+    const int lim = causal ? (r + 1 < cols ? r + 1 : cols) : cols;
+    float x[SM_R];
+#pragma unroll
+    for (int k = 0; k < SM_R; ++k) {
+        const int i = lane + 64 * k;
+        x[k] = row[i < cols ? i : cols - 1];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SM_R; ++k)
+        if (lane + 64 * k < lim) mx = fmaxf(mx, x[k]);
+    mx = wave_max(mx);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SM_R; ++k) {
+        if (lane + 64 * k < lim) {
+            x[k] = exp_f(x[k] - mx);
+            s += x[k];
+        }
+    }
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < SM_R; ++k) {
+        const int i = lane + 64 * k;
+        if (i < lim) row[i] = x[k] * inv;
+        else if (i < cols) row[i] = 0.0f;
+    }
+}
+
 int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t st) {
     if (rows == 0 || cols == 0) return VMLM_OK;
-    softmax_kernel<<<(unsigned)rows, 256, 0, st>>>(p, (int)cols, causal ? 1 : 0);
+    if (cols <= 64 * SM_R)
+        softmax_wave_kernel<<<(unsigned)cdiv(rows, (size_t)4), 256, 0, st>>>(
+            p, (int)rows, (int)cols, causal ? 1 : 0);
+    else
+        softmax_kernel<<<(unsigned)rows, 256, 0, st>>>(p, (int)cols, causal ? 1 : 0);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

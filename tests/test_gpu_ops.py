@@ -104,6 +104,23 @@ def test_rmsnorm_softmax(ops, oracle):
             assert np.all(got[np.triu_indices(37, 1, 300)] == 0)
 
 
+@pytest.mark.parametrize("rows,cols", [(600, 1024), (5, 2000), (3, 1)])
+def test_softmax_shapes(ops, oracle, rows, cols):
+    """Rows held by one wavefront (cols <= 1024) and the long-row path. The
+    row sum is a tree sum against the reference's left-to-right loop; on a
+    row of 1024 whose sum is ~1.014 the loop alone is 3.6e-6 from the exact
+    sum (adding small terms to ~1 drops their low bits), so probabilities
+    (<= 1) are held to 1e-5 absolute and every row to a sum of 1."""
+    rng = np.random.default_rng(rows + cols)
+    p = rng.standard_normal((rows, cols), dtype=np.float32) * 4
+    for causal in (False, True):
+        got, ref = ops.softmax(p, causal), oracle.softmax(p, causal)
+        assert np.abs(got - ref).max() <= 1e-5
+        assert np.abs(got.astype(np.float64).sum(1) - 1).max() <= 1e-5
+        if causal:
+            assert np.all(got[np.triu_indices(rows, 1, cols)] == 0)
+
+
 @pytest.mark.parametrize("kind", range(6))
 def test_act_bitwise(ops, oracle, kind):
     rng = np.random.default_rng(kind)
