@@ -22,6 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+VALU_MAC_PEAK_T = 256 * 64 * 2.4e9 / 2 / 1e12  # non-FMA multiply + add per lane
 
 
 def log(msg):
@@ -244,10 +245,17 @@ def run_suite(iters, cpu=True):
                       max(8, iters // 4))
     layer_bytes = 12976128
     gbs = 8 * layer_bytes / us / 1e3
+    # the t8 contract sums without FMA: one multiply and one add per
+    # connection and token, so the vector ALU bound is 64 lanes x 2.4 GHz x
+    # 256 CUs / 2 ops = 19.66 T connection-tokens/s (tanh_f comes on top)
+    macs = 8 * d * k0 * T
+    tmac = macs / us / 1e6
     out["cfg4_b1_stack"] = {"us": round(us, 2), "host_us": round(wall, 2),
                             "us_per_layer": round(us / 8, 2), "GBps_unique": round(gbs, 1),
                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                            "note": "includes the two transposes of the stack"}
+                            "T_mac_per_s": round(tmac, 3),
+                            "frac_valu_mac": round(tmac / VALU_MAC_PEAK_T, 4),
+                            "note": "plan kernel + one kernel for all 8 layers, x and y [T][d]"}
     if orc:  # one layer of the stack on the host (the t8 contract), per layer
         w0, s0 = conn.make_block_aligned(np.random.default_rng(4), d, k0)
         xt_h = orc.transpose_t8(np.random.default_rng(5).standard_normal((T, d), dtype=np.float32),
@@ -405,6 +413,8 @@ def main():
     ap.add_argument("--gemv-iters", type=int, default=400)
     ap.add_argument("--suite-iters", type=int, default=100)
     ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--suite-only", action="store_true",
+                    help="only configs 0, 1, 2, 4 and the op timings (no decoder, no CPU)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
     args = ap.parse_args()
@@ -420,6 +430,9 @@ def main():
     sparrow_amd.init(0)
     if args.traffic_probe:
         traffic_probe(20)
+        return
+    if args.suite_only:
+        print(json.dumps({"suite": run_suite(args.suite_iters, cpu=False)}))
         return
     cfg = M.minicpm_2b_config()
     t = time.time()

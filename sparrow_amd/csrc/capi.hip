@@ -526,14 +526,33 @@ int vmlm_hip_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y,
     return launch_b1_forward(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, x, n_tokens,
                              (int)n_tokens, y, 1, -1, as_stream(stream));
 }
+// One T8 layer over the reference layout xt[n][t8]: through a plan (from the
+// stream's workspace) when the shape allows it, else one lane per (neuron, token).
+static int b1_t8_layer(const float *w, const uint32_t *src, int n, int k0, const float *xt,
+                       size_t t8, size_t n_tokens, float *yt, Stage &stg, hipStream_t st) {
+    if (n_tokens == 0 || n == 0) return VMLM_OK;
+    if (b1_plan_ok(n, k0, n) && round_up(n_tokens, 16) <= t8) {
+        B1PlanJobs jobs{};
+        jobs.job[0] = B1PlanJob{w, src, stg.alloc<char>(b1_plan_bytes(n, k0)), k0};
+        STAGE_OK(stg);
+        int rc = launch_b1_plan(jobs, 1, n, n, st);
+        if (rc) return rc;
+        return launch_b1_t8_plan_layer(jobs.job[0].plan, n, k0, n, xt, 16, t8, (int)n_tokens, yt,
+                                       16, t8, -1, st);
+    }
+    return launch_b1_forward(w, src, n, k0, xt, t8, (int)n_tokens, yt, 0, -1, st);
+}
+
 int vmlm_hip_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
                            size_t n_tokens, float *yt, void *stream) {
     INIT_OR_RETURN();
     int rc = check_conn(sc);
     if (rc) return rc;
     VMLM_GUARD(t8 >= n_tokens, "B1_T8: row stride t8 < n_tokens");
-    return launch_b1_forward(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, xt, t8,
-                             (int)n_tokens, yt, 0, -1, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    return b1_t8_layer(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, xt, t8, n_tokens, yt,
+                       stg, st);
 }
 int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8,
                           void *stream) {
@@ -827,8 +846,9 @@ static int host_b1(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8, siz
         float *dx = stg.upload(xt, n * t8);
         float *dy = stg.upload((const float *)yt, n * t8);
         STAGE_OK(stg);
-        rc = launch_b1_forward(dw, ds, (int)n, (int)sc->k0, dx, t8, (int)n_tokens, dy, mode, -1,
-                               st);
+        rc = mode == 0 ? b1_t8_layer(dw, ds, (int)n, (int)sc->k0, dx, t8, n_tokens, dy, stg, st)
+                       : launch_b1_forward(dw, ds, (int)n, (int)sc->k0, dx, t8, (int)n_tokens, dy,
+                                           mode, -1, st);
         if (!rc) rc = download(yt, dy, n * t8 * sizeof(float), st);
         if (rc) return rc;
     }

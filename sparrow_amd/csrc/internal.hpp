@@ -145,11 +145,32 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
 // B1 gather forward over source-major activations.
 int launch_b1_forward(const float *w, const uint32_t *src, int n, int k0, const float *xt,
                       size_t t8, int n_tokens, float *yt, int mode, int act, hipStream_t st);
-// T8 layer over d source rows (indices clamped to d - 1) with the sources of
-// each 16-token block staged in LDS; other shapes take launch_b1_forward.
-int launch_b1_t8_layer(const float *w, const uint32_t *src, int n, int k0, int d,
-                       const float *xt, size_t t8, int n_tokens, float *yt, int act,
-                       hipStream_t st);
+// T8 layers with a prepared plan (k0 <= 32, d <= 2032). A plan job rewrites
+// one layer's (src, w) into b1_plan_bytes(n, k0) bytes at `plan`; the layer
+// kernel reads activations addressed as (t / 16) * bs + s * rs + t % 16.
+struct B1PlanJob {
+    const float *w;
+    const uint32_t *src;
+    void *plan;
+    int k0;
+};
+constexpr int B1_PLAN_JOBS = 16;
+struct B1PlanJobs {
+    B1PlanJob job[B1_PLAN_JOBS];
+};
+bool b1_plan_ok(int n, int k0, int d);
+size_t b1_plan_bytes(int n, int k0);
+int launch_b1_plan(const B1PlanJobs &jobs, int njobs, int n, int d, hipStream_t st);
+// Whole layer stack in one kernel (every layer n = d, k0 <= 32, d <= 5104):
+// a workgroup carries 4 tokens through all layers with the activations in
+// LDS. x and y are [T][d]; plans are prepared by launch_b1_stack.
+bool b1_stack_ok(int d, const int *k0, int n_layers);
+size_t b1_stack_plan_bytes(int d, const int *k0, int n_layers);
+int launch_b1_stack(const B1PlanJob *layers, int n_layers, int d, const float *x, float *y,
+                    int T, int act, void *plan, hipStream_t st);
+int launch_b1_t8_plan_layer(const void *plan, int n, int k0, int d, const float *x, size_t xbs,
+                            size_t xrs, int n_tokens, float *y, size_t ybs, size_t yrs, int act,
+                            hipStream_t st);
 int launch_transpose_t8(const float *x, size_t T, size_t d, float *xt, size_t t8,
                         hipStream_t st);
 int launch_transpose_back(const float *a, size_t rows, size_t cols, float *out, size_t os,

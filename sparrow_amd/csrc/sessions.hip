@@ -652,15 +652,32 @@ int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers, c
     }
     if (n_tokens == 0) return VMLM_OK;
     hipStream_t st = as_stream(stream);
+    const int actk = act == 0xFFFF ? -1 : (int)act;
+    std::vector<B1PlanJob> jobs(n_layers);
+    std::vector<int> k0s(n_layers);
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        k0s[l] = (int)layers[l].k0;
+        jobs[l] = B1PlanJob{layers[l].w, layers[l].src_u32, nullptr, k0s[l]};
+    }
+    if (b1_stack_ok((int)d, k0s.data(), (int)n_layers)) {
+        // one kernel for the whole stack (activations stay in LDS)
+        void *plan = nullptr;
+        VMLM_HIP_CHECK(
+            hipMallocAsync(&plan, b1_stack_plan_bytes((int)d, k0s.data(), (int)n_layers), st));
+        rc = launch_b1_stack(jobs.data(), (int)n_layers, (int)d, x, y, (int)n_tokens, actk, plan,
+                             st);
+        (void)hipFreeAsync(plan, st);
+        return rc;
+    }
+    // layer by layer over the reference layout [d][t8], one lane per (neuron, token)
     const size_t t8 = (n_tokens + 63) / 64 * 64;
     float *a = nullptr, *b = nullptr;
     VMLM_HIP_CHECK(hipMallocAsync((void **)&a, d * t8 * 4, st));
     VMLM_HIP_CHECK(hipMallocAsync((void **)&b, d * t8 * 4, st));
     rc = launch_transpose_t8(x, n_tokens, d, a, t8, st);
-    const int actk = act == 0xFFFF ? -1 : (int)act;
     for (uint32_t l = 0; l < n_layers && !rc; ++l) {
-        rc = launch_b1_t8_layer(layers[l].w, layers[l].src_u32, (int)d, (int)layers[l].k0,
-                                (int)d, a, t8, (int)n_tokens, b, actk, st);
+        rc = launch_b1_forward(layers[l].w, layers[l].src_u32, (int)d, (int)layers[l].k0, a, t8,
+                               (int)n_tokens, b, 0, actk, st);
         std::swap(a, b);
     }
     if (!rc) rc = launch_transpose_back(a, d, n_tokens, y, d, t8, st);

@@ -50,3 +50,33 @@ def test_b1_stack_prng_topology(hip, oracle):
     y = yb.to_array((T, d), np.float32)
     ref = oracle.transpose_t8_back(oracle.b1_forward_t8(w, src, oracle.transpose_t8(x, 72), T), T)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("d,k0s,T,act", [(1000, (32, 7, 1, 20), 37, 4),   # mixed k0, ragged
+                                         (3000, (8, 8), 9, 0xFFFF),       # wide, no activation
+                                         (40, (5,), 4, 4)])               # one pass, one block
+def test_b1_stack_shapes(hip, oracle, d, k0s, T, act):
+    """The one-kernel stack (plans padded to the widest layer with no-op
+    steps, activations kept in LDS), bitwise against the oracle layer by
+    layer."""
+    from sparrow_amd import conn
+    rng = np.random.default_rng(d + T)
+    layers = [(rng.standard_normal((d, k0), dtype=np.float32),
+               rng.integers(0, d, size=(d, k0)).astype(np.uint32)) for k0 in k0s]
+    x = rng.standard_normal((T, d), dtype=np.float32)
+    dev = [conn.DeviceConn(w, s, li) for li, (w, s) in enumerate(layers)]
+    xb = conn.DeviceBuffer.from_array(x)
+    yb = conn.DeviceBuffer(x.nbytes)
+    conn.stack_forward(dev, xb.ptr, yb.ptr, T, act=act)
+    y = yb.to_array((T, d), np.float32)
+    for b in dev:
+        b.free()
+    xb.free()
+    yb.free()
+    xt = oracle.transpose_t8(x, (T + 7) // 8 * 8)
+    for w, s in layers:
+        xt = oracle.b1_forward_t8(w, s, xt, T)
+        if act != 0xFFFF:
+            xt = oracle.vmap("tanh", xt)
+    ref = oracle.transpose_t8_back(xt, T)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))

@@ -212,10 +212,14 @@ def test_b1_forward_bitwise(ops, oracle, k0):
     assert np.array_equal(bits(y), bits(oracle.b1_forward(w, src, x)))
 
 
-@pytest.mark.parametrize("k0,T,t8", [(32, 1024, 1024), (20, 37, 40), (1, 5, 8), (0, 3, 8)])
-def test_b1_forward_t8_bitwise(ops, oracle, k0, T, t8):
+@pytest.mark.parametrize("k0,T,t8,n", [(32, 1024, 1024, 96), (20, 37, 40, 96), (1, 5, 8, 96),
+                                       (0, 3, 8, 96), (33, 40, 48, 70),   # one lane per token
+                                       (20, 37, 48, 100), (5, 16, 16, 33),  # planned, ragged
+                                       (32, 200, 208, 1000), (1, 70, 80, 2032)])
+def test_b1_forward_t8_bitwise(ops, oracle, k0, T, t8, n):
+    """Planned layers (k0 <= 32, 16 | t8) and the one-lane-per-(neuron, token)
+    kernel, bitwise against the t8 scalar contract."""
     rng = np.random.default_rng(k0 + T)
-    n = 96
     w = rng.standard_normal((n, k0), dtype=np.float32)
     src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
     x = rng.standard_normal((T, n), dtype=np.float32)
@@ -226,6 +230,32 @@ def test_b1_forward_t8_bitwise(ops, oracle, k0, T, t8):
     assert np.array_equal(bits(yt[:, :T]), bits(ref[:, :T]))
     back = ops.transpose_t8_back(yt, T)
     assert np.array_equal(back, oracle.transpose_t8_back(yt, T))
+
+
+def test_b1_t8_special_values(ops, oracle):
+    """k0 = 5 pads each neuron's last group of four with three (zero row,
+    weight -0.0) steps; the sums must keep signed zeros and infinities and
+    produce NaN exactly where the contract does."""
+    rng = np.random.default_rng(11)
+    n, k0, T, t8 = 64, 5, 32, 32
+    w = rng.standard_normal((n, k0), dtype=np.float32)
+    w[:8] = -0.0                      # every product -0.0 (x > 0): sum -0.0
+    w[8:16] = 0.0                     # +0.0 sums
+    w[16:20, 2] = np.inf
+    w[20:24, 0] = -np.inf
+    src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
+    src[:16] = 0
+    xt = rng.standard_normal((n, t8), dtype=np.float32)
+    xt[0] = np.abs(xt[0]) + 0.5
+    xt[1, ::3] = -0.0
+    xt[2, ::5] = np.inf
+    yt, _ = ops.b1_forward_t8(w, src, xt, T)
+    ref = oracle.b1_forward_t8(w, src, xt, T)
+    got, want = yt[:, :T], ref[:, :T]
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+    assert np.all(bits(got[:8]) == 0x80000000) and np.all(bits(got[8:16]) == 0)
 
 
 def test_b1_guards(ops):
