@@ -151,13 +151,23 @@ __global__ __launch_bounds__(256) void b1_plan_kernel(B1PlanJobs jobs, int n, in
     const int k0 = jb.k0, G = g_pad > 0 ? g_pad : (k0 + 3) / 4;
     const int i0 = (int)blockIdx.x * 64, rows = n - i0 < 64 ? n - i0 : 64;
     {
-        // 8 rows per sweep, thread (tid >> 5, tid & 31): consecutive j of a row
-        const int j = threadIdx.x & 31;
-        for (int r = threadIdx.x >> 5; r < rows; r += 8) {
-            if (j < k0) {
-                ss[r][j] = jb.src[(size_t)(i0 + r) * k0 + j];
-                sw[r][j] = jb.w[(size_t)(i0 + r) * k0 + j];
-            }
+        // thread (tid >> 5, tid & 31) takes rows tid >> 5, + 8, ..., + 56 at
+        // column tid & 31; all 16 loads are issued before any store (rows and
+        // columns clamped, so the loads do not branch)
+        const int j = threadIdx.x & 31, jc = j < k0 ? j : k0 - 1;
+        uint32_t vs[8];
+        float vw[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int r = min((int)(threadIdx.x >> 5) + 8 * k, rows - 1);
+            vs[k] = jb.src[(size_t)(i0 + r) * k0 + jc];
+            vw[k] = jb.w[(size_t)(i0 + r) * k0 + jc];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int r = min((int)(threadIdx.x >> 5) + 8 * k, rows - 1);
+            ss[r][jc] = vs[k];
+            sw[r][jc] = vw[k];
         }
     }
     __syncthreads();
