@@ -68,6 +68,17 @@ float vo_round_f32(float v) {
     return (v + MAGIC) - MAGIC;
 }
 
+/* Rust's `f as i32` (saturating; NaN -> 0). The callers convert values that
+ * are integral and small after their clamps, or NaN; C's (int) cast of NaN is
+ * undefined (x86 yields INT_MIN, which would send exp_f(NaN) to the
+ * underflow branch instead of the reference's NaN). */
+static inline int rust_as_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return 2147483647;
+    if (v <= -2147483648.0f) return (int)-2147483647 - 1;
+    return (int)v;
+}
+
 /* sys/src/math/mod.rs:74-140 -- clamp, Cody-Waite ln2 split, degree-7
  * polynomial in Horner form, normal / subnormal / underflow 2^n. */
 float vo_exp_f(float x) {
@@ -88,7 +99,7 @@ float vo_exp_f(float x) {
     p = p * r + 1.6666665e-1f;
     p = p * r + 0.5f;
     p = p * r2 + r + 1.0f;
-    int ni = (int)n;
+    int ni = rust_as_i32(n);
     if (ni >= -126) return p * f_from_bits((uint32_t)(ni + 127) << 23);
     if (ni >= -149) return p * f_from_bits(1u << (ni + 149));
     return 0.0f;
@@ -124,7 +135,7 @@ static inline void sin_cos_reduce(float x, float *r_out, float *r2_out, int *n_o
     float r = ((x - n * PI2_HI) - n * PI2_MID) - n * PI2_LO;
     *r_out = r;
     *r2_out = r * r;
-    *n_out = (int)n;
+    *n_out = rust_as_i32(n);
 }
 
 /* ops/src/kernels.rs:194-200 */

@@ -111,6 +111,11 @@ __device__ __forceinline__ float round_f32(float v) {
     return (v + MAGIC) - MAGIC;
 }
 
+// Rust's `f as i32` for the values these routines convert: NaN becomes 0
+// (the others are integral and within +-2^24 after the clamps). The explicit
+// test keeps C++ from treating the NaN conversion as undefined.
+__device__ __forceinline__ int as_i32(float n) { return n == n ? (int)n : 0; }
+
 // sys/src/math/mod.rs:74-140
 __device__ __forceinline__ float exp_f(float x) {
     x = x < -88.0f ? -88.0f : (x > 88.0f ? 88.0f : x);
@@ -127,7 +132,7 @@ __device__ __forceinline__ float exp_f(float x) {
     p = p * r + 1.6666665e-1f;
     p = p * r + 0.5f;
     p = p * r2 + r + 1.0f;
-    int ni = (int)n;
+    int ni = as_i32(n);
     if (ni >= -126) return p * __uint_as_float((uint32_t)(ni + 127) << 23);
     if (ni >= -149) return p * __uint_as_float(1u << (ni + 149));
     return 0.0f;
@@ -169,7 +174,7 @@ __device__ __forceinline__ void sincos_f(float x, float *s_out, float *c_out) {
     p = p * r2 + 4.1666630e-2f;
     p = p * r2 - 5.0e-1f;
     float cp = r2 * p + 1.0f;
-    switch (((int)n) & 3) {
+    switch (as_i32(n) & 3) {
     case 0: *s_out = sp; *c_out = cp; break;
     case 1: *s_out = cp; *c_out = -sp; break;
     case 2: *s_out = -sp; *c_out = -cp; break;

@@ -349,64 +349,111 @@ int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t 
     return VMLM_OK;
 }
 
+// Element kernels: four elements per thread through float4 loads and stores
+// when every pointer is 16-byte aligned (the scalar form otherwise); the tail
+// past the last full quad is done element by element. Each element gets the
+// reference's operation, so vector and scalar forms agree bit for bit.
+static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 // ops/src/kernels.rs:1144-1167 -- RELU: maxps(v,0) on the 8-wide body
 // (returns 0 unless v > 0), `if x < 0 {0}` on the tail; others act_scalar.
-__global__ void act_kernel(float *__restrict__ d, size_t n, int kind) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    float x = d[i];
-    if (kind == VMLM_ACT_RELU) {
-        size_t n8 = n / 8 * 8;
-        if (i < n8) {
-            d[i] = x > 0.0f ? x : 0.0f;
-        } else if (x < 0.0f) {
-            d[i] = 0.0f;
+__device__ __forceinline__ float act_elem(float x, size_t i, size_t n8, int kind) {
+    if (kind == VMLM_ACT_RELU) return i < n8 ? (x > 0.0f ? x : 0.0f) : (x < 0.0f ? 0.0f : x);
+    return act_scalar(x, kind);
+}
+template <bool V4>
+__global__ __launch_bounds__(256) void act_kernel(float *__restrict__ d, size_t n, int kind) {
+    const size_t n8 = n / 8 * 8;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (V4) {
+        const size_t i = 4 * t;
+        if (i + 4 <= n) {
+            float4 v = *(const float4 *)(d + i);
+            v.x = act_elem(v.x, i, n8, kind);
+            v.y = act_elem(v.y, i + 1, n8, kind);
+            v.z = act_elem(v.z, i + 2, n8, kind);
+            v.w = act_elem(v.w, i + 3, n8, kind);
+            *(float4 *)(d + i) = v;
+        } else {
+            for (size_t k = i; k < n; ++k) d[k] = act_elem(d[k], k, n8, kind);
         }
-        return;
+    } else if (t < n) {
+        d[t] = act_elem(d[t], t, n8, kind);
     }
-    d[i] = act_scalar(x, kind);
 }
 
 int launch_act(float *dst, size_t n, int kind, hipStream_t st) {
     if (n == 0) return VMLM_OK;
-    act_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, n, kind);
+    if (aligned16(dst))
+        act_kernel<true><<<cdiv(cdiv(n, 4), 256), 256, 0, st>>>(dst, n, kind);
+    else
+        act_kernel<false><<<cdiv(n, 256), 256, 0, st>>>(dst, n, kind);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
 
 // ops/src/kernels.rs:1115-1142
-__global__ void ew_kernel(float *__restrict__ d, const float *__restrict__ x,
-                          const float *__restrict__ y, size_t n, int op) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    float a = x[i], b = y[i];
-    float r;
+__device__ __forceinline__ float ew_elem(float a, float b, int op) {
     switch (op) {
-    case VMLM_OP_EWADD: r = a + b; break;
-    case VMLM_OP_EWMUL: r = a * b; break;
-    case VMLM_OP_EWSUB: r = a - b; break;
-    default: r = a / b; break;
+    case VMLM_OP_EWADD: return a + b;
+    case VMLM_OP_EWMUL: return a * b;
+    case VMLM_OP_EWSUB: return a - b;
+    default: return a / b;
     }
-    d[i] = r;
+}
+template <bool V4>
+__global__ __launch_bounds__(256) void ew_kernel(float *__restrict__ d, const float *__restrict__ x,
+                                                 const float *__restrict__ y, size_t n, int op) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (V4) {
+        const size_t i = 4 * t;
+        if (i + 4 <= n) {
+            const float4 a = *(const float4 *)(x + i), b = *(const float4 *)(y + i);
+            *(float4 *)(d + i) = make_float4(ew_elem(a.x, b.x, op), ew_elem(a.y, b.y, op),
+                                             ew_elem(a.z, b.z, op), ew_elem(a.w, b.w, op));
+        } else {
+            for (size_t k = i; k < n; ++k) d[k] = ew_elem(x[k], y[k], op);
+        }
+    } else if (t < n) {
+        d[t] = ew_elem(x[t], y[t], op);
+    }
 }
 
 int launch_ew(float *dst, const float *x, const float *y, size_t n, int op, hipStream_t st) {
     if (n == 0) return VMLM_OK;
-    ew_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, x, y, n, op);
+    if (aligned16(dst) && aligned16(x) && aligned16(y))
+        ew_kernel<true><<<cdiv(cdiv(n, 4), 256), 256, 0, st>>>(dst, x, y, n, op);
+    else
+        ew_kernel<false><<<cdiv(n, 256), 256, 0, st>>>(dst, x, y, n, op);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
 
 // core/src/interp.rs:1225-1235
-__global__ void scale_kernel(float *__restrict__ d, const float *__restrict__ s, size_t n,
-                             float a) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) d[i] = s[i] * a;
+template <bool V4>
+__global__ __launch_bounds__(256) void scale_kernel(float *__restrict__ d,
+                                                    const float *__restrict__ s, size_t n,
+                                                    float a) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (V4) {
+        const size_t i = 4 * t;
+        if (i + 4 <= n) {
+            const float4 v = *(const float4 *)(s + i);
+            *(float4 *)(d + i) = make_float4(v.x * a, v.y * a, v.z * a, v.w * a);
+        } else {
+            for (size_t k = i; k < n; ++k) d[k] = s[k] * a;
+        }
+    } else if (t < n) {
+        d[t] = s[t] * a;
+    }
 }
 
 int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st) {
     if (n == 0) return VMLM_OK;
-    scale_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, src, n, s);
+    if (aligned16(dst) && aligned16(src))
+        scale_kernel<true><<<cdiv(cdiv(n, 4), 256), 256, 0, st>>>(dst, src, n, s);
+    else
+        scale_kernel<false><<<cdiv(n, 256), 256, 0, st>>>(dst, src, n, s);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -415,11 +462,13 @@ int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st
 __global__ void rope_kernel(float *__restrict__ dst, const float *__restrict__ src, int rows,
                             int hd, size_t ld, float step, float pos0, int heads) {
     const int half = hd / 2;
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)rows * heads * half) return;
-    const int i = (int)(idx % half);
-    const int h = (int)((idx / half) % heads);
-    const int row = (int)(idx / ((size_t)half * heads));
+    // rows * heads * half < 2^32 (checked by the launcher): 32-bit index math
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint32_t)rows * (uint32_t)heads * (uint32_t)half) return;
+    const uint32_t rh = idx / (uint32_t)half;
+    const int i = (int)(idx - rh * (uint32_t)half);
+    const int row = (int)(rh / (uint32_t)heads);
+    const int h = (int)(rh - (uint32_t)row * (uint32_t)heads);
     const float pos = pos0 + (float)row;
     const float *sr = src + (size_t)row * ld + (size_t)h * hd;
     float *dr = dst + (size_t)row * ld + (size_t)h * hd;
@@ -437,6 +486,7 @@ int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld,
     // step = -2/hd * ln_f(theta), evaluated on the host with the same operations
     float step = -2.0f / (float)hd * host_ln_f(theta);
     size_t n = rows * heads * (hd / 2);
+    VMLM_GUARD(n <= 0xFFFFFF00u, "ROPE: rows * heads * hd / 2 = %zu exceeds 2^32 - 256", n);
     rope_kernel<<<cdiv(n, 256), 256, 0, st>>>(dst, src, (int)rows, (int)hd, ld, step, pos0,
                                               heads);
     VMLM_HIP_CHECK(hipGetLastError());

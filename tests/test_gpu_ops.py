@@ -138,6 +138,61 @@ def test_ew_scale_bitwise(ops, oracle, op):
     assert np.array_equal(bits(ops.scale(x, 0.125)), bits(oracle.scale(x, 0.125)))
 
 
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_elementwise_device_alignment(hip, oracle, offset):
+    """Device-pointer element ops on buffers that start `offset` floats past a
+    16-byte boundary: the aligned (four per thread) and scalar forms, and the
+    ReLU body/tail split at n // 8 * 8, agree bitwise with the oracle."""
+    import ctypes as C
+    rng = np.random.default_rng(offset)
+    n = 1029
+    x = (rng.standard_normal(n, dtype=np.float32) * 6).astype(np.float32)
+    x[:3] = [-0.0, np.nan, -3.0]
+    x[-3:] = [-0.0, np.nan, -3.0]
+    y = rng.standard_normal(n, dtype=np.float32) + np.float32(0.1)
+    nb = (n + 8) * 4
+    bufs = []
+    for _ in range(3):
+        p = C.c_void_p()
+        assert hip.vmlm_hip_malloc(C.byref(p), nb) == 0
+        bufs.append(p.value)
+    dx, dy, dd = (b + 4 * offset for b in bufs)
+
+    def up(dev, a):
+        assert hip.vmlm_hip_memcpy_h2d(C.c_void_p(dev), a.ctypes.data, a.nbytes) == 0
+
+    def down(dev):
+        out = np.empty(n, np.float32)
+        assert hip.vmlm_hip_sync() == 0
+        assert hip.vmlm_hip_memcpy_d2h(out.ctypes.data, C.c_void_p(dev), out.nbytes) == 0
+        return out
+
+    try:
+        up(dy, y)
+        for kind in (0, 2, 4):
+            up(dx, x)
+            assert hip.vmlm_hip_act(C.c_void_p(dx), n, kind, None) == 0
+            want = oracle.act(x, kind)
+            got = down(dx)
+            assert np.array_equal(np.isnan(got), np.isnan(want))
+            ok = ~np.isnan(want)
+            assert np.array_equal(bits(got[ok]), bits(want[ok])), kind
+        up(dx, x)
+        for op in (20, 21, 22, 23):
+            assert hip.vmlm_hip_ew_op(C.c_void_p(dd), C.c_void_p(dx), C.c_void_p(dy), n, op,
+                                      None) == 0
+            got, want = down(dd), oracle.ew_op(x, y, op)
+            ok = ~np.isnan(want)
+            assert np.array_equal(bits(got[ok]), bits(want[ok])), op
+        assert hip.vmlm_hip_scale(C.c_void_p(dd), C.c_void_p(dx), n, C.c_float(0.125), None) == 0
+        got, want = down(dd), oracle.scale(x, 0.125)
+        ok = ~np.isnan(want)
+        assert np.array_equal(bits(got[ok]), bits(want[ok]))
+    finally:
+        for b in bufs:
+            hip.vmlm_hip_free(C.c_void_p(b))
+
+
 @pytest.mark.parametrize("pos0", [0, 1, 127, 1000, 65000])
 def test_rope_bitwise(ops, oracle, pos0):
     rng = np.random.default_rng(pos0)

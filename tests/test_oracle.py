@@ -38,6 +38,19 @@ def test_exp_f_reference_kats(oracle):
     assert np.all(np.diff(ys.astype(np.float64)) >= 0)
 
 
+def test_nan_propagates_like_rust(oracle):
+    """sys/src/math/mod.rs:133 converts with Rust's `n as i32`, which maps NaN
+    to 0: exp_f(NaN) = p * 2^0 with p NaN, so NaN (not the underflow branch's
+    0.0); tanh / sigmoid / SiLU of NaN are NaN; sin/cos of NaN are NaN."""
+    nan = float("nan")
+    assert math.isnan(oracle.exp_f(nan))
+    x = np.array([nan, -nan], np.float32)
+    for name in ("exp", "tanh", "sin", "cos"):
+        assert np.all(np.isnan(oracle.vmap(name, x))), name
+    for kind in (2, 3, 4):  # SiLU, sigmoid, tanh
+        assert np.all(np.isnan(oracle.act(x, kind))), kind
+
+
 def test_exp_f_full_domain_sweep(oracle):
     """tests/src/main.rs:84-160: max rel <= 1e-6 over the normal-result range
     of [-88, 88] (reference measured 7.91e-8); subnormal results within the
