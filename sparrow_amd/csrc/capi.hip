@@ -576,15 +576,12 @@ int vmlm_hip_attention_prefill(const float *q, const float *k, const float *v, f
     hipStream_t st = as_stream(stream);
     Stage stg(st);
     const size_t W = n_heads * head_dim;
-    float *kr = stg.alloc<float>(S * W);
+    char *work = stg.alloc<char>(attention_prefill_work_bytes((int)S, (int)n_heads, 1));
     STAGE_OK(stg);
-    // K rotated once into the workspace; Q rotated as the attention loads it
-    int rc = launch_rope(kr, k, S, head_dim, W, theta, (float)pos0, (int)n_heads, st);
-    if (!rc)
-        rc = launch_attention_prefill(q, kr, v, out, (int)S, (int)n_heads, (int)W, (int)W, scale,
-                                      causal, st, true, -2.0f / (float)head_dim * host_ln_f(theta),
-                                      (float)pos0);
-    return rc;
+    // K rotated as its bf16 terms are prepared, Q as the attention loads it
+    return launch_attention_prefill(q, k, v, out, (int)S, (int)n_heads, (int)W, (int)W, scale,
+                                    causal, work, st, true,
+                                    -2.0f / (float)head_dim * host_ln_f(theta), (float)pos0);
 }
 
 int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v_new,

@@ -213,16 +213,21 @@ __device__ __forceinline__ float act_scalar(float x, int kind) {
     }
 }
 
-// core/src/interp.rs:1183-1221: one RoPE pair at position `pos`, component i.
-__device__ __forceinline__ void rope_pair(float x1, float x2, float pos, int i, float step,
-                                          float *y1, float *y2) {
+// core/src/interp.rs:1183-1221: the rotation of RoPE component i at position
+// `pos` (a function of (pos, i) only, so rows at one position share it) ...
+__device__ __forceinline__ void rope_angle(float pos, int i, float step, float *si, float *co) {
     const float TWO_PI = 6.2831855f;
     float inv = exp_f((float)i * step);
     float period = TWO_PI / inv;
     float pr = period >= 1.0e6f ? pos : pos - period * floor_f(pos / period);
     float ang = pr * inv;
+    sincos_f(ang, si, co);
+}
+// ... and one rotated pair
+__device__ __forceinline__ void rope_pair(float x1, float x2, float pos, int i, float step,
+                                          float *y1, float *y2) {
     float si, co;
-    sincos_f(ang, &si, &co);
+    rope_angle(pos, i, step, &si, &co);
     *y1 = x1 * co - x2 * si;
     *y2 = x1 * si + x2 * co;
 }

@@ -121,9 +121,14 @@ int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
 // row positions pos0 + row).
 // nseq sequences (one launch, grid z) at strides sin (q/k/v) and sout (out)
 // elements.
-int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
-                             int S, int H, int ld, int ldo, float scale, bool causal,
-                             hipStream_t st, bool rope_q = false, float rope_step = 0.0f,
+// Causal / full attention over [S][ld] rows (head h at columns 64 h), for
+// nseq sequences at strides sin / sout. `work` holds
+// attention_prefill_work_bytes(S, H, nseq) bytes (bf16 term planes of K and
+// V); with rope, K is rotated there and Q as it is loaded (positions pos0 + row).
+size_t attention_prefill_work_bytes(int S, int H, int nseq);
+int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
+                             int H, int ld, int ldo, float scale, bool causal, void *work,
+                             hipStream_t st, bool rope = false, float rope_step = 0.0f,
                              float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0);
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]

@@ -206,15 +206,22 @@ int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n
 // Flash attention on the bf16 matrix cores. Q, K and the probabilities are
 // carried as two bf16 terms x0 = bf16(x), x1 = bf16(x - x0) (|x - x0 - x1|
 // <= 2^-17 |x|), V as three (exact); a product is the sum of the term
-// products (q0k0 + q0k1 + q1k0 + q1k1; p0v0 + p0v1 + p0v2 + p1v0 + p1v1),
+// products (q0k0 + q0k1 + q1k0 + q1k1; v0p0 + v1p0 + v2p0 + v0p1 + v1p1),
 // each exact, accumulated in f32 by v_mfma_f32_16x16x32_bf16: relative error
 // ~2^-16, well inside the 1e-4 * RMS contract of the attention composition,
 // and a one-key softmax row returns its V row exactly. A workgroup owns 64
 // queries of one head (wave w: queries 16w..16w+15) and walks the key blocks
 // of 64 up to the diagonal: K is staged as [key][dim] terms, V transposed as
-// [dim][key] terms, the probabilities go back through LDS as terms, and the
-// running max / sum are per query row (rows 4g..4g+3 of lane (g, r), reduced
-// over the 16 lanes r of a DPP row).
+// [dim][key] terms.
+//
+// Both products are computed transposed, S^T = K Q^T and O^T += V^T P^T, so
+// that the accumulator layout (lane (g, r): rows 4g..4g+3 of column r) puts
+// one query (column r) in each lane: its scores for keys 16j + 4g + i are
+// exactly the B-operand fragment of the next product once the key slots of a
+// 32-key step are taken in the order (32m + 4g + i, 32m + 16 + 4g + i), and V
+// is read in the same order. The probabilities never leave registers; the
+// running max / sum of a query live in its lane (the four lanes g of a query
+// exchange partial max / sum with permlane swaps).
 constexpr int AT_B = 64;   // query / key block
 constexpr int AT_LD = 72;  // bf16 elements per LDS row (64 + 8)
 
@@ -240,6 +247,19 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
     v += dpp_f<DPP_QUAD_REV>(v);
     return v + dpp_f<DPP_QUAD_SWAP>(v);
+}
+
+// value of the same register in lane l ^ 16 / l ^ 32 (v_permlane16_swap pairs
+// rows 0-1 and 2-3 of 16 lanes; v_permlane32_swap pairs the two halves)
+__device__ __forceinline__ float lane_xor16(float v) {
+    const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float((__lane_id() & 16) ? t[0] : t[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float((__lane_id() & 32) ? t[0] : t[1]);
 }
 
 __device__ __forceinline__ f32x4 mfma_b(u32x4 a, u32x4 b, f32x4 c) {
@@ -278,18 +298,99 @@ __device__ __forceinline__ void split8x3(const float (&x)[8], u32x4 &t0, u32x4 &
 // One workgroup per (query block, head, sequence); sequences at strides
 // sin / sout (elements) along grid z. The longest causal rows go first.
 struct PrefillParams {
-    const float *Q, *K, *V;
+    const uint16_t *Qt, *Kt, *Vt;  // bf16 term planes written by attn_qkv_prep_kernel
     float *O;
-    size_t sin, sout;
-    int S, ld, ldo, causal, rope_q, nqb;
-    float scale, rope_step, pos0;
+    size_t sout;
+    int S, Sp, ldo, causal, nqb, H;
+    int o_vec;  // O rows 16-byte aligned: float4 stores
+    float scale;
 };
+
+// Q, K and V of every (sequence, head) as bf16 term planes, rows padded to Sp
+// (a multiple of 64) with zeros:
+//   Qt[z][t][h][row][64], Kt[z][t][h][row][64]  (t < 2; rotated here when
+//                                               rope is set)
+//   Vt[z][t][h][dim][Sp]                        (t < 3; V transposed)
+// so that the attention kernel loads its Q fragments and stages each key
+// block with 16-byte copies. One workgroup per (64-row block, head,
+// sequence); thread (row, c) rotates RoPE pairs 2c and 2c + 1 of its Q and K
+// rows with one angle evaluation per pair (Q and K share the position).
+struct QKVPrepParams {
+    const float *Q, *K, *V;
+    uint16_t *Qt, *Kt, *Vt;
+    size_t sin;
+    int S, Sp, ld, H, rope;
+    float rope_step, pos0;
+};
+__global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
+    const int h = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+    const int k0 = blockIdx.x * AT_B;
+    const size_t plane = (size_t)p.H * p.Sp * 64;
+    {
+        const int row = k0 + (tid >> 4), c = tid & 15, rr = min(row, p.S - 1);
+        const size_t src = z * p.sin + (size_t)rr * p.ld + h * 64 + 2 * c;
+        float2 q1 = *(const float2 *)(p.Q + src), q2 = *(const float2 *)(p.Q + src + 32);
+        float2 k1 = *(const float2 *)(p.K + src), k2 = *(const float2 *)(p.K + src + 32);
+        if (p.rope) {
+            const float fpos = p.pos0 + (float)rr;
+            float si, co, a, b;
+            rope_angle(fpos, 2 * c, p.rope_step, &si, &co);
+            a = q1.x * co - q2.x * si, b = q1.x * si + q2.x * co, q1.x = a, q2.x = b;
+            a = k1.x * co - k2.x * si, b = k1.x * si + k2.x * co, k1.x = a, k2.x = b;
+            rope_angle(fpos, 2 * c + 1, p.rope_step, &si, &co);
+            a = q1.y * co - q2.y * si, b = q1.y * si + q2.y * co, q1.y = a, q2.y = b;
+            a = k1.y * co - k2.y * si, b = k1.y * si + k2.y * co, k1.y = a, k2.y = b;
+        }
+        if (row >= p.S) q1 = q2 = k1 = k2 = make_float2(0.0f, 0.0f);
+        const size_t dst = ((size_t)z * 2 * p.H + h) * p.Sp * 64 + (size_t)row * 64 + 2 * c;
+        auto put = [&](uint16_t *base, float2 lo, float2 hi) {
+            const uint32_t l0 = bf16x2_rne_bits(lo.x, lo.y), h0 = bf16x2_rne_bits(hi.x, hi.y);
+            *(uint32_t *)(base + dst) = l0;
+            *(uint32_t *)(base + dst + 32) = h0;
+            *(uint32_t *)(base + dst + plane) =
+                bf16x2_rne_bits(lo.x - bf16_lo_f32(l0), lo.y - bf16_hi_f32(l0));
+            *(uint32_t *)(base + dst + plane + 32) =
+                bf16x2_rne_bits(hi.x - bf16_lo_f32(h0), hi.y - bf16_hi_f32(h0));
+        };
+        put(p.Qt, q1, q2);
+        put(p.Kt, k1, k2);
+    }
+    {
+        // V transposed through LDS: rows read as float4 (thread: row tid / 16,
+        // dims 4 (tid % 16) ..), then thread (dim, key octet) of the first 512
+        // splits 8 consecutive keys and writes each term as one 16-byte piece
+        __shared__ float vs[AT_B][AT_B + 1];
+        {
+            const int row = k0 + (tid >> 4), d0 = 4 * (tid & 15);
+            const float4 x =
+                *(const float4 *)(p.V + z * p.sin + (size_t)min(row, p.S - 1) * p.ld + h * 64 + d0);
+            const bool ok = row < p.S;
+            vs[tid >> 4][d0] = ok ? x.x : 0.0f;
+            vs[tid >> 4][d0 + 1] = ok ? x.y : 0.0f;
+            vs[tid >> 4][d0 + 2] = ok ? x.z : 0.0f;
+            vs[tid >> 4][d0 + 3] = ok ? x.w : 0.0f;
+        }
+        __syncthreads();
+        if (tid < 512) {
+            const int dim = tid >> 3, kg = tid & 7;
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = vs[8 * kg + i][dim];
+            u32x4 t0, t1, t2;
+            split8x3(x, t0, t1, t2);
+            uint16_t *vt =
+                p.Vt + ((size_t)z * 3 * p.H + h) * 64 * p.Sp + (size_t)dim * p.Sp + k0 + 8 * kg;
+            *(u32x4 *)vt = t0;
+            *(u32x4 *)(vt + plane) = t1;
+            *(u32x4 *)(vt + 2 * plane) = t2;
+        }
+    }
+}
 
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
-    __shared__ __attribute__((aligned(16))) uint16_t Ps[4][2][16][AT_LD];  // [wave][term][q][key]
-    const int S = P.S, ld = P.ld, causal = P.causal;
+    const int S = P.S, causal = P.causal;
     const int h = blockIdx.y, z = blockIdx.z;
     const int qb = causal ? P.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
     const int kb0 = 0, kb1 = causal ? qb + 1 : (S + AT_B - 1) / AT_B;
@@ -297,93 +398,63 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r = lane & 15;
     const int q0 = qb * AT_B + wave * 16;
-    const float *Qh = P.Q + z * P.sin + h * 64, *Kh = P.K + z * P.sin + h * 64,
-                *Vh = P.V + z * P.sin + h * 64;
+    const size_t kplane = (size_t)P.H * P.Sp * 64;
+    const uint16_t *Kth = P.Kt + ((size_t)z * 2 * P.H + h) * P.Sp * 64;
+    const uint16_t *Vth = P.Vt + ((size_t)z * 3 * P.H + h) * 64 * P.Sp;
 
-    // this lane's query fragments: row q0 + r, dims 32s + 8g .. +7, two terms;
-    // the lane holds both members (i, i + 32) of its RoPE pairs, so an
-    // unrotated Q is rotated here (position pos0 + row)
+    // this lane's query fragments: row q0 + r, dims 32 sl + 8g .. +7, two terms
     u32x4 aq[2][2];  // [slice][term]
     {
-        const int qr = q0 + r < S ? q0 + r : S - 1;
-        float x[2][8];
+        const uint16_t *Qth = P.Qt + ((size_t)z * 2 * P.H + h) * P.Sp * 64 + (size_t)(q0 + r) * 64;
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-            const float4 *src = (const float4 *)(Qh + (size_t)qr * ld + sl * 32 + g * 8);
-            const float4 x0 = src[0], x1 = src[1];
-            x[sl][0] = x0.x, x[sl][1] = x0.y, x[sl][2] = x0.z, x[sl][3] = x0.w;
-            x[sl][4] = x1.x, x[sl][5] = x1.y, x[sl][6] = x1.z, x[sl][7] = x1.w;
-        }
-        if (P.rope_q) {
-            const float fpos = P.pos0 + (float)qr;
+        for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                rope_pair(x[0][e], x[1][e], fpos, g * 8 + e, P.rope_step, &x[0][e], &x[1][e]);
-        }
-        split8(x[0], aq[0][0], aq[0][1]);
-        split8(x[1], aq[1][0], aq[1][1]);
+            for (int t = 0; t < 2; ++t)
+                aq[sl][t] = *(const u32x4 *)(Qth + t * (size_t)P.H * P.Sp * 64 + sl * 32 + g * 8);
     }
-    float m[4], l[4];
-    f32x4 o[4];
+    float m = -INFINITY, l = 0.0f;  // query q0 + r
+    f32x4 o[4];                      // o[jd][i]: dim 16 jd + 4g + i of query q0 + r
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m[i] = -INFINITY;
-        l[i] = 0.0f;
-        o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    // staging roles: K rows (key tid/4, dims 16*(tid%4) ..), V columns (dim
-    // tid%64, keys 16*(tid/64) ..)
-    const int kkey = tid >> 2, kd0 = (tid & 3) * 16;
-    const int vd = tid & 63, vk0 = (tid >> 6) * 16;
-    // the next key block's K / V are loaded into registers while the current
-    // one is consumed (the last block reloads itself)
-    float kx[16], vx[16];
+    for (int i = 0; i < 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // staging: 16-byte pieces, 4 of K (term, key, eighth) and 6 of V^T
+    // (term, dim, eighth) per thread; the next key block's pieces are loaded
+    // into registers while the current one is consumed (the last block
+    // reloads itself)
+    u32x4 stg[10];
     auto load_kv = [&](int kb) {
         const int k0 = kb * AT_B;
-        const int kr = k0 + kkey < S ? k0 + kkey : S - 1;
-        const float4 *src = (const float4 *)(Kh + (size_t)kr * ld + kd0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = src[i];
-            kx[4 * i] = v.x;
-            kx[4 * i + 1] = v.y;
-            kx[4 * i + 2] = v.z;
-            kx[4 * i + 3] = v.w;
+        for (int k = 0; k < 4; ++k) {
+            const int idx = tid + 256 * k, t = idx >> 9, key = (idx >> 3) & 63, pc = idx & 7;
+            stg[k] = *(const u32x4 *)(Kth + t * kplane + (size_t)(k0 + key) * 64 + 8 * pc);
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int vr = k0 + vk0 + i < S ? k0 + vk0 + i : S - 1;
-            vx[i] = Vh[(size_t)vr * ld + vd];
+        for (int k = 0; k < 6; ++k) {
+            const int idx = tid + 256 * k, t = idx >> 9, dim = (idx >> 3) & 63, pc = idx & 7;
+            stg[4 + k] = *(const u32x4 *)(Vth + t * kplane + (size_t)dim * P.Sp + k0 + 8 * pc);
         }
     };
+    const int qa = q0 + r;
     load_kv(kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
         const int k0 = kb * AT_B;
         __syncthreads();  // the previous block's K / V are no longer read
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            float x[8], y[8];
+        for (int k = 0; k < 4; ++k) {
+            const int idx = tid + 256 * k, t = idx >> 9, key = (idx >> 3) & 63, pc = idx & 7;
+            *(u32x4 *)&Ks[t][key][8 * pc] = stg[k];
+        }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                x[i] = k0 + kkey < S ? kx[8 * half + i] : 0.0f;
-                y[i] = k0 + vk0 + 8 * half + i < S ? vx[8 * half + i] : 0.0f;
-            }
-            u32x4 t0, t1, t2;
-            split8(x, t0, t1);
-            *(u32x4 *)&Ks[0][kkey][kd0 + 8 * half] = t0;
-            *(u32x4 *)&Ks[1][kkey][kd0 + 8 * half] = t1;
-            split8x3(y, t0, t1, t2);
-            *(u32x4 *)&Vt[0][vd][vk0 + 8 * half] = t0;
-            *(u32x4 *)&Vt[1][vd][vk0 + 8 * half] = t1;
-            *(u32x4 *)&Vt[2][vd][vk0 + 8 * half] = t2;
+        for (int k = 0; k < 6; ++k) {
+            const int idx = tid + 256 * k, t = idx >> 9, dim = (idx >> 3) & 63, pc = idx & 7;
+            *(u32x4 *)&Vt[t][dim][8 * pc] = stg[4 + k];
         }
         __syncthreads();
         load_kv(kb + 1 < kb1 ? kb + 1 : kb);
         __builtin_amdgcn_sched_barrier(0);
 
-        // scores: block j = keys 16j..16j+15; lane (g, r): queries 4g+i, key
-        // 16j+r. The four blocks' MFMA chains are interleaved (each block's
-        // own term order is q0k0, q0k1, q1k0, q1k1 per 32-dim slice).
+        // S^T: block j = keys 16j..16j+15; lane (g, r): keys 16j + 4g + i of
+        // query q0 + r. The four blocks' MFMA chains are interleaved.
         f32x4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -396,125 +467,147 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
                 b1[j] = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][0], b0[j], sc[j]);
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][0], sc[j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][0], b1[j], sc[j]);
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][0], sc[j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][1], b0[j], sc[j]);
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][1], sc[j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(aq[sl][1], b1[j], sc[j]);
+            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][1], sc[j]);
         }
-        float rmax[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qa = q0 + 4 * g + i;
-            float mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int ka = k0 + 16 * j + r;
-                const bool valid = ka < S && (!causal || ka <= qa);
-                sc[j][i] = valid ? sc[j][i] * P.scale : -INFINITY;
-                mx = fmaxf(mx, sc[j][i]);
-            }
-            rmax[i] = row16_max(mx);
-        }
-        float p[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float mn = fmaxf(m[i], rmax[i]);
-            const float alpha = m[i] == -INFINITY ? 0.0f : __expf(m[i] - mn);
-            float rs = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                p[j][i] = sc[j][i] == -INFINITY ? 0.0f : __expf(sc[j][i] - mn);
-                rs += p[j][i];
-            }
-            rs = row16_sum(rs);
-            l[i] = l[i] * alpha + rs;
-            m[i] = mn;
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd][i] *= alpha;
-        }
-        // P terms -> LDS as [q][key] rows of this wave
+        float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t hb = bf16_rne_bits(p[j][i]);
-                const uint32_t lb = bf16_rne_bits(p[j][i] - bf16_bits_to_f32(hb));
-                Ps[wave][0][4 * g + i][16 * j + r] = (uint16_t)hb;
-                Ps[wave][1][4 * g + i][16 * j + r] = (uint16_t)lb;
+                const int ka = k0 + 16 * j + 4 * g + i;
+                const bool valid = ka < S && (!causal || ka <= qa);
+                sc[j][i] = valid ? sc[j][i] * P.scale : -INFINITY;
+                mx = fmaxf(mx, sc[j][i]);
             }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O[q][d] += P[q][key] V[key][d]: A = P rows, B = V^T rows (dims);
-        // the four dim blocks' chains interleaved, each in the term order
-        // p0v0, p0v1, p0v2, p1v0, p1v1
+        mx = fmaxf(mx, lane_xor16(mx));
+        mx = fmaxf(mx, lane_xor32(mx));
+        const float mn = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.0f : __expf(m - mn);
+        float pv[4][4], rs = 0.0f;
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-            const u32x4 p0 = *(const u32x4 *)&Ps[wave][0][r][sl * 32 + g * 8];
-            const u32x4 p1 = *(const u32x4 *)&Ps[wave][1][r][sl * 32 + g * 8];
-            u32x4 v0[4], v1[4], v2[4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int jd = 0; jd < 4; ++jd) {
-                v0[jd] = *(const u32x4 *)&Vt[0][16 * jd + r][sl * 32 + g * 8];
-                v1[jd] = *(const u32x4 *)&Vt[1][16 * jd + r][sl * 32 + g * 8];
-                v2[jd] = *(const u32x4 *)&Vt[2][16 * jd + r][sl * 32 + g * 8];
+            for (int i = 0; i < 4; ++i) {
+                pv[j][i] = sc[j][i] == -INFINITY ? 0.0f : __expf(sc[j][i] - mn);
+                rs += pv[j][i];
             }
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v0[jd], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v1[jd], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p0, v2[jd], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p1, v0[jd], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(p1, v1[jd], o[jd]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    // lane (g, r) of block jd: queries 4g+i, dim 16jd + r
-    float *Oz = P.O + z * P.sout;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int qa = q0 + 4 * g + i;
-        if (qa >= S) continue;
-        const float inv = 1.0f / l[i];
+        rs += lane_xor16(rs);
+        rs += lane_xor32(rs);
+        l = l * alpha + rs;
+        m = mn;
 #pragma unroll
         for (int jd = 0; jd < 4; ++jd)
-            Oz[(size_t)qa * P.ldo + h * 64 + 16 * jd + r] = o[jd][i] * inv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[jd][i] *= alpha;
+        // P^T fragments of the two 32-key steps: slots 8g..8g+7 hold keys
+        // 32 st + 4g + i and 32 st + 16 + 4g + i
+        u32x4 pb[2][2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const float x[8] = {pv[2 * st][0],     pv[2 * st][1],     pv[2 * st][2],
+                                pv[2 * st][3],     pv[2 * st + 1][0], pv[2 * st + 1][1],
+                                pv[2 * st + 1][2], pv[2 * st + 1][3]};
+            split8(x, pb[st][0], pb[st][1]);
+        }
+        // O^T[d][q] += V^T[d][key] P^T[key][q]: A = V^T rows (dim 16 jd + r)
+        // at the same key slots; the four dim blocks' chains interleaved
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            u32x4 va[3][4];
+#pragma unroll
+            for (int t = 0; t < 3; ++t)
+#pragma unroll
+                for (int jd = 0; jd < 4; ++jd) {
+                    const uint16_t *row = &Vt[t][16 * jd + r][32 * st + 4 * g];
+                    const uint2 lo = *(const uint2 *)row, hi = *(const uint2 *)(row + 16);
+                    va[t][jd] = u32x4{lo.x, lo.y, hi.x, hi.y};
+                }
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][0], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][0], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[2][jd], pb[st][0], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][1], o[jd]);
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][1], o[jd]);
+        }
+    }
+    // lane (g, r): query q0 + r, dims 16 jd + 4g .. +3
+    if (qa < S) {
+        const float inv = 1.0f / l;
+        float *orow = P.O + z * P.sout + (size_t)qa * P.ldo + h * 64 + 4 * g;
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) {
+            const float4 v =
+                make_float4(o[jd][0] * inv, o[jd][1] * inv, o[jd][2] * inv, o[jd][3] * inv);
+            if (P.o_vec) {
+                *(float4 *)(orow + 16 * jd) = v;
+            } else {
+                orow[16 * jd] = v.x;
+                orow[16 * jd + 1] = v.y;
+                orow[16 * jd + 2] = v.z;
+                orow[16 * jd + 3] = v.w;
+            }
+        }
     }
 }
 
-int launch_attention_prefill(const float *q, const float *krot, const float *v, float *out,
-                             int S, int H, int ld, int ldo, float scale, bool causal,
-                             hipStream_t st, bool rope_q, float rope_step, float pos0, int nseq,
+size_t attention_prefill_work_bytes(int S, int H, int nseq) {
+    const size_t Sp = (size_t)(S + AT_B - 1) / AT_B * AT_B;
+    return (size_t)nseq * H * Sp * 64 * 7 * sizeof(uint16_t);
+}
+
+int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
+                             int H, int ld, int ldo, float scale, bool causal, void *work,
+                             hipStream_t st, bool rope, float rope_step, float pos0, int nseq,
                              size_t sin, size_t sout) {
-    VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)krot & 15) == 0 &&
-                   (nseq == 1 || sin % 4 == 0),
-               "attention prefill: 16-byte aligned rows required");
+    VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 7) == 0 && ((uintptr_t)k & 7) == 0 &&
+                   ((uintptr_t)v & 15) == 0 && (nseq == 1 || sin % 4 == 0),
+               "attention prefill: 16-byte aligned V rows and 8-byte aligned Q / K rows "
+               "required");
     VMLM_GUARD(nseq >= 1 && nseq <= 65535 && H <= 65535, "attention prefill: grid too large");
     if (S <= 0) return VMLM_OK;
+    const int Sp = (S + AT_B - 1) / AT_B * AT_B;
+    const size_t plane = (size_t)nseq * 2 * H * Sp * 64;
+    QKVPrepParams kp;
+    kp.Q = q;
+    kp.K = k;
+    kp.V = v;
+    kp.Qt = (uint16_t *)work;
+    kp.Kt = kp.Qt + plane;
+    kp.Vt = kp.Kt + plane;
+    kp.sin = sin;
+    kp.S = S;
+    kp.Sp = Sp;
+    kp.ld = ld;
+    kp.H = H;
+    kp.rope = rope ? 1 : 0;
+    kp.rope_step = rope_step;
+    kp.pos0 = pos0;
+    attn_qkv_prep_kernel<<<dim3(Sp / AT_B, H, nseq), 1024, 0, st>>>(kp);
+    VMLM_HIP_CHECK(hipGetLastError());
     PrefillParams P;
-    P.Q = q;
-    P.K = krot;
-    P.V = v;
+    P.Qt = kp.Qt;
+    P.Kt = kp.Kt;
+    P.Vt = kp.Vt;
     P.O = out;
-    P.sin = sin;
     P.sout = sout;
     P.S = S;
-    P.ld = ld;
+    P.Sp = Sp;
     P.ldo = ldo;
     P.causal = causal ? 1 : 0;
-    P.rope_q = rope_q ? 1 : 0;
-    P.nqb = cdiv(S, AT_B);
+    P.nqb = Sp / AT_B;
+    P.H = H;
+    P.o_vec = ((uintptr_t)out & 15) == 0 && ldo % 4 == 0 && (nseq == 1 || sout % 4 == 0);
     P.scale = scale;
-    P.rope_step = rope_step;
-    P.pos0 = pos0;
     attn_prefill_kernel<<<dim3(P.nqb, H, nseq), 256, 0, st>>>(P);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;

@@ -418,6 +418,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     float *h, *h2, *qkv, *att, *o, *gu, *act;
     uint16_t *terms;
     int32_t *toks;
+    char *kvw;
     std::vector<void *> tmp;
     auto get = [&](auto **p, size_t bytes) -> int {
         void *q = nullptr;
@@ -433,7 +434,8 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
         (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) || (rc = get(&gu, M * 2 * I * 4)) ||
         (rc = get(&act, M * I * 4)) || (rc = get(&terms, (size_t)T * M * I * 2)) ||
-        (rc = get(&toks, M * 4))) {
+        (rc = get(&toks, M * 4)) ||
+        (rc = get(&kvw, attention_prefill_work_bytes((int)S, (int)NH, (int)B)))) {
         release();
         return rc;
     }
@@ -470,8 +472,8 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
                                                            (int)d->cap, (int)B);
             VMLM_HIP_CHECK(hipGetLastError());
             if ((r = launch_attention_prefill(qkv, qkv + H, qkv + 2 * H, att, (int)S, (int)NH,
-                                              (int)(3 * H), (int)H, d->c.attn_scale, true, st,
-                                              false, 0.0f, 0.0f, (int)B, S * 3 * H, S * H)))
+                                              (int)(3 * H), (int)H, d->c.attn_scale, true, kvw,
+                                              st, false, 0.0f, 0.0f, (int)B, S * 3 * H, S * H)))
                 return r;
             if ((r = launch_split_terms(att, H, (int)M, (int)H, T, terms, (int)H, st))) return r;
             GemmArgs go = g;
