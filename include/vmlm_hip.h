@@ -234,10 +234,20 @@ int vmlm_decoder_position(const vmlm_decoder *dec, uint32_t *pos);
 /* 1 = replay one captured HIP graph per step (default), 0 = launch eagerly. */
 int vmlm_decoder_set_graph(vmlm_decoder *dec, int enable);
 void *vmlm_decoder_stream(vmlm_decoder *dec);
+/* Layer program of the decode step. Batches of at most 5 sequences default
+ * to the fused layer (five launches: RMSNorm fused into the q/k/v and
+ * gate/up projections, the residual adds into o and down, SiLU * up into
+ * gate/up; full-K GEMVs over weights kept a second time in MFMA-operand
+ * order); larger batches use k-slice GEMVs with separate reduction kernels
+ * (eight launches). 0 selects the k-slice program at any batch. (No
+ * reference counterpart: the reference runs one opcode per instruction.) */
+int vmlm_decoder_set_fused(vmlm_decoder *dec, int enable);
+int vmlm_decoder_fused(const vmlm_decoder *dec);
 /* Times `iters` launches of one decode-step GEMV of every layer in turn
  * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head) on the session stream;
  * writes the mean per-launch duration (HIP events) and its algorithmic
- * HBM bytes (weights + scales + activations in + outputs). */
+ * HBM bytes (weights + scales + activations in + outputs; on the fused
+ * path also the norm gain or the residual rows). */
 int vmlm_decoder_time_gemv(vmlm_decoder *dec, int which, uint32_t iters, float *avg_us,
                            double *bytes_per_launch);
 

@@ -66,6 +66,44 @@ int launch_gemv(const GemvArgs &a, hipStream_t st);
 int launch_gemv_reduce(const float *part, int ks, int M, int N, const float *scale, float *C,
                        int ldc, hipStream_t st);
 
+// Full-K GEMV for decode batches of M <= 5 rows with fused row ops. Input:
+// bf16 term planes A [3][M][lda]; with ssp, the rows are RMSNorm inputs
+// given as terms of x * g, and the dot products are multiplied by
+// inv = 1 / sqrt(sum(ssp[.][b]) / K + eps). Output: Y = acc * scale[j]
+// (FK_STORE), Y = R + acc * scale[j] (FK_RESID; with ssp_out also the terms
+// of Y * gout into Aout and sum Y^2 per 16 columns into ssp_out [N/16][M]),
+// or over 16-row gate/up tile pairs Y[.][16p + r] = silu(gate) * up
+// (FK_SILU; Y and/or its terms in Aout). W is the copy made by
+// launch_swizzle_w.
+enum FkEpi { FK_STORE = 0, FK_RESID = 1, FK_SILU = 2 };
+struct FkArgs {
+    const int8_t *W = nullptr;
+    const float *scale = nullptr;
+    const uint16_t *A = nullptr;
+    int lda = 0;
+    const float *ssp = nullptr;
+    int nssp = 0;
+    float eps = 0.0f;
+    float *Y = nullptr;
+    int ldy = 0;
+    const float *R = nullptr;
+    int ldr = 0;
+    uint16_t *Aout = nullptr;
+    const float *gout = nullptr;
+    float *ssp_out = nullptr;
+    int M = 1, N = 0, K = 0;
+    int epi = FK_STORE;
+    int kb = 0;  // 64-wide k-blocks per wave (2, 3, 4, 6, 8); 0 = chosen by shape
+};
+bool fk_gemv_ok(int M, int N, int K, int epi);
+int launch_fk_gemv(const FkArgs &a, hipStream_t st);
+// Rows h [M][ldh] entering the fused path: terms of h * g into [3][M][ldt]
+// and the partial sums of squares [N/16][M].
+int launch_fk_norm_prep(const float *h, int ldh, const float *g, int M, int N, uint16_t *terms,
+                        int ldt, float *ssp, hipStream_t st);
+// int8 [N][K] row-major -> [N/16][K/64][64 lanes][16 B] MFMA-operand order.
+int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
+
 // Tiled MFMA GEMM for M > 16: C[M,N] = A[M,K] . W[N,K]^T (* scale[n]).
 struct GemmArgs {
     const void *W = nullptr;

@@ -98,6 +98,9 @@ struct vmlm_decoder {
     size_t H = 0, I = 0, NH = 0, V = 0, B = 0, cap = 0, L = 0;
     size_t w_layer = 0, s_layer = 0;  // per-layer element counts
     int8_t *w = nullptr;
+    int8_t *wsw = nullptr;  // the same weights in MFMA-operand order (fused path)
+    float *ssp = nullptr;   // fused path: RMSNorm partial sums of squares [H/16][B]
+    bool fused = false;     // five-launch layers of full-K fused GEMVs (batch <= 5)
     float *s = nullptr, *norms = nullptr;
     uint16_t *embed = nullptr, *lm_head = nullptr;
     float *final_norm = nullptr;
@@ -119,6 +122,8 @@ struct vmlm_decoder {
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
 
+    // swizzled copy at the same offsets
+    const int8_t *Sw(const int8_t *p) const { return wsw + (p - w); }
     const int8_t *Wqkv(size_t l) const { return w + l * w_layer; }
     const int8_t *Wo(size_t l) const { return Wqkv(l) + 3 * H * H; }
     const int8_t *Wgu(size_t l) const { return Wo(l) + H * H; }
@@ -238,11 +243,92 @@ int enqueue_step(vmlm_decoder *d) {
     return VMLM_OK;
 }
 
+// The fused path's four projections of layer l (which: 0 q/k/v, 1 o, 2
+// gate/up, 3 down). Residual rows stay f32 (h, h2); every projection input
+// is a set of bf16 term planes: t_x (terms of x * g of the next RMSNorm, with
+// the partial sums of squares in ssp), t_att (attention output) and t_act
+// (SiLU(gate) * up).
+FkArgs fk_args(vmlm_decoder *d, size_t l, int which) {
+    const int H = (int)d->H, I = (int)d->I;
+    FkArgs f;
+    f.eps = d->c.eps;
+    f.M = (int)d->B;
+    f.nssp = H / 16;
+    switch (which) {
+    case 0:
+        f.W = d->Sw(d->Wqkv(l)), f.scale = d->Sqkv(l), f.N = 3 * H, f.K = H;
+        f.A = d->t_x, f.ssp = d->ssp;
+        f.Y = d->qkv, f.ldy = 3 * H, f.epi = FK_STORE;
+        break;
+    case 1:
+        f.W = d->Sw(d->Wo(l)), f.scale = d->So(l), f.N = H, f.K = H;
+        f.A = d->t_att;
+        f.Y = d->h2, f.ldy = H, f.epi = FK_RESID, f.R = d->h, f.ldr = H;
+        f.Aout = d->t_x, f.gout = d->PostLn(l), f.ssp_out = d->ssp;
+        break;
+    case 2:
+        f.W = d->Sw(d->Wgu(l)), f.scale = d->Sgu(l), f.N = 2 * I, f.K = H;
+        f.A = d->t_x, f.ssp = d->ssp;
+        f.ldy = I, f.epi = FK_SILU, f.Aout = d->t_act;
+        break;
+    default:
+        f.W = d->Sw(d->Wd(l)), f.scale = d->Sd(l), f.N = H, f.K = I;
+        f.A = d->t_act;
+        f.Y = d->h, f.ldy = H, f.epi = FK_RESID, f.R = d->h2, f.ldr = H;
+        f.Aout = d->t_x, f.gout = l + 1 < d->L ? d->InLn(l + 1) : d->final_norm;
+        f.ssp_out = d->ssp;
+        break;
+    }
+    f.lda = f.K;
+    return f;
+}
+
+// The same step with five launches per layer (batch <= 5): RMSNorm split
+// between the residual epilogues and the q/k/v and gate/up projections,
+// the residual adds in the o and down projections, SiLU * up in the gate/up
+// epilogue; q, k, v reach the attention kernel as final rows.
+int enqueue_step_fused(vmlm_decoder *d) {
+    hipStream_t st = d->st;
+    const int B = (int)d->B, H = (int)d->H;
+    int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
+    if (rc) return rc;
+    if ((rc = launch_fk_norm_prep(d->h, H, d->InLn(0), B, H, d->t_x, H, d->ssp, st))) return rc;
+    for (size_t l = 0; l < d->L; ++l) {
+        if ((rc = launch_fk_gemv(fk_args(d, l, 0), st))) return rc;
+        DecodeArgs a;
+        a.q = d->qkv;
+        a.k_new = d->qkv + H;
+        a.v_new = d->qkv + 2 * H;
+        a.ldq = 3 * H;
+        a.kc = d->Kc(l);
+        a.vc = d->Vc(l);
+        a.cap = (int)d->cap;
+        a.H = (int)d->NH;
+        a.posp = d->pos;
+        a.pos = 0;
+        a.step = d->rope_step;
+        a.scale = d->c.attn_scale;
+        if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, 3, H, st))) return rc;
+        for (int which = 1; which < 4; ++which)
+            if ((rc = launch_fk_gemv(fk_args(d, l, which), st))) return rc;
+    }
+    if ((rc = launch_rmsnorm(nullptr, d->h, d->final_norm, B, H, d->c.eps, d->t_x, 3, H, st)))
+        return rc;
+    if ((rc = enqueue_head(d, true))) return rc;
+    step_advance_kernel<<<1, 1, 0, st>>>(d->step, d->pos);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+int enqueue_any_step(vmlm_decoder *d) {
+    return d->fused ? enqueue_step_fused(d) : enqueue_step(d);
+}
+
 int ensure_graph(vmlm_decoder *d) {
     if (d->graph) return VMLM_OK;
     hipGraph_t g = nullptr;
     VMLM_HIP_CHECK(hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(d);
+    int rc = enqueue_any_step(d);
     hipError_t e = hipStreamEndCapture(d->st, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -253,6 +339,14 @@ int ensure_graph(vmlm_decoder *d) {
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
     return VMLM_OK;
+}
+
+// Batches of up to five sequences run the five-launch layer when every
+// projection shape fits the fused kernel.
+bool fused_ok(const vmlm_decoder *d) {
+    const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
+    return H / 16 * B <= 768 && fk_gemv_ok(B, 3 * H, H, FK_STORE) && fk_gemv_ok(B, H, H, FK_RESID) &&
+           fk_gemv_ok(B, 2 * I, H, FK_SILU) && fk_gemv_ok(B, H, I, FK_RESID);
 }
 
 }  // namespace
@@ -293,6 +387,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     };
     d->ks_h = pick_ks(d->H, 2);
     d->ks_i = pick_ks(d->I, 3);
+    d->fused = fused_ok(d);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
         vmlm_decoder_destroy(d);
@@ -305,6 +400,8 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->norms, d->L * 2 * d->H)) || (rc = dalloc(d, &d->embed, d->V * d->H)) ||
         (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
+        (d->fused && (rc = dalloc(d, &d->wsw, d->L * d->w_layer))) ||
+        (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
         (rc = dalloc(d, &d->act, d->B * d->I)) ||
@@ -367,6 +464,17 @@ int vmlm_decoder_load_layer(vmlm_decoder *d, uint32_t layer, const int8_t *wq, c
                               hipMemcpyHostToDevice, st)) != hipSuccess)
         return hip_fail(e, "load_layer gate/up");
     H2D(Wgu + 2 * I * H, wd, H * I);
+    if (d->wsw) {  // the fused path's copy in MFMA-operand order
+        int rc;
+        if ((rc = launch_swizzle_w(W, d->wsw + l * d->w_layer, (int)(3 * H), (int)H, st)) ||
+            (rc = launch_swizzle_w(W + 3 * H * H, d->wsw + l * d->w_layer + 3 * H * H, (int)H,
+                                   (int)H, st)) ||
+            (rc = launch_swizzle_w(Wgu, d->wsw + l * d->w_layer + 4 * H * H, (int)(2 * I),
+                                   (int)H, st)) ||
+            (rc = launch_swizzle_w(Wgu + 2 * I * H, d->wsw + l * d->w_layer + 4 * H * H + 2 * I * H,
+                                   (int)H, (int)I, st)))
+            return rc;
+    }
     H2D(S, sq, H * 4);
     H2D(S + H, sk, H * 4);
     H2D(S + 2 * H, sv, H * 4);
@@ -546,7 +654,7 @@ int vmlm_decoder_decode(vmlm_decoder *d, uint32_t n_steps, int32_t *tokens_out,
     for (uint32_t i = 0; i < n_steps; ++i) {
         if (d->use_graph) {
             VMLM_HIP_CHECK(hipGraphLaunch(d->graph, d->st));
-        } else if ((rc = enqueue_step(d))) {
+        } else if ((rc = enqueue_any_step(d))) {
             return rc;
         }
     }
@@ -577,6 +685,22 @@ int vmlm_decoder_set_graph(vmlm_decoder *d, int enable) {
 
 void *vmlm_decoder_stream(vmlm_decoder *d) { return d ? (void *)d->st : nullptr; }
 
+int vmlm_decoder_set_fused(vmlm_decoder *d, int enable) {
+    VMLM_GUARD(d, "decoder: null");
+    VMLM_GUARD(!enable || d->wsw, "decoder: the fused layer needs a batch of at most 5");
+    if (d->fused != (enable != 0)) {
+        if (d->graph) {
+            VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
+            (void)hipGraphExecDestroy(d->graph);
+            d->graph = nullptr;
+        }
+        d->fused = enable != 0;
+    }
+    return VMLM_OK;
+}
+
+int vmlm_decoder_fused(const vmlm_decoder *d) { return d && d->fused ? 1 : 0; }
+
 int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *avg_us,
                            double *bytes_per_launch) {
     int rc = check_loaded(d);
@@ -584,6 +708,33 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     VMLM_GUARD(which >= 0 && which <= 4 && iters >= 1, "time_gemv: which 0..4, iters >= 1");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     // the launches of the decode step (k-split wide GEMVs; LM head bf16)
+    // the fused path's launches: the full-K kernels with their row ops
+    if (d->fused && which < 4) {
+        auto makef = [&](size_t l) { return fk_args(d, l, which); };
+        hipEvent_t e0, e1;
+        VMLM_HIP_CHECK(hipEventCreate(&e0));
+        VMLM_HIP_CHECK(hipEventCreate(&e1));
+        for (size_t l = 0; l < d->L; ++l)
+            if ((rc = launch_fk_gemv(makef(l), d->st))) return rc;
+        VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
+        for (uint32_t i = 0; i < iters; ++i)
+            if ((rc = launch_fk_gemv(makef(i % d->L), d->st))) return rc;
+        VMLM_HIP_CHECK(hipEventRecord(e1, d->st));
+        VMLM_HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        VMLM_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *avg_us = ms * 1000.0f / (float)iters;
+        // weights, row scales, the input rows and outputs as f32, plus the
+        // residual rows read (the term planes, the norm partials and the
+        // gain are this implementation's operands, not the algorithm's)
+        const FkArgs f = makef(0);
+        const double nout = f.epi == FK_SILU ? f.N / 2.0 : (double)f.N;
+        *bytes_per_launch = (double)f.N * f.K + 4.0 * f.N + 4.0 * B * f.K + 4.0 * B * nout +
+                            (f.R ? 4.0 * B * f.N : 0.0);
+        return VMLM_OK;
+    }
     auto make = [&](size_t l) {
         switch (which) {
         case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H, d->ks_h);

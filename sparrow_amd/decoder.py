@@ -58,6 +58,15 @@ class Decoder:
         check(L.vmlm_decoder_load_globals(self._h, e.ctypes.data, m.ctypes.data, f.ctypes.data))
 
     # ------------------------------------------------------------ running
+    def set_fused(self, enable: bool) -> None:
+        """Fused five-launch layers (default at batch <= 5) or the k-slice
+        eight-launch program."""
+        check(lib().vmlm_decoder_set_fused(self._h, int(bool(enable))))
+
+    @property
+    def fused(self) -> bool:
+        return bool(lib().vmlm_decoder_fused(self._h))
+
     def set_graph(self, enable: bool) -> None:
         check(lib().vmlm_decoder_set_graph(self._h, int(bool(enable))))
 

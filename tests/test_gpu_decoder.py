@@ -47,6 +47,49 @@ def test_tiny_generate_matches_oracle(hip, oracle, tiny):
         assert np.array_equal(got, chain)
 
 
+@pytest.mark.parametrize("batch", [1, 3, 5])
+def test_tiny_fused_matches_kslice_and_oracle(hip, oracle, tiny, batch):
+    """The fused five-launch layer (default at batch <= 5) against the
+    k-slice eight-launch program and the oracle: logits within 1e-4 of
+    their RMS, identical greedy chains."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = tiny
+    prompts = M.make_prompts(cfg, batch, 13, seed=21)
+    out = {}
+    for fused in (True, False):
+        with Decoder(cfg, batch=batch, cap=64) as dec:
+            assert dec.fused  # the default at this batch
+            dec.load(W)
+            dec.set_fused(fused)
+            assert dec.fused == fused
+            t0, _ = dec.prefill(prompts)
+            toks, last = dec.decode(16, want_logits=True)
+        out[fused] = (np.concatenate([t0[None, :], toks], 0), last)
+    assert np.array_equal(out[True][0], out[False][0])
+    for b in range(batch):
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        chain, _ = ref.generate(prompts[b], 16)
+        assert np.array_equal(out[True][0][:, b], chain)
+        # the oracle's logits of the last step: prefill, then 16 steps fed
+        # with the chain's tokens
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        ref.prefill(prompts[b])
+        for i in range(16):
+            lr, _ = ref.step(chain[i], 13 + i)
+        assert np.abs(out[True][1][b] - lr).max() <= 1e-4 * rms(lr)
+        assert np.abs(out[False][1][b] - lr).max() <= 1e-4 * rms(lr)
+
+
+def test_fused_guard(hip, tiny):
+    from sparrow_amd import VmlmError
+    from sparrow_amd.decoder import Decoder
+    cfg, W = tiny
+    with Decoder(cfg, batch=6, cap=64) as dec:
+        assert not dec.fused
+        with pytest.raises(VmlmError):
+            dec.set_fused(True)
+
+
 def test_tiny_graph_equals_eager(hip, tiny):
     from sparrow_amd.decoder import Decoder
     cfg, W = tiny
