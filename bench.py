@@ -49,7 +49,10 @@ def measured_traffic():
 def gemv_roofline(dec, iters):
     """q8 GEMV (the int8 projections of a decode step): mean launch duration
     per shape from HIP events on the session stream, and the step-mix
-    achieved bandwidth = sum(bytes) / sum(time) over one launch of each."""
+    achieved bandwidth = sum(bytes) / sum(time) over one launch of each.
+    At batch 16 these are the k-slice kernels (gemv_wide_kernel); at batch
+    <= 5 the fused full-K kernels (fk_gemv_kernel, with their RMSNorm,
+    residual and SiLU work)."""
     per = {}
     tot_b = tot_t = 0.0
     for which, name in ((0, "qkv"), (1, "o"), (2, "gate_up"), (3, "down")):
@@ -64,9 +67,11 @@ def gemv_roofline(dec, iters):
     achieved = tot_b / tot_t / 1e3  # GB/s
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
-            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
-            "kernel": "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)",
+            "traffic": measured_traffic() if not dec.fused else None,
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if not dec.fused else None,
+            "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues)"
+                       if dec.fused else
+                       "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "per_shape": per}
 
@@ -447,9 +452,11 @@ def main():
     dec.close()
 
     if args.batch == 1:
-        wall1 = wall
+        wall1, roof1 = wall, roof
     else:
         dec1, wall1, _, _, _ = run_decode(cfg, W, 1, args.steps, args.warmup)
+        roof1 = gemv_roofline(dec1, args.gemv_iters)
+        log(f"batch 1 q8 GEMV: {roof1['achieved']} GB/s ({roof1['frac'] * 100:.1f}% of peak)")
         dec1.close()
         log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
 
@@ -487,6 +494,7 @@ def main():
         },
         "batch1_tokens_per_s": round(args.steps / wall1, 2),
         "batch1_ms_per_step": round(wall1 / args.steps * 1e3, 4),
+        "batch1_roofline": roof1,
         "event_ms_per_step": round(ev_s / args.steps * 1e3, 4),
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -116,8 +116,11 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
     // planes (row (tt, b), k = kb*64 + 8g .. +7 and kb*64 + 32 + 8g .. +7),
     // the weight blocks of its k-run for each tile, the norm partials, the
     // epilogue's scales and residual
+    // Only the live lanes load (address work scales with the active lanes);
+    // the other columns of the MFMA hold whatever the registers held and are
+    // never read: each output column depends on its own B column only.
     u32x4 av[KB][2];
-    {
+    if (live) {
         const uint16_t *ar = p.A + ((size_t)tt * M + b) * p.lda + 8 * g;
 #pragma unroll
         for (int i = 0; i < KB; ++i) {
@@ -193,17 +196,12 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
         if (kb0 + i < nkb) {
-            u32x4 b0 = u32x4{0u, 0u, 0u, 0u}, b1 = b0;
-            if (live) {
-                b0 = av[i][0];
-                b1 = av[i][1];
-            }
 #pragma unroll
             for (int t = 0; t < TPW; ++t) {
                 u32x4 a0, a1;
                 i8x16_to_bf16(wr[t][i], a0, a1);
-                acc[t] = mfma16(a0, b0, acc[t]);
-                acc[t] = mfma16(a1, b1, acc[t]);
+                acc[t] = mfma16(a0, av[i][0], acc[t]);
+                acc[t] = mfma16(a1, av[i][1], acc[t]);
             }
         }
     }
