@@ -30,14 +30,15 @@ def log(msg):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wide_decode_minicpm2b_traffic.md")
+TRAFFIC_PROFILE_FUSED = os.path.join(ROOT, "profiles", "fk_gemv_decode_minicpm2b_b1_traffic.md")
 
 
-def measured_traffic():
+def measured_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per launch of the decode GEMV from the committed counter
     summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
     a plain copy's reading; the command is in the file), or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch_mean:"):
                     return int(line.split(":")[1])
@@ -67,8 +68,9 @@ def gemv_roofline(dec, iters):
     achieved = tot_b / tot_t / 1e3  # GB/s
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic() if not dec.fused else None,
-            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if not dec.fused else None,
+            "traffic": measured_traffic(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE),
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE,
+                                              ROOT),
             "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues)"
                        if dec.fused else
                        "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)"),
@@ -381,7 +383,8 @@ def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
 def traffic_probe(iters):
     """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` runs: a plain device copy
     of 256 MiB (the calibration: its bytes are known) three times, then the
-    four decode GEMV shapes of the batch-16 session `iters` times each."""
+    four decode GEMV shapes of the batch-16 session and of the batch-1 session
+    `iters` times each (after a warm-up pass over the 40 layers)."""
     import ctypes as C
     from sparrow_amd import check, lib
     from sparrow_amd import model as M
@@ -398,12 +401,13 @@ def traffic_probe(iters):
     check(L.vmlm_hip_free(b))
     cfg = M.minicpm_2b_config()
     W = M.make_weights(cfg, seed=3, threads=16)
-    dec = Decoder(cfg, batch=16, cap=1024)
-    dec.load(W)
-    dec.prefill(M.make_prompts(cfg, 16, 128, seed=3))
-    for which in range(4):
-        dec.time_gemv(which, iters)
-    dec.close()
+    for batch in (16, 1):  # the k-slice GEMVs (batch 16), then the fused ones (batch 1)
+        dec = Decoder(cfg, batch=batch, cap=1024)
+        dec.load(W)
+        dec.prefill(M.make_prompts(cfg, batch, 128, seed=3))
+        for which in range(4):
+            dec.time_gemv(which, iters)
+        dec.close()
     print(json.dumps({"probe": "traffic", "copy_bytes": nbytes, "gemv_iters": iters}))
 
 
