@@ -29,7 +29,7 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wide_decode_minicpm2b_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "ks_gemv_decode_minicpm2b_b16_traffic.md")
 TRAFFIC_PROFILE_FUSED = os.path.join(ROOT, "profiles", "fk_gemv_decode_minicpm2b_b1_traffic.md")
 
 
@@ -51,7 +51,7 @@ def gemv_roofline(dec, iters):
     """q8 GEMV (the int8 projections of a decode step): mean launch duration
     per shape from HIP events on the session stream, and the step-mix
     achieved bandwidth = sum(bytes) / sum(time) over one launch of each.
-    At batch 16 these are the k-slice kernels (gemv_wide_kernel); at batch
+    At batch 16 these are the k-slice kernels (ks_gemv_kernel); at batch
     <= 5 the fused full-K kernels (fk_gemv_kernel, with their RMSNorm,
     residual and SiLU work)."""
     per = {}
@@ -73,7 +73,7 @@ def gemv_roofline(dec, iters):
                                               ROOT),
             "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues)"
                        if dec.fused else
-                       "gemv_wide_kernel<T=3> (q/k/v, o, gate+up, down; k-split partials)"),
+                       "ks_gemv_kernel (q/k/v, o, gate+up, down; k-slice partials)"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "per_shape": per}
 

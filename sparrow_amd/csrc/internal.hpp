@@ -101,6 +101,21 @@ int launch_fk_gemv(const FkArgs &a, hipStream_t st);
 // and the partial sums of squares [N/16][M].
 int launch_fk_norm_prep(const float *h, int ldh, const float *g, int M, int N, uint16_t *terms,
                         int ldt, float *ssp, hipStream_t st);
+// k-slice GEMV for decode batches up to 16 over the swizzled weights: raw
+// slice sums Y[ks][M][ldy] of A [3][M][lda] (bf16 term planes) . W^T, with
+// ks = ks_gemv_slices(K) slices of K / ks; the consumer reduces the slices
+// in order and applies the row scales.
+struct KsArgs {
+    const int8_t *W = nullptr;
+    const uint16_t *A = nullptr;
+    int lda = 0;
+    float *Y = nullptr;
+    int ldy = 0;
+    int M = 1, N = 0, K = 0;
+    int tw = 0, nwv = 0;  // tiles per wave, waves per workgroup; 0 = 2, 4
+};
+int ks_gemv_slices(int K);
+int launch_ks_gemv(const KsArgs &a, hipStream_t st);
 // int8 [N][K] row-major -> [N/16][K/64][64 lanes][16 B] MFMA-operand order.
 int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
 

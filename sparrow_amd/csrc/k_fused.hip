@@ -251,6 +251,116 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
     }
 }
 
+// k-slice GEMV for decode batches of 6..16 rows, over the swizzled weights.
+// Workgroup (row group, k-slice): NWV waves each own TW 16-row tiles over the
+// slice's KB 64-wide blocks. The slice of the three term planes
+// ([3][16 tokens][KB*64] bf16, rows past M repeat row 0) is staged once in
+// LDS; each wave reads a B fragment once per block and term and uses it for
+// all TW tiles. Output: raw slice sums Y[ks][M][ldy] (no scale), reduced in
+// slice order by the consumer (attention, residual RMSNorm, SiLU).
+struct KsParams {
+    const uint8_t *W;   // swizzled [N/16][K/64][64][16]
+    const uint16_t *A;  // [3][M][lda]
+    int lda;
+    float *Y;
+    int ldy;
+    int M, N, K;
+};
+
+template <int KB, int TW, int NWV>
+__global__ __launch_bounds__(NWV * 64) void ks_gemv_kernel(KsParams p) {
+    constexpr int NTH = NWV * 64;
+    constexpr int KW = KB * 64;      // k of the slice
+    constexpr int ALD = KW + 8;      // padded LDS row (16 B): rows start on different banks
+    __shared__ __attribute__((aligned(16))) uint16_t as[FK_T][16][ALD];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int nkb = p.K >> 6;
+    const int kb0 = blockIdx.y * KB;
+    const int tile0 = (blockIdx.x * NWV + wave) * TW;
+
+    // 1. the activation slice (16-byte pieces, all issued before anything waits)
+    constexpr int PIECES = FK_T * 16 * (KW / 8);
+    constexpr int PER = (PIECES + NTH - 1) / NTH;
+    u32x4 ap[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        int e = tid + i * NTH;
+        e = e < PIECES ? e : PIECES - 1;
+        const int t = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+        const int rs = r < p.M ? r : 0;
+        ap[i] = *(const u32x4 *)(p.A + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c8 * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. this wave's weight blocks
+    u32x4 wr[TW][KB];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tl = tile0 + t < (p.N >> 4) ? tile0 + t : (p.N >> 4) - 1;
+        const uint8_t *wt = p.W + ((size_t)tl * nkb + kb0) * 1024 + lane * 16;
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+            wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = tid + i * NTH;
+        if (e < PIECES) {
+            const int t = e / (16 * (KW / 8)), r = (e / (KW / 8)) % 16, c8 = e % (KW / 8);
+            *(u32x4 *)&as[t][r][c8 * 8] = ap[i];
+        }
+    }
+    __syncthreads();
+
+    // 3. per block: the B fragments of the three terms (lane (g, n): token n,
+    // k = 8g .. +7 and 32 + 8g .. +7), then 2 x 3 MFMAs per tile
+    f32x4 acc[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+        u32x4 b[FK_T][2];
+#pragma unroll
+        for (int q = 0; q < FK_T; ++q) {
+            b[q][0] = *(const u32x4 *)&as[q][n][i * 64 + 8 * g];
+            b[q][1] = *(const u32x4 *)&as[q][n][i * 64 + 32 + 8 * g];
+        }
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            u32x4 a0, a1;
+            i8x16_to_bf16(wr[t][i], a0, a1);
+#pragma unroll
+            for (int q = 0; q < FK_T; ++q) {
+                acc[t] = mfma16(a0, b[q][0], acc[t]);
+                acc[t] = mfma16(a1, b[q][1], acc[t]);
+            }
+        }
+    }
+    // 4. D[row 4g + i][token n]: rows 4g .. 4g + 3 of the tile are 16 contiguous
+    // bytes of the token's partial row
+    if (n < p.M) {
+        float *yr = p.Y + ((size_t)blockIdx.y * p.M + n) * p.ldy;
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const int tl = tile0 + t;
+            if (tl < (p.N >> 4))
+                *(f32x4 *)(yr + tl * 16 + 4 * g) = acc[t];
+        }
+    }
+}
+
+template <int KB, int TW, int NWV>
+int launch_ks_t(const KsParams &p, int ks, hipStream_t st) {
+    const int rows = 16 * TW * NWV;
+    const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ks);
+    ks_gemv_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 // (N, K) int8 row-major -> swizzled blocks (see the header comment). One
 // thread per 16-byte lane of a block.
 __global__ void swizzle_w_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
@@ -387,6 +497,44 @@ int launch_fk_norm_prep(const float *h, int ldh, const float *g, int M, int N, u
     fk_norm_prep_kernel<<<(unsigned)(N / 16), 64, 0, st>>>(h, ldh, g, M, N, terms, ldt, ssp);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
+}
+
+int ks_gemv_slices(int K) {
+    const int nkb = K / 64;
+    return nkb % 4 == 0 ? nkb / 4 : nkb % 6 == 0 ? nkb / 6 : nkb % 2 == 0 ? nkb / 2 : nkb;
+}
+
+int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
+    VMLM_GUARD(a.M >= 1 && a.M <= 16 && a.K % 64 == 0 && a.K >= 64 && a.N % 16 == 0 && a.N >= 16,
+               "k-slice GEMV: shape M=%d N=%d K=%d unsupported", a.M, a.N, a.K);
+    VMLM_GUARD(a.A && a.lda % 8 == 0 && ((uintptr_t)a.A & 15) == 0 && a.Y && a.ldy % 4 == 0 &&
+                   ((uintptr_t)a.Y & 15) == 0,
+               "k-slice GEMV: term planes and partial rows must be 16-byte aligned");
+    KsParams p;
+    p.W = (const uint8_t *)a.W;
+    p.A = a.A;
+    p.lda = a.lda;
+    p.Y = a.Y;
+    p.ldy = a.ldy;
+    p.M = a.M;
+    p.N = a.N;
+    p.K = a.K;
+    const int nkb = a.K / 64, ks = ks_gemv_slices(a.K), kb = nkb / ks;
+    const int tw = a.tw ? a.tw : 2, nwv = a.nwv ? a.nwv : 4;
+#define KS_CASE(KBV)                                                                  \
+    if (kb == KBV) {                                                                  \
+        if (tw == 1 && nwv == 8) return launch_ks_t<KBV, 1, 8>(p, ks, st);            \
+        if (tw == 2 && nwv == 8) return launch_ks_t<KBV, 2, 8>(p, ks, st);            \
+        if (tw == 4 && nwv == 2) return launch_ks_t<KBV, 4, 2>(p, ks, st);            \
+        if (tw == 4 && nwv == 4) return launch_ks_t<KBV, 4, 4>(p, ks, st);            \
+        return launch_ks_t<KBV, 2, 4>(p, ks, st);                                     \
+    }
+    KS_CASE(1)
+    KS_CASE(2)
+    KS_CASE(4)
+    KS_CASE(6)
+#undef KS_CASE
+    return fail(VMLM_ERR_GUARD, "k-slice GEMV: K=%d", a.K);
 }
 
 int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st) {

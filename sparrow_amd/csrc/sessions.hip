@@ -98,7 +98,7 @@ struct vmlm_decoder {
     size_t H = 0, I = 0, NH = 0, V = 0, B = 0, cap = 0, L = 0;
     size_t w_layer = 0, s_layer = 0;  // per-layer element counts
     int8_t *w = nullptr;
-    int8_t *wsw = nullptr;  // the same weights in MFMA-operand order (fused path)
+    int8_t *wsw = nullptr;  // the same weights in MFMA-operand order (decode GEMVs)
     float *ssp = nullptr;   // fused path: RMSNorm partial sums of squares [H/16][B]
     bool fused = false;     // five-launch layers of full-K fused GEMVs (batch <= 5)
     float *s = nullptr, *norms = nullptr;
@@ -175,24 +175,19 @@ int enqueue_head(vmlm_decoder *d, bool record) {
     return VMLM_OK;
 }
 
-// Decode GEMV of the step: the wide kernel (8 tiles of 16 rows per
-// workgroup, activation slice shared through LDS) over k-slices, raw slice
-// sums to d->part; the consumer (attention, residual RMSNorm, SiLU) reduces
-// them in slice order and applies the row scales.
-GemvArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int K, int ks) {
-    GemvArgs g;
-    g.W = W;
+// Decode GEMV of the step (k-slice program): raw slice sums to d->part from
+// the swizzled weights; the consumer (attention, residual RMSNorm, SiLU)
+// reduces them in slice order and applies the row scales.
+KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int K) {
+    KsArgs g;
+    g.W = d->Sw(W);
     g.A = A;
-    g.T = 3;
     g.lda = K;
     g.M = (int)d->B;
     g.N = N;
     g.K = K;
     g.Y = d->part;
     g.ldy = N;
-    g.epi = EPI_PARTIAL;
-    g.tiles = 8;
-    g.ksplit = ks;
     return g;
 }
 
@@ -207,7 +202,7 @@ int enqueue_step(vmlm_decoder *d) {
     if ((rc = launch_rmsnorm(nullptr, d->h, d->InLn(0), B, H, d->c.eps, d->t_x, T, H, st)))
         return rc;
     for (size_t l = 0; l < d->L; ++l) {
-        if ((rc = launch_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H, d->ks_h), st))) return rc;
+        if ((rc = launch_ks_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H), st))) return rc;
         DecodeArgs a;
         a.q = a.k_new = a.v_new = nullptr;
         a.ldq = 3 * H;
@@ -224,14 +219,14 @@ int enqueue_step(vmlm_decoder *d) {
         a.ldp = 3 * H;
         a.wscale = d->Sqkv(l);
         if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
-        if ((rc = launch_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H, d->ks_h), st))) return rc;
+        if ((rc = launch_ks_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H), st))) return rc;
         if ((rc = launch_rmsnorm_resid(d->h, d->part, d->ks_h, H, d->So(l), d->h2, B, H,
                                        d->PostLn(l), d->c.eps, d->t_x, T, H, st)))
             return rc;
-        if ((rc = launch_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H, d->ks_h), st))) return rc;
+        if ((rc = launch_ks_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H), st))) return rc;
         if ((rc = launch_silu_reduce(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->t_act, T, st)))
             return rc;
-        if ((rc = launch_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I, d->ks_i), st))) return rc;
+        if ((rc = launch_ks_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I), st))) return rc;
         const float *g_next = l + 1 < d->L ? d->InLn(l + 1) : d->final_norm;
         if ((rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H, g_next,
                                        d->c.eps, d->t_x, T, H, st)))
@@ -377,16 +372,11 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     d->w_layer = 4 * d->H * d->H + 3 * d->I * d->H;
     d->s_layer = 5 * d->H + 2 * d->I;
     d->rope_step = -2.0f / 64.0f * host_ln_f(c.theta);
-    // k-slices: 2 chunks (256 k) per slice for K = hidden, 3 for K = inter,
-    // else the largest of 3, 2, 1 chunks that divides the chunk count
-    auto pick_ks = [](size_t K, int want) {
-        const int nch = (int)(K / 128);
-        for (int nc = want; nc > 1; --nc)
-            if (nch % nc == 0) return nch / nc;
-        return nch;
-    };
-    d->ks_h = pick_ks(d->H, 2);
-    d->ks_i = pick_ks(d->I, 3);
+    // k-slices of the K = hidden and K = inter projections (k-slice program)
+    d->ks_h = ks_gemv_slices((int)d->H);
+    d->ks_i = ks_gemv_slices((int)d->I);
+    VMLM_GUARD(d->ks_h <= 16 && d->ks_i <= 16, "decoder: hidden %u / inter %u need over 16 k-slices",
+               c.hidden, c.inter);
     d->fused = fused_ok(d);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
@@ -400,7 +390,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->norms, d->L * 2 * d->H)) || (rc = dalloc(d, &d->embed, d->V * d->H)) ||
         (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
-        (d->fused && (rc = dalloc(d, &d->wsw, d->L * d->w_layer))) ||
+        (rc = dalloc(d, &d->wsw, d->L * d->w_layer)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
@@ -464,7 +454,7 @@ int vmlm_decoder_load_layer(vmlm_decoder *d, uint32_t layer, const int8_t *wq, c
                               hipMemcpyHostToDevice, st)) != hipSuccess)
         return hip_fail(e, "load_layer gate/up");
     H2D(Wgu + 2 * I * H, wd, H * I);
-    if (d->wsw) {  // the fused path's copy in MFMA-operand order
+    {  // the decode GEMVs' copy in MFMA-operand order
         int rc;
         if ((rc = launch_swizzle_w(W, d->wsw + l * d->w_layer, (int)(3 * H), (int)H, st)) ||
             (rc = launch_swizzle_w(W + 3 * H * H, d->wsw + l * d->w_layer + 3 * H * H, (int)H,
@@ -687,7 +677,7 @@ void *vmlm_decoder_stream(vmlm_decoder *d) { return d ? (void *)d->st : nullptr;
 
 int vmlm_decoder_set_fused(vmlm_decoder *d, int enable) {
     VMLM_GUARD(d, "decoder: null");
-    VMLM_GUARD(!enable || d->wsw, "decoder: the fused layer needs a batch of at most 5");
+    VMLM_GUARD(!enable || fused_ok(d), "decoder: the fused layer needs a batch of at most 5");
     if (d->fused != (enable != 0)) {
         if (d->graph) {
             VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
@@ -707,57 +697,32 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     if (rc) return rc;
     VMLM_GUARD(which >= 0 && which <= 4 && iters >= 1, "time_gemv: which 0..4, iters >= 1");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
-    // the launches of the decode step (k-split wide GEMVs; LM head bf16)
-    // the fused path's launches: the full-K kernels with their row ops
-    if (d->fused && which < 4) {
-        auto makef = [&](size_t l) { return fk_args(d, l, which); };
-        hipEvent_t e0, e1;
-        VMLM_HIP_CHECK(hipEventCreate(&e0));
-        VMLM_HIP_CHECK(hipEventCreate(&e1));
-        for (size_t l = 0; l < d->L; ++l)
-            if ((rc = launch_fk_gemv(makef(l), d->st))) return rc;
-        VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
-        for (uint32_t i = 0; i < iters; ++i)
-            if ((rc = launch_fk_gemv(makef(i % d->L), d->st))) return rc;
-        VMLM_HIP_CHECK(hipEventRecord(e1, d->st));
-        VMLM_HIP_CHECK(hipEventSynchronize(e1));
-        float ms = 0.0f;
-        VMLM_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
-        *avg_us = ms * 1000.0f / (float)iters;
-        // weights, row scales, the input rows and outputs as f32, plus the
-        // residual rows read (the term planes, the norm partials and the
-        // gain are this implementation's operands, not the algorithm's)
-        const FkArgs f = makef(0);
-        const double nout = f.epi == FK_SILU ? f.N / 2.0 : (double)f.N;
-        *bytes_per_launch = (double)f.N * f.K + 4.0 * f.N + 4.0 * B * f.K + 4.0 * B * nout +
-                            (f.R ? 4.0 * B * f.N : 0.0);
-        return VMLM_OK;
-    }
+    // the launches of the decode step: the k-slice GEMVs, or the LM head (bf16)
+    auto make_lm = [&]() {
+        GemvArgs g;
+        g.T = 3;
+        g.M = B;
+        g.lda = H;
+        g.K = H;
+        g.A = d->t_x;
+        g.W = d->lm_head;
+        g.w_int8 = false;
+        g.N = (int)d->V;
+        g.Y = d->logits;
+        g.ldy = (int)d->V;
+        g.tiles = 9;
+        return g;
+    };
     auto make = [&](size_t l) {
         switch (which) {
-        case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H, d->ks_h);
-        case 1: return step_gemv(d, d->Wo(l), d->t_att, H, H, d->ks_h);
-        case 2: return step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H, d->ks_h);
-        case 3: return step_gemv(d, d->Wd(l), d->t_act, H, I, d->ks_i);
-        default: {
-            GemvArgs g;
-            g.T = 3;
-            g.M = B;
-            g.lda = H;
-            g.K = H;
-            g.A = d->t_x;
-            g.W = d->lm_head;
-            g.w_int8 = false;
-            g.N = (int)d->V;
-            g.Y = d->logits;
-            g.ldy = (int)d->V;
-            g.tiles = 9;
-            return g;
-        }
+        case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H);
+        case 1: return step_gemv(d, d->Wo(l), d->t_att, H, H);
+        case 2: return step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H);
+        default: return step_gemv(d, d->Wd(l), d->t_act, H, I);
         }
     };
+    auto launch = [&](size_t l) { return which == 4 ? launch_gemv(make_lm(), d->st)
+                                                    : launch_ks_gemv(make(l), d->st); };
     // one event pair around `iters` back-to-back launches (the mean launch
     // duration, launch gaps included); successive launches walk the layers
     // so that no weight is re-read from cache
@@ -765,10 +730,10 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     VMLM_HIP_CHECK(hipEventCreate(&e0));
     VMLM_HIP_CHECK(hipEventCreate(&e1));
     for (size_t l = 0; l < (which == 4 ? 1 : d->L); ++l)  // warm-up pass over every layer
-        if ((rc = launch_gemv(make(l), d->st))) return rc;
+        if ((rc = launch(l))) return rc;
     VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
     for (uint32_t i = 0; i < iters; ++i)
-        if ((rc = launch_gemv(make(which == 4 ? 0 : i % d->L), d->st))) return rc;
+        if ((rc = launch(which == 4 ? 0 : i % d->L))) return rc;
     VMLM_HIP_CHECK(hipEventRecord(e1, d->st));
     VMLM_HIP_CHECK(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -779,12 +744,10 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     // algorithmic bytes of the projection: weights, row scales (int8), the
     // f32 activation in and the f32 result out (the partial sums and the
     // bf16 term planes are this implementation's, not the algorithm's)
-    GemvArgs g = make(0);
-    const double wbytes = (double)g.N * g.K * (g.w_int8 ? 1 : 2);
-    const double sbytes = g.w_int8 ? (double)g.N * 4 : 0.0;
-    const double xbytes = (double)B * g.K * 4;
-    const double ybytes = (double)B * g.N * 4;
-    *bytes_per_launch = wbytes + sbytes + xbytes + ybytes;
+    const bool i8 = which != 4;
+    const double n = i8 ? make(0).N : make_lm().N, k = i8 ? make(0).K : make_lm().K;
+    *bytes_per_launch = n * k * (i8 ? 1 : 2) + (i8 ? n * 4 : 0.0) + (double)B * k * 4 +
+                        (double)B * n * 4;
     return VMLM_OK;
 }
 

@@ -80,6 +80,29 @@ def test_tiny_fused_matches_kslice_and_oracle(hip, oracle, tiny, batch):
         assert np.abs(out[False][1][b] - lr).max() <= 1e-4 * rms(lr)
 
 
+def test_tiny_batch16_kslice_matches_oracle(hip, oracle, tiny):
+    """Batch 16 (the k-slice program): every sequence's chain equals the
+    oracle's, and the last step's logits are within 1e-4 of their RMS."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = tiny
+    prompts = M.make_prompts(cfg, 16, 7, seed=31)
+    with Decoder(cfg, batch=16, cap=64) as dec:
+        assert not dec.fused
+        dec.load(W)
+        t0, _ = dec.prefill(prompts)
+        toks, last = dec.decode(6, want_logits=True)
+    got = np.concatenate([t0[None, :], toks], 0)
+    for b in (0, 5, 15):
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        chain, _ = ref.generate(prompts[b], 6)
+        assert np.array_equal(got[:, b], chain)
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        ref.prefill(prompts[b])
+        for i in range(6):
+            lr, _ = ref.step(chain[i], 7 + i)
+        assert np.abs(last[b] - lr).max() <= 1e-4 * rms(lr)
+
+
 def test_fused_guard(hip, tiny):
     from sparrow_amd import VmlmError
     from sparrow_amd.decoder import Decoder
