@@ -71,6 +71,17 @@ int vmlm_hip_memset(void *dptr, int value, size_t bytes);
 int vmlm_hip_event_record(void *stream, int *event_id);
 int vmlm_hip_event_elapsed_ms(int start_id, int end_id, float *ms);
 int vmlm_hip_event_release_all(void);
+/* Stream capture of device-API calls into a HIP graph (for replaying a fixed
+ * sequence of ops without host launch cost). capture_end fails, with the
+ * capture discarded, when the captured work holds anything but kernel
+ * launches (a memset, a copy or an allocation), so only kernel-only
+ * sequences are ever replayed. The calls must have run once on the stream
+ * before (their workspace is then in place). (No reference counterpart: the
+ * reference dispatches each op from its interpreter loop.) */
+int vmlm_hip_capture_begin(void *stream);
+int vmlm_hip_capture_end(void *stream, void **graph);
+int vmlm_hip_graph_launch(void *graph, void *stream);
+int vmlm_hip_graph_destroy(void *graph);
 
 /* B1 connection block, field for field ops/src/conn.rs:8-53 SparseConnW
  * (the Rust struct is not repr(C); the FFI shim fills this one). The GPU

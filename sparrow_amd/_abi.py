@@ -41,6 +41,10 @@ SIGNATURES = {
     "vmlm_hip_event_record": (I, [P, C.POINTER(I)]),
     "vmlm_hip_event_elapsed_ms": (I, [I, I, C.POINTER(F)]),
     "vmlm_hip_event_release_all": (I, []),
+    "vmlm_hip_capture_begin": (I, [P]),
+    "vmlm_hip_capture_end": (I, [P, C.POINTER(P)]),
+    "vmlm_hip_graph_launch": (I, [P, P]),
+    "vmlm_hip_graph_destroy": (I, [P]),
     # layer 1
     "vmlm_gemm_nt_int8": (I, [P, P, P, P, SZ, SZ, SZ]),
     "vmlm_gemm_nt_bf16": (I, [P, P, P, SZ, SZ, SZ]),

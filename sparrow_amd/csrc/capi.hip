@@ -391,6 +391,52 @@ int vmlm_hip_event_release_all(void) {
     return VMLM_OK;
 }
 
+int vmlm_hip_capture_begin(void *stream) {
+    INIT_OR_RETURN();
+    VMLM_HIP_CHECK(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+    return VMLM_OK;
+}
+
+int vmlm_hip_capture_end(void *stream, void **graph) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(graph, "capture_end: null graph");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    VMLM_HIP_CHECK(hipStreamEndCapture(as_stream(stream), &g));
+    VMLM_GUARD(g, "capture_end: nothing captured");
+    size_t n = 0;
+    hipError_t e = hipGraphGetNodes(g, nullptr, &n);
+    std::vector<hipGraphNode_t> nodes(n);
+    if (e == hipSuccess && n) e = hipGraphGetNodes(g, nodes.data(), &n);
+    int rc = e == hipSuccess ? VMLM_OK : hip_fail(e, "hipGraphGetNodes");
+    for (size_t i = 0; rc == VMLM_OK && i < n; ++i) {
+        hipGraphNodeType t;
+        if ((e = hipGraphNodeGetType(nodes[i], &t)) != hipSuccess) rc = hip_fail(e, "node type");
+        else if (t != hipGraphNodeTypeKernel)
+            rc = fail(VMLM_ERR_UNIMPL, "capture_end: node %zu is not a kernel launch (type %d)",
+                      i, (int)t);
+    }
+    hipGraphExec_t x = nullptr;
+    if (rc == VMLM_OK && (e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0)) != hipSuccess)
+        rc = hip_fail(e, "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc == VMLM_OK) *graph = (void *)x;
+    return rc;
+}
+
+int vmlm_hip_graph_launch(void *graph, void *stream) {
+    INIT_OR_RETURN();
+    VMLM_GUARD(graph, "graph_launch: null graph");
+    VMLM_HIP_CHECK(hipGraphLaunch((hipGraphExec_t)graph, as_stream(stream)));
+    return VMLM_OK;
+}
+
+int vmlm_hip_graph_destroy(void *graph) {
+    INIT_OR_RETURN();
+    if (graph) VMLM_HIP_CHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return VMLM_OK;
+}
+
 int vmlm_hip_check_guards(void) {
     INIT_OR_RETURN();
     int v = 0;
