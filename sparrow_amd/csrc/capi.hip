@@ -652,7 +652,11 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
     a.pos = (int)pos;
     a.step = -2.0f / (float)head_dim * host_ln_f(theta);
     a.scale = scale;
-    return launch_attention_decode(a, 1, out, (int)(n_heads * head_dim), nullptr, 0, 0, st);
+    Stage stg(st);
+    const size_t wf = attention_decode_work_floats(a, 1);
+    float *work = wf ? stg.alloc<float>(wf) : nullptr;
+    STAGE_OK(stg);
+    return launch_attention_decode(a, 1, out, (int)(n_heads * head_dim), nullptr, 0, 0, st, work);
 }
 
 // ================================================================ layer 1

@@ -197,8 +197,13 @@ struct DecodeArgs {
     int ks = 0, ldp = 0;
     const float *wscale = nullptr;
 };
+// `work` (optional, attention_decode_work_floats() floats): with a host
+// position (posp null) and few (head, sequence) pairs, the cached positions
+// are split over several workgroups per pair and merged in order by a second
+// kernel.
+size_t attention_decode_work_floats(const DecodeArgs &a, int B);
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
-                            int T, int ldt, hipStream_t st);
+                            int T, int ldt, hipStream_t st, float *work = nullptr);
 
 // B1 gather forward over source-major activations.
 int launch_b1_forward(const float *w, const uint32_t *src, int n, int k0, const float *xt,

@@ -674,7 +674,7 @@ constexpr int PART_KS_MAX = 16;             // k-slices of partial q/k/v read up
 template <int AD_NW, bool PART>
 __global__ __launch_bounds__(AD_NW * 64) __attribute__((amdgpu_waves_per_eu(AD_NW == 4 ? 3 : 2)))
 void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int T, int ldt,
-                        int B) {
+                        int B, int cpp, float *ppart) {
     extern __shared__ float cpart[];  // [ceil(cap / 64)][AD_PART]
     __shared__ float qs[64], kn[64], vn[64];
     __shared__ float es[AD_NW][64];
@@ -688,6 +688,9 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     const int grp = lane >> 4, q = lane & 15;
     const int pos = a.posp ? *a.posp : a.pos;
     const int nch = (pos + 1 + 63) / 64;
+    // this workgroup's chunks [c0, c1): all, or partition blockIdx.z of cpp
+    const int c0 = cpp ? (int)blockIdx.z * cpp : 0;
+    const int c1 = cpp ? min(c0 + cpp, nch) : nch;
     const size_t head = ((size_t)b * a.H + h) * a.cap * 64;
 
     // Cache rows through buffer loads whose range ends at row `pos`: rows at
@@ -745,7 +748,9 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
         vnew = a.v_new[(size_t)b * a.ldq + h * 64 + lane];
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_chunk(wave);
+    // waves past the workgroup's last chunk load a chunk past `pos`: zeros,
+    // no memory access
+    load_chunk(c0 + wave < c1 ? c0 + wave : nch + wave);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PART) {  // slices summed in order, then the row scale
         float v = pv[0];
@@ -774,7 +779,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
         vn[lane] = vnew;
     }
     __syncthreads();
-    if (tid < 64) {  // append the new row (no wave reads row `pos` from the cache)
+    if (tid < 64 && blockIdx.z == 0) {  // append the new row (no wave reads row `pos` from the cache)
         a.kc[head + (size_t)pos * 64 + tid] = kn[tid];
         a.vc[head + (size_t)pos * 64 + tid] = vn[tid];
     }
@@ -785,8 +790,8 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     // 8 waves (few workgroups, long rows per wave): a wave's next chunk is
     // loaded while the current one is consumed; 4 waves: loaded at the top
     constexpr bool PIPE = AD_NW == 8;
-    for (int c = wave; c < nch; c += AD_NW) {
-        if (!PIPE && c != wave) load_chunk(c);
+    for (int c = c0 + wave; c < c1; c += AD_NW) {
+        if (!PIPE && c != c0 + wave) load_chunk(c);
         const int p0 = c * 64;
         // partial dots (4 dims per lane), then a transposing butterfly over
         // the 16 lanes of a group: lane (grp, q) ends with position
@@ -845,16 +850,25 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     __syncthreads();
     // each chunk's weight e^{m_c - M} once (into the chunk's spare slot),
     // then every output dim sums over the chunks in order
-    float M = cpart[0];
-    for (int c = 1; c < nch; ++c) M = fmaxf(M, cpart[c * AD_PART]);
-    for (int c = tid; c < nch; c += AD_NW * 64) cpart[c * AD_PART + 2] = exp_f(cpart[c * AD_PART] - M);
+    float M = cpart[c0 * AD_PART];
+    for (int c = c0 + 1; c < c1; ++c) M = fmaxf(M, cpart[c * AD_PART]);
+    for (int c = c0 + tid; c < c1; c += AD_NW * 64) cpart[c * AD_PART + 2] = exp_f(cpart[c * AD_PART] - M);
     __syncthreads();
     if (tid >= 64) return;
     float L = 0.0f, O = 0.0f;
-    for (int c = 0; c < nch; ++c) {
+    for (int c = c0; c < c1; ++c) {
         const float f = cpart[c * AD_PART + 2];
         L = __builtin_fmaf(cpart[c * AD_PART + 1], f, L);
         O = __builtin_fmaf(cpart[c * AD_PART + 4 + tid], f, O);
+    }
+    if (ppart) {  // partition partial (M, L, O[64]) for the merge kernel
+        float *pp = ppart + (((size_t)b * a.H + h) * gridDim.z + blockIdx.z) * AD_PART;
+        if (tid == 0) {
+            pp[0] = M;
+            pp[1] = L;
+        }
+        pp[4 + tid] = O;
+        return;
     }
     float y = O / L;
     const int col = h * 64 + tid;
@@ -868,8 +882,50 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     }
 }
 
+// Merges the P partition partials (M_p, L_p, O_p) of each (head, sequence)
+// in partition order: out = sum_p O_p e^{M_p - M} / sum_p L_p e^{M_p - M}.
+__global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float *__restrict__ ppart, int P,
+                                                               int H, float *out, int ldo,
+                                                               uint16_t *terms, int T, int ldt,
+                                                               int B) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const float *pp = ppart + ((size_t)b * H + h) * P * AD_PART;
+    float M = pp[0];
+    for (int p = 1; p < P; ++p) M = fmaxf(M, pp[p * AD_PART]);
+    float L = 0.0f, O = 0.0f;
+    for (int p = 0; p < P; ++p) {
+        const float f = exp_f(pp[p * AD_PART] - M);
+        L = __builtin_fmaf(pp[p * AD_PART + 1], f, L);
+        O = __builtin_fmaf(pp[p * AD_PART + 4 + d], f, O);
+    }
+    float y = O / L;
+    const int col = h * 64 + d;
+    out[(size_t)b * ldo + col] = y;
+    if (terms) {
+        for (int t = 0; t < T; ++t) {
+            const uint32_t hb = bf16_rne_bits(y);
+            y = y - bf16_bits_to_f32(hb);
+            terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
+        }
+    }
+}
+
+// Partitions of 4 chunks (one per wave) when the position is known on the
+// host, the (head, sequence) pairs are fewer than the CUs and the cache holds
+// at least 8 chunks; else 0 (one workgroup per pair).
+static int decode_partitions(const DecodeArgs &a, int B) {
+    if (a.posp || a.part || a.H * B >= 256) return 0;
+    const int nch = (a.pos + 1 + 63) / 64;
+    return nch >= 8 ? (nch + 3) / 4 : 0;
+}
+
+size_t attention_decode_work_floats(const DecodeArgs &a, int B) {
+    const int P = decode_partitions(a, B);
+    return P ? (size_t)B * a.H * P * AD_PART : 0;
+}
+
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
-                            int T, int ldt, hipStream_t st) {
+                            int T, int ldt, hipStream_t st, float *work) {
     VMLM_GUARD(a.cap >= 1 && a.H >= 1 && B >= 1, "attention decode: empty shape");
     const size_t lds = (size_t)((a.cap + 63) / 64) * AD_PART * sizeof(float);
     VMLM_GUARD(lds <= 96 * 1024, "attention decode: cache capacity %d beyond %d positions",
@@ -877,17 +933,31 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
     VMLM_GUARD((size_t)a.cap * 256 <= 0x7fffffffu, "attention decode: cache row range too large");
     VMLM_GUARD(!a.part || (a.ks >= 1 && a.ks <= PART_KS_MAX && a.wscale && a.ldp >= 3 * a.H * 64),
                "attention decode: partial q/k/v need ks, ldp and scales");
+    const int P = work ? decode_partitions(a, B) : 0;
+    if (P > 1) {
+        attn_decode_kernel<4, false><<<dim3(a.H, B, P), 4 * 64, lds, st>>>(a, out, ldo, terms, T,
+                                                                            ldt, B, 4, work);
+        VMLM_HIP_CHECK(hipGetLastError());
+        attn_decode_merge_kernel<<<dim3(a.H, B), 64, 0, st>>>(work, P, a.H, out, ldo, terms, T,
+                                                              ldt, B);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     const dim3 grid(a.H, B);
     if (a.H * B < 256) {
         if (a.part)
-            attn_decode_kernel<8, true><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+            attn_decode_kernel<8, true><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B, 0,
+                                                                   nullptr);
         else
-            attn_decode_kernel<8, false><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+            attn_decode_kernel<8, false><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B,
+                                                                    0, nullptr);
     } else {
         if (a.part)
-            attn_decode_kernel<4, true><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+            attn_decode_kernel<4, true><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B, 0,
+                                                                   nullptr);
         else
-            attn_decode_kernel<4, false><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B);
+            attn_decode_kernel<4, false><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B,
+                                                                    0, nullptr);
     }
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;

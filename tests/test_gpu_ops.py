@@ -333,11 +333,14 @@ def test_attention_prefill(ops, oracle, S, H):
     assert np.array_equal(got[0], v[0]) or np.abs(got[0] - v[0]).max() <= 1e-6
 
 
-def test_attention_decode_cfg2(ops, oracle):
-    """Config 2 decode: 1 query against a KV cache of length 1024."""
+@pytest.mark.parametrize("H,pos", [(36, 1023), (36, 700), (4, 511), (36, 300)])
+def test_attention_decode_cfg2(ops, oracle, H, pos):
+    """Config 2 decode: 1 query against a KV cache of length 1024 (pos 1023),
+    and shorter caches: split over partitions of 4 chunks merged in order
+    (pos 1023, 700, 511: a partial last partition at 700) or one workgroup
+    per head (pos 300, under 8 chunks)."""
     rng = np.random.default_rng(2)
-    H, hd, cap = 36, 64, 1024
-    pos = cap - 1
+    hd, cap = 64, 1024
     kc = np.zeros((H, cap, hd), np.float32)
     vc = np.zeros((H, cap, hd), np.float32)
     kraw = rng.standard_normal((pos, H * hd), dtype=np.float32)
