@@ -354,3 +354,62 @@ def test_attention_decode_cfg2(ops, oracle, H, pos):
     assert_close_rms(got, ref)
     assert np.array_equal(bits(kc[:, pos]), bits(kc2[:, pos]))  # appended rotated k, bitwise
     assert np.array_equal(vc[:, pos], vc2[:, pos])
+
+
+def test_graph_capture_replay(hip, oracle):
+    """Device-API ops captured into a HIP graph (vmlm_hip_capture_begin/end)
+    and replayed three times, with eager work and synchronisations between
+    the replays: every replay equals the eager result bitwise. A capture that
+    records a memset (gemm_nt with k = 0 clears C) is refused and the stream
+    stays usable."""
+    import ctypes as C
+    rng = np.random.default_rng(7)
+    rows, cols = 37, 1024
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    g = (rng.standard_normal(cols, dtype=np.float32) * 0.5 + 1).astype(np.float32)
+    nb = x.nbytes
+    bufs = {}
+    for name, size in (("x", nb), ("g", g.nbytes), ("y", nb), ("z", nb), ("w", nb)):
+        p = C.c_void_p()
+        assert hip.vmlm_hip_malloc(C.byref(p), size) == 0
+        bufs[name] = p
+    dx, dg, dy, dz, dw = (bufs[k] for k in ("x", "g", "y", "z", "w"))
+
+    def down(dev):
+        out = np.empty((rows, cols), np.float32)
+        assert hip.vmlm_hip_sync() == 0
+        assert hip.vmlm_hip_memcpy_d2h(out.ctypes.data, dev, out.nbytes) == 0
+        return out
+
+    def seq():  # y = rmsnorm(x) * g; z = y + x
+        return (hip.vmlm_hip_rmsnorm(dy, dx, dg, rows, cols, C.c_float(1e-5), None) or
+                hip.vmlm_hip_ew_op(dz, dy, dx, rows * cols, 20, None))
+
+    graph = C.c_void_p()
+    try:
+        assert hip.vmlm_hip_memcpy_h2d(dx, x.ctypes.data, nb) == 0
+        assert hip.vmlm_hip_memcpy_h2d(dg, g.ctypes.data, g.nbytes) == 0
+        assert seq() == 0
+        want = down(dz)
+        assert_close_rms(want, oracle.ew_op(oracle.rmsnorm(x, g, 1e-5), x, 20))
+        assert hip.vmlm_hip_capture_begin(None) == 0
+        assert seq() == 0
+        assert hip.vmlm_hip_capture_end(None, C.byref(graph)) == 0 and graph.value
+        for r in range(3):
+            assert hip.vmlm_hip_memset(dz, 0xFF, nb) == 0  # garbage the result
+            assert hip.vmlm_hip_memset(dy, 0xFF, nb) == 0
+            assert hip.vmlm_hip_scale(dw, dx, rows * cols, C.c_float(0.5), None) == 0  # eager work
+            assert hip.vmlm_hip_sync() == 0
+            assert hip.vmlm_hip_graph_launch(graph, None) == 0
+            assert np.array_equal(bits(down(dz)), bits(want)), r
+        # a captured memset is refused
+        assert hip.vmlm_hip_capture_begin(None) == 0
+        hip.vmlm_hip_gemm_nt(dx, dx, dw, 4, 4, 0, False, None)
+        bad = C.c_void_p()
+        assert hip.vmlm_hip_capture_end(None, C.byref(bad)) != 0 and not bad.value
+        assert seq() == 0
+        assert np.array_equal(bits(down(dz)), bits(want))
+    finally:
+        hip.vmlm_hip_graph_destroy(graph)
+        for p in bufs.values():
+            hip.vmlm_hip_free(p)
