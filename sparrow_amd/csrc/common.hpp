@@ -101,6 +101,40 @@ __device__ __forceinline__ void i8x16_to_bf16(u32x4 w, u32x4 &lo, u32x4 &hi) {
     hi = u32x4{d[4], d[5], d[6], d[7]};
 }
 
+// ------------------------------------------------------------------ int8 rows
+// An f32 row y enters the int8 MFMA as four int8 terms with one power-of-two
+// scale 2^k per row: the largest k with m * 2^k <= 127, m = max|y| or a bound
+// on it within a few ulps. With u = y * 2^k (exact), a0 = rint(u), then each
+// further term is rint of the remainder times 128, so
+// u = a0 + a1/2^7 + a2/2^14 + a3/2^21 + e with |e| <= 2^-22: 28 bits below the
+// row maximum (f32 carries 24). |a0| <= 127, |a1..a3| <= 64; every step is
+// exact in f32. NaN gives 0 terms; a non-finite maximum gives the scale 1.
+constexpr int Q8_T = 4;
+__device__ __forceinline__ int q8_row_k(float mx) {
+    if (!(mx > 0.0f) || mx > 3.0e38f) return 0;
+    int k = 6 - ilogbf(mx);
+    if (mx * ldexpf(1.0f, k) > 127.0f) --k;
+    return k < -120 ? -120 : k > 120 ? 120 : k;
+}
+__device__ __forceinline__ void q8_split(float y, int k, int (&a)[Q8_T]) {
+    float u = ldexpf(y, k);
+    if (!(u == u)) u = 0.0f;
+    // the scale keeps |u| <= 127 up to a few ulps of a bounding estimate;
+    // 127.25 still rounds to 127 and leaves the excess to the next term
+    u = fminf(fmaxf(u, -127.25f), 127.25f);
+#pragma unroll
+    for (int t = 0; t < Q8_T; ++t) {
+        const float r = rintf(u);
+        a[t] = (int)r;
+        u = (u - r) * 128.0f;
+    }
+}
+// packs the bytes of four ints (low bytes) into one dword
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
 // ------------------------------------------------------------------ math
 // Device ports of the reference's scalar math, operation for operation, so
 // that elementwise kernels are bitwise equal to the CPU kernels.

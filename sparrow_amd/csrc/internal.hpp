@@ -107,7 +107,9 @@ int launch_fk_norm_prep(const float *h, int ldh, const float *g, int M, int N, u
 // in order and applies the row scales.
 struct KsArgs {
     const int8_t *W = nullptr;
-    const uint16_t *A = nullptr;
+    const uint16_t *A = nullptr;  // bf16 term planes [3][M][lda], or
+    const int8_t *A8 = nullptr;   // int8 rows [Q8_T][M][lda] with factors a8s[M]
+    const float *a8s = nullptr;
     int lda = 0;
     float *Y = nullptr;
     int ldy = 0;
@@ -146,10 +148,16 @@ int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, si
                    float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st);
 // x = base + (sum of ks k-slice partials [ks][rows][ldp]) * scale -> resid;
 // RMSNorm(x) * g -> T bf16 terms [T][rows][cols].
+// With q8 (optional), also the int8 rows of the normalised values: Q8_T terms
+// [Q8_T][rows][cols] and the per-row factor q8s[row] = 2^-k (see q8_split).
+// terms may then be null.
 int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
                          const float *scale, float *resid, size_t rows, size_t cols,
                          const float *g, float eps, uint16_t *terms, int T, int ld_terms,
-                         hipStream_t st);
+                         hipStream_t st, int8_t *q8 = nullptr, float *q8s = nullptr);
+// RMSNorm of rows into int8 rows only (Q8_T terms and per-row factors).
+int launch_rmsnorm_q8(const float *src, const float *g, size_t rows, size_t cols, float eps,
+                      int8_t *q8, float *q8s, hipStream_t st);
 // SiLU(gate) * up from the partials of the interleaved gate/up projection.
 int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
                        uint16_t *terms, int T, hipStream_t st);

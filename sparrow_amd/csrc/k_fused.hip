@@ -260,12 +260,113 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
 // slice order by the consumer (attention, residual RMSNorm, SiLU).
 struct KsParams {
     const uint8_t *W;   // swizzled [N/16][K/64][64][16]
-    const uint16_t *A;  // [3][M][lda]
+    const uint16_t *A;  // [3][M][lda] bf16 term planes, or
+    const int8_t *A8;   // [Q8_T][M][lda] int8 rows with per-row factors a8s[M]
+    const float *a8s;
     int lda;
     float *Y;
     int ldy;
     int M, N, K;
 };
+
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+
+// The int8 form: the slice of the Q8_T int8 term planes is staged in LDS; per
+// block and term one v_mfma_i32_16x16x64_i8 per tile straight on the int8
+// weights (no conversion), accumulated exactly in int32 (|sum| < 2^24 over
+// a slice of at most 6 blocks). The epilogue forms
+// ((s0 + s1 / 2^7) + s2 / 2^14) + s3 / 2^21 in f32, times the row factor.
+// The swizzled weight bytes of lane (g, r) are k = 8g .. +7 and 32 + 8g .. +7
+// of the block; the B fragment of lane (g, n) takes the same k of token n,
+// so each product pairs matching k whatever order the MFMA sums them in.
+template <int KB, int TW, int NWV>
+__global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
+    constexpr int NTH = NWV * 64;
+    constexpr int KW = KB * 64;
+    constexpr int ALD = KW + 16;     // padded LDS row (bytes)
+    __shared__ __attribute__((aligned(16))) int8_t as8[Q8_T][16][ALD];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int nkb = p.K >> 6;
+    const int kb0 = blockIdx.y * KB;
+    const int tile0 = (blockIdx.x * NWV + wave) * TW;
+
+    constexpr int PIECES = Q8_T * 16 * (KW / 16);
+    constexpr int PER = (PIECES + NTH - 1) / NTH;
+    u32x4 ap[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        int e = tid + i * NTH;
+        e = e < PIECES ? e : PIECES - 1;
+        const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
+        const int rs = r < p.M ? r : 0;
+        ap[i] = *(const u32x4 *)(p.A8 + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c16 * 16);
+    }
+    const float rowf = p.a8s[n < p.M ? n : 0];
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wr[TW][KB];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tl = tile0 + t < (p.N >> 4) ? tile0 + t : (p.N >> 4) - 1;
+        const uint8_t *wt = p.W + ((size_t)tl * nkb + kb0) * 1024 + lane * 16;
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+            wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = tid + i * NTH;
+        if (e < PIECES) {
+            const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
+            *(u32x4 *)&as8[t][r][c16 * 16] = ap[i];
+        }
+    }
+    __syncthreads();
+
+    i32x4 acc[TW][Q8_T];
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q) acc[t][q] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+        i32x4 b[Q8_T];
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q) {
+            const uint2 lo = *(const uint2 *)&as8[q][n][i * 64 + 8 * g];
+            const uint2 hi = *(const uint2 *)&as8[q][n][i * 64 + 32 + 8 * g];
+            b[q] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        }
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const i32x4 a = __builtin_bit_cast(i32x4, wr[t][i]);
+#pragma unroll
+            for (int q = 0; q < Q8_T; ++q)
+                acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[q], acc[t][q], 0, 0, 0);
+        }
+    }
+    if (n < p.M) {
+        float *yr = p.Y + ((size_t)blockIdx.y * p.M + n) * p.ldy;
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const int tl = tile0 + t;
+            if (tl >= (p.N >> 4)) continue;
+            f32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float f = (float)acc[t][0][j];
+                f = f + (float)acc[t][1][j] * 0.0078125f;
+                f = f + (float)acc[t][2][j] * 6.103515625e-05f;
+                f = f + (float)acc[t][3][j] * 4.76837158203125e-07f;
+                v[j] = f * rowf;
+            }
+            *(f32x4 *)(yr + tl * 16 + 4 * g) = v;
+        }
+    }
+}
 
 template <int KB, int TW, int NWV>
 __global__ __launch_bounds__(NWV * 64) void ks_gemv_kernel(KsParams p) {
@@ -356,7 +457,10 @@ template <int KB, int TW, int NWV>
 int launch_ks_t(const KsParams &p, int ks, hipStream_t st) {
     const int rows = 16 * TW * NWV;
     const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ks);
-    ks_gemv_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
+    if (p.A8)
+        ks_gemv_i8_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
+    else
+        ks_gemv_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -507,12 +611,16 @@ int ks_gemv_slices(int K) {
 int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.M <= 16 && a.K % 64 == 0 && a.K >= 64 && a.N % 16 == 0 && a.N >= 16,
                "k-slice GEMV: shape M=%d N=%d K=%d unsupported", a.M, a.N, a.K);
-    VMLM_GUARD(a.A && a.lda % 8 == 0 && ((uintptr_t)a.A & 15) == 0 && a.Y && a.ldy % 4 == 0 &&
-                   ((uintptr_t)a.Y & 15) == 0,
-               "k-slice GEMV: term planes and partial rows must be 16-byte aligned");
+    VMLM_GUARD((a.A != nullptr) != (a.A8 != nullptr) && (!a.A8 || a.a8s),
+               "k-slice GEMV: bf16 term planes or int8 rows with their factors");
+    VMLM_GUARD(a.lda % 16 == 0 && ((uintptr_t)(a.A ? (const void *)a.A : (const void *)a.A8) & 15) == 0 &&
+                   a.Y && a.ldy % 4 == 0 && ((uintptr_t)a.Y & 15) == 0,
+               "k-slice GEMV: input rows and partial rows must be 16-byte aligned");
     KsParams p;
     p.W = (const uint8_t *)a.W;
     p.A = a.A;
+    p.A8 = a.A8;
+    p.a8s = a.a8s;
     p.lda = a.lda;
     p.Y = a.Y;
     p.ldy = a.ldy;

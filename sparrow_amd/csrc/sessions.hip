@@ -53,9 +53,11 @@ __global__ void step_advance_kernel(int *step, int *pos) {
     *pos = *pos + 1;
 }
 
-// Scatter rotated K / raw V of prefill rows [b*S + s][...] into the cache.
+// Scatter K rotated at its position s (the ROPE of the program, bit for bit)
+// and raw V of prefill rows [b*S + s][...] into the cache.
 __global__ void kv_fill_kernel(const float *__restrict__ qkv, int ldq, int H, int NH, int S,
-                               float *__restrict__ kc, float *__restrict__ vc, int cap, int B) {
+                               float *__restrict__ kc, float *__restrict__ vc, int cap, int B,
+                               float step) {
     size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t total = (size_t)B * S * NH * 64;
     if (idx >= total) return;
@@ -65,7 +67,10 @@ __global__ void kv_fill_kernel(const float *__restrict__ qkv, int ldq, int H, in
     const int b = idx / ((size_t)64 * NH * S);
     const float *row = qkv + ((size_t)b * S + s) * ldq;
     const size_t o = (((size_t)b * NH + h) * cap + s) * 64 + d;
-    kc[o] = row[H + h * 64 + d];
+    const int i = d & 31;
+    float y1, y2;
+    rope_pair(row[H + h * 64 + i], row[H + h * 64 + i + 32], (float)s, i, step, &y1, &y2);
+    kc[o] = d < 32 ? y1 : y2;
     vc[o] = row[2 * H + h * 64 + d];
 }
 
@@ -109,6 +114,8 @@ struct vmlm_decoder {
     float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
     float *logits = nullptr;
     uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
+    int8_t *x8 = nullptr;   // k-slice program: int8 rows of the normed input [Q8_T][B][H]
+    float *x8s = nullptr;   // and their per-row factors [B]
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     float *part = nullptr;               // k-slice partial sums of the decode GEMVs
@@ -181,7 +188,12 @@ int enqueue_head(vmlm_decoder *d, bool record) {
 KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int K) {
     KsArgs g;
     g.W = d->Sw(W);
-    g.A = A;
+    if (A == d->t_x) {  // the normed rows enter as int8 rows
+        g.A8 = d->x8;
+        g.a8s = d->x8s;
+    } else {
+        g.A = A;
+    }
     g.lda = K;
     g.M = (int)d->B;
     g.N = N;
@@ -199,8 +211,7 @@ int enqueue_step(vmlm_decoder *d) {
     const int T = 3;
     int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
     if (rc) return rc;
-    if ((rc = launch_rmsnorm(nullptr, d->h, d->InLn(0), B, H, d->c.eps, d->t_x, T, H, st)))
-        return rc;
+    if ((rc = launch_rmsnorm_q8(d->h, d->InLn(0), B, H, d->c.eps, d->x8, d->x8s, st))) return rc;
     for (size_t l = 0; l < d->L; ++l) {
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H), st))) return rc;
         DecodeArgs a;
@@ -221,15 +232,19 @@ int enqueue_step(vmlm_decoder *d) {
         if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H), st))) return rc;
         if ((rc = launch_rmsnorm_resid(d->h, d->part, d->ks_h, H, d->So(l), d->h2, B, H,
-                                       d->PostLn(l), d->c.eps, d->t_x, T, H, st)))
+                                       d->PostLn(l), d->c.eps, nullptr, T, H, st, d->x8, d->x8s)))
             return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H), st))) return rc;
         if ((rc = launch_silu_reduce(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->t_act, T, st)))
             return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I), st))) return rc;
-        const float *g_next = l + 1 < d->L ? d->InLn(l + 1) : d->final_norm;
+        // the next layer's input as int8 rows; after the last layer the final
+        // norm's bf16 terms for the LM head
+        const bool last = l + 1 == d->L;
+        const float *g_next = last ? d->final_norm : d->InLn(l + 1);
         if ((rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H, g_next,
-                                       d->c.eps, d->t_x, T, H, st)))
+                                       d->c.eps, last ? d->t_x : nullptr, T, H, st,
+                                       last ? nullptr : d->x8, last ? nullptr : d->x8s)))
             return rc;
     }
     if ((rc = enqueue_head(d, true))) return rc;
@@ -391,6 +406,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
         (rc = dalloc(d, &d->wsw, d->L * d->w_layer)) ||
+        (rc = dalloc(d, &d->x8, (size_t)Q8_T * d->B * d->H)) || (rc = dalloc(d, &d->x8s, d->B)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
@@ -556,22 +572,17 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             g.C = qkv;
             g.ldc = (int)(3 * H);
             if ((r = launch_gemm(g, st))) return r;
-            for (size_t b = 0; b < B; ++b) {  // RoPE q and k in place at positions 0..S-1
-                float *rowq = qkv + b * S * 3 * H;
-                if ((r = launch_rope(rowq, rowq, S, 64, 3 * H, d->c.theta, 0.0f, (int)NH, st)))
-                    return r;
-                if ((r = launch_rope(rowq + H, rowq + H, S, 64, 3 * H, d->c.theta, 0.0f, (int)NH,
-                                     st)))
-                    return r;
-            }
+            // q and k stay unrotated in qkv: the cache fill rotates k at positions
+            // 0..S-1 and the attention kernel rotates q and k as it loads them
             size_t nkv = M * NH * 64;
             kv_fill_kernel<<<cdiv(nkv, 256), 256, 0, st>>>(qkv, (int)(3 * H), (int)H, (int)NH,
                                                            (int)S, d->Kc(l), d->Vc(l),
-                                                           (int)d->cap, (int)B);
+                                                           (int)d->cap, (int)B, d->rope_step);
             VMLM_HIP_CHECK(hipGetLastError());
             if ((r = launch_attention_prefill(qkv, qkv + H, qkv + 2 * H, att, (int)S, (int)NH,
                                               (int)(3 * H), (int)H, d->c.attn_scale, true, kvw,
-                                              st, false, 0.0f, 0.0f, (int)B, S * 3 * H, S * H)))
+                                              st, true, d->rope_step, 0.0f, (int)B, S * 3 * H,
+                                              S * H)))
                 return r;
             if ((r = launch_split_terms(att, H, (int)M, (int)H, T, terms, (int)H, st))) return r;
             GemmArgs go = g;
