@@ -102,14 +102,20 @@ int launch_fk_gemv(const FkArgs &a, hipStream_t st);
 int launch_fk_norm_prep(const float *h, int ldh, const float *g, int M, int N, uint16_t *terms,
                         int ldt, float *ssp, hipStream_t st);
 // k-slice GEMV for decode batches up to 16 over the swizzled weights: raw
-// slice sums Y[ks][M][ldy] of A [3][M][lda] (bf16 term planes) . W^T, with
-// ks = ks_gemv_slices(K) slices of K / ks; the consumer reduces the slices
-// in order and applies the row scales.
+// slice sums Y[ks][M][ldy] of A . W^T, with ks = ks_gemv_slices(K) slices of
+// ks_gemv_window(K) columns; the consumer reduces the slices in order and
+// applies the row scales. A is given as bf16 term planes [3][M][lda], or as
+// int8 rows from launch_resid_q8 (segments = the slices): the int8 terms
+// [Q8_T][M][lda] of x * g, each slice's row factors a8s[ks][M] and the
+// segment sums of squares ssp[ks][M]; slice s of row m is then multiplied by
+// a8s[s][m] / sqrt(sum_s ssp[s][m] / K + eps).
 struct KsArgs {
     const int8_t *W = nullptr;
-    const uint16_t *A = nullptr;  // bf16 term planes [3][M][lda], or
-    const int8_t *A8 = nullptr;   // int8 rows [Q8_T][M][lda] with factors a8s[M]
+    const uint16_t *A = nullptr;
+    const int8_t *A8 = nullptr;
     const float *a8s = nullptr;
+    const float *ssp = nullptr;
+    float eps = 0.0f;
     int lda = 0;
     float *Y = nullptr;
     int ldy = 0;
@@ -117,6 +123,7 @@ struct KsArgs {
     int tw = 0, nwv = 0;  // tiles per wave, waves per workgroup; 0 = 2, 4
 };
 int ks_gemv_slices(int K);
+inline int ks_gemv_window(int K) { return K / ks_gemv_slices(K); }
 int launch_ks_gemv(const KsArgs &a, hipStream_t st);
 // int8 [N][K] row-major -> [N/16][K/64][64 lanes][16 B] MFMA-operand order.
 int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
@@ -148,16 +155,20 @@ int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, si
                    float eps, uint16_t *terms, int T, int ld_terms, hipStream_t st);
 // x = base + (sum of ks k-slice partials [ks][rows][ldp]) * scale -> resid;
 // RMSNorm(x) * g -> T bf16 terms [T][rows][cols].
-// With q8 (optional), also the int8 rows of the normalised values: Q8_T terms
-// [Q8_T][rows][cols] and the per-row factor q8s[row] = 2^-k (see q8_split).
-// terms may then be null.
 int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
                          const float *scale, float *resid, size_t rows, size_t cols,
                          const float *g, float eps, uint16_t *terms, int T, int ld_terms,
-                         hipStream_t st, int8_t *q8 = nullptr, float *q8s = nullptr);
-// RMSNorm of rows into int8 rows only (Q8_T terms and per-row factors).
-int launch_rmsnorm_q8(const float *src, const float *g, size_t rows, size_t cols, float eps,
-                      int8_t *q8, float *q8s, hipStream_t st);
+                         hipStream_t st);
+// The residual add of a k-split projection and the int8 input of the next
+// k-slice GEMVs, by segments of `seg` columns (the consumers' k window):
+//   x = base + (sum_ks part[ks]) * scale   (ks == 0: x = base, nothing stored)
+//   resid = x;  q8/q8s = int8 terms of x * g with each segment's power-of-two
+//   factor [cols/seg][rows];  ssp = each segment's sum of x^2 [cols/seg][rows].
+// The consumer applies 1/sqrt(sum(ssp)/cols + eps) (the RMSNorm) to its dot
+// products.
+int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
+                    float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
+                    float *q8s, float *ssp, hipStream_t st);
 // SiLU(gate) * up from the partials of the interleaved gate/up projection.
 int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
                        uint16_t *terms, int T, hipStream_t st);

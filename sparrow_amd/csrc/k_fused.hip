@@ -261,8 +261,10 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
 struct KsParams {
     const uint8_t *W;   // swizzled [N/16][K/64][64][16]
     const uint16_t *A;  // [3][M][lda] bf16 term planes, or
-    const int8_t *A8;   // [Q8_T][M][lda] int8 rows with per-row factors a8s[M]
+    const int8_t *A8;   // [Q8_T][M][lda] int8 rows, slice factors a8s[ks][M]
     const float *a8s;
+    const float *ssp;   // [ks][M] segment sums of squares (RMSNorm), or null
+    float eps;
     int lda;
     float *Y;
     int ldy;
@@ -270,12 +272,15 @@ struct KsParams {
 };
 
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+constexpr int KS_SSP_MAX = 16;  // k-slices whose segment sums are read up front
 
 // The int8 form: the slice of the Q8_T int8 term planes is staged in LDS; per
 // block and term one v_mfma_i32_16x16x64_i8 per tile straight on the int8
 // weights (no conversion), accumulated exactly in int32 (|sum| < 2^24 over
 // a slice of at most 6 blocks). The epilogue forms
-// ((s0 + s1 / 2^7) + s2 / 2^14) + s3 / 2^21 in f32, times the row factor.
+// ((s0 + s1 / 2^7) + s2 / 2^14) + s3 / 2^21 in f32, times the row factor:
+// the slice's segment factor a8s[slice][row], and with ssp the RMSNorm's
+// 1 / sqrt(sum ssp[.][row] / K + eps) (the int8 terms are of x * g).
 // The swizzled weight bytes of lane (g, r) are k = 8g .. +7 and 32 + 8g .. +7
 // of the block; the B fragment of lane (g, n) takes the same k of token n,
 // so each product pairs matching k whatever order the MFMA sums them in.
@@ -304,7 +309,16 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
         const int rs = r < p.M ? r : 0;
         ap[i] = *(const u32x4 *)(p.A8 + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c16 * 16);
     }
-    const float rowf = p.a8s[n < p.M ? n : 0];
+    // the row factor: this slice's segment factor, times the RMSNorm's
+    // 1 / sqrt(mean(x^2) + eps) from the segment sums (in segment order)
+    const int nr = n < p.M ? n : 0;
+    const float segf = p.a8s[blockIdx.y * p.M + nr];
+    float ssr[KS_SSP_MAX];
+#pragma unroll
+    for (int s = 0; s < KS_SSP_MAX; ++s) {
+        const int ss = s < (int)gridDim.y ? s : (int)gridDim.y - 1;
+        ssr[s] = p.ssp ? p.ssp[ss * p.M + nr] : 0.0f;
+    }
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wr[TW][KB];
 #pragma unroll
@@ -323,6 +337,15 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
             const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
             *(u32x4 *)&as8[t][r][c16 * 16] = ap[i];
         }
+    }
+    float rowf = segf;
+    if (p.ssp) {
+        float ss = ssr[0];
+#pragma unroll
+        for (int s = 1; s < KS_SSP_MAX; ++s)
+            if (s < (int)gridDim.y) ss += ssr[s];
+        ss = ss / (float)p.K;
+        rowf = segf * (1.0f / sqrtf(ss + p.eps));
     }
     __syncthreads();
 
@@ -613,6 +636,8 @@ int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
                "k-slice GEMV: shape M=%d N=%d K=%d unsupported", a.M, a.N, a.K);
     VMLM_GUARD((a.A != nullptr) != (a.A8 != nullptr) && (!a.A8 || a.a8s),
                "k-slice GEMV: bf16 term planes or int8 rows with their factors");
+    VMLM_GUARD(!a.ssp || (a.A8 && ks_gemv_slices(a.K) <= KS_SSP_MAX),
+               "k-slice GEMV: segment sums go with int8 rows of at most %d slices", KS_SSP_MAX);
     VMLM_GUARD(a.lda % 16 == 0 && ((uintptr_t)(a.A ? (const void *)a.A : (const void *)a.A8) & 15) == 0 &&
                    a.Y && a.ldy % 4 == 0 && ((uintptr_t)a.Y & 15) == 0,
                "k-slice GEMV: input rows and partial rows must be 16-byte aligned");
@@ -621,6 +646,8 @@ int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
     p.A = a.A;
     p.A8 = a.A8;
     p.a8s = a.a8s;
+    p.ssp = a.ssp;
+    p.eps = a.eps;
     p.lda = a.lda;
     p.Y = a.Y;
     p.ldy = a.ldy;

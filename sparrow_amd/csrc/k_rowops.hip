@@ -70,9 +70,7 @@ __global__ __launch_bounds__(256) void rmsnorm_v4_kernel(float *__restrict__ dst
                                                          const float *__restrict__ src,
                                                          const float *__restrict__ g, int cols,
                                                          float eps, uint16_t *__restrict__ terms,
-                                                         int T, int ld_terms, int rows,
-                                                         int8_t *__restrict__ q8,
-                                                         float *__restrict__ q8s) {
+                                                         int T, int ld_terms, int rows) {
     __shared__ float sh[4];
     const int row = blockIdx.x, n4 = cols >> 2;
     const float4 *p = (const float4 *)(src + (size_t)row * cols);
@@ -119,34 +117,6 @@ __global__ __launch_bounds__(256) void rmsnorm_v4_kernel(float *__restrict__ dst
         for (int i = cols + threadIdx.x; i < ld_terms; i += 256)
             for (int t = 0; t < T; ++t) terms[((size_t)t * rows + row) * ld_terms + i] = 0;
     }
-    if (q8) {  // int8 terms of y with the row's power-of-two scale
-        float mx = 0.0f;
-        float y[U][4];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = threadIdx.x + u * 256;
-            y[u][0] = x[u].x * inv * gg[u].x, y[u][1] = x[u].y * inv * gg[u].y;
-            y[u][2] = x[u].z * inv * gg[u].z, y[u][3] = x[u].w * inv * gg[u].w;
-            if (c < n4)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fabsf(y[u][q]));
-        }
-        mx = block_max256(mx, sh);
-        const int k = q8_row_k(mx);
-        if (threadIdx.x == 0) q8s[row] = ldexpf(1.0f, -k);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = threadIdx.x + u * 256;
-            if (c >= n4) continue;
-            int a[4][Q8_T];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) q8_split(y[u][q], k, a[q]);
-#pragma unroll
-            for (int t = 0; t < Q8_T; ++t)
-                *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + 4 * c) =
-                    pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
-        }
-    }
 }
 
 int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
@@ -161,8 +131,7 @@ int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, si
 #define RMS_CASE(U)                                                                            \
     case U:                                                                                    \
         rmsnorm_v4_kernel<U><<<(unsigned)rows, 256, 0, st>>>(dst, src, g, (int)cols, eps,     \
-                                                              terms, T, ld_terms, (int)rows,  \
-                                                              nullptr, nullptr);              \
+                                                              terms, T, ld_terms, (int)rows); \
         break;
             RMS_CASE(1)
             RMS_CASE(2)
@@ -179,30 +148,6 @@ int launch_rmsnorm(float *dst, const float *src, const float *g, size_t rows, si
     return VMLM_OK;
 }
 
-int launch_rmsnorm_q8(const float *src, const float *g, size_t rows, size_t cols, float eps,
-                      int8_t *q8, float *q8s, hipStream_t st) {
-    if (rows == 0) return VMLM_OK;
-    const size_t u = (cols / 4 + 255) / 256;
-    VMLM_GUARD(cols % 4 == 0 && u >= 1 && u <= 4 && ((uintptr_t)src & 15) == 0 &&
-                   ((uintptr_t)g & 15) == 0 && ((uintptr_t)q8 & 3) == 0 && q8s,
-               "rmsnorm (int8 rows): cols %% 4 == 0, cols <= 4096, aligned rows");
-    switch (u) {
-#define RMSQ_CASE(U)                                                                       \
-    case U:                                                                                \
-        rmsnorm_v4_kernel<U><<<(unsigned)rows, 256, 0, st>>>(nullptr, src, g, (int)cols,  \
-                                                              eps, nullptr, 0, 0,          \
-                                                              (int)rows, q8, q8s);         \
-        break;
-        RMSQ_CASE(1)
-        RMSQ_CASE(2)
-        RMSQ_CASE(3)
-        RMSQ_CASE(4)
-#undef RMSQ_CASE
-    }
-    VMLM_HIP_CHECK(hipGetLastError());
-    return VMLM_OK;
-}
-
 // Residual add of a k-split projection fused with the RMSNorm that follows
 // it (OP_GEMM + OP_EWADD + OP_RMSNORM of the decoder program): per row,
 //   x = base + (sum_ks part[ks]) * scale      (slices summed in order)
@@ -214,9 +159,8 @@ constexpr int KS_MAX = 16;
 __global__ __launch_bounds__(1024) void rmsnorm_resid_kernel(
     const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
     const float *__restrict__ scale, float *__restrict__ resid, const float *__restrict__ g,
-    int cols, float eps, uint16_t *__restrict__ terms, int T, int ld_terms, int rows,
-    int8_t *__restrict__ q8, float *__restrict__ q8s) {
-    __shared__ float sh[2][16];
+    int cols, float eps, uint16_t *__restrict__ terms, int T, int ld_terms, int rows) {
+    __shared__ float sh[16];
     const int row = blockIdx.x, n4 = cols >> 2;
     const int c = threadIdx.x < n4 ? threadIdx.x : n4 - 1;
     float4 pv[KS_MAX];
@@ -242,38 +186,17 @@ __global__ __launch_bounds__(1024) void rmsnorm_resid_kernel(
                                  bb.w + acc.w * sc.w);
     const bool live = threadIdx.x < n4;
     float ss = live ? x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w : 0.0f;
-    // max |x * g| rides along the sum of squares: times inv it bounds max |y|
-    // to a few ulps, which the int8 split's clamp margin absorbs
-    float mg = live && q8 ? fmaxf(fmaxf(fabsf(x.x * gg.x), fabsf(x.y * gg.y)),
-                                  fmaxf(fabsf(x.z * gg.z), fabsf(x.w * gg.w)))
-                          : 0.0f;
     ss = wave_sum(ss);
-    if (q8) mg = wave_max(mg);
-    if ((threadIdx.x & 63) == 0) sh[0][threadIdx.x >> 6] = ss, sh[1][threadIdx.x >> 6] = mg;
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = ss;
     __syncthreads();
     ss = 0.0f;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) ss += sh[0][w];
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) ss += sh[w];
     ss = ss / (float)cols;
     const float inv = 1.0f / sqrtf(ss + eps);
-    float y[4] = {x.x * inv * gg.x, x.y * inv * gg.y, x.z * inv * gg.z, x.w * inv * gg.w};
-    if (q8) {  // int8 terms of y with the row's power-of-two scale
-        float mx = 0.0f;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, sh[1][w]);
-        const int k = q8_row_k(mx * inv);
-        if (threadIdx.x == 0) q8s[row] = ldexpf(1.0f, -k);
-        if (live) {
-            int a[4][Q8_T];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) q8_split(y[q], k, a[q]);
-#pragma unroll
-            for (int t = 0; t < Q8_T; ++t)
-                *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + 4 * c) =
-                    pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
-        }
-    }
     if (!live) return;
     ((float4 *)(resid + (size_t)row * cols))[c] = x;
-    for (int t = 0; terms && t < T; ++t) {
+    float y[4] = {x.x * inv * gg.x, x.y * inv * gg.y, x.z * inv * gg.z, x.w * inv * gg.w};
+    for (int t = 0; t < T; ++t) {
         uint32_t h[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -288,9 +211,8 @@ __global__ __launch_bounds__(1024) void rmsnorm_resid_kernel(
 int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
                          const float *scale, float *resid, size_t rows, size_t cols,
                          const float *g, float eps, uint16_t *terms, int T, int ld_terms,
-                         hipStream_t st, int8_t *q8, float *q8s) {
+                         hipStream_t st) {
     if (rows == 0) return VMLM_OK;
-    VMLM_GUARD(!q8 || (((uintptr_t)q8 & 3) == 0 && q8s), "rmsnorm_resid: int8 rows need scales");
     VMLM_GUARD(cols % 4 == 0 && cols <= 4096 && ldp % 4 == 0 && ks >= 1 && ks <= KS_MAX &&
                    (int)cols == ld_terms,
                "rmsnorm_resid: cols %% 4 (<= 4096), ldp %% 4, 1 <= ks <= %d, ld_terms == cols",
@@ -298,7 +220,104 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
     const unsigned threads = (unsigned)((cols / 4 + 63) / 64 * 64);
     rmsnorm_resid_kernel<<<(unsigned)rows, threads, 0, st>>>(base, part, ks, ldp, scale, resid,
                                                              g, (int)cols, eps, terms, T,
-                                                             ld_terms, (int)rows, q8, q8s);
+                                                             ld_terms, (int)rows);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// One wave per (segment, row): the residual add of a k-split projection and
+// the int8 input of the next k-slice GEMVs (see launch_resid_q8). Lane l
+// holds columns 4c..4c+3 of the segment, c = l + 64i (i < SI); all slices of
+// a column are loaded up front (index clamped) so the reads take one round
+// trip. The segment's power-of-two factor comes from its own max |x * g|.
+template <int SI>
+__global__ __launch_bounds__(64) void resid_q8_kernel(
+    const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
+    const float *__restrict__ scale, float *__restrict__ resid, const float *__restrict__ g,
+    int cols, int rows, int seg, int8_t *__restrict__ q8, float *__restrict__ q8s,
+    float *__restrict__ ssp) {
+    const int sgi = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+    const int n4 = seg >> 2;
+    float4 xg[SI];
+    float ss = 0.0f, mg = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+        const int c = lane + 64 * i;
+        const bool live = c < n4;
+        const int col = sgi * seg + 4 * (live ? c : n4 - 1);
+        float4 bb = *(const float4 *)(base + (size_t)row * cols + col);
+        const float4 gg = *(const float4 *)(g + col);
+        if (ks > 0) {
+            float4 pv[KS_MAX];
+#pragma unroll
+            for (int k = 0; k < KS_MAX; ++k) {
+                const int kk = k < ks ? k : ks - 1;
+                pv[k] = *(const float4 *)(part + ((size_t)kk * rows + row) * ldp + col);
+            }
+            const float4 sc = *(const float4 *)(scale + col);
+            float4 acc = pv[0];
+#pragma unroll
+            for (int k = 1; k < KS_MAX; ++k) {
+                if (k < ks) {
+                    acc.x += pv[k].x;
+                    acc.y += pv[k].y;
+                    acc.z += pv[k].z;
+                    acc.w += pv[k].w;
+                }
+            }
+            bb = make_float4(bb.x + acc.x * sc.x, bb.y + acc.y * sc.y, bb.z + acc.z * sc.z,
+                             bb.w + acc.w * sc.w);
+            if (live) *(float4 *)(resid + (size_t)row * cols + col) = bb;
+        }
+        xg[i] = make_float4(bb.x * gg.x, bb.y * gg.y, bb.z * gg.z, bb.w * gg.w);
+        if (live) {
+            ss += bb.x * bb.x + bb.y * bb.y + bb.z * bb.z + bb.w * bb.w;
+            mg = fmaxf(mg, fmaxf(fmaxf(fabsf(xg[i].x), fabsf(xg[i].y)),
+                                 fmaxf(fabsf(xg[i].z), fabsf(xg[i].w))));
+        }
+    }
+    ss = wave_sum(ss);
+    mg = wave_max(mg);
+    const int k = q8_row_k(mg);
+    if (lane == 0) {
+        q8s[(size_t)sgi * rows + row] = ldexpf(1.0f, -k);
+        ssp[(size_t)sgi * rows + row] = ss;
+    }
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+        const int c = lane + 64 * i;
+        if (c >= n4) continue;
+        const int col = sgi * seg + 4 * c;
+        int a[4][Q8_T];
+        q8_split(xg[i].x, k, a[0]);
+        q8_split(xg[i].y, k, a[1]);
+        q8_split(xg[i].z, k, a[2]);
+        q8_split(xg[i].w, k, a[3]);
+#pragma unroll
+        for (int t = 0; t < Q8_T; ++t)
+            *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + col) =
+                pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+    }
+}
+
+int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
+                    float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
+                    float *q8s, float *ssp, hipStream_t st) {
+    if (rows == 0) return VMLM_OK;
+    VMLM_GUARD(seg >= 64 && seg <= 512 && seg % 64 == 0 && cols % seg == 0 && cols / seg <= 65535,
+               "resid_q8: segments of 64..512 columns (multiple of 64) tiling the row");
+    VMLM_GUARD(ks >= 0 && ks <= KS_MAX && (ks == 0 || (part && scale && resid && ldp % 4 == 0)),
+               "resid_q8: 0 <= ks <= %d; a k-split needs partials, scales and a residual", KS_MAX);
+    VMLM_GUARD(((uintptr_t)base & 15) == 0 && ((uintptr_t)g & 15) == 0 && ((uintptr_t)q8 & 3) == 0 &&
+                   q8s && ssp && rows <= 65535,
+               "resid_q8: aligned rows and outputs");
+    const dim3 grid((unsigned)(cols / seg), (unsigned)rows);
+    if (seg <= 256)
+        resid_q8_kernel<1><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g, (int)cols,
+                                                (int)rows, seg, q8, q8s, ssp);
+    else
+        resid_q8_kernel<2><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g, (int)cols,
+                                                (int)rows, seg, q8, q8s, ssp);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

@@ -114,8 +114,11 @@ struct vmlm_decoder {
     float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
     float *logits = nullptr;
     uint16_t *t_x = nullptr, *t_att = nullptr, *t_act = nullptr;
-    int8_t *x8 = nullptr;   // k-slice program: int8 rows of the normed input [Q8_T][B][H]
-    float *x8s = nullptr;   // and their per-row factors [B]
+    // k-slice program: the normed input as int8 terms of h * g [Q8_T][B][H],
+    // by segments of the GEMVs' k window: factors and sums of squares [H/seg][B]
+    int8_t *x8 = nullptr;
+    float *x8s = nullptr, *x8ssp = nullptr;
+    int seg = 0;
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     float *part = nullptr;               // k-slice partial sums of the decode GEMVs
@@ -191,6 +194,8 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
     if (A == d->t_x) {  // the normed rows enter as int8 rows
         g.A8 = d->x8;
         g.a8s = d->x8s;
+        g.ssp = d->x8ssp;
+        g.eps = d->c.eps;
     } else {
         g.A = A;
     }
@@ -211,7 +216,9 @@ int enqueue_step(vmlm_decoder *d) {
     const int T = 3;
     int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
     if (rc) return rc;
-    if ((rc = launch_rmsnorm_q8(d->h, d->InLn(0), B, H, d->c.eps, d->x8, d->x8s, st))) return rc;
+    if ((rc = launch_resid_q8(d->h, nullptr, 0, 0, nullptr, nullptr, d->InLn(0), B, H, d->seg,
+                              d->x8, d->x8s, d->x8ssp, st)))
+        return rc;
     for (size_t l = 0; l < d->L; ++l) {
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H), st))) return rc;
         DecodeArgs a;
@@ -231,8 +238,8 @@ int enqueue_step(vmlm_decoder *d) {
         a.wscale = d->Sqkv(l);
         if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H), st))) return rc;
-        if ((rc = launch_rmsnorm_resid(d->h, d->part, d->ks_h, H, d->So(l), d->h2, B, H,
-                                       d->PostLn(l), d->c.eps, nullptr, T, H, st, d->x8, d->x8s)))
+        if ((rc = launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
+                                  d->seg, d->x8, d->x8s, d->x8ssp, st)))
             return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H), st))) return rc;
         if ((rc = launch_silu_reduce(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->t_act, T, st)))
@@ -240,12 +247,13 @@ int enqueue_step(vmlm_decoder *d) {
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I), st))) return rc;
         // the next layer's input as int8 rows; after the last layer the final
         // norm's bf16 terms for the LM head
-        const bool last = l + 1 == d->L;
-        const float *g_next = last ? d->final_norm : d->InLn(l + 1);
-        if ((rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H, g_next,
-                                       d->c.eps, last ? d->t_x : nullptr, T, H, st,
-                                       last ? nullptr : d->x8, last ? nullptr : d->x8s)))
-            return rc;
+        if (l + 1 < d->L)
+            rc = launch_resid_q8(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, d->InLn(l + 1), B, H,
+                                 d->seg, d->x8, d->x8s, d->x8ssp, st);
+        else
+            rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H,
+                                      d->final_norm, d->c.eps, d->t_x, T, H, st);
+        if (rc) return rc;
     }
     if ((rc = enqueue_head(d, true))) return rc;
     step_advance_kernel<<<1, 1, 0, st>>>(d->step, d->pos);
@@ -392,6 +400,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     d->ks_i = ks_gemv_slices((int)d->I);
     VMLM_GUARD(d->ks_h <= 16 && d->ks_i <= 16, "decoder: hidden %u / inter %u need over 16 k-slices",
                c.hidden, c.inter);
+    d->seg = ks_gemv_window((int)d->H);  // 64 .. 384 columns
     d->fused = fused_ok(d);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
@@ -406,7 +415,9 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
         (rc = dalloc(d, &d->wsw, d->L * d->w_layer)) ||
-        (rc = dalloc(d, &d->x8, (size_t)Q8_T * d->B * d->H)) || (rc = dalloc(d, &d->x8s, d->B)) ||
+        (rc = dalloc(d, &d->x8, (size_t)Q8_T * d->B * d->H)) ||
+        (rc = dalloc(d, &d->x8s, d->H / d->seg * d->B)) ||
+        (rc = dalloc(d, &d->x8ssp, d->H / d->seg * d->B)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
