@@ -51,9 +51,10 @@ def gemv_roofline(dec, iters):
     """q8 GEMV (the int8 projections of a decode step): mean launch duration
     per shape from HIP events on the session stream, and the step-mix
     achieved bandwidth = sum(bytes) / sum(time) over one launch of each.
-    At batch 16 these are the k-slice kernels (ks_gemv_kernel); at batch
-    <= 5 the fused full-K kernels (fk_gemv_kernel, with their RMSNorm,
-    residual and SiLU work)."""
+    At batch 16 these are the k-slice kernels (ks_gemv_i8_kernel on int8
+    rows for q/k/v and gate/up, ks_gemv_kernel on bf16 terms for o and
+    down); at batch <= 5 the fused full-K kernels (fk_gemv_kernel, with
+    their RMSNorm, residual and SiLU work)."""
     per = {}
     tot_b = tot_t = 0.0
     for which, name in ((0, "qkv"), (1, "o"), (2, "gate_up"), (3, "down")):
@@ -73,7 +74,8 @@ def gemv_roofline(dec, iters):
                                               ROOT),
             "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues)"
                        if dec.fused else
-                       "ks_gemv_kernel (q/k/v, o, gate+up, down; k-slice partials)"),
+                       "ks_gemv_i8_kernel (q/k/v, gate+up; int8 rows) and ks_gemv_kernel "
+                       "(o, down); k-slice partials"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "per_shape": per}
 

@@ -290,6 +290,7 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
     constexpr int KW = KB * 64;
     constexpr int ALD = KW + 16;     // padded LDS row (bytes)
     __shared__ __attribute__((aligned(16))) int8_t as8[Q8_T][16][ALD];
+    __shared__ float ssp_s[KS_SSP_MAX][16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -310,14 +311,19 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
         ap[i] = *(const u32x4 *)(p.A8 + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c16 * 16);
     }
     // the row factor: this slice's segment factor, times the RMSNorm's
-    // 1 / sqrt(mean(x^2) + eps) from the segment sums (in segment order)
+    // 1 / sqrt(mean(x^2) + eps) from the segment sums (one load per thread
+    // into LDS; summed per row in segment order after the barrier)
     const int nr = n < p.M ? n : 0;
     const float segf = p.a8s[blockIdx.y * p.M + nr];
-    float ssr[KS_SSP_MAX];
+    const int nsl = (int)gridDim.y;
+    constexpr int SPER = (KS_SSP_MAX * 16 + NTH - 1) / NTH;
+    float sspv[SPER];
 #pragma unroll
-    for (int s = 0; s < KS_SSP_MAX; ++s) {
-        const int ss = s < (int)gridDim.y ? s : (int)gridDim.y - 1;
-        ssr[s] = p.ssp ? p.ssp[ss * p.M + nr] : 0.0f;
+    for (int i = 0; i < SPER; ++i) {
+        int e = tid + i * NTH;
+        e = e < nsl * 16 ? e : 0;
+        const int r = e & 15;
+        sspv[i] = p.ssp ? p.ssp[(e >> 4) * p.M + (r < p.M ? r : 0)] : 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wr[TW][KB];
@@ -338,16 +344,19 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
             *(u32x4 *)&as8[t][r][c16 * 16] = ap[i];
         }
     }
+#pragma unroll
+    for (int i = 0; i < SPER; ++i) {
+        const int e = tid + i * NTH;
+        if (e < nsl * 16) ssp_s[e >> 4][e & 15] = sspv[i];
+    }
+    __syncthreads();
     float rowf = segf;
     if (p.ssp) {
-        float ss = ssr[0];
-#pragma unroll
-        for (int s = 1; s < KS_SSP_MAX; ++s)
-            if (s < (int)gridDim.y) ss += ssr[s];
+        float ss = ssp_s[0][n];
+        for (int s = 1; s < nsl; ++s) ss += ssp_s[s][n];
         ss = ss / (float)p.K;
         rowf = segf * (1.0f / sqrtf(ss + p.eps));
     }
-    __syncthreads();
 
     i32x4 acc[TW][Q8_T];
 #pragma unroll
