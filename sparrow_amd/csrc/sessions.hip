@@ -205,6 +205,17 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
     g.K = K;
     g.Y = d->part;
     g.ldy = N;
+    // launch shape (16-row tiles per wave, waves per workgroup), measured at
+    // the MiniCPM-2B shapes, batch 16: q/k/v 2 x 8 (5.22 us against 5.53 at
+    // 2 x 4), gate/up 4 x 4 (7.73 against 8.25), down 2 x 8 (6.32 against
+    // 6.53), o 2 x 4
+    if (g.A8) {
+        g.tw = N >= 4 * K ? 4 : 2;
+        g.nwv = N >= 4 * K ? 4 : 8;
+    } else {
+        g.tw = 2;
+        g.nwv = K > (int)d->H ? 8 : 4;
+    }
     return g;
 }
 
