@@ -205,8 +205,9 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;
-    float *kc, *vc;  // [B][H][cap][64]
+    float *kc, *vc;  // [B][H][hs][64]
     int cap, H;
+    int hs = 0;      // rows from one head's cache to the next (0: cap)
     const int *posp;  // device position (graph replay) or null -> `pos`
     int pos;
     float step, scale;  // RoPE step -2/64*ln_f(theta); score scale

@@ -691,7 +691,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     // this workgroup's chunks [c0, c1): all, or partition blockIdx.z of cpp
     const int c0 = cpp ? (int)blockIdx.z * cpp : 0;
     const int c1 = cpp ? min(c0 + cpp, nch) : nch;
-    const size_t head = ((size_t)b * a.H + h) * a.cap * 64;
+    const size_t head = ((size_t)b * a.H + h) * (a.hs ? a.hs : a.cap) * 64;
 
     // Cache rows through buffer loads whose range ends at row `pos`: rows at
     // or past it (the new row, unused rows, chunks past the last) read as
@@ -926,7 +926,8 @@ size_t attention_decode_work_floats(const DecodeArgs &a, int B) {
 
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st, float *work) {
-    VMLM_GUARD(a.cap >= 1 && a.H >= 1 && B >= 1, "attention decode: empty shape");
+    VMLM_GUARD(a.cap >= 1 && a.H >= 1 && B >= 1 && (a.hs == 0 || a.hs >= a.cap),
+               "attention decode: empty shape, or head stride below the capacity");
     const size_t lds = (size_t)((a.cap + 63) / 64) * AD_PART * sizeof(float);
     VMLM_GUARD(lds <= 96 * 1024, "attention decode: cache capacity %d beyond %d positions",
                a.cap, 96 * 1024 / (AD_PART * 4) * 64);
