@@ -169,9 +169,12 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
                     float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
                     float *q8s, float *ssp, hipStream_t st);
-// SiLU(gate) * up from the partials of the interleaved gate/up projection.
-int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
-                       uint16_t *terms, int T, hipStream_t st);
+// SiLU(gate) * up from the partials of the interleaved gate/up projection,
+// as int8 terms [Q8_T][rows][I] with a power-of-two
+// factor per segment of `seg` columns, q8s [I/seg][rows] (the input of a
+// k-slice GEMV whose slices are the segments).
+int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int rows, int I, int seg,
+                   int8_t *q8, float *q8s, hipStream_t st);
 int launch_softmax(float *p, size_t rows, size_t cols, bool causal, hipStream_t st);
 int launch_act(float *dst, size_t n, int kind, hipStream_t st);
 int launch_ew(float *dst, const float *x, const float *y, size_t n, int op, hipStream_t st);

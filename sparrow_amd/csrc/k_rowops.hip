@@ -230,7 +230,7 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 // holds columns 4c..4c+3 of the segment, c = l + 64i (i < SI); all slices of
 // a column are loaded up front (index clamped) so the reads take one round
 // trip. The segment's power-of-two factor comes from its own max |x * g|.
-template <int SI>
+template <int SI, int KSN>
 __global__ __launch_bounds__(64) void resid_q8_kernel(
     const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
     const float *__restrict__ scale, float *__restrict__ resid, const float *__restrict__ g,
@@ -248,16 +248,16 @@ __global__ __launch_bounds__(64) void resid_q8_kernel(
         float4 bb = *(const float4 *)(base + (size_t)row * cols + col);
         const float4 gg = *(const float4 *)(g + col);
         if (ks > 0) {
-            float4 pv[KS_MAX];
+            float4 pv[KSN];
 #pragma unroll
-            for (int k = 0; k < KS_MAX; ++k) {
+            for (int k = 0; k < KSN; ++k) {
                 const int kk = k < ks ? k : ks - 1;
                 pv[k] = *(const float4 *)(part + ((size_t)kk * rows + row) * ldp + col);
             }
             const float4 sc = *(const float4 *)(scale + col);
             float4 acc = pv[0];
 #pragma unroll
-            for (int k = 1; k < KS_MAX; ++k) {
+            for (int k = 1; k < KSN; ++k) {
                 if (k < ks) {
                     acc.x += pv[k].x;
                     acc.y += pv[k].y;
@@ -312,64 +312,102 @@ int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const
                    q8s && ssp && rows <= 65535,
                "resid_q8: aligned rows and outputs");
     const dim3 grid((unsigned)(cols / seg), (unsigned)rows);
-    if (seg <= 256)
-        resid_q8_kernel<1><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g, (int)cols,
-                                                (int)rows, seg, q8, q8s, ssp);
-    else
-        resid_q8_kernel<2><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g, (int)cols,
-                                                (int)rows, seg, q8, q8s, ssp);
+    // slice loads sized to the slice count of the decoder's projections (9
+    // for K = 2304, 15 for K = 5760), else 4 or 16 with the index clamped
+#define RQ_LAUNCH(SI, KSN)                                                                      \
+    resid_q8_kernel<SI, KSN><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g,        \
+                                                  (int)cols, (int)rows, seg, q8, q8s, ssp)
+#define RQ_KS(SI)                                                                               \
+    if (ks == 9) RQ_LAUNCH(SI, 9);                                                              \
+    else if (ks == 15) RQ_LAUNCH(SI, 15);                                                       \
+    else if (ks <= 4) RQ_LAUNCH(SI, 4);                                                         \
+    else RQ_LAUNCH(SI, 16);
+    if (seg <= 256) {
+        RQ_KS(1)
+    } else {
+        RQ_KS(2)
+    }
+#undef RQ_KS
+#undef RQ_LAUNCH
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
 
-// SiLU(gate) * up from the k-slice partials of the interleaved gate/up
-// projection (16-row blocks: rows 32t..32t+15 gate and 32t+16..32t+31 up
-// of output columns 16t..16t+15), written as T bf16 terms [T][rows][I]:
-//   gate = (sum_ks P) * sg, up = (sum_ks P) * su, a = gate / (1 + exp_f(-gate)) * up.
-// One output per thread, every slice loaded up front.
-__global__ __launch_bounds__(256) void silu_reduce_kernel(const float *__restrict__ part, int ks,
-                                                          int ldp, const float *__restrict__ sgu,
-                                                          int rows, int I,
-                                                          uint16_t *__restrict__ terms, int T) {
-    const int n = rows * I;
-    int i = blockIdx.x * 256 + threadIdx.x;
-    const bool live = i < n;
-    i = live ? i : n - 1;
-    const int row = i / I, jo = i % I;
-    const int jg = (jo >> 4) * 32 + (jo & 15), ju = jg + 16;
-    float gv[KS_MAX], uv[KS_MAX];
+// SiLU(gate) * up as the int8 input of the down projection's k-slice GEMV.
+// The gate/up projection interleaves its rows in blocks of 16 (rows
+// 32t..32t+15 gate, 32t+16..32t+31 up, for outputs 16t..16t+15); its k-slice
+// partials are summed in slice order and scaled, then
+// y = (gate / (1 + exp_f(-gate))) * up, the element operations of ACT silu
+// then EWMUL. One workgroup per (segment of `seg` columns, row), one thread
+// per 4 columns; the segment's power-of-two factor from its own max |y|.
+template <int KSN>
+__global__ __launch_bounds__(128) void silu_q8_kernel(const float *__restrict__ part, int ks,
+                                                      int ldp, const float *__restrict__ sgu,
+                                                      int rows, int I, int seg,
+                                                      int8_t *__restrict__ q8,
+                                                      float *__restrict__ q8s) {
+    __shared__ float sh[2];
+    const int sgi = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int n4 = seg >> 2;
+    const bool live = tid < n4;
+    const int jo = sgi * seg + 4 * (live ? tid : n4 - 1);
+    const int jg = (jo >> 4) * 32 + (jo & 15), ju = jg + 16;  // gate/up tiles interleave by 16
+    float4 gv[KSN], uv[KSN];
 #pragma unroll
-    for (int k = 0; k < KS_MAX; ++k) {
-        const int kk = k < ks ? k : ks - 1;
-        const float *pr = part + ((size_t)kk * rows + row) * ldp;
-        gv[k] = pr[jg];
-        uv[k] = pr[ju];
+    for (int k = 0; k < KSN; ++k) {
+        const float *pr = part + ((size_t)(k < ks ? k : ks - 1) * rows + row) * ldp;
+        gv[k] = *(const float4 *)(pr + jg);
+        uv[k] = *(const float4 *)(pr + ju);
     }
-    const float sg = sgu[jg], su = sgu[ju];
-    float ga = gv[0], ua = uv[0];
+    const float4 sg = *(const float4 *)(sgu + jg), su = *(const float4 *)(sgu + ju);
+    float4 ga = gv[0], ua = uv[0];
 #pragma unroll
-    for (int k = 1; k < KS_MAX; ++k) {
+    for (int k = 1; k < KSN; ++k) {
         if (k < ks) {
-            ga += gv[k];
-            ua += uv[k];
+            ga.x += gv[k].x, ga.y += gv[k].y, ga.z += gv[k].z, ga.w += gv[k].w;
+            ua.x += uv[k].x, ua.y += uv[k].y, ua.z += uv[k].z, ua.w += uv[k].w;
         }
     }
-    if (!live) return;
-    const float gate = ga * sg, up = ua * su;
-    float y = (gate / (1.0f + exp_f(-gate))) * up;
-    for (int t = 0; t < T; ++t) {
-        const uint32_t h = bf16_rne_bits(y);
-        y = y - bf16_bits_to_f32(h);
-        terms[((size_t)t * rows + row) * I + jo] = (uint16_t)h;
+    float y[4];
+    const float gs[4] = {ga.x * sg.x, ga.y * sg.y, ga.z * sg.z, ga.w * sg.w};
+    const float us[4] = {ua.x * su.x, ua.y * su.y, ua.z * su.z, ua.w * su.w};
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        y[q] = (gs[q] / (1.0f + exp_f(-gs[q]))) * us[q];
+        mx = fmaxf(mx, fabsf(y[q]));
     }
+    mx = wave_max(live ? mx : 0.0f);
+    if ((tid & 63) == 0) sh[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(sh[0], blockDim.x > 64 ? sh[1] : 0.0f);
+    const int k = q8_row_k(mx);
+    if (tid == 0) q8s[(size_t)sgi * rows + row] = ldexpf(1.0f, -k);
+    if (!live) return;
+    int a[4][Q8_T];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) q8_split(y[q], k, a[q]);
+#pragma unroll
+    for (int t = 0; t < Q8_T; ++t)
+        *(uint32_t *)(q8 + ((size_t)t * rows + row) * I + jo) =
+            pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
 }
 
-int launch_silu_reduce(const float *part, int ks, int ldp, const float *sgu, int rows, int I,
-                       uint16_t *terms, int T, hipStream_t st) {
-    VMLM_GUARD(I % 16 == 0 && ks >= 1 && ks <= KS_MAX && rows >= 1,
-               "silu_reduce: I %% 16, 1 <= ks <= %d", KS_MAX);
-    const size_t n = (size_t)rows * I;
-    silu_reduce_kernel<<<cdiv(n, 256), 256, 0, st>>>(part, ks, ldp, sgu, rows, I, terms, T);
+int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int rows, int I, int seg,
+                   int8_t *q8, float *q8s, hipStream_t st) {
+    VMLM_GUARD(I % 16 == 0 && ks >= 1 && ks <= KS_MAX && rows >= 1 && rows <= 65535 &&
+                   seg >= 64 && seg <= 512 && seg % 64 == 0 && I % seg == 0 && ldp % 4 == 0 &&
+                   ((uintptr_t)part & 15) == 0 && ((uintptr_t)sgu & 15) == 0 &&
+                   ((uintptr_t)q8 & 3) == 0 && q8s,
+               "silu_q8: I %% seg, segments of 64..512 columns, 1 <= ks <= %d, aligned", KS_MAX);
+    const unsigned threads = (unsigned)((seg / 4 + 63) / 64 * 64);
+    const dim3 grid((unsigned)(I / seg), (unsigned)rows);
+#define SQ_LAUNCH(KSN) \
+    silu_q8_kernel<KSN><<<grid, threads, 0, st>>>(part, ks, ldp, sgu, rows, I, seg, q8, q8s)
+    if (ks == 9) SQ_LAUNCH(9);
+    else if (ks <= 4) SQ_LAUNCH(4);
+    else SQ_LAUNCH(16);
+#undef SQ_LAUNCH
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

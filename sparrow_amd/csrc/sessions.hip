@@ -119,6 +119,11 @@ struct vmlm_decoder {
     int8_t *x8 = nullptr;
     float *x8s = nullptr, *x8ssp = nullptr;
     int seg = 0;
+    // and the down projection's input silu(gate) * up: [Q8_T][B][I], factors
+    // [I/seg_i][B]
+    int8_t *act8 = nullptr;
+    float *act8s = nullptr;
+    int seg_i = 0;
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     float *part = nullptr;               // k-slice partial sums of the decode GEMVs
@@ -200,6 +205,9 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
         g.a8s = d->x8s;
         g.ssp = d->x8ssp;
         g.eps = d->c.eps;
+    } else if (A == d->t_act) {
+        g.A8 = d->act8;
+        g.a8s = d->act8s;
     } else {
         g.A = A;
     }
@@ -258,7 +266,8 @@ int enqueue_step(vmlm_decoder *d) {
                                   d->seg, d->x8, d->x8s, d->x8ssp, st)))
             return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H), st))) return rc;
-        if ((rc = launch_silu_reduce(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->t_act, T, st)))
+        if ((rc = launch_silu_q8(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->seg_i, d->act8,
+                                 d->act8s, st)))
             return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wd(l), d->t_act, H, I), st))) return rc;
         // the next layer's input as int8 rows; after the last layer the final
@@ -418,6 +427,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     VMLM_GUARD(d->ks_h <= 16 && d->ks_i <= 16, "decoder: hidden %u / inter %u need over 16 k-slices",
                c.hidden, c.inter);
     d->seg = ks_gemv_window((int)d->H);  // 64 .. 384 columns
+    d->seg_i = ks_gemv_window((int)d->I);
     d->fused = fused_ok(d);
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
@@ -436,6 +446,8 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->x8, (size_t)Q8_T * d->B * d->H)) ||
         (rc = dalloc(d, &d->x8s, d->H / d->seg * d->B)) ||
         (rc = dalloc(d, &d->x8ssp, d->H / d->seg * d->B)) ||
+        (rc = dalloc(d, &d->act8, (size_t)Q8_T * d->B * d->I)) ||
+        (rc = dalloc(d, &d->act8s, d->I / d->seg_i * d->B)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
