@@ -773,8 +773,13 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
         default: return step_gemv(d, d->Wd(l), d->t_act, H, I);
         }
     };
-    auto launch = [&](size_t l) { return which == 4 ? launch_gemv(make_lm(), d->st)
-                                                    : launch_ks_gemv(make(l), d->st); };
+    // the fused program (batch <= 5) runs the full-K kernels with their row ops
+    const bool fk = d->fused && which < 4;
+    auto launch = [&](size_t l) {
+        if (which == 4) return launch_gemv(make_lm(), d->st);
+        if (fk) return launch_fk_gemv(fk_args(d, l, which), d->st);
+        return launch_ks_gemv(make(l), d->st);
+    };
     // one event pair around `iters` back-to-back launches (the mean launch
     // duration, launch gaps included); successive launches walk the layers
     // so that no weight is re-read from cache
@@ -796,6 +801,13 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     // algorithmic bytes of the projection: weights, row scales (int8), the
     // f32 activation in and the f32 result out (the partial sums and the
     // bf16 term planes are this implementation's, not the algorithm's)
+    if (fk) {  // plus the residual rows that the o and down epilogues read
+        const FkArgs f = fk_args(d, 0, which);
+        const double nout = f.epi == FK_SILU ? f.N / 2.0 : (double)f.N;
+        *bytes_per_launch = (double)f.N * f.K + 4.0 * f.N + 4.0 * B * f.K + 4.0 * B * nout +
+                            (f.R ? 4.0 * B * f.N : 0.0);
+        return VMLM_OK;
+    }
     const bool i8 = which != 4;
     const double n = i8 ? make(0).N : make_lm().N, k = i8 ? make(0).K : make_lm().K;
     *bytes_per_launch = n * k * (i8 ? 1 : 2) + (i8 ? n * 4 : 0.0) + (double)B * k * 4 +

@@ -187,3 +187,20 @@ def test_minicpm_batch16_equals_batch1(hip, minicpm):
             dec.load(W)
             alone = dec.generate(prompts[b:b + 1], 8)
         assert np.array_equal(chains[b], alone[0])
+
+
+def test_time_gemv_follows_program(hip, tiny):
+    """time_gemv times the launches of the program the session runs: on the
+    fused program the o projection's bytes include the residual rows its
+    epilogue reads (4 * batch * hidden more than the k-slice kernel's)."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = tiny
+    with Decoder(cfg, batch=1, cap=64) as dec:
+        dec.load(W)
+        dec.prefill(M.make_prompts(cfg, 1, 5, seed=2))
+        assert dec.fused
+        us_f, b_f = dec.time_gemv(1, 4)
+        dec.set_fused(False)
+        us_k, b_k = dec.time_gemv(1, 4)
+    assert us_f > 0 and us_k > 0
+    assert b_f - b_k == 4 * 1 * cfg["hidden"]
