@@ -141,6 +141,10 @@ struct GemmArgs {
     int ldc = 0;
     int bm = 0;      // tile rows (64, 128); 0 = chosen by shape
     int stages = 0;  // LDS stages of the copy pipeline (2..4); 0 = chosen by shape
+    // or int8 rows (with int8 weights): Q8_T term planes [Q8_T][M][lda] and
+    // row factors [M] from launch_rows_q8 (A and T unused)
+    const int8_t *A8 = nullptr;
+    const float *a8s = nullptr;
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
 
@@ -169,6 +173,11 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
                     float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
                     float *q8s, float *ssp, hipStream_t st);
+// Rows x [rows][ldx] (with g: RMSNorm(x) * g) as Q8_T int8 terms
+// [Q8_T][rows][cols] with per-row power-of-two factors q8s [rows]: the input
+// of launch_gemm's int8-row path.
+int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
+                   int8_t *q8, float *q8s, hipStream_t st);
 // SiLU(gate) * up from the partials of the interleaved gate/up projection,
 // as int8 terms [Q8_T][rows][I] with a power-of-two
 // factor per segment of `seg` columns, q8s [I/seg][rows] (the input of a

@@ -19,7 +19,11 @@ struct GemmParams {
     float *C;
     size_t tstride;
     int lda, M, N, K, ldc;
+    const int8_t *A8;   // int8 rows: Q8_T term planes [Q8_T][M][lda] and
+    const float *a8s;   // row factors [M] (gemm_dma_i8_kernel)
 };
+
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int gi32x4;
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -222,6 +226,151 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
     }
 }
 
+// The same pipeline for int8 weights and int8 rows (Q8_T term planes of
+// each row with a power-of-two row factor, from launch_rows_q8): both tiles
+// stay int8 in LDS (64-byte rows, the int8 XOR swizzle), and each 64-wide
+// k-step runs one v_mfma_i32_16x16x64_i8 per term and 16 x 16 tile, exact
+// int32 sums per term. Lane (g, r) takes 16-byte piece g of its A row and of
+// its W row, so both operands pair the same k. The epilogue forms
+// ((s0 + s1/2^7) + s2/2^14) + s3/2^21 in f32, times the row factor and the
+// column scale. No int8 -> bf16 conversion, and Q8_T MFMAs of 8 passes per
+// k-step against six for three bf16 terms.
+template <int BM, int BN, int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_i8_kernel(GemmParams p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    constexpr int ROW = 64;  // bytes of an LDS row (64 k of int8)
+    constexpr int A_BYTES = Q8_T * BM * ROW, B_BYTES = BN * ROW;
+    constexpr int STAGE = A_BYTES + B_BYTES;
+    constexpr int C_LD = WN + 4;
+    constexpr int C_BYTES = 4 * 16 * C_LD * 4;
+    constexpr int SMEM = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
+    constexpr int A_INS = A_BYTES / 1024 / 4, B_INS = B_BYTES / 1024 / 4;  // per wave per step
+    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copy instructions per wave");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, r = lane & 15;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int nk = p.K / 64;
+
+    // copy plan: each instruction fills 16 rows x 64 B of LDS; lane i brings
+    // piece (i & 3) ^ ((R >> 1) & 3) of row R = 16 * instr + i / 4
+    const uint8_t *a_src[A_INS];
+    const uint8_t *b_src[B_INS];
+#pragma unroll
+    for (int q = 0; q < A_INS; ++q) {
+        const int rowg = (q * 4 + wave) * 16 + (lane >> 2);  // over the Q8_T*BM rows
+        const int t = rowg / BM, R = rowg % BM;
+        const int c = (lane & 3) ^ ((R >> 1) & 3);
+        int gm = m0 + R;
+        gm = gm < p.M ? gm : p.M - 1;
+        a_src[q] = (const uint8_t *)(p.A8 + t * p.tstride + (size_t)gm * p.lda) + c * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < B_INS; ++q) {
+        const int R = (q * 4 + wave) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((R >> 1) & 3);
+        int gn = n0 + R;
+        gn = gn < p.N ? gn : p.N - 1;
+        b_src[q] = p.W + (size_t)gn * p.K + c * 16;
+    }
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+    auto issue = [&](int kt) {
+        const int kc = kt < nk ? kt : nk - 1;
+        const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
+#pragma unroll
+        for (int q = 0; q < A_INS; ++q)
+            dma16(a_src[q] + (size_t)kc * ROW, sb + (q * 4 + wave) * 1024);
+#pragma unroll
+        for (int q = 0; q < B_INS; ++q)
+            dma16(b_src[q] + (size_t)kc * ROW, sb + A_BYTES + (q * 4 + wave) * 1024);
+    };
+
+    gi32x4 acc[Q8_T][TM][TN];
+#pragma unroll
+    for (int t = 0; t < Q8_T; ++t)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[t][i][j] = gi32x4{0, 0, 0, 0};
+
+    auto compute = [&](const uint8_t *sA) {
+        const uint8_t *sB = sA + A_BYTES;
+        gi32x4 bf[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int R = wn * WN + j * 16 + r;
+            bf[j] = *(const gi32x4 *)(sB + R * ROW + ((g ^ ((R >> 1) & 3)) * 16));
+        }
+#pragma unroll
+        for (int t = 0; t < Q8_T; ++t)
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int R = wm * WM + i * 16 + r;
+                const gi32x4 af =
+                    *(const gi32x4 *)(sA + (t * BM + R) * ROW + ((g ^ ((R >> 1) & 3)) * 16));
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[t][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[t][i][j], 0, 0, 0);
+            }
+    };
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * (A_INS + B_INS)));
+        __syncthreads();
+        issue(kt + NS - 1);
+        compute(smem + (kt % NS) * STAGE);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // copies past the end land before reuse
+    __syncthreads();
+
+    // epilogue: the terms combined, 16-row slabs through LDS, 16-byte stores
+    float *cs = (float *)smem + wave * 16 * C_LD;
+    const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.C & 15) == 0;
+    constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float f = (float)acc[0][i][j][q];
+                f = f + (float)acc[1][i][j][q] * 0.0078125f;
+                f = f + (float)acc[2][i][j][q] * 6.103515625e-05f;
+                f = f + (float)acc[3][i][j][q] * 4.76837158203125e-07f;
+                cs[(g * 4 + q) * C_LD + j * 16 + r] = f;
+            }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's slab is in LDS
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int pass = 0; pass < 16 / RPP; ++pass) {
+            const int rr_ = pass * RPP + lane / LPR, c4 = (lane % LPR) * 4;
+            float4 v = *(const float4 *)&cs[rr_ * C_LD + c4];
+            const int row = m0 + wm * WM + i * 16 + rr_, col = n0 + wn * WN + c4;
+            if (row >= p.M || col >= p.N) continue;
+            const float rf = p.a8s[row];
+            float y[4] = {v.x * rf, v.y * rf, v.z * rf, v.w * rf};
+            if (p.scale) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = y[e] * p.scale[col + e < p.N ? col + e : col];
+            }
+            float *dst = p.C + (size_t)row * p.ldc + col;
+            if (vec && col + 3 < p.N) {
+                *(float4 *)dst = make_float4(y[0], y[1], y[2], y[3]);
+            } else {
+                for (int e = 0; e < 4 && col + e < p.N; ++e) dst[e] = y[e];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 constexpr int DMA_LDS_MAX = 160 * 1024;
 constexpr int dma_stage_bytes(bool wi8, int T, int BM, int BN) {
     return T * BM * 128 + BN * (wi8 ? 64 : 128);
@@ -263,12 +412,45 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
     return bm == 128 ? launch_dma<WI8, T, 128, 128>(p, ns, st) : launch_dma<WI8, T, 64, 128>(p, ns, st);
 }
 
+template <int BM, int NS>
+static int launch_i8(const GemmParams &p, hipStream_t st) {
+    constexpr int stage = Q8_T * BM * 64 + 128 * 64;
+    static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
+    const dim3 grid((p.N + 127) / 128, (p.M + BM - 1) / BM);
+    gemm_dma_i8_kernel<BM, 128, NS><<<grid, 256, 0, st>>>(p);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 int launch_gemm(const GemmArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.N >= 1, "gemm: empty shape");
+    if (a.A8) {  // int8 rows x int8 weights
+        VMLM_GUARD(a.w_int8 && a.a8s && a.K > 0 && a.K % 64 == 0 && a.lda % 16 == 0 &&
+                       ((uintptr_t)a.W & 15) == 0 && ((uintptr_t)a.A8 & 15) == 0 && a.K % 16 == 0,
+                   "gemm (int8 rows): int8 weights, row factors, K %% 64 == 0, 16-byte aligned rows");
+        GemmParams p{};
+        p.W = (const uint8_t *)a.W;
+        p.scale = a.scale;
+        p.C = a.C;
+        p.tstride = (size_t)a.M * a.lda;
+        p.lda = a.lda;
+        p.M = a.M;
+        p.N = a.N;
+        p.K = a.K;
+        p.ldc = a.ldc;
+        p.A8 = a.A8;
+        p.a8s = a.a8s;
+        const int ns = a.stages ? a.stages : 3;
+        switch (ns) {  // 72 KB at 3 stages: two workgroups per CU
+        case 2: return launch_i8<64, 2>(p, st);
+        case 3: return launch_i8<64, 3>(p, st);
+        }
+        return fail(VMLM_ERR_UNIMPL, "gemm (int8 rows): %d LDS stages", ns);
+    }
     VMLM_GUARD(a.K > 0 && a.K % 64 == 0, "gemm: K=%d not a positive multiple of 64", a.K);
     VMLM_GUARD(((uintptr_t)a.W & 15) == 0 && ((uintptr_t)a.A & 15) == 0 && a.lda % 8 == 0,
                "gemm: operands must be 16-byte aligned");
-    GemmParams p;
+    GemmParams p{};
     p.W = (const uint8_t *)a.W;
     p.scale = a.scale;
     p.A = a.A;

@@ -412,6 +412,76 @@ int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int row
     return VMLM_OK;
 }
 
+// Rows as the int8 input of the int8-row GEMM: y = x, or with g the RMSNorm
+// y = (x * inv) * g, inv = 1 / sqrt(mean(x^2) + eps) (ops/src/kernels.rs:
+// 1346-1368); then Q8_T int8 terms of y with the row's power-of-two factor
+// (q8_split) into q8 [Q8_T][rows][cols] and q8s[row] = 2^-k. One workgroup
+// of 256 threads per row, 4 columns per thread and pass, cols <= 8192.
+constexpr int RQ_U = 8;
+__global__ __launch_bounds__(256) void rows_q8_kernel(const float *__restrict__ x, int ldx,
+                                                      const float *__restrict__ g, float eps,
+                                                      int cols, int rows,
+                                                      int8_t *__restrict__ q8,
+                                                      float *__restrict__ q8s) {
+    __shared__ float sh[4];
+    const int row = blockIdx.x, n4 = cols >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)row * ldx);
+    float4 v[RQ_U];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < RQ_U; ++u) {
+        const int c = threadIdx.x + u * 256;
+        v[u] = c < n4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+    }
+    if (g) {
+        ss = block_sum256(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+        for (int u = 0; u < RQ_U; ++u) {
+            const int c = threadIdx.x + u * 256;
+            if (c >= n4) continue;
+            const float4 gg = ((const float4 *)g)[c];
+            v[u] = make_float4(v[u].x * inv * gg.x, v[u].y * inv * gg.y, v[u].z * inv * gg.z,
+                               v[u].w * inv * gg.w);
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < RQ_U; ++u)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    mx = block_max256(mx, sh);
+    const int k = q8_row_k(mx);
+    if (threadIdx.x == 0) q8s[row] = ldexpf(1.0f, -k);
+#pragma unroll
+    for (int u = 0; u < RQ_U; ++u) {
+        const int c = threadIdx.x + u * 256;
+        if (c >= n4) continue;
+        int a[4][Q8_T];
+        q8_split(v[u].x, k, a[0]);
+        q8_split(v[u].y, k, a[1]);
+        q8_split(v[u].z, k, a[2]);
+        q8_split(v[u].w, k, a[3]);
+#pragma unroll
+        for (int t = 0; t < Q8_T; ++t)
+            *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + 4 * c) =
+                pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+    }
+}
+
+int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
+                   int8_t *q8, float *q8s, hipStream_t st) {
+    if (rows == 0) return VMLM_OK;
+    VMLM_GUARD(cols % 16 == 0 && cols <= 4 * 256 * RQ_U && ldx % 4 == 0 &&
+                   ((uintptr_t)x & 15) == 0 && (!g || ((uintptr_t)g & 15) == 0) &&
+                   ((uintptr_t)q8 & 15) == 0 && q8s && rows <= 0x7fffffff,
+               "rows_q8: cols %% 16 == 0, cols <= %d, 16-byte aligned rows", 4 * 256 * RQ_U);
+    rows_q8_kernel<<<(unsigned)rows, 256, 0, st>>>(x, (int)ldx, g, eps, (int)cols, (int)rows, q8,
+                                                   q8s);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 // ops/src/kernels.rs:1388-1414 -- max, exp_f(x-max), sum, * (1/sum), causal tail 0.
 __global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ p, int cols,
                                                       int causal) {

@@ -74,23 +74,17 @@ __global__ void kv_fill_kernel(const float *__restrict__ qkv, int ldq, int H, in
     vc[o] = row[2 * H + h * 64 + d];
 }
 
-// Prefill MLP: act = silu(gate) * up from the interleaved GEMM output, plus
-// its bf16 terms (same element operations as ACT silu then EWMUL).
+// Prefill MLP: act = silu(gate) * up from the interleaved GEMM output (the
+// element operations of ACT silu then EWMUL).
 __global__ void silu_mul_kernel(const float *__restrict__ gu, int I, int M,
-                                float *__restrict__ act, uint16_t *__restrict__ terms, int T) {
+                                float *__restrict__ act) {
     size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (size_t)M * I) return;
     const int m = idx / I, j = idx % I;
     const int pg = (j / 16) * 32 + (j % 16);
     const float gate = gu[(size_t)m * 2 * I + pg];
     const float up = gu[(size_t)m * 2 * I + pg + 16];
-    float a = (gate / (1.0f + exp_f(-gate))) * up;
-    act[idx] = a;
-    for (int t = 0; t < T; ++t) {
-        uint32_t hb = bf16_rne_bits(a);
-        a = a - bf16_bits_to_f32(hb);
-        terms[((size_t)t * M + m) * I + j] = (uint16_t)hb;
-    }
+    act[idx] = (gate / (1.0f + exp_f(-gate))) * up;
 }
 
 }  // namespace vmlm
@@ -569,9 +563,9 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     hipStream_t st = d->st;
     const size_t B = d->B, H = d->H, I = d->I, NH = d->NH, M = B * S;
     const int T = 3;
-    // per-prefill buffers
-    float *h, *h2, *qkv, *att, *o, *gu, *act;
-    uint16_t *terms;
+    // per-prefill buffers; every projection input is int8 rows (a8, a8s)
+    float *h, *h2, *qkv, *att, *o, *gu, *act, *a8s;
+    int8_t *a8;
     int32_t *toks;
     char *kvw;
     std::vector<void *> tmp;
@@ -588,7 +582,8 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     };
     if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
         (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) || (rc = get(&gu, M * 2 * I * 4)) ||
-        (rc = get(&act, M * I * 4)) || (rc = get(&terms, (size_t)T * M * I * 2)) ||
+        (rc = get(&act, M * I * 4)) || (rc = get(&a8, (size_t)Q8_T * M * I)) ||
+        (rc = get(&a8s, M * 4)) ||
         (rc = get(&toks, M * 4)) ||
         (rc = get(&kvw, attention_prefill_work_bytes((int)S, (int)NH, (int)B)))) {
         release();
@@ -599,13 +594,12 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         int r = launch_emb_bf16(h, H, d->embed, d->V, H, nullptr, toks, (int)M, st);
         if (r) return r;
         for (size_t l = 0; l < d->L; ++l) {
-            if ((r = launch_rmsnorm(nullptr, h, d->InLn(l), M, H, d->c.eps, terms, T, (int)H, st)))
-                return r;
+            if ((r = launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st))) return r;
             GemmArgs g;
             g.W = d->Wqkv(l);
             g.scale = d->Sqkv(l);
-            g.A = terms;
-            g.T = T;
+            g.A8 = a8;
+            g.a8s = a8s;
             g.lda = (int)H;
             g.M = (int)M;
             g.N = (int)(3 * H);
@@ -625,7 +619,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
                                               st, true, d->rope_step, 0.0f, (int)B, S * 3 * H,
                                               S * H)))
                 return r;
-            if ((r = launch_split_terms(att, H, (int)M, (int)H, T, terms, (int)H, st))) return r;
+            if ((r = launch_rows_q8(att, H, nullptr, 0.0f, M, H, a8, a8s, st))) return r;
             GemmArgs go = g;
             go.W = d->Wo(l);
             go.scale = d->So(l);
@@ -634,9 +628,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             go.ldc = (int)H;
             if ((r = launch_gemm(go, st))) return r;
             if ((r = launch_ew(h2, h, o, M * H, VMLM_OP_EWADD, st))) return r;
-            if ((r = launch_rmsnorm(nullptr, h2, d->PostLn(l), M, H, d->c.eps, terms, T, (int)H,
-                                    st)))
-                return r;
+            if ((r = launch_rows_q8(h2, H, d->PostLn(l), d->c.eps, M, H, a8, a8s, st))) return r;
             GemmArgs ggu = g;
             ggu.W = d->Wgu(l);
             ggu.scale = d->Sgu(l);
@@ -644,8 +636,9 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             ggu.C = gu;
             ggu.ldc = (int)(2 * I);
             if ((r = launch_gemm(ggu, st))) return r;
-            silu_mul_kernel<<<cdiv(M * I, 256), 256, 0, st>>>(gu, (int)I, (int)M, act, terms, T);
+            silu_mul_kernel<<<cdiv(M * I, 256), 256, 0, st>>>(gu, (int)I, (int)M, act);
             VMLM_HIP_CHECK(hipGetLastError());
+            if ((r = launch_rows_q8(act, I, nullptr, 0.0f, M, I, a8, a8s, st))) return r;
             GemmArgs gd = g;
             gd.W = d->Wd(l);
             gd.scale = d->Sd(l);
