@@ -206,8 +206,10 @@ static int download(void *host, const void *dev, size_t bytes, hipStream_t st) {
 static inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
 // int8 / bf16 weight GEMM on device operands: C[m,n] = A[m,k] . W[n,k]^T (* scale).
-// Pads K to a multiple of 64 when needed, splits A into 3 bf16 terms, then the
-// GEMV kernel (m <= 16) or the tiled MFMA GEMM.
+// Pads K to a multiple of 128 when needed, then: int8 weights and m <= 16,
+// the wide k-split GEMV; int8 weights, m > 16 and K unpadded, int8 rows and
+// the int8 MFMA GEMM; otherwise A split into 3 bf16 terms and the GEMV kernel
+// (m <= 16) or the tiled bf16 MFMA GEMM.
 static int q_matmul(const float *a, const void *W, bool wi8, const float *scale, float *c,
                     size_t m, size_t n, size_t k, hipStream_t st) {
     if (m == 0 || n == 0) return VMLM_OK;
@@ -257,6 +259,28 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         int rc = launch_gemv(g, st);
         if (rc) return rc;
         return launch_gemv_reduce(part, ks, (int)m, (int)n, scale, c, (int)n, st);
+    }
+    // int8 weights, many rows, unpadded K: the rows as int8 terms with a
+    // per-row factor, then the int8 x int8 MFMA GEMM
+    if (wi8 && m > 16 && Wd == W && Kp == k && k <= 8192 && ((uintptr_t)a & 15) == 0) {
+        int8_t *a8 = stg.alloc<int8_t>((size_t)Q8_T * m * k);
+        float *a8s = stg.alloc<float>(m);
+        STAGE_OK(stg);
+        int rc = launch_rows_q8(a, k, nullptr, 0.0f, m, k, a8, a8s, st);
+        if (rc) return rc;
+        GemmArgs g;
+        g.W = Wd;
+        g.w_int8 = true;
+        g.scale = scale;
+        g.A8 = a8;
+        g.a8s = a8s;
+        g.lda = (int)k;
+        g.M = (int)m;
+        g.N = (int)n;
+        g.K = (int)k;
+        g.C = c;
+        g.ldc = (int)n;
+        return launch_gemm(g, st);
     }
     uint16_t *terms = stg.alloc<uint16_t>((size_t)T * m * Kp);
     STAGE_OK(stg);

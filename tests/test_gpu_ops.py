@@ -54,6 +54,32 @@ def test_gemm_nt_int8(ops, oracle, m, n, k):
     assert_close_rms(ops.gemm_nt_int8(a, q, s), oracle.gemm_nt_int8(a, q, s))
 
 
+def test_gemm_nt_int8_rows_of_mixed_magnitude(ops, oracle):
+    """M > 16 runs on int8 rows with one power-of-two factor per row: rows
+    scaled from 1e-6 to 1e6 each stay within 1e-4 of their own RMS, and a
+    zero row gives zeros."""
+    rng = np.random.default_rng(17)
+    a, q, s = q8_case(rng, 48, 320, 1024)
+    a *= np.float32(10.0) ** rng.integers(-6, 7, size=(48, 1)).astype(np.float32)
+    a[7] = 0.0
+    got, ref = ops.gemm_nt_int8(a, q, s), oracle.gemm_nt_int8(a, q, s)
+    assert not got[7].any()
+    for i in range(48):
+        if i != 7:
+            assert_close_rms(got[i], ref[i])
+
+
+def test_gemm_nt_int8_exact_case_many_rows(ops):
+    """Integer activations at M > 16 (int8 rows): each row's terms are exact
+    and so is every int32 sum, so the result is exact."""
+    rng = np.random.default_rng(6)
+    a = rng.integers(-3, 4, size=(40, 512)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(130, 512), dtype=np.int8)
+    s = np.full(130, 1 / 64, np.float32)
+    ref = (a.astype(np.float64) @ q.astype(np.float64).T) / 64
+    assert np.array_equal(ops.gemm_nt_int8(a, q, s).astype(np.float64), ref)
+
+
 def test_gemm_nt_int8_exact_case(ops):
     """Integer activations and power-of-two scales: every term and partial
     sum is exact, so the result is exact."""
