@@ -265,6 +265,8 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     if (wi8 && m > 16 && Wd == W && Kp == k && k <= 8192 && ((uintptr_t)a & 15) == 0) {
         int8_t *a8 = stg.alloc<int8_t>((size_t)Q8_T * m * k);
         float *a8s = stg.alloc<float>(m);
+        const size_t gw = gemm_i8_work_floats((int)m, (int)n, (int)k);
+        float *gwork = gw ? stg.alloc<float>(gw) : nullptr;
         STAGE_OK(stg);
         int rc = launch_rows_q8(a, k, nullptr, 0.0f, m, k, a8, a8s, st);
         if (rc) return rc;
@@ -274,6 +276,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         g.scale = scale;
         g.A8 = a8;
         g.a8s = a8s;
+        g.work = gwork;
         g.lda = (int)k;
         g.M = (int)m;
         g.N = (int)n;

@@ -145,8 +145,16 @@ struct GemmArgs {
     // row factors [M] from launch_rows_q8 (A and T unused)
     const int8_t *A8 = nullptr;
     const float *a8s = nullptr;
+    // int8 rows, optional: gemm_i8_work_floats() floats for the k-slices of
+    // a grid that would leave most CUs idle (null: one slice)
+    float *work = nullptr;
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
+int gemm_i8_kslices(int M, int N, int K);
+inline size_t gemm_i8_work_floats(int M, int N, int K) {
+    const int ks = gemm_i8_kslices(M, N, K);
+    return ks > 1 ? (size_t)ks * M * N : 0;
+}
 
 // f32 GEMMs (NT and NN) with optional accumulate.
 // work: gemm_f32_work_floats() floats (narrow outputs are split over k; null: no split).

@@ -21,6 +21,7 @@ struct GemmParams {
     int lda, M, N, K, ldc;
     const int8_t *A8;   // int8 rows: Q8_T term planes [Q8_T][M][lda] and
     const float *a8s;   // row factors [M] (gemm_dma_i8_kernel)
+    float *part;        // k-slices > 1: raw sums times the row factor [ks][M][N]
 };
 
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int gi32x4;
@@ -254,7 +255,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int wm = wave >> 1, wn = wave & 1;
     const int g = lane >> 4, r = lane & 15;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int nk = p.K / 64;
+    // this workgroup's k-steps [kb0, kb0 + nk): all, or k-slice blockIdx.z
+    const int nkt = p.K / 64, ksl = (int)gridDim.z;
+    const int kb0 = (int)blockIdx.z * nkt / ksl;
+    const int nk = ((int)blockIdx.z + 1) * nkt / ksl - kb0;
 
     // copy plan: each instruction fills 16 rows x 64 B of LDS; lane i brings
     // piece (i & 3) ^ ((R >> 1) & 3) of row R = 16 * instr + i / 4
@@ -279,7 +283,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
     auto issue = [&](int kt) {
-        const int kc = kt < nk ? kt : nk - 1;
+        const int kc = kb0 + (kt < nk ? kt : nk - 1);
         const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
 #pragma unroll
         for (int q = 0; q < A_INS; ++q)
@@ -355,12 +359,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (row >= p.M || col >= p.N) continue;
             const float rf = p.a8s[row];
             float y[4] = {v.x * rf, v.y * rf, v.z * rf, v.w * rf};
-            if (p.scale) {
+            if (p.scale && ksl == 1) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) y[e] = y[e] * p.scale[col + e < p.N ? col + e : col];
             }
-            float *dst = p.C + (size_t)row * p.ldc + col;
-            if (vec && col + 3 < p.N) {
+            float *dst = ksl == 1 ? p.C + (size_t)row * p.ldc + col
+                                  : p.part + ((size_t)blockIdx.z * p.M + row) * p.N + col;
+            if ((ksl > 1 || vec) && col + 3 < p.N) {
                 *(float4 *)dst = make_float4(y[0], y[1], y[2], y[3]);
             } else {
                 for (int e = 0; e < 4 && col + e < p.N; ++e) dst[e] = y[e];
@@ -413,13 +418,21 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
 }
 
 template <int BM, int NS>
-static int launch_i8(const GemmParams &p, hipStream_t st) {
+static int launch_i8(const GemmParams &p, int ksl, hipStream_t st) {
     constexpr int stage = Q8_T * BM * 64 + 128 * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
-    const dim3 grid((p.N + 127) / 128, (p.M + BM - 1) / BM);
+    const dim3 grid((p.N + 127) / 128, (p.M + BM - 1) / BM, ksl);
     gemm_dma_i8_kernel<BM, 128, NS><<<grid, 256, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
-    return VMLM_OK;
+    if (ksl == 1) return VMLM_OK;
+    return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
+}
+
+int gemm_i8_kslices(int M, int N, int K) {
+    if (N % 4) return 1;  // the partial rows are written as 16-byte stores
+    const int wgs = ((N + 127) / 128) * ((M + 63) / 64), nk = K / 64;
+    const int ks = wgs < 64 ? 4 : wgs < 160 ? 2 : 1;  // fill the 256 CUs
+    return nk >= 8 * ks ? ks : 1;
 }
 
 int launch_gemm(const GemmArgs &a, hipStream_t st) {
@@ -440,12 +453,16 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         p.ldc = a.ldc;
         p.A8 = a.A8;
         p.a8s = a.a8s;
+        // skinny grids: ordered k-slices through `work`, then the in-order
+        // slice reduction applies the column scale
+        const int ksl = a.work ? gemm_i8_kslices(a.M, a.N, a.K) : 1;
+        p.part = a.work;
         const int ns = a.stages ? a.stages : 3;
         // 64 x 128 tiles: 128-row tiles need 256 accumulator registers, run one
         // wave per SIMD and measured 30 % slower at the prefill shapes
         switch (ns) {  // 72 KB at 3 stages: two workgroups per CU
-        case 2: return launch_i8<64, 2>(p, st);
-        case 3: return launch_i8<64, 3>(p, st);
+        case 2: return launch_i8<64, 2>(p, ksl, st);
+        case 3: return launch_i8<64, 3>(p, ksl, st);
         }
         return fail(VMLM_ERR_UNIMPL, "gemm (int8 rows): %d LDS stages", ns);
     }

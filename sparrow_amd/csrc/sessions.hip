@@ -564,7 +564,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     const size_t B = d->B, H = d->H, I = d->I, NH = d->NH, M = B * S;
     const int T = 3;
     // per-prefill buffers; every projection input is int8 rows (a8, a8s)
-    float *h, *h2, *qkv, *att, *o, *gu, *act, *a8s;
+    float *h, *h2, *qkv, *att, *o, *gu, *act, *a8s, *gwork = nullptr;
     int8_t *a8;
     int32_t *toks;
     char *kvw;
@@ -589,6 +589,15 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         release();
         return rc;
     }
+    // k-slice work of the int8-row GEMMs whose grids would leave CUs idle
+    const size_t gw = std::max(std::max(gemm_i8_work_floats((int)M, (int)(3 * H), (int)H),
+                                        gemm_i8_work_floats((int)M, (int)H, (int)H)),
+                               std::max(gemm_i8_work_floats((int)M, (int)(2 * I), (int)H),
+                                        gemm_i8_work_floats((int)M, (int)H, (int)I)));
+    if (gw && (rc = get(&gwork, gw * 4))) {
+        release();
+        return rc;
+    }
     auto run = [&]() -> int {
         VMLM_HIP_CHECK(hipMemcpyAsync(toks, tokens, M * 4, hipMemcpyHostToDevice, st));
         int r = launch_emb_bf16(h, H, d->embed, d->V, H, nullptr, toks, (int)M, st);
@@ -600,6 +609,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             g.scale = d->Sqkv(l);
             g.A8 = a8;
             g.a8s = a8s;
+            g.work = gwork;
             g.lda = (int)H;
             g.M = (int)M;
             g.N = (int)(3 * H);

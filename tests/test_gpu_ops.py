@@ -69,12 +69,14 @@ def test_gemm_nt_int8_rows_of_mixed_magnitude(ops, oracle):
             assert_close_rms(got[i], ref[i])
 
 
-def test_gemm_nt_int8_exact_case_many_rows(ops):
+@pytest.mark.parametrize("k", [512, 2304])
+def test_gemm_nt_int8_exact_case_many_rows(ops, k):
     """Integer activations at M > 16 (int8 rows): each row's terms are exact
-    and so is every int32 sum, so the result is exact."""
+    and so is every int32 sum, so the result is exact; at K = 2304 the small
+    grid runs as ordered k-slices, whose partial sums are exact too."""
     rng = np.random.default_rng(6)
-    a = rng.integers(-3, 4, size=(40, 512)).astype(np.float32)
-    q = rng.integers(-127, 128, size=(130, 512), dtype=np.int8)
+    a = rng.integers(-3, 4, size=(40, k)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(130, k), dtype=np.int8)
     s = np.full(130, 1 / 64, np.float32)
     ref = (a.astype(np.float64) @ q.astype(np.float64).T) / 64
     assert np.array_equal(ops.gemm_nt_int8(a, q, s).astype(np.float64), ref)
