@@ -218,9 +218,17 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     Stage stg(st);
     const void *Wd = W;
     if (Kp != k || ((uintptr_t)W & 15)) {
+        // the padded weight copy is a device copy: refused up front while the
+        // stream is being captured, so a capture never records it
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        VMLM_HIP_CHECK(hipStreamIsCapturing(st, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(VMLM_ERR_UNIMPL, "q8/bf16 GEMM with K %% 128 != 0 or unaligned weights "
+                                         "stages a padded weight copy and cannot be captured");
         uint8_t *wp = stg.alloc<uint8_t>(n * Kp * esz);
         STAGE_OK(stg);
-        VMLM_HIP_CHECK(hipMemsetAsync(wp, 0, n * Kp * esz, st));
+        int rc0 = launch_fill_zero(wp, n * Kp * esz, st);
+        if (rc0) return rc0;
         if (k) VMLM_HIP_CHECK(hipMemcpy2DAsync(wp, Kp * esz, W, k * esz, k * esz, n,
                                                hipMemcpyDeviceToDevice, st));
         Wd = wp;
@@ -283,7 +291,10 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         g.K = (int)k;
         g.C = c;
         g.ldc = (int)n;
-        return launch_gemm(g, st);
+        rc = launch_gemm(g, st);
+        if (rc) return rc;
+        return launch_gemm_i8_nonfinite_rows(a, (int)k, (const int8_t *)Wd, (int)k, scale, a8s, c,
+                                             (int)n, (int)m, (int)n, (int)k, st);
     }
     uint16_t *terms = stg.alloc<uint16_t>((size_t)T * m * Kp);
     STAGE_OK(stg);

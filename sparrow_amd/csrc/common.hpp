@@ -65,17 +65,28 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
 }
 
+// What is left of y after its bf16 term h: y - h, or 0 when y is not
+// finite (inf - inf would be NaN), so an infinite value sits in its first
+// term alone and its products stay +-inf (NaN against a zero weight).
+__device__ __forceinline__ float term_rem(float y, uint32_t h) {
+    const float r = y - bf16_bits_to_f32(h);
+    return r == r ? r : 0.0f;
+}
+
 // Splits f32 x into up to three bf16 terms hi + mid + lo whose sum equals x
 // to within 2^-24 |x| (each residual is exact in f32). Products of a bf16
 // term with a bf16 (or small-integer) weight are exact in f32, so an MFMA
 // over the terms reproduces f32 x . w up to the order of f32 accumulation.
+// A non-finite x keeps its value in the first term and zeros in the others
+// (inf - inf would make the residual NaN), so the products of an infinite
+// activation are +-inf, or NaN against a zero weight, as in the f32 product.
 template <int T>
 __device__ __forceinline__ void split_bf16(float x, uint32_t (&t)[T]) {
     float r = x;
 #pragma unroll
     for (int i = 0; i < T; ++i) {
         t[i] = bf16_rne_bits(r);
-        r = r - bf16_bits_to_f32(t[i]);
+        r = term_rem(r, t[i]);
     }
 }
 
@@ -108,16 +119,34 @@ __device__ __forceinline__ void i8x16_to_bf16(u32x4 w, u32x4 &lo, u32x4 &hi) {
 // further term is rint of the remainder times 128, so
 // u = a0 + a1/2^7 + a2/2^14 + a3/2^21 + e with |e| <= 2^-22: 28 bits below the
 // row maximum (f32 carries 24). |a0| <= 127, |a1..a3| <= 64; every step is
-// exact in f32. NaN gives 0 terms; a non-finite maximum gives the scale 1.
+// exact in f32. k is clamped to [-126, 126] (rows whose maximum is below
+// 2^-120 keep fewer bits).
+//
+// Non-finite rows: the magnitude used for the maximum maps NaN to +inf
+// (q8_mag; fmaxf alone would drop a NaN), a non-finite maximum gives
+// k = Q8_NONFINITE, whose factor is NaN and whose terms are 0. Every output
+// of such a row is then NaN, never a finite value. (The standalone GEMM
+// recomputes those rows in f32 to give the exact +-inf / NaN pattern.)
 constexpr int Q8_T = 4;
+constexpr int Q8_NONFINITE = 0x4000;
+__device__ __forceinline__ float q8_mag(float y) {
+    const float a = fabsf(y);
+    return a == a ? a : __builtin_inff();
+}
 __device__ __forceinline__ int q8_row_k(float mx) {
-    if (!(mx > 0.0f) || mx > 3.0e38f) return 0;
+    if (!(mx <= 3.40282347e38f)) return Q8_NONFINITE;
+    if (!(mx > 0.0f)) return 0;
     int k = 6 - ilogbf(mx);
-    if (mx * ldexpf(1.0f, k) > 127.0f) --k;
-    return k < -120 ? -120 : k > 120 ? 120 : k;
+    if (ldexpf(mx, k) > 127.0f) --k;
+    return k < -126 ? -126 : k > 126 ? 126 : k;
+}
+// the factor a consumer multiplies the term sums by: 2^-k, NaN for a
+// non-finite row
+__device__ __forceinline__ float q8_factor(int k) {
+    return k == Q8_NONFINITE ? __builtin_nanf("") : ldexpf(1.0f, -k);
 }
 __device__ __forceinline__ void q8_split(float y, int k, int (&a)[Q8_T]) {
-    float u = ldexpf(y, k);
+    float u = k == Q8_NONFINITE ? 0.0f : ldexpf(y, k);
     if (!(u == u)) u = 0.0f;
     // the scale keeps |u| <= 127 up to a few ulps of a bounding estimate;
     // 127.25 still rounds to 127 and leaves the excess to the next term

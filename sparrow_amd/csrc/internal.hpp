@@ -150,6 +150,13 @@ struct GemmArgs {
     float *work = nullptr;
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
+// Recomputes in f32 the rows of an int8-row GEMM whose factor a8s[i] is NaN
+// (non-finite inputs), giving the reference's +-inf / NaN pattern.
+int launch_gemm_i8_nonfinite_rows(const float *a, int lda, const int8_t *q, int ldq,
+                                  const float *scale, const float *a8s, float *c, int ldc, int M,
+                                  int N, int K, hipStream_t st);
+// Zero-fills `bytes` bytes with a kernel (capturable, unlike hipMemsetAsync).
+int launch_fill_zero(void *p, size_t bytes, hipStream_t st);
 int gemm_i8_kslices(int M, int N, int K);
 inline size_t gemm_i8_work_floats(int M, int N, int K) {
     const int ks = gemm_i8_kslices(M, N, K);

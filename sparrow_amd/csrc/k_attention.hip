@@ -169,7 +169,7 @@ int launch_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t n
                     bool acc, bool b_is_nt, hipStream_t st, float *work) {
     if (m == 0 || n == 0) return VMLM_OK;
     if (k == 0) {
-        if (!acc) VMLM_HIP_CHECK(hipMemsetAsync(c, 0, m * n * sizeof(float), st));
+        if (!acc) return launch_fill_zero(c, m * n * sizeof(float), st);
         return VMLM_OK;
     }
     VMLM_GUARD(m <= 0x7fffffffu && n <= 0x7fffffffu && k <= 0x7fffffffu, "gemm f32: shape too large");
@@ -876,7 +876,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     if (terms) {
         for (int t = 0; t < T; ++t) {
             const uint32_t hb = bf16_rne_bits(y);
-            y = y - bf16_bits_to_f32(hb);
+            y = term_rem(y, hb);
             terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
         }
     }
@@ -904,7 +904,7 @@ __global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float *__re
     if (terms) {
         for (int t = 0; t < T; ++t) {
             const uint32_t hb = bf16_rne_bits(y);
-            y = y - bf16_bits_to_f32(hb);
+            y = term_rem(y, hb);
             terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
         }
     }

@@ -67,10 +67,20 @@ __global__ __launch_bounds__(64) void b1_forward_kernel(const float *__restrict_
         for (int j = 1; j < k0; ++j) acc = acc + wi[j] * xt[(size_t)si[j] * t8 + t];
         y = acc;
     } else {
-        // b1_forward: packed rows for k0 in {1,4,8} (k0 == 2 computes the row
-        // sum; see the header note on the reference's k0 == 2 branch)
+        // b1_forward: packed rows for k0 in {1,2,4,8}. At k0 == 2 the
+        // reference reduces a 128-bit half that holds two rows' products, so
+        // rows 2r and 2r + 1 (r < n / 4 * 2) both get the sum of the pair's
+        // four products, (p0+p2)+(p1+p3) and (p2+p0)+(p3+p1) for the odd row
+        // (ops/src/kernels.rs:2748-2766).
         if (k0 == 1 && i < (n / 8) * 8) {
             y = wi[0] * xt[(size_t)si[0] * t8 + t];
+        } else if (k0 == 2 && i < (n / 4) * 4) {
+            const float *wp = w + (size_t)(i & ~1) * 2;
+            const uint32_t *sp = src + (size_t)(i & ~1) * 2;
+            float p[4];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) p[l] = wp[l] * xt[(size_t)sp[l] * t8 + t];
+            y = (i & 1) ? hsum4(p[2], p[3], p[0], p[1]) : hsum4(p[0], p[1], p[2], p[3]);
         } else if (k0 == 4 && i < (n / 2) * 2) {
             float p[4];
 #pragma unroll

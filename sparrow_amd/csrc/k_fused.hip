@@ -80,7 +80,7 @@ __device__ __forceinline__ void store_terms(uint16_t *dst, size_t plane, size_t 
 #pragma unroll
     for (int q = 0; q < FK_T; ++q) {
         const uint32_t hb = bf16_rne_bits(v);
-        v = v - bf16_bits_to_f32(hb);
+        v = term_rem(v, hb);
         dst[q * plane + o] = (uint16_t)hb;
     }
 }

@@ -435,6 +435,61 @@ int gemm_i8_kslices(int M, int N, int K) {
     return nk >= 8 * ks ? ks : 1;
 }
 
+// Rows of an int8-row GEMM whose factor is NaN (a NaN or infinite input,
+// q8_row_k) are recomputed here in f32 in the reference's order
+// (ops/src/kernels.rs:1256-1287: eight FMA lanes over k, the 8 -> 1 fold,
+// the scalar tail, then the scale), so their +-inf / NaN pattern is the
+// reference's. One thread per output column; each workgroup scans the row
+// factors 256 at a time into an LDS list and skips clean rows, so a GEMM
+// without such rows pays one short launch.
+__global__ __launch_bounds__(256) void gemm_i8_nonfinite_rows_kernel(
+    const float *__restrict__ a, int lda, const int8_t *__restrict__ q, int ldq,
+    const float *__restrict__ scale, const float *__restrict__ a8s, float *__restrict__ c,
+    int ldc, int M, int N, int K) {
+    __shared__ int list[256];
+    __shared__ int cnt;
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    for (int base = 0; base < M; base += 256) {
+        if (threadIdx.x == 0) cnt = 0;
+        __syncthreads();
+        const int r = base + threadIdx.x;
+        if (r < M) {
+            const float f = a8s[r];
+            if (!(f == f)) list[atomicAdd(&cnt, 1)] = r;
+        }
+        __syncthreads();
+        const int n = cnt;
+        for (int e = 0; e < n && j < N; ++e) {
+            const int i = list[e];
+            const float *ar = a + (size_t)i * lda;
+            const int8_t *qr = q + (size_t)j * ldq;
+            float acc[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+            int kk = 0;
+            for (; kk + 8 <= K; kk += 8) {
+#pragma unroll
+                for (int l = 0; l < 8; ++l)
+                    acc[l] = __builtin_fmaf(ar[kk + l], (float)qr[kk + l], acc[l]);
+            }
+            float s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+            for (; kk < K; ++kk) s += ar[kk] * (float)qr[kk];
+            c[(size_t)i * ldc + j] = s * scale[j];
+        }
+        __syncthreads();
+    }
+}
+
+int launch_gemm_i8_nonfinite_rows(const float *a, int lda, const int8_t *q, int ldq,
+                                  const float *scale, const float *a8s, float *c, int ldc, int M,
+                                  int N, int K, hipStream_t st) {
+    if (M <= 0 || N <= 0) return VMLM_OK;
+    gemm_i8_nonfinite_rows_kernel<<<(N + 255) / 256, 256, 0, st>>>(a, lda, q, ldq, scale, a8s, c,
+                                                                   ldc, M, N, K);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 int launch_gemm(const GemmArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.N >= 1, "gemm: empty shape");
     if (a.A8) {  // int8 rows x int8 weights

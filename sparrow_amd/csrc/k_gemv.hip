@@ -238,7 +238,7 @@ __global__ __launch_bounds__(GEMV_NW * 64) void gemv_kernel(GemvParams p) {
             p.Y[(size_t)b * p.ldy + jo] = a;
             for (int tt = 0; tt < p.Tout; ++tt) {
                 const uint32_t h = bf16_rne_bits(a);
-                a = a - bf16_bits_to_f32(h);
+                a = term_rem(a, h);
                 p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
             }
             continue;
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     hb[q] = bf16_rne_bits(y[q]);
-                    y[q] = y[q] - bf16_bits_to_f32(hb[q]);
+                    y[q] = term_rem(y[q], hb[q]);
                 }
                 const u32x4 pk = u32x4{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16),
                                        hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16)};
@@ -417,7 +417,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
             p.Y[(size_t)b * p.ldy + jo] = a;
             for (int tt = 0; tt < p.Tout; ++tt) {
                 const uint32_t h = bf16_rne_bits(a);
-                a = a - bf16_bits_to_f32(h);
+                a = term_rem(a, h);
                 p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
             }
         }
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(512) void gemv_wloop_kernel(GemvParams p) {
             p.Y[(size_t)b * p.ldy + jo] = a;
             for (int tt = 0; tt < p.Tout; ++tt) {
                 const uint32_t h = bf16_rne_bits(a);
-                a = a - bf16_bits_to_f32(h);
+                a = term_rem(a, h);
                 p.Aout[((size_t)tt * p.M + b) * p.ldaout + jo] = (uint16_t)h;
             }
         }
@@ -683,7 +683,7 @@ __global__ void split_terms_kernel(const float *__restrict__ x, size_t ldx, int 
     float v = k < K ? x[(size_t)r * ldx + k] : 0.0f;
     for (int t = 0; t < T; ++t) {
         uint32_t h = bf16_rne_bits(v);
-        v = v - bf16_bits_to_f32(h);
+        v = term_rem(v, h);
         out[((size_t)t * rows + r) * ldo + k] = (uint16_t)h;
     }
 }

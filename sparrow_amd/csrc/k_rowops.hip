@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ dst,
         if (terms) {
             for (int t = 0; t < T; ++t) {
                 uint32_t h = bf16_rne_bits(y);
-                y = y - bf16_bits_to_f32(h);
+                y = term_rem(y, h);
                 terms[((size_t)t * rows + row) * ld_terms + i] = (uint16_t)h;
             }
         }
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void rmsnorm_v4_kernel(float *__restrict__ dst
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     h[q] = bf16_rne_bits(y[q]);
-                    y[q] = y[q] - bf16_bits_to_f32(h[q]);
+                    y[q] = term_rem(y[q], h[q]);
                 }
                 uint2 pk = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
                 *(uint2 *)(terms + ((size_t)t * rows + row) * ld_terms + 4 * c) = pk;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_resid_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             h[q] = bf16_rne_bits(y[q]);
-            y[q] = y[q] - bf16_bits_to_f32(h[q]);
+            y[q] = term_rem(y[q], h[q]);
         }
         *(uint2 *)(terms + ((size_t)t * rows + row) * ld_terms + 4 * c) =
             make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
@@ -272,15 +272,15 @@ __global__ __launch_bounds__(64) void resid_q8_kernel(
         xg[i] = make_float4(bb.x * gg.x, bb.y * gg.y, bb.z * gg.z, bb.w * gg.w);
         if (live) {
             ss += bb.x * bb.x + bb.y * bb.y + bb.z * bb.z + bb.w * bb.w;
-            mg = fmaxf(mg, fmaxf(fmaxf(fabsf(xg[i].x), fabsf(xg[i].y)),
-                                 fmaxf(fabsf(xg[i].z), fabsf(xg[i].w))));
+            mg = fmaxf(mg, fmaxf(fmaxf(q8_mag(xg[i].x), q8_mag(xg[i].y)),
+                                 fmaxf(q8_mag(xg[i].z), q8_mag(xg[i].w))));
         }
     }
     ss = wave_sum(ss);
     mg = wave_max(mg);
     const int k = q8_row_k(mg);
     if (lane == 0) {
-        q8s[(size_t)sgi * rows + row] = ldexpf(1.0f, -k);
+        q8s[(size_t)sgi * rows + row] = q8_factor(k);
         ssp[(size_t)sgi * rows + row] = ss;
     }
 #pragma unroll
@@ -375,14 +375,14 @@ __global__ __launch_bounds__(128) void silu_q8_kernel(const float *__restrict__ 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         y[q] = (gs[q] / (1.0f + exp_f(-gs[q]))) * us[q];
-        mx = fmaxf(mx, fabsf(y[q]));
+        mx = fmaxf(mx, q8_mag(y[q]));
     }
     mx = wave_max(live ? mx : 0.0f);
     if ((tid & 63) == 0) sh[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(sh[0], blockDim.x > 64 ? sh[1] : 0.0f);
     const int k = q8_row_k(mx);
-    if (tid == 0) q8s[(size_t)sgi * rows + row] = ldexpf(1.0f, -k);
+    if (tid == 0) q8s[(size_t)sgi * rows + row] = q8_factor(k);
     if (!live) return;
     int a[4][Q8_T];
 #pragma unroll
@@ -449,10 +449,10 @@ __global__ __launch_bounds__(256) void rows_q8_kernel(const float *__restrict__ 
     float mx = 0.0f;
 #pragma unroll
     for (int u = 0; u < RQ_U; ++u)
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+        mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(v[u].x), q8_mag(v[u].y)), fmaxf(q8_mag(v[u].z), q8_mag(v[u].w))));
     mx = block_max256(mx, sh);
     const int k = q8_row_k(mx);
-    if (threadIdx.x == 0) q8s[row] = ldexpf(1.0f, -k);
+    if (threadIdx.x == 0) q8s[row] = q8_factor(k);
 #pragma unroll
     for (int u = 0; u < RQ_U; ++u) {
         const int c = threadIdx.x + u * 256;
@@ -659,6 +659,32 @@ int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st
         scale_kernel<true><<<cdiv(cdiv(n, 4), 256), 256, 0, st>>>(dst, src, n, s);
     else
         scale_kernel<false><<<cdiv(n, 256), 256, 0, st>>>(dst, src, n, s);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+// Zero fill as a kernel, so that a caller's stream capture records only
+// kernel nodes. `head` bytes up to the first 16-byte boundary, `n16` 16-byte
+// stores, then `tail` bytes.
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t *__restrict__ p, size_t head,
+                                                        size_t n16, size_t tail) {
+    const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    if (tid < head) p[tid] = 0;
+    uint4 *q = (uint4 *)(p + head);
+    for (size_t i = tid; i < n16; i += stride) q[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < tail) p[head + 16 * n16 + tid] = 0;
+}
+
+int launch_fill_zero(void *ptr, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return VMLM_OK;
+    uint8_t *p = (uint8_t *)ptr;
+    size_t head = (16 - ((uintptr_t)p & 15)) & 15;
+    if (head > bytes) head = bytes;
+    const size_t n16 = (bytes - head) / 16, tail = bytes - head - 16 * n16;
+    size_t blocks = cdiv(n16 > 0 ? n16 : 1, (size_t)256);
+    if (blocks > 4096) blocks = 4096;
+    fill_zero_kernel<<<(unsigned)blocks, 256, 0, st>>>(p, head, n16, tail);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

@@ -173,6 +173,40 @@ def test_minicpm_batch1_64_greedy_tokens_identical(hip, oracle, minicpm):
     assert np.array_equal(got, chain), f"first divergence at {np.argmax(got != chain)}"
 
 
+def test_minicpm_batch16_64_greedy_tokens_identical(hip, oracle, minicpm, golden_dir):
+    """BASELINE config 3 at batch 16: 16 prompts of 128 ids, 64 greedy steps
+    on the k-slice program. Every sequence's 65 tokens equal the CPU
+    oracle's chain (tests/golden/minicpm2b_b16_chains.npz, written by
+    make_decoder_chains.py from oracle.DecoderOracle.generate); for
+    sequences 0 and 15 the oracle runs here as well, fed the chain, and the
+    last step's logits are within 1e-4 of their RMS."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = minicpm
+    gold = np.load(golden_dir / "minicpm2b_b16_chains.npz")
+    prompts = M.make_prompts(cfg, 16, 128, seed=3)
+    assert np.array_equal(prompts, gold["prompts"])
+    t = time.time()
+    with Decoder(cfg, batch=16, cap=200) as dec:
+        assert not dec.fused
+        dec.load(W)
+        t0, _ = dec.prefill(prompts)
+        toks, last = dec.decode(64, want_logits=True)
+    got = np.concatenate([t0[None, :], toks], 0).T
+    log(f"GPU batch-16 prefill+64 steps in {time.time() - t:.1f}s; "
+        f"min oracle margin {gold['margins'].min():.3e}")
+    for b in range(16):
+        assert np.array_equal(got[b], gold["tokens"][b]), \
+            f"sequence {b}: first divergence at {np.argmax(got[b] != gold['tokens'][b])}"
+    for b in (0, 15):
+        t = time.time()
+        ref = oracle.DecoderOracle(W, cfg, cap=200)
+        ref.prefill(prompts[b])
+        for i in range(64):
+            lr, _ = ref.step(gold["tokens"][b, i], 128 + i)
+        log(f"oracle logits of sequence {b} in {time.time() - t:.1f}s")
+        assert np.abs(last[b] - lr).max() <= 1e-4 * rms(lr)
+
+
 def test_minicpm_batch16_equals_batch1(hip, minicpm):
     """Batch-16 decode: each sequence's chain is bitwise the chain it gets
     alone (rows never mix), checked for sequences 0 and 9 over 8 steps."""

@@ -75,6 +75,9 @@ def dev(hip):
 
 
 @pytest.mark.parametrize("m,n,k", [(1024, 2048, 512),   # config 1
+                                   (1, 2048, 512),      # config 1, M = 1 (GEMV path)
+                                   (16, 2048, 512),     # GEMV path, 16 rows
+                                   (5, 300, 192),       # GEMV path, ragged N
                                    (2048, 4096, 128),   # 128-row tiles
                                    (130, 201, 192),     # ragged, odd row stride
                                    (17, 128, 64)])      # one k-step, one spare row

@@ -72,14 +72,66 @@ def test_gemm_nt_int8_rows_of_mixed_magnitude(ops, oracle):
 @pytest.mark.parametrize("k", [512, 2304])
 def test_gemm_nt_int8_exact_case_many_rows(ops, k):
     """Integer activations at M > 16 (int8 rows): each row's terms are exact
-    and so is every int32 sum, so the result is exact; at K = 2304 the small
-    grid runs as ordered k-slices, whose partial sums are exact too."""
+    and so is every int32 sum, so the result is exact. The grid is one
+    64 x 128 tile; at K = 2304 (36 k-steps) it runs as 4 ordered k-slices
+    (the rule needs N % 4 == 0 and at least 8 k-steps per slice), whose
+    partial sums are exact too; at K = 512 it runs unsliced."""
     rng = np.random.default_rng(6)
     a = rng.integers(-3, 4, size=(40, k)).astype(np.float32)
-    q = rng.integers(-127, 128, size=(130, k), dtype=np.int8)
-    s = np.full(130, 1 / 64, np.float32)
+    q = rng.integers(-127, 128, size=(128, k), dtype=np.int8)
+    s = np.full(128, 1 / 64, np.float32)
     ref = (a.astype(np.float64) @ q.astype(np.float64).T) / 64
     assert np.array_equal(ops.gemm_nt_int8(a, q, s).astype(np.float64), ref)
+
+
+def nonfinite_masks_equal(got, ref):
+    for f in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(f(got), f(ref)), f.__name__
+
+
+@pytest.mark.parametrize("m,k,path", [(40, 2304, "int8 rows"), (5, 2304, "k-split GEMV"),
+                                      (24, 200, "bf16 terms"), (3, 100, "GEMV")])
+def test_gemm_nt_int8_nonfinite(ops, oracle, m, k, path):
+    """NaN and +-inf activations give the reference's pattern: a NaN row is
+    all NaN; an infinite entry gives +-inf, or NaN where its weight is 0 or
+    where +inf and -inf products meet (ops/src/kernels.rs:1256-1287 in f32).
+    Rows without them stay within 1e-4 of their RMS. Covers the int8-row
+    GEMM (M > 16, K % 128 == 0: rows with a NaN factor are recomputed in
+    f32), the k-split GEMV (M <= 16) and the bf16-term paths."""
+    rng = np.random.default_rng(m + k)
+    n = 256
+    a, q, s = q8_case(rng, m, n, k)
+    a[1, 7] = np.nan
+    a[2, 9] = np.inf
+    a[2, 10] = np.inf
+    q[:40, 9] = 0                      # inf * 0 -> NaN in those columns
+    a[m - 1, 3] = -np.inf
+    a[m - 2, 4] = np.inf               # +inf and -inf in one row
+    a[m - 2, 5] = -np.inf
+    q[40:80, 5] = -q[40:80, 4]         # columns where both products have one sign
+    got, ref = ops.gemm_nt_int8(a, q, s), oracle.gemm_nt_int8(a, q, s)
+    nonfinite_masks_equal(got, ref)
+    assert np.isnan(got[1]).all()
+    assert np.isposinf(got[2]).any() and np.isneginf(got[2]).any() and np.isnan(got[2, :40]).all()
+    assert np.isfinite(got[m - 2]).sum() == 0
+    clean = [i for i in range(m) if i not in (1, 2, m - 1, m - 2)]
+    for i in clean:
+        assert_close_rms(got[i], ref[i])
+
+
+def test_gemm_nt_bf16_nonfinite(ops, oracle):
+    """bf16 weights (term-split activations): the same non-finite pattern."""
+    rng = np.random.default_rng(11)
+    for m in (3, 20):
+        a = rng.standard_normal((m, 256), dtype=np.float32)
+        b = (rng.standard_normal((64, 256), dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        b[:8, 6] = 0
+        a[0, 6] = np.inf
+        a[1, 2] = np.nan
+        got, ref = ops.gemm_nt_bf16(a, b), oracle.gemm_nt_bf16(a, b)
+        nonfinite_masks_equal(got, ref)
+        for i in range(2, m):
+            assert_close_rms(got[i], ref[i])
 
 
 def test_gemm_nt_int8_exact_case(ops):
@@ -283,10 +335,14 @@ def test_topk_idx_edges(ops, oracle):
     assert ops.topk_idx(x) == oracle.topk_idx(x)[1] == 5000.0
 
 
-@pytest.mark.parametrize("k0", [1, 4, 8, 20, 32, 37])
-def test_b1_forward_bitwise(ops, oracle, k0):
-    rng = np.random.default_rng(k0)
-    n = 200
+@pytest.mark.parametrize("k0,n", [(1, 200), (1, 203), (2, 200), (2, 203), (2, 3), (4, 200),
+                                  (4, 201), (8, 200), (20, 200), (32, 200), (37, 200)])
+def test_b1_forward_bitwise(ops, oracle, k0, n):
+    """b1_forward against the reference's packed rows (k0 in {1, 2, 4, 8},
+    including k0 == 2, where rows 2r and 2r + 1 both get the pair's sum) and
+    the 8-lane fold for the rows the packed path leaves (n not a multiple of
+    the rows per 256-bit vector)."""
+    rng = np.random.default_rng(k0 * 1000 + n)
     w = rng.standard_normal((n, k0), dtype=np.float32)
     src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
     x = rng.standard_normal(n, dtype=np.float32)
@@ -387,9 +443,11 @@ def test_attention_decode_cfg2(ops, oracle, H, pos):
 def test_graph_capture_replay(hip, oracle):
     """Device-API ops captured into a HIP graph (vmlm_hip_capture_begin/end)
     and replayed three times, with eager work and synchronisations between
-    the replays: every replay equals the eager result bitwise. A capture that
-    records a memset (gemm_nt with k = 0 clears C) is refused and the stream
-    stays usable."""
+    the replays: every replay equals the eager result bitwise. gemm_nt with
+    k = 0 clears C with a fill kernel, so it captures and replays like any
+    other op; a call that would stage a device copy (int8 GEMM with K not a
+    multiple of 128) returns 5 before it issues anything, and the capture
+    stays valid."""
     import ctypes as C
     rng = np.random.default_rng(7)
     rows, cols = 37, 1024
@@ -407,6 +465,12 @@ def test_graph_capture_replay(hip, oracle):
         out = np.empty((rows, cols), np.float32)
         assert hip.vmlm_hip_sync() == 0
         assert hip.vmlm_hip_memcpy_d2h(out.ctypes.data, dev, out.nbytes) == 0
+        return out
+
+    def down_bytes(dev, n):
+        out = np.empty(n, np.uint8)
+        assert hip.vmlm_hip_sync() == 0
+        assert hip.vmlm_hip_memcpy_d2h(out.ctypes.data, dev, n) == 0
         return out
 
     def seq():  # y = rmsnorm(x) * g; z = y + x
@@ -430,11 +494,31 @@ def test_graph_capture_replay(hip, oracle):
             assert hip.vmlm_hip_sync() == 0
             assert hip.vmlm_hip_graph_launch(graph, None) == 0
             assert np.array_equal(bits(down(dz)), bits(want)), r
-        # a captured memset is refused
+        # k = 0 zero-fills C with a kernel, so it captures like any other op
+        assert hip.vmlm_hip_memset(dw, 0xFF, 64) == 0
+        assert hip.vmlm_hip_sync() == 0
+        g0 = C.c_void_p()
         assert hip.vmlm_hip_capture_begin(None) == 0
-        hip.vmlm_hip_gemm_nt(dx, dx, dw, 4, 4, 0, False, None)
-        bad = C.c_void_p()
-        assert hip.vmlm_hip_capture_end(None, C.byref(bad)) != 0 and not bad.value
+        assert hip.vmlm_hip_gemm_nt(dx, dx, dw, 4, 4, 0, False, None) == 0
+        assert hip.vmlm_hip_capture_end(None, C.byref(g0)) == 0 and g0.value
+        try:
+            for r in range(3):
+                assert hip.vmlm_hip_memset(dw, 0xFF, 64) == 0
+                assert hip.vmlm_hip_sync() == 0
+                assert hip.vmlm_hip_graph_launch(g0, None) == 0
+                assert hip.vmlm_hip_sync() == 0
+                assert not down_bytes(dw, 64).any(), r
+        finally:
+            hip.vmlm_hip_graph_destroy(g0)
+        # a call that would stage a device copy is refused before it issues
+        # anything, and the capture stays empty and valid
+        assert hip.vmlm_hip_capture_begin(None) == 0
+        rc = hip.vmlm_hip_gemm_nt_int8(dx, dx, dx, dw, 2, 2, 100, None)
+        empty = C.c_void_p()
+        assert hip.vmlm_hip_capture_end(None, C.byref(empty)) == 0
+        assert rc == 5
+        if empty.value:
+            hip.vmlm_hip_graph_destroy(empty)
         assert seq() == 0
         assert np.array_equal(bits(down(dz)), bits(want))
     finally:

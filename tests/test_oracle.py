@@ -567,3 +567,103 @@ def test_decoder_tiny_decode_equals_reprefill(oracle):
     toks, margins = dec3.generate(prompt, 4)
     assert toks[0] == t0 and toks[1] == int(np.argmax(step_logits))
     assert np.all(margins >= 0)
+
+
+# ------------------------------------------------- decoder, independent pin
+def _f64_decoder_logits(W, cfg, tokens, variant=None):
+    """float64 forward of the decoder program over `tokens`, written from the
+    program text of tools/p12_build_minicpm.py:766-792 (layer) and :990-994
+    (final norm and LM head), with OP_ROPE's rotation (core/src/interp.rs:
+    1159-1223, angle pos * theta^(-2i/hd) in float64), OP_RMSNORM
+    y = (x * inv) * g, the int8 GEMM C = (A . Q^T) * scale and causal
+    softmax(scale * q.k) attention. It shares no code with the C oracle.
+    Returns the logits of every row; row p is what a decode step at position
+    p must give. `variant` plants one mistake for the can-fail controls."""
+    H, NH, HD, eps = cfg["hidden"], cfg["n_heads"], cfg["head_dim"], cfg["eps"]
+    S = len(tokens)
+    f = np.float64
+
+    def widen(t):
+        return (t.astype(np.uint32) << np.uint32(16)).view(np.float32).astype(f)
+
+    def rmsnorm(x, g):
+        inv = 1.0 / np.sqrt((x * x).mean(1, keepdims=True) + eps)
+        return (x * inv) * g.astype(f)
+
+    def q8(x, w, s):
+        return (x @ w.astype(f).T) * s.astype(f)
+
+    pos = np.arange(S, dtype=f)[:, None]
+    inv_freq = f(cfg["theta"]) ** (-2.0 * np.arange(HD // 2, dtype=f) / HD)
+    ang = pos * inv_freq
+    co, si = np.cos(ang), np.sin(ang)
+
+    def rope(x):
+        x1, x2 = x[:, :HD // 2], x[:, HD // 2:]
+        return np.concatenate([x1 * co - x2 * si, x1 * si + x2 * co], 1)
+
+    causal = np.tril(np.ones((S, S), bool))
+    h = widen(W["embed"][np.asarray(tokens)])
+    for L in W["layers"]:
+        in_ln, post_ln = (L["post_ln"], L["in_ln"]) if variant == "norms_swapped" else \
+            (L["in_ln"], L["post_ln"])
+        xn = rmsnorm(h, in_ln)
+        q, k, v = q8(xn, L["wq"], L["sq"]), q8(xn, L["wk"], L["sk"]), q8(xn, L["wv"], L["sv"])
+        att = np.empty_like(q)
+        for hh in range(NH):
+            cs = slice(hh * HD, (hh + 1) * HD)
+            sc = rope(q[:, cs]) @ rope(k[:, cs]).T * f(cfg["attn_scale"])
+            sc = np.where(causal, sc, -np.inf)
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            att[:, cs] = p @ v[:, cs]
+        h2 = h + q8(att, L["wo"], L["so"])
+        xn = rmsnorm(h2, post_ln)
+        gate, up = q8(xn, L["wg"], L["sg"]), q8(xn, L["wu"], L["su"])
+        if variant == "gate_up_swapped":
+            gate, up = up, gate
+        acts = gate / (1.0 + np.exp(-gate)) * up
+        h = (h if variant == "residual_from_h" else h2) + q8(acts, L["wd"], L["sd"])
+    xn = rmsnorm(h, W["final_norm"])
+    return xn @ widen(W["lm_head"]).T
+
+
+def test_decoder_oracle_vs_independent_f64(oracle):
+    """Pins the C oracle's decoder composition (vo_decoder_prefill / step /
+    generate) against the float64 forward above: the prefill's last-row
+    logits and three greedy decode steps (each compared with the row of the
+    float64 forward over the extended sequence) within 1e-5 * RMS, and the
+    greedy tokens equal. Norm gains are random so a swapped norm shows.
+    Controls: the same forward with gate and up swapped, the second
+    residual taken from h instead of h2, or in_ln / post_ln swapped, is
+    far outside the bound."""
+    from sparrow_amd import model as M
+    cfg = M.tiny_config(n_layers=2, hidden=128, n_heads=2, inter=256, vocab=500)
+    W = M.make_weights(cfg, seed=5)
+    rng = np.random.default_rng(55)
+    for L in W["layers"]:
+        L["in_ln"] = (1.0 + 0.5 * rng.standard_normal(cfg["hidden"])).astype(np.float32)
+        L["post_ln"] = (1.0 + 0.5 * rng.standard_normal(cfg["hidden"])).astype(np.float32)
+    W["final_norm"] = (1.0 + 0.5 * rng.standard_normal(cfg["hidden"])).astype(np.float32)
+    prompt = np.array([3, 141, 59, 265, 358, 97, 9], np.int32)
+    dec = oracle.DecoderOracle(W, cfg, cap=32)
+    logits, _ = dec.prefill(prompt)
+
+    def close(got, ref, tol=1e-5):
+        return np.abs(got - ref).max() <= tol * np.sqrt(np.mean(ref ** 2))
+
+    seq = list(prompt)
+    ref = _f64_decoder_logits(W, cfg, seq)[-1]
+    assert close(logits, ref)
+    tok = int(np.argmax(logits))
+    assert tok == int(np.argmax(ref))
+    for step in range(3):
+        step_logits, _ = dec.step(tok, len(seq))
+        seq.append(tok)
+        ref = _f64_decoder_logits(W, cfg, seq)[-1]
+        assert close(step_logits, ref), step
+        tok = int(np.argmax(step_logits))
+        assert tok == int(np.argmax(ref))
+    for variant in ("gate_up_swapped", "residual_from_h", "norms_swapped"):
+        bad = _f64_decoder_logits(W, cfg, seq, variant)[-1]
+        assert not close(step_logits, bad, tol=1e-2), variant
