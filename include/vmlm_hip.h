@@ -165,6 +165,18 @@ int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new
  * Device pointers, asynchronous on `stream`. Same semantics as layer 1. */
 int vmlm_hip_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float *c,
                           size_t m, size_t n, size_t k, void *stream);
+/* The same GEMM with no device allocation: no counterpart in the
+ * reference. For callers that cannot allocate (HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Its temporaries (k-slice
+ * partials, int8 rows, a padded weight copy) live in one fixed 16 MiB
+ * array per GPU, set up by vmlm_hip_init (which must have run; this call
+ * never initialises the library). A shape whose temporaries exceed it
+ * returns 9 before launching anything (M <= 16 at the decoder's shapes and
+ * small prefills fit; M = 16 over N = 5760, K = 2304 needs 3.3 MB). All
+ * calls on one GPU share the array: calls that overlap in time (two
+ * streams, two threads) race and must be serialised by the caller. */
+int vmlm_hip_gemm_nt_int8_noalloc(const float *a, const int8_t *q, const float *scale, float *c,
+                                  size_t m, size_t n, size_t k, void *stream);
 int vmlm_hip_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
                           size_t k, void *stream);
 /* bf16 x bf16 -> f32 (the dense training shape): C = A[m,k] . B[n,k]^T. */

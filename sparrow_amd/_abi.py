@@ -68,6 +68,7 @@ SIGNATURES = {
     "vmlm_attention_decode": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F]),
     # layer 2
     "vmlm_hip_gemm_nt_int8": (I, [P, P, P, P, SZ, SZ, SZ, P]),
+    "vmlm_hip_gemm_nt_int8_noalloc": (I, [P, P, P, P, SZ, SZ, SZ, P]),
     "vmlm_hip_gemm_nt_bf16": (I, [P, P, P, SZ, SZ, SZ, P]),
     "vmlm_hip_gemm_nt_bf16bf16": (I, [P, P, P, SZ, SZ, SZ, P]),
     "vmlm_hip_gemm_nt": (I, [P, P, P, SZ, SZ, SZ, B, P]),

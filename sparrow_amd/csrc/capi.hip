@@ -5,6 +5,7 @@
 // synchronises (serialised by a mutex). Layer 2 (vmlm_hip_*): device pointers,
 // asynchronous. Both validate like the reference interpreter's guards and
 // return its exit codes instead of exiting.
+#include <atomic>
 #include <cstdarg>
 #include <cstring>
 #include <memory>
@@ -32,9 +33,39 @@ int hip_fail(hipError_t e, const char *what) {
     return fail(VMLM_ERR_DEVICE, "HIP error %d (%s) in %s", (int)e, hipGetErrorString(e), what);
 }
 
+// ------------------------------------------------------------------ scratch
+// Device memory of the allocation-free entry point
+// (vmlm_hip_gemm_nt_int8_noalloc): one fixed array in the code object, held
+// by every GPU the library is loaded on until the process ends. In host code
+// `scratch` names a host-side stand-in, never a device address: init
+// resolves the array's address on its device once (hipGetSymbolAddress) and
+// only that pointer is passed to kernels.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+static void *g_scratch_ptr[MAX_DEVICES];  // device address of `scratch`, per device
+static int g_scratch_status = VMLM_ERR_DEVICE;
+static char g_scratch_err[256] = "scratch not set up";
+
+// With `device` current: records the device address of `scratch`.
+static void setup_scratch(int device) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        snprintf(g_scratch_err, sizeof(g_scratch_err), "hipGetSymbolAddress(scratch): %s",
+                 hipGetErrorString(e));
+        return;
+    }
+    if (device >= 0 && device < MAX_DEVICES) {
+        g_scratch_ptr[device] = p;
+        g_scratch_status = VMLM_OK;
+    }
+}
+
 // ------------------------------------------------------------------ init
 static std::once_flag g_once;
 static int g_init_status = -1;
+static std::atomic<bool> g_ready{false};
 static hipStream_t g_stream = nullptr;
 static int *g_guard = nullptr;
 static std::mutex g_host_mutex;
@@ -72,7 +103,9 @@ static void do_init(int device) {
         g_init_status = hip_fail(e, "guard flag");
         return;
     }
+    setup_scratch(device);
     g_init_status = VMLM_OK;
+    g_ready.store(true, std::memory_order_release);
 }
 
 int ensure_init() {
@@ -193,6 +226,31 @@ struct Stage {
     }
 };
 
+// Bump allocation inside the fixed scratch array: the workspace of the
+// allocation-free entry point. A request past the end fails with status 9
+// and nothing is launched.
+struct ScratchBump {
+    char *base;
+    size_t cap;
+    size_t off = 0;
+    int status = VMLM_OK;
+    template <typename T>
+    T *alloc(size_t count) {
+        if (status) return nullptr;
+        const size_t bytes = (count * sizeof(T) + 255) / 256 * 256;
+        if (off + bytes > cap) {
+            status = fail(VMLM_ERR_GUARD,
+                          "allocation-free call: this shape needs more than the %zu bytes of "
+                          "scratch (%zu in use, %zu more requested)",
+                          cap, off, bytes);
+            return nullptr;
+        }
+        T *p = (T *)(base + off);
+        off += bytes;
+        return p;
+    }
+};
+
 static int download(void *host, const void *dev, size_t bytes, hipStream_t st) {
     if (bytes) VMLM_HIP_CHECK(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, st));
     return VMLM_OK;
@@ -210,12 +268,14 @@ static inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; 
 // the wide k-split GEMV; int8 weights, m > 16 and K unpadded, int8 rows and
 // the int8 MFMA GEMM; otherwise A split into 3 bf16 terms and the GEMV kernel
 // (m <= 16) or the tiled bf16 MFMA GEMM.
+// Temporaries come from `stg`: the stream's arena (Stage) or the fixed
+// scratch array of the allocation-free entry point (ScratchBump).
+template <class WS>
 static int q_matmul(const float *a, const void *W, bool wi8, const float *scale, float *c,
-                    size_t m, size_t n, size_t k, hipStream_t st) {
+                    size_t m, size_t n, size_t k, hipStream_t st, WS &stg) {
     if (m == 0 || n == 0) return VMLM_OK;
     const size_t esz = wi8 ? 1 : 2;
     const size_t Kp = round_up(k == 0 ? 1 : k, 128);  // one 128-byte GEMV chunk covers 128 k
-    Stage stg(st);
     const void *Wd = W;
     if (Kp != k || ((uintptr_t)W & 15)) {
         // the padded weight copy is a device copy: refused up front while the
@@ -225,7 +285,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         if (cs != hipStreamCaptureStatusNone)
             return fail(VMLM_ERR_UNIMPL, "q8/bf16 GEMM with K %% 128 != 0 or unaligned weights "
                                          "stages a padded weight copy and cannot be captured");
-        uint8_t *wp = stg.alloc<uint8_t>(n * Kp * esz);
+        uint8_t *wp = stg.template alloc<uint8_t>(n * Kp * esz);
         STAGE_OK(stg);
         int rc0 = launch_fill_zero(wp, n * Kp * esz, st);
         if (rc0) return rc0;
@@ -241,7 +301,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     if (wi8 && m <= 16 && Wd == W && k % 4 == 0 && ((uintptr_t)a & 15) == 0 &&
         nch / nc <= 16) {
         const int ks = (int)(nch / nc);
-        float *part = ks > 1 ? stg.alloc<float>((size_t)ks * m * n) : nullptr;
+        float *part = ks > 1 ? stg.template alloc<float>((size_t)ks * m * n) : nullptr;
         STAGE_OK(stg);
         GemvArgs g;
         g.W = Wd;
@@ -271,10 +331,10 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     // int8 weights, many rows, unpadded K: the rows as int8 terms with a
     // per-row factor, then the int8 x int8 MFMA GEMM
     if (wi8 && m > 16 && Wd == W && Kp == k && k <= 8192 && ((uintptr_t)a & 15) == 0) {
-        int8_t *a8 = stg.alloc<int8_t>((size_t)Q8_T * m * k);
-        float *a8s = stg.alloc<float>(m);
+        int8_t *a8 = stg.template alloc<int8_t>((size_t)Q8_T * m * k);
+        float *a8s = stg.template alloc<float>(m);
         const size_t gw = gemm_i8_work_floats((int)m, (int)n, (int)k);
-        float *gwork = gw ? stg.alloc<float>(gw) : nullptr;
+        float *gwork = gw ? stg.template alloc<float>(gw) : nullptr;
         STAGE_OK(stg);
         int rc = launch_rows_q8(a, k, nullptr, 0.0f, m, k, a8, a8s, st);
         if (rc) return rc;
@@ -296,7 +356,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         return launch_gemm_i8_nonfinite_rows(a, (int)k, (const int8_t *)Wd, (int)k, scale, a8s, c,
                                              (int)n, (int)m, (int)n, (int)k, st);
     }
-    uint16_t *terms = stg.alloc<uint16_t>((size_t)T * m * Kp);
+    uint16_t *terms = stg.template alloc<uint16_t>((size_t)T * m * Kp);
     STAGE_OK(stg);
     int rc = launch_split_terms(a, k, (int)m, (int)k, T, terms, (int)Kp, st);
     if (rc) return rc;
@@ -492,12 +552,30 @@ int vmlm_hip_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, f
                           size_t m, size_t n, size_t k, void *stream) {
     INIT_OR_RETURN();
     VMLM_GUARD(scale != nullptr, "int8 gemm: scale slot must be f32 (null)");
-    return q_matmul(a, q, true, scale, c, m, n, k, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    return q_matmul(a, q, true, scale, c, m, n, k, st, stg);
+}
+int vmlm_hip_gemm_nt_int8_noalloc(const float *a, const int8_t *q, const float *scale, float *c,
+                                  size_t m, size_t n, size_t k, void *stream) {
+    // never initialises the library itself (init allocates)
+    if (!g_ready.load(std::memory_order_acquire))
+        return fail(VMLM_ERR_DEVICE, "gemm_nt_int8_noalloc: call vmlm_hip_init first");
+    if (g_scratch_status != VMLM_OK) return fail(g_scratch_status, "%s", g_scratch_err);
+    VMLM_GUARD(scale != nullptr, "int8 gemm: scale slot must be f32 (null)");
+    int dev = -1;
+    VMLM_HIP_CHECK(hipGetDevice(&dev));
+    VMLM_GUARD(dev >= 0 && dev < MAX_DEVICES && g_scratch_ptr[dev],
+               "gemm_nt_int8_noalloc: no scratch set up on device %d", dev);
+    ScratchBump ws{(char *)g_scratch_ptr[dev], NOALLOC_SCRATCH_BYTES};
+    return q_matmul(a, q, true, scale, c, m, n, k, as_stream(stream), ws);
 }
 int vmlm_hip_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, size_t n,
                           size_t k, void *stream) {
     INIT_OR_RETURN();
-    return q_matmul(a, b, false, nullptr, c, m, n, k, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    return q_matmul(a, b, false, nullptr, c, m, n, k, st, stg);
 }
 int vmlm_hip_gemm_nt_bf16bf16(const uint16_t *a, const uint16_t *b, float *c, size_t m,
                               size_t n, size_t k, void *stream) {
@@ -710,7 +788,7 @@ int vmlm_gemm_nt_int8(const float *a, const int8_t *q, const float *scale, float
         float *ds = stg.upload(scale, n);
         float *dc = stg.alloc<float>(m * n);
         STAGE_OK(stg);
-        int rc = q_matmul(da, dq, true, ds, dc, m, n, k, st);
+        int rc = q_matmul(da, dq, true, ds, dc, m, n, k, st, stg);
         if (rc) return rc;
         rc = download(c, dc, m * n * sizeof(float), st);
         if (rc) return rc;
@@ -728,7 +806,7 @@ int vmlm_gemm_nt_bf16(const float *a, const uint16_t *b, float *c, size_t m, siz
         uint16_t *db = stg.upload(b, n * k);
         float *dc = stg.alloc<float>(m * n);
         STAGE_OK(stg);
-        int rc = q_matmul(da, db, false, nullptr, dc, m, n, k, st);
+        int rc = q_matmul(da, db, false, nullptr, dc, m, n, k, st, stg);
         if (rc) return rc;
         rc = download(c, dc, m * n * sizeof(float), st);
         if (rc) return rc;
