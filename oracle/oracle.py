@@ -86,6 +86,15 @@ def lib() -> C.CDLL:
         "vo_b1_forward_t8_scalar": (_sz, [_f32p, _u32p, _sz, _sz, _f32p, _sz, _sz, _f32p]),
         "vo_transpose_t8": (None, [_f32p, _sz, _sz, _f32p, _sz]),
         "vo_transpose_t8_back": (None, [_f32p, _sz, _sz, _f32p, _sz, _sz]),
+        "vo_dot256": (C.c_float, [_f32p, _f32p, _sz]),
+        "vo_axpy256": (None, [_f32p, _f32p, C.c_float, _sz]),
+        "vo_add256": (None, [_f32p, _f32p, _sz]),
+        "vo_max256": (C.c_float, [_f32p, _sz]),
+        "vo_sum256": (C.c_float, [_f32p, _sz]),
+        "vo_scale_mul": (None, [_f32p, _f32p, C.c_float, _sz]),
+        "vo_layernorm": (None, [_f32p, _f32p, _f32p, _sz, _sz, C.c_float]),
+        "vo_bias": (None, [_f32p, _f32p, _sz, _sz]),
+        "vo_outer": (None, [_f32p, _f32p, _f32p, _sz, _sz, C.c_float]),
         "vo_attention_prefill": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz,
                                         C.c_float, C.c_uint32, C.c_float, C.c_int]),
         "vo_attention_decode": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz,
@@ -234,6 +243,62 @@ def softmax(p, causal=False):
     rows, cols = p.shape
     lib().vo_softmax(p, rows, cols, int(causal))
     return p
+
+
+# ------------------------------------------------ Backend table, jit helpers
+def dot256(a, b):
+    a, b = _c(a, np.float32).ravel(), _c(b, np.float32).ravel()
+    return np.float32(lib().vo_dot256(a, b, a.size))
+
+
+def axpy256(y, x, a):
+    y, x = _c(y, np.float32).ravel().copy(), _c(x, np.float32).ravel()
+    lib().vo_axpy256(y, x, float(a), y.size)
+    return y
+
+
+def add256(y, x):
+    y, x = _c(y, np.float32).ravel().copy(), _c(x, np.float32).ravel()
+    lib().vo_add256(y, x, y.size)
+    return y
+
+
+def max256(x):
+    x = _c(x, np.float32).ravel()
+    return np.float32(lib().vo_max256(x, x.size))
+
+
+def sum256(x):
+    x = _c(x, np.float32).ravel()
+    return np.float32(lib().vo_sum256(x, x.size))
+
+
+def scale_mul(x, a):
+    x = _c(x, np.float32).ravel()
+    d = np.empty_like(x)
+    lib().vo_scale_mul(d, x, float(a), x.size)
+    return d
+
+
+def layernorm(x, g, b, eps=1e-5):
+    y = _c(x, np.float32).copy()
+    rows, cols = y.shape
+    lib().vo_layernorm(y, _c(g, np.float32), _c(b, np.float32), rows, cols, float(eps))
+    return y
+
+
+def bias(d, b):
+    d = _c(d, np.float32).copy()
+    rows, cols = d.shape
+    lib().vo_bias(d, _c(b, np.float32), rows, cols)
+    return d
+
+
+def outer(s, v, k, sc=1.0):
+    s = _c(s, np.float32).copy()
+    m, n = s.shape
+    lib().vo_outer(s, _c(v, np.float32), _c(k, np.float32), m, n, float(sc))
+    return s
 
 
 def act(x, kind):

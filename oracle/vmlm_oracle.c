@@ -882,3 +882,129 @@ out:
     free(logits);
     return st;
 }
+
+/* ====================================================================== */
+/* Backend primitives and the jit_* helpers                                */
+/* ====================================================================== */
+
+/* sys/src/x86_avx2/simd.rs:17-26 hsum256: lo + hi, then two hadds, i.e.
+ * ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7)) -- not the hsum_ps order of fold8. */
+static inline float hsum256(const float l[8]) {
+    float s0 = l[0] + l[4], s1 = l[1] + l[5], s2 = l[2] + l[6], s3 = l[3] + l[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* sys/src/x86_avx2/simd.rs:27-57 dot256_f32: four 8-lane FMA chains over
+ * 32-blocks, 8-blocks into chain 0, (a0+a1)+(a2+a3), hsum256, scalar tail. */
+float vo_dot256(const float *a, const float *b, size_t n) {
+    float c[4][8] = {{0}};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int r = 0; r < 4; ++r)
+            for (int l = 0; l < 8; ++l) c[r][l] = fmaf(a[i + 8 * r + l], b[i + 8 * r + l], c[r][l]);
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) c[0][l] = fmaf(a[i + l], b[i + l], c[0][l]);
+    float s[8];
+    for (int l = 0; l < 8; ++l) s[l] = (c[0][l] + c[1][l]) + (c[2][l] + c[3][l]);
+    float acc = hsum256(s);
+    for (; i < n; ++i) acc += a[i] * b[i];
+    return acc;
+}
+
+/* sys/src/x86_avx2/simd.rs:70-95 axpy256_f32: y = fma(a, x, y) on 8-blocks,
+ * y += a * x (no FMA) on the tail. */
+void vo_axpy256(float *y, const float *x, float a, size_t n) {
+    size_t n8 = n / 8 * 8;
+    for (size_t i = 0; i < n8; ++i) y[i] = fmaf(a, x[i], y[i]);
+    for (size_t i = n8; i < n; ++i) y[i] += a * x[i];
+}
+
+/* sys/src/x86_avx2/simd.rs:170-193 add256_f32. */
+void vo_add256(float *y, const float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] += x[i];
+}
+
+/* _mm256_max_ps(a, b) per lane: a > b ? a : b (b on NaN or equal). */
+static inline float maxps(float a, float b) { return a > b ? a : b; }
+
+/* sys/src/x86_avx2/simd.rs:203-235 max256_f32: 8 lanes from -inf over the
+ * 8-blocks, fold max(lo,hi), max(s, movehl), max(s, s1), then the tail with
+ * a strict `>`. Empty input gives -inf. */
+float vo_max256(const float *x, size_t n) {
+    float m[8];
+    for (int l = 0; l < 8; ++l) m[l] = -INFINITY;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) m[l] = maxps(m[l], x[i + l]);
+    float s[4];
+    for (int l = 0; l < 4; ++l) s[l] = maxps(m[l], m[l + 4]);
+    float t0 = maxps(s[0], s[2]), t1 = maxps(s[1], s[3]);
+    float r = maxps(t0, t1);
+    for (; i < n; ++i)
+        if (x[i] > r) r = x[i];
+    return r;
+}
+
+/* sys/src/x86_avx2/simd.rs:380-405 sum256_f32: two chains (s0 takes blocks
+ * i and i+16, s1 blocks i+8 and i+24), 8-blocks into s0, hsum256(s0+s1),
+ * scalar tail. */
+float vo_sum256(const float *x, size_t n) {
+    float s0[8] = {0}, s1[8] = {0};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int l = 0; l < 8; ++l) {
+            s0[l] = s0[l] + x[i + l];
+            s1[l] = s1[l] + x[i + 8 + l];
+            s0[l] = s0[l] + x[i + 16 + l];
+            s1[l] = s1[l] + x[i + 24 + l];
+        }
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) s0[l] = s0[l] + x[i + l];
+    float s[8];
+    for (int l = 0; l < 8; ++l) s[l] = s0[l] + s1[l];
+    float acc = hsum256(s);
+    for (; i < n; ++i) acc += x[i];
+    return acc;
+}
+
+/* sys/src/x86_avx2/simd.rs:349-372 scale_mul_avx2: dst = a * src. */
+void vo_scale_mul(float *dst, const float *src, float a, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = a * src[i];
+}
+
+/* ops/src/kernels.rs:1308-1333 layernorm (in place): sequential mean and
+ * variance sums, inv = 1/sqrt_f(var + eps), y = (x - mean) * inv * g + b. */
+void vo_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                  float eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        float *p = x + r * cols;
+        float mean = 0.0f;
+        for (size_t i = 0; i < cols; ++i) mean += p[i];
+        mean /= (float)cols;
+        float var = 0.0f;
+        for (size_t i = 0; i < cols; ++i) {
+            float d = p[i] - mean;
+            var += d * d;
+        }
+        var /= (float)cols;
+        float inv = 1.0f / vo_sqrt_f(var + eps);
+        for (size_t i = 0; i < cols; ++i) p[i] = (p[i] - mean) * inv * g[i] + b[i];
+    }
+}
+
+/* ops/src/kernels.rs:1069-1076 jit_bias: d[i, j] += b[j]. */
+void vo_bias(float *d, const float *b, size_t rows, size_t cols) {
+    for (size_t i = 0; i < rows; ++i)
+        for (size_t j = 0; j < cols; ++j) d[i * cols + j] += b[j];
+}
+
+/* ops/src/kernels.rs:1416-1448 outer (AVX2 path outer_avx2): vi = v[i] * sc,
+ * s = fma(vi, k, s) on 8-blocks of j, s += v[i] * sc * k[j] on the tail. */
+void vo_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc) {
+    size_t n8 = n / 8 * 8;
+    for (size_t i = 0; i < m; ++i) {
+        float vi = v[i] * sc;
+        for (size_t j = 0; j < n8; ++j) s[i * n + j] = fmaf(vi, k[j], s[i * n + j]);
+        for (size_t j = n8; j < n; ++j) s[i * n + j] += v[i] * sc * k[j];
+    }
+}

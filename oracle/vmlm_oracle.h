@@ -57,6 +57,18 @@ void vo_gemm_nt(const float *a, const float *b, float *c, size_t m, size_t n, si
 void vo_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
              int acc);
 
+/* ---- Backend primitives (sys/src/x86_avx2/simd.rs) and jit helpers ---- */
+float vo_dot256(const float *a, const float *b, size_t n);
+void vo_axpy256(float *y, const float *x, float a, size_t n);
+void vo_add256(float *y, const float *x, size_t n);
+float vo_max256(const float *x, size_t n);
+float vo_sum256(const float *x, size_t n);
+void vo_scale_mul(float *dst, const float *src, float a, size_t n);
+void vo_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                  float eps);
+void vo_bias(float *d, const float *b, size_t rows, size_t cols);
+void vo_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc);
+
 /* ---- row / elementwise ops ---- */
 void vo_rmsnorm(float *dst, const float *src, const float *g, size_t rows, size_t cols,
                 float eps);

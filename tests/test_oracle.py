@@ -667,3 +667,106 @@ def test_decoder_oracle_vs_independent_f64(oracle):
     for variant in ("gate_up_swapped", "residual_from_h", "norms_swapped"):
         bad = _f64_decoder_logits(W, cfg, seq, variant)[-1]
         assert not close(step_logits, bad, tol=1e-2), variant
+
+
+# ------------------------------------------- Backend primitives, jit helpers
+def test_backend_dot_sum_oracle(oracle):
+    """dot256 / sum256 (sys/src/x86_avx2/simd.rs:27-57, 380-405): float64
+    within n * 2^-24 * sum|terms|; exact on small integers; n = 0 gives 0.
+    Fold control: lane sums (l0+l4, l1+l5, l2+l6, l3+l7) = (2^24, 1, -2^24, 1)
+    give 1 under hsum256's hadd order ((a+b)+(c+d)) and 2 under the hsum_ps
+    order ((a+c)+(b+d)), so the restatement must return 1."""
+    rng = np.random.default_rng(30)
+    for n in (0, 1, 7, 8, 31, 32, 33, 1000, 4099):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        t = a.astype(np.float64) * b
+        bound = (n + 1) * 2.0 ** -24 * np.abs(t).sum() + 1e-30
+        assert abs(oracle.dot256(a, b) - t.sum()) <= bound
+        assert abs(oracle.sum256(a) - a.astype(np.float64).sum()) <= \
+            (n + 1) * 2.0 ** -24 * np.abs(a).sum() + 1e-30
+        ia = rng.integers(-50, 50, n).astype(np.float32)
+        ib = rng.integers(-50, 50, n).astype(np.float32)
+        assert oracle.dot256(ia, ib) == float(ia.astype(np.int64) @ ib.astype(np.int64))
+        assert oracle.sum256(ia) == float(ia.astype(np.int64).sum())
+    lanes = np.float32([2 ** 24, 1, -2 ** 24, 1, 0, 0, 0, 0])
+    assert oracle.dot256(lanes, np.ones(8, np.float32)) == 1.0
+    assert oracle.sum256(lanes) == 1.0
+
+
+def test_backend_max_oracle(oracle):
+    """max256 (sys/src/x86_avx2/simd.rs:203-235): NaN-free input gives
+    np.max; empty input -inf; MAXPS(a, b) returns b when a NaN is involved,
+    so a NaN in lane 0 is dropped by the fold max(lane0, lane4) but a NaN in
+    lane 4 survives it and is dropped one step later; an all-NaN block stays
+    NaN and the tail's strict `>` never replaces it."""
+    rng = np.random.default_rng(31)
+    for n in (1, 5, 8, 9, 64, 1001):
+        x = rng.standard_normal(n).astype(np.float32)
+        assert oracle.max256(x) == x.max()
+    assert oracle.max256(np.zeros(0, np.float32)) == -np.inf
+    x = np.ones(8, np.float32)
+    x[0] = np.nan
+    assert oracle.max256(x) == 1.0
+    x = np.ones(8, np.float32)
+    x[4] = np.nan
+    assert oracle.max256(x) == 1.0
+    assert np.isnan(oracle.max256(np.full(9, np.nan, np.float32)))
+    x = np.full(9, np.nan, np.float32)
+    x[8] = 5.0
+    assert np.isnan(oracle.max256(x))
+
+
+def test_backend_elementwise_oracle(oracle):
+    """axpy256 fuses a*x + y (one rounding) on the 8-blocks and rounds twice
+    on the tail; add256 / scale_mul are single f32 operations (numpy float32
+    is exact for them). The control a = x = 1 + 2^-12, y = -(1 + 2^-11):
+    the fused result is 2^-24, the two-rounding one 0."""
+    rng = np.random.default_rng(32)
+    n = 45
+    y = rng.standard_normal(n).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    a = np.float32(0.37)
+    got = oracle.axpy256(y, x, a)
+    fused = (np.float64(a) * x + y).astype(np.float32)  # exact product, one rounding
+    assert np.array_equal(got[:40], fused[:40])
+    assert np.array_equal(got[40:], (a * x[40:] + y[40:]).astype(np.float32))
+    e = np.float32(1 + 2 ** -12)
+    yy = np.full(9, -(1 + 2 ** -11), np.float32)
+    xx = np.full(9, e, np.float32)
+    got = oracle.axpy256(yy, xx, e)
+    assert np.all(got[:8] == np.float32(2 ** -24)) and got[8] == 0.0
+    assert np.array_equal(oracle.add256(y, x), y + x)
+    assert np.array_equal(oracle.scale_mul(x, a), a * x)
+
+
+def test_layernorm_bias_outer_oracle(oracle):
+    """layernorm (ops/src/kernels.rs:1308-1333) vs float64 within 1e-5; a
+    constant row normalises to exactly b. jit_bias adds b to every row
+    exactly. outer (:1416-1448) fuses on 8-blocks of j: the same control
+    as axpy256 gives 2^-24 there and 0 on the tail."""
+    rng = np.random.default_rng(33)
+    x = rng.standard_normal((5, 77)).astype(np.float32)
+    g = rng.standard_normal(77).astype(np.float32)
+    b = rng.standard_normal(77).astype(np.float32)
+    x[3] = 2.5
+    y = oracle.layernorm(x, g, b, 1e-5)
+    xd = x.astype(np.float64)
+    mu = xd.mean(1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(1, keepdims=True) + 1e-5) * g + b
+    assert np.abs(y - ref).max() < 1e-5 * np.abs(ref).max()
+    assert np.array_equal(y[3], b)
+    d = rng.standard_normal((4, 9)).astype(np.float32)
+    assert np.array_equal(oracle.bias(d, b[:9]), d + b[:9])
+    e = np.float32(1 + 2 ** -12)
+    s = np.full((2, 10), -(1 + 2 ** -11), np.float32)
+    out = oracle.outer(s, np.full(2, e, np.float32), np.full(10, e, np.float32))
+    assert np.all(out[:, :8] == np.float32(2 ** -24)) and np.all(out[:, 8:] == 0.0)
+    s = rng.standard_normal((3, 20)).astype(np.float32)
+    v = rng.standard_normal(3).astype(np.float32)
+    k = rng.standard_normal(20).astype(np.float32)
+    out = oracle.outer(s, v, k, 0.5)
+    vi = (v * np.float32(0.5)).astype(np.float32)
+    assert np.array_equal(out[:, :16], (vi[:, None].astype(np.float64) * k[:16] + s[:, :16])
+                          .astype(np.float32))
+    assert np.array_equal(out[:, 16:], s[:, 16:] + vi[:, None] * k[16:])
