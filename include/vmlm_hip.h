@@ -143,9 +143,35 @@ int vmlm_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8);
 /* ops/src/kernels.rs:3307 transpose_t8_back_avx2(a,rows,cols,out,os,in_stride). */
 int vmlm_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out, size_t os,
                            size_t in_stride);
-/* ops/src/kernels.rs:1017-1033 jit_gemm_nt(a,b,c,dims),
- * dims = m | n<<16 | k<<32 | acc<<48. */
+/* ops/src/kernels.rs:1308 layernorm(x,g,b,rows,cols,eps), in place. */
+int vmlm_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                   float eps);
+/* ops/src/kernels.rs:1436 outer(s,v,k,m,n,sc): S[i,j] += v[i] * sc * k[j]. */
+int vmlm_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc);
+/* ops/src/kernels.rs:1058-1065 jit_bias's body: d[i,j] += b[j]. */
+int vmlm_bias(float *d, const float *b, size_t rows, size_t cols);
+
+/* The JIT glue's entry points (ops/src/kernels.rs:1017-1113), host pointers,
+ * with the reference's packed dims; they return the status the reference's
+ * extern "system" functions cannot. jit_print / jit_unimpl / jit_memcpy are
+ * host utilities (stdout, abort, memcpy), not kernels, and are not here. */
+/* :1017-1033 jit_gemm_nt(a,b,c,dims), dims = m | n<<16 | k<<32 | acc<<48. */
 int vmlm_jit_gemm_nt(const float *a, const float *b, float *c, uint64_t dims);
+/* :1036 jit_act(p,n,kind). */
+int vmlm_jit_act(float *p, size_t n, uint64_t kind);
+/* :1041-1056 jit_ewadd / ewmul / ewsub / ewdiv(d,x,y,n). */
+int vmlm_jit_ewadd(float *d, const float *x, const float *y, size_t n);
+int vmlm_jit_ewmul(float *d, const float *x, const float *y, size_t n);
+int vmlm_jit_ewsub(float *d, const float *x, const float *y, size_t n);
+int vmlm_jit_ewdiv(float *d, const float *x, const float *y, size_t n);
+/* :1058 jit_bias(d,b,rows,cols). */
+int vmlm_jit_bias(float *d, const float *b, size_t rows, size_t cols);
+/* :1068 jit_ln(x,g,b,dims,pad), dims = m | c<<32, eps 1e-5, in place. */
+int vmlm_jit_ln(float *x, const float *g, const float *b, uint64_t dims, uint64_t pad);
+/* :1081 jit_softmax(p,dims,causal), dims = m | c<<32. */
+int vmlm_jit_softmax(float *p, uint64_t dims, uint64_t causal);
+/* :1088 jit_outer(s,v,k,dims), dims = m | n<<32, scale 1. */
+int vmlm_jit_outer(float *s, const float *v, const float *k, uint64_t dims);
 
 /* Attention as tools/p12_build_minicpm.py:770-781 composes it (SLICE, ROPE,
  * GEMM NT, SCALE, SOFTMAX causal, GEMM NN, WRITECOL), fused.
@@ -209,6 +235,11 @@ int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t 
                           void *stream);
 int vmlm_hip_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out,
                                size_t os, size_t in_stride, void *stream);
+int vmlm_hip_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                       float eps, void *stream);
+int vmlm_hip_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc,
+                   void *stream);
+int vmlm_hip_bias(float *d, const float *b, size_t rows, size_t cols, void *stream);
 int vmlm_hip_attention_prefill(const float *q, const float *k, const float *v, float *out,
                                size_t S, size_t n_heads, size_t head_dim, float theta,
                                uint16_t pos0, float scale, bool causal, void *stream);
@@ -281,10 +312,43 @@ int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers,
                           const float *x, float *y, size_t n_tokens, uint16_t act,
                           void *stream);
 
-/* The backend function table (sys/src/lib.rs:24-72 defines the reference's
- * `#[repr(C)] Backend` as the cross-language backend form; this is the
- * kernel-level table of this backend). */
-typedef struct vmlm_hip_backend_t {
+/* ================================================================ tables */
+
+/* sys/src/lib.rs:29-38 `#[repr(C)] struct Backend`, field for field: the
+ * reference's cross-language backend form. The functions keep the
+ * reference's signatures (no status return): pointers may be device memory
+ * (used in place) or host memory (staged through the library's workspace);
+ * each call is synchronous. On failure the value-returning functions return
+ * NaN, the others leave their output untouched, and vmlm_hip_last_error()
+ * holds the message. dot256 / sum256 are tree sums within f32 rounding of
+ * the reference's 8-lane chains; the others are bitwise
+ * (sys/src/x86_avx2/simd.rs:27-405). */
+typedef struct vmlm_backend_t {
+    const char *name; /* "hip_gfx950" */
+    float (*dot256)(const float *a, const float *b, size_t n);
+    void (*axpy256)(float *y, const float *x, float a, size_t n);
+    void (*add256)(float *y, const float *x, size_t n);
+    float (*max256)(const float *x, size_t n);
+    float (*sum256)(const float *x, size_t n);
+    void (*scale_mul)(float *dst, const float *src, float a, size_t n);
+} vmlm_backend_t;
+const vmlm_backend_t *vmlm_hip_backend(void);
+/* sys/src/x86_avx2/simd.rs:32 dot256_f32: sum of a[i] * b[i]. */
+float vmlm_backend_dot256(const float *a, const float *b, size_t n);
+/* :76 axpy256_f32: y[i] += a * x[i] (fused on 8-blocks, mul + add on the tail). */
+void vmlm_backend_axpy256(float *y, const float *x, float a, size_t n);
+/* :175 add256_f32: y[i] += x[i]. */
+void vmlm_backend_add256(float *y, const float *x, size_t n);
+/* :207 max256_f32: max over x (MAXPS lanes, -inf when empty). */
+float vmlm_backend_max256(const float *x, size_t n);
+/* :386 sum256_f32: sum of x. */
+float vmlm_backend_sum256(const float *x, size_t n);
+/* :353 scale_mul_avx2: dst[i] = a * src[i]. */
+void vmlm_backend_scale_mul(float *dst, const float *src, float a, size_t n);
+
+/* The kernel-level table of this library (host-pointer entry points of
+ * layer 1); no reference counterpart. */
+typedef struct vmlm_hip_kernel_table_t {
     const char *name;
     int (*gemm_nt_int8)(const float *, const int8_t *, const float *, float *, size_t,
                         size_t, size_t);
@@ -298,8 +362,8 @@ typedef struct vmlm_hip_backend_t {
     int (*b1_forward)(const vmlm_sparse_conn_w *, const float *, float *, size_t *);
     int (*b1_forward_t8)(const vmlm_sparse_conn_w *, const float *, size_t, size_t, float *,
                          size_t *);
-} vmlm_hip_backend_t;
-const vmlm_hip_backend_t *vmlm_hip_backend(void);
+} vmlm_hip_kernel_table_t;
+const vmlm_hip_kernel_table_t *vmlm_hip_kernel_table(void);
 
 #ifdef __cplusplus
 }

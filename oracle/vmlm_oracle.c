@@ -992,7 +992,7 @@ void vo_layernorm(float *x, const float *g, const float *b, size_t rows, size_t 
     }
 }
 
-/* ops/src/kernels.rs:1069-1076 jit_bias: d[i, j] += b[j]. */
+/* ops/src/kernels.rs:1058-1065 jit_bias: d[i, j] += b[j]. */
 void vo_bias(float *d, const float *b, size_t rows, size_t cols) {
     for (size_t i = 0; i < rows; ++i)
         for (size_t j = 0; j < cols; ++j) d[i * cols + j] += b[j];

@@ -20,6 +20,17 @@ class SparseConnW(C.Structure):
                 ("w", P), ("src", P), ("src_u32", P), ("act", P)]
 
 
+class Backend(C.Structure):
+    """sys/src/lib.rs:29-38 Backend, as vmlm_backend_t."""
+    _fields_ = [("name", C.c_char_p),
+                ("dot256", C.CFUNCTYPE(F, P, P, SZ)),
+                ("axpy256", C.CFUNCTYPE(None, P, P, F, SZ)),
+                ("add256", C.CFUNCTYPE(None, P, P, SZ)),
+                ("max256", C.CFUNCTYPE(F, P, SZ)),
+                ("sum256", C.CFUNCTYPE(F, P, SZ)),
+                ("scale_mul", C.CFUNCTYPE(None, P, P, F, SZ))]
+
+
 class DecoderCfg(C.Structure):
     _fields_ = [("n_layers", U32), ("hidden", U32), ("n_heads", U32), ("head_dim", U32),
                 ("inter", U32), ("vocab", U32), ("batch", U32), ("cap", U32),
@@ -63,7 +74,19 @@ SIGNATURES = {
     "vmlm_b1_forward_t8": (I, [C.POINTER(SparseConnW), P, SZ, SZ, P, C.POINTER(SZ)]),
     "vmlm_transpose_t8": (I, [P, SZ, SZ, P, SZ]),
     "vmlm_transpose_t8_back": (I, [P, SZ, SZ, P, SZ, SZ]),
+    "vmlm_layernorm": (I, [P, P, P, SZ, SZ, F]),
+    "vmlm_outer": (I, [P, P, P, SZ, SZ, F]),
+    "vmlm_bias": (I, [P, P, SZ, SZ]),
     "vmlm_jit_gemm_nt": (I, [P, P, P, U64]),
+    "vmlm_jit_act": (I, [P, SZ, U64]),
+    "vmlm_jit_ewadd": (I, [P, P, P, SZ]),
+    "vmlm_jit_ewmul": (I, [P, P, P, SZ]),
+    "vmlm_jit_ewsub": (I, [P, P, P, SZ]),
+    "vmlm_jit_ewdiv": (I, [P, P, P, SZ]),
+    "vmlm_jit_bias": (I, [P, P, SZ, SZ]),
+    "vmlm_jit_ln": (I, [P, P, P, U64, U64]),
+    "vmlm_jit_softmax": (I, [P, U64, U64]),
+    "vmlm_jit_outer": (I, [P, P, P, U64]),
     "vmlm_attention_prefill": (I, [P, P, P, P, SZ, SZ, SZ, F, U16, F, B]),
     "vmlm_attention_decode": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F]),
     # layer 2
@@ -86,6 +109,9 @@ SIGNATURES = {
     "vmlm_hip_b1_forward_t8": (I, [C.POINTER(SparseConnW), P, SZ, SZ, P, P]),
     "vmlm_hip_transpose_t8": (I, [P, SZ, SZ, P, SZ, P]),
     "vmlm_hip_transpose_t8_back": (I, [P, SZ, SZ, P, SZ, SZ, P]),
+    "vmlm_hip_layernorm": (I, [P, P, P, SZ, SZ, F, P]),
+    "vmlm_hip_outer": (I, [P, P, P, SZ, SZ, F, P]),
+    "vmlm_hip_bias": (I, [P, P, SZ, SZ, P]),
     "vmlm_hip_attention_prefill": (I, [P, P, P, P, SZ, SZ, SZ, F, U16, F, B, P]),
     "vmlm_hip_attention_decode": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F, P]),
     # layer 3
@@ -103,6 +129,13 @@ SIGNATURES = {
     "vmlm_decoder_time_gemv": (I, [P, I, U32, C.POINTER(F), C.POINTER(C.c_double)]),
     "vmlm_b1_stack_forward": (I, [C.POINTER(SparseConnW), U32, P, P, SZ, U16, P]),
     "vmlm_hip_backend": (P, []),
+    "vmlm_backend_dot256": (F, [P, P, SZ]),
+    "vmlm_backend_axpy256": (None, [P, P, F, SZ]),
+    "vmlm_backend_add256": (None, [P, P, SZ]),
+    "vmlm_backend_max256": (F, [P, SZ]),
+    "vmlm_backend_sum256": (F, [P, SZ]),
+    "vmlm_backend_scale_mul": (None, [P, P, F, SZ]),
+    "vmlm_hip_kernel_table": (P, []),
 }
 
 

@@ -1100,12 +1100,185 @@ int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new
     FINISH(st);
 }
 
-// ================================================================ backend table
-static const vmlm_hip_backend_t g_backend = {
+// ================================================================ jit helpers
+int vmlm_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                   float eps) {
+    HOST_CALL_BEGIN();
+    if (rows == 0 || cols == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dx = stg.upload((const float *)x, rows * cols);
+        float *dg = stg.upload(g, cols);
+        float *db = stg.upload(b, cols);
+        STAGE_OK(stg);
+        int rc = launch_layernorm(dx, dg, db, rows, cols, eps, st);
+        if (!rc) rc = download(x, dx, rows * cols * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc) {
+    HOST_CALL_BEGIN();
+    if (m == 0 || n == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *ds = stg.upload((const float *)s, m * n);
+        float *dv = stg.upload(v, m);
+        float *dk = stg.upload(k, n);
+        STAGE_OK(stg);
+        int rc = launch_outer(ds, dv, dk, m, n, sc, st);
+        if (!rc) rc = download(s, ds, m * n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_bias(float *d, const float *b, size_t rows, size_t cols) {
+    HOST_CALL_BEGIN();
+    if (rows == 0 || cols == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        float *dd = stg.upload((const float *)d, rows * cols);
+        float *db = stg.upload(b, cols);
+        STAGE_OK(stg);
+        int rc = launch_bias(dd, db, rows, cols, st);
+        if (!rc) rc = download(d, dd, rows * cols * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_jit_act(float *p, size_t n, uint64_t kind) { return vmlm_act(p, n, (uint16_t)kind); }
+int vmlm_jit_ewadd(float *d, const float *x, const float *y, size_t n) {
+    return vmlm_ew_op(d, x, y, n, VMLM_OP_EWADD);
+}
+int vmlm_jit_ewmul(float *d, const float *x, const float *y, size_t n) {
+    return vmlm_ew_op(d, x, y, n, VMLM_OP_EWMUL);
+}
+int vmlm_jit_ewsub(float *d, const float *x, const float *y, size_t n) {
+    return vmlm_ew_op(d, x, y, n, VMLM_OP_EWSUB);
+}
+int vmlm_jit_ewdiv(float *d, const float *x, const float *y, size_t n) {
+    return vmlm_ew_op(d, x, y, n, VMLM_OP_EWDIV);
+}
+int vmlm_jit_bias(float *d, const float *b, size_t rows, size_t cols) {
+    return vmlm_bias(d, b, rows, cols);
+}
+int vmlm_jit_ln(float *x, const float *g, const float *b, uint64_t dims, uint64_t pad) {
+    (void)pad;
+    return vmlm_layernorm(x, g, b, (size_t)(dims & 0xFFFFFFFFu), (size_t)(dims >> 32), 1e-5f);
+}
+int vmlm_jit_softmax(float *p, uint64_t dims, uint64_t causal) {
+    return vmlm_softmax(p, (size_t)(dims & 0xFFFFFFFFu), (size_t)(dims >> 32), causal != 0);
+}
+int vmlm_jit_outer(float *s, const float *v, const float *k, uint64_t dims) {
+    return vmlm_outer(s, v, k, (size_t)(dims & 0xFFFFFFFFu), (size_t)(dims >> 32), 1.0f);
+}
+
+int vmlm_hip_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                       float eps, void *stream) {
+    INIT_OR_RETURN();
+    return launch_layernorm(x, g, b, rows, cols, eps, as_stream(stream));
+}
+int vmlm_hip_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc,
+                   void *stream) {
+    INIT_OR_RETURN();
+    return launch_outer(s, v, k, m, n, sc, as_stream(stream));
+}
+int vmlm_hip_bias(float *d, const float *b, size_t rows, size_t cols, void *stream) {
+    INIT_OR_RETURN();
+    return launch_bias(d, b, rows, cols, as_stream(stream));
+}
+
+// ================================================================ Backend table
+// Operands of the Backend functions: device (or managed) memory is used in
+// place; anything else is host memory, staged through the call's workspace.
+static bool device_ptr(const void *p) {
+    hipPointerAttribute_t at{};
+    if (!p || hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+}
+static const float *bk_operand(Stage &stg, const float *p, size_t n) {
+    return device_ptr(p) ? p : stg.upload(p, n);
+}
+
+// Runs a Backend reduction (0 dot, 1 sum, 2 max) and returns its value, or
+// NaN with the message in vmlm_hip_last_error().
+static float bk_scalar(int op, const float *a, const float *b, size_t n) {
+    const float nan = __builtin_nanf("");
+    if (ensure_init()) return nan;
+    std::lock_guard<std::mutex> lk(g_host_mutex);
+    hipStream_t st = lib_stream();
+    float r = nan;
+    {
+        Stage stg(st);
+        const float *da = bk_operand(stg, a, n);
+        const float *db = op == 0 ? bk_operand(stg, b, n) : nullptr;
+        float *out = stg.alloc<float>(1);
+        float *part = op < 2 ? stg.alloc<float>(bk_reduce_work_floats()) : nullptr;
+        char *work = op == 2 ? stg.alloc<char>(bk_max_work_bytes()) : nullptr;
+        if (stg.status) return nan;
+        int rc = op == 2 ? launch_bk_max(da, n, work, out, st)
+                         : launch_bk_reduce(da, db, n, op == 0, part, out, st);
+        if (rc) return nan;
+        hipError_t e = hipMemcpyAsync(&r, out, sizeof(float), hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+            hip_fail(e, "Backend reduction");
+            return nan;
+        }
+    }
+    return r;
+}
+
+// Runs a Backend elementwise op (0 axpy, 1 add, 2 scale_mul) into `y`.
+static void bk_elementwise(int op, float *y, const float *x, float a, size_t n) {
+    if (ensure_init() || n == 0) return;
+    std::lock_guard<std::mutex> lk(g_host_mutex);
+    hipStream_t st = lib_stream();
+    Stage stg(st);
+    const bool ydev = device_ptr(y);
+    float *dy = ydev ? y : (op == 2 ? stg.alloc<float>(n) : stg.upload((const float *)y, n));
+    const float *dx = bk_operand(stg, x, n);
+    if (stg.status) return;
+    int rc = op == 0 ? launch_bk_axpy(dy, dx, a, n, st)
+             : op == 1 ? launch_bk_add(dy, dx, n, st)
+                       : launch_bk_scale_mul(dy, dx, a, n, st);
+    if (rc) return;
+    hipError_t e = hipSuccess;
+    if (!ydev) e = hipMemcpyAsync(y, dy, n * sizeof(float), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) hip_fail(e, "Backend elementwise op");
+}
+
+float vmlm_backend_dot256(const float *a, const float *b, size_t n) {
+    return bk_scalar(0, a, b, n);
+}
+void vmlm_backend_axpy256(float *y, const float *x, float a, size_t n) {
+    bk_elementwise(0, y, x, a, n);
+}
+void vmlm_backend_add256(float *y, const float *x, size_t n) { bk_elementwise(1, y, x, 0.0f, n); }
+float vmlm_backend_max256(const float *x, size_t n) { return bk_scalar(2, x, nullptr, n); }
+float vmlm_backend_sum256(const float *x, size_t n) { return bk_scalar(1, x, nullptr, n); }
+void vmlm_backend_scale_mul(float *dst, const float *src, float a, size_t n) {
+    bk_elementwise(2, dst, src, a, n);
+}
+
+static const vmlm_backend_t g_backend = {
+    "hip_gfx950",          vmlm_backend_dot256, vmlm_backend_axpy256, vmlm_backend_add256,
+    vmlm_backend_max256,   vmlm_backend_sum256, vmlm_backend_scale_mul,
+};
+const vmlm_backend_t *vmlm_hip_backend(void) { return &g_backend; }
+
+static const vmlm_hip_kernel_table_t g_kernels = {
     "hip_gfx950",      vmlm_gemm_nt_int8, vmlm_gemm_nt_bf16, vmlm_gemm_nt,
     vmlm_gemm,         vmlm_rmsnorm,      vmlm_softmax,      vmlm_act,
     vmlm_ew_op,        vmlm_b1_forward,   vmlm_b1_forward_t8,
 };
-const vmlm_hip_backend_t *vmlm_hip_backend(void) { return &g_backend; }
+const vmlm_hip_kernel_table_t *vmlm_hip_kernel_table(void) { return &g_kernels; }
 
 }  // extern "C"

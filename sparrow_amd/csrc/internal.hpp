@@ -155,6 +155,22 @@ int launch_gemm(const GemmArgs &a, hipStream_t st);
 int launch_gemm_i8_nonfinite_rows(const float *a, int lda, const int8_t *q, int ldq,
                                   const float *scale, const float *a8s, float *c, int ldc, int M,
                                   int N, int K, hipStream_t st);
+// Backend-table primitives and jit helpers (k_backend.hip). `part` holds
+// bk_reduce_work_floats() floats, `work` bk_max_work_bytes() bytes; the
+// scalar result goes to out[0] on the device.
+int bk_reduce_work_floats();
+size_t bk_max_work_bytes();
+int launch_bk_reduce(const float *a, const float *b, size_t n, bool dot, float *part, float *out,
+                     hipStream_t st);
+int launch_bk_max(const float *x, size_t n, void *work, float *out, hipStream_t st);
+int launch_bk_axpy(float *y, const float *x, float a, size_t n, hipStream_t st);
+int launch_bk_add(float *y, const float *x, size_t n, hipStream_t st);
+int launch_bk_scale_mul(float *d, const float *s, float a, size_t n, hipStream_t st);
+int launch_layernorm(float *x, const float *g, const float *b, size_t rows, size_t cols,
+                     float eps, hipStream_t st);
+int launch_bias(float *d, const float *b, size_t rows, size_t cols, hipStream_t st);
+int launch_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc,
+                 hipStream_t st);
 // Zero-fills `bytes` bytes with a kernel (capturable, unlike hipMemsetAsync).
 int launch_fill_zero(void *p, size_t bytes, hipStream_t st);
 int gemm_i8_kslices(int M, int N, int K);
