@@ -50,3 +50,34 @@ def test_no_oracle_in_product_path():
         assert "oracle" not in src.replace("oracle/", ""), p
     for p in (ROOT / "sparrow_amd" / "csrc").glob("*"):
         assert "vmlm_oracle" not in p.read_text(), p
+
+
+def _header_params():
+    """name -> parameter count of every function include/vmlm_hip.h declares."""
+    text = (ROOT / "include" / "vmlm_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(vmlm_\w+)\s*\(([^;{]*?)\)\s*;", text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_ffi_crate_matches_header():
+    """ffi/vmlm-ops-hip/src/lib.rs (the Rust FFI crate; no Rust toolchain
+    here, so it is checked as text): every C function its extern block
+    declares exists in include/vmlm_hip.h with the same parameter count, and
+    the library exports it."""
+    import sparrow_amd
+    src = (ROOT / "ffi" / "vmlm-ops-hip" / "src" / "lib.rs").read_text()
+    block = src[src.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    decls = re.findall(r"fn\s+(vmlm_\w+)\s*\(([^)]*)\)", block, flags=re.S)
+    assert len(decls) >= 30
+    header = _header_params()
+    L = C.CDLL(str(sparrow_amd.LIB_PATH))
+    for name, args in decls:
+        n = 0 if not args.strip() else args.count(":")
+        assert name in header, name
+        assert header[name] == n, (name, header[name], n)
+        assert hasattr(L, name), name
