@@ -114,6 +114,25 @@ def lib() -> C.CDLL:
     L.vo_decoder_generate.restype = C.c_int
     L.vo_decoder_generate.argtypes = [C.c_void_p, _f32p, _f32p, _sz, _i32p, _sz, _sz,
                                       _i32p, C.c_void_p]
+    # the VM
+    L.vo_vm_load.restype = C.c_int
+    L.vo_vm_load.argtypes = [C.c_char_p, _sz, C.POINTER(C.c_void_p)]
+    L.vo_vm_run.restype = C.c_int
+    L.vo_vm_run.argtypes = [C.c_void_p]
+    L.vo_vm_free.restype = None
+    L.vo_vm_free.argtypes = [C.c_void_p]
+    L.vo_vm_find.restype = C.c_int
+    L.vo_vm_find.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32)]
+    L.vo_vm_slot.restype = C.c_int
+    L.vo_vm_slot.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_void_p),
+                             C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                             C.POINTER(C.c_uint8)]
+    L.vo_vm_output.restype = _sz
+    L.vo_vm_output.argtypes = [C.c_void_p, C.c_void_p, _sz]
+    L.vo_vm_message.restype = C.c_char_p
+    L.vo_vm_message.argtypes = [C.c_void_p]
+    L.vo_vm_last_load_error.restype = C.c_char_p
+    L.vo_vm_last_load_error.argtypes = []
     threads = int(os.environ.get("VMLM_ORACLE_THREADS", "0") or 0)
     if threads <= 0:
         threads = min(16, os.cpu_count() or 1)
@@ -496,3 +515,78 @@ class DecoderOracle:
         if st:
             raise ValueError(f"oracle generate failed ({st})")
         return toks, margins
+
+
+# ---------------------------------------------------------------- the VM
+class VmError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"exit {code}: {msg}")
+        self.code, self.msg = code, msg
+
+
+class OracleVm:
+    """The reference VM restated on the CPU (vmlm_vm_oracle.c): load a .vmb
+    image (core/src/interp.rs Vm::load), run it (Vm::run), read slots and
+    the PRINT output. Failures raise VmError with the reference's exit code."""
+
+    def __init__(self, image: bytes):
+        self._h = None
+        h = C.c_void_p()
+        rc = lib().vo_vm_load(image, len(image), C.byref(h))
+        if rc:
+            raise VmError(rc, lib().vo_vm_last_load_error().decode())
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().vo_vm_free(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    def run(self):
+        rc = lib().vo_vm_run(self._h)
+        if rc:
+            raise VmError(rc, lib().vo_vm_message(self._h).decode())
+
+    def slot_index(self, name: str) -> int:
+        from sparrow_amd.vmb import hash32
+        i = C.c_uint32()
+        if lib().vo_vm_find(self._h, hash32(name), C.byref(i)):
+            raise KeyError(name)
+        return i.value
+
+    def read(self, name_or_index):
+        i = name_or_index if isinstance(name_or_index, int) else self.slot_index(name_or_index)
+        p, r, c, dt = C.c_void_p(), C.c_uint32(), C.c_uint32(), C.c_uint8()
+        rc = lib().vo_vm_slot(self._h, i, C.byref(p), C.byref(r), C.byref(c), C.byref(dt))
+        if rc:
+            raise VmError(rc, lib().vo_vm_message(self._h).decode())
+        if dt.value != 0:
+            raise TypeError("only f32 slots are read back")
+        buf = (C.c_float * (r.value * c.value)).from_address(p.value)
+        return np.array(buf, np.float32).reshape(r.value, c.value)
+
+    def write(self, name_or_index, values):
+        i = name_or_index if isinstance(name_or_index, int) else self.slot_index(name_or_index)
+        p, r, c, dt = C.c_void_p(), C.c_uint32(), C.c_uint32(), C.c_uint8()
+        rc = lib().vo_vm_slot(self._h, i, C.byref(p), C.byref(r), C.byref(c), C.byref(dt))
+        if rc or dt.value != 0:
+            raise VmError(rc or 9, "slot not writable as f32")
+        v = np.ascontiguousarray(values, np.float32).ravel()
+        if v.size > r.value * c.value:
+            raise ValueError("more values than the slot holds")
+        C.memmove(p.value, v.ctypes.data, v.nbytes)
+
+    def output(self):
+        n = lib().vo_vm_output(self._h, None, 0)
+        out = np.empty(n, np.float32)
+        lib().vo_vm_output(self._h, out.ctypes.data, n)
+        return out

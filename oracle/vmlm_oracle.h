@@ -141,6 +141,19 @@ int vo_decoder_generate(const vo_model *md, float *kcache, float *vcache, size_t
                         const int32_t *prompt, size_t S, size_t n_steps,
                         int32_t *out_tokens, float *margins);
 
+/* ---- the VM (vmlm_vm_oracle.c): core/src/interp.rs load + run ---- */
+typedef struct vo_vm vo_vm;
+int vo_vm_load(const uint8_t *image, size_t len, vo_vm **out); /* exit code */
+int vo_vm_run(vo_vm *vm);                                      /* exit code */
+void vo_vm_free(vo_vm *vm);
+int vo_vm_find(const vo_vm *vm, uint32_t hash, uint32_t *slot);
+int vo_vm_slot(vo_vm *vm, uint32_t slot, float **p, uint32_t *rows, uint32_t *cols,
+               uint8_t *dtype);
+size_t vo_vm_output(const vo_vm *vm, float *dst, size_t cap);
+const char *vo_vm_message(const vo_vm *vm);
+const char *vo_vm_last_load_error(void);
+void vo_vm_last_load_error_set(const char *m);
+
 #ifdef __cplusplus
 }
 #endif
