@@ -312,6 +312,45 @@ int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers,
                           const float *x, float *y, size_t n_tokens, uint16_t act,
                           void *stream);
 
+/* ================================================================ VM
+ * Device-resident executor of .vmb programs: core/src/interp.rs Vm::load /
+ * load_weights_mapped (:108-236) and Vm::run (:720-2370), with the constant
+ * pool uploaded to the GPU once (read-only there), the activation / state /
+ * gradient arenas in HBM (64-byte aligned, zeroed) and every opcode
+ * dispatched to this library's kernels by slot address. Status codes are
+ * the interpreter's exit codes (9 guard, 5 unimplemented op, 6 training op,
+ * 3 bad magic, 7 slot not found, 8 EW shape mismatch, 2 device failure).
+ * Extensions (no reference counterpart): bit 6 of `fl` reads the ROPE
+ * position and the WRITECOL column from slot `dt`, and the SOFTMAX live
+ * width from slot `b`, at run time. */
+typedef struct vmlm_vm vmlm_vm;
+/* Loads `image` (.vmb bytes). `weights` (optional) is the constant region
+ * of a mapped weights file (load_weights_mapped): VMs loaded over the same
+ * (weights, weights_len) share one device copy, uploaded once; the caller
+ * keeps that memory unchanged while they live. Without it the image's own
+ * CONST region is uploaded for this VM. The audit of audit_const_dtypes
+ * (:241-348) runs here (9). */
+int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weights_len,
+                 vmlm_vm **out);
+int vmlm_vm_destroy(vmlm_vm *vm);
+/* Runs TEXT from instruction 0 to HALT (or its end); synchronous. */
+int vmlm_vm_run(vmlm_vm *vm);
+/* Slot lookup by name (FNV-1a hash, core/src/interp.rs:410-418 find_slot). */
+int vmlm_vm_find_slot(const vmlm_vm *vm, const char *name, uint32_t *slot);
+/* Device address (layer base applied), shape and dtype of a slot. */
+int vmlm_vm_slot_info(vmlm_vm *vm, uint32_t slot, void **dptr, uint32_t *rows, uint32_t *cols,
+                      uint8_t *dtype);
+/* Copies f32 values into / out of an activation, state or gradient slot
+ * (the runtime's token files: st_tok, st_gen). */
+int vmlm_vm_write_slot(vmlm_vm *vm, uint32_t slot, const float *host, size_t count);
+int vmlm_vm_read_slot(vmlm_vm *vm, uint32_t slot, float *host, size_t count);
+/* Values PRINTed so far (all runs): *count of them, the first `cap` copied. */
+int vmlm_vm_output(vmlm_vm *vm, float *host, size_t cap, size_t *count);
+int vmlm_vm_clear_output(vmlm_vm *vm);
+void *vmlm_vm_stream(vmlm_vm *vm);
+/* Constant pools uploaded by this process so far (shared pools count once). */
+int vmlm_vm_pool_uploads(size_t *n);
+
 /* ================================================================ tables */
 
 /* sys/src/lib.rs:29-38 `#[repr(C)] struct Backend`, field for field: the

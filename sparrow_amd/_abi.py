@@ -128,6 +128,18 @@ SIGNATURES = {
     "vmlm_decoder_fused": (I, [P]),
     "vmlm_decoder_time_gemv": (I, [P, I, U32, C.POINTER(F), C.POINTER(C.c_double)]),
     "vmlm_b1_stack_forward": (I, [C.POINTER(SparseConnW), U32, P, P, SZ, U16, P]),
+    "vmlm_vm_load": (I, [C.c_char_p, SZ, P, SZ, C.POINTER(P)]),
+    "vmlm_vm_destroy": (I, [P]),
+    "vmlm_vm_run": (I, [P]),
+    "vmlm_vm_find_slot": (I, [P, C.c_char_p, C.POINTER(U32)]),
+    "vmlm_vm_slot_info": (I, [P, U32, C.POINTER(P), C.POINTER(U32), C.POINTER(U32),
+                              C.POINTER(U8)]),
+    "vmlm_vm_write_slot": (I, [P, U32, P, SZ]),
+    "vmlm_vm_read_slot": (I, [P, U32, P, SZ]),
+    "vmlm_vm_output": (I, [P, P, SZ, C.POINTER(SZ)]),
+    "vmlm_vm_clear_output": (I, [P]),
+    "vmlm_vm_stream": (P, [P]),
+    "vmlm_vm_pool_uploads": (I, [C.POINTER(SZ)]),
     "vmlm_hip_backend": (P, []),
     "vmlm_backend_dot256": (F, [P, P, SZ]),
     "vmlm_backend_axpy256": (None, [P, P, F, SZ]),

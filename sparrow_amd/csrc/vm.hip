@@ -1,0 +1,1242 @@
+// vm.hip -- device-resident executor of .vmb programs: the reference VM's
+// loader and interpreter (core/src/interp.rs) with every tensor in HBM.
+//
+// Load (Vm::load_impl, core/src/interp.rs:108-236): the image's TEXT and META
+// are parsed on the host; the constant pool is uploaded to the device once
+// (read-only there; a mapped weights region passed to vmlm_vm_load is shared
+// by every VM loaded over the same host range); the activation, state and
+// gradient arenas are allocated on the device, 64-byte aligned and zeroed;
+// every slot is bound to a byte offset in its region (bind_slots :351-396);
+// the load-time audit (audit_const_dtypes :241-348) runs over TEXT.
+//
+// Run (Vm::run :720-2370): the host walks TEXT and enqueues each opcode's
+// kernels on the VM's stream with the slots' device addresses; constants
+// are addressed through the layer base (const_ptr :434-467). Scalars that
+// steer the host (LOOP_CNT / CMPLE / LAYERB operands, RMSNORM / LN eps, ROPE
+// theta, SCALE factor) are read back from the device; values of constant
+// slots are cached per device address since the pool never changes.
+// Index guards that depend on device data (EMB rows, SPARSE_MATVEC offsets
+// and sources, runtime columns and positions) set the library's device
+// guard flag and skip the offending work; run() then returns 9.
+//
+// Status codes are the reference's exit codes: 9 guard, 5 unimplemented op,
+// 6 training op (the engine's build without the train feature), 3 bad magic,
+// 2 device failure. Beyond the reference, operand extents are checked
+// against the slots before a kernel touches them (9 where the reference
+// would read neighbouring memory), and bit 6 of `fl` gives three opcodes a
+// runtime operand read from a slot (ROPE position from slot `dt`, WRITECOL
+// column from slot `dt`, SOFTMAX live width from slot `b`).
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace vmlm {
+
+enum : uint8_t {
+    VOP_HALT = 0, VOP_COPY = 2, VOP_TRANSPOSE = 4, VOP_CONCAT = 5, VOP_SLICE = 6,
+    VOP_LAYERB = 7, VOP_GEMM = 10, VOP_BMM = 11, VOP_OUTER = 12, VOP_GEMV = 13, VOP_EMB = 14,
+    VOP_EWADD = 20, VOP_EWMUL = 21, VOP_EWSUB = 22, VOP_EWDIV = 23, VOP_SCALE = 24,
+    VOP_ACT = 25, VOP_EXP = 26, VOP_LOG = 27, VOP_CLAMP = 28, VOP_NEG = 29, VOP_LN = 30,
+    VOP_RMSNORM = 31, VOP_SUM = 32, VOP_MAX = 34, VOP_SOFTMAX = 36, VOP_MASK_MUL = 40,
+    VOP_TOPK_THRESH = 41, VOP_TOPK_IDX = 42, VOP_JMP = 46, VOP_CMPLE = 47, VOP_SAVE = 49,
+    VOP_LOAD = 50, VOP_PRINT = 51, VOP_SHAPE = 52, VOP_BIAS = 53, VOP_WRITECOL = 71,
+    VOP_EWMAX = 72, VOP_GEMASK = 73, VOP_LN_EPS = 85, VOP_PUSH = 86, VOP_POP = 87,
+    VOP_STACK_INIT = 88, VOP_LOOP_CNT = 89, VOP_ROPE = 90, VOP_SIN = 91, VOP_COS = 92,
+    VOP_TOPK_BY_STRENGTH = 93, VOP_SPARSE_MATVEC = 94,
+};
+enum : uint8_t { VDT_F32 = 0, VDT_F16 = 1, VDT_I8 = 2, VDT_I32 = 3, VDT_BF16 = 4 };
+enum : uint32_t { VSLOT_CONST = 0, VSLOT_ACT = 1, VSLOT_STATE = 2, VSLOT_GRAD = 3,
+                  VSLOT_PARAM = 4 };
+constexpr uint8_t VFL_ACC = 1, VFL_TRANS_B = 2, VFL_CAUSAL = 16, VFL_NNZ = 64,
+                  VFL_SELGATE = 128, VFL_RUNTIME = 64;
+constexpr size_t VM_TOPK_MAX_L = 2048;
+
+static size_t vdtype_size(uint8_t dt) {
+    switch (dt) {
+    case VDT_F32: case VDT_I32: return 4;
+    case VDT_BF16: case VDT_F16: return 2;
+    case VDT_I8: return 1;
+    default: return 0;
+    }
+}
+
+// ------------------------------------------------------------------ kernels
+// An f32 value in device memory used as a count, column or position:
+// non-negative, integral and below `limit` (the EMB rule); else the guard
+// flag is set and -1 returned.
+__device__ __forceinline__ long dev_index(const float *p, long limit, int *guard) {
+    const float v = *p;
+    bool bad = !(v >= 0.0f) || v >= (float)limit;
+    long u = 0;
+    if (!bad) {
+        u = (long)v;
+        bad = (float)u != v;
+    }
+    if (bad) {
+        atomicOr(guard, 1);
+        return -1;
+    }
+    return u;
+}
+
+// Rust's `f as usize` (saturating: NaN and negatives give 0), the cast the
+// reference applies to f32-held offsets and ids before checking them.
+__device__ __forceinline__ size_t as_usize(float f) {
+    return f > 0.0f ? (f >= 1.8446744e19f ? ~(size_t)0 : (size_t)f) : 0;
+}
+
+// EWADD/EWMUL/EWSUB/EWDIV with the broadcast forms of core/src/interp.rs:
+// 829-883: b is [r,1] (mode 1), [1,c] (mode 2) or one value (mode 3).
+__global__ __launch_bounds__(256) void vm_ew_bcast_kernel(float *d, const float *a,
+                                                          const float *b, size_t r, size_t c,
+                                                          int mode, int op) {
+    const size_t n = r * c, stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+        const float x = a[e];
+        const float y = mode == 1 ? b[e / c] : mode == 2 ? b[e % c] : b[0];
+        d[e] = op == VOP_EWADD ? x + y : op == VOP_EWMUL ? x * y : op == VOP_EWSUB ? x - y : x / y;
+    }
+}
+
+// EXP / LOG / SIN / COS / NEG / GEMASK / CLAMP / EWMAX (:1045-1065,
+// 1133-1157, 1273-1318): the reference's scalar functions, element by element.
+__global__ __launch_bounds__(256) void vm_unary_kernel(float *d, const float *a, const float *b,
+                                                       size_t n, int op) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+        const float x = a[e];
+        float y;
+        switch (op) {
+        case VOP_EXP: y = exp_f(x); break;
+        case VOP_LOG: y = ln_f(x); break;
+        case VOP_SIN: { float s, c; sincos_f(x, &s, &c); y = s; } break;
+        case VOP_COS: { float s, c; sincos_f(x, &s, &c); y = c; } break;
+        case VOP_NEG: y = -x; break;
+        case VOP_GEMASK: y = x >= 0.0f ? 1.0f : 0.0f; break;
+        case VOP_CLAMP: { const float lo = b[0], hi = b[1]; y = x < lo ? lo : x > hi ? hi : x; } break;
+        default: { const float z = b[e]; y = x > z ? x : z; }  // EWMAX
+        }
+        d[e] = y;
+    }
+}
+
+// MASK_MUL (:1067-1083): d[i,j] = a[i,j] * (b[i] or b[i,j]).
+__global__ __launch_bounds__(256) void vm_mask_mul_kernel(float *d, const float *a,
+                                                          const float *b, size_t r, size_t c,
+                                                          size_t bcols) {
+    const size_t n = r * c, stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+        const size_t i = e / c, j = e % c;
+        d[e] = a[e] * (bcols == 1 ? b[i] : b[i * bcols + j]);
+    }
+}
+
+// d[j * m + i] = a[i * c + j] (TRANSPOSE, :1468-1484).
+__global__ __launch_bounds__(256) void vm_transpose_kernel(float *d, const float *a, size_t m,
+                                                           size_t c) {
+    const size_t n = m * c, stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+        const size_t j = e / m, i = e % m;
+        d[e] = a[i * c + j];
+    }
+}
+
+// Row-strided copy: d[i * dld + doff + j] = s[i * sld + soff + j] for i < rows,
+// j < cols (SLICE, WRITECOL, CONCAT halves, PUSH / POP). With `offp` the
+// destination offset is read from the device (WRITECOL with a runtime column)
+// and checked against `dlimit` columns.
+__global__ __launch_bounds__(256) void vm_copy2d_kernel(float *d, size_t dld, size_t doff,
+                                                        const float *s, size_t sld, size_t soff,
+                                                        size_t rows, size_t cols,
+                                                        const float *offp, size_t dlimit,
+                                                        int *guard) {
+    if (offp) {
+        const long o = dev_index(offp, (long)dlimit + 1, guard);
+        if (o < 0 || (size_t)o + cols > dlimit) {
+            if (o >= 0) atomicOr(guard, 1);
+            return;
+        }
+        doff = (size_t)o;
+    }
+    const size_t n = rows * cols, stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) {
+        const size_t i = e / cols, j = e % cols;
+        d[i * dld + doff + j] = s[i * sld + soff + j];
+    }
+}
+
+// One thread per row, left to right: SUM (:1535-1546), MAX (:1584-1621:
+// first element, then strict `>`) and GEMV (:815-827, s += a * b).
+__global__ __launch_bounds__(256) void vm_rowwise_kernel(float *d, const float *a, const float *b,
+                                                         size_t r, size_t c, int op) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= r) return;
+    const float *row = a + i * c;
+    float s;
+    if (op == VOP_MAX) {
+        s = row[0];
+        for (size_t j = 1; j < c; ++j)
+            if (row[j] > s) s = row[j];
+    } else if (op == VOP_GEMV) {
+        s = 0.0f;
+        for (size_t j = 0; j < c; ++j) s += row[j] * b[j];
+    } else {
+        s = 0.0f;
+        for (size_t j = 0; j < c; ++j) s += row[j];
+    }
+    d[i] = s;
+}
+
+// SCALE (:1225-1235): d = a * s, s from the device.
+__global__ __launch_bounds__(256) void vm_scale_kernel(float *d, const float *a, const float *sp,
+                                                       size_t n) {
+    const float s = *sp;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += stride) d[e] = a[e] * s;
+}
+
+// EMB over an f32 table (:1423-1434); the bf16 table goes through
+// emb_bf16_kernel.
+__global__ void vm_emb_f32_kernel(float *d, const float *table, size_t rows, size_t cols,
+                                  const float *rowf, int *guard) {
+    const long row = dev_index(rowf, (long)rows, guard);
+    if (row < 0) return;
+    for (size_t i = threadIdx.x; i < cols; i += blockDim.x) d[i] = table[(size_t)row * cols + i];
+}
+
+// ROPE with the position read from the device (runtime position): the
+// rotation of rope_kernel, positions pos + row.
+__global__ void vm_rope_kernel(float *dst, const float *src, int rows, int hd, float step,
+                               const float *posp, int *guard) {
+    const long pos = dev_index(posp, 1L << 24, guard);
+    if (pos < 0) return;
+    const int half = hd / 2;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * half) return;
+    const int row = (int)(idx / half), i = (int)(idx % half);
+    const float *sr = src + (size_t)row * hd;
+    float *dr = dst + (size_t)row * hd;
+    float y1, y2;
+    rope_pair(sr[i], sr[i + half], (float)pos + (float)row, i, step, &y1, &y2);
+    dr[i] = y1;
+    dr[i + half] = y2;
+}
+
+// SOFTMAX with the live width read from the device: columns [0, live) as
+// the softmax kernel (block max, exp_f, block sum, * 1/sum), the rest 0.
+__global__ __launch_bounds__(256) void vm_softmax_live_kernel(float *p, int cols,
+                                                              const float *livep, int *guard) {
+    __shared__ float sh[4];
+    const long live = dev_index(livep, (long)cols + 1, guard);
+    if (live < 0) return;
+    float *row = p + (size_t)blockIdx.x * cols;
+    const int lim = (int)live;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < lim; i += 256) mx = fmaxf(mx, row[i]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < lim; i += 256) {
+        const float e = exp_f(row[i] - mx);
+        row[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    const float inv = 1.0f / s;
+    for (int i = threadIdx.x; i < lim; i += 256) row[i] *= inv;
+    for (int i = lim + threadIdx.x; i < cols; i += 256) row[i] = 0.0f;
+}
+
+// ops/src/kernels.rs:1462-1495 topk_thresh per row (one thread, the
+// reference's repeated strict-`>` selection; `used` holds c flags per row).
+__global__ __launch_bounds__(64) void vm_topk_thresh_kernel(float *d, const float *a, size_t r,
+                                                            size_t c, size_t k,
+                                                            unsigned char *used) {
+    const size_t i = (size_t)blockIdx.x * 64 + threadIdx.x;
+    if (i >= r) return;
+    const float *x = a + i * c;
+    unsigned char *u = used + i * c;
+    for (size_t j = 0; j < c; ++j) u[j] = 0;
+    float best = -__builtin_inff();
+    size_t found = 0;
+    while (found < k && found < c) {
+        long bi = -1;
+        float bv = -__builtin_inff();
+        for (size_t j = 0; j < c; ++j)
+            if (!u[j] && x[j] > bv) {
+                bv = x[j];
+                bi = (long)j;
+            }
+        if (bi < 0) break;
+        u[bi] = 1;
+        best = bv;
+        ++found;
+    }
+    d[i] = best;
+}
+
+// TOPK_BY_STRENGTH (:1743-1955) per row of L values (one thread each; the
+// flat form is one row of sr * sc): k rounds of "the first untaken value,
+// replaced by a strictly greater untaken one", then the chosen indices in
+// ascending order with their values; `kseg` output pairs per row, the
+// unused ones 0. k comes from the device and is checked there.
+__global__ __launch_bounds__(64) void vm_topk_strength_kernel(float *d, size_t dld,
+                                                              const float *s, size_t rows,
+                                                              size_t L, const float *kp,
+                                                              size_t kmax, size_t kseg,
+                                                              unsigned char *taken, int *guard) {
+    const size_t r = (size_t)blockIdx.x * 64 + threadIdx.x;
+    if (r >= rows) return;
+    const float kf = *kp;
+    const size_t k = as_usize(kf);
+    if (!(kf >= 0.0f) || k > kmax) {
+        atomicOr(guard, 1);
+        return;
+    }
+    const float *row = s + r * L;
+    unsigned char *t = taken + r * L;
+    for (size_t i = 0; i < L; ++i) t[i] = 0;
+    for (size_t q = 0; q < k; ++q) {
+        long best = -1;
+        float bv = 0.0f;
+        for (size_t i = 0; i < L; ++i) {
+            if (t[i]) continue;
+            const float v = row[i];
+            if (best < 0 || v > bv) {
+                bv = v;
+                best = (long)i;
+            }
+        }
+        if (best < 0) break;
+        t[best] = 1;
+    }
+    float *out = d + r * dld;
+    size_t o = 0;
+    for (size_t i = 0; i < L && o < kseg; ++i)
+        if (t[i]) {
+            out[2 * o] = (float)i;
+            out[2 * o + 1] = row[i];
+            ++o;
+        }
+    for (; o < kseg; ++o) out[2 * o] = out[2 * o + 1] = 0.0f;
+}
+
+// SPARSE_MATVEC (:2058-2346), one thread per neuron j over its CSR row
+// [off[j], off[j+1]) (or, with selgate, the row-relative survivors listed in
+// sel[j]): first term assigned, then acc + w * x[src], in order. Offsets,
+// survivors and source ids are checked here (guard flag, neuron skipped);
+// each neuron's term count goes to cnt[j].
+__global__ __launch_bounds__(64) void vm_sparse_matvec_kernel(
+    float *d, const float *off, const float *src, const float *w, const float *x, size_t n,
+    size_t nnz, size_t nx, const float *sel, size_t seg, unsigned *cnt, int *guard) {
+    const size_t j = (size_t)blockIdx.x * 64 + threadIdx.x;
+    if (j >= n) return;
+    cnt[j] = 0;
+    const size_t o0 = as_usize(off[j]), o1 = as_usize(off[j + 1]);
+    if (o1 > nnz || o0 > o1) {
+        atomicOr(guard, 1);
+        return;
+    }
+    if (o0 == o1) {
+        d[j] = 0.0f;
+        return;
+    }
+    float acc = 0.0f;
+    unsigned done = 0;
+    if (sel) {
+        for (size_t q = 0; q < seg; ++q) {
+            const size_t rel = as_usize(sel[(j * seg + q) * 2]);
+            if (q > 0 && rel == 0) break;
+            const size_t idx = o0 + rel;
+            if (idx < o0 || idx >= o1) {
+                atomicOr(guard, 1);
+                return;
+            }
+            const size_t sid = as_usize(src[idx]);
+            if (sid >= nx) {
+                atomicOr(guard, 1);
+                return;
+            }
+            const float term = w[idx] * x[sid];
+            acc = done == 0 ? term : acc + term;
+            ++done;
+        }
+    } else {
+        for (size_t t = o0; t < o1; ++t) {
+            const size_t sid = as_usize(src[t]);
+            if (sid >= nx) {
+                atomicOr(guard, 1);
+                return;
+            }
+            const float term = w[t] * x[sid];
+            acc = t == o0 ? term : acc + term;
+            ++done;
+        }
+    }
+    d[j] = acc;
+    cnt[j] = done;
+}
+
+// The count of terms performed (FL_NNZ): d[0] = sum of cnt, one thread.
+__global__ void vm_nnz_kernel(float *d, const unsigned *cnt, size_t n) {
+    if (threadIdx.x != 0) return;
+    size_t s = 0;
+    for (size_t j = 0; j < n; ++j) s += cnt[j];
+    d[0] = (float)s;
+}
+
+static unsigned vm_blocks(size_t n, unsigned per = 256) {
+    size_t b = (n + per - 1) / per;
+    return (unsigned)(b < 1 ? 1 : b > 65535 ? 65535 : b);
+}
+
+// ------------------------------------------------------------------ pools
+// Constant pools on the device, shared by every VM loaded over the same
+// mapped host range (vmlm_vm_load with `weights`); an image's own CONST
+// region is uploaded privately.
+struct ConstPool {
+    const void *host;  // null: private
+    size_t len;
+    char *dev;
+    int refs;
+};
+static std::mutex g_pool_mu;
+static std::vector<ConstPool *> g_pools;
+static size_t g_pool_uploads = 0;
+
+static void pool_release(ConstPool *p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    if (--p->refs > 0) return;
+    for (size_t i = 0; i < g_pools.size(); ++i)
+        if (g_pools[i] == p) g_pools.erase(g_pools.begin() + i);
+    (void)hipFree(p->dev);
+    delete p;
+}
+
+}  // namespace vmlm
+
+using namespace vmlm;
+
+struct VmIns {
+    uint8_t op, fl;
+    uint16_t dt;
+    uint32_t dst, a, b;
+};
+struct VmSlot {
+    size_t off;  // byte offset in its region (constants: in the pool)
+    uint32_t rows, cols;
+    uint32_t kind;
+    uint8_t dtype;
+};
+
+struct vmlm_vm {
+    std::vector<VmIns> text;
+    std::vector<VmSlot> slots;
+    std::vector<uint32_t> names;
+    ConstPool *pool = nullptr;
+    size_t const_bytes = 0;
+    char *act = nullptr, *state = nullptr, *grad = nullptr;
+    size_t act_b = 0, state_b = 0, grad_b = 0;
+    hipStream_t st = nullptr;
+    size_t layer_base = 0;
+    float ln_eps = 1e-5f;
+    std::vector<float> out;
+    std::unordered_map<uintptr_t, float> kcache;  // values of constant scalars
+    void *ws = nullptr;                            // executor workspace
+    size_t ws_bytes = 0;
+    unsigned long long *keys = nullptr;            // TOPK_IDX reduction keys
+};
+
+static uint32_t rd32(const uint8_t *p, size_t off) {
+    uint32_t v;
+    std::memcpy(&v, p + off, 4);
+    return v;
+}
+
+static void vm_free(vmlm_vm *vm) {
+    if (!vm) return;
+    if (vm->st) (void)hipStreamSynchronize(vm->st);
+    pool_release(vm->pool);
+    for (void *p : {(void *)vm->act, (void *)vm->state, (void *)vm->grad, vm->ws, (void *)vm->keys})
+        if (p) (void)hipFree(p);
+    if (vm->st) (void)hipStreamDestroy(vm->st);
+    delete vm;
+}
+
+// core/src/interp.rs:241-348 audit_const_dtypes.
+static int vm_audit(const vmlm_vm *vm) {
+    const size_t ns = vm->slots.size();
+    auto dt = [&](uint32_t s) { return s < ns ? vm->slots[s].dtype : (uint8_t)VDT_F32; };
+    for (const VmIns &in : vm->text) {
+        if (in.op == VOP_GEMM) {
+            const uint8_t b = dt(in.b);
+            if (b == VDT_BF16 || b == VDT_I8) continue;
+            VMLM_GUARD(b == VDT_F32, "gemm B has no kernel for this dtype");
+            continue;
+        }
+        if (in.op == VOP_EMB && dt(in.a) == VDT_BF16 && in.dst < ns && dt(in.dst) == VDT_F32)
+            continue;
+        bool cd = true, ca = true, cb = true;
+        if (in.op == VOP_SHAPE) cd = ca = cb = false;
+        else if (in.op == VOP_LOOP_CNT) cd = cb = false;
+        else if (in.op == VOP_SLICE || in.op == VOP_WRITECOL || in.op == VOP_PUSH ||
+                 in.op == VOP_POP)
+            cb = false;
+        const uint32_t probe[3] = {cd ? in.dst : UINT32_MAX, ca ? in.a : UINT32_MAX,
+                                   cb ? in.b : UINT32_MAX};
+        for (uint32_t s : probe) {
+            if (s >= ns || dt(s) == VDT_F32) continue;
+            const uint8_t d = dt(s);
+            return fail(VMLM_ERR_GUARD,
+                        "op %u uses %s const at slot %u (only a GEMM may read a non-f32 operand)",
+                        in.op, d == VDT_BF16 ? "bf16" : d == VDT_I8 ? "i8" : "non-f32", s);
+        }
+    }
+    return VMLM_OK;
+}
+
+extern "C" {
+
+int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weights_len,
+                 vmlm_vm **out) {
+    VMLM_GUARD(out != nullptr && image != nullptr, "vm_load: null argument");
+    *out = nullptr;
+    int rc = ensure_init();
+    if (rc) return rc;
+    const uint8_t *img = (const uint8_t *)image;
+    if (len < 32 || rd32(img, 0) != 0x4D4C4D56u) return fail(3, "bad magic");
+    vmlm_vm *vm = new vmlm_vm();
+    auto bad = [&](int code) {
+        vm_free(vm);
+        return code;
+    };
+    const size_t text_off = rd32(img, 8), text_len = rd32(img, 12), const_off = rd32(img, 16),
+                 meta_off = rd32(img, 24);
+    vm->const_bytes = rd32(img, 20);
+    if (text_off + text_len > len || meta_off + 28 > len ||
+        (!weights && const_off + vm->const_bytes > len) ||
+        (weights && weights_len < vm->const_bytes))
+        return bad(fail(VMLM_ERR_GUARD, "vm_load: image regions past its end"));
+    vm->text.resize(text_len / 16);
+    for (size_t i = 0; i < vm->text.size(); ++i) {
+        const uint8_t *q = img + text_off + 16 * i;
+        VmIns &in = vm->text[i];
+        in.op = q[0];
+        in.fl = q[1];
+        std::memcpy(&in.dt, q + 2, 2);
+        in.dst = rd32(q, 4);
+        in.a = rd32(q, 8);
+        in.b = rd32(q, 12);
+    }
+    const uint8_t *meta = img + meta_off;
+    const size_t n_const = rd32(meta, 0), n_slot = rd32(meta, 4), slots_off = rd32(meta, 8),
+                 names_off = rd32(meta, 24);
+    vm->act_b = rd32(meta, 12);
+    vm->state_b = rd32(meta, 16);
+    vm->grad_b = rd32(meta, 20);
+    if (meta_off + slots_off + 16 * n_slot > len || meta_off + names_off + 4 * n_slot > len ||
+        meta_off + 28 + 24 * n_const > len)
+        return bad(fail(VMLM_ERR_GUARD, "vm_load: META tables past the image end"));
+    vm->slots.resize(n_slot);
+    vm->names.resize(n_slot);
+    for (size_t i = 0; i < n_slot; ++i) {
+        const uint8_t *e = meta + slots_off + 16 * i;
+        VmSlot &s = vm->slots[i];
+        s.kind = rd32(e, 0);
+        const uint32_t idx = rd32(e, 4);
+        s.rows = rd32(e, 8);
+        s.cols = rd32(e, 12);
+        s.dtype = VDT_F32;
+        vm->names[i] = rd32(meta + names_off, 4 * i);
+        const size_t need = (size_t)s.rows * s.cols;
+        if (s.kind == VSLOT_CONST || s.kind == VSLOT_PARAM) {
+            if (idx >= n_const)
+                return bad(fail(VMLM_ERR_GUARD, "slot %zu names const %u of %zu", i, idx, n_const));
+            const uint8_t *ce = meta + 28 + 24 * (size_t)idx;
+            const uint32_t off = rd32(ce, 0), clen = rd32(ce, 4);
+            s.dtype = ce[16];
+            const size_t esz = vdtype_size(s.dtype);
+            if (esz == 0) return bad(fail(VMLM_ERR_GUARD, "const has unknown dtype"));
+            if (need * esz > clen || (size_t)off + clen > vm->const_bytes)
+                return bad(fail(VMLM_ERR_GUARD, "slot %zu (%ux%u) exceeds its constant", i,
+                                s.rows, s.cols));
+            s.off = off;
+        } else {
+            const size_t bytes = s.kind == VSLOT_STATE ? vm->state_b
+                                 : s.kind == VSLOT_GRAD ? vm->grad_b : vm->act_b;
+            if ((size_t)idx + need * 4 > bytes + 64)
+                return bad(fail(VMLM_ERR_GUARD, "slot %zu (%ux%u) exceeds its arena", i, s.rows,
+                                s.cols));
+            s.off = idx / 4 * 4;
+        }
+    }
+    if ((rc = vm_audit(vm))) return bad(rc);
+
+    hipError_t e = hipStreamCreateWithFlags(&vm->st, hipStreamNonBlocking);
+    if (e != hipSuccess) return bad(hip_fail(e, "vm stream"));
+    // the constant pool: shared when the caller maps its weights, else private
+    const void *host = weights ? weights : (const void *)(img + const_off);
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        if (weights)
+            for (ConstPool *p : g_pools)
+                if (p->host == weights && p->len == vm->const_bytes) {
+                    ++p->refs;
+                    vm->pool = p;
+                    break;
+                }
+        if (!vm->pool) {
+            ConstPool *p = new ConstPool{weights, vm->const_bytes, nullptr, 1};
+            if ((e = hipMalloc(&p->dev, vm->const_bytes + 64)) != hipSuccess) {
+                delete p;
+                return bad(hip_fail(e, "const pool"));
+            }
+            if (vm->const_bytes &&
+                (e = hipMemcpy(p->dev, host, vm->const_bytes, hipMemcpyHostToDevice)) != hipSuccess) {
+                (void)hipFree(p->dev);
+                delete p;
+                return bad(hip_fail(e, "const pool upload"));
+            }
+            ++g_pool_uploads;
+            if (weights) g_pools.push_back(p);
+            vm->pool = p;
+        }
+    }
+    for (auto [pp, bytes] : {std::pair<char **, size_t>{&vm->act, vm->act_b},
+                             {&vm->state, vm->state_b}, {&vm->grad, vm->grad_b}}) {
+        if ((e = hipMalloc((void **)pp, bytes + 64)) != hipSuccess) return bad(hip_fail(e, "arena"));
+        if ((rc = launch_fill_zero(*pp, bytes + 64, vm->st))) return bad(rc);
+    }
+    if ((e = hipMalloc((void **)&vm->keys, 64)) != hipSuccess) return bad(hip_fail(e, "vm keys"));
+    if ((e = hipStreamSynchronize(vm->st)) != hipSuccess) return bad(hip_fail(e, "vm load"));
+    *out = vm;
+    return VMLM_OK;
+}
+
+int vmlm_vm_destroy(vmlm_vm *vm) {
+    vm_free(vm);
+    return VMLM_OK;
+}
+
+int vmlm_vm_pool_uploads(size_t *n) {
+    VMLM_GUARD(n, "null argument");
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    *n = g_pool_uploads;
+    return VMLM_OK;
+}
+
+void *vmlm_vm_stream(vmlm_vm *vm) { return vm ? (void *)vm->st : nullptr; }
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ run
+namespace {
+
+struct Exec {
+    vmlm_vm *vm;
+    int *guard;
+
+    size_t nel(uint32_t s) const {
+        return s < vm->slots.size() ? (size_t)vm->slots[s].rows * vm->slots[s].cols : 0;
+    }
+    uint32_t rows(uint32_t s) const { return s < vm->slots.size() ? vm->slots[s].rows : 0; }
+    uint32_t cols(uint32_t s) const { return s < vm->slots.size() ? vm->slots[s].cols : 0; }
+    uint8_t dt(uint32_t s) const {
+        return s < vm->slots.size() ? vm->slots[s].dtype : (uint8_t)VDT_F32;
+    }
+
+    // core/src/interp.rs:434-467: a slot's device address, constants through
+    // the layer base with its bound check.
+    int ptr(uint32_t i, float **p) {
+        VMLM_GUARD(i < vm->slots.size(), "slot %u does not exist", i);
+        const VmSlot &s = vm->slots[i];
+        char *base;
+        size_t off = s.off;
+        if (s.kind == VSLOT_CONST || s.kind == VSLOT_PARAM) {
+            const size_t bytes = (size_t)s.rows * s.cols * vdtype_size(s.dtype);
+            VMLM_GUARD(off + vm->layer_base + bytes <= vm->const_bytes,
+                       "layer base walks past the constant pool: off=%zu base=%zu bytes=%zu limit=%zu",
+                       off, vm->layer_base, bytes, vm->const_bytes);
+            base = vm->pool->dev;
+            off += vm->layer_base;
+        } else {
+            base = s.kind == VSLOT_STATE ? vm->state : s.kind == VSLOT_GRAD ? vm->grad : vm->act;
+        }
+        *p = (float *)(base + off);
+        return VMLM_OK;
+    }
+    // element 0 of a slot on the host (constants cached by device address)
+    int scalar(uint32_t i, float *v) {
+        float *p;
+        int rc = ptr(i, &p);
+        if (rc) return rc;
+        VMLM_GUARD(nel(i) >= 1 && dt(i) == VDT_F32, "slot %u holds no f32 value", i);
+        const bool is_const = vm->slots[i].kind == VSLOT_CONST;
+        if (is_const) {
+            auto it = vm->kcache.find((uintptr_t)p);
+            if (it != vm->kcache.end()) {
+                *v = it->second;
+                return VMLM_OK;
+            }
+        }
+        VMLM_HIP_CHECK(hipMemcpyAsync(v, p, 4, hipMemcpyDeviceToHost, vm->st));
+        VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
+        if (is_const) vm->kcache[(uintptr_t)p] = *v;
+        return VMLM_OK;
+    }
+    int ws(size_t bytes, void **p) {
+        if (bytes > vm->ws_bytes) {
+            VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
+            if (vm->ws) VMLM_HIP_CHECK(hipFree(vm->ws));
+            vm->ws = nullptr;
+            vm->ws_bytes = 0;
+            VMLM_HIP_CHECK(hipMalloc(&vm->ws, bytes));
+            vm->ws_bytes = bytes;
+        }
+        *p = vm->ws;
+        return VMLM_OK;
+    }
+    int copy(float *d, const float *s, size_t n) {
+        if (n && d != s)
+            VMLM_HIP_CHECK(hipMemcpyAsync(d, s, n * 4, hipMemcpyDeviceToDevice, vm->st));
+        return VMLM_OK;
+    }
+    int copy2d(float *d, size_t dld, size_t doff, const float *s, size_t sld, size_t soff,
+               size_t r, size_t c, const float *offp = nullptr, size_t dlimit = 0) {
+        if (r * c == 0) return VMLM_OK;
+        vm_copy2d_kernel<<<vm_blocks(r * c), 256, 0, vm->st>>>(d, dld, doff, s, sld, soff, r, c,
+                                                               offp, dlimit, guard);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+
+    int step(const VmIns &in, size_t *ip);
+};
+
+#define P_(name, slot)                 \
+    float *name;                       \
+    if ((rc = ptr((slot), &name))) return rc
+#define NEED(cond, ...) VMLM_GUARD(cond, __VA_ARGS__)
+
+int Exec::step(const VmIns &in, size_t *ip) {
+    int rc = VMLM_OK;
+    const uint32_t d = in.dst, a = in.a, b = in.b;
+    hipStream_t st = vm->st;
+    switch (in.op) {
+    case VOP_SHAPE: return VMLM_OK;
+    case VOP_COPY: case VOP_SAVE: case VOP_LOAD: {
+        NEED(nel(d) >= nel(a), "COPY: dst smaller than src");
+        P_(cd, d);
+        P_(ca, a);
+        return copy(cd, ca, nel(a));
+    }
+    case VOP_GEMM: {  // core/src/interp.rs:734-813
+        const size_t m = rows(a), k = cols(a), brows = rows(b), bcols = cols(b);
+        const bool nt = (in.fl & VFL_TRANS_B) == 0, acc = (in.fl & VFL_ACC) != 0;
+        const uint8_t bt = dt(b);
+        const size_t n = nt ? brows : bcols;
+        if (bt == VDT_BF16 || bt == VDT_I8) {
+            NEED(nt, "%s NN gemm unimplemented", bt == VDT_I8 ? "int8" : "bf16");
+            NEED(!acc, "%s acc gemm unimplemented", bt == VDT_I8 ? "int8" : "bf16");
+        }
+        if (bt == VDT_I8) {
+            NEED(in.dt < vm->slots.size() && dt(in.dt) == VDT_F32,
+                 "int8 gemm: scale slot must be f32");
+            NEED(nel(in.dt) >= brows, "int8 gemm: scale shorter than N rows");
+        }
+        NEED(nel(d) >= m * n && brows * bcols >= n * k, "GEMM: operand extents");
+        P_(cc, d);
+        P_(ca, a);
+        P_(cb, b);
+        if (bt == VDT_BF16)
+            return vmlm_hip_gemm_nt_bf16(ca, (const uint16_t *)cb, cc, m, brows, k, st);
+        if (bt == VDT_I8) {
+            P_(cs, in.dt);
+            return vmlm_hip_gemm_nt_int8(ca, (const int8_t *)cb, cs, cc, m, brows, k, st);
+        }
+        NEED(bt == VDT_F32, "gemm operand dtype unsupported");
+        return nt ? vmlm_hip_gemm_nt(ca, cb, cc, m, brows, k, acc, st)
+                  : vmlm_hip_gemm(ca, cb, cc, m, bcols, k, acc, st);
+    }
+    case VOP_GEMV: {
+        const size_t m = rows(a), k = cols(a);
+        NEED(nel(b) >= k && nel(d) >= m, "GEMV: operand extents");
+        P_(ca, a);
+        P_(cb, b);
+        P_(cc, d);
+        if (m == 0) return VMLM_OK;
+        vm_rowwise_kernel<<<vm_blocks(m), 256, 0, st>>>(cc, ca, cb, m, k, VOP_GEMV);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_EWADD: case VOP_EWMUL: case VOP_EWSUB: case VOP_EWDIV: {
+        const size_t r = rows(a), c = cols(a), br = rows(b), bc = cols(b);
+        NEED(nel(d) >= r * c, "EW: dst smaller than a");
+        P_(ca, a);
+        P_(cb, b);
+        P_(cc, d);
+        if (br == r && bc == c) return launch_ew(cc, ca, cb, r * c, in.op, st);
+        int mode = br == r && bc == 1 ? 1 : br == 1 && bc == c ? 2 : br * bc == 1 ? 3 : 0;
+        if (!mode) return fail(8, "EW shape mismatch");
+        if (r * c == 0) return VMLM_OK;
+        vm_ew_bcast_kernel<<<vm_blocks(r * c), 256, 0, st>>>(cc, ca, cb, r, c, mode, in.op);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_ACT: {
+        const size_t n = nel(d);
+        NEED(nel(a) >= n, "ACT: src smaller than dst");
+        P_(cd, d);
+        P_(ca, a);
+        if ((rc = copy(cd, ca, n))) return rc;
+        return launch_act(cd, n, in.fl == 0 ? VMLM_ACT_RELU : in.fl, st);
+    }
+    case VOP_LN: {
+        const size_t r = rows(a), c = cols(a);
+        NEED(nel(d) >= r * c && nel(b) >= c && nel(in.dt) >= c, "LN: operand extents");
+        P_(cd, d);
+        P_(ca, a);
+        P_(g, b);
+        P_(bias, in.dt);
+        if ((rc = copy(cd, ca, r * c))) return rc;
+        return launch_layernorm(cd, g, bias, r, c, vm->ln_eps, st);
+    }
+    case VOP_LN_EPS: return scalar(d, &vm->ln_eps);
+    case VOP_RMSNORM: {
+        const size_t r = rows(a), c = cols(a);
+        NEED(nel(d) >= r * c && nel(b) >= c, "RMSNORM: operand extents");
+        float eps;
+        if ((rc = scalar(in.dt, &eps))) return rc;
+        P_(cd, d);
+        P_(ca, a);
+        P_(g, b);
+        return launch_rmsnorm(cd, ca, g, r, c, eps, nullptr, 0, 0, st);
+    }
+    case VOP_PUSH: case VOP_POP: {
+        const uint32_t stk = in.op == VOP_PUSH ? d : a, one = in.op == VOP_PUSH ? a : d;
+        const size_t w = cols(stk);
+        NEED(nel(one) == w, in.op == VOP_PUSH ? "PUSH: src elems != stack row width"
+                                              : "POP: dst elems != stack row width");
+        NEED((size_t)b < rows(stk), "PUSH/POP: step past the stack");
+        P_(cs, stk);
+        P_(co, one);
+        return in.op == VOP_PUSH ? copy(cs + (size_t)b * w, co, w) : copy(co, cs + (size_t)b * w, w);
+    }
+    case VOP_STACK_INIT: {
+        P_(ca, a);
+        return launch_fill_zero(ca, nel(a) * 4, st);
+    }
+    case VOP_SOFTMAX: {
+        const size_t r = rows(d), c = cols(d);
+        NEED(nel(a) >= r * c, "SOFTMAX: src smaller than dst");
+        P_(cd, d);
+        P_(ca, a);
+        if ((rc = copy(cd, ca, r * c))) return rc;
+        if (in.fl & VFL_RUNTIME) {
+            P_(lp, b);
+            if (r == 0 || c == 0) return VMLM_OK;
+            vm_softmax_live_kernel<<<(unsigned)r, 256, 0, st>>>(cd, (int)c, lp, guard);
+            VMLM_HIP_CHECK(hipGetLastError());
+            return VMLM_OK;
+        }
+        return launch_softmax(cd, r, c, (in.fl & VFL_CAUSAL) != 0, st);
+    }
+    case VOP_OUTER: {
+        const size_t m = rows(a) == 1 ? cols(a) : rows(a), nn = rows(b) == 1 ? cols(b) : rows(b);
+        NEED(nel(d) >= m * nn, "OUTER: dst smaller than m x n");
+        P_(cs, d);
+        P_(cv, a);
+        P_(ck, b);
+        return launch_outer(cs, cv, ck, m, nn, 1.0f, st);
+    }
+    case VOP_TOPK_THRESH: {
+        const size_t r = rows(a), c = cols(a);
+        NEED(nel(d) >= r, "TOPK_THRESH: dst shorter than rows");
+        NEED(c <= 8192, "TOPK_THRESH: row wider than 8192");
+        P_(ca, a);
+        P_(cd, d);
+        void *used;
+        if ((rc = ws(r * c + 1, &used))) return rc;
+        if (r == 0) return VMLM_OK;
+        vm_topk_thresh_kernel<<<vm_blocks(r, 64), 64, 0, st>>>(cd, ca, r, c, in.fl < c ? in.fl : c,
+                                                                (unsigned char *)used);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_LAYERB: {
+        float d0;
+        if ((rc = scalar(a, &d0))) return rc;
+        if (d0 >= 0.0f) {
+            vm->layer_base += (size_t)d0;
+        } else {
+            const size_t back = (size_t)(-d0);
+            vm->layer_base = back > vm->layer_base ? 0 : vm->layer_base - back;
+        }
+        return VMLM_OK;
+    }
+    case VOP_EWMAX: case VOP_GEMASK: case VOP_EXP: case VOP_NEG: case VOP_LOG: case VOP_SIN:
+    case VOP_COS: case VOP_CLAMP: {
+        const size_t n = nel(a);
+        NEED(nel(d) >= n, "elementwise: dst smaller than src");
+        if (in.op == VOP_EWMAX) NEED(nel(b) >= n, "EWMAX: b smaller than a");
+        if (in.op == VOP_CLAMP) NEED(nel(b) >= 2, "CLAMP: bounds slot needs 2 values");
+        P_(ca, a);
+        P_(cd, d);
+        float *cb = nullptr;
+        if (in.op == VOP_EWMAX || in.op == VOP_CLAMP)
+            if ((rc = ptr(b, &cb))) return rc;
+        if (n == 0) return VMLM_OK;
+        vm_unary_kernel<<<vm_blocks(n), 256, 0, st>>>(cd, ca, cb, n, in.op);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_MASK_MUL: {
+        const size_t r = rows(d), c = cols(d), bc = cols(b);
+        NEED(nel(a) >= r * c && (r == 0 || (bc == 1 ? nel(b) >= r : nel(b) >= (r - 1) * bc + c)),
+             "MASK_MUL: operand extents");
+        P_(cd, d);
+        P_(ca, a);
+        P_(cb, b);
+        if (r * c == 0) return VMLM_OK;
+        vm_mask_mul_kernel<<<vm_blocks(r * c), 256, 0, st>>>(cd, ca, cb, r, c, bc);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_JMP:
+        *ip = d;
+        return VMLM_OK;
+    case VOP_CMPLE: {
+        float x, y;
+        if ((rc = scalar(a, &x)) || (rc = scalar(b, &y))) return rc;
+        if (x <= y) *ip = d;
+        return VMLM_OK;
+    }
+    case VOP_LOOP_CNT: {  // :1108-1131
+        NEED(rows(a) == 1, "LOOP_CNT: ctr must be [1,N]");
+        NEED(d < *ip, "LOOP_CNT: target must be back");
+        float v;
+        if ((rc = scalar(a, &v))) return rc;
+        const float nv = v - 1.0f;
+        P_(ca, a);
+        VMLM_HIP_CHECK(hipMemcpyAsync(ca, &nv, 4, hipMemcpyHostToDevice, st));
+        VMLM_HIP_CHECK(hipStreamSynchronize(st));  // `nv` lives on this frame
+        if (nv > 0.0f) *ip = d;
+        return VMLM_OK;
+    }
+    case VOP_ROPE: {  // :1159-1223
+        const size_t r = rows(a), c = cols(a);
+        NEED(c >= 2 && (c & 1) == 0, "ROPE: hd must be even >= 2");
+        NEED(nel(d) >= r * c, "ROPE: dst smaller than src");
+        float theta;
+        if ((rc = scalar(b, &theta))) return rc;
+        NEED(theta > 0.0f, "ROPE: theta must be > 0");
+        P_(cd, d);
+        P_(ca, a);
+        if (in.fl & VFL_RUNTIME) {
+            P_(pp, in.dt);
+            if (r == 0) return VMLM_OK;
+            const float step = -2.0f / (float)c * host_ln_f(theta);
+            vm_rope_kernel<<<vm_blocks(r * c / 2), 256, 0, st>>>(cd, ca, (int)r, (int)c, step, pp,
+                                                                 guard);
+            VMLM_HIP_CHECK(hipGetLastError());
+            return VMLM_OK;
+        }
+        return launch_rope(cd, ca, r, c, c, theta, (float)in.dt, 1, st);
+    }
+    case VOP_SCALE: {
+        const size_t n = nel(d);
+        NEED(nel(a) >= n && nel(b) >= 1, "SCALE: operand extents");
+        P_(cd, d);
+        P_(ca, a);
+        P_(cb, b);
+        if (n == 0) return VMLM_OK;
+        vm_scale_kernel<<<vm_blocks(n), 256, 0, st>>>(cd, ca, cb, n);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_PRINT: {
+        P_(cd, d);
+        const size_t n = nel(d), o = vm->out.size();
+        vm->out.resize(o + n);
+        if (n) VMLM_HIP_CHECK(hipMemcpyAsync(vm->out.data() + o, cd, n * 4, hipMemcpyDeviceToHost, st));
+        VMLM_HIP_CHECK(hipStreamSynchronize(st));
+        return VMLM_OK;
+    }
+    case VOP_BIAS: {
+        const size_t r = rows(d), c = cols(d);
+        NEED(nel(a) >= c, "BIAS: bias shorter than the row");
+        P_(cd, d);
+        P_(cb, a);
+        return launch_bias(cd, cb, r, c, st);
+    }
+    case VOP_EMB: {  // :1351-1436
+        const size_t r = rows(a), c = cols(a);
+        NEED(nel(d) >= c && nel(b) >= 1, "EMB: operand extents");
+        P_(cd, d);
+        P_(ca, a);
+        P_(rowp, b);
+        if (dt(a) == VDT_BF16)
+            return launch_emb_bf16(cd, c, (const uint16_t *)ca, r, c, rowp, nullptr, 1, st);
+        NEED(dt(a) == VDT_F32, "EMB table dtype unsupported");
+        vm_emb_f32_kernel<<<1, 256, 0, st>>>(cd, ca, r, c, rowp, guard);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_BMM: {  // :1440-1466
+        const size_t abm = rows(a), k = cols(a), bk = rows(b), nn = cols(b);
+        P_(ca, a);
+        P_(cb, b);
+        P_(cc, d);
+        if (bk == k) {
+            NEED(nel(d) >= abm * nn, "BMM: dst too small");
+            return vmlm_hip_gemm(ca, cb, cc, abm, nn, k, false, st);
+        }
+        NEED(k > 0 && bk % k == 0 && bk / k > 0 && abm % (bk / k) == 0, "BMM: batch shapes");
+        const size_t bs = bk / k, m = abm / bs;
+        NEED(nel(d) >= bs * m * nn, "BMM: dst too small");
+        for (size_t i = 0; i < bs; ++i)
+            if ((rc = vmlm_hip_gemm(ca + i * m * k, cb + i * k * nn, cc + i * m * nn, m, nn, k,
+                                    false, st)))
+                return rc;
+        return VMLM_OK;
+    }
+    case VOP_TRANSPOSE: {
+        const size_t m = rows(a), c = cols(a);
+        NEED(nel(d) >= m * c, "TRANSPOSE: dst smaller than src");
+        P_(ca, a);
+        P_(cd, d);
+        if (m * c == 0) return VMLM_OK;
+        vm_transpose_kernel<<<vm_blocks(m * c), 256, 0, st>>>(cd, ca, m, c);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_SLICE: {  // :1486-1497
+        const size_t dr = rows(d), dc = cols(d), sc = cols(a);
+        NEED(dr == 0 || dc == 0 || (dr - 1) * sc + b + dc <= nel(a), "SLICE: reads past src");
+        P_(ca, a);
+        P_(cd, d);
+        return copy2d(cd, dc, 0, ca, sc, b, dr, dc);
+    }
+    case VOP_CONCAT: {
+        const size_t r = rows(a), ac = cols(a), bc = cols(b);
+        NEED(rows(b) >= r && nel(d) >= r * (ac + bc), "CONCAT: operand extents");
+        P_(pa, a);
+        P_(pb, b);
+        P_(pd, d);
+        if ((rc = copy2d(pd, ac + bc, 0, pa, ac, 0, r, ac))) return rc;
+        return copy2d(pd, ac + bc, ac, pb, bc, 0, r, bc);
+    }
+    case VOP_WRITECOL: {  // :1515-1533
+        const size_t dr = rows(d), dc = cols(d), sr = rows(a), sc = cols(a);
+        NEED(sr >= dr, "WRITECOL: src has fewer rows than dst");
+        P_(ca, a);
+        P_(cd, d);
+        if (in.fl & VFL_RUNTIME) {
+            P_(cp, in.dt);
+            return copy2d(cd, dc, 0, ca, sc, 0, dr, sc, cp, dc);
+        }
+        NEED((size_t)b + sc <= dc, "WRITECOL: off + src.cols exceeds dst row width");
+        return copy2d(cd, dc, b, ca, sc, 0, dr, sc);
+    }
+    case VOP_SUM: case VOP_MAX: {
+        const size_t r = rows(a), c = cols(a);
+        if (in.op == VOP_MAX) {
+            NEED(c != 0 && rows(d) != 0 && cols(d) != 0, "MAX: src or dst slot has width 0");
+            NEED(rows(d) == r && cols(d) == 1, "MAX: dst must be [rows,1]");
+        }
+        NEED(nel(d) >= r, "SUM: dst shorter than rows");
+        P_(ca, a);
+        P_(cd, d);
+        if (r == 0) return VMLM_OK;
+        vm_rowwise_kernel<<<vm_blocks(r), 256, 0, st>>>(cd, ca, nullptr, r, c, in.op);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_TOPK_IDX: {  // :1649-1681
+        NEED(rows(a) && cols(a) && rows(d) && cols(d), "TOPK_IDX: src or dst slot has width 0");
+        NEED(rows(d) == 1 && cols(d) == 1, "TOPK_IDX: dst must be [1,1]");
+        P_(ca, a);
+        P_(cd, d);
+        return launch_argmax(ca, cols(a), cd, nullptr, vm->keys, st);
+    }
+    case VOP_TOPK_BY_STRENGTH: {  // :1743-1955
+        const size_t sr = rows(a), sc = cols(a), dr = rows(d), dc = cols(d);
+        NEED(sr && sc && dr && dc, "TOPK_BY_STRENGTH: src or dst slot has width 0");
+        const bool seg = (in.fl & VFL_SELGATE) != 0;
+        size_t nrow, L, kmax, kseg;
+        if (seg) {
+            NEED(sc >= 1 && dc % 2 == 0, "TOPK_BY_STRENGTH: segmented dst must be [n,2k]");
+            NEED(dr == sr, "TOPK_BY_STRENGTH: segmented dst rows != src rows");
+            NEED(sc <= VM_TOPK_MAX_L, "TOPK_BY_STRENGTH: row width exceeds the bitmap (2048)");
+            nrow = sr, L = sc, kseg = dc / 2, kmax = sc < kseg ? sc : kseg;
+        } else {
+            NEED(dc == 2, "TOPK_BY_STRENGTH: dst must be [L,2]");
+            NEED(dr >= sr * sc, "TOPK_BY_STRENGTH: dst needs L rows");
+            NEED(sr * sc <= VM_TOPK_MAX_L, "TOPK_BY_STRENGTH: L exceeds the selection bitmap (2048)");
+            nrow = 1, L = sr * sc, kseg = L, kmax = L;
+        }
+        // k is checked on the host as well, so that its message is the reference's
+        float kf;
+        if ((rc = scalar(b, &kf))) return rc;
+        NEED(kf >= 0.0f, "TOPK_BY_STRENGTH: k is negative or NaN");
+        const size_t kk = kf >= 1.8446744e19f ? ~(size_t)0 : (size_t)kf;
+        NEED(kk <= (seg ? sc : L), seg ? "TOPK_BY_STRENGTH: k > row width"
+                                       : "TOPK_BY_STRENGTH: k > L");
+        NEED(!seg || kk <= kseg, "TOPK_BY_STRENGTH: k > dst segment width");
+        P_(cs, a);
+        P_(ck, b);
+        P_(cd, d);
+        void *taken;
+        if ((rc = ws(nrow * L, &taken))) return rc;
+        vm_topk_strength_kernel<<<vm_blocks(nrow, 64), 64, 0, st>>>(
+            cd, seg ? dc : 0, cs, nrow, L, ck, kmax, kseg, (unsigned char *)taken, guard);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    case VOP_SPARSE_MATVEC: {  // :2058-2346
+        const uint32_t wslot = in.fl & 0x3Fu, xslot = in.dt;
+        const bool want_nnz = (in.fl & VFL_NNZ) != 0, selgate = (in.fl & VFL_SELGATE) != 0;
+        const size_t orows = rows(a), ocols = cols(a), srows = rows(b), scols = cols(b);
+        const size_t dr = rows(d), dc = cols(d);
+        NEED(orows && ocols && srows && scols, "SPARSE_MATVEC: offsets or src slot has width 0");
+        NEED(dr && dc, "SPARSE_MATVEC: dst slot has width 0");
+        const uint32_t selslot = selgate ? b + 1 : b;
+        NEED(!selgate || selslot < vm->slots.size(), "SPARSE_MATVEC: sel slot (src+1) does not exist");
+        const size_t secols = cols(selslot), serows = rows(selslot);
+        NEED(!selgate || (secols != 0 && secols % 2 == 0),
+             "SPARSE_MATVEC: selgate needs an even sel width");
+        NEED(ocols == 1 && scols == 1, "SPARSE_MATVEC: offsets and src must be column vectors");
+        NEED(orows >= 2, "SPARSE_MATVEC: offsets must have n_neurons+1 entries");
+        const size_t n = orows - 1, nnz = srows;
+        NEED(dc == 1 && dr >= n, "SPARSE_MATVEC: dst must be [n_neurons(,1)]");
+        NEED(!want_nnz || dr >= n + 1, "SPARSE_MATVEC: nnz needs dst to be [n_neurons+1]");
+        const size_t nx = nel(xslot);
+        NEED(nx != 0, "SPARSE_MATVEC: x slot (dt) has width 0");
+        NEED(nel(wslot) != 0, "SPARSE_MATVEC: weight slot (fl) has width 0");
+        NEED(nel(wslot) >= nnz, "SPARSE_MATVEC: weight slot shorter than src");
+        const size_t segw = secols / 2;
+        NEED(!selgate || (segw && n * segw * 2 <= serows * secols),
+             "SPARSE_MATVEC: sel table too small for n_neurons");
+        P_(co, a);
+        P_(cs, b);
+        P_(cw, wslot);
+        P_(cx, xslot);
+        P_(cd, d);
+        float *csel = nullptr;
+        if (selgate && (rc = ptr(selslot, &csel))) return rc;
+        void *cnt;
+        if ((rc = ws(n * sizeof(unsigned), &cnt))) return rc;
+        vm_sparse_matvec_kernel<<<vm_blocks(n, 64), 64, 0, st>>>(
+            cd, co, cs, cw, cx, n, nnz, nx, csel, segw, (unsigned *)cnt, guard);
+        VMLM_HIP_CHECK(hipGetLastError());
+        if (want_nnz) {
+            vm_nnz_kernel<<<1, 64, 0, st>>>(cd + n, (const unsigned *)cnt, n);
+            VMLM_HIP_CHECK(hipGetLastError());
+        }
+        return VMLM_OK;
+    }
+    case 60: case 61: case 62: case 63: case 64: case 65: case 66: case 67: case 68:
+    case 69: case 70: case 80: case 81: case 82: case 83: case 84:
+        return fail(6, "train feature disabled");
+    default:
+        return fail(VMLM_ERR_UNIMPL, "unimpl op %u", in.op);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int vmlm_vm_run(vmlm_vm *vm) {
+    VMLM_GUARD(vm, "vm_run: null vm");
+    int rc = ensure_init();
+    if (rc) return rc;
+    // a device guard raised before this run is not this run's
+    if ((rc = vmlm_hip_check_guards())) (void)rc;
+    Exec ex{vm, guard_flag_ptr()};
+    size_t ip = 0;
+    const size_t n = vm->text.size();
+    while (ip < n) {
+        const VmIns in = vm->text[ip++];
+        if (in.op == VOP_HALT) break;
+        if ((rc = ex.step(in, &ip))) {
+            (void)hipStreamSynchronize(vm->st);
+            return rc;
+        }
+    }
+    VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
+    return vmlm_hip_check_guards();
+}
+
+int vmlm_vm_find_slot(const vmlm_vm *vm, const char *name, uint32_t *slot) {
+    VMLM_GUARD(vm && name && slot, "vm_find_slot: null argument");
+    uint32_t h = 0x811C9DC5u;  // FNV-1a (core/src/format.rs hash32)
+    for (const char *c = name; *c; ++c) h = (h ^ (uint8_t)*c) * 0x01000193u;
+    for (size_t i = 0; i < vm->names.size(); ++i)
+        if (vm->names[i] == h) {
+            *slot = (uint32_t)i;
+            return VMLM_OK;
+        }
+    return fail(7, "slot not found: %s", name);
+}
+
+int vmlm_vm_slot_info(vmlm_vm *vm, uint32_t slot, void **dptr, uint32_t *rows, uint32_t *cols,
+                      uint8_t *dtype) {
+    VMLM_GUARD(vm, "vm_slot_info: null vm");
+    Exec ex{vm, guard_flag_ptr()};
+    float *p;
+    int rc = ex.ptr(slot, &p);
+    if (rc) return rc;
+    if (dptr) *dptr = p;
+    if (rows) *rows = vm->slots[slot].rows;
+    if (cols) *cols = vm->slots[slot].cols;
+    if (dtype) *dtype = vm->slots[slot].dtype;
+    return VMLM_OK;
+}
+
+static int vm_xfer(vmlm_vm *vm, uint32_t slot, void *host, size_t count, bool write) {
+    VMLM_GUARD(vm && (host || count == 0), "vm slot transfer: null argument");
+    Exec ex{vm, guard_flag_ptr()};
+    float *p;
+    int rc = ex.ptr(slot, &p);
+    if (rc) return rc;
+    VMLM_GUARD(vm->slots[slot].dtype == VDT_F32, "slot %u is not f32", slot);
+    VMLM_GUARD(vm->slots[slot].kind != VSLOT_CONST || !write, "constant slot %u is read-only", slot);
+    VMLM_GUARD(count <= ex.nel(slot), "slot %u holds %zu values, %zu requested", slot, ex.nel(slot),
+               count);
+    if (count)
+        VMLM_HIP_CHECK(hipMemcpyAsync(write ? (void *)p : host, write ? host : (void *)p, count * 4,
+                                      write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost, vm->st));
+    VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
+    return VMLM_OK;
+}
+int vmlm_vm_write_slot(vmlm_vm *vm, uint32_t slot, const float *host, size_t count) {
+    return vm_xfer(vm, slot, (void *)host, count, true);
+}
+int vmlm_vm_read_slot(vmlm_vm *vm, uint32_t slot, float *host, size_t count) {
+    return vm_xfer(vm, slot, host, count, false);
+}
+
+int vmlm_vm_output(vmlm_vm *vm, float *host, size_t cap, size_t *count) {
+    VMLM_GUARD(vm && count, "vm_output: null argument");
+    *count = vm->out.size();
+    if (host && cap) std::memcpy(host, vm->out.data(), (cap < *count ? cap : *count) * 4);
+    return VMLM_OK;
+}
+int vmlm_vm_clear_output(vmlm_vm *vm) {
+    VMLM_GUARD(vm, "vm_clear_output: null vm");
+    vm->out.clear();
+    return VMLM_OK;
+}
+
+}  // extern "C"
