@@ -138,6 +138,22 @@ int vmlm_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y, size
 /* ops/src/b1_pure.rs:271 b1_forward_t8(sc,xt,t8,n_tokens,yt) -> macs. */
 int vmlm_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
                        size_t n_tokens, float *yt, size_t *macs);
+/* ops/src/b1_pure.rs:642 b1_backward(sc,dy,x,dw) -> macs: dw[i,j] +=
+ * dy[i] * x[src[i,j]] over the f32 ids `sc->src`. */
+int vmlm_b1_backward(const vmlm_sparse_conn_w *sc, const float *dy, const float *x, float *dw,
+                     size_t *macs);
+/* ops/src/b1_pure.rs:410 b1_backward_dx(sc,dy,dx) -> accs: dx[src[i,j]] +=
+ * dy[i] * w[i,j], i and j ascending (bitwise). */
+int vmlm_b1_backward_dx(const vmlm_sparse_conn_w *sc, const float *dy, float *dx, size_t *accs);
+/* ops/src/b1_pure.rs:466 b1_backward_fused(sc,dy,x,dw,dx) -> n*k0: both of
+ * the above over `src_u32` (ops/src/kernels.rs:2401 fused kernel). */
+int vmlm_b1_backward_fused(const vmlm_sparse_conn_w *sc, const float *dy, const float *x,
+                           float *dw, float *dx, size_t *conns);
+/* ops/src/kernels.rs:3229 b1_backward_t8_avx2(w,src_u32,xt,dyt,t8,n,k0,dxt,dw):
+ * source-major activations [n][t8] (t8 % 8 == 0); dxt and dw accumulate. */
+int vmlm_b1_backward_t8(const float *w, const uint32_t *src_u32, const float *xt,
+                        const float *dyt, size_t t8, size_t n, size_t k0, float *dxt,
+                        float *dw);
 /* ops/src/kernels.rs:1881 transpose_t8_avx2(x,t,d,xt,t8). */
 int vmlm_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8);
 /* ops/src/kernels.rs:3307 transpose_t8_back_avx2(a,rows,cols,out,os,in_stride). */
@@ -231,6 +247,11 @@ int vmlm_hip_b1_forward(const vmlm_sparse_conn_w *sc, const float *x, float *y,
                         size_t n_tokens, void *stream);
 int vmlm_hip_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
                            size_t n_tokens, float *yt, void *stream);
+int vmlm_hip_b1_backward_fused(const vmlm_sparse_conn_w *sc, const float *dy, const float *x,
+                               float *dw, float *dx, void *stream);
+int vmlm_hip_b1_backward_t8(const float *w, const uint32_t *src_u32, const float *xt,
+                            const float *dyt, size_t t8, size_t n, size_t k0, float *dxt,
+                            float *dw, void *stream);
 int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8,
                           void *stream);
 int vmlm_hip_transpose_t8_back(const float *a, size_t rows, size_t cols, float *out,

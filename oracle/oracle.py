@@ -95,6 +95,10 @@ def lib() -> C.CDLL:
         "vo_layernorm": (None, [_f32p, _f32p, _f32p, _sz, _sz, C.c_float]),
         "vo_bias": (None, [_f32p, _f32p, _sz, _sz]),
         "vo_outer": (None, [_f32p, _f32p, _f32p, _sz, _sz, C.c_float]),
+        "vo_b1_backward": (_sz, [_sz, _sz, _f32p, _f32p, _f32p, _f32p]),
+        "vo_b1_backward_dx": (_sz, [_sz, _sz, _f32p, _u32p, _f32p, _f32p]),
+        "vo_b1_backward_fused": (_sz, [_sz, _sz, _f32p, _u32p, _f32p, _f32p, _f32p, _f32p]),
+        "vo_b1_backward_t8": (None, [_f32p, _u32p, _f32p, _f32p, _sz, _sz, _sz, _f32p, _f32p]),
         "vo_attention_prefill": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz,
                                         C.c_float, C.c_uint32, C.c_float, C.c_int]),
         "vo_attention_decode": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz,
@@ -262,6 +266,41 @@ def softmax(p, causal=False):
     rows, cols = p.shape
     lib().vo_softmax(p, rows, cols, int(causal))
     return p
+
+
+# ---------------------------------------------------------------- B1 backward
+def b1_backward(w, src, dy, x, dw=None):
+    """ops/src/b1_pure.rs:642 (reads the f32 ids): dw += dy[i] * x[src]."""
+    n, k0 = w.shape
+    srcf = _c(src, np.float32)
+    dw = np.zeros((n, k0), np.float32) if dw is None else _c(dw, np.float32).copy()
+    lib().vo_b1_backward(n, k0, srcf, _c(dy, np.float32), _c(x, np.float32), dw)
+    return dw
+
+
+def b1_backward_dx(w, src, dy, dx):
+    n, k0 = w.shape
+    dx = _c(dx, np.float32).copy()
+    lib().vo_b1_backward_dx(n, k0, _c(w, np.float32), _c(src, np.uint32), _c(dy, np.float32), dx)
+    return dx
+
+
+def b1_backward_fused(w, src, dy, x, dw, dx):
+    n, k0 = w.shape
+    dw, dx = _c(dw, np.float32).copy(), _c(dx, np.float32).copy()
+    lib().vo_b1_backward_fused(n, k0, _c(w, np.float32), _c(src, np.uint32), _c(dy, np.float32),
+                               _c(x, np.float32), dw, dx)
+    return dw, dx
+
+
+def b1_backward_t8(w, src, xt, dyt, dxt, dw):
+    """ops/src/kernels.rs:3229: xt [d][t8], dyt [n][t8], dxt [d][t8], dw [n][k0]."""
+    n, k0 = w.shape
+    t8 = xt.shape[1]
+    dxt, dw = _c(dxt, np.float32).copy(), _c(dw, np.float32).copy()
+    lib().vo_b1_backward_t8(_c(w, np.float32), _c(src, np.uint32), _c(xt, np.float32),
+                            _c(dyt, np.float32), t8, n, k0, dxt, dw)
+    return dxt, dw
 
 
 # ------------------------------------------------ Backend table, jit helpers

@@ -1008,3 +1008,73 @@ void vo_outer(float *s, const float *v, const float *k, size_t m, size_t n, floa
         for (size_t j = n8; j < n; ++j) s[i * n + j] += v[i] * sc * k[j];
     }
 }
+
+/* ====================================================================== */
+/* B1 backward                                                             */
+/* ====================================================================== */
+
+/* ops/src/b1_pure.rs:642-656 b1_backward: dw[i*k0+j] += dy[i] * x[src[i*k0+j]]
+ * with the f32 source ids (`sc.src`, cast as usize). */
+size_t vo_b1_backward(size_t n, size_t k0, const float *srcf, const float *dy, const float *x,
+                      float *dw) {
+    for (size_t i = 0; i < n; ++i) {
+        float g = dy[i];
+        for (size_t j = 0; j < k0; ++j) {
+            float f = srcf[i * k0 + j];
+            size_t s = f > 0.0f ? (size_t)f : 0;
+            dw[i * k0 + j] += g * x[s];
+        }
+    }
+    return n * k0;
+}
+
+/* ops/src/b1_pure.rs:410-428 b1_backward_dx: dx[src[i*k0+j]] += dy[i] * w[i*k0+j],
+ * i ascending, j ascending. */
+size_t vo_b1_backward_dx(size_t n, size_t k0, const float *w, const uint32_t *src,
+                         const float *dy, float *dx) {
+    for (size_t i = 0; i < n; ++i) {
+        float g = dy[i];
+        for (size_t j = 0; j < k0; ++j) dx[src[i * k0 + j]] += g * w[i * k0 + j];
+    }
+    return n * k0;
+}
+
+/* ops/src/kernels.rs:2458-2478 b1_backward_fused_dwdx_scalar, the contract of
+ * the AVX2 fused kernel (:2401-2456): per connection dw first, then dx, i and
+ * j ascending, mul then add. */
+size_t vo_b1_backward_fused(size_t n, size_t k0, const float *w, const uint32_t *src,
+                            const float *dy, const float *x, float *dw, float *dx) {
+    for (size_t i = 0; i < n; ++i) {
+        float g = dy[i];
+        for (size_t j = 0; j < k0; ++j) {
+            size_t s = src[i * k0 + j];
+            dw[i * k0 + j] += g * x[s];
+            dx[s] += g * w[i * k0 + j];
+        }
+    }
+    return n * k0;
+}
+
+/* ops/src/kernels.rs:3229-3275 b1_backward_t8_avx2 over source-major
+ * activations (t8 a multiple of 8): per connection (i, j), s = src: the
+ * token dot product in eight FMA lanes (lane l takes p = l, l+8, ...),
+ * reduced by hsum256 and added to dw; dxt[s][p] = fma(dyt[i][p], w, dxt[s][p]). */
+void vo_b1_backward_t8(const float *w, const uint32_t *src, const float *xt, const float *dyt,
+                       size_t t8, size_t n, size_t k0, float *dxt, float *dw) {
+    for (size_t i = 0; i < n; ++i) {
+        const float *dy = dyt + i * t8;
+        for (size_t j = 0; j < k0; ++j) {
+            size_t s = src[i * k0 + j];
+            float wij = w[i * k0 + j];
+            const float *xr = xt + s * t8;
+            float *dr = dxt + s * t8;
+            float acc[8] = {0};
+            for (size_t p = 0; p + 8 <= t8; p += 8)
+                for (int l = 0; l < 8; ++l) {
+                    acc[l] = fmaf(dy[p + l], xr[p + l], acc[l]);
+                    dr[p + l] = fmaf(dy[p + l], wij, dr[p + l]);
+                }
+            dw[i * k0 + j] += hsum256(acc);
+        }
+    }
+}

@@ -141,6 +141,16 @@ int vo_decoder_generate(const vo_model *md, float *kcache, float *vcache, size_t
                         const int32_t *prompt, size_t S, size_t n_steps,
                         int32_t *out_tokens, float *margins);
 
+/* ---- B1 backward (ops/src/b1_pure.rs, ops/src/kernels.rs) ---- */
+size_t vo_b1_backward(size_t n, size_t k0, const float *srcf, const float *dy, const float *x,
+                      float *dw);
+size_t vo_b1_backward_dx(size_t n, size_t k0, const float *w, const uint32_t *src,
+                         const float *dy, float *dx);
+size_t vo_b1_backward_fused(size_t n, size_t k0, const float *w, const uint32_t *src,
+                            const float *dy, const float *x, float *dw, float *dx);
+void vo_b1_backward_t8(const float *w, const uint32_t *src, const float *xt, const float *dyt,
+                       size_t t8, size_t n, size_t k0, float *dxt, float *dw);
+
 /* ---- the VM (vmlm_vm_oracle.c): core/src/interp.rs load + run ---- */
 typedef struct vo_vm vo_vm;
 int vo_vm_load(const uint8_t *image, size_t len, vo_vm **out); /* exit code */

@@ -306,6 +306,12 @@ static int slot_index(vo_vm *vm, uint32_t s, size_t limit, size_t *val, const ch
     return 0;
 }
 
+/* Rust's `f as usize`: saturating, NaN and negatives give 0 (the cast the
+ * reference applies to f32-held offsets, ids and counts). */
+static size_t as_usize(float f) {
+    return f > 0.0f ? (f >= 1.8446744e19f ? (size_t)-1 : (size_t)f) : 0;
+}
+
 static void print_out(vo_vm *vm, const float *p, size_t n) {
     if (vm->n_out + n > vm->cap_out) {
         size_t cap = vm->cap_out ? vm->cap_out : 1024;
@@ -825,7 +831,7 @@ static int exec(vo_vm *vm, ins_t in, size_t *ip) {
         P(cd, d);
         float kf = ck[0];
         NEED(kf >= 0.0f, "TOPK_BY_STRENGTH: k is negative or NaN");
-        k = (size_t)kf;
+        k = as_usize(kf);
         size_t hit[TOPK_MAX_L];
         char taken[TOPK_MAX_L];
         if (seg) {
@@ -882,7 +888,7 @@ static int exec(vo_vm *vm, ins_t in, size_t *ip) {
         P(cd, d);
         size_t done = 0;
         for (size_t j = 0; j < n; ++j) {
-            size_t o0 = (size_t)co[j], o1 = (size_t)co[j + 1];
+            size_t o0 = as_usize(co[j]), o1 = as_usize(co[j + 1]);
             NEED(o1 <= nnz && o0 <= o1, "SPARSE_MATVEC: offsets out of range j=%zu o0=%zu o1=%zu nnz=%zu",
                  j, o0, o1, nnz);
             if (o0 == o1) {
@@ -897,11 +903,11 @@ static int exec(vo_vm *vm, ins_t in, size_t *ip) {
                      "SPARSE_MATVEC: sel table too small for n_neurons");
                 int first = 1;
                 for (size_t q = 0; q < segw; ++q) {
-                    size_t rel = (size_t)csel[(j * segw + q) * 2];
+                    size_t rel = as_usize(csel[(j * segw + q) * 2]);
                     if (q > 0 && rel == 0) break;
                     size_t idx = o0 + rel;
                     NEED(idx >= o0 && idx < o1, "SPARSE_MATVEC: sel index outside its CSR row");
-                    size_t sid = (size_t)cs[idx];
+                    size_t sid = as_usize(cs[idx]);
                     NEED(sid < nx, "SPARSE_MATVEC: src_id out of range");
                     float term = cw[idx] * cx[sid];
                     acc = first ? term : acc + term;
@@ -912,7 +918,7 @@ static int exec(vo_vm *vm, ins_t in, size_t *ip) {
                 continue;
             }
             for (size_t t = o0; t < o1; ++t) {
-                size_t sid = (size_t)cs[t];
+                size_t sid = as_usize(cs[t]);
                 NEED(sid < nx, "SPARSE_MATVEC: src_id out of range");
                 float term = cw[t] * cx[sid];
                 acc = t == o0 ? term : acc + term;

@@ -72,6 +72,10 @@ SIGNATURES = {
     "vmlm_topk_idx": (I, [P, SZ, SZ, P]),
     "vmlm_b1_forward": (I, [C.POINTER(SparseConnW), P, P, C.POINTER(SZ)]),
     "vmlm_b1_forward_t8": (I, [C.POINTER(SparseConnW), P, SZ, SZ, P, C.POINTER(SZ)]),
+    "vmlm_b1_backward": (I, [C.POINTER(SparseConnW), P, P, P, C.POINTER(SZ)]),
+    "vmlm_b1_backward_dx": (I, [C.POINTER(SparseConnW), P, P, C.POINTER(SZ)]),
+    "vmlm_b1_backward_fused": (I, [C.POINTER(SparseConnW), P, P, P, P, C.POINTER(SZ)]),
+    "vmlm_b1_backward_t8": (I, [P, P, P, P, SZ, SZ, SZ, P, P]),
     "vmlm_transpose_t8": (I, [P, SZ, SZ, P, SZ]),
     "vmlm_transpose_t8_back": (I, [P, SZ, SZ, P, SZ, SZ]),
     "vmlm_layernorm": (I, [P, P, P, SZ, SZ, F]),
@@ -107,6 +111,8 @@ SIGNATURES = {
     "vmlm_hip_check_guards": (I, []),
     "vmlm_hip_b1_forward": (I, [C.POINTER(SparseConnW), P, P, SZ, P]),
     "vmlm_hip_b1_forward_t8": (I, [C.POINTER(SparseConnW), P, SZ, SZ, P, P]),
+    "vmlm_hip_b1_backward_fused": (I, [C.POINTER(SparseConnW), P, P, P, P, P]),
+    "vmlm_hip_b1_backward_t8": (I, [P, P, P, P, SZ, SZ, SZ, P, P, P]),
     "vmlm_hip_transpose_t8": (I, [P, SZ, SZ, P, SZ, P]),
     "vmlm_hip_transpose_t8_back": (I, [P, SZ, SZ, P, SZ, SZ, P]),
     "vmlm_hip_layernorm": (I, [P, P, P, SZ, SZ, F, P]),

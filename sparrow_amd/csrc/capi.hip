@@ -716,6 +716,28 @@ int vmlm_hip_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t
     return b1_t8_layer(sc->w, sc->src_u32, (int)sc->n_neurons, (int)sc->k0, xt, t8, n_tokens, yt,
                        stg, st);
 }
+int vmlm_hip_b1_backward_fused(const vmlm_sparse_conn_w *sc, const float *dy, const float *x,
+                               float *dw, float *dx, void *stream) {
+    INIT_OR_RETURN();
+    int rc = check_conn(sc);
+    if (rc) return rc;
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    char *work = dx ? stg.alloc<char>(b1_rev_work_bytes(sc->e, sc->n_neurons)) : nullptr;
+    STAGE_OK(stg);
+    return launch_b1_backward(sc->w, nullptr, sc->src_u32, sc->n_neurons, sc->k0, dy, x, dw, dx,
+                              work, st);
+}
+int vmlm_hip_b1_backward_t8(const float *w, const uint32_t *src_u32, const float *xt,
+                            const float *dyt, size_t t8, size_t n, size_t k0, float *dxt,
+                            float *dw, void *stream) {
+    INIT_OR_RETURN();
+    hipStream_t st = as_stream(stream);
+    Stage stg(st);
+    char *work = stg.alloc<char>(b1_rev_work_bytes(n * k0, n));
+    STAGE_OK(stg);
+    return launch_b1_backward_t8(w, src_u32, xt, dyt, t8, n, k0, dxt, dw, work, st);
+}
 int vmlm_hip_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8,
                           void *stream) {
     INIT_OR_RETURN();
@@ -1026,6 +1048,91 @@ int vmlm_b1_forward_t8(const vmlm_sparse_conn_w *sc, const float *xt, size_t t8,
                        size_t n_tokens, float *yt, size_t *macs) {
     VMLM_GUARD(t8 >= n_tokens, "B1_T8: row stride t8 < n_tokens");
     return host_b1(sc, xt, t8, n_tokens, yt, macs, 0);
+}
+
+// B1 backward on host buffers: `dw` and `dx` accumulate (+=) like the
+// reference's; sources are checked against n_neurons (the square layer's
+// source dimension) before anything runs.
+static int host_b1_bwd(const vmlm_sparse_conn_w *sc, const float *dy, const float *x, float *dw,
+                       float *dx, bool f32_ids) {
+    int rc = check_conn(sc);
+    if (rc) return rc;
+    const size_t n = sc->n_neurons, e = sc->e;
+    if (f32_ids) {
+        VMLM_GUARD(sc->src != nullptr, "B1 backward: SparseConnW.src (f32 ids) is null");
+        for (size_t t = 0; t < e; ++t) {
+            const float f = sc->src[t];
+            const size_t u = f > 0.0f ? (size_t)f : 0;
+            VMLM_GUARD(u < n, "B1: src[%zu]=%g >= n_neurons=%zu", t, (double)f, n);
+        }
+    } else {
+        for (size_t t = 0; t < e; ++t)
+            VMLM_GUARD(sc->src_u32[t] < n, "B1: src_u32[%zu]=%u >= n_neurons=%zu", t,
+                       sc->src_u32[t], n);
+    }
+    HOST_CALL_BEGIN();
+    {
+        Stage stg(st);
+        float *dwt = stg.upload(sc->w, e);
+        const float *dsf = f32_ids ? stg.upload((const float *)sc->src, e) : nullptr;
+        const uint32_t *ds = f32_ids ? nullptr : stg.upload(sc->src_u32, e);
+        float *ddy = stg.upload(dy, n);
+        float *dxs = x ? stg.upload(x, n) : nullptr;
+        float *ddw = dw ? stg.upload((const float *)dw, e) : nullptr;
+        float *ddx = dx ? stg.upload((const float *)dx, n) : nullptr;
+        char *work = dx ? stg.alloc<char>(b1_rev_work_bytes(e, n)) : nullptr;
+        STAGE_OK(stg);
+        rc = launch_b1_backward(dwt, dsf, ds, n, sc->k0, ddy, dxs, ddw, ddx, work, st);
+        if (!rc && dw) rc = download(dw, ddw, e * sizeof(float), st);
+        if (!rc && dx) rc = download(dx, ddx, n * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
+}
+
+int vmlm_b1_backward(const vmlm_sparse_conn_w *sc, const float *dy, const float *x, float *dw,
+                     size_t *macs) {
+    int rc = host_b1_bwd(sc, dy, x, dw, nullptr, true);
+    if (!rc && macs) *macs = sc->e;
+    return rc;
+}
+int vmlm_b1_backward_dx(const vmlm_sparse_conn_w *sc, const float *dy, float *dx, size_t *accs) {
+    int rc = host_b1_bwd(sc, dy, nullptr, nullptr, dx, false);
+    if (!rc && accs) *accs = sc->e;
+    return rc;
+}
+int vmlm_b1_backward_fused(const vmlm_sparse_conn_w *sc, const float *dy, const float *x,
+                           float *dw, float *dx, size_t *conns) {
+    int rc = host_b1_bwd(sc, dy, x, dw, dx, false);
+    if (!rc && conns) *conns = sc->e;
+    return rc;
+}
+
+int vmlm_b1_backward_t8(const float *w, const uint32_t *src_u32, const float *xt,
+                        const float *dyt, size_t t8, size_t n, size_t k0, float *dxt,
+                        float *dw) {
+    VMLM_GUARD(t8 % 8 == 0, "B1_T8 backward: t8 = %zu is not a multiple of 8", t8);
+    for (size_t t = 0; t < n * k0; ++t)
+        VMLM_GUARD(src_u32[t] < n, "B1: src_u32[%zu]=%u >= n=%zu", t, src_u32[t], n);
+    HOST_CALL_BEGIN();
+    if (n == 0 || k0 == 0 || t8 == 0) return VMLM_OK;
+    {
+        Stage stg(st);
+        const size_t e = n * k0;
+        float *dwt = stg.upload(w, e);
+        uint32_t *ds = stg.upload(src_u32, e);
+        float *dxt_in = stg.upload(xt, n * t8);
+        float *ddy = stg.upload(dyt, n * t8);
+        float *ddx = stg.upload((const float *)dxt, n * t8);
+        float *ddw = stg.upload((const float *)dw, e);
+        char *work = stg.alloc<char>(b1_rev_work_bytes(e, n));
+        STAGE_OK(stg);
+        int rc = launch_b1_backward_t8(dwt, ds, dxt_in, ddy, t8, n, k0, ddx, ddw, work, st);
+        if (!rc) rc = download(dxt, ddx, n * t8 * sizeof(float), st);
+        if (!rc) rc = download(dw, ddw, e * sizeof(float), st);
+        if (rc) return rc;
+    }
+    FINISH(st);
 }
 
 int vmlm_transpose_t8(const float *x, size_t t, size_t d, float *xt, size_t t8) {

@@ -171,6 +171,16 @@ int launch_layernorm(float *x, const float *g, const float *b, size_t rows, size
 int launch_bias(float *d, const float *b, size_t rows, size_t cols, hipStream_t st);
 int launch_outer(float *s, const float *v, const float *k, size_t m, size_t n, float sc,
                  hipStream_t st);
+// B1 backward (k_b1_bwd.hip). dw / dx / dxt accumulate; `work` holds
+// b1_rev_work_bytes(n * k0, n) bytes (the reverse index of the sources).
+// srcf (f32 ids) feeds dw when given, else src (u32 ids).
+size_t b1_rev_work_bytes(size_t E, size_t d);
+int launch_b1_backward(const float *w, const float *srcf, const uint32_t *src, size_t n,
+                       size_t k0, const float *dy, const float *x, float *dw, float *dx,
+                       void *work, hipStream_t st);
+int launch_b1_backward_t8(const float *w, const uint32_t *src, const float *xt, const float *dyt,
+                          size_t t8, size_t n, size_t k0, float *dxt, float *dw, void *work,
+                          hipStream_t st);
 // Zero-fills `bytes` bytes with a kernel (capturable, unlike hipMemsetAsync).
 int launch_fill_zero(void *p, size_t bytes, hipStream_t st);
 int gemm_i8_kslices(int M, int N, int K);

@@ -136,12 +136,15 @@ def topk_idx(x):
 
 
 def _conn(w, src):
+    """SparseConnW over host arrays: the u32 ids and their f32 copy (the
+    struct's `src`, which b1_backward reads)."""
     w = _c(w, np.float32)
     src = _c(src, np.uint32)
+    srcf = src.astype(np.float32)
     n, k0 = w.shape
-    sc = _abi.SparseConnW(e=n * k0, k0=k0, layer=0, n_neurons=n, w=_p(w), src=None,
+    sc = _abi.SparseConnW(e=n * k0, k0=k0, layer=0, n_neurons=n, w=_p(w), src=_p(srcf),
                           src_u32=_p(src), act=None)
-    return sc, (w, src)
+    return sc, (w, src, srcf)
 
 
 def b1_forward(w, src, x):
@@ -164,6 +167,48 @@ def b1_forward_t8(w, src, xt, n_tokens, yt=None):
     check(lib().vmlm_b1_forward_t8(C.byref(sc), _p(xt), t8, int(n_tokens), _p(yt),
                                    C.byref(macs)))
     return yt, macs.value
+
+
+def b1_backward(w, src, dy, x, dw=None):
+    """ops/src/b1_pure.rs:642 -- dw += dy[i] * x[src] (over the f32 ids)."""
+    sc, keep = _conn(w, src)
+    dw = np.zeros(w.shape, np.float32) if dw is None else _c(dw, np.float32).copy()
+    n = C.c_size_t(0)
+    check(lib().vmlm_b1_backward(C.byref(sc), _p(_c(dy, np.float32)), _p(_c(x, np.float32)),
+                                 _p(dw), C.byref(n)))
+    return dw, n.value
+
+
+def b1_backward_dx(w, src, dy, dx=None):
+    """ops/src/b1_pure.rs:410 -- dx[src] += dy[i] * w, i and j ascending."""
+    sc, keep = _conn(w, src)
+    dx = np.zeros(sc.n_neurons, np.float32) if dx is None else _c(dx, np.float32).copy()
+    n = C.c_size_t(0)
+    check(lib().vmlm_b1_backward_dx(C.byref(sc), _p(_c(dy, np.float32)), _p(dx), C.byref(n)))
+    return dx, n.value
+
+
+def b1_backward_fused(w, src, dy, x, dw=None, dx=None):
+    """ops/src/b1_pure.rs:466 -- dw and dx in one call."""
+    sc, keep = _conn(w, src)
+    dw = np.zeros(w.shape, np.float32) if dw is None else _c(dw, np.float32).copy()
+    dx = np.zeros(sc.n_neurons, np.float32) if dx is None else _c(dx, np.float32).copy()
+    n = C.c_size_t(0)
+    check(lib().vmlm_b1_backward_fused(C.byref(sc), _p(_c(dy, np.float32)),
+                                       _p(_c(x, np.float32)), _p(dw), _p(dx), C.byref(n)))
+    return dw, dx, n.value
+
+
+def b1_backward_t8(w, src, xt, dyt, dxt=None, dw=None):
+    """ops/src/kernels.rs:3229 -- source-major [n][t8] activations."""
+    w, src = _c(w, np.float32), _c(src, np.uint32)
+    n, k0 = w.shape
+    xt, dyt = _c(xt, np.float32), _c(dyt, np.float32)
+    t8 = xt.shape[1]
+    dxt = np.zeros((n, t8), np.float32) if dxt is None else _c(dxt, np.float32).copy()
+    dw = np.zeros((n, k0), np.float32) if dw is None else _c(dw, np.float32).copy()
+    check(lib().vmlm_b1_backward_t8(_p(w), _p(src), _p(xt), _p(dyt), t8, n, k0, _p(dxt), _p(dw)))
+    return dxt, dw
 
 
 def transpose_t8(x, t8):

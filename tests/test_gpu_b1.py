@@ -80,3 +80,64 @@ def test_b1_stack_shapes(hip, oracle, d, k0s, T, act):
             xt = oracle.vmap("tanh", xt)
     ref = oracle.transpose_t8_back(xt, T)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------ B1 backward
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("n,k0", [(200, 1), (200, 2), (96, 8), (200, 20), (64, 37), (1536, 32)])
+def test_b1_backward_bitwise(hip, oracle, n, k0):
+    """b1_backward (f32 ids), b1_backward_dx and the fused pass against the
+    reference's scalar contract, bit for bit, accumulating into non-zero
+    buffers; sources repeat (each source is read by ~k0 connections)."""
+    from sparrow_amd import ops
+    rng = np.random.default_rng(n + k0)
+    w = rng.standard_normal((n, k0)).astype(np.float32)
+    src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
+    x = rng.standard_normal(n).astype(np.float32)
+    dy = rng.standard_normal(n).astype(np.float32)
+    dw0 = rng.standard_normal((n, k0)).astype(np.float32)
+    dx0 = rng.standard_normal(n).astype(np.float32)
+    dw, macs = ops.b1_backward(w, src, dy, x, dw0)
+    assert macs == n * k0
+    assert np.array_equal(bits(dw), bits(oracle.b1_backward(w, src.astype(np.float32), dy, x, dw0)))
+    dx, accs = ops.b1_backward_dx(w, src, dy, dx0)
+    assert accs == n * k0
+    assert np.array_equal(bits(dx), bits(oracle.b1_backward_dx(w, src, dy, dx0)))
+    fw, fx, _ = ops.b1_backward_fused(w, src, dy, x, dw0, dx0)
+    ow, ox = oracle.b1_backward_fused(w, src, dy, x, dw0, dx0)
+    assert np.array_equal(bits(fw), bits(ow)) and np.array_equal(bits(fx), bits(ox))
+
+
+@pytest.mark.parametrize("n,k0,t8", [(96, 9, 32), (200, 20, 40), (1536, 32, 1024)])
+def test_b1_backward_t8_bitwise(hip, oracle, n, k0, t8):
+    """ops/src/kernels.rs:3229 over source-major activations: dw (eight FMA
+    lanes folded in hsum256 order) and dxt (FMA per token, connections in
+    order) bit for bit; the config-4 shape included."""
+    from sparrow_amd import ops
+    rng = np.random.default_rng(n * k0)
+    w = (rng.standard_normal((n, k0)) / np.sqrt(k0)).astype(np.float32)
+    src = rng.integers(0, n, size=(n, k0)).astype(np.uint32)
+    xt = rng.standard_normal((n, t8)).astype(np.float32)
+    dyt = rng.standard_normal((n, t8)).astype(np.float32)
+    dxt0 = rng.standard_normal((n, t8)).astype(np.float32)
+    dw0 = rng.standard_normal((n, k0)).astype(np.float32)
+    gx, gw = ops.b1_backward_t8(w, src, xt, dyt, dxt0, dw0)
+    ox, ow = oracle.b1_backward_t8(w, src, xt, dyt, dxt0, dw0)
+    assert np.array_equal(bits(gw), bits(ow))
+    assert np.array_equal(bits(gx), bits(ox))
+
+
+def test_b1_backward_guards(hip):
+    from sparrow_amd import VmlmError, ops
+    w = np.ones((4, 2), np.float32)
+    src = np.array([[0, 1], [2, 3], [1, 4], [0, 0]], np.uint32)  # 4 >= n
+    with pytest.raises(VmlmError) as e:
+        ops.b1_backward_fused(w, src, np.ones(4, np.float32), np.ones(4, np.float32))
+    assert e.value.code == 9
+    with pytest.raises(VmlmError) as e:
+        ops.b1_backward_t8(w, np.zeros((4, 2), np.uint32), np.ones((4, 12), np.float32),
+                           np.ones((4, 12), np.float32))
+    assert e.value.code == 9  # t8 not a multiple of 8

@@ -770,3 +770,82 @@ def test_layernorm_bias_outer_oracle(oracle):
     assert np.array_equal(out[:, :16], (vi[:, None].astype(np.float64) * k[:16] + s[:, :16])
                           .astype(np.float32))
     assert np.array_equal(out[:, 16:], s[:, 16:] + vi[:, None] * k[16:])
+
+
+# ------------------------------------------------------------ B1 backward
+def _b1_case(seed, n=40, k0=11, d=None):
+    rng = np.random.default_rng(seed)
+    d = d or n
+    w = rng.standard_normal((n, k0)).astype(np.float32)
+    src = rng.integers(0, d, size=(n, k0)).astype(np.uint32)
+    x = rng.standard_normal(d).astype(np.float32)
+    dy = rng.standard_normal(n).astype(np.float32)
+    return w, src, x, dy
+
+
+def test_b1_backward_gradient_check(oracle):
+    """b1_backward / b1_backward_dx (ops/src/b1_pure.rs:410, 642) are the
+    gradients of L = sum_i dy_i * y_i with y_i = sum_j w_ij x[src_ij]:
+    central differences of that forward (float64, a gather-sum, not the
+    scatter under test) match dx and dw; a transposed scatter would not."""
+    w, src, x, dy = _b1_case(50)
+    n, k0 = w.shape
+
+    def loss(xx, ww):
+        return float((dy.astype(np.float64) * (ww.astype(np.float64) * xx[src]).sum(1)).sum())
+
+    dx = oracle.b1_backward_dx(w, src, dy, np.zeros(n, np.float32))
+    dw = oracle.b1_backward(w, src.astype(np.float32), dy, x)
+    h = 1e-3
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    for s in range(n):
+        e = np.zeros(n)
+        e[s] = h
+        fd = (loss(x64 + e, w64) - loss(x64 - e, w64)) / (2 * h)
+        assert abs(fd - dx[s]) <= 1e-5 * (1 + abs(fd)), s
+    for (i, j) in [(0, 0), (3, 7), (n - 1, k0 - 1), (17, 2)]:
+        e = np.zeros((n, k0))
+        e[i, j] = h
+        fd = (loss(x64, w64 + e) - loss(x64, w64 - e)) / (2 * h)
+        assert abs(fd - dw[i, j]) <= 1e-5 * (1 + abs(fd))
+
+
+def test_b1_backward_fused_equals_separate(oracle):
+    """ops/src/b1_pure.rs:466-490: the fused dw + dx pass is bit for bit the
+    separate b1_backward (dw) and b1_backward_dx (dx), accumulating into
+    non-zero buffers."""
+    w, src, x, dy = _b1_case(51, n=64, k0=20)
+    rng = np.random.default_rng(1)
+    dw0 = rng.standard_normal(w.shape).astype(np.float32)
+    dx0 = rng.standard_normal(64).astype(np.float32)
+    dw, dx = oracle.b1_backward_fused(w, src, dy, x, dw0, dx0)
+    assert np.array_equal(dw.view(np.uint32),
+                          oracle.b1_backward(w, src.astype(np.float32), dy, x, dw0).view(np.uint32))
+    assert np.array_equal(dx.view(np.uint32),
+                          oracle.b1_backward_dx(w, src, dy, dx0).view(np.uint32))
+
+
+def test_b1_backward_t8(oracle):
+    """ops/src/kernels.rs:3229-3275 over source-major activations: dw is the
+    token dot product (float64 within 1e-5), dxt[:, t] is token t's dx
+    (float64 within 1e-5). Fold control: a connection whose eight lane sums
+    are (2^24, 1, -2^24, 1, 0, 0, 0, 0) gets 1 (hsum256), not 2 (hsum_ps)."""
+    w, src, _, _ = _b1_case(52, n=48, k0=9)
+    rng = np.random.default_rng(2)
+    t8 = 32
+    xt = rng.standard_normal((48, t8)).astype(np.float32)
+    dyt = rng.standard_normal((48, t8)).astype(np.float32)
+    dxt, dw = oracle.b1_backward_t8(w, src, xt, dyt, np.zeros((48, t8), np.float32),
+                                    np.zeros(w.shape, np.float32))
+    ref_dw = (dyt.astype(np.float64)[:, None, :] * xt.astype(np.float64)[src]).sum(2)
+    assert np.abs(dw - ref_dw).max() <= 1e-5 * np.abs(ref_dw).max()
+    ref_dx = np.zeros((48, t8))
+    np.add.at(ref_dx, src.ravel(), (dyt.astype(np.float64)[:, None, :] *
+                                    w.astype(np.float64)[:, :, None]).reshape(-1, t8))
+    assert np.abs(dxt - ref_dx).max() <= 1e-5 * np.abs(ref_dx).max()
+    w1 = np.ones((1, 1), np.float32)
+    s1 = np.zeros((1, 1), np.uint32)
+    dyt1 = np.float32([[2 ** 24, 1, -2 ** 24, 1, 0, 0, 0, 0]])
+    _, dw1 = oracle.b1_backward_t8(w1, s1, np.ones((1, 8), np.float32), dyt1,
+                                   np.zeros((1, 8), np.float32), np.zeros((1, 1), np.float32))
+    assert dw1[0, 0] == 1.0
