@@ -202,6 +202,15 @@ int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new
                           float *kcache, float *vcache, float *out, size_t n_heads,
                           size_t head_dim, size_t cap, size_t pos, float theta,
                           float scale);
+/* The same decode with the cached positions split over workgroups of
+ * `split` 16-position sub-chunks (0: one workgroup per head; -1: chosen by
+ * the library). No counterpart in the reference (a tuning choice); every
+ * split gives the same bits, since the sub-chunk partials are merged in
+ * position order whichever workgroup computed them. */
+int vmlm_attention_decode_split(const float *q, const float *k_new, const float *v_new,
+                                float *kcache, float *vcache, float *out, size_t n_heads,
+                                size_t head_dim, size_t cap, size_t pos, float theta,
+                                float scale, int split);
 
 /* ================================================================ layer 2
  * Device pointers, asynchronous on `stream`. Same semantics as layer 1. */
@@ -268,6 +277,10 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
                               float *kcache, float *vcache, float *out, size_t n_heads,
                               size_t head_dim, size_t cap, size_t pos, float theta,
                               float scale, void *stream);
+int vmlm_hip_attention_decode_split(const float *q, const float *k_new, const float *v_new,
+                                    float *kcache, float *vcache, float *out, size_t n_heads,
+                                    size_t head_dim, size_t cap, size_t pos, float theta,
+                                    float scale, int split, void *stream);
 
 /* ================================================================ layer 3 */
 

@@ -93,6 +93,7 @@ SIGNATURES = {
     "vmlm_jit_outer": (I, [P, P, P, U64]),
     "vmlm_attention_prefill": (I, [P, P, P, P, SZ, SZ, SZ, F, U16, F, B]),
     "vmlm_attention_decode": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F]),
+    "vmlm_attention_decode_split": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F, I]),
     # layer 2
     "vmlm_hip_gemm_nt_int8": (I, [P, P, P, P, SZ, SZ, SZ, P]),
     "vmlm_hip_gemm_nt_int8_noalloc": (I, [P, P, P, P, SZ, SZ, SZ, P]),
@@ -120,6 +121,7 @@ SIGNATURES = {
     "vmlm_hip_bias": (I, [P, P, SZ, SZ, P]),
     "vmlm_hip_attention_prefill": (I, [P, P, P, P, SZ, SZ, SZ, F, U16, F, B, P]),
     "vmlm_hip_attention_decode": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F, P]),
+    "vmlm_hip_attention_decode_split": (I, [P, P, P, P, P, P, SZ, SZ, SZ, SZ, F, F, I, P]),
     # layer 3
     "vmlm_decoder_create": (I, [C.POINTER(DecoderCfg), C.POINTER(P)]),
     "vmlm_decoder_destroy": (I, [P]),

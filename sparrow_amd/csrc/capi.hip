@@ -772,7 +772,16 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
                               float *kcache, float *vcache, float *out, size_t n_heads,
                               size_t head_dim, size_t cap, size_t pos, float theta,
                               float scale, void *stream) {
+    return vmlm_hip_attention_decode_split(q, k_new, v_new, kcache, vcache, out, n_heads,
+                                           head_dim, cap, pos, theta, scale, -1, stream);
+}
+
+int vmlm_hip_attention_decode_split(const float *q, const float *k_new, const float *v_new,
+                                    float *kcache, float *vcache, float *out, size_t n_heads,
+                                    size_t head_dim, size_t cap, size_t pos, float theta,
+                                    float scale, int split, void *stream) {
     INIT_OR_RETURN();
+    VMLM_GUARD(split >= -1 && split <= 4096, "attention decode: split %d out of range", split);
     VMLM_GUARD(head_dim == 64, "attention: head_dim %zu unsupported (64 only)", head_dim);
     VMLM_GUARD(pos < cap, "WRITECOL: column %zu beyond cache capacity %zu", pos, cap);
     VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
@@ -790,6 +799,7 @@ int vmlm_hip_attention_decode(const float *q, const float *k_new, const float *v
     a.pos = (int)pos;
     a.step = -2.0f / (float)head_dim * host_ln_f(theta);
     a.scale = scale;
+    a.split = split;
     Stage stg(st);
     const size_t wf = attention_decode_work_floats(a, 1);
     float *work = wf ? stg.alloc<float>(wf) : nullptr;
@@ -1188,6 +1198,14 @@ int vmlm_attention_prefill(const float *q, const float *k, const float *v, float
 int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new,
                           float *kcache, float *vcache, float *out, size_t n_heads,
                           size_t head_dim, size_t cap, size_t pos, float theta, float scale) {
+    return vmlm_attention_decode_split(q, k_new, v_new, kcache, vcache, out, n_heads, head_dim,
+                                       cap, pos, theta, scale, -1);
+}
+
+int vmlm_attention_decode_split(const float *q, const float *k_new, const float *v_new,
+                                float *kcache, float *vcache, float *out, size_t n_heads,
+                                size_t head_dim, size_t cap, size_t pos, float theta, float scale,
+                                int split) {
     HOST_CALL_BEGIN();
     const size_t w = n_heads * head_dim, cn = n_heads * cap * head_dim;
     {
@@ -1197,8 +1215,8 @@ int vmlm_attention_decode(const float *q, const float *k_new, const float *v_new
         float *dvc = stg.upload((const float *)vcache, cn);
         float *dout = stg.alloc<float>(w);
         STAGE_OK(stg);
-        int rc = vmlm_hip_attention_decode(dq, dk, dv, dkc, dvc, dout, n_heads, head_dim, cap,
-                                           pos, theta, scale, st);
+        int rc = vmlm_hip_attention_decode_split(dq, dk, dv, dkc, dvc, dout, n_heads, head_dim,
+                                                 cap, pos, theta, scale, split, st);
         if (!rc) rc = download(out, dout, w * sizeof(float), st);
         if (!rc) rc = download(kcache, dkc, cn * sizeof(float), st);
         if (!rc) rc = download(vcache, dvc, cn * sizeof(float), st);

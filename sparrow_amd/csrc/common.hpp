@@ -195,10 +195,13 @@ __device__ __forceinline__ float exp_f(float x) {
     p = p * r + 1.6666665e-1f;
     p = p * r + 0.5f;
     p = p * r2 + r + 1.0f;
-    int ni = as_i32(n);
-    if (ni >= -126) return p * __uint_as_float((uint32_t)(ni + 127) << 23);
-    if (ni >= -149) return p * __uint_as_float(1u << (ni + 149));
-    return 0.0f;
+    // p * 2^n, 2^n a normal or (n < -126) a subnormal float; the two cases
+    // as one select so the function has no branch (n >= -127 after the clamp)
+    const int ni = as_i32(n);
+    const float sc = ni >= -126 ? __uint_as_float((uint32_t)(ni + 127) << 23)
+                     : ni >= -149 ? __uint_as_float(1u << ((ni + 149) & 31))
+                                  : 0.0f;
+    return p * sc;
 }
 
 // ops/src/kernels.rs:240-255

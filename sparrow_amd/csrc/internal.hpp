@@ -269,11 +269,14 @@ struct DecodeArgs {
     const float *part = nullptr;
     int ks = 0, ldp = 0;
     const float *wscale = nullptr;
+    // 16-position sub-chunks per workgroup when the positions are split over
+    // several workgroups per pair (then merged by a second kernel); 0: one
+    // workgroup per pair; -1: chosen by the launcher. The result is the same
+    // bits for every choice.
+    int split = -1;
 };
-// `work` (optional, attention_decode_work_floats() floats): with a host
-// position (posp null) and few (head, sequence) pairs, the cached positions
-// are split over several workgroups per pair and merged in order by a second
-// kernel.
+// `work` (attention_decode_work_floats() floats, 0 when the positions are
+// not split) holds the sub-chunk partials of a split launch.
 size_t attention_decode_work_floats(const DecodeArgs &a, int B);
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st, float *work = nullptr);

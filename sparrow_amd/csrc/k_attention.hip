@@ -230,6 +230,10 @@ constexpr int AT_LD = 72;  // bf16 elements per LDS row (64 + 8)
 // [1,0,3,2]): partners that differ in bit 3, 2, 1, 0 of the lane index.
 constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_QUAD_REV = 0x1B, DPP_QUAD_SWAP = 0xB1;
+// row_ror:n (the row's 16 lanes rotated by n) and row_newbcast:n (every
+// lane of the row <- lane n of the row)
+constexpr int DPP_ROW_ROR1 = 0x121, DPP_ROW_ROR2 = 0x122, DPP_ROW_ROR4 = 0x124,
+              DPP_ROW_ROR8 = 0x128, DPP_ROW_BCAST0 = 0x150;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -614,28 +618,32 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
 }
 
 // ---------------------------------------------------------------- decode
-// Decode attention, one workgroup per (head, sequence): the new query and key
-// are rotated once, the new key/value row is appended to the cache, and the
-// AD_NW waves stride over the positions in chunks of 64 (wave w takes chunks
-// w, w + AD_NW, ...). Each chunk leaves (m_c, l_c, o_c) = (max score,
-// sum e^{s - m_c}, sum e^{s - m_c} v) in LDS; after a barrier they are merged
-// in chunk order,
-//   out = sum_c o_c e^{m_c - M} / sum_c l_c e^{m_c - M},
-// so the result does not depend on the wave count.
-// Lane (grp, q) of a wave holds dims 4q..4q+3 of positions p0 + 4*it + grp
-// (it = 0..15): one load instruction covers 4 consecutive 256-byte rows.
-// All 32 row loads of a chunk are issued together, unconditionally.
-// AD_NW is 8 when the (head, sequence) pairs are fewer than the CUs (one
-// workgroup per CU), else 4 with a register budget for three workgroups per
-// CU so that all of them are resident at once.
+// Decode attention over sub-chunks of 16 cached positions. A wave takes one
+// sub-chunk s at a time (rows 16 s .. 16 s + 15) and leaves its partial
+//   (m_s, l_s, o_s) = (max score, sum e^{x - m_s}, sum e^{x - m_s} v)
+// then the partials are merged in sub-chunk order,
+//   out = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M},  M = max_s m_s,
+// either by the workgroup itself (one workgroup per (head, sequence), the
+// partials in LDS) or, with the positions split over several workgroups, by
+// attn_decode_merge_kernel from partials in global memory. Both merges are
+// the same arithmetic over the same partials, so the result does not depend
+// on how the positions are split.
+// Lane (grp, q) of a wave holds dims 4q..4q+3 of rows 16 s + 4 it + grp
+// (it = 0..3): one load instruction covers 4 consecutive 256-byte rows. Dot
+// products are summed over the 16 lanes of a row group with DPP and over
+// the four groups with lane swaps (v_permlane16/32_swap), so every sum runs
+// in VALU registers and each lane ends with the values it consumes. The
+// next sub-chunk's rows are loaded while the current one is consumed (small
+// loads in flight on many waves stream faster than one large batch per wave).
+// The workgroup that holds sub-chunk 0 rotates the new query and key once
+// and appends the new key/value row to the cache.
 constexpr int BUF_RSRC_WORD3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 constexpr int BUF_NT = 2;  // buffer load cache policy: nontemporal (streamed once)
 
-
 // One stage of the transposing butterfly: N values per lane become N/2 sums;
 // the lane with `up` keeps the upper half and sends the lower.
-template <int N, int CTRL>
-__device__ __forceinline__ void bfly_stage(float (&d)[16], bool up) {
+template <int N, int CTRL, int SZ>
+__device__ __forceinline__ void bfly_stage(float (&d)[SZ], bool up) {
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
         const float send = up ? d[j] : d[j + N / 2];
@@ -668,64 +676,147 @@ __device__ __forceinline__ float rows_to_uniform_sum(float v) {
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
     return (r0 + r1) + (r2 + r3);
 }
-constexpr int AD_PART = 68;                 // floats per chunk partial: m, l, pad, o[64]
-constexpr int PART_KS_MAX = 16;             // k-slices of partial q/k/v read up front
+constexpr int AD_PART = 68;             // floats per sub-chunk partial: m, l, f, pad, o[64]
+constexpr int AD_SUB = 16;              // cached positions per sub-chunk (16, 32 or 64)
+constexpr int AD_NV = AD_SUB / 4;       // rows of a sub-chunk per lane
+constexpr int AD_RSH = AD_NV == 4 ? 2 : AD_NV == 8 ? 1 : 0;  // lane q holds row q >> AD_RSH
+constexpr int AD_LDS_MAX = 64 * 1024;   // partials of one workgroup's positions in LDS
+constexpr int PART_KS_MAX = 16;         // k-slices of partial q/k/v read up front
 
-template <int AD_NW, bool PART>
-__global__ __launch_bounds__(AD_NW * 64) __attribute__((amdgpu_waves_per_eu(AD_NW == 4 ? 3 : 2)))
-void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int T, int ldt,
-                        int B, int cpp, float *ppart) {
-    extern __shared__ float cpart[];  // [ceil(cap / 64)][AD_PART]
+// The output row: y = O / L, written as f32 and, with T > 0, as T bf16
+// terms (y0 = bf16(y), y1 = bf16(y - y0), ...).
+__device__ __forceinline__ void decode_store(float y, int col, int b, float *out, int ldo,
+                                             uint16_t *terms, int T, int ldt, int B) {
+    out[(size_t)b * ldo + col] = y;
+    if (terms) {
+        for (int t = 0; t < T; ++t) {
+            const uint32_t hb = bf16_rne_bits(y);
+            y = term_rem(y, hb);
+            terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
+        }
+    }
+}
+
+// w[it] = lane it << RSH of the lane's row (row_newbcast), it = 0..NV-1.
+template <int NV, int RSH>
+__device__ __forceinline__ void bcast_rows(float e, float (&w)[NV]) {
+    w[0] = dpp_f<DPP_ROW_BCAST0>(e);
+    if constexpr (NV > 1) w[1] = dpp_f<DPP_ROW_BCAST0 + (1 << RSH)>(e);
+    if constexpr (NV > 2) w[2] = dpp_f<DPP_ROW_BCAST0 + (2 << RSH)>(e);
+    if constexpr (NV > 3) w[3] = dpp_f<DPP_ROW_BCAST0 + (3 << RSH)>(e);
+    if constexpr (NV > 4) {
+        w[4] = dpp_f<DPP_ROW_BCAST0 + (4 << RSH)>(e);
+        w[5] = dpp_f<DPP_ROW_BCAST0 + (5 << RSH)>(e);
+        w[6] = dpp_f<DPP_ROW_BCAST0 + (6 << RSH)>(e);
+        w[7] = dpp_f<DPP_ROW_BCAST0 + (7 << RSH)>(e);
+    }
+    if constexpr (NV > 8) {
+        w[8] = dpp_f<DPP_ROW_BCAST0 + 8>(e);
+        w[9] = dpp_f<DPP_ROW_BCAST0 + 9>(e);
+        w[10] = dpp_f<DPP_ROW_BCAST0 + 10>(e);
+        w[11] = dpp_f<DPP_ROW_BCAST0 + 11>(e);
+        w[12] = dpp_f<DPP_ROW_BCAST0 + 12>(e);
+        w[13] = dpp_f<DPP_ROW_BCAST0 + 13>(e);
+        w[14] = dpp_f<DPP_ROW_BCAST0 + 14>(e);
+        w[15] = dpp_f<DPP_ROW_BCAST0 + 15>(e);
+    }
+}
+
+// M = max_s m_s, as a wave-uniform value (lane j takes s = j, j + 64, ...;
+// a max is exact, so the grouping does not change it).
+__device__ __forceinline__ float partial_max(const float *pp, int n) {
+    const int lane = threadIdx.x & 63;
+    float M = pp[(lane < n ? lane : 0) * AD_PART];
+    for (int c = lane + 64; c < n; c += 64) M = fmaxf(M, pp[c * AD_PART]);
+    M = row16_max(M);
+    M = fmaxf(M, lane_xor16(M));
+    return fmaxf(M, lane_xor32(M));
+}
+// L += sum_s l_s f_s and O += sum_s o_s[d] f_s over n partials in order,
+// the weights f_s = e^{m_s - M} in slot 2; the loads of four sub-chunks are
+// issued before their FMAs.
+__device__ __forceinline__ void merge_partials(const float *pp, int n, int d, float &L, float &O) {
+    int c = 0;
+    for (; c + 16 <= n; c += 16) {
+        float f[16], l[16], o[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            f[j] = pp[(c + j) * AD_PART + 2];
+            l[j] = pp[(c + j) * AD_PART + 1];
+            o[j] = pp[(c + j) * AD_PART + 4 + d];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            L = __builtin_fmaf(l[j], f[j], L);
+            O = __builtin_fmaf(o[j], f[j], O);
+        }
+    }
+    for (; c + 4 <= n; c += 4) {
+        float f[4], l[4], o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[j] = pp[(c + j) * AD_PART + 2];
+            l[j] = pp[(c + j) * AD_PART + 1];
+            o[j] = pp[(c + j) * AD_PART + 4 + d];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            L = __builtin_fmaf(l[j], f[j], L);
+            O = __builtin_fmaf(o[j], f[j], O);
+        }
+    }
+    for (; c < n; ++c) {
+        const float f = pp[c * AD_PART + 2];
+        L = __builtin_fmaf(pp[c * AD_PART + 1], f, L);
+        O = __builtin_fmaf(pp[c * AD_PART + 4 + d], f, O);
+    }
+}
+
+// grid (H, B, partitions); partition z takes sub-chunks [z spp, z spp + spp)
+// (spp = 0: all of them, merged here). gsub: sub-chunk slots per (head,
+// sequence) in gpart.
+template <int NW, bool PART, bool SPLIT>
+__global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, float *out, int ldo,
+                                                              uint16_t *terms, int T, int ldt,
+                                                              int B, int spp, float *gpart,
+                                                              int gsub) {
+    extern __shared__ float spart[];  // [nsub][AD_PART] when this workgroup merges
     __shared__ float qs[64], kn[64], vn[64];
-    __shared__ float es[AD_NW][64];
     __shared__ float qkv_s[PART ? 192 : 1];
-    // the cache rows are streamed once per step: nontemporal loads (measured
-    // 2 % faster at batch 16, equal at batch 1)
+    // the cache rows are streamed once per step: nontemporal loads
     constexpr int KV_POLICY = BUF_NT;
     const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = lane >> 4, q = lane & 15;
     const int pos = a.posp ? *a.posp : a.pos;
-    const int nch = (pos + 1 + 63) / 64;
-    // this workgroup's chunks [c0, c1): all, or partition blockIdx.z of cpp
-    const int c0 = cpp ? (int)blockIdx.z * cpp : 0;
-    const int c1 = cpp ? min(c0 + cpp, nch) : nch;
+    const int nsub = pos / AD_SUB + 1;
+    const int s0 = spp ? (int)blockIdx.z * spp : 0;
+    const int s1 = spp ? min(s0 + spp, nsub) : nsub;
+    if (s0 >= s1) return;  // a partition past the cached positions (never z = 0)
     const size_t head = ((size_t)b * a.H + h) * (a.hs ? a.hs : a.cap) * 64;
 
     // Cache rows through buffer loads whose range ends at row `pos`: rows at
-    // or past it (the new row, unused rows, chunks past the last) read as
-    // zero without a memory access, so every wave issues its first chunk
-    // unconditionally and the memory counter waits stay exact.
+    // or past it (the new row, rows of a sub-chunk past the last) read as
+    // zero without a memory access, so every load is issued unconditionally
+    // and the memory counter waits stay exact.
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc((void *)(a.kc + head), 0, pos * 256, BUF_RSRC_WORD3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + head), 0, pos * 256, BUF_RSRC_WORD3);
-    float4 kv[16], vv[16];
-    auto load_chunk = [&](int c) {
+    auto load = [&](float4 (&kk)[AD_NV], float4 (&vv)[AD_NV], int s) {
 #pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const int off = (c * 64 + it * 4 + grp) * 256 + 16 * q;
-            kv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, KV_POLICY));
+        for (int it = 0; it < AD_NV; ++it) {
+            const int off = (s * AD_SUB + it * 4 + grp) * 256 + 16 * q;
+            kk[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, KV_POLICY));
             vv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, KV_POLICY));
         }
     };
-    // a wave's next chunk: its keys as soon as the scores are out of kv, its
-    // values once the weighted sum is out of vv (chunks past the last read as 0)
-    auto load_k = [&](int c) {
-#pragma unroll
-        for (int it = 0; it < 16; ++it)
-            kv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    krs, (c * 64 + it * 4 + grp) * 256 + 16 * q, 0, KV_POLICY));
-    };
-    auto load_v = [&](int c) {
-#pragma unroll
-        for (int it = 0; it < 16; ++it)
-            vv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    vrs, (c * 64 + it * 4 + grp) * 256 + 16 * q, 0, KV_POLICY));
-    };
+    // a sub-chunk this workgroup owns, else one wholly past `pos` (zeros)
+    auto live = [&](int s) { return s < s1 ? s : nsub + wave; };
+
     // the new q/k/v values first (every lane, unconditionally), then the
-    // chunk rows; the scheduling barriers keep that issue order so the
+    // first rows; the scheduling barriers keep that issue order so the
     // rotation below waits only for the former
     const int l32 = lane & 31;
     float q1 = 0.f, q2 = 0.f, k1 = 0.f, k2 = 0.f, vnew = 0.f;
@@ -733,7 +824,7 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     float wsc = 0.f;
     if constexpr (PART) {
         // threads 0..191 each own one of the head's q/k/v columns and load
-        // every k-slice partial of it (index clamped) before the chunk rows
+        // every k-slice partial of it (index clamped) before the cache rows
         const int c = tid < 192 ? tid : 191;
         const int pcol = (c >> 6) * a.H * 64 + h * 64 + (c & 63);
         const float *pp = a.part + (size_t)b * a.ldp + pcol;
@@ -748,9 +839,9 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
         vnew = a.v_new[(size_t)b * a.ldq + h * 64 + lane];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // waves past the workgroup's last chunk load a chunk past `pos`: zeros,
-    // no memory access
-    load_chunk(c0 + wave < c1 ? c0 + wave : nch + wave);
+    float4 ka[AD_NV], va[AD_NV], kb[AD_NV], vb[AD_NV];
+    int s = s0 + wave;
+    load(ka, va, live(s));
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PART) {  // slices summed in order, then the row scale
         float v = pv[0];
@@ -787,179 +878,196 @@ void attn_decode_kernel(DecodeArgs a, float *out, int ldo, uint16_t *terms, int 
     const float4 kq = make_float4(kn[4 * q], kn[4 * q + 1], kn[4 * q + 2], kn[4 * q + 3]);
     const float4 vq = make_float4(vn[4 * q], vn[4 * q + 1], vn[4 * q + 2], vn[4 * q + 3]);
 
-    // 8 waves (few workgroups, long rows per wave): a wave's next chunk is
-    // loaded while the current one is consumed; 4 waves: loaded at the top
-    constexpr bool PIPE = AD_NW == 8;
-    for (int c = c0 + wave; c < c1; c += AD_NW) {
-        if (!PIPE && c != c0 + wave) load_chunk(c);
-        const int p0 = c * 64;
+    auto consume = [&](const float4 (&kk)[AD_NV], const float4 (&vv)[AD_NV], int sc_) {
+        const int p0 = sc_ * AD_SUB;
         // partial dots (4 dims per lane), then a transposing butterfly over
-        // the 16 lanes of a group: lane (grp, q) ends with position
-        // p0 + 4q + grp (15 DPP exchanges for 16 sums)
-        float d[16];
+        // the 16 lanes of a row group: lane (grp, q) ends with row
+        // p0 + 4 (q >> AD_RSH) + grp, the same value on the lanes that
+        // differ only in the low AD_RSH bits of q
+        float d[AD_NV];
 #pragma unroll
-        for (int it = 0; it < 16; ++it) {
+        for (int it = 0; it < AD_NV; ++it) {
             const int p = p0 + it * 4 + grp;
-            const float4 k4 = p == pos ? kq : kv[it];
+            const float4 k4 = p == pos ? kq : kk[it];
             float t = qv.x * k4.x;
             t = __builtin_fmaf(qv.y, k4.y, t);
             t = __builtin_fmaf(qv.z, k4.z, t);
             d[it] = __builtin_fmaf(qv.w, k4.w, t);
         }
-        bfly_stage<16, DPP_ROW_MIRROR>(d, (q & 8) != 0);
-        bfly_stage<8, DPP_ROW_HALF_MIRROR>(d, (q & 4) != 0);
-        bfly_stage<4, DPP_QUAD_REV>(d, (q & 2) != 0);
-        bfly_stage<2, DPP_QUAD_SWAP>(d, (q & 1) != 0);
-        if constexpr (PIPE) load_k(c + AD_NW);
-        const float sc = p0 + 4 * q + grp <= pos ? d[0] * a.scale : -INFINITY;
-        const float mc = rows_to_uniform_max(sc);  // chunk c holds position p0 <= pos: finite
+        bfly_stage<AD_NV, DPP_ROW_MIRROR>(d, (q & 8) != 0);
+        bfly_stage<AD_NV / 2, DPP_ROW_HALF_MIRROR>(d, (q & 4) != 0);
+        if constexpr (AD_NV >= 8) bfly_stage<AD_NV / 4, DPP_QUAD_REV>(d, (q & 2) != 0);
+        if constexpr (AD_NV >= 16) bfly_stage<AD_NV / 8, DPP_QUAD_SWAP>(d, (q & 1) != 0);
+        float dd = d[0];
+        if constexpr (AD_NV < 8) dd = dd + dpp_f<DPP_QUAD_REV>(dd);
+        if constexpr (AD_NV < 16) dd = dd + dpp_f<DPP_QUAD_SWAP>(dd);
+        const float sc = p0 + 4 * (q >> AD_RSH) + grp <= pos ? dd * a.scale : -INFINITY;
+        // the sub-chunk's max and sum: the rows of the group (lanes rotated
+        // by 8, 4, ... within the row, each row once), then the four groups
+        // (lanes l ^ 16, l ^ 32)
+        float mc = fmaxf(sc, dpp_f<DPP_ROW_ROR8>(sc));
+        mc = fmaxf(mc, dpp_f<DPP_ROW_ROR4>(mc));
+        if constexpr (AD_NV >= 8) mc = fmaxf(mc, dpp_f<DPP_ROW_ROR2>(mc));
+        if constexpr (AD_NV >= 16) mc = fmaxf(mc, dpp_f<DPP_ROW_ROR1>(mc));
+        mc = fmaxf(mc, lane_xor16(mc));
+        mc = fmaxf(mc, lane_xor32(mc));  // row p0 <= pos: finite
         const float e = sc == -INFINITY ? 0.0f : exp_f(sc - mc);
-        const float lc = rows_to_uniform_sum(e);
-        es[wave][4 * q + grp] = e;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float lc = e + dpp_f<DPP_ROW_ROR8>(e);
+        lc = lc + dpp_f<DPP_ROW_ROR4>(lc);
+        if constexpr (AD_NV >= 8) lc = lc + dpp_f<DPP_ROW_ROR2>(lc);
+        if constexpr (AD_NV >= 16) lc = lc + dpp_f<DPP_ROW_ROR1>(lc);
+        lc = lc + lane_xor16(lc);
+        lc = lc + lane_xor32(lc);
+        // weights of rows (it, grp): lane it << AD_RSH of the row, broadcast
+        float w[AD_NV];
+        bcast_rows<AD_NV, AD_RSH>(e, w);
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const float w = es[wave][it * 4 + grp];
+        for (int it = 0; it < AD_NV; ++it) {
             const float4 v4 = p0 + it * 4 + grp == pos ? vq : vv[it];
-            o.x = __builtin_fmaf(w, v4.x, o.x);
-            o.y = __builtin_fmaf(w, v4.y, o.y);
-            o.z = __builtin_fmaf(w, v4.z, o.z);
-            o.w = __builtin_fmaf(w, v4.w, o.w);
+            o.x = __builtin_fmaf(w[it], v4.x, o.x);
+            o.y = __builtin_fmaf(w[it], v4.y, o.y);
+            o.z = __builtin_fmaf(w[it], v4.z, o.z);
+            o.w = __builtin_fmaf(w[it], v4.w, o.w);
         }
-        if constexpr (PIPE) load_v(c + AD_NW);
-#pragma unroll
-        for (int off = 16; off < 64; off <<= 1) {
-            o.x += __shfl_xor(o.x, off, 64);
-            o.y += __shfl_xor(o.y, off, 64);
-            o.z += __shfl_xor(o.z, off, 64);
-            o.w += __shfl_xor(o.w, off, 64);
+        o.x = o.x + lane_xor16(o.x);
+        o.y = o.y + lane_xor16(o.y);
+        o.z = o.z + lane_xor16(o.z);
+        o.w = o.w + lane_xor16(o.w);
+        o.x = o.x + lane_xor32(o.x);
+        o.y = o.y + lane_xor32(o.y);
+        o.z = o.z + lane_xor32(o.z);
+        o.w = o.w + lane_xor32(o.w);
+        if constexpr (SPLIT) {
+            float *pc = gpart + (((size_t)b * a.H + h) * gsub + sc_) * AD_PART;
+            if (lane == 0) *(float2 *)pc = make_float2(mc, lc);
+            if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
+        } else {
+            float *pc = spart + sc_ * AD_PART;
+            if (lane == 0) *(float2 *)pc = make_float2(mc, lc);
+            if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
         }
-        float *pc = cpart + (size_t)c * AD_PART;
-        if (lane == 0) {
-            pc[0] = mc;
-            pc[1] = lc;
-        }
-        if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    while (s < s1) {
+        load(kb, vb, live(s + NW));
+        consume(ka, va, s);
+        s += NW;
+        if (s >= s1) break;
+        load(ka, va, live(s + NW));
+        consume(kb, vb, s);
+        s += NW;
     }
+    if constexpr (SPLIT) return;  // merged by attn_decode_merge_kernel
     __syncthreads();
-    // each chunk's weight e^{m_c - M} once (into the chunk's spare slot),
-    // then every output dim sums over the chunks in order
-    float M = cpart[c0 * AD_PART];
-    for (int c = c0 + 1; c < c1; ++c) M = fmaxf(M, cpart[c * AD_PART]);
-    for (int c = c0 + tid; c < c1; c += AD_NW * 64) cpart[c * AD_PART + 2] = exp_f(cpart[c * AD_PART] - M);
+    const float M = partial_max(spart, nsub);  // every wave, the same value
+    for (int c = tid; c < nsub; c += NW * 64) spart[c * AD_PART + 2] = exp_f(spart[c * AD_PART] - M);
     __syncthreads();
     if (tid >= 64) return;
     float L = 0.0f, O = 0.0f;
-    for (int c = c0; c < c1; ++c) {
-        const float f = cpart[c * AD_PART + 2];
-        L = __builtin_fmaf(cpart[c * AD_PART + 1], f, L);
-        O = __builtin_fmaf(cpart[c * AD_PART + 4 + tid], f, O);
-    }
-    if (ppart) {  // partition partial (M, L, O[64]) for the merge kernel
-        float *pp = ppart + (((size_t)b * a.H + h) * gridDim.z + blockIdx.z) * AD_PART;
-        if (tid == 0) {
-            pp[0] = M;
-            pp[1] = L;
-        }
-        pp[4 + tid] = O;
-        return;
-    }
-    float y = O / L;
-    const int col = h * 64 + tid;
-    out[(size_t)b * ldo + col] = y;
-    if (terms) {
-        for (int t = 0; t < T; ++t) {
-            const uint32_t hb = bf16_rne_bits(y);
-            y = term_rem(y, hb);
-            terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
-        }
-    }
+    merge_partials(spart, nsub, tid, L, O);
+    decode_store(O / L, h * 64 + tid, b, out, ldo, terms, T, ldt, B);
 }
 
-// Merges the P partition partials (M_p, L_p, O_p) of each (head, sequence)
-// in partition order: out = sum_p O_p e^{M_p - M} / sum_p L_p e^{M_p - M}.
-__global__ __launch_bounds__(64) void attn_decode_merge_kernel(const float *__restrict__ ppart, int P,
-                                                               int H, float *out, int ldo,
-                                                               uint16_t *terms, int T, int ldt,
-                                                               int B) {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const float *pp = ppart + ((size_t)b * H + h) * P * AD_PART;
-    float M = pp[0];
-    for (int p = 1; p < P; ++p) M = fmaxf(M, pp[p * AD_PART]);
+// The same merge over the partials of every partition, in sub-chunk order:
+// blocks of AD_MBLK sub-chunks copied to LDS (one coalesced pass by the 256
+// threads) and folded into the running sums in order; M from the copy when
+// one block holds them all, else from a first pass over the m_s.
+constexpr int AD_MBLK = AD_LDS_MAX / (AD_PART * sizeof(float));
+__global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float *__restrict__ gpart,
+                                                                int gsub, const int *posp, int pos,
+                                                                int H, float *out, int ldo,
+                                                                uint16_t *terms, int T, int ldt,
+                                                                int B) {
+    extern __shared__ float sm[];  // [min(nsub, AD_MBLK)][AD_PART]
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int nsub = (posp ? *posp : pos) / AD_SUB + 1;
+    const float *pp = gpart + ((size_t)b * H + h) * gsub * AD_PART;
+    float M = nsub > AD_MBLK ? partial_max(pp, nsub) : 0.0f;
     float L = 0.0f, O = 0.0f;
-    for (int p = 0; p < P; ++p) {
-        const float f = exp_f(pp[p * AD_PART] - M);
-        L = __builtin_fmaf(pp[p * AD_PART + 1], f, L);
-        O = __builtin_fmaf(pp[p * AD_PART + 4 + d], f, O);
+    for (int c0 = 0; c0 < nsub; c0 += AD_MBLK) {
+        const int n = min(AD_MBLK, nsub - c0);
+        const float4 *src = (const float4 *)(pp + (size_t)c0 * AD_PART);
+        for (int i = tid; i < n * (AD_PART / 4); i += 256) ((float4 *)sm)[i] = src[i];
+        __syncthreads();
+        if (nsub <= AD_MBLK) M = partial_max(sm, n);
+        for (int c = tid; c < n; c += 256) sm[c * AD_PART + 2] = exp_f(sm[c * AD_PART] - M);
+        __syncthreads();
+        if (tid < 64) merge_partials(sm, n, tid, L, O);
+        __syncthreads();
     }
-    float y = O / L;
-    const int col = h * 64 + d;
-    out[(size_t)b * ldo + col] = y;
-    if (terms) {
-        for (int t = 0; t < T; ++t) {
-            const uint32_t hb = bf16_rne_bits(y);
-            y = term_rem(y, hb);
-            terms[((size_t)t * B + b) * ldt + col] = (uint16_t)hb;
-        }
-    }
+    if (tid < 64) decode_store(O / L, h * 64 + tid, b, out, ldo, terms, T, ldt, B);
 }
 
-// Partitions of 4 chunks (one per wave) when the position is known on the
-// host, the (head, sequence) pairs are fewer than the CUs and the cache holds
-// at least 8 chunks; else 0 (one workgroup per pair).
-static int decode_partitions(const DecodeArgs &a, int B) {
+// Sub-chunks per partition, or 0 for one workgroup per (head, sequence):
+// the caller's choice (a.split >= 0), else partitions when one workgroup's
+// partials would not fit in LDS, or with a host position when the pairs are
+// fewer than the CUs and the rows long (512 positions or more; 128
+// positions per workgroup).
+static int decode_spp(const DecodeArgs &a, int B) {
+    if (a.split >= 0) return a.split;
+    const int gsub = (a.cap + AD_SUB - 1) / AD_SUB;
+    if ((size_t)gsub * AD_PART * sizeof(float) > AD_LDS_MAX) return 4;
     if (a.posp || a.part || a.H * B >= 256) return 0;
-    const int nch = (a.pos + 1 + 63) / 64;
-    return nch >= 8 ? (nch + 3) / 4 : 0;
+    return a.pos + 1 >= 512 ? (128 / AD_SUB > 1 ? 128 / AD_SUB : 1) : 0;
 }
 
 size_t attention_decode_work_floats(const DecodeArgs &a, int B) {
-    const int P = decode_partitions(a, B);
-    return P ? (size_t)B * a.H * P * AD_PART : 0;
+    return decode_spp(a, B) ? (size_t)B * a.H * ((a.cap + AD_SUB - 1) / AD_SUB) * AD_PART : 0;
+}
+
+template <int NW>
+static void launch_decode_nw(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
+                             int T, int ldt, hipStream_t st, dim3 grid, size_t lds, int spp,
+                             float *work, int gsub) {
+    if (spp) {
+        if (a.part)
+            attn_decode_kernel<NW, true, true><<<grid, NW * 64, lds, st>>>(a, out, ldo, terms, T,
+                                                                           ldt, B, spp, work, gsub);
+        else
+            attn_decode_kernel<NW, false, true><<<grid, NW * 64, lds, st>>>(a, out, ldo, terms, T,
+                                                                            ldt, B, spp, work, gsub);
+    } else {
+        if (a.part)
+            attn_decode_kernel<NW, true, false><<<grid, NW * 64, lds, st>>>(a, out, ldo, terms, T,
+                                                                            ldt, B, 0, work, gsub);
+        else
+            attn_decode_kernel<NW, false, false><<<grid, NW * 64, lds, st>>>(a, out, ldo, terms, T,
+                                                                             ldt, B, 0, work, gsub);
+    }
 }
 
 int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uint16_t *terms,
                             int T, int ldt, hipStream_t st, float *work) {
     VMLM_GUARD(a.cap >= 1 && a.H >= 1 && B >= 1 && (a.hs == 0 || a.hs >= a.cap),
                "attention decode: empty shape, or head stride below the capacity");
-    const size_t lds = (size_t)((a.cap + 63) / 64) * AD_PART * sizeof(float);
-    VMLM_GUARD(lds <= 96 * 1024, "attention decode: cache capacity %d beyond %d positions",
-               a.cap, 96 * 1024 / (AD_PART * 4) * 64);
-    VMLM_GUARD((size_t)a.cap * 256 <= 0x7fffffffu, "attention decode: cache row range too large");
+    VMLM_GUARD((size_t)(a.cap + 16 * AD_SUB) * 256 <= 0x7fffffffu,
+               "attention decode: cache row range too large");
     VMLM_GUARD(!a.part || (a.ks >= 1 && a.ks <= PART_KS_MAX && a.wscale && a.ldp >= 3 * a.H * 64),
                "attention decode: partial q/k/v need ks, ldp and scales");
-    const int P = work ? decode_partitions(a, B) : 0;
-    if (P > 1) {
-        attn_decode_kernel<4, false><<<dim3(a.H, B, P), 4 * 64, lds, st>>>(a, out, ldo, terms, T,
-                                                                            ldt, B, 4, work);
+    const int gsub = (a.cap + AD_SUB - 1) / AD_SUB;
+    const int spp = decode_spp(a, B);
+    if (spp > 0) {
+        VMLM_GUARD(work, "attention decode: split positions need a work buffer of %zu floats",
+                   attention_decode_work_floats(a, B));
+        // grid from the capacity for a device position, else from `pos`
+        const int nsub = a.posp ? gsub : a.pos / AD_SUB + 1;
+        const dim3 grid(a.H, B, (nsub + spp - 1) / spp);
+        launch_decode_nw<4>(a, B, out, ldo, terms, T, ldt, st, grid, 0, spp, work, gsub);
         VMLM_HIP_CHECK(hipGetLastError());
-        attn_decode_merge_kernel<<<dim3(a.H, B), 64, 0, st>>>(work, P, a.H, out, ldo, terms, T,
-                                                              ldt, B);
+        const size_t mlds = (size_t)(gsub < AD_MBLK ? gsub : AD_MBLK) * AD_PART * sizeof(float);
+        attn_decode_merge_kernel<<<dim3(a.H, B), 256, mlds, st>>>(
+            work, gsub, a.posp, a.pos, a.H, out, ldo, terms, T, ldt, B);
         VMLM_HIP_CHECK(hipGetLastError());
         return VMLM_OK;
     }
+    const size_t lds = (size_t)gsub * AD_PART * sizeof(float);
+    VMLM_GUARD(lds <= AD_LDS_MAX, "attention decode: cache capacity %d needs split positions",
+               a.cap);
     const dim3 grid(a.H, B);
-    if (a.H * B < 256) {
-        if (a.part)
-            attn_decode_kernel<8, true><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B, 0,
-                                                                   nullptr);
-        else
-            attn_decode_kernel<8, false><<<grid, 8 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B,
-                                                                    0, nullptr);
-    } else {
-        if (a.part)
-            attn_decode_kernel<4, true><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B, 0,
-                                                                   nullptr);
-        else
-            attn_decode_kernel<4, false><<<grid, 4 * 64, lds, st>>>(a, out, ldo, terms, T, ldt, B,
-                                                                    0, nullptr);
-    }
+    if (a.H * B < 256)
+        launch_decode_nw<8>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
+    else
+        launch_decode_nw<4>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

@@ -242,8 +242,11 @@ def attention_prefill(q, k, v, n_heads, theta=10000.0, pos0=0, scale=None, causa
     return out
 
 
-def attention_decode(q, k_new, v_new, kcache, vcache, pos, theta=10000.0, scale=None):
-    """tools/p12_build_minicpm.py:941-967; caches [H, cap, hd] updated in place."""
+def attention_decode(q, k_new, v_new, kcache, vcache, pos, theta=10000.0, scale=None,
+                     split=-1):
+    """tools/p12_build_minicpm.py:941-967; caches [H, cap, hd] updated in place.
+    `split`: 16-position sub-chunks per workgroup (0: one workgroup per head,
+    -1: the library's choice); the result is the same bits for every split."""
     H, cap, hd = kcache.shape
     assert kcache.dtype == np.float32 and kcache.flags.c_contiguous
     assert vcache.dtype == np.float32 and vcache.flags.c_contiguous
@@ -251,7 +254,7 @@ def attention_decode(q, k_new, v_new, kcache, vcache, pos, theta=10000.0, scale=
         scale = float(np.float32(1.0 / np.sqrt(hd)))
     q, k_new, v_new = (_c(t, np.float32).reshape(-1) for t in (q, k_new, v_new))
     out = np.empty(H * hd, np.float32)
-    check(lib().vmlm_attention_decode(_p(q), _p(k_new), _p(v_new), _p(kcache), _p(vcache),
-                                      _p(out), H, hd, cap, int(pos), float(theta),
-                                      float(scale)))
+    check(lib().vmlm_attention_decode_split(_p(q), _p(k_new), _p(v_new), _p(kcache),
+                                            _p(vcache), _p(out), H, hd, cap, int(pos),
+                                            float(theta), float(scale), int(split)))
     return out

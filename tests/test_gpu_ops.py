@@ -420,9 +420,10 @@ def test_attention_prefill(ops, oracle, S, H):
 @pytest.mark.parametrize("H,pos", [(36, 1023), (36, 700), (4, 511), (36, 300)])
 def test_attention_decode_cfg2(ops, oracle, H, pos):
     """Config 2 decode: 1 query against a KV cache of length 1024 (pos 1023),
-    and shorter caches: split over partitions of 4 chunks merged in order
-    (pos 1023, 700, 511: a partial last partition at 700) or one workgroup
-    per head (pos 300, under 8 chunks)."""
+    and shorter caches: split over partitions of four 16-position
+    sub-chunks merged in order (pos 1023, 700, 511: a partial last partition
+    at 700), or one workgroup per head (pos 300: 19 sub-chunks, under the 32
+    from which the library splits)."""
     rng = np.random.default_rng(2)
     hd, cap = 64, 1024
     kc = np.zeros((H, cap, hd), np.float32)
@@ -438,6 +439,37 @@ def test_attention_decode_cfg2(ops, oracle, H, pos):
     assert_close_rms(got, ref)
     assert np.array_equal(bits(kc[:, pos]), bits(kc2[:, pos]))  # appended rotated k, bitwise
     assert np.array_equal(vc[:, pos], vc2[:, pos])
+
+
+@pytest.mark.parametrize("pos", [1023, 700, 257, 100, 16, 15, 0])
+def test_attention_decode_split_bitwise(ops, oracle, pos):
+    """The cached positions split over workgroups of 1, 2, 3, 4, 8 or 64
+    sub-chunks of 16 positions, or one workgroup per head: the same bits
+    every time (the sub-chunk partials are merged in position order
+    whichever workgroup computed them), within 1e-4 RMS of the oracle, and
+    the appended row bitwise the oracle's. pos 0 attends the new row only;
+    15 and 16 end a sub-chunk and start the next."""
+    rng = np.random.default_rng(20 + pos)
+    H, hd, cap = 8, 64, 1024
+    kc = np.zeros((H, cap, hd), np.float32)
+    vc = np.zeros((H, cap, hd), np.float32)
+    kc[:, :pos, :] = rng.standard_normal((H, pos, hd), dtype=np.float32)
+    vc[:, :pos, :] = rng.standard_normal((H, pos, hd), dtype=np.float32)
+    q, kn, vn = (rng.standard_normal(H * hd, dtype=np.float32) for _ in range(3))
+    kr, vr = kc.copy(), vc.copy()
+    ref = oracle.attention_decode(q, kn, vn, kr, vr, pos)
+    first = None
+    for split in (0, -1, 1, 2, 3, 4, 8, 64):
+        k2, v2 = kc.copy(), vc.copy()
+        got = ops.attention_decode(q, kn, vn, k2, v2, pos, split=split)
+        assert np.array_equal(bits(k2[:, pos]), bits(kr[:, pos])), split
+        assert np.array_equal(v2[:, pos], vr[:, pos]), split
+        assert np.array_equal(k2[:, :pos], kc[:, :pos]), split
+        if first is None:
+            first = got
+            assert_close_rms(got, ref)
+        else:
+            assert np.array_equal(bits(got), bits(first)), split
 
 
 def test_graph_capture_replay(hip, oracle):
