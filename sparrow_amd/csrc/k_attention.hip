@@ -7,12 +7,13 @@
 // online softmax (exp_f of the reference, scores scaled exactly as OP_SCALE
 // does) -- the [S,S] score matrix never reaches HBM.
 //
-// Decode (tools/p12_build_minicpm.py:941-967): per (sequence, head, 64-
-// position split) one wavefront rotates q and the new k at `pos`, appends the
-// rotated k and raw v to the f32 cache, scores its positions (16 lanes per
-// 256-byte K row, four rows per coalesced load instruction, all loads of
-// the split in flight together), and accumulates its share of p.V; a
-// combine kernel merges the splits (flash-decoding).
+// Decode (tools/p12_build_minicpm.py:941-967): per (sequence, head) one
+// workgroup rotates q and the new k at `pos` and appends the rotated k and
+// raw v to the f32 cache; its waves score 16-position sub-chunks (16 lanes
+// per 256-byte K row, four rows per coalesced load instruction, the next
+// sub-chunk's rows in flight) and leave a (max, sum, p.V) partial for each;
+// the partials are merged in position order, in LDS or, with the positions
+// split over several workgroups, by a second kernel (flash-decoding).
 //
 // Both change the order of the reference's sums (E contract: 1e-4 of the
 // output RMS); RoPE, the scale multiply and every exp_f are bitwise.
