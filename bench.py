@@ -66,6 +66,26 @@ def gemv_roofline(dec, iters):
     lm_us, lm_b = dec.time_gemv(4, max(4, iters // 10))
     per["lm_head_bf16"] = {"us": round(lm_us, 3), "bytes": int(lm_b),
                            "GBps": round(lm_b / lm_us / 1e3, 1)}
+    # 40 layers of o weights (212 MB) fit the 256 MB Infinity Cache, so its
+    # loop may read them warm; the other shapes' 40-layer sets do not fit
+    per["o"]["cache"] = "212 MB of o weights fit the 256 MB Infinity Cache: may read warm"
+    with_red = None
+    if not dec.fused:
+        # the k-slice projections followed by the kernel that reduces their
+        # partials (o: residual RMSNorm into int8 rows, gate/up: SiLU * up,
+        # down: residual RMSNorm); q/k/v's partials are reduced inside the
+        # attention kernel
+        with_red = {}
+        rb = rt = 0.0
+        for which, name in ((5, "o+resid_q8"), (6, "gate_up+silu_q8"), (7, "down+resid_q8")):
+            us, nbytes = dec.time_gemv(which, iters)
+            with_red[name] = {"us": round(us, 3), "bytes": int(nbytes),
+                              "GBps": round(nbytes / us / 1e3, 1)}
+            rb += nbytes
+            rt += us
+        with_red["frac"] = round(rb / rt / 1e3 / HBM_PEAK_GBS, 4)
+        with_red["note"] = ("projection plus its partial reduction, per pair; frac = sum bytes / "
+                            "sum time over the three pairs")
     achieved = tot_b / tot_t / 1e3  # GB/s
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -77,7 +97,7 @@ def gemv_roofline(dec, iters):
                        "ks_gemv_i8_kernel (q/k/v, gate+up; int8 rows) and ks_gemv_kernel "
                        "(o, down); k-slice partials"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
-            "per_shape": per}
+            "per_shape": per, "with_reduction": with_red}
 
 
 def cpu_baseline(cfg, W, steps, threads):
@@ -100,11 +120,38 @@ def cpu_baseline(cfg, W, steps, threads):
         logits, _ = ref.step(tok, 129 + s)
         tok = int(np.argmax(logits))
     dt = time.perf_counter() - t
+    model, physical, logical = host_cpu()
     return {"value": round(steps / dt, 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{steps} greedy decode steps, batch 1, all 40 layers + LM head at the "
-                      f"MiniCPM-2B shape, positions 129..{128 + steps}; oracle/vmlm_oracle.c "
-                      f"(AVX2 restatement of ops/src/kernels.rs), {threads} OpenMP threads"}
+            "kind": "port", "batch": 1,
+            "cpu_model": model, "host_physical_cores": physical, "host_logical_cpus": logical,
+            "sample": f"{steps} greedy decode steps, batch 1 (the oracle decodes one sequence "
+                      f"at a time), all 40 layers + LM head at the MiniCPM-2B shape, positions "
+                      f"129..{128 + steps}; oracle/vmlm_oracle.c (AVX2 restatement of "
+                      f"ops/src/kernels.rs), {threads} OpenMP threads on {model}"}
+
+
+def host_cpu():
+    """The host's CPU model name, physical core count and logical CPU count
+    (from /proc/cpuinfo; None where unreadable)."""
+    model, cores, logical = None, set(), 0
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    logical += 1
+                elif k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                    cores.add((phys, core))
+    except OSError:
+        pass
+    return model, (len(cores) or None), (logical or os.cpu_count())
 
 
 PEAK_BF16_TFLOPS = 2500.0   # dense MFMA bf16
@@ -284,8 +331,15 @@ def run_suite(iters, cpu=True):
     xb = up(rng.standard_normal((T, d), dtype=np.float32))
     yb = zeros(T * d * 4)
     arr = (type(layers[0].struct) * 8)(*[l.struct for l in layers])
-    us, wall = _timed(L, lambda: L.vmlm_b1_stack_forward(arr, 8, xb, yb, T, 4, None),
+    us_fwd, wall_fwd = _timed(L, lambda: L.vmlm_b1_stack_forward(arr, 8, xb, yb, T, 4, None),
+                              max(8, iters // 4))
+    tm_fwd = _LAST[0]
+    # the plan built once (vmlm_b1_stack_create): one kernel per forward,
+    # captured and replayed
+    plan = conn.StackPlan(layers)
+    us, wall = _timed(L, lambda: L.vmlm_b1_stack_run(plan._h, xb, yb, T, 4, None),
                       max(8, iters // 4))
+    plan.close()
     layer_bytes = 12976128
     gbs = 8 * layer_bytes / us / 1e3
     # the t8 contract sums without FMA: one multiply and one add per
@@ -298,7 +352,13 @@ def run_suite(iters, cpu=True):
                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                             "T_mac_per_s": round(tmac, 3),
                             "frac_valu_mac": round(tmac / VALU_MAC_PEAK_T, 4),
-                            "note": "plan kernel + one kernel for all 8 layers, x and y [T][d]"}
+                            "note": "one kernel for all 8 layers over a plan built once "
+                                    "(vmlm_b1_stack_create), x and y [T][d]",
+                            "per_call_forward": {"us": round(us_fwd, 2),
+                                                 "host_us": round(wall_fwd, 2),
+                                                 "timing": tm_fwd,
+                                                 "note": "vmlm_b1_stack_forward: plan kernel "
+                                                         "+ stack kernel on every call"}}
     if orc:  # one layer of the stack on the host (the t8 contract), per layer
         w0, s0 = conn.make_block_aligned(np.random.default_rng(4), d, k0)
         xt_h = orc.transpose_t8(np.random.default_rng(5).standard_normal((T, d), dtype=np.float32),

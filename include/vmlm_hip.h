@@ -332,10 +332,12 @@ void *vmlm_decoder_stream(vmlm_decoder *dec);
 int vmlm_decoder_set_fused(vmlm_decoder *dec, int enable);
 int vmlm_decoder_fused(const vmlm_decoder *dec);
 /* Times `iters` launches of one decode-step GEMV of every layer in turn
- * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head) on the session stream;
- * writes the mean per-launch duration (HIP events) and its algorithmic
- * HBM bytes (weights + scales + activations in + outputs; on the fused
- * path also the norm gain or the residual rows). */
+ * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; on the k-slice
+ * program also 5, 6, 7: the o, gate/up or down projection followed by the
+ * kernel that reduces its k-slice partials) on the session stream; writes
+ * the mean per-launch (or per-pair) duration (HIP events) and the
+ * projection's algorithmic HBM bytes (weights + scales + activations in +
+ * outputs; on the fused path also the norm gain or the residual rows). */
 int vmlm_decoder_time_gemv(vmlm_decoder *dec, int which, uint32_t iters, float *avg_us,
                            double *bytes_per_launch);
 
@@ -345,6 +347,19 @@ int vmlm_decoder_time_gemv(vmlm_decoder *dec, int which, uint32_t iters, float *
 int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers,
                           const float *x, float *y, size_t n_tokens, uint16_t act,
                           void *stream);
+/* The same stack with its connection plan built once (no reference
+ * counterpart: the reference re-reads the SparseConnW arrays on every
+ * forward). create validates the layers as vmlm_b1_stack_forward does,
+ * prepares the plan from the current weights and indices on `stream` and
+ * waits for it (later changes to the arrays need a new plan; stacks the
+ * one-kernel path does not cover return 5). run is one kernel launch with
+ * no allocation, so it can be captured into a graph. */
+typedef struct vmlm_b1_stack vmlm_b1_stack;
+int vmlm_b1_stack_create(const vmlm_sparse_conn_w *layers, uint32_t n_layers, void *stream,
+                         vmlm_b1_stack **out);
+int vmlm_b1_stack_run(vmlm_b1_stack *stack, const float *x, float *y, size_t n_tokens,
+                      uint16_t act, void *stream);
+int vmlm_b1_stack_destroy(vmlm_b1_stack *stack);
 
 /* ================================================================ VM
  * Device-resident executor of .vmb programs: core/src/interp.rs Vm::load /

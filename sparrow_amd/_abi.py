@@ -136,6 +136,9 @@ SIGNATURES = {
     "vmlm_decoder_fused": (I, [P]),
     "vmlm_decoder_time_gemv": (I, [P, I, U32, C.POINTER(F), C.POINTER(C.c_double)]),
     "vmlm_b1_stack_forward": (I, [C.POINTER(SparseConnW), U32, P, P, SZ, U16, P]),
+    "vmlm_b1_stack_create": (I, [C.POINTER(SparseConnW), U32, P, C.POINTER(C.c_void_p)]),
+    "vmlm_b1_stack_run": (I, [P, P, P, SZ, U16, P]),
+    "vmlm_b1_stack_destroy": (I, [P]),
     "vmlm_vm_load": (I, [C.c_char_p, SZ, P, SZ, C.POINTER(P)]),
     "vmlm_vm_destroy": (I, [P]),
     "vmlm_vm_run": (I, [P]),

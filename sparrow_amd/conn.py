@@ -106,3 +106,29 @@ def stack_forward(layers: list[DeviceConn], x_dev: int, y_dev: int, n_tokens: in
     arr = (_abi.SparseConnW * len(layers))(*[l.struct for l in layers])
     check(lib().vmlm_b1_stack_forward(arr, len(layers), x_dev, y_dev, int(n_tokens), int(act),
                                       stream))
+
+
+class StackPlan:
+    """A B1 stack with its connection plan built once (vmlm_b1_stack_create):
+    run() is one kernel launch with no allocation. The plan holds the weights
+    and indices as they were at creation."""
+
+    def __init__(self, layers: list[DeviceConn], stream=None):
+        arr = (_abi.SparseConnW * len(layers))(*[l.struct for l in layers])
+        h = C.c_void_p()
+        check(lib().vmlm_b1_stack_create(arr, len(layers), stream, C.byref(h)))
+        self._h = h
+
+    def run(self, x_dev: int, y_dev: int, n_tokens: int, act: int = 4, stream=None) -> None:
+        check(lib().vmlm_b1_stack_run(self._h, x_dev, y_dev, int(n_tokens), int(act), stream))
+
+    def close(self) -> None:
+        if self._h:
+            lib().vmlm_b1_stack_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

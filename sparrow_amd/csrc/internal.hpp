@@ -307,6 +307,11 @@ bool b1_stack_ok(int d, const int *k0, int n_layers);
 size_t b1_stack_plan_bytes(int d, const int *k0, int n_layers);
 int launch_b1_stack(const B1PlanJob *layers, int n_layers, int d, const float *x, float *y,
                     int T, int act, void *plan, hipStream_t st);
+// launch_b1_stack in two parts: the plan (once per topology) and the stack
+// kernel over it.
+int launch_b1_stack_plan(const B1PlanJob *layers, int n_layers, int d, void *plan, hipStream_t st);
+int launch_b1_stack_run(const void *plan, const int *k0, int n_layers, int d, const float *x,
+                        float *y, int T, int act, hipStream_t st);
 int launch_b1_t8_plan_layer(const void *plan, int n, int k0, int d, const float *x, size_t xbs,
                             size_t xrs, int n_tokens, float *y, size_t ybs, size_t yrs, int act,
                             hipStream_t st);

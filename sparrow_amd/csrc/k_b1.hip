@@ -554,6 +554,17 @@ static int launch_stack_g(const char *plan, size_t stride, int n_layers, int d, 
 int launch_b1_stack(const B1PlanJob *layers, int n_layers, int d, const float *x, float *y, int T,
                     int act, void *plan, hipStream_t st) {
     if (T == 0) return VMLM_OK;
+    int rc = launch_b1_stack_plan(layers, n_layers, d, plan, st);
+    if (rc) return rc;
+    std::vector<int> k0(n_layers);
+    for (int l = 0; l < n_layers; ++l) k0[l] = layers[l].k0;
+    return launch_b1_stack_run(plan, k0.data(), n_layers, d, x, y, T, act, st);
+}
+
+// The plan of every layer (connection words in the stack kernel's layout),
+// a function of the topology and weights only.
+int launch_b1_stack_plan(const B1PlanJob *layers, int n_layers, int d, void *plan,
+                         hipStream_t st) {
     std::vector<int> k0(n_layers);
     for (int l = 0; l < n_layers; ++l) k0[l] = layers[l].k0;
     if (!b1_stack_ok(d, k0.data(), n_layers)) return fail(VMLM_ERR_DEVICE, "b1 stack: bad shape");
@@ -569,6 +580,16 @@ int launch_b1_stack(const B1PlanJob *layers, int n_layers, int d, const float *x
         b1_plan_kernel<<<dim3(cdiv((size_t)d, 64), nj), 256, 0, st>>>(jobs, d, d, B1_SROW, G);
         VMLM_HIP_CHECK(hipGetLastError());
     }
+    return VMLM_OK;
+}
+
+// The stack kernel over a prepared plan (one launch, no allocation).
+int launch_b1_stack_run(const void *plan, const int *k0, int n_layers, int d, const float *x,
+                        float *y, int T, int act, hipStream_t st) {
+    if (T == 0) return VMLM_OK;
+    if (!b1_stack_ok(d, k0, n_layers)) return fail(VMLM_ERR_DEVICE, "b1 stack: bad shape");
+    const int G = stack_groups(k0, n_layers);
+    const size_t stride = stack_plan_stride(d, G);
     const char *p = (const char *)plan;
     switch (G) {
     case 1: return launch_stack_g<1>(p, stride, n_layers, d, x, y, T, act, st);

@@ -750,7 +750,9 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
                            double *bytes_per_launch) {
     int rc = check_loaded(d);
     if (rc) return rc;
-    VMLM_GUARD(which >= 0 && which <= 4 && iters >= 1, "time_gemv: which 0..4, iters >= 1");
+    VMLM_GUARD(which >= 0 && which <= 7 && iters >= 1, "time_gemv: which 0..7, iters >= 1");
+    VMLM_GUARD(which <= 4 || !d->fused,
+               "time_gemv: 5..7 time a k-slice projection with its reduction (k-slice program)");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     // the launches of the decode step: the k-slice GEMVs, or the LM head (bf16)
     auto make_lm = [&]() {
@@ -768,8 +770,11 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
         g.tiles = 9;
         return g;
     };
+    // 5, 6, 7: the o, gate/up or down projection and the kernel that reduces
+    // its k-slice partials (residual RMSNorm into int8 rows, SiLU * up)
+    const int proj = which >= 5 ? which - 4 : which;
     auto make = [&](size_t l) {
-        switch (which) {
+        switch (proj) {
         case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H);
         case 1: return step_gemv(d, d->Wo(l), d->t_att, H, H);
         case 2: return step_gemv(d, d->Wgu(l), d->t_x, 2 * I, H);
@@ -778,10 +783,21 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     };
     // the fused program (batch <= 5) runs the full-K kernels with their row ops
     const bool fk = d->fused && which < 4;
+    auto reduce = [&](size_t l) {
+        if (which == 5)
+            return launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
+                                   d->seg, d->x8, d->x8s, d->x8ssp, d->st);
+        if (which == 6)
+            return launch_silu_q8(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->seg_i, d->act8,
+                                  d->act8s, d->st);
+        return launch_resid_q8(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, d->InLn((l + 1) % d->L),
+                               B, H, d->seg, d->x8, d->x8s, d->x8ssp, d->st);
+    };
     auto launch = [&](size_t l) {
         if (which == 4) return launch_gemv(make_lm(), d->st);
         if (fk) return launch_fk_gemv(fk_args(d, l, which), d->st);
-        return launch_ks_gemv(make(l), d->st);
+        int r = launch_ks_gemv(make(l), d->st);
+        return r || which < 5 ? r : reduce(l);
     };
     // one event pair around `iters` back-to-back launches (the mean launch
     // duration, launch gaps included); successive launches walk the layers
@@ -867,6 +883,72 @@ int vmlm_b1_stack_forward(const vmlm_sparse_conn_w *layers, uint32_t n_layers, c
     (void)hipFreeAsync(a, st);
     (void)hipFreeAsync(b, st);
     return rc;
+}
+
+
+struct vmlm_b1_stack {
+    void *plan = nullptr;
+    std::vector<int> k0;
+    size_t d = 0;
+};
+
+int vmlm_b1_stack_create(const vmlm_sparse_conn_w *layers, uint32_t n_layers, void *stream,
+                         vmlm_b1_stack **out) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    VMLM_GUARD(out && layers && n_layers >= 1, "b1 stack: no layers");
+    const size_t d = layers[0].n_neurons;
+    std::vector<B1PlanJob> jobs(n_layers);
+    std::vector<int> k0s(n_layers);
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const vmlm_sparse_conn_w &sc = layers[l];
+        VMLM_GUARD(sc.n_neurons == d, "b1 stack: layer %u width %u != %zu", l, sc.n_neurons, d);
+        VMLM_GUARD(sc.e == (size_t)sc.n_neurons * sc.k0,
+                   "CONN_TRAIN: SparseConnW geometry inconsistent at layer %u", l);
+        VMLM_GUARD(sc.k0 <= 1024, "B1: k0 exceeds the safe stack bound");
+        k0s[l] = (int)sc.k0;
+        jobs[l] = B1PlanJob{sc.w, sc.src_u32, nullptr, k0s[l]};
+    }
+    if (!b1_stack_ok((int)d, k0s.data(), (int)n_layers))
+        return fail(VMLM_ERR_UNIMPL, "b1 stack plan: width %zu or k0 beyond the one-kernel stack",
+                    d);
+    hipStream_t st = as_stream(stream);
+    vmlm_b1_stack *s = new vmlm_b1_stack();
+    s->k0 = k0s;
+    s->d = d;
+    hipError_t e = hipMalloc(&s->plan, b1_stack_plan_bytes((int)d, k0s.data(), (int)n_layers));
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(e, "hipMalloc (b1 stack plan)");
+    }
+    rc = launch_b1_stack_plan(jobs.data(), (int)n_layers, (int)d, s->plan, st);
+    if (!rc) {
+        e = hipStreamSynchronize(st);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    if (rc) {
+        (void)hipFree(s->plan);
+        delete s;
+        return rc;
+    }
+    *out = s;
+    return VMLM_OK;
+}
+
+int vmlm_b1_stack_run(vmlm_b1_stack *stack, const float *x, float *y, size_t n_tokens,
+                      uint16_t act, void *stream) {
+    VMLM_GUARD(stack, "b1 stack: null plan");
+    VMLM_GUARD(n_tokens <= 0x7fffffff, "b1 stack: %zu tokens", n_tokens);
+    return launch_b1_stack_run(stack->plan, stack->k0.data(), (int)stack->k0.size(),
+                               (int)stack->d, x, y, (int)n_tokens, act == 0xFFFF ? -1 : (int)act,
+                               as_stream(stream));
+}
+
+int vmlm_b1_stack_destroy(vmlm_b1_stack *stack) {
+    if (!stack) return VMLM_OK;
+    (void)hipFree(stack->plan);
+    delete stack;
+    return VMLM_OK;
 }
 
 }  // extern "C"

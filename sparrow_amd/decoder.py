@@ -106,7 +106,9 @@ class Decoder:
         """Mean per-launch duration (us, HIP events on the session stream) of
         one decode-step GEMV over every layer in turn, and its algorithmic
         bytes. which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; the kernels of
-        the program the session runs (fused full-K or k-slice)."""
+        the program the session runs (fused full-K or k-slice). On the k-slice
+        program 5, 6, 7 time the o, gate/up or down projection together with
+        the kernel that reduces its partials."""
         us = C.c_float()
         nbytes = C.c_double()
         check(lib().vmlm_decoder_time_gemv(self._h, int(which), int(iters), C.byref(us),

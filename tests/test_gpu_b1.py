@@ -31,6 +31,52 @@ def test_b1_stack_cfg4_bitwise(hip, oracle):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
+def test_b1_stack_plan_equals_forward_and_replays(hip):
+    """vmlm_b1_stack_create / run (the plan built once) give the bits of
+    vmlm_b1_stack_forward at config 4; run captured into a HIP graph and
+    replayed three times, with eager calls and syncs between the replays,
+    equals the eager result every time; a stack beyond the one-kernel path
+    returns 5."""
+    import ctypes as C
+    from sparrow_amd import VmlmError, check, conn, lib
+    L = lib()
+    rng = np.random.default_rng(44)
+    d, k0, T = 1536, 32, 1024
+    dev = [conn.DeviceConn(*conn.make_block_aligned(rng, d, k0), layer=li) for li in range(8)]
+    x = rng.standard_normal((T, d), dtype=np.float32)
+    xb = conn.DeviceBuffer.from_array(x)
+    yf, yp, yg = (conn.DeviceBuffer(x.nbytes) for _ in range(3))
+    conn.stack_forward(dev, xb.ptr, yf.ptr, T, act=4)
+    plan = conn.StackPlan(dev)
+    plan.run(xb.ptr, yp.ptr, T, act=4)
+    ref = yf.to_array((T, d), np.float32)
+    assert np.array_equal(yp.to_array((T, d), np.float32).view(np.uint32), ref.view(np.uint32))
+    g = C.c_void_p()
+    check(L.vmlm_hip_capture_begin(None))
+    plan.run(xb.ptr, yg.ptr, T, act=4)
+    check(L.vmlm_hip_capture_end(None, C.byref(g)))
+    try:
+        for _ in range(3):
+            check(L.vmlm_hip_memset(yg.ptr, 0, x.nbytes))
+            plan.run(xb.ptr, yp.ptr, T, act=4)
+            check(L.vmlm_hip_sync())
+            check(L.vmlm_hip_graph_launch(g, None))
+            check(L.vmlm_hip_sync())
+            assert np.array_equal(yg.to_array((T, d), np.float32).view(np.uint32),
+                                  ref.view(np.uint32))
+    finally:
+        L.vmlm_hip_graph_destroy(g)
+    plan.close()
+    wide = [conn.DeviceConn(*conn.make_block_aligned(rng, 6000, 8))]
+    with pytest.raises(VmlmError) as e:
+        conn.StackPlan(wide)
+    assert e.value.code == 5
+    for b_ in dev + wide:
+        b_.free()
+    for b_ in (xb, yf, yp, yg):
+        b_.free()
+
+
 def test_b1_stack_prng_topology(hip, oracle):
     """The reference PRNG topology (core/src/conn_sparse.rs:157-214) as the
     index source, no activation."""
