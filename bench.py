@@ -510,6 +510,50 @@ def traffic_probe(iters):
     print(json.dumps({"probe": "traffic", "copy_bytes": nbytes, "gemv_iters": iters}))
 
 
+def mfma_probe(reps):
+    """For `rocprofv3 --pmc` runs of the MFMA kernels: config 1 (bf16 GEMM
+    1024 x 512 x 2048) and the four prefill projections of the decoder at
+    batch 16 (M = 2048 rows of f32 activations through the int8-row path:
+    q/k/v 6912 x 2304, o 2304 x 2304, gate/up 11520 x 2304, down 2304 x 5760),
+    `reps` eager calls each after one warm-up call."""
+    import ctypes as C
+    from sparrow_amd import check, lib
+    L = lib()
+    rng = np.random.default_rng(1)
+    bufs = []
+
+    def dev(a):
+        a = np.ascontiguousarray(a)
+        p = C.c_void_p()
+        check(L.vmlm_hip_malloc(C.byref(p), a.nbytes))
+        check(L.vmlm_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes))
+        bufs.append(p)
+        return p
+
+    def out(nbytes):
+        p = C.c_void_p()
+        check(L.vmlm_hip_malloc(C.byref(p), nbytes))
+        bufs.append(p)
+        return p
+
+    a = dev(rng.integers(0, 65535, (1024, 512)).astype(np.uint16) & 0xBFFF)
+    bt = dev(rng.integers(0, 65535, (2048, 512)).astype(np.uint16) & 0xBFFF)
+    c = out(1024 * 2048 * 4)
+    for _ in range(reps + 1):
+        check(L.vmlm_hip_gemm_nt_bf16bf16(a, bt, c, 1024, 2048, 512, None))
+    x = dev(rng.standard_normal((2048, 5760), dtype=np.float32))
+    for n, k in ((6912, 2304), (2304, 2304), (11520, 2304), (2304, 5760)):
+        w = dev(rng.integers(-127, 128, (n, k), dtype=np.int8))
+        sc = dev(np.full(n, 1e-3, np.float32))
+        y = out(2048 * n * 4)
+        for _ in range(reps + 1):
+            check(L.vmlm_hip_gemm_nt_int8(x, w, sc, y, 2048, n, k, None))
+    check(L.vmlm_hip_sync())
+    for p in bufs:
+        L.vmlm_hip_free(p)
+    print(json.dumps({"probe": "mfma", "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -523,6 +567,8 @@ def main():
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--suite-only", action="store_true",
                     help="only configs 0, 1, 2, 4 and the op timings (no decoder, no CPU)")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only config 1 and the prefill GEMMs, for the MFMA counter runs")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
     args = ap.parse_args()
@@ -538,6 +584,9 @@ def main():
     sparrow_amd.init(0)
     if args.traffic_probe:
         traffic_probe(20)
+        return
+    if args.mfma_probe:
+        mfma_probe(3)
         return
     if args.suite_only:
         print(json.dumps({"suite": run_suite(args.suite_iters, cpu=False)}))

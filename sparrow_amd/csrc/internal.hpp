@@ -141,6 +141,7 @@ struct GemmArgs {
     int ldc = 0;
     int bm = 0;      // tile rows (64, 128); 0 = chosen by shape
     int stages = 0;  // LDS stages of the copy pipeline (2..4); 0 = chosen by shape
+    int group = -1;  // tile order: 0 as dispatched, g > 0 grouped per XCD; -1 = default
     // or int8 rows (with int8 weights): Q8_T term planes [Q8_T][M][lda] and
     // row factors [M] from launch_rows_q8 (A and T unused)
     const int8_t *A8 = nullptr;
