@@ -156,6 +156,7 @@ def host_cpu():
 
 PEAK_BF16_TFLOPS = 2500.0   # dense MFMA bf16
 PEAK_FP32_TFLOPS = 157.3    # FP32
+PEAK_INT8_TOPS = 5000.0     # dense MFMA int8
 
 
 _LAST = ["eager"]  # how the last _timed call measured the GPU time
@@ -286,6 +287,34 @@ def run_suite(iters, cpu=True):
     tf = 2147483648 / us / 1e6
     out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0],
                              "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    # config 1's M = 1 variant (the GEMV path of the same entry point)
+    us1, wall1 = _timed(L, lambda: L.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, 1, 2048, 512, None),
+                        iters)
+    b1 = 2048 * 512 * 2 + 512 * 2 + 2048 * 4
+    out["cfg1_bf16_gemm"]["M1"] = {"us": round(us1, 2), "host_us": round(wall1, 2),
+                                   "timing": _LAST[0], "bytes": b1,
+                                   "GBps": round(b1 / us1 / 1e3, 1),
+                                   "frac_hbm": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4)}
+    # the decoder's prefill projections at batch 16 (M = 2048 rows of f32
+    # activations) through the device API: rows_q8 (the int8 terms of the
+    # rows), the int8 x int8 MFMA GEMM and the non-finite-row check, per call
+    xp = up(rng.standard_normal((2048, 5760), dtype=np.float32))
+    pre = {}
+    for name, n, k in (("qkv", 6912, 2304), ("o", 2304, 2304), ("gate_up", 11520, 2304),
+                       ("down", 2304, 5760)):
+        wq = up(rng.integers(-127, 128, (n, k), dtype=np.int8))
+        sq = up(np.full(n, 1e-3, np.float32))
+        yq = zeros(2048 * n * 4)
+        usp, wallp = _timed(L, lambda: L.vmlm_hip_gemm_nt_int8(xp, wq, sq, yq, 2048, n, k, None),
+                            max(8, iters // 10))
+        useful = 2 * 2048 * n * k / usp / 1e6
+        pre[name] = {"us": round(usp, 2), "host_us": round(wallp, 2), "timing": _LAST[0],
+                     "useful_TOPs": round(useful, 1),
+                     "frac_int8_peak_useful": round(useful / PEAK_INT8_TOPS, 4),
+                     "frac_int8_peak_issued": round(4 * useful / PEAK_INT8_TOPS, 4)}
+    pre["note"] = ("per call: rows_q8 + gemm_dma_i8_kernel + non-finite-row check; issued = 4 int8 "
+                   "MFMAs per product (four terms per activation)")
+    out["cfg3_prefill_gemm"] = pre
     if orc:
         af = orc.bf16_to_f32(a)
         out["cfg1_bf16_gemm"]["cpu_us"] = _cpu_us(lambda: orc.gemm_nt_bf16(af, bt))
