@@ -57,12 +57,20 @@ def gemv_roofline(dec, iters):
     their RMSNorm, residual and SiLU work)."""
     per = {}
     tot_b = tot_t = 0.0
+    rd_b = rd_t = 0.0
     for which, name in ((0, "qkv"), (1, "o"), (2, "gate_up"), (3, "down")):
         us, nbytes = dec.time_gemv(which, iters)
         per[name] = {"us": round(us, 3), "bytes": int(nbytes),
                      "GBps": round(nbytes / us / 1e3, 1)}
         tot_b += nbytes
         tot_t += us
+        # the same shape's weights read by a plain streaming kernel, launched
+        # the same way: what one launch of these bytes can reach at best
+        r_us, r_b = dec.time_gemv(8 + which, iters)
+        per[name]["read_floor"] = {"us": round(r_us, 3), "weight_bytes": int(r_b),
+                                   "GBps": round(r_b / r_us / 1e3, 1)}
+        rd_b += r_b
+        rd_t += r_us
     lm_us, lm_b = dec.time_gemv(4, max(4, iters // 10))
     per["lm_head_bf16"] = {"us": round(lm_us, 3), "bytes": int(lm_b),
                            "GBps": round(lm_b / lm_us / 1e3, 1)}
@@ -97,6 +105,8 @@ def gemv_roofline(dec, iters):
                        "ks_gemv_i8_kernel (q/k/v, gate+up; int8 rows) and ks_gemv_kernel "
                        "(o, down); k-slice partials"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
+            "timing": "graph replay of back-to-back launches (launch gaps included)",
+            "read_floor_frac": round(rd_b / rd_t / 1e3 / HBM_PEAK_GBS, 4),
             "per_shape": per, "with_reduction": with_red}
 
 

@@ -669,6 +669,7 @@ int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
     if (kb == KBV) {                                                                  \
         if (tw == 1 && nwv == 8) return launch_ks_t<KBV, 1, 8>(p, ks, st);            \
         if (tw == 2 && nwv == 8) return launch_ks_t<KBV, 2, 8>(p, ks, st);            \
+        if (tw == 3 && nwv == 4) return launch_ks_t<KBV, 3, 4>(p, ks, st);            \
         if (tw == 4 && nwv == 2) return launch_ks_t<KBV, 4, 2>(p, ks, st);            \
         if (tw == 4 && nwv == 4) return launch_ks_t<KBV, 4, 4>(p, ks, st);            \
         return launch_ks_t<KBV, 2, 4>(p, ks, st);                                     \

@@ -48,6 +48,26 @@ __global__ __launch_bounds__(64) void argmax_advance_kernel(
     else atomicOr(guard, 2);
 }
 
+// Reads n16 16-byte pieces with nontemporal loads, eight per thread, all
+// issued before any is used: the load pattern of the decode GEMVs without
+// their arithmetic, i.e. the floor of one launch that streams the same
+// bytes. The xor of the data goes to `sink` only if it hits a constant, so
+// the loads stay and nothing is written in practice.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4 *__restrict__ src, size_t n16,
+                                                          uint32_t *__restrict__ sink) {
+    const size_t base = (size_t)blockIdx.x * 2048 + threadIdx.x;
+    u32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const size_t idx = base + (size_t)i * 256;
+        v[i] = idx < n16 ? __builtin_nontemporal_load(src + idx) : u32x4{0u, 0u, 0u, 0u};
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+    if (x == 0x9e3779b9u) sink[0] = x;
+}
+
 __global__ void step_advance_kernel(int *step, int *pos) {
     *step = *step + 1;
     *pos = *pos + 1;
@@ -211,13 +231,15 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
     g.K = K;
     g.Y = d->part;
     g.ldy = N;
-    // launch shape (16-row tiles per wave, waves per workgroup), measured at
-    // the MiniCPM-2B shapes, batch 16: q/k/v 2 x 8 (5.22 us against 5.53 at
-    // 2 x 4), gate/up 4 x 4 (7.73 against 8.25), down 2 x 8 (6.32 against
-    // 6.53), o 2 x 4
+    // launch shape (16-row tiles per wave, waves per workgroup), from a sweep
+    // of 1..6 tiles x 2, 4, 8 waves at the MiniCPM-2B shapes, batch 16 (graph
+    // replay over 40 layers' weights): q/k/v 2 x 8 (5.40 us; 2 x 4 5.36,
+    // 4 x 4 5.64), gate/up 4 x 4 (7.90; 2 x 8 8.19), down 3 x 4 (5.46; 2 x 8
+    // 6.08, 4 x 4 5.86), o 2 x 4
     if (g.A8) {
-        g.tw = N >= 4 * K ? 4 : 2;
-        g.nwv = N >= 4 * K ? 4 : 8;
+        const bool wide = N >= 4 * K, deep = K > N;
+        g.tw = wide ? 4 : deep ? 3 : 2;
+        g.nwv = wide || deep ? 4 : 8;
     } else {
         g.tw = 2;
         g.nwv = K > (int)d->H ? 8 : 4;
@@ -750,8 +772,8 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
                            double *bytes_per_launch) {
     int rc = check_loaded(d);
     if (rc) return rc;
-    VMLM_GUARD(which >= 0 && which <= 7 && iters >= 1, "time_gemv: which 0..7, iters >= 1");
-    VMLM_GUARD(which <= 4 || !d->fused,
+    VMLM_GUARD(which >= 0 && which <= 11 && iters >= 1, "time_gemv: which 0..11, iters >= 1");
+    VMLM_GUARD(which <= 4 || which >= 8 || !d->fused,
                "time_gemv: 5..7 time a k-slice projection with its reduction (k-slice program)");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     // the launches of the decode step: the k-slice GEMVs, or the LM head (bf16)
@@ -772,7 +794,10 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     };
     // 5, 6, 7: the o, gate/up or down projection and the kernel that reduces
     // its k-slice partials (residual RMSNorm into int8 rows, SiLU * up)
-    const int proj = which >= 5 ? which - 4 : which;
+    // 8..11: a plain read of the q/k/v, o, gate/up or down weights of the
+    // layer (stream_read_kernel), the single-launch floor of that shape
+    const bool rd = which >= 8;
+    const int proj = rd ? which - 8 : which >= 5 ? which - 4 : which;
     auto make = [&](size_t l) {
         switch (proj) {
         case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H);
@@ -783,6 +808,14 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     };
     // the fused program (batch <= 5) runs the full-K kernels with their row ops
     const bool fk = d->fused && which < 4;
+    auto read = [&](size_t l) {
+        const KsArgs g = make(l);
+        const size_t n16 = (size_t)g.N * g.K / 16;
+        stream_read_kernel<<<(unsigned)((n16 + 2047) / 2048), 256, 0, d->st>>>(
+            (const u32x4 *)g.W, n16, (uint32_t *)d->logits);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return (int)VMLM_OK;
+    };
     auto reduce = [&](size_t l) {
         if (which == 5)
             return launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
@@ -794,29 +827,47 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
                                B, H, d->seg, d->x8, d->x8s, d->x8ssp, d->st);
     };
     auto launch = [&](size_t l) {
+        if (rd) return read(l);
         if (which == 4) return launch_gemv(make_lm(), d->st);
         if (fk) return launch_fk_gemv(fk_args(d, l, which), d->st);
         int r = launch_ks_gemv(make(l), d->st);
         return r || which < 5 ? r : reduce(l);
     };
-    // one event pair around `iters` back-to-back launches (the mean launch
-    // duration, launch gaps included); successive launches walk the layers
-    // so that no weight is re-read from cache
-    hipEvent_t e0, e1;
-    VMLM_HIP_CHECK(hipEventCreate(&e0));
-    VMLM_HIP_CHECK(hipEventCreate(&e1));
+    // `iters` back-to-back launches captured into one HIP graph, as the
+    // decode step runs; one event pair around a replay gives the mean launch
+    // duration, launch gaps included. Successive launches walk the layers so
+    // that no weight is re-read from cache.
     for (size_t l = 0; l < (which == 4 ? 1 : d->L); ++l)  // warm-up pass over every layer
         if ((rc = launch(l))) return rc;
-    VMLM_HIP_CHECK(hipEventRecord(e0, d->st));
-    for (uint32_t i = 0; i < iters; ++i)
-        if ((rc = launch(which == 4 ? 0 : i % d->L))) return rc;
-    VMLM_HIP_CHECK(hipEventRecord(e1, d->st));
-    VMLM_HIP_CHECK(hipEventSynchronize(e1));
+    VMLM_HIP_CHECK(hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal));
+    for (uint32_t i = 0; i < iters && !rc; ++i) rc = launch(which == 4 ? 0 : i % d->L);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(d->st, &g);
+    if (rc || e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc ? rc : hip_fail(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
     float ms = 0.0f;
-    VMLM_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
+    if ((e = hipEventCreate(&e0)) == hipSuccess && (e = hipEventCreate(&e1)) == hipSuccess &&
+        (e = hipGraphLaunch(x, d->st)) == hipSuccess && (e = hipEventRecord(e0, d->st)) == hipSuccess &&
+        (e = hipGraphLaunch(x, d->st)) == hipSuccess && (e = hipEventRecord(e1, d->st)) == hipSuccess &&
+        (e = hipEventSynchronize(e1)) == hipSuccess)
+        e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipGraphExecDestroy(x);
+    if (e != hipSuccess) return hip_fail(e, "time_gemv replay");
     *avg_us = ms * 1000.0f / (float)iters;
+    if (rd) {  // the weight bytes read
+        const KsArgs k = make(0);
+        *bytes_per_launch = (double)k.N * k.K;
+        return VMLM_OK;
+    }
     // algorithmic bytes of the projection: weights, row scales (int8), the
     // f32 activation in and the f32 result out (the partial sums and the
     // bf16 term planes are this implementation's, not the algorithm's)
