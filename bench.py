@@ -95,6 +95,7 @@ def gemv_roofline(dec, iters):
         with_red["note"] = ("projection plus its partial reduction, per pair; frac = sum bytes / "
                             "sum time over the three pairs")
     achieved = tot_b / tot_t / 1e3  # GB/s
+    gap_us, _ = dec.time_gemv(13, iters)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE),
@@ -107,7 +108,18 @@ def gemv_roofline(dec, iters):
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "timing": "graph replay of back-to-back launches (launch gaps included)",
             "read_floor_frac": round(rd_b / rd_t / 1e3 / HBM_PEAK_GBS, 4),
+            "empty_kernel_us": round(gap_us, 3),
+            "frac_excl_empty_kernel": round(tot_b / (tot_t - 4 * gap_us) / 1e3 / HBM_PEAK_GBS, 4),
             "per_shape": per, "with_reduction": with_red}
+
+
+def decode_attention(dec, iters):
+    """The session's decode attention (one launch per layer, every layer in
+    turn, graph-replayed): K and V rows of the cached positions plus the new
+    row, against HBM."""
+    us, nbytes = dec.time_gemv(12, iters)
+    return {"us": round(us, 3), "bytes": int(nbytes), "GBps": round(nbytes / us / 1e3, 1),
+            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "position": dec.position()}
 
 
 def cpu_baseline(cfg, W, steps, threads):
@@ -641,6 +653,7 @@ def main():
     prefill = {f"batch{args.batch}_ms": round(dec.prefill_s * 1e3, 3)}
     roof = gemv_roofline(dec, args.gemv_iters)
     log(f"q8 GEMV: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    attn = {f"batch{args.batch}": decode_attention(dec, args.gemv_iters)}
     dec.close()
 
     if args.batch == 1:
@@ -650,6 +663,7 @@ def main():
         prefill["batch1_ms"] = round(dec1.prefill_s * 1e3, 3)
         roof1 = gemv_roofline(dec1, args.gemv_iters)
         log(f"batch 1 q8 GEMV: {roof1['achieved']} GB/s ({roof1['frac'] * 100:.1f}% of peak)")
+        attn["batch1"] = decode_attention(dec1, args.gemv_iters)
         dec1.close()
         log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
 
@@ -693,6 +707,8 @@ def main():
                              "40 layers, LM head and first argmax), after a first call"),
         "event_ms_per_step": round(ev_s / args.steps * 1e3, 4),
         "roofline": roof,
+        "decode_attention": dict(attn, note="attn_decode_kernel per layer after the timed "
+                                            "steps (position: the row being appended)"),
         "cpu_baseline": cpu,
         "other_configs": suite,
         "tokens_checksum": int(np.asarray(toks, np.int64).sum()),

@@ -334,10 +334,14 @@ int vmlm_decoder_fused(const vmlm_decoder *dec);
 /* Times `iters` launches of one decode-step GEMV of every layer in turn
  * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; on the k-slice
  * program also 5, 6, 7: the o, gate/up or down projection followed by the
- * kernel that reduces its k-slice partials) on the session stream; writes
- * the mean per-launch (or per-pair) duration (HIP events) and the
- * projection's algorithmic HBM bytes (weights + scales + activations in +
- * outputs; on the fused path also the norm gain or the residual rows). */
+ * kernel that reduces its k-slice partials; 8..11: a plain streaming read
+ * of the q/k/v, o, gate/up or down weights, the single-launch floor of
+ * those bytes; 12: the decode attention; 13: an empty kernel) captured into
+ * one HIP graph on the session stream; writes the mean per-launch (or
+ * per-pair) duration of a replay (HIP events, launch gaps included) and the
+ * algorithmic HBM bytes (weights + scales + activations in + outputs; on the
+ * fused path also the norm gain or the residual rows; 8..11 the weight
+ * bytes; 12 the K and V rows read). */
 int vmlm_decoder_time_gemv(vmlm_decoder *dec, int which, uint32_t iters, float *avg_us,
                            double *bytes_per_launch);
 

@@ -68,6 +68,10 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4 *__restric
     if (x == 0x9e3779b9u) sink[0] = x;
 }
 
+// An empty kernel: back to back in a graph, its launches measure the fixed
+// cost every launch of the step pays before any work.
+__global__ void empty_kernel() {}
+
 __global__ void step_advance_kernel(int *step, int *pos) {
     *step = *step + 1;
     *pos = *pos + 1;
@@ -247,6 +251,36 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
     return g;
 }
 
+// Decode attention of layer l at the device position: q/k/v as the q/k/v
+// projection's k-slice partials (k-slice program) or as final rows (fused
+// program).
+DecodeArgs attn_args(vmlm_decoder *d, size_t l) {
+    const int H = (int)d->H;
+    DecodeArgs a;
+    a.q = a.k_new = a.v_new = nullptr;
+    if (d->fused) {
+        a.q = d->qkv;
+        a.k_new = d->qkv + H;
+        a.v_new = d->qkv + 2 * H;
+    } else {
+        a.part = d->part;
+        a.ks = d->ks_h;
+        a.ldp = 3 * H;
+        a.wscale = d->Sqkv(l);
+    }
+    a.ldq = 3 * H;
+    a.kc = d->Kc(l);
+    a.vc = d->Vc(l);
+    a.hs = (int)d->hs;
+    a.cap = (int)d->cap;
+    a.H = (int)d->NH;
+    a.posp = d->pos;
+    a.pos = 0;
+    a.step = d->rope_step;
+    a.scale = d->c.attn_scale;
+    return a;
+}
+
 // One decode step over the B sequences (all launches on d->st). Layer l's
 // input norm is produced by the previous layer's closing residual RMSNorm.
 int enqueue_step(vmlm_decoder *d) {
@@ -260,23 +294,8 @@ int enqueue_step(vmlm_decoder *d) {
         return rc;
     for (size_t l = 0; l < d->L; ++l) {
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H), st))) return rc;
-        DecodeArgs a;
-        a.q = a.k_new = a.v_new = nullptr;
-        a.ldq = 3 * H;
-        a.kc = d->Kc(l);
-        a.vc = d->Vc(l);
-        a.hs = (int)d->hs;
-        a.cap = (int)d->cap;
-        a.H = (int)d->NH;
-        a.posp = d->pos;
-        a.pos = 0;
-        a.step = d->rope_step;
-        a.scale = d->c.attn_scale;
-        a.part = d->part;
-        a.ks = d->ks_h;
-        a.ldp = 3 * H;
-        a.wscale = d->Sqkv(l);
-        if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, T, H, st))) return rc;
+        if ((rc = launch_attention_decode(attn_args(d, l), B, d->att, H, d->t_att, T, H, st)))
+            return rc;
         if ((rc = launch_ks_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H), st))) return rc;
         if ((rc = launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
                                   d->seg, d->x8, d->x8s, d->x8ssp, st)))
@@ -354,21 +373,8 @@ int enqueue_step_fused(vmlm_decoder *d) {
     if ((rc = launch_fk_norm_prep(d->h, H, d->InLn(0), B, H, d->t_x, H, d->ssp, st))) return rc;
     for (size_t l = 0; l < d->L; ++l) {
         if ((rc = launch_fk_gemv(fk_args(d, l, 0), st))) return rc;
-        DecodeArgs a;
-        a.q = d->qkv;
-        a.k_new = d->qkv + H;
-        a.v_new = d->qkv + 2 * H;
-        a.ldq = 3 * H;
-        a.kc = d->Kc(l);
-        a.vc = d->Vc(l);
-        a.hs = (int)d->hs;
-        a.cap = (int)d->cap;
-        a.H = (int)d->NH;
-        a.posp = d->pos;
-        a.pos = 0;
-        a.step = d->rope_step;
-        a.scale = d->c.attn_scale;
-        if ((rc = launch_attention_decode(a, B, d->att, H, d->t_att, 3, H, st))) return rc;
+        if ((rc = launch_attention_decode(attn_args(d, l), B, d->att, H, d->t_att, 3, H, st)))
+            return rc;
         for (int which = 1; which < 4; ++which)
             if ((rc = launch_fk_gemv(fk_args(d, l, which), st))) return rc;
     }
@@ -772,7 +778,7 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
                            double *bytes_per_launch) {
     int rc = check_loaded(d);
     if (rc) return rc;
-    VMLM_GUARD(which >= 0 && which <= 11 && iters >= 1, "time_gemv: which 0..11, iters >= 1");
+    VMLM_GUARD(which >= 0 && which <= 13 && iters >= 1, "time_gemv: which 0..13, iters >= 1");
     VMLM_GUARD(which <= 4 || which >= 8 || !d->fused,
                "time_gemv: 5..7 time a k-slice projection with its reduction (k-slice program)");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
@@ -796,8 +802,8 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     // its k-slice partials (residual RMSNorm into int8 rows, SiLU * up)
     // 8..11: a plain read of the q/k/v, o, gate/up or down weights of the
     // layer (stream_read_kernel), the single-launch floor of that shape
-    const bool rd = which >= 8;
-    const int proj = rd ? which - 8 : which >= 5 ? which - 4 : which;
+    const bool rd = which >= 8 && which <= 11;
+    const int proj = which >= 12 ? 0 : rd ? which - 8 : which >= 5 ? which - 4 : which;
     auto make = [&](size_t l) {
         switch (proj) {
         case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H);
@@ -828,6 +834,13 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     };
     auto launch = [&](size_t l) {
         if (rd) return read(l);
+        if (which == 13) {  // 13: an empty kernel (the per-launch fixed cost)
+            empty_kernel<<<1, 64, 0, d->st>>>();
+            VMLM_HIP_CHECK(hipGetLastError());
+            return (int)VMLM_OK;
+        }
+        if (which == 12)  // 12: the decode attention of the layer
+            return launch_attention_decode(attn_args(d, l), B, d->att, H, d->t_att, 3, H, d->st);
         if (which == 4) return launch_gemv(make_lm(), d->st);
         if (fk) return launch_fk_gemv(fk_args(d, l, which), d->st);
         int r = launch_ks_gemv(make(l), d->st);
@@ -866,6 +879,16 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     if (rd) {  // the weight bytes read
         const KsArgs k = make(0);
         *bytes_per_launch = (double)k.N * k.K;
+        return VMLM_OK;
+    }
+    if (which == 13) {
+        *bytes_per_launch = 0.0;
+        return VMLM_OK;
+    }
+    if (which == 12) {  // K and V rows of the cached positions and the new row
+        int pos = 0;
+        VMLM_HIP_CHECK(hipMemcpy(&pos, d->pos, sizeof(int), hipMemcpyDeviceToHost));
+        *bytes_per_launch = 512.0 * B * d->NH * (pos + 1);
         return VMLM_OK;
     }
     // algorithmic bytes of the projection: weights, row scales (int8), the

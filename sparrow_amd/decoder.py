@@ -108,7 +108,9 @@ class Decoder:
         bytes. which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; the kernels of
         the program the session runs (fused full-K or k-slice). On the k-slice
         program 5, 6, 7 time the o, gate/up or down projection together with
-        the kernel that reduces its partials."""
+        the kernel that reduces its partials. 8..11: a plain read of the
+        q/k/v, o, gate/up or down weights; 12: the decode attention; 13: an
+        empty kernel. Launches are replayed from one HIP graph."""
         us = C.c_float()
         nbytes = C.c_double()
         check(lib().vmlm_decoder_time_gemv(self._h, int(which), int(iters), C.byref(us),
