@@ -331,7 +331,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     // int8 weights, many rows, unpadded K: the rows as int8 terms with a
     // per-row factor, then the int8 x int8 MFMA GEMM
     if (wi8 && m > 16 && Wd == W && Kp == k && k <= 8192 && ((uintptr_t)a & 15) == 0) {
-        int8_t *a8 = stg.template alloc<int8_t>((size_t)Q8_T * m * k);
+        int8_t *a8 = stg.template alloc<int8_t>(q8_rows_bytes(m, k));
         float *a8s = stg.template alloc<float>(m);
         const size_t gw = gemm_i8_work_floats((int)m, (int)n, (int)k);
         float *gwork = gw ? stg.template alloc<float>(gw) : nullptr;

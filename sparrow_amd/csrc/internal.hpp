@@ -142,10 +142,12 @@ struct GemmArgs {
     int bm = 0;      // tile rows (64, 128); 0 = chosen by shape
     int stages = 0;  // LDS stages of the copy pipeline (2..4); 0 = chosen by shape
     int group = -1;  // tile order: 0 as dispatched, g > 0 grouped per XCD; -1 = default
-    // or int8 rows (with int8 weights): Q8_T term planes [Q8_T][M][lda] and
-    // row factors [M] from launch_rows_q8 (A and T unused)
+    // or int8 rows (with int8 weights): the blocked term planes and row
+    // factors [M] of launch_rows_q8 (A, T and lda unused)
     const int8_t *A8 = nullptr;
     const float *a8s = nullptr;
+    // int8 rows: W is the swizzled copy (launch_swizzle_w) instead of row-major
+    bool w_blocked = false;
     // int8 rows, optional: gemm_i8_work_floats() floats for the k-slices of
     // a grid that would leave most CUs idle (null: one slice)
     float *work = nullptr;
@@ -215,9 +217,18 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
                     float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
                     float *q8s, float *ssp, hipStream_t st);
-// Rows x [rows][ldx] (with g: RMSNorm(x) * g) as Q8_T int8 terms
-// [Q8_T][rows][cols] with per-row power-of-two factors q8s [rows]: the input
-// of launch_gemm's int8-row path.
+// Rows x [rows][ldx] (with g: RMSNorm(x) * g) as Q8_T int8 terms with
+// per-row power-of-two factors q8s [rows]: the input of launch_gemm's
+// int8-row path. Layout (q8_rows_bytes(rows, cols) bytes): Q8_T planes of
+// q8_rows_tiles(rows) x (cols / 64) blocks of 1 KiB; block (row tile rt,
+// k-block kb) holds rows 16 rt .. 16 rt + 15, k 64 kb .. 64 kb + 63, lane
+// (g, r) = 16 bytes at (16 g + r) * 16: row r, k 8g .. 8g + 7 and 32 + 8g ..
+// 32 + 8g + 7 (the order of the swizzled weights, launch_swizzle_w); then
+// one float per row tile row, used between the two launches. Rows past
+// `rows` in the last 16-row tile are zero terms, later tiles are not
+// written. cols % 64 == 0, cols <= 8192.
+size_t q8_rows_tiles(size_t rows);
+size_t q8_rows_bytes(size_t rows, size_t cols);
 int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
                    int8_t *q8, float *q8s, hipStream_t st);
 // SiLU(gate) * up from the partials of the interleaved gate/up projection,

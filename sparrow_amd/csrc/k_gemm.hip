@@ -19,8 +19,8 @@ struct GemmParams {
     float *C;
     size_t tstride;
     int lda, M, N, K, ldc;
-    const int8_t *A8;   // int8 rows: Q8_T term planes [Q8_T][M][lda] and
-    const float *a8s;   // row factors [M] (gemm_dma_i8_kernel)
+    const int8_t *A8;   // int8 rows: Q8_T blocked term planes (launch_rows_q8), tstride
+    const float *a8s;   // bytes apart, and row factors [M] (gemm_dma_i8_kernel)
     float *part;        // k-slices > 1: raw sums times the row factor [ks][M][N]
     int group;          // tile order: 0 as dispatched, g > 0 XCD-grouped (gemm_tile)
 };
@@ -254,25 +254,33 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
 
 // The same pipeline for int8 weights and int8 rows (Q8_T term planes of
 // each row with a power-of-two row factor, from launch_rows_q8): both tiles
-// stay int8 in LDS (64-byte rows, the int8 XOR swizzle), and each 64-wide
-// k-step runs one v_mfma_i32_16x16x64_i8 per term and 16 x 16 tile, exact
-// int32 sums per term. Lane (g, r) takes 16-byte piece g of its A row and of
-// its W row, so both operands pair the same k. The epilogue forms
-// ((s0 + s1/2^7) + s2/2^14) + s3/2^21 in f32, times the row factor and the
-// column scale. No int8 -> bf16 conversion, and Q8_T MFMAs of 8 passes per
-// k-step against six for three bf16 terms.
-template <int BM, int BN, int NS>
+// stay int8 in LDS, and each 64-wide k-step runs one v_mfma_i32_16x16x64_i8
+// per term and 16 x 16 tile, exact int32 sums per term. The rows arrive in
+// 1 KiB blocks of 16 rows x 64 k in MFMA lane order (lane (g, r): row r, k
+// 8g .. 8g + 7 and 32 + 8g .. +7), so each copy instruction moves one
+// contiguous block and each fragment read is one conflict-free 16-byte LDS
+// read per lane. The weights are either the same blocks (WB: the swizzled
+// copy of launch_swizzle_w) or row-major [N][K] (64-byte LDS rows, the int8
+// XOR swizzle; lane (g, r) reads the two 8-byte halves of row r at k 8g and
+// 32 + 8g); both pair the same k as the rows' fragments. Rows of 64 bytes fill half a cache line
+// per copy lane; whole blocks fill full lines, which measured 25-30 % faster
+// at the prefill shapes. The epilogue forms ((s0 + s1/2^7) + s2/2^14) +
+// s3/2^21 in f32, times the row factor and the column scale. No int8 -> bf16
+// conversion, and Q8_T MFMAs of 8 passes per k-step against six for three
+// bf16 terms.
+template <int BM, int BN, int NS, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_i8_kernel(GemmParams p) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 16, TN = WN / 16;
-    constexpr int ROW = 64;  // bytes of an LDS row (64 k of int8)
-    constexpr int A_BYTES = Q8_T * BM * ROW, B_BYTES = BN * ROW;
+    constexpr int ROW = 64;  // bytes of a row-major W row in LDS (64 k of int8)
+    constexpr int ABLK = Q8_T * BM / 16;  // 1 KiB blocks of A per k-step
+    constexpr int A_BYTES = ABLK * 1024, B_BYTES = BN * ROW;
     constexpr int STAGE = A_BYTES + B_BYTES;
     constexpr int C_LD = WN + 4;
     constexpr int C_BYTES = 4 * 16 * C_LD * 4;
     constexpr int SMEM = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
-    constexpr int A_INS = A_BYTES / 1024 / 4, B_INS = B_BYTES / 1024 / 4;  // per wave per step
-    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copy instructions per wave");
+    constexpr int A_INS = ABLK / 4, B_INS = B_BYTES / 1024 / 4;  // per wave per step
+    static_assert(ABLK % 4 == 0 && B_BYTES % 4096 == 0, "copy instructions per wave");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -287,26 +295,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int kb0 = (int)blockIdx.z * nkt / ksl;
     const int nk = ((int)blockIdx.z + 1) * nkt / ksl - kb0;
 
-    // copy plan: each instruction fills 16 rows x 64 B of LDS; lane i brings
-    // piece (i & 3) ^ ((R >> 1) & 3) of row R = 16 * instr + i / 4
+    // copy plan: A block blk = term blk / (BM / 16), row tile blk % (BM / 16)
+    // of this tile (the planes are p.tstride bytes apart, row tiles nkt KiB);
+    // W blocks of the swizzled copy, or 16 rows x 64 B of row-major W per
+    // instruction with lane i bringing piece (i & 3) ^ ((R >> 1) & 3) of row
+    // R = 16 * instr + i / 4
     const uint8_t *a_src[A_INS];
     const uint8_t *b_src[B_INS];
 #pragma unroll
     for (int q = 0; q < A_INS; ++q) {
-        const int rowg = (q * 4 + wave) * 16 + (lane >> 2);  // over the Q8_T*BM rows
-        const int t = rowg / BM, R = rowg % BM;
-        const int c = (lane & 3) ^ ((R >> 1) & 3);
-        int gm = m0 + R;
-        gm = gm < p.M ? gm : p.M - 1;
-        a_src[q] = (const uint8_t *)(p.A8 + t * p.tstride + (size_t)gm * p.lda) + c * 16;
+        const int blk = q * 4 + wave, t = blk / (BM / 16), i = blk % (BM / 16);
+        a_src[q] = (const uint8_t *)p.A8 + t * p.tstride +
+                   ((size_t)(m0 / 16 + i) * nkt) * 1024 + lane * 16;
     }
 #pragma unroll
     for (int q = 0; q < B_INS; ++q) {
-        const int R = (q * 4 + wave) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((R >> 1) & 3);
-        int gn = n0 + R;
-        gn = gn < p.N ? gn : p.N - 1;
-        b_src[q] = p.W + (size_t)gn * p.K + c * 16;
+        if constexpr (WB) {
+            int tn = n0 / 16 + q * 4 + wave;
+            tn = tn < p.N / 16 ? tn : p.N / 16 - 1;
+            b_src[q] = p.W + ((size_t)tn * nkt) * 1024 + lane * 16;
+        } else {
+            const int R = (q * 4 + wave) * 16 + (lane >> 2);
+            const int c = (lane & 3) ^ ((R >> 1) & 3);
+            int gn = n0 + R;
+            gn = gn < p.N ? gn : p.N - 1;
+            b_src[q] = p.W + (size_t)gn * p.K + c * 16;
+        }
     }
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
     auto issue = [&](int kt) {
@@ -314,10 +328,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
 #pragma unroll
         for (int q = 0; q < A_INS; ++q)
-            dma16(a_src[q] + (size_t)kc * ROW, sb + (q * 4 + wave) * 1024);
+            dma16(a_src[q] + (size_t)kc * 1024, sb + (q * 4 + wave) * 1024);
 #pragma unroll
         for (int q = 0; q < B_INS; ++q)
-            dma16(b_src[q] + (size_t)kc * ROW, sb + A_BYTES + (q * 4 + wave) * 1024);
+            dma16(b_src[q] + (size_t)kc * (WB ? 1024 : ROW), sb + A_BYTES + (q * 4 + wave) * 1024);
     };
 
     gi32x4 acc[Q8_T][TM][TN];
@@ -333,16 +347,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         gi32x4 bf[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int R = wn * WN + j * 16 + r;
-            bf[j] = *(const gi32x4 *)(sB + R * ROW + ((g ^ ((R >> 1) & 3)) * 16));
+            if constexpr (WB) {
+                bf[j] = *(const gi32x4 *)(sB + (wn * TN + j) * 1024 + lane * 16);
+            } else {  // k 8g .. 8g + 7 (in piece g / 2) and 32 + 8g .. (piece 2 + g / 2)
+                const int R = wn * WN + j * 16 + r, sw = (R >> 1) & 3;
+                const uint2 lo = *(const uint2 *)(sB + R * ROW + (((g >> 1) ^ sw) * 16) + (g & 1) * 8);
+                const uint2 hi =
+                    *(const uint2 *)(sB + R * ROW + (((2 + (g >> 1)) ^ sw) * 16) + (g & 1) * 8);
+                bf[j] = gi32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
         }
 #pragma unroll
         for (int t = 0; t < Q8_T; ++t)
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const int R = wm * WM + i * 16 + r;
                 const gi32x4 af =
-                    *(const gi32x4 *)(sA + (t * BM + R) * ROW + ((g ^ ((R >> 1) & 3)) * 16));
+                    *(const gi32x4 *)(sA + (t * (BM / 16) + wm * TM + i) * 1024 + lane * 16);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[t][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[t][i][j], 0, 0, 0);
@@ -445,11 +465,14 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
 }
 
 template <int BM, int NS>
-static int launch_i8(const GemmParams &p, int ksl, hipStream_t st) {
+static int launch_i8(const GemmParams &p, bool wb, int ksl, hipStream_t st) {
     constexpr int stage = Q8_T * BM * 64 + 128 * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
     const dim3 grid((p.N + 127) / 128, (p.M + BM - 1) / BM, ksl);
-    gemm_dma_i8_kernel<BM, 128, NS><<<grid, 256, 0, st>>>(p);
+    if (wb)
+        gemm_dma_i8_kernel<BM, 128, NS, true><<<grid, 256, 0, st>>>(p);
+    else
+        gemm_dma_i8_kernel<BM, 128, NS, false><<<grid, 256, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     if (ksl == 1) return VMLM_OK;
     return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
@@ -520,15 +543,16 @@ int launch_gemm_i8_nonfinite_rows(const float *a, int lda, const int8_t *q, int 
 int launch_gemm(const GemmArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.N >= 1, "gemm: empty shape");
     if (a.A8) {  // int8 rows x int8 weights
-        VMLM_GUARD(a.w_int8 && a.a8s && a.K > 0 && a.K % 64 == 0 && a.lda % 16 == 0 &&
-                       ((uintptr_t)a.W & 15) == 0 && ((uintptr_t)a.A8 & 15) == 0 && a.K % 16 == 0,
-                   "gemm (int8 rows): int8 weights, row factors, K %% 64 == 0, 16-byte aligned rows");
+        VMLM_GUARD(a.w_int8 && a.a8s && a.K > 0 && a.K % 64 == 0 && ((uintptr_t)a.W & 15) == 0 &&
+                       ((uintptr_t)a.A8 & 15) == 0 && (!a.w_blocked || a.N % 16 == 0),
+                   "gemm (int8 rows): int8 weights, row factors, K %% 64 == 0, 16-byte aligned "
+                   "operands, whole 16-row weight blocks");
         GemmParams p{};
         p.W = (const uint8_t *)a.W;
         p.scale = a.scale;
         p.C = a.C;
-        p.tstride = (size_t)a.M * a.lda;
-        p.lda = a.lda;
+        p.tstride = q8_rows_tiles((size_t)a.M) * 16 * (size_t)a.K;  // bytes per term plane
+        p.lda = a.K;
         p.M = a.M;
         p.N = a.N;
         p.K = a.K;
@@ -548,8 +572,8 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         // stages (48 KB, 166 VGPRs) keep three workgroups per CU, three
         // stages (72 KB) two: 4 to 8 % faster at the prefill shapes
         switch (ns) {
-        case 2: return launch_i8<64, 2>(p, ksl, st);
-        case 3: return launch_i8<64, 3>(p, ksl, st);
+        case 2: return launch_i8<64, 2>(p, a.w_blocked, ksl, st);
+        case 3: return launch_i8<64, 3>(p, a.w_blocked, ksl, st);
         }
         return fail(VMLM_ERR_UNIMPL, "gemm (int8 rows): %d LDS stages", ns);
     }

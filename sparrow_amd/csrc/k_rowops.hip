@@ -415,14 +415,20 @@ int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int row
 // Rows as the int8 input of the int8-row GEMM: y = x, or with g the RMSNorm
 // y = (x * inv) * g, inv = 1 / sqrt(mean(x^2) + eps) (ops/src/kernels.rs:
 // 1346-1368); then Q8_T int8 terms of y with the row's power-of-two factor
-// (q8_split) into q8 [Q8_T][rows][cols] and q8s[row] = 2^-k. One workgroup
-// of 256 threads per row, 4 columns per thread and pass, cols <= 8192.
-constexpr int RQ_U = 8;
-__global__ __launch_bounds__(256) void rows_q8_kernel(const float *__restrict__ x, int ldx,
-                                                      const float *__restrict__ g, float eps,
-                                                      int cols, int rows,
-                                                      int8_t *__restrict__ q8,
-                                                      float *__restrict__ q8s) {
+// (q8_split), q8s[row] = 2^-k. The terms are written in 1 KiB blocks of 16
+// rows x 64 k in MFMA operand order (the layout of launch_rows_q8), so that
+// the GEMM copies each block into LDS with one contiguous 16-byte-per-lane
+// load. Two launches: rows_q8_stats_kernel (one workgroup per row) finds inv
+// and the factor, rows_q8_terms_kernel (one workgroup per 16 rows x 32 lane
+// pieces) forms y again with the same operations and writes the terms, the
+// 16 threads of a piece index writing 256 contiguous bytes of a block.
+// Lane piece p of a row: k-block p / 4, lane group g = p % 4, values
+// k = 64 (p / 4) + 8 g + 0..7 and 64 (p / 4) + 32 + 8 g + 0..7.
+constexpr int RQ_U = 8;  // 4-column groups per thread in the stats kernel (cols <= 8192)
+__global__ __launch_bounds__(256) void rows_q8_stats_kernel(const float *__restrict__ x, int ldx,
+                                                            const float *__restrict__ g, float eps,
+                                                            int cols, float *__restrict__ inv_out,
+                                                            float *__restrict__ q8s) {
     __shared__ float sh[4];
     const int row = blockIdx.x, n4 = cols >> 2;
     const float4 *xr = (const float4 *)(x + (size_t)row * ldx);
@@ -434,9 +440,10 @@ __global__ __launch_bounds__(256) void rows_q8_kernel(const float *__restrict__ 
         v[u] = c < n4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
         ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
     }
+    float inv = 1.0f;
     if (g) {
         ss = block_sum256(ss, sh);
-        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+        inv = 1.0f / sqrtf(ss / (float)cols + eps);
 #pragma unroll
         for (int u = 0; u < RQ_U; ++u) {
             const int c = threadIdx.x + u * 256;
@@ -451,33 +458,84 @@ __global__ __launch_bounds__(256) void rows_q8_kernel(const float *__restrict__ 
     for (int u = 0; u < RQ_U; ++u)
         mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(v[u].x), q8_mag(v[u].y)), fmaxf(q8_mag(v[u].z), q8_mag(v[u].w))));
     mx = block_max256(mx, sh);
-    const int k = q8_row_k(mx);
-    if (threadIdx.x == 0) q8s[row] = q8_factor(k);
-#pragma unroll
-    for (int u = 0; u < RQ_U; ++u) {
-        const int c = threadIdx.x + u * 256;
-        if (c >= n4) continue;
-        int a[4][Q8_T];
-        q8_split(v[u].x, k, a[0]);
-        q8_split(v[u].y, k, a[1]);
-        q8_split(v[u].z, k, a[2]);
-        q8_split(v[u].w, k, a[3]);
-#pragma unroll
-        for (int t = 0; t < Q8_T; ++t)
-            *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + 4 * c) =
-                pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+    if (threadIdx.x == 0) {
+        q8s[row] = q8_factor(q8_row_k(mx));
+        inv_out[row] = inv;
     }
+}
+
+constexpr int RQ_J = 32;  // lane pieces per terms workgroup (16 rows each)
+__global__ __launch_bounds__(16 * RQ_J) void rows_q8_terms_kernel(
+    const float *__restrict__ x, int ldx, const float *__restrict__ g, int cols, int rows,
+    int row_tiles, const float *__restrict__ inv_in, const float *__restrict__ q8s,
+    int8_t *__restrict__ q8) {
+    const int t = threadIdx.x, r = t & 15;
+    const int row = (int)blockIdx.x * 16 + r, pc = (int)blockIdx.y * RQ_J + (t >> 4);
+    const int npc = cols >> 4, nkb = cols >> 6;
+    if (pc >= npc) return;
+    const bool live = row < rows;
+    const int rowc = live ? row : rows - 1;
+    const float *xr = x + (size_t)rowc * ldx;
+    const int k0 = (pc >> 2) * 64 + 8 * (pc & 3);
+    float v[16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float4 a = *(const float4 *)(xr + k0 + 32 * h);
+        const float4 b = *(const float4 *)(xr + k0 + 32 * h + 4);
+        v[8 * h + 0] = a.x, v[8 * h + 1] = a.y, v[8 * h + 2] = a.z, v[8 * h + 3] = a.w;
+        v[8 * h + 4] = b.x, v[8 * h + 5] = b.y, v[8 * h + 6] = b.z, v[8 * h + 7] = b.w;
+    }
+    if (g) {  // the stats kernel's operations: (x * inv) * g
+        const float inv = inv_in[rowc];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 ga = *(const float4 *)(g + k0 + 32 * h);
+            const float4 gb = *(const float4 *)(g + k0 + 32 * h + 4);
+            const float e[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[8 * h + i] = v[8 * h + i] * inv * e[i];
+        }
+    }
+    // the row's k from its factor 2^-k (NaN: a non-finite row)
+    const float f = q8s[rowc];
+    const int k = f == f ? -ilogbf(f) : Q8_NONFINITE;
+    uint32_t w[Q8_T][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        int a[4][Q8_T];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q8_split(live ? v[4 * q + e] : 0.0f, k, a[e]);
+#pragma unroll
+        for (int tt = 0; tt < Q8_T; ++tt) w[tt][q] = pack_i8x4(a[0][tt], a[1][tt], a[2][tt], a[3][tt]);
+    }
+    const size_t plane = (size_t)row_tiles * cols * 16;
+    const size_t off = ((size_t)blockIdx.x * nkb + (pc >> 2)) * 1024 + (size_t)((pc & 3) * 16 + r) * 16;
+#pragma unroll
+    for (int tt = 0; tt < Q8_T; ++tt)
+        *(u32x4 *)(q8 + tt * plane + off) = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
+}
+
+size_t q8_rows_tiles(size_t rows) { return (rows + 63) / 64 * 4; }
+// the term planes, then one float per row (inv of the RMSNorm, kept between
+// the two launches)
+size_t q8_rows_bytes(size_t rows, size_t cols) {
+    return (size_t)Q8_T * q8_rows_tiles(rows) * 16 * cols + q8_rows_tiles(rows) * 16 * sizeof(float);
 }
 
 int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
                    int8_t *q8, float *q8s, hipStream_t st) {
     if (rows == 0) return VMLM_OK;
-    VMLM_GUARD(cols % 16 == 0 && cols <= 4 * 256 * RQ_U && ldx % 4 == 0 &&
-                   ((uintptr_t)x & 15) == 0 && (!g || ((uintptr_t)g & 15) == 0) &&
+    VMLM_GUARD(cols % 64 == 0 && cols >= 64 && cols <= 4 * 256 * RQ_U && ldx % 4 == 0 &&
+                   ldx >= cols && ((uintptr_t)x & 15) == 0 && (!g || ((uintptr_t)g & 15) == 0) &&
                    ((uintptr_t)q8 & 15) == 0 && q8s && rows <= 0x7fffffff,
-               "rows_q8: cols %% 16 == 0, cols <= %d, 16-byte aligned rows", 4 * 256 * RQ_U);
-    rows_q8_kernel<<<(unsigned)rows, 256, 0, st>>>(x, (int)ldx, g, eps, (int)cols, (int)rows, q8,
-                                                   q8s);
+               "rows_q8: cols %% 64 == 0, 64 <= cols <= %d, 16-byte aligned rows", 4 * 256 * RQ_U);
+    const size_t tiles = q8_rows_tiles(rows);
+    float *inv = (float *)(q8 + (size_t)Q8_T * tiles * 16 * cols);
+    rows_q8_stats_kernel<<<(unsigned)rows, 256, 0, st>>>(x, (int)ldx, g, eps, (int)cols, inv, q8s);
+    VMLM_HIP_CHECK(hipGetLastError());
+    const dim3 grid((unsigned)((rows + 15) / 16), (unsigned)((cols / 16 + RQ_J - 1) / RQ_J));
+    rows_q8_terms_kernel<<<grid, 16 * RQ_J, 0, st>>>(x, (int)ldx, g, (int)cols, (int)rows,
+                                                     (int)tiles, inv, q8s, q8);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

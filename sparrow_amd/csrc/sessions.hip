@@ -6,7 +6,11 @@
 //   weights per layer  [Wqkv 3H x H | Wo H x H | Wgu 2I x H | Wd H x I] int8
 //                      Wqkv = rows of q, k, v concatenated; Wgu interleaves
 //                      16-row blocks of gate and up so one GEMV workgroup owns
-//                      the gate and up rows of the same 16 outputs.
+//                      the gate and up rows of the same 16 outputs. Held once,
+//                      swizzled into 1 KiB blocks of 16 rows x 64 k in MFMA
+//                      operand order (launch_swizzle_w), which the decode
+//                      GEMVs and the prefill GEMMs both read; the row-major
+//                      form passes through a one-layer staging buffer at load.
 //   scales per layer   [sqkv 3H | so H | sgu 2I (same interleave) | sd H] f32
 //   norms per layer    [in_ln H | post_ln H] f32
 //   KV cache           [layer][seq][head][cap][64] f32, rotated K and raw V
@@ -120,8 +124,8 @@ struct vmlm_decoder {
     hipStream_t st = nullptr;
     size_t H = 0, I = 0, NH = 0, V = 0, B = 0, cap = 0, L = 0;
     size_t w_layer = 0, s_layer = 0;  // per-layer element counts
-    int8_t *w = nullptr;
-    int8_t *wsw = nullptr;  // the same weights in MFMA-operand order (decode GEMVs)
+    int8_t *wstage = nullptr;  // one layer's row-major weights, swizzled into wsw at load
+    int8_t *wsw = nullptr;     // the weights in MFMA-operand order (every projection)
     float *ssp = nullptr;   // fused path: RMSNorm partial sums of squares [H/16][B]
     bool fused = false;     // five-launch layers of full-K fused GEMVs (batch <= 5)
     float *s = nullptr, *norms = nullptr;
@@ -155,9 +159,8 @@ struct vmlm_decoder {
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
 
-    // swizzled copy at the same offsets
-    const int8_t *Sw(const int8_t *p) const { return wsw + (p - w); }
-    const int8_t *Wqkv(size_t l) const { return w + l * w_layer; }
+    // layer l's projections in the swizzled copy ([N/16][K/64][1 KiB] blocks)
+    const int8_t *Wqkv(size_t l) const { return wsw + l * w_layer; }
     const int8_t *Wo(size_t l) const { return Wqkv(l) + 3 * H * H; }
     const int8_t *Wgu(size_t l) const { return Wo(l) + H * H; }
     const int8_t *Wd(size_t l) const { return Wgu(l) + 2 * I * H; }
@@ -217,7 +220,7 @@ int enqueue_head(vmlm_decoder *d, bool record) {
 // reduces them in slice order and applies the row scales.
 KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int K) {
     KsArgs g;
-    g.W = d->Sw(W);
+    g.W = W;
     if (A == d->t_x) {  // the normed rows enter as int8 rows
         g.A8 = d->x8;
         g.a8s = d->x8s;
@@ -334,23 +337,23 @@ FkArgs fk_args(vmlm_decoder *d, size_t l, int which) {
     f.nssp = H / 16;
     switch (which) {
     case 0:
-        f.W = d->Sw(d->Wqkv(l)), f.scale = d->Sqkv(l), f.N = 3 * H, f.K = H;
+        f.W = d->Wqkv(l), f.scale = d->Sqkv(l), f.N = 3 * H, f.K = H;
         f.A = d->t_x, f.ssp = d->ssp;
         f.Y = d->qkv, f.ldy = 3 * H, f.epi = FK_STORE;
         break;
     case 1:
-        f.W = d->Sw(d->Wo(l)), f.scale = d->So(l), f.N = H, f.K = H;
+        f.W = d->Wo(l), f.scale = d->So(l), f.N = H, f.K = H;
         f.A = d->t_att;
         f.Y = d->h2, f.ldy = H, f.epi = FK_RESID, f.R = d->h, f.ldr = H;
         f.Aout = d->t_x, f.gout = d->PostLn(l), f.ssp_out = d->ssp;
         break;
     case 2:
-        f.W = d->Sw(d->Wgu(l)), f.scale = d->Sgu(l), f.N = 2 * I, f.K = H;
+        f.W = d->Wgu(l), f.scale = d->Sgu(l), f.N = 2 * I, f.K = H;
         f.A = d->t_x, f.ssp = d->ssp;
         f.ldy = I, f.epi = FK_SILU, f.Aout = d->t_act;
         break;
     default:
-        f.W = d->Sw(d->Wd(l)), f.scale = d->Sd(l), f.N = H, f.K = I;
+        f.W = d->Wd(l), f.scale = d->Sd(l), f.N = H, f.K = I;
         f.A = d->t_act;
         f.Y = d->h, f.ldy = H, f.epi = FK_RESID, f.R = d->h2, f.ldr = H;
         f.Aout = d->t_x, f.gout = l + 1 < d->L ? d->InLn(l + 1) : d->final_norm;
@@ -460,7 +463,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
     if (e != hipSuccess) return cleanup(hip_fail(e, "decoder stream"));
     d->hs = d->cap + 1;
     const size_t kvn = d->L * d->B * d->NH * d->hs * 64;
-    if ((rc = dalloc(d, &d->w, d->L * d->w_layer)) || (rc = dalloc(d, &d->s, d->L * d->s_layer)) ||
+    if ((rc = dalloc(d, &d->wstage, d->w_layer)) || (rc = dalloc(d, &d->s, d->L * d->s_layer)) ||
         (rc = dalloc(d, &d->norms, d->L * 2 * d->H)) || (rc = dalloc(d, &d->embed, d->V * d->H)) ||
         (rc = dalloc(d, &d->lm_head, d->V * d->H)) || (rc = dalloc(d, &d->final_norm, d->H)) ||
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
@@ -512,7 +515,7 @@ int vmlm_decoder_load_layer(vmlm_decoder *d, uint32_t layer, const int8_t *wq, c
                             const float *in_ln, const float *post_ln) {
     VMLM_GUARD(d && layer < d->L, "decoder: layer %u out of range", layer);
     const size_t H = d->H, I = d->I, l = layer;
-    int8_t *W = d->w + l * d->w_layer;
+    int8_t *W = d->wstage;  // stream-ordered: the previous layer's swizzles have read it
     float *S = d->s + l * d->s_layer;
     hipStream_t st = d->st;
     auto h2d = [&](void *dst, const void *src, size_t bytes) {
@@ -533,7 +536,7 @@ int vmlm_decoder_load_layer(vmlm_decoder *d, uint32_t layer, const int8_t *wq, c
                               hipMemcpyHostToDevice, st)) != hipSuccess)
         return hip_fail(e, "load_layer gate/up");
     H2D(Wgu + 2 * I * H, wd, H * I);
-    {  // the decode GEMVs' copy in MFMA-operand order
+    {  // the copy in MFMA-operand order that every projection reads
         int rc;
         if ((rc = launch_swizzle_w(W, d->wsw + l * d->w_layer, (int)(3 * H), (int)H, st)) ||
             (rc = launch_swizzle_w(W + 3 * H * H, d->wsw + l * d->w_layer + 3 * H * H, (int)H,
@@ -610,7 +613,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     };
     if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
         (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) || (rc = get(&gu, M * 2 * I * 4)) ||
-        (rc = get(&act, M * I * 4)) || (rc = get(&a8, (size_t)Q8_T * M * I)) ||
+        (rc = get(&act, M * I * 4)) || (rc = get(&a8, q8_rows_bytes(M, std::max(H, I)))) ||
         (rc = get(&a8s, M * 4)) ||
         (rc = get(&toks, M * 4)) ||
         (rc = get(&kvw, attention_prefill_work_bytes((int)S, (int)NH, (int)B)))) {
@@ -634,6 +637,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             if ((r = launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st))) return r;
             GemmArgs g;
             g.W = d->Wqkv(l);
+            g.w_blocked = true;
             g.scale = d->Sqkv(l);
             g.A8 = a8;
             g.a8s = a8s;
