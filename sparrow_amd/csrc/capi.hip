@@ -10,6 +10,7 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -335,11 +336,18 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         float *a8s = stg.template alloc<float>(m);
         const size_t gw = gemm_i8_work_floats((int)m, (int)n, (int)k);
         float *gwork = gw ? stg.template alloc<float>(gw) : nullptr;
+        // many rows: the weights swizzled into 1 KiB blocks first (one pass
+        // over N x K bytes), so the GEMM's weight copies move whole blocks;
+        // the allocation-free entry point keeps its scratch for the rows
+        const bool blk = std::is_same<WS, Stage>::value && m >= 256 && n % 16 == 0;
+        int8_t *wsw = blk ? stg.template alloc<int8_t>(n * k) : nullptr;
         STAGE_OK(stg);
         int rc = launch_rows_q8(a, k, nullptr, 0.0f, m, k, a8, a8s, st);
         if (rc) return rc;
+        if (blk && (rc = launch_swizzle_w((const int8_t *)Wd, wsw, (int)n, (int)k, st))) return rc;
         GemmArgs g;
-        g.W = Wd;
+        g.W = blk ? (const void *)wsw : Wd;
+        g.w_blocked = blk;
         g.w_int8 = true;
         g.scale = scale;
         g.A8 = a8;
