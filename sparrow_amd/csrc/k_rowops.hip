@@ -418,19 +418,43 @@ int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int row
 // (q8_split), q8s[row] = 2^-k. The terms are written in 1 KiB blocks of 16
 // rows x 64 k in MFMA operand order (the layout of launch_rows_q8), so that
 // the GEMM copies each block into LDS with one contiguous 16-byte-per-lane
-// load. Two launches: rows_q8_stats_kernel (one workgroup per row) finds inv
-// and the factor, rows_q8_terms_kernel (one workgroup per 16 rows x 32 lane
-// pieces) forms y again with the same operations and writes the terms, the
-// 16 threads of a piece index writing 256 contiguous bytes of a block.
-// Lane piece p of a row: k-block p / 4, lane group g = p % 4, values
-// k = 64 (p / 4) + 8 g + 0..7 and 64 (p / 4) + 32 + 8 g + 0..7.
+// load. Lane piece p of a row: k-block p / 4, lane group g = p % 4, values
+// k = 64 (p / 4) + 8 g + 0..7 and 64 (p / 4) + 32 + 8 g + 0..7; rows past
+// the last (to the tile count) hold zero terms.
+// Many rows: two launches. rows_q8_stats_kernel (one workgroup per row) finds
+// inv and the factor, rows_q8_terms_kernel (one workgroup per 16 rows x 32
+// lane pieces) forms y again with the same operations and writes the terms,
+// the 16 threads of a piece index writing 256 contiguous bytes of a block.
+// Few rows (RQ_ONE_MAX or fewer): rows_q8_stats_kernel<true> alone, one
+// workgroup per row that also writes its row's terms (4 bytes of a lane
+// piece per store), which saves the second launch where the grid is small.
+// Both give the same bits: the same sums in the same order.
 constexpr int RQ_U = 8;  // 4-column groups per thread in the stats kernel (cols <= 8192)
-__global__ __launch_bounds__(256) void rows_q8_stats_kernel(const float *__restrict__ x, int ldx,
-                                                            const float *__restrict__ g, float eps,
-                                                            int cols, float *__restrict__ inv_out,
-                                                            float *__restrict__ q8s) {
+constexpr size_t RQ_ONE_MAX = 256;
+template <bool TERMS>
+__global__ __launch_bounds__(256) void rows_q8_stats_kernel(
+    const float *__restrict__ x, int ldx, const float *__restrict__ g, float eps, int cols,
+    int rows, int row_tiles, float *__restrict__ inv_out, float *__restrict__ q8s,
+    int8_t *__restrict__ q8) {
     __shared__ float sh[4];
     const int row = blockIdx.x, n4 = cols >> 2;
+    // byte offset in a term plane of the 4 terms of columns 4c..4c+3
+    auto term_off = [&](int c) {
+        const int kk = 4 * c, w = kk & 63;
+        return ((size_t)(row >> 4) * (cols >> 6) + (kk >> 6)) * 1024 +
+               (size_t)((((w & 31) >> 3) * 16 + (row & 15)) * 16 + (w >> 5) * 8 + (w & 4));
+    };
+    const size_t plane = (size_t)row_tiles * cols * 16;
+    if (TERMS && row >= rows) {  // a row past the last: zero terms
+#pragma unroll
+        for (int u = 0; u < RQ_U; ++u) {
+            const int c = threadIdx.x + u * 256;
+            if (c >= n4) continue;
+#pragma unroll
+            for (int tt = 0; tt < Q8_T; ++tt) *(uint32_t *)(q8 + tt * plane + term_off(c)) = 0u;
+        }
+        return;
+    }
     const float4 *xr = (const float4 *)(x + (size_t)row * ldx);
     float4 v[RQ_U];
     float ss = 0.0f;
@@ -458,9 +482,26 @@ __global__ __launch_bounds__(256) void rows_q8_stats_kernel(const float *__restr
     for (int u = 0; u < RQ_U; ++u)
         mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(v[u].x), q8_mag(v[u].y)), fmaxf(q8_mag(v[u].z), q8_mag(v[u].w))));
     mx = block_max256(mx, sh);
+    const int k = q8_row_k(mx);
     if (threadIdx.x == 0) {
-        q8s[row] = q8_factor(q8_row_k(mx));
-        inv_out[row] = inv;
+        q8s[row] = q8_factor(k);
+        if (!TERMS) inv_out[row] = inv;
+    }
+    if constexpr (TERMS) {
+#pragma unroll
+        for (int u = 0; u < RQ_U; ++u) {
+            const int c = threadIdx.x + u * 256;
+            if (c >= n4) continue;
+            int a[4][Q8_T];
+            q8_split(v[u].x, k, a[0]);
+            q8_split(v[u].y, k, a[1]);
+            q8_split(v[u].z, k, a[2]);
+            q8_split(v[u].w, k, a[3]);
+            const size_t off = term_off(c);
+#pragma unroll
+            for (int tt = 0; tt < Q8_T; ++tt)
+                *(uint32_t *)(q8 + tt * plane + off) = pack_i8x4(a[0][tt], a[1][tt], a[2][tt], a[3][tt]);
+        }
     }
 }
 
@@ -530,8 +571,15 @@ int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t
                    ((uintptr_t)q8 & 15) == 0 && q8s && rows <= 0x7fffffff,
                "rows_q8: cols %% 64 == 0, 64 <= cols <= %d, 16-byte aligned rows", 4 * 256 * RQ_U);
     const size_t tiles = q8_rows_tiles(rows);
+    if (rows <= RQ_ONE_MAX) {
+        rows_q8_stats_kernel<true><<<(unsigned)(tiles * 16), 256, 0, st>>>(
+            x, (int)ldx, g, eps, (int)cols, (int)rows, (int)tiles, nullptr, q8s, q8);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     float *inv = (float *)(q8 + (size_t)Q8_T * tiles * 16 * cols);
-    rows_q8_stats_kernel<<<(unsigned)rows, 256, 0, st>>>(x, (int)ldx, g, eps, (int)cols, inv, q8s);
+    rows_q8_stats_kernel<false><<<(unsigned)rows, 256, 0, st>>>(
+        x, (int)ldx, g, eps, (int)cols, (int)rows, (int)tiles, inv, q8s, q8);
     VMLM_HIP_CHECK(hipGetLastError());
     const dim3 grid((unsigned)((rows + 15) / 16), (unsigned)((cols / 16 + RQ_J - 1) / RQ_J));
     rows_q8_terms_kernel<<<grid, 16 * RQ_J, 0, st>>>(x, (int)ldx, g, (int)cols, (int)rows,

@@ -105,3 +105,31 @@ def test_gemm_int8_three_terms(dev, oracle, m, n, k):
     ref = (a.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
     assert_close_rms(got, ref)
     assert_close_rms(got, oracle.gemm_nt_int8(a, q, s))
+
+
+def test_gemm_int8_row_split_paths_agree(dev):
+    """Up to 256 rows are split into int8 terms by one launch (stats and terms
+    per row), more rows by a stats launch and a blocked terms launch. Both
+    form the same sums in the same order, so rows 0..255 of a 256-row and a
+    257-row call give the same bits (N = 8192: neither call is k-sliced).
+    Rows of mixed magnitude, a zero row and a NaN row are among them."""
+    m, n, k = 257, 8192, 512
+    rng = np.random.default_rng(257)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    a *= np.float32(10.0) ** rng.integers(-6, 7, size=(m, 1)).astype(np.float32)
+    a[5] = 0.0
+    a[17, 3] = np.nan
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
+    da, dq, ds = dev.up(a), dev.up(q), dev.up(s)
+    c256, c257 = dev.empty(256 * n * 4), dev.empty(m * n * 4)
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, c256, 256, n, k, None))
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, c257, m, n, k, None))
+    g256 = dev.down(c256, (256, n), np.float32)
+    g257 = dev.down(c257, (m, n), np.float32)
+    assert np.isnan(g256[17]).all() and (g256[5] == 0).all()
+    np.testing.assert_array_equal(g256.view(np.uint32), g257[:256].view(np.uint32))
+    ref = (a.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    ok = np.isfinite(ref).all(axis=1)
+    for r in np.flatnonzero(ok)[:40]:
+        assert_close_rms(g257[r], ref[r])
