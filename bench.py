@@ -179,6 +179,7 @@ def host_cpu():
 PEAK_BF16_TFLOPS = 2500.0   # dense MFMA bf16
 PEAK_FP32_TFLOPS = 157.3    # FP32
 PEAK_INT8_TOPS = 5000.0     # dense MFMA int8
+Q8_TERMS = 3                # int8 terms per f32 activation in the int8-row path (Q8_T)
 
 
 _LAST = ["eager"]  # how the last _timed call measured the GPU time
@@ -333,9 +334,9 @@ def run_suite(iters, cpu=True):
         pre[name] = {"us": round(usp, 2), "host_us": round(wallp, 2), "timing": _LAST[0],
                      "useful_TOPs": round(useful, 1),
                      "frac_int8_peak_useful": round(useful / PEAK_INT8_TOPS, 4),
-                     "frac_int8_peak_issued": round(4 * useful / PEAK_INT8_TOPS, 4)}
-    pre["note"] = ("per call: rows_q8 + gemm_dma_i8_kernel + non-finite-row check; issued = 4 int8 "
-                   "MFMAs per product (four terms per activation)")
+                     "frac_int8_peak_issued": round(Q8_TERMS * useful / PEAK_INT8_TOPS, 4)}
+    pre["note"] = (f"per call: rows_q8 + gemm_dma_i8_kernel + non-finite-row check; issued = "
+                   f"{Q8_TERMS} int8 MFMAs per product ({Q8_TERMS} int8 terms per activation)")
     out["cfg3_prefill_gemm"] = pre
     if orc:
         af = orc.bf16_to_f32(a)

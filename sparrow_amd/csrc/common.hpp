@@ -113,21 +113,25 @@ __device__ __forceinline__ void i8x16_to_bf16(u32x4 w, u32x4 &lo, u32x4 &hi) {
 }
 
 // ------------------------------------------------------------------ int8 rows
-// An f32 row y enters the int8 MFMA as four int8 terms with one power-of-two
-// scale 2^k per row: the largest k with m * 2^k <= 127, m = max|y| or a bound
-// on it within a few ulps. With u = y * 2^k (exact), a0 = rint(u), then each
-// further term is rint of the remainder times 128, so
-// u = a0 + a1/2^7 + a2/2^14 + a3/2^21 + e with |e| <= 2^-22: 28 bits below the
-// row maximum (f32 carries 24). |a0| <= 127, |a1..a3| <= 64; every step is
+// An f32 row y enters the int8 MFMA as Q8_T = 3 int8 terms with one
+// power-of-two scale 2^k per row: the largest k with m * 2^k <= 127,
+// m = max|y| or a bound on it within a few ulps. With u = y * 2^k (exact),
+// a0 = rint(u), then each further term is rint of the remainder times 128, so
+// u = a0 + a1/2^7 + a2/2^14 + e with |e| <= 2^-15: every value to within
+// 2^-21 of the row maximum. |a0| <= 127, |a1|, |a2| <= 64; every step is
 // exact in f32. k is clamped to [-126, 126] (rows whose maximum is below
-// 2^-120 keep fewer bits).
+// 2^-120 keep fewer bits). The error this adds to a dot product over K
+// values is about 2^-21 * max|y| * sqrt(K) * rms(w), against the
+// 1e-4 * RMS(C) contract of gemm_nt_int8: a row's maximum would have to be
+// some 400 times its RMS to reach it. A fourth term (28 bits) gave the same
+// greedy tokens and costs a third more MFMAs and row bytes.
 //
 // Non-finite rows: the magnitude used for the maximum maps NaN to +inf
 // (q8_mag; fmaxf alone would drop a NaN), a non-finite maximum gives
 // k = Q8_NONFINITE, whose factor is NaN and whose terms are 0. Every output
 // of such a row is then NaN, never a finite value. (The standalone GEMM
 // recomputes those rows in f32 to give the exact +-inf / NaN pattern.)
-constexpr int Q8_T = 4;
+constexpr int Q8_T = 3;
 constexpr int Q8_NONFINITE = 0x4000;
 __device__ __forceinline__ float q8_mag(float y) {
     const float a = fabsf(y);
@@ -157,6 +161,10 @@ __device__ __forceinline__ void q8_split(float y, int k, int (&a)[Q8_T]) {
         a[t] = (int)r;
         u = (u - r) * 128.0f;
     }
+}
+// the weight 2^-7t of term t's sum when the terms are combined in f32
+__device__ __forceinline__ constexpr float q8_term_weight(int t) {
+    return t == 1 ? 0.0078125f : t == 2 ? 6.103515625e-05f : 4.76837158203125e-07f;
 }
 // packs the bytes of four ints (low bytes) into one dword
 __device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {

@@ -312,7 +312,7 @@ constexpr int KS_SSP_MAX = 16;  // k-slices whose segment sums are read up front
 // block and term one v_mfma_i32_16x16x64_i8 per tile straight on the int8
 // weights (no conversion), accumulated exactly in int32 (|sum| < 2^24 over
 // a slice of at most 6 blocks). The epilogue forms
-// ((s0 + s1 / 2^7) + s2 / 2^14) + s3 / 2^21 in f32, times the row factor:
+// (s0 + s1 / 2^7) + s2 / 2^14 in f32 (q8_term_weight), times the row factor:
 // the slice's segment factor a8s[slice][row], and with ssp the RMSNorm's
 // 1 / sqrt(sum ssp[.][row] / K + eps) (the int8 terms are of x * g).
 // The swizzled weight bytes of lane (g, r) are k = 8g .. +7 and 32 + 8g .. +7
@@ -424,9 +424,8 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float f = (float)acc[t][0][j];
-                f = f + (float)acc[t][1][j] * 0.0078125f;
-                f = f + (float)acc[t][2][j] * 6.103515625e-05f;
-                f = f + (float)acc[t][3][j] * 4.76837158203125e-07f;
+#pragma unroll
+                for (int u = 1; u < Q8_T; ++u) f = f + (float)acc[t][u][j] * q8_term_weight(u);
                 v[j] = f * rowf;
             }
             *(f32x4 *)(yr + tl * 16 + 4 * g) = v;

@@ -264,10 +264,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
 // XOR swizzle; lane (g, r) reads the two 8-byte halves of row r at k 8g and
 // 32 + 8g); both pair the same k as the rows' fragments. Rows of 64 bytes fill half a cache line
 // per copy lane; whole blocks fill full lines, which measured 25-30 % faster
-// at the prefill shapes. The epilogue forms ((s0 + s1/2^7) + s2/2^14) +
-// s3/2^21 in f32, times the row factor and the column scale. No int8 -> bf16
-// conversion, and Q8_T MFMAs of 8 passes per k-step against six for three
-// bf16 terms.
+// at the prefill shapes. The epilogue forms (s0 + s1/2^7) + s2/2^14 in f32
+// (q8_term_weight), times the row factor and the column scale. No int8 ->
+// bf16 conversion, and Q8_T MFMAs of 8 passes per k-step against six for
+// three bf16 terms.
 template <int BM, int BN, int NS, bool WB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_i8_kernel(GemmParams p) {
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -391,9 +391,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float f = (float)acc[0][i][j][q];
-                f = f + (float)acc[1][i][j][q] * 0.0078125f;
-                f = f + (float)acc[2][i][j][q] * 6.103515625e-05f;
-                f = f + (float)acc[3][i][j][q] * 4.76837158203125e-07f;
+#pragma unroll
+                for (int t = 1; t < Q8_T; ++t) f = f + (float)acc[t][i][j][q] * q8_term_weight(t);
                 cs[(g * 4 + q) * C_LD + j * 16 + r] = f;
             }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's slab is in LDS

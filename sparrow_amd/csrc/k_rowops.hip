@@ -438,7 +438,7 @@ __global__ __launch_bounds__(256) void rows_q8_stats_kernel(
     int8_t *__restrict__ q8) {
     __shared__ float sh[4];
     const int row = blockIdx.x, n4 = cols >> 2;
-    // byte offset in a term plane of the 4 terms of columns 4c..4c+3
+    // byte offset in a term plane of the terms of columns 4c..4c+3
     auto term_off = [&](int c) {
         const int kk = 4 * c, w = kk & 63;
         return ((size_t)(row >> 4) * (cols >> 6) + (kk >> 6)) * 1024 +
