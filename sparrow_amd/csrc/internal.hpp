@@ -151,6 +151,12 @@ struct GemmArgs {
     // int8 rows, optional: gemm_i8_work_floats() floats for the k-slices of
     // a grid that would leave most CUs idle (null: one slice)
     float *work = nullptr;
+    // int8 rows: the N weight rows are (gate, up) pairs interleaved in blocks
+    // of 16 (rows 32t .. 32t + 15 gate, 32t + 16 .. 32t + 31 up); C receives
+    // act = SiLU(gate) * up [M][N / 2] (column 16t + j from rows 32t + j and
+    // 32t + 16 + j), formed in the epilogue from the scaled results (one
+    // slice; N % 32 == 0)
+    bool silu_pairs = false;
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
 // Recomputes in f32 the rows of an int8-row GEMM whose factor a8s[i] is NaN
@@ -225,12 +231,14 @@ int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const
 // (g, r) = 16 bytes at (16 g + r) * 16: row r, k 8g .. 8g + 7 and 32 + 8g ..
 // 32 + 8g + 7 (the order of the swizzled weights, launch_swizzle_w); then
 // one float per row tile row, used between the two launches. Rows past
-// `rows` in the last 16-row tile are zero terms, later tiles are not
-// written. cols % 64 == 0, cols <= 8192.
+// `rows` in the last 16-row tile are zero terms; later tiles may be left
+// unwritten. cols % 64 == 0, cols <= 8192. With ra and rb (same ldx) the
+// rows are first formed as x = ra + rb and written to x (a residual add).
 size_t q8_rows_tiles(size_t rows);
 size_t q8_rows_bytes(size_t rows, size_t cols);
 int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
-                   int8_t *q8, float *q8s, hipStream_t st);
+                   int8_t *q8, float *q8s, hipStream_t st, const float *ra = nullptr,
+                   const float *rb = nullptr);
 // SiLU(gate) * up from the partials of the interleaved gate/up projection,
 // as int8 terms [Q8_T][rows][I] with a power-of-two
 // factor per segment of `seg` columns, q8s [I/seg][rows] (the input of a
@@ -262,11 +270,14 @@ int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
 // nseq sequences at strides sin / sout. `work` holds
 // attention_prefill_work_bytes(S, H, nseq) bytes (bf16 term planes of K and
 // V); with rope, K is rotated there and Q as it is loaded (positions pos0 + row).
+// With kc and vc (pos0 = 0) the rotated K rows and raw V rows are also written
+// to a KV cache [nseq][H][hs][64] at positions 0 .. S-1.
 size_t attention_prefill_work_bytes(int S, int H, int nseq);
 int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope = false, float rope_step = 0.0f,
-                             float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0);
+                             float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0,
+                             float *kc = nullptr, float *vc = nullptr, int hs = 0);
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;

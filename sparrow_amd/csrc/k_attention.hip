@@ -320,11 +320,14 @@ struct PrefillParams {
 // block with 16-byte copies. One workgroup per (64-row block, head,
 // sequence); thread (row, c) rotates RoPE pairs 2c and 2c + 1 of its Q and K
 // rows with one angle evaluation per pair (Q and K share the position).
+// With kc / vc the rotated K rows and the raw V rows also go to a KV cache
+// [sequence][head][hs][64] f32 at positions 0 .. S-1 (the decoder's prefill).
 struct QKVPrepParams {
     const float *Q, *K, *V;
     uint16_t *Qt, *Kt, *Vt;
+    float *kc, *vc;
     size_t sin;
-    int S, Sp, ld, H, rope;
+    int S, Sp, ld, H, rope, hs;
     float rope_step, pos0;
 };
 __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
@@ -347,6 +350,11 @@ __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
             a = k1.y * co - k2.y * si, b = k1.y * si + k2.y * co, k1.y = a, k2.y = b;
         }
         if (row >= p.S) q1 = q2 = k1 = k2 = make_float2(0.0f, 0.0f);
+        else if (p.kc) {
+            float *kr = p.kc + (((size_t)z * p.H + h) * p.hs + row) * 64 + 2 * c;
+            *(float2 *)kr = k1;
+            *(float2 *)(kr + 32) = k2;
+        }
         const size_t dst = ((size_t)z * 2 * p.H + h) * p.Sp * 64 + (size_t)row * 64 + 2 * c;
         auto put = [&](uint16_t *base, float2 lo, float2 hi) {
             const uint32_t l0 = bf16x2_rne_bits(lo.x, lo.y), h0 = bf16x2_rne_bits(hi.x, hi.y);
@@ -370,6 +378,7 @@ __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
             const float4 x =
                 *(const float4 *)(p.V + z * p.sin + (size_t)min(row, p.S - 1) * p.ld + h * 64 + d0);
             const bool ok = row < p.S;
+            if (ok && p.vc) *(float4 *)(p.vc + (((size_t)z * p.H + h) * p.hs + row) * 64 + d0) = x;
             vs[tid >> 4][d0] = ok ? x.x : 0.0f;
             vs[tid >> 4][d0 + 1] = ok ? x.y : 0.0f;
             vs[tid >> 4][d0 + 2] = ok ? x.z : 0.0f;
@@ -573,11 +582,15 @@ size_t attention_prefill_work_bytes(int S, int H, int nseq) {
 int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope, float rope_step, float pos0, int nseq,
-                             size_t sin, size_t sout) {
+                             size_t sin, size_t sout, float *kc, float *vc, int hs) {
     VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 7) == 0 && ((uintptr_t)k & 7) == 0 &&
                    ((uintptr_t)v & 15) == 0 && (nseq == 1 || sin % 4 == 0),
                "attention prefill: 16-byte aligned V rows and 8-byte aligned Q / K rows "
                "required");
+    VMLM_GUARD(!kc == !vc && (!kc || (hs >= S && pos0 == 0.0f && ((uintptr_t)kc & 15) == 0 &&
+                                      ((uintptr_t)vc & 15) == 0)),
+               "attention prefill: a KV cache needs both rows, hs >= S, position 0 and "
+               "16-byte alignment");
     VMLM_GUARD(nseq >= 1 && nseq <= 65535 && H <= 65535, "attention prefill: grid too large");
     if (S <= 0) return VMLM_OK;
     const int Sp = (S + AT_B - 1) / AT_B * AT_B;
@@ -597,6 +610,9 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
     kp.rope = rope ? 1 : 0;
     kp.rope_step = rope_step;
     kp.pos0 = pos0;
+    kp.kc = kc;
+    kp.vc = vc;
+    kp.hs = hs;
     attn_qkv_prep_kernel<<<dim3(Sp / AT_B, H, nseq), 1024, 0, st>>>(kp);
     VMLM_HIP_CHECK(hipGetLastError());
     PrefillParams P;

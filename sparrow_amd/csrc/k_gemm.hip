@@ -23,6 +23,7 @@ struct GemmParams {
     const float *a8s;   // bytes apart, and row factors [M] (gemm_dma_i8_kernel)
     float *part;        // k-slices > 1: raw sums times the row factor [ks][M][N]
     int group;          // tile order: 0 as dispatched, g > 0 XCD-grouped (gemm_tile)
+    int silu;           // int8 rows: C = SiLU(gate) * up of interleaved pairs (GemmArgs)
 };
 
 // The (N-block, M-block) tile of this workgroup. Workgroups are dispatched
@@ -404,6 +405,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             const int row = m0 + wm * WM + i * 16 + rr_, col = n0 + wn * WN + c4;
             if (row >= p.M || col >= p.N) continue;
             const float rf = p.a8s[row];
+            if (p.silu) {
+                // the slab's 64 columns are two (16 gate, 16 up) pairs: a gate
+                // lane takes its up values 16 columns on, as silu_mul would
+                // read them from C (the same scaled f32 results)
+                if (c4 & 16) continue;
+                const float4 u = *(const float4 *)&cs[rr_ * C_LD + c4 + 16];
+                const float gv[4] = {v.x, v.y, v.z, v.w}, uv[4] = {u.x, u.y, u.z, u.w};
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gate = (gv[e] * rf) * p.scale[col + e];
+                    const float up = (uv[e] * rf) * p.scale[col + 16 + e];
+                    y[e] = act_scalar(gate, VMLM_ACT_SILU) * up;
+                }
+                *(float4 *)(p.C + (size_t)row * p.ldc + (col - 16 * (col >> 5))) =
+                    make_float4(y[0], y[1], y[2], y[3]);
+                continue;
+            }
             float y[4] = {v.x * rf, v.y * rf, v.z * rf, v.w * rf};
             if (p.scale && ksl == 1) {
 #pragma unroll
@@ -546,6 +565,10 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
                        ((uintptr_t)a.A8 & 15) == 0 && (!a.w_blocked || a.N % 16 == 0),
                    "gemm (int8 rows): int8 weights, row factors, K %% 64 == 0, 16-byte aligned "
                    "operands, whole 16-row weight blocks");
+        VMLM_GUARD(!a.silu_pairs || (a.N % 32 == 0 && a.scale && a.ldc % 4 == 0 &&
+                                     a.ldc >= a.N / 2 && ((uintptr_t)a.C & 15) == 0),
+                   "gemm (int8 rows, SiLU pairs): N %% 32 == 0, column scales, 16-byte aligned "
+                   "output rows of at least N / 2");
         GemmParams p{};
         p.W = (const uint8_t *)a.W;
         p.scale = a.scale;
@@ -563,8 +586,9 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         p.a8s = a.a8s;
         // skinny grids: ordered k-slices through `work`, then the in-order
         // slice reduction applies the column scale
-        const int ksl = a.work ? gemm_i8_kslices(a.M, a.N, a.K) : 1;
+        const int ksl = a.work && !a.silu_pairs ? gemm_i8_kslices(a.M, a.N, a.K) : 1;
         p.part = a.work;
+        p.silu = a.silu_pairs ? 1 : 0;
         const int ns = a.stages ? a.stages : 2;
         // 64 x 128 tiles: 128-row tiles need 256 accumulator registers, run one
         // wave per SIMD and measured 30 % slower at the prefill shapes. Two

@@ -81,40 +81,6 @@ __global__ void step_advance_kernel(int *step, int *pos) {
     *pos = *pos + 1;
 }
 
-// Scatter K rotated at its position s (the ROPE of the program, bit for bit)
-// and raw V of prefill rows [b*S + s][...] into the cache.
-__global__ void kv_fill_kernel(const float *__restrict__ qkv, int ldq, int H, int NH, int S,
-                               float *__restrict__ kc, float *__restrict__ vc, int hs, int B,
-                               float step) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t total = (size_t)B * S * NH * 64;
-    if (idx >= total) return;
-    const int d = idx % 64;
-    const int h = (idx / 64) % NH;
-    const int s = (idx / (64 * NH)) % S;
-    const int b = idx / ((size_t)64 * NH * S);
-    const float *row = qkv + ((size_t)b * S + s) * ldq;
-    const size_t o = (((size_t)b * NH + h) * hs + s) * 64 + d;
-    const int i = d & 31;
-    float y1, y2;
-    rope_pair(row[H + h * 64 + i], row[H + h * 64 + i + 32], (float)s, i, step, &y1, &y2);
-    kc[o] = d < 32 ? y1 : y2;
-    vc[o] = row[2 * H + h * 64 + d];
-}
-
-// Prefill MLP: act = silu(gate) * up from the interleaved GEMM output (the
-// element operations of ACT silu then EWMUL).
-__global__ void silu_mul_kernel(const float *__restrict__ gu, int I, int M,
-                                float *__restrict__ act) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)M * I) return;
-    const int m = idx / I, j = idx % I;
-    const int pg = (j / 16) * 32 + (j % 16);
-    const float gate = gu[(size_t)m * 2 * I + pg];
-    const float up = gu[(size_t)m * 2 * I + pg + 16];
-    act[idx] = (gate / (1.0f + exp_f(-gate))) * up;
-}
-
 }  // namespace vmlm
 
 using namespace vmlm;
@@ -595,7 +561,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     const size_t B = d->B, H = d->H, I = d->I, NH = d->NH, M = B * S;
     const int T = 3;
     // per-prefill buffers; every projection input is int8 rows (a8, a8s)
-    float *h, *h2, *qkv, *att, *o, *gu, *act, *a8s, *gwork = nullptr;
+    float *h, *h2, *qkv, *att, *o, *act, *a8s, *gwork = nullptr;
     int8_t *a8;
     int32_t *toks;
     char *kvw;
@@ -612,7 +578,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         for (void *p : tmp) (void)hipFreeAsync(p, st);
     };
     if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
-        (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) || (rc = get(&gu, M * 2 * I * 4)) ||
+        (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) ||
         (rc = get(&act, M * I * 4)) || (rc = get(&a8, q8_rows_bytes(M, std::max(H, I)))) ||
         (rc = get(&a8s, M * 4)) ||
         (rc = get(&toks, M * 4)) ||
@@ -621,10 +587,10 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         return rc;
     }
     // k-slice work of the int8-row GEMMs whose grids would leave CUs idle
+    // (gate/up runs as one slice: its epilogue forms SiLU(gate) * up)
     const size_t gw = std::max(std::max(gemm_i8_work_floats((int)M, (int)(3 * H), (int)H),
                                         gemm_i8_work_floats((int)M, (int)H, (int)H)),
-                               std::max(gemm_i8_work_floats((int)M, (int)(2 * I), (int)H),
-                                        gemm_i8_work_floats((int)M, (int)H, (int)I)));
+                               gemm_i8_work_floats((int)M, (int)H, (int)I));
     if (gw && (rc = get(&gwork, gw * 4))) {
         release();
         return rc;
@@ -634,7 +600,11 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         int r = launch_emb_bf16(h, H, d->embed, d->V, H, nullptr, toks, (int)M, st);
         if (r) return r;
         for (size_t l = 0; l < d->L; ++l) {
-            if ((r = launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st))) return r;
+            // the input norm; from layer 1 on it first adds the previous
+            // layer's down projection (o) to its residual h2: h = h2 + o
+            if ((r = l ? launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st, h2, o)
+                       : launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st)))
+                return r;
             GemmArgs g;
             g.W = d->Wqkv(l);
             g.w_blocked = true;
@@ -649,17 +619,13 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             g.C = qkv;
             g.ldc = (int)(3 * H);
             if ((r = launch_gemm(g, st))) return r;
-            // q and k stay unrotated in qkv: the cache fill rotates k at positions
-            // 0..S-1 and the attention kernel rotates q and k as it loads them
-            size_t nkv = M * NH * 64;
-            kv_fill_kernel<<<cdiv(nkv, 256), 256, 0, st>>>(qkv, (int)(3 * H), (int)H, (int)NH,
-                                                           (int)S, d->Kc(l), d->Vc(l),
-                                                           (int)d->hs, (int)B, d->rope_step);
-            VMLM_HIP_CHECK(hipGetLastError());
+            // q and k stay unrotated in qkv: the attention's prep pass rotates
+            // them and writes the rotated K and raw V rows to the cache
+            // (positions 0..S-1)
             if ((r = launch_attention_prefill(qkv, qkv + H, qkv + 2 * H, att, (int)S, (int)NH,
                                               (int)(3 * H), (int)H, d->c.attn_scale, true, kvw,
                                               st, true, d->rope_step, 0.0f, (int)B, S * 3 * H,
-                                              S * H)))
+                                              S * H, d->Kc(l), d->Vc(l), (int)d->hs)))
                 return r;
             if ((r = launch_rows_q8(att, H, nullptr, 0.0f, M, H, a8, a8s, st))) return r;
             GemmArgs go = g;
@@ -669,17 +635,17 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             go.C = o;
             go.ldc = (int)H;
             if ((r = launch_gemm(go, st))) return r;
-            if ((r = launch_ew(h2, h, o, M * H, VMLM_OP_EWADD, st))) return r;
-            if ((r = launch_rows_q8(h2, H, d->PostLn(l), d->c.eps, M, H, a8, a8s, st))) return r;
+            // h2 = h + o, then the post-attention norm
+            if ((r = launch_rows_q8(h2, H, d->PostLn(l), d->c.eps, M, H, a8, a8s, st, h, o)))
+                return r;
             GemmArgs ggu = g;
             ggu.W = d->Wgu(l);
             ggu.scale = d->Sgu(l);
             ggu.N = (int)(2 * I);
-            ggu.C = gu;
-            ggu.ldc = (int)(2 * I);
+            ggu.C = act;  // SiLU(gate) * up formed in the epilogue
+            ggu.ldc = (int)I;
+            ggu.silu_pairs = true;
             if ((r = launch_gemm(ggu, st))) return r;
-            silu_mul_kernel<<<cdiv(M * I, 256), 256, 0, st>>>(gu, (int)I, (int)M, act);
-            VMLM_HIP_CHECK(hipGetLastError());
             if ((r = launch_rows_q8(act, I, nullptr, 0.0f, M, I, a8, a8s, st))) return r;
             GemmArgs gd = g;
             gd.W = d->Wd(l);
@@ -690,8 +656,9 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             gd.C = o;
             gd.ldc = (int)H;
             if ((r = launch_gemm(gd, st))) return r;
-            if ((r = launch_ew(h, h2, o, M * H, VMLM_OP_EWADD, st))) return r;
         }
+        // the last layer's residual add (the others are in the next input norm)
+        if ((r = launch_ew(h, h2, o, M * H, VMLM_OP_EWADD, st))) return r;
         // last row of every sequence -> decode buffers, then the shared tail
         VMLM_HIP_CHECK(hipMemcpy2DAsync(d->h, H * 4, h + (S - 1) * H, S * H * 4, H * 4, B,
                                         hipMemcpyDeviceToDevice, st));
