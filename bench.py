@@ -609,6 +609,26 @@ def mfma_probe(reps):
     print(json.dumps({"probe": "mfma", "reps": reps}))
 
 
+def prefill_probe(reps):
+    """For `rocprofv3 --kernel-trace` runs of the prefill: the batch-16
+    session (16 x 128 prompt tokens, M = 2048 rows) prefilled once, then
+    `reps` more times; no decode."""
+    from sparrow_amd import model as M
+    from sparrow_amd.decoder import Decoder
+    cfg = M.minicpm_2b_config()
+    W = M.make_weights(cfg, seed=3, threads=16)
+    dec = Decoder(cfg, batch=16, cap=1024)
+    dec.load(W)
+    prompts = M.make_prompts(cfg, 16, 128, seed=3)
+    ts = []
+    for _ in range(reps + 1):
+        t = time.perf_counter()
+        dec.prefill(prompts)
+        ts.append(time.perf_counter() - t)
+    dec.close()
+    print(json.dumps({"probe": "prefill", "batch": 16, "ms": [round(x * 1e3, 3) for x in ts]}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -624,6 +644,8 @@ def main():
                     help="only configs 0, 1, 2, 4 and the op timings (no decoder, no CPU)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only config 1 and the prefill GEMMs, for the MFMA counter runs")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only the batch-16 prefill (a first call, then two more), for kernel traces")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
     args = ap.parse_args()
@@ -642,6 +664,9 @@ def main():
         return
     if args.mfma_probe:
         mfma_probe(3)
+        return
+    if args.prefill_probe:
+        prefill_probe(2)
         return
     if args.suite_only:
         print(json.dumps({"suite": run_suite(args.suite_iters, cpu=False)}))

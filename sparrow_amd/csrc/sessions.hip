@@ -119,6 +119,11 @@ struct vmlm_decoder {
     int *pos = nullptr, *step = nullptr;
     float rope_step = 0.0f;
     uint32_t pos_host = 0, step_host = 0;
+    // the prefill's workspace, kept between calls (grown for a longer prompt)
+    void *pf = nullptr;
+    size_t pf_bytes = 0;
+    // host sources of the step / position reset copies (live as long as the session)
+    int32_t reset_step = 0, reset_pos = 0;
     bool loaded_globals = false;
     std::vector<bool> loaded;
     bool use_graph = true;
@@ -468,6 +473,7 @@ int vmlm_decoder_destroy(vmlm_decoder *d) {
     if (d->st) (void)hipStreamSynchronize(d->st);
     if (d->graph) (void)hipGraphExecDestroy(d->graph);
     for (void *p : d->allocs) (void)hipFree(p);
+    if (d->pf) (void)hipFree(d->pf);
     if (d->st) (void)hipStreamDestroy(d->st);
     delete d;
     return VMLM_OK;
@@ -560,40 +566,41 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     hipStream_t st = d->st;
     const size_t B = d->B, H = d->H, I = d->I, NH = d->NH, M = B * S;
     const int T = 3;
-    // per-prefill buffers; every projection input is int8 rows (a8, a8s)
+    // the prefill's buffers, carved from the session's workspace (256-byte
+    // aligned parts); every projection input is int8 rows (a8, a8s)
     float *h, *h2, *qkv, *att, *o, *act, *a8s, *gwork = nullptr;
     int8_t *a8;
     int32_t *toks;
     char *kvw;
-    std::vector<void *> tmp;
-    auto get = [&](auto **p, size_t bytes) -> int {
-        void *q = nullptr;
-        hipError_t e = hipMallocAsync(&q, bytes ? bytes : 1, st);
-        if (e != hipSuccess) return hip_fail(e, "prefill buffers");
-        tmp.push_back(q);
-        *p = (std::remove_reference_t<decltype(*p)>)q;
-        return VMLM_OK;
-    };
-    auto release = [&]() {
-        for (void *p : tmp) (void)hipFreeAsync(p, st);
-    };
-    if ((rc = get(&h, M * H * 4)) || (rc = get(&h2, M * H * 4)) || (rc = get(&qkv, M * 3 * H * 4)) ||
-        (rc = get(&att, M * H * 4)) || (rc = get(&o, M * H * 4)) ||
-        (rc = get(&act, M * I * 4)) || (rc = get(&a8, q8_rows_bytes(M, std::max(H, I)))) ||
-        (rc = get(&a8s, M * 4)) ||
-        (rc = get(&toks, M * 4)) ||
-        (rc = get(&kvw, attention_prefill_work_bytes((int)S, (int)NH, (int)B)))) {
-        release();
-        return rc;
-    }
     // k-slice work of the int8-row GEMMs whose grids would leave CUs idle
     // (gate/up runs as one slice: its epilogue forms SiLU(gate) * up)
     const size_t gw = std::max(std::max(gemm_i8_work_floats((int)M, (int)(3 * H), (int)H),
                                         gemm_i8_work_floats((int)M, (int)H, (int)H)),
                                gemm_i8_work_floats((int)M, (int)H, (int)I));
-    if (gw && (rc = get(&gwork, gw * 4))) {
-        release();
-        return rc;
+    const size_t parts[] = {M * H * 4, M * H * 4, M * 3 * H * 4, M * H * 4, M * H * 4, M * I * 4,
+                            q8_rows_bytes(M, std::max(H, I)), M * 4, M * 4,
+                            attention_prefill_work_bytes((int)S, (int)NH, (int)B), gw * 4};
+    size_t need = 0;
+    for (size_t b : parts) need += (b + 255) / 256 * 256;
+    if (d->pf_bytes < need) {
+        VMLM_HIP_CHECK(hipStreamSynchronize(st));
+        if (d->pf) (void)hipFree(d->pf);
+        d->pf = nullptr;
+        d->pf_bytes = 0;
+        hipError_t e = hipMalloc(&d->pf, need);
+        if (e != hipSuccess) return hip_fail(e, "prefill workspace");
+        d->pf_bytes = need;
+    }
+    {
+        char *c = (char *)d->pf;
+        int i = 0;
+        auto carve = [&](auto **p) {
+            *p = (std::remove_reference_t<decltype(*p)>)c;
+            c += (parts[i++] + 255) / 256 * 256;
+        };
+        carve(&h), carve(&h2), carve(&qkv), carve(&att), carve(&o), carve(&act), carve(&a8);
+        carve(&a8s), carve(&toks), carve(&kvw), carve(&gwork);
+        if (!gw) gwork = nullptr;
     }
     auto run = [&]() -> int {
         VMLM_HIP_CHECK(hipMemcpyAsync(toks, tokens, M * 4, hipMemcpyHostToDevice, st));
@@ -666,9 +673,10 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
                                 st)))
             return r;
         if ((r = enqueue_head(d, false))) return r;
-        int zero = 0, p = (int)S;
-        VMLM_HIP_CHECK(hipMemcpyAsync(d->step, &zero, 4, hipMemcpyHostToDevice, st));
-        VMLM_HIP_CHECK(hipMemcpyAsync(d->pos, &p, 4, hipMemcpyHostToDevice, st));
+        d->reset_step = 0;
+        d->reset_pos = (int32_t)S;
+        VMLM_HIP_CHECK(hipMemcpyAsync(d->step, &d->reset_step, 4, hipMemcpyHostToDevice, st));
+        VMLM_HIP_CHECK(hipMemcpyAsync(d->pos, &d->reset_pos, 4, hipMemcpyHostToDevice, st));
         if (first_tokens)
             VMLM_HIP_CHECK(hipMemcpyAsync(first_tokens, d->tok, B * 4, hipMemcpyDeviceToHost, st));
         if (logits_last)
@@ -677,7 +685,6 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         return VMLM_OK;
     };
     rc = run();
-    release();
     VMLM_HIP_CHECK(hipStreamSynchronize(st));
     if (rc) return rc;
     d->pos_host = S;
