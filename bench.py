@@ -534,11 +534,12 @@ def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
     return dec, wall, ms.value / 1e3, t0, toks
 
 
-def traffic_probe(iters):
+def traffic_probe(iters, batches=(16, 1)):
     """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` runs: a plain device copy
     of 256 MiB (the calibration: its bytes are known) three times, then the
     four decode GEMV shapes of the batch-16 session and of the batch-1 session
-    `iters` times each (after a warm-up pass over the 40 layers)."""
+    (or only the sessions in `batches`) `iters` times each (after a warm-up
+    pass over the 40 layers)."""
     import ctypes as C
     from sparrow_amd import check, lib
     from sparrow_amd import model as M
@@ -555,7 +556,7 @@ def traffic_probe(iters):
     check(L.vmlm_hip_free(b))
     cfg = M.minicpm_2b_config()
     W = M.make_weights(cfg, seed=3, threads=16)
-    for batch in (16, 1):  # the k-slice GEMVs (batch 16), then the fused ones (batch 1)
+    for batch in batches:  # the k-slice GEMVs (batch 16), then the fused ones (batch 1)
         dec = Decoder(cfg, batch=batch, cap=1024)
         dec.load(W)
         dec.prefill(M.make_prompts(cfg, batch, 128, seed=3))
@@ -646,6 +647,9 @@ def main():
                     help="only config 1 and the prefill GEMMs, for the MFMA counter runs")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only the batch-16 prefill (a first call, then two more), for kernel traces")
+    ap.add_argument("--no-batch1", action="store_true",
+                    help="only the --batch session (no batch-1 session): for kernel traces "
+                         "and traffic counters of the batch-16 program")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
     args = ap.parse_args()
@@ -660,7 +664,7 @@ def main():
     from sparrow_amd import model as M
     sparrow_amd.init(0)
     if args.traffic_probe:
-        traffic_probe(20)
+        traffic_probe(20, (16,) if args.no_batch1 else (16, 1))
         return
     if args.mfma_probe:
         mfma_probe(3)
@@ -684,6 +688,12 @@ def main():
     log(f"q8 GEMV: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     attn = {f"batch{args.batch}": decode_attention(dec, args.gemv_iters)}
     dec.close()
+    if args.no_batch1:
+        print(json.dumps({"probe": "decode", "batch": args.batch,
+                          "tokens_per_s": round(args.batch * args.steps / wall, 2),
+                          "roofline_frac": roof["frac"], "decode_attention": attn,
+                          "prefill": prefill}))
+        return
 
     if args.batch == 1:
         wall1, roof1 = wall, roof
