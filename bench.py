@@ -610,6 +610,36 @@ def mfma_probe(reps):
     print(json.dumps({"probe": "mfma", "reps": reps}))
 
 
+def b1_probe(reps):
+    """For `rocprofv3` runs of the B1 stack kernel: config 4 (8 layers,
+    d = 1536, k0 = 32, 1024 tokens, tanh) over a plan built once, `reps` + 1
+    forwards."""
+    import ctypes as C
+    from sparrow_amd import check, conn, lib
+    L = lib()
+    rng = np.random.default_rng(4)
+    d, k0, T = 1536, 32, 1024
+    layers = []
+    for li in range(8):
+        w, src = conn.make_block_aligned(rng, d, k0)
+        layers.append(conn.DeviceConn(w, src, layer=li))
+    x = np.ascontiguousarray(rng.standard_normal((T, d), dtype=np.float32))
+    xb, yb = C.c_void_p(), C.c_void_p()
+    check(L.vmlm_hip_malloc(C.byref(xb), x.nbytes))
+    check(L.vmlm_hip_memcpy_h2d(xb, x.ctypes.data, x.nbytes))
+    check(L.vmlm_hip_malloc(C.byref(yb), x.nbytes))
+    plan = conn.StackPlan(layers)
+    for _ in range(reps + 1):
+        check(L.vmlm_b1_stack_run(plan._h, xb, yb, T, 4, None))
+    check(L.vmlm_hip_sync())
+    plan.close()
+    for l in layers:
+        l.free()
+    L.vmlm_hip_free(xb)
+    L.vmlm_hip_free(yb)
+    print(json.dumps({"probe": "b1", "reps": reps}))
+
+
 def prefill_probe(reps):
     """For `rocprofv3 --kernel-trace` runs of the prefill: the batch-16
     session (16 x 128 prompt tokens, M = 2048 rows) prefilled once, then
@@ -645,6 +675,8 @@ def main():
                     help="only configs 0, 1, 2, 4 and the op timings (no decoder, no CPU)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only config 1 and the prefill GEMMs, for the MFMA counter runs")
+    ap.add_argument("--b1-probe", action="store_true",
+                    help="only config 4's stack kernel (plan built once), for counter runs")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only the batch-16 prefill (a first call, then two more), for kernel traces")
     ap.add_argument("--no-batch1", action="store_true",
@@ -671,6 +703,9 @@ def main():
         return
     if args.prefill_probe:
         prefill_probe(2)
+        return
+    if args.b1_probe:
+        b1_probe(3)
         return
     if args.suite_only:
         print(json.dumps({"suite": run_suite(args.suite_iters, cpu=False)}))

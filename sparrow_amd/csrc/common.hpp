@@ -187,9 +187,10 @@ __device__ __forceinline__ float round_f32(float v) {
 // test keeps C++ from treating the NaN conversion as undefined.
 __device__ __forceinline__ int as_i32(float n) { return n == n ? (int)n : 0; }
 
-// sys/src/math/mod.rs:74-140
-__device__ __forceinline__ float exp_f(float x) {
-    x = x < -88.0f ? -88.0f : (x > 88.0f ? 88.0f : x);
+// sys/src/math/mod.rs:74-140. exp_f_poly is the reduction and polynomial,
+// e^x = p * 2^n; exp_f clamps x to [-88, 88] first and scales by 2^n, a
+// normal or (n < -126) a subnormal float.
+__device__ __forceinline__ float exp_f_poly(float x, float &n_out) {
     const float LOG2E = 1.4426950f;
     const float LN2_HI = 0.69314575f;
     const float LN2_LO = 1.4286068e-6f;
@@ -203,6 +204,13 @@ __device__ __forceinline__ float exp_f(float x) {
     p = p * r + 1.6666665e-1f;
     p = p * r + 0.5f;
     p = p * r2 + r + 1.0f;
+    n_out = n;
+    return p;
+}
+__device__ __forceinline__ float exp_f(float x) {
+    x = x < -88.0f ? -88.0f : (x > 88.0f ? 88.0f : x);
+    float n;
+    const float p = exp_f_poly(x, n);
     // p * 2^n, 2^n a normal or (n < -126) a subnormal float; the two cases
     // as one select so the function has no branch (n >= -127 after the clamp)
     const int ni = as_i32(n);
@@ -262,11 +270,15 @@ __device__ __forceinline__ float floor_f(float x) {
     return t > x ? t - 1.0f : t;
 }
 
-// ops/src/kernels.rs:58-67
+// ops/src/kernels.rs:58-67. Past the clamps 2x is within [-30, 30] (or NaN),
+// where exp_f's own clamp does nothing and 2^n (|n| <= 44, or n NaN -> 0) is
+// a normal float: exp_f's operations without those two selects.
 __device__ __forceinline__ float tanh_f(float x) {
     if (x > 15.0f) return 1.0f;
     if (x < -15.0f) return -1.0f;
-    float e = exp_f(2.0f * x);
+    float n;
+    const float p = exp_f_poly(2.0f * x, n);
+    const float e = p * __uint_as_float((uint32_t)(as_i32(n) + 127) << 23);
     return (e - 1.0f) / (e + 1.0f);
 }
 

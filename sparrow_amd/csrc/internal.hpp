@@ -315,6 +315,7 @@ struct B1PlanJob {
     const uint32_t *src;
     void *plan;
     int k0;
+    uint32_t base = 0;  // added to every LDS offset of the plan (the stack's buffer)
 };
 constexpr int B1_PLAN_JOBS = 16;
 struct B1PlanJobs {

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void b1_plan_kernel(B1PlanJobs jobs, int n, in
         }
     }
     __syncthreads();
-    const uint32_t zero_row = (uint32_t)((d + 15) & ~15) * (uint32_t)row_bytes;
+    const uint32_t zero_row = jb.base + (uint32_t)((d + 15) & ~15) * (uint32_t)row_bytes;
     uint4 *off = (uint4 *)jb.plan;
     float4 *wp = (float4 *)(off + (size_t)G * n);
     for (int q = threadIdx.x; q < 64 * G; q += 256) {
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void b1_plan_kernel(B1PlanJobs jobs, int n, in
             const int j = 4 * g + e;
             if (j < k0) {
                 const uint32_t s = ss[r][j] < (uint32_t)d ? ss[r][j] : (uint32_t)(d - 1);
-                o[e] = b1_row_slot(s) * (uint32_t)row_bytes;
+                o[e] = jb.base + b1_row_slot(s) * (uint32_t)row_bytes;
                 w[e] = sw[r][j];
             } else {
                 o[e] = zero_row;
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(64 * B1_SNW) void b1_stack_kernel(const char *__res
             load(u + 1 < units ? u + 1 : u, on, wn);  // unconditional: no branch around the loads
         else
             load(u, o, w);
-        const char *in = lds + (l & 1) * bufb;
+        const char *in = lds;  // the plan's offsets include buffer l & 1
         float acc[4];
         // ring of LDS reads B1_SPD steps ahead of the step being summed
         float4 ring[B1_SPD];
@@ -573,9 +573,12 @@ int launch_b1_stack_plan(const B1PlanJob *layers, int n_layers, int d, void *pla
     for (int l0 = 0; l0 < n_layers; l0 += B1_PLAN_JOBS) {
         B1PlanJobs jobs{};
         const int nj = std::min(B1_PLAN_JOBS, n_layers - l0);
+        // layer l reads LDS buffer l & 1: its offsets carry that buffer's base
+        const uint32_t bufb = (uint32_t)(((d + 15) & ~15) + 1) * B1_SROW;
         for (int k = 0; k < nj; ++k) {
             jobs.job[k] = layers[l0 + k];
             jobs.job[k].plan = (char *)plan + (size_t)(l0 + k) * stride;
+            jobs.job[k].base = ((l0 + k) & 1) * bufb;
         }
         b1_plan_kernel<<<dim3(cdiv((size_t)d, 64), nj), 256, 0, st>>>(jobs, d, d, B1_SROW, G);
         VMLM_HIP_CHECK(hipGetLastError());
