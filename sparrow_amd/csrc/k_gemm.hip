@@ -275,13 +275,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int ROW = 64;  // bytes of a row-major W row in LDS (64 k of int8)
     constexpr int ABLK = Q8_T * BM / 16;  // 1 KiB blocks of A per k-step
+    constexpr int BBLK = BN / 16;         // 1 KiB copies of W per k-step
     constexpr int A_BYTES = ABLK * 1024, B_BYTES = BN * ROW;
     constexpr int STAGE = A_BYTES + B_BYTES;
     constexpr int C_LD = WN + 4;
     constexpr int C_BYTES = 4 * 16 * C_LD * 4;
     constexpr int SMEM = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
-    constexpr int A_INS = ABLK / 4, B_INS = B_BYTES / 1024 / 4;  // per wave per step
-    static_assert(ABLK % 4 == 0 && B_BYTES % 4096 == 0, "copy instructions per wave");
+    // copy instructions per wave and step: W blocks q * 4 + wave < BBLK (with
+    // BN = 96 waves 0-1 copy two, waves 2-3 one, which the vmcnt wait of two
+    // stages (wait for all) allows)
+    constexpr int A_INS = ABLK / 4, B_INS = (BBLK + 3) / 4;
+    static_assert(ABLK % 4 == 0 && BN % 16 == 0, "copy instructions per wave");
+    static_assert(BBLK % 4 == 0 || NS == 2, "uneven W copies need the two-stage wait");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -312,11 +317,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
     for (int q = 0; q < B_INS; ++q) {
         if constexpr (WB) {
-            int tn = n0 / 16 + q * 4 + wave;
+            int tn = n0 / 16 + (q * 4 + wave < BBLK ? q * 4 + wave : BBLK - 1);
             tn = tn < p.N / 16 ? tn : p.N / 16 - 1;
             b_src[q] = p.W + ((size_t)tn * nkt) * 1024 + lane * 16;
         } else {
-            const int R = (q * 4 + wave) * 16 + (lane >> 2);
+            const int R = (q * 4 + wave < BBLK ? q * 4 + wave : BBLK - 1) * 16 + (lane >> 2);
             const int c = (lane & 3) ^ ((R >> 1) & 3);
             int gn = n0 + R;
             gn = gn < p.N ? gn : p.N - 1;
@@ -332,7 +337,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             dma16(a_src[q] + (size_t)kc * 1024, sb + (q * 4 + wave) * 1024);
 #pragma unroll
         for (int q = 0; q < B_INS; ++q)
-            dma16(b_src[q] + (size_t)kc * (WB ? 1024 : ROW), sb + A_BYTES + (q * 4 + wave) * 1024);
+            if (BBLK % 4 == 0 || q * 4 + wave < BBLK)  // wave-uniform
+                dma16(b_src[q] + (size_t)kc * (WB ? 1024 : ROW), sb + A_BYTES + (q * 4 + wave) * 1024);
     };
 
     gi32x4 acc[Q8_T][TM][TN];
@@ -384,7 +390,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // epilogue: the terms combined, 16-row slabs through LDS, 16-byte stores
     float *cs = (float *)smem + wave * 16 * C_LD;
     const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.C & 15) == 0;
-    constexpr int LPR = WN / 4, RPP = 64 / LPR;  // lanes per row, rows per pass
+    // lanes per row, rows per pass (the last pass may be partial)
+    constexpr int LPR = WN / 4, RPP = 64 / LPR, NPASS = (16 + RPP - 1) / RPP;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -399,13 +406,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's slab is in LDS
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int pass = 0; pass < 16 / RPP; ++pass) {
+        for (int pass = 0; pass < NPASS; ++pass) {
             const int rr_ = pass * RPP + lane / LPR, c4 = (lane % LPR) * 4;
+            if (lane >= RPP * LPR || rr_ >= 16) continue;
             float4 v = *(const float4 *)&cs[rr_ * C_LD + c4];
             const int row = m0 + wm * WM + i * 16 + rr_, col = n0 + wn * WN + c4;
             if (row >= p.M || col >= p.N) continue;
             const float rf = p.a8s[row];
-            if (p.silu) {
+            if (WN % 32 == 0 && p.silu) {
                 // the slab's 64 columns are two (16 gate, 16 up) pairs: a gate
                 // lane takes its up values 16 columns on, as silu_mul would
                 // read them from C (the same scaled f32 results)
@@ -482,15 +490,15 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
     return bm == 128 ? launch_dma<WI8, T, 128, 128>(p, ns, st) : launch_dma<WI8, T, 64, 128>(p, ns, st);
 }
 
-template <int BM, int NS>
+template <int BM, int BN, int NS>
 static int launch_i8(const GemmParams &p, bool wb, int ksl, hipStream_t st) {
-    constexpr int stage = Q8_T * BM * 64 + 128 * 64;
+    constexpr int stage = Q8_T * BM * 64 + BN * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
-    const dim3 grid((p.N + 127) / 128, (p.M + BM - 1) / BM, ksl);
+    const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, ksl);
     if (wb)
-        gemm_dma_i8_kernel<BM, 128, NS, true><<<grid, 256, 0, st>>>(p);
+        gemm_dma_i8_kernel<BM, BN, NS, true><<<grid, 256, 0, st>>>(p);
     else
-        gemm_dma_i8_kernel<BM, 128, NS, false><<<grid, 256, 0, st>>>(p);
+        gemm_dma_i8_kernel<BM, BN, NS, false><<<grid, 256, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     if (ksl == 1) return VMLM_OK;
     return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
@@ -593,10 +601,21 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         // 64 x 128 tiles: 128-row tiles need 256 accumulator registers, run one
         // wave per SIMD and measured 30 % slower at the prefill shapes. Two
         // stages (48 KB, 166 VGPRs) keep three workgroups per CU, three
-        // stages (72 KB) two: 4 to 8 % faster at the prefill shapes
+        // stages (72 KB) two: 4 to 8 % faster at the prefill shapes.
+        // 64 x 96 tiles where they load the CUs more evenly: the busiest CU
+        // holds ceil(tiles / 256) workgroups, each copying 12 KiB of rows and
+        // BN / 16 KiB of weights per k-step (N = 2304: 768 tiles, three on
+        // every CU, instead of 576 with three on a quarter of them)
+        auto load = [&](int bn) {
+            const size_t t = (size_t)((a.N + bn - 1) / bn) * ((a.M + 63) / 64) * ksl;
+            return (t + 255) / 256 * (size_t)(Q8_T * 4 * 1024 + bn * 64);
+        };
+        const bool bn96 = !a.silu_pairs && ns == 2 && a.N % 96 == 0 && load(96) < load(128);
         switch (ns) {
-        case 2: return launch_i8<64, 2>(p, a.w_blocked, ksl, st);
-        case 3: return launch_i8<64, 3>(p, a.w_blocked, ksl, st);
+        case 2:
+            return bn96 ? launch_i8<64, 96, 2>(p, a.w_blocked, ksl, st)
+                        : launch_i8<64, 128, 2>(p, a.w_blocked, ksl, st);
+        case 3: return launch_i8<64, 128, 3>(p, a.w_blocked, ksl, st);
         }
         return fail(VMLM_ERR_UNIMPL, "gemm (int8 rows): %d LDS stages", ns);
     }
