@@ -651,24 +651,24 @@ def b1_probe(reps):
     print(json.dumps({"probe": "b1", "reps": reps}))
 
 
-def prefill_probe(reps):
-    """For `rocprofv3 --kernel-trace` runs of the prefill: the batch-16
-    session (16 x 128 prompt tokens, M = 2048 rows) prefilled once, then
-    `reps` more times; no decode."""
+def prefill_probe(reps, batch=16):
+    """For `rocprofv3 --kernel-trace` runs of the prefill: the session
+    (`batch` x 128 prompt tokens; batch 16: M = 2048 rows) prefilled once,
+    then `reps` more times; no decode."""
     from sparrow_amd import model as M
     from sparrow_amd.decoder import Decoder
     cfg = M.minicpm_2b_config()
     W = M.make_weights(cfg, seed=3, threads=16)
-    dec = Decoder(cfg, batch=16, cap=1024)
+    dec = Decoder(cfg, batch=batch, cap=1024)
     dec.load(W)
-    prompts = M.make_prompts(cfg, 16, 128, seed=3)
+    prompts = M.make_prompts(cfg, batch, 128, seed=3)
     ts = []
     for _ in range(reps + 1):
         t = time.perf_counter()
         dec.prefill(prompts)
         ts.append(time.perf_counter() - t)
     dec.close()
-    print(json.dumps({"probe": "prefill", "batch": 16, "ms": [round(x * 1e3, 3) for x in ts]}))
+    print(json.dumps({"probe": "prefill", "batch": batch, "ms": [round(x * 1e3, 3) for x in ts]}))
 
 
 def main():
@@ -689,7 +689,7 @@ def main():
     ap.add_argument("--b1-probe", action="store_true",
                     help="only config 4's stack kernel (plan built once), for counter runs")
     ap.add_argument("--prefill-probe", action="store_true",
-                    help="only the batch-16 prefill (a first call, then two more), for kernel traces")
+                    help="only the prefill at --batch (a first call, then more), for kernel traces")
     ap.add_argument("--no-batch1", action="store_true",
                     help="only the --batch session (no batch-1 session): for kernel traces "
                          "and traffic counters of the batch-16 program")
@@ -713,7 +713,7 @@ def main():
         mfma_probe(3)
         return
     if args.prefill_probe:
-        prefill_probe(2)
+        prefill_probe(4, args.batch)
         return
     if args.b1_probe:
         b1_probe(3)

@@ -353,6 +353,7 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         g.A8 = a8;
         g.a8s = a8s;
         g.work = gwork;
+        g.work_floats = gw;
         g.lda = (int)k;
         g.M = (int)m;
         g.N = (int)n;

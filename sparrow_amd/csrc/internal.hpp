@@ -149,8 +149,10 @@ struct GemmArgs {
     // int8 rows: W is the swizzled copy (launch_swizzle_w) instead of row-major
     bool w_blocked = false;
     // int8 rows, optional: gemm_i8_work_floats() floats for the k-slices of
-    // a grid that would leave most CUs idle (null: one slice)
+    // a grid that would leave most CUs idle (null: one slice); work_floats is
+    // its size, checked against the slices the launch would write
     float *work = nullptr;
+    size_t work_floats = 0;
     // int8 rows: the N weight rows are (gate, up) pairs interleaved in blocks
     // of 16 (rows 32t .. 32t + 15 gate, 32t + 16 .. 32t + 31 up); C receives
     // act = SiLU(gate) * up [M][N / 2] (column 16t + j from rows 32t + j and

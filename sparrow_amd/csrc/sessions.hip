@@ -619,6 +619,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             g.A8 = a8;
             g.a8s = a8s;
             g.work = gwork;
+            g.work_floats = gw;
             g.lda = (int)H;
             g.M = (int)M;
             g.N = (int)(3 * H);
