@@ -153,6 +153,9 @@ struct GemmArgs {
     // its size, checked against the slices the launch would write
     float *work = nullptr;
     size_t work_floats = 0;
+    // int8 rows with k-slices: leave the slices in `work` for the consumer
+    // (Slices below) instead of reducing them into C
+    bool keep_slices = false;
     // int8 rows: the N weight rows are (gate, up) pairs interleaved in blocks
     // of 16 (rows 32t .. 32t + 15 gate, 32t + 16 .. 32t + 31 up); C receives
     // act = SiLU(gate) * up [M][N / 2] (column 16t + j from rows 32t + j and
@@ -161,6 +164,16 @@ struct GemmArgs {
     bool silu_pairs = false;
 };
 int launch_gemm(const GemmArgs &a, hipStream_t st);
+// An [M][N] matrix left as ks ordered k-slices [ks][M][N] (row factors
+// applied) by launch_gemm with keep_slices: element (i, j) is
+// (part[0][i][j] + part[1][i][j] + ...) * scale[j], the arithmetic of the
+// slice reduction (launch_gemv_reduce).
+struct Slices {
+    const float *part = nullptr;
+    int ks = 0;
+    size_t pst = 0;  // floats from one slice to the next (M * N)
+    const float *scale = nullptr;
+};
 // Recomputes in f32 the rows of an int8-row GEMM whose factor a8s[i] is NaN
 // (non-finite inputs), giving the reference's +-inf / NaN pattern.
 int launch_gemm_i8_nonfinite_rows(const float *a, int lda, const int8_t *q, int ldq,
@@ -240,7 +253,7 @@ size_t q8_rows_tiles(size_t rows);
 size_t q8_rows_bytes(size_t rows, size_t cols);
 int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
                    int8_t *q8, float *q8s, hipStream_t st, const float *ra = nullptr,
-                   const float *rb = nullptr);
+                   const float *rb = nullptr, const Slices &rbs = Slices{});
 // SiLU(gate) * up from the partials of the interleaved gate/up projection,
 // as int8 terms [Q8_T][rows][I] with a power-of-two
 // factor per segment of `seg` columns, q8s [I/seg][rows] (the input of a
@@ -273,13 +286,17 @@ int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
 // attention_prefill_work_bytes(S, H, nseq) bytes (bf16 term planes of K and
 // V); with rope, K is rotated there and Q as it is loaded (positions pos0 + row).
 // With kc and vc (pos0 = 0) the rotated K rows and raw V rows are also written
-// to a KV cache [nseq][H][hs][64] at positions 0 .. S-1.
+// to a KV cache [nseq][H][hs][64] at positions 0 .. S-1. With qs.part, q, k and
+// v point into slice 0 of k-slices (qs.ks slices qs.pst floats apart) and
+// qs.scale holds the column scales of q's columns (k's and v's follow at
+// k - q and v - q).
 size_t attention_prefill_work_bytes(int S, int H, int nseq);
 int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope = false, float rope_step = 0.0f,
                              float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0,
-                             float *kc = nullptr, float *vc = nullptr, int hs = 0);
+                             float *kc = nullptr, float *vc = nullptr, int hs = 0,
+                             const Slices &qs = Slices{});
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;

@@ -322,6 +322,9 @@ struct PrefillParams {
 // rows with one angle evaluation per pair (Q and K share the position).
 // With kc / vc the rotated K rows and the raw V rows also go to a KV cache
 // [sequence][head][hs][64] f32 at positions 0 .. S-1 (the decoder's prefill).
+// With pks > 0, Q, K and V point into slice 0 of pks k-slices pst floats
+// apart: each value is the slices summed in order times its column scale
+// (sq, sk, sv), as the slice reduction would have written it.
 struct QKVPrepParams {
     const float *Q, *K, *V;
     uint16_t *Qt, *Kt, *Vt;
@@ -329,6 +332,9 @@ struct QKVPrepParams {
     size_t sin;
     int S, Sp, ld, H, rope, hs;
     float rope_step, pos0;
+    int pks;
+    size_t pst;
+    const float *sq, *sk, *sv;
 };
 __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
     const int h = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
@@ -337,8 +343,21 @@ __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
     {
         const int row = k0 + (tid >> 4), c = tid & 15, rr = min(row, p.S - 1);
         const size_t src = z * p.sin + (size_t)rr * p.ld + h * 64 + 2 * c;
-        float2 q1 = *(const float2 *)(p.Q + src), q2 = *(const float2 *)(p.Q + src + 32);
-        float2 k1 = *(const float2 *)(p.K + src), k2 = *(const float2 *)(p.K + src + 32);
+        auto ld2 = [&](const float *b, const float *sc, int off) {
+            float2 v = *(const float2 *)(b + src + off);
+            if (p.pks) {
+                for (int s = 1; s < p.pks; ++s) {
+                    const float2 t = *(const float2 *)(b + (size_t)s * p.pst + src + off);
+                    v.x += t.x;
+                    v.y += t.y;
+                }
+                const int j = h * 64 + 2 * c + off;
+                v = make_float2(v.x * sc[j], v.y * sc[j + 1]);
+            }
+            return v;
+        };
+        float2 q1 = ld2(p.Q, p.sq, 0), q2 = ld2(p.Q, p.sq, 32);
+        float2 k1 = ld2(p.K, p.sk, 0), k2 = ld2(p.K, p.sk, 32);
         if (p.rope) {
             const float fpos = p.pos0 + (float)rr;
             float si, co, a, b;
@@ -375,8 +394,16 @@ __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
         __shared__ float vs[AT_B][AT_B + 1];
         {
             const int row = k0 + (tid >> 4), d0 = 4 * (tid & 15);
-            const float4 x =
-                *(const float4 *)(p.V + z * p.sin + (size_t)min(row, p.S - 1) * p.ld + h * 64 + d0);
+            const size_t vsrc = z * p.sin + (size_t)min(row, p.S - 1) * p.ld + h * 64 + d0;
+            float4 x = *(const float4 *)(p.V + vsrc);
+            if (p.pks) {
+                for (int s = 1; s < p.pks; ++s) {
+                    const float4 t = *(const float4 *)(p.V + (size_t)s * p.pst + vsrc);
+                    x = make_float4(x.x + t.x, x.y + t.y, x.z + t.z, x.w + t.w);
+                }
+                const float4 sc = *(const float4 *)(p.sv + h * 64 + d0);
+                x = make_float4(x.x * sc.x, x.y * sc.y, x.z * sc.z, x.w * sc.w);
+            }
             const bool ok = row < p.S;
             if (ok && p.vc) *(float4 *)(p.vc + (((size_t)z * p.H + h) * p.hs + row) * 64 + d0) = x;
             vs[tid >> 4][d0] = ok ? x.x : 0.0f;
@@ -582,7 +609,8 @@ size_t attention_prefill_work_bytes(int S, int H, int nseq) {
 int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope, float rope_step, float pos0, int nseq,
-                             size_t sin, size_t sout, float *kc, float *vc, int hs) {
+                             size_t sin, size_t sout, float *kc, float *vc, int hs,
+                             const Slices &qs) {
     VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 7) == 0 && ((uintptr_t)k & 7) == 0 &&
                    ((uintptr_t)v & 15) == 0 && (nseq == 1 || sin % 4 == 0),
                "attention prefill: 16-byte aligned V rows and 8-byte aligned Q / K rows "
@@ -591,6 +619,10 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
                                       ((uintptr_t)vc & 15) == 0)),
                "attention prefill: a KV cache needs both rows, hs >= S, position 0 and "
                "16-byte alignment");
+    VMLM_GUARD(!qs.part || (qs.ks >= 1 && qs.pst % 4 == 0 && qs.scale &&
+                            ((uintptr_t)qs.scale & 15) == 0 && (k - q) % 4 == 0 && (v - q) % 4 == 0),
+               "attention prefill: k-slice q/k/v need ks >= 1, a slice stride that is a "
+               "multiple of 4 and 16-byte aligned column scales");
     VMLM_GUARD(nseq >= 1 && nseq <= 65535 && H <= 65535, "attention prefill: grid too large");
     if (S <= 0) return VMLM_OK;
     const int Sp = (S + AT_B - 1) / AT_B * AT_B;
@@ -613,6 +645,11 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
     kp.kc = kc;
     kp.vc = vc;
     kp.hs = hs;
+    kp.pks = qs.part ? qs.ks : 0;
+    kp.pst = qs.pst;
+    kp.sq = qs.scale;
+    kp.sk = qs.part ? qs.scale + (k - q) : nullptr;
+    kp.sv = qs.part ? qs.scale + (v - q) : nullptr;
     attn_qkv_prep_kernel<<<dim3(Sp / AT_B, H, nseq), 1024, 0, st>>>(kp);
     VMLM_HIP_CHECK(hipGetLastError());
     PrefillParams P;

@@ -491,7 +491,7 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
 }
 
 template <int BM, int BN, int NS>
-static int launch_i8(const GemmParams &p, bool wb, int ksl, hipStream_t st) {
+static int launch_i8(const GemmParams &p, bool wb, int ksl, bool keep, hipStream_t st) {
     constexpr int stage = Q8_T * BM * 64 + BN * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
     const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, ksl);
@@ -500,7 +500,7 @@ static int launch_i8(const GemmParams &p, bool wb, int ksl, hipStream_t st) {
     else
         gemm_dma_i8_kernel<BM, BN, NS, false><<<grid, 256, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
-    if (ksl == 1) return VMLM_OK;
+    if (ksl == 1 || keep) return VMLM_OK;
     return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
 }
 
@@ -618,14 +618,14 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         // A grid of at most one workgroup per CU (small M) waits on each
         // copy: four stages (80 KB) keep three steps in flight. Batch-1
         // prefill (M = 128) 5.63 -> 4.60 ms; five and six stages were slower.
-        if (!a.stages && tiles(128) <= 256) return launch_i8<64, 128, 4>(p, a.w_blocked, ksl, st);
+        if (!a.stages && tiles(128) <= 256) return launch_i8<64, 128, 4>(p, a.w_blocked, ksl, a.keep_slices, st);
         const bool bn96 = !a.silu_pairs && ns == 2 && a.N % 96 == 0 && load(96) < load(128);
         switch (ns) {
         case 2:
-            return bn96 ? launch_i8<64, 96, 2>(p, a.w_blocked, ksl, st)
-                        : launch_i8<64, 128, 2>(p, a.w_blocked, ksl, st);
-        case 3: return launch_i8<64, 128, 3>(p, a.w_blocked, ksl, st);
-        case 4: return launch_i8<64, 128, 4>(p, a.w_blocked, ksl, st);
+            return bn96 ? launch_i8<64, 96, 2>(p, a.w_blocked, ksl, a.keep_slices, st)
+                        : launch_i8<64, 128, 2>(p, a.w_blocked, ksl, a.keep_slices, st);
+        case 3: return launch_i8<64, 128, 3>(p, a.w_blocked, ksl, a.keep_slices, st);
+        case 4: return launch_i8<64, 128, 4>(p, a.w_blocked, ksl, a.keep_slices, st);
         }
         return fail(VMLM_ERR_UNIMPL, "gemm (int8 rows): %d LDS stages", ns);
     }

@@ -431,11 +431,14 @@ int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int row
 // Both give the same bits: the same sums in the same order.
 // With ra / rb the rows are first formed as x = ra + rb (a residual add, the
 // f32 add of EWADD) and written to x; the terms kernel then reads them there.
+// rb may instead be k-slices (rbs.part, row stride cols): each element of rb
+// is then the slices summed in order times the column scale, as the slice
+// reduction would have written it.
 constexpr int RQ_U = 8;  // 4-column groups per thread in the stats kernel (cols <= 8192)
 constexpr size_t RQ_ONE_MAX = 256;
 template <bool TERMS>
 __global__ __launch_bounds__(256) void rows_q8_stats_kernel(
-    float *x, int ldx, const float *__restrict__ ra, const float *__restrict__ rb,
+    float *x, int ldx, const float *__restrict__ ra, const float *__restrict__ rb, Slices rbs,
     const float *__restrict__ g, float eps, int cols, int rows, int row_tiles,
     float *__restrict__ inv_out, float *__restrict__ q8s, int8_t *__restrict__ q8) {
     __shared__ float sh[4];
@@ -462,12 +465,22 @@ __global__ __launch_bounds__(256) void rows_q8_stats_kernel(
     float ss = 0.0f;
     if (ra) {
         const float4 *ar = (const float4 *)(ra + (size_t)row * ldx);
-        const float4 *br = (const float4 *)(rb + (size_t)row * ldx);
+        const float4 *br = (const float4 *)(rbs.part ? rbs.part + (size_t)row * cols
+                                                     : rb + (size_t)row * ldx);
 #pragma unroll
         for (int u = 0; u < RQ_U; ++u) {
             const int c = threadIdx.x + u * 256;
             if (c < n4) {
-                const float4 a = ar[c], b = br[c];
+                const float4 a = ar[c];
+                float4 b = br[c];
+                if (rbs.part) {  // slices in order, then the column scale
+                    for (int s = 1; s < rbs.ks; ++s) {
+                        const float4 t = br[(size_t)s * (rbs.pst / 4) + c];
+                        b = make_float4(b.x + t.x, b.y + t.y, b.z + t.z, b.w + t.w);
+                    }
+                    const float4 sc = ((const float4 *)rbs.scale)[c];
+                    b = make_float4(b.x * sc.x, b.y * sc.y, b.z * sc.z, b.w * sc.w);
+                }
                 v[u] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
                 xr[c] = v[u];
             } else {
@@ -584,10 +597,16 @@ size_t q8_rows_bytes(size_t rows, size_t cols) {
 }
 
 int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t rows, size_t cols,
-                   int8_t *q8, float *q8s, hipStream_t st, const float *ra, const float *rb) {
+                   int8_t *q8, float *q8s, hipStream_t st, const float *ra, const float *rb,
+                   const Slices &rbs) {
     if (rows == 0) return VMLM_OK;
-    VMLM_GUARD(!ra == !rb && (!ra || (((uintptr_t)ra & 15) == 0 && ((uintptr_t)rb & 15) == 0)),
+    const float *rbx = rbs.part ? rbs.part : rb;
+    VMLM_GUARD(!ra == !rbx && (!ra || (((uintptr_t)ra & 15) == 0 && ((uintptr_t)rbx & 15) == 0)),
                "rows_q8: a residual add needs both 16-byte aligned operands");
+    VMLM_GUARD(!rbs.part || (ra && rbs.ks >= 1 && rbs.pst % 4 == 0 && rbs.pst >= rows * cols &&
+                             rbs.scale && ((uintptr_t)rbs.scale & 15) == 0),
+               "rows_q8: k-slices of the added rows need ks >= 1, a slice stride of at least "
+               "rows x cols floats (a multiple of 4) and 16-byte aligned column scales");
     VMLM_GUARD(cols % 64 == 0 && cols >= 64 && cols <= 4 * 256 * RQ_U && ldx % 4 == 0 &&
                    ldx >= cols && ((uintptr_t)x & 15) == 0 && (!g || ((uintptr_t)g & 15) == 0) &&
                    ((uintptr_t)q8 & 15) == 0 && q8s && rows <= 0x7fffffff,
@@ -595,14 +614,14 @@ int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t
     const size_t tiles = q8_rows_tiles(rows);
     if (rows <= RQ_ONE_MAX) {
         rows_q8_stats_kernel<true><<<(unsigned)(tiles * 16), 256, 0, st>>>(
-            (float *)x, (int)ldx, ra, rb, g, eps, (int)cols, (int)rows, (int)tiles, nullptr, q8s,
-            q8);
+            (float *)x, (int)ldx, ra, rb, rbs, g, eps, (int)cols, (int)rows, (int)tiles, nullptr,
+            q8s, q8);
         VMLM_HIP_CHECK(hipGetLastError());
         return VMLM_OK;
     }
     float *inv = (float *)(q8 + (size_t)Q8_T * tiles * 16 * cols);
     rows_q8_stats_kernel<false><<<(unsigned)rows, 256, 0, st>>>(
-        (float *)x, (int)ldx, ra, rb, g, eps, (int)cols, (int)rows, (int)tiles, inv, q8s, q8);
+        (float *)x, (int)ldx, ra, rb, rbs, g, eps, (int)cols, (int)rows, (int)tiles, inv, q8s, q8);
     VMLM_HIP_CHECK(hipGetLastError());
     const dim3 grid((unsigned)((rows + 15) / 16), (unsigned)((cols / 16 + RQ_J - 1) / RQ_J));
     rows_q8_terms_kernel<<<grid, 16 * RQ_J, 0, st>>>(x, (int)ldx, g, (int)cols, (int)rows,

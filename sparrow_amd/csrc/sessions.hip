@@ -606,10 +606,20 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         VMLM_HIP_CHECK(hipMemcpyAsync(toks, tokens, M * 4, hipMemcpyHostToDevice, st));
         int r = launch_emb_bf16(h, H, d->embed, d->V, H, nullptr, toks, (int)M, st);
         if (r) return r;
+        // k-sliced projections (grids that would leave CUs idle, small M) hand
+        // their slices to the consumer, which sums them in order and applies
+        // the column scale (no reduction launch): q/k/v to the attention's
+        // prep pass, o and down (but the last) to the next rows_q8's residual
+        // add
+        const int ks_qkv = gemm_i8_kslices((int)M, (int)(3 * H), (int)H);
+        const int ks_o = gemm_i8_kslices((int)M, (int)H, (int)H);
+        const int ks_d = gemm_i8_kslices((int)M, (int)H, (int)I);
         for (size_t l = 0; l < d->L; ++l) {
             // the input norm; from layer 1 on it first adds the previous
-            // layer's down projection (o) to its residual h2: h = h2 + o
-            if ((r = l ? launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st, h2, o)
+            // layer's down projection to its residual h2: h = h2 + down
+            Slices down;
+            if (l && ks_d > 1) down = Slices{gwork, ks_d, M * H, d->Sd(l - 1)};
+            if ((r = l ? launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st, h2, o, down)
                        : launch_rows_q8(h, H, d->InLn(l), d->c.eps, M, H, a8, a8s, st)))
                 return r;
             GemmArgs g;
@@ -626,14 +636,18 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             g.K = (int)H;
             g.C = qkv;
             g.ldc = (int)(3 * H);
+            g.keep_slices = ks_qkv > 1;
             if ((r = launch_gemm(g, st))) return r;
-            // q and k stay unrotated in qkv: the attention's prep pass rotates
-            // them and writes the rotated K and raw V rows to the cache
-            // (positions 0..S-1)
-            if ((r = launch_attention_prefill(qkv, qkv + H, qkv + 2 * H, att, (int)S, (int)NH,
+            g.keep_slices = false;
+            // q and k stay unrotated: the attention's prep pass rotates them
+            // and writes the rotated K and raw V rows to the cache (positions
+            // 0..S-1)
+            const float *qb = ks_qkv > 1 ? gwork : qkv;
+            const Slices qs = ks_qkv > 1 ? Slices{gwork, ks_qkv, M * 3 * H, d->Sqkv(l)} : Slices{};
+            if ((r = launch_attention_prefill(qb, qb + H, qb + 2 * H, att, (int)S, (int)NH,
                                               (int)(3 * H), (int)H, d->c.attn_scale, true, kvw,
                                               st, true, d->rope_step, 0.0f, (int)B, S * 3 * H,
-                                              S * H, d->Kc(l), d->Vc(l), (int)d->hs)))
+                                              S * H, d->Kc(l), d->Vc(l), (int)d->hs, qs)))
                 return r;
             if ((r = launch_rows_q8(att, H, nullptr, 0.0f, M, H, a8, a8s, st))) return r;
             GemmArgs go = g;
@@ -642,9 +656,11 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             go.N = (int)H;
             go.C = o;
             go.ldc = (int)H;
+            go.keep_slices = ks_o > 1;
             if ((r = launch_gemm(go, st))) return r;
             // h2 = h + o, then the post-attention norm
-            if ((r = launch_rows_q8(h2, H, d->PostLn(l), d->c.eps, M, H, a8, a8s, st, h, o)))
+            const Slices os = ks_o > 1 ? Slices{gwork, ks_o, M * H, d->So(l)} : Slices{};
+            if ((r = launch_rows_q8(h2, H, d->PostLn(l), d->c.eps, M, H, a8, a8s, st, h, o, os)))
                 return r;
             GemmArgs ggu = g;
             ggu.W = d->Wgu(l);
@@ -663,6 +679,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             gd.N = (int)H;
             gd.C = o;
             gd.ldc = (int)H;
+            gd.keep_slices = ks_d > 1 && l + 1 < d->L;  // the last layer's is reduced into o
             if ((r = launch_gemm(gd, st))) return r;
         }
         // the last layer's residual add (the others are in the next input norm)
