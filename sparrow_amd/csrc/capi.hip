@@ -674,7 +674,7 @@ int vmlm_hip_topk_idx(const float *src, size_t rows, size_t cols, float *dst, vo
     VMLM_GUARD(rows > 0 && cols > 0, "TOPK_IDX: src or dst slot has width 0");
     hipStream_t st = as_stream(stream);
     Stage stg(st);
-    unsigned long long *keys = stg.alloc<unsigned long long>(1);
+    unsigned long long *keys = stg.alloc<unsigned long long>(ARGMAX_KEYS);
     STAGE_OK(stg);
     return launch_argmax(src, cols, dst, nullptr, keys, st);
 }
@@ -1025,7 +1025,7 @@ int vmlm_topk_idx(const float *src, size_t rows, size_t cols, float *dst) {
     {
         Stage stg(st);
         float *ds = stg.upload(src, cols), *dd = stg.alloc<float>(1);
-        unsigned long long *keys = stg.alloc<unsigned long long>(1);
+        unsigned long long *keys = stg.alloc<unsigned long long>(ARGMAX_KEYS);
         STAGE_OK(stg);
         int rc = launch_argmax(ds, cols, dd, nullptr, keys, st);
         if (!rc) rc = download(dst, dd, sizeof(float), st);

@@ -271,8 +271,9 @@ int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld,
 int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
                     const float *rowf, const int32_t *rowi, int n, hipStream_t st);
 // OP_TOPK_IDX over one row of cols values: index of the largest non-NaN value,
-// lowest index on ties, 0 when x[0] is NaN or every value is; keys: one
-// 64-bit device word of workspace.
+// lowest index on ties, 0 when x[0] is NaN or every value is; keys:
+// ARGMAX_KEYS 64-bit device words of workspace.
+constexpr int ARGMAX_KEYS = 4096;
 int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
                   unsigned long long *keys, hipStream_t st);
 

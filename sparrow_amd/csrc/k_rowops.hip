@@ -914,32 +914,31 @@ __device__ __forceinline__ void am_merge(float &bv, int &bi, float v, int i) {
     }
 }
 
-// The row is split over many workgroups: each thread scans AM_E values
-// (loads issued together, index clamped), the wave reduces (value, index)
-// pairs with the strict-`>` / lowest-index rule, and one 64-bit atomicMax per
-// wave folds the order-preserving key into keys[0] (max is order-independent,
-// so the result is deterministic). A single-thread kernel clears the key
-// before and turns it into the index after.
+// Two launches. The row is split over at most ARGMAX_KEYS / 4 workgroups:
+// each thread scans AM_E values per sweep (loads issued together, index
+// clamped), the wave reduces (value, index) pairs with the strict-`>` /
+// lowest-index rule and writes its order-preserving 64-bit key (0: no
+// candidate) to keys[wave]. One workgroup then takes the largest key (a max,
+// so the order of the waves does not matter) and turns it into the index.
 constexpr int AM_E = 8;
 
-__global__ void argmax_clear_kernel(unsigned long long *keys) { keys[0] = 0ull; }
-
 __global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restrict__ src, int cols,
-                                                          unsigned long long *keys) {
+                                                          unsigned long long *__restrict__ keys) {
     const int stride = gridDim.x * 256;
-    const int i0 = blockIdx.x * 256 + threadIdx.x;
-    float v[AM_E];
-#pragma unroll
-    for (int e = 0; e < AM_E; ++e) {
-        const int i = i0 + e * stride;
-        v[e] = src[i < cols ? i : cols - 1];
-    }
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    for (int i0 = blockIdx.x * 256 + threadIdx.x; i0 < cols; i0 += AM_E * stride) {
+        float v[AM_E];
 #pragma unroll
-    for (int e = 0; e < AM_E; ++e) {
-        const int i = i0 + e * stride;
-        if (i < cols && v[e] == v[e]) am_merge(bv, bi, v[e], i);
+        for (int e = 0; e < AM_E; ++e) {
+            const int i = i0 + e * stride;
+            v[e] = src[i < cols ? i : cols - 1];
+        }
+#pragma unroll
+        for (int e = 0; e < AM_E; ++e) {
+            const int i = i0 + e * stride;
+            if (i < cols && v[e] == v[e]) am_merge(bv, bi, v[e], i);
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -947,13 +946,26 @@ __global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restric
         const int oi = __shfl_xor(bi, o, 64);
         am_merge(bv, bi, ov, oi);
     }
-    if ((threadIdx.x & 63) == 0 && bi != 0x7fffffff) atomicMax(keys, argmax_key(bv, (uint32_t)bi));
+    if ((threadIdx.x & 63) == 0)
+        keys[blockIdx.x * 4 + (threadIdx.x >> 6)] =
+            bi != 0x7fffffff ? argmax_key(bv, (uint32_t)bi) : 0ull;
 }
 
-__global__ void argmax_final_kernel(const float *__restrict__ src,
-                                    const unsigned long long *__restrict__ keys, float *dst_f,
-                                    int32_t *dst_i) {
-    const unsigned long long k = keys[0];
+__global__ __launch_bounds__(256) void argmax_final_kernel(
+    const float *__restrict__ src, const unsigned long long *__restrict__ keys, int nkeys,
+    float *dst_f, int32_t *dst_i) {
+    __shared__ unsigned long long sk[4];
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x; i < nkeys; i += 256) k = keys[i] > k ? keys[i] : k;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long ok = __shfl_xor(k, o, 64);
+        k = ok > k ? ok : k;
+    }
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < 4; ++w) k = sk[w] > k ? sk[w] : k;
     const float x0 = src[0];
     const int bi = (x0 != x0 || k == 0ull) ? 0 : argmax_key_index(k);  // NaN at 0, or all NaN
     if (dst_f) dst_f[0] = (float)bi;
@@ -962,11 +974,11 @@ __global__ void argmax_final_kernel(const float *__restrict__ src,
 
 int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
                   unsigned long long *keys, hipStream_t st) {
-    VMLM_GUARD(cols >= 1 && cols <= 0x7fffffffu, "TOPK_IDX: %zu values", cols);
-    const unsigned nwg = (unsigned)cdiv(cols, (size_t)256 * AM_E);
-    argmax_clear_kernel<<<1, 1, 0, st>>>(keys);
+    VMLM_GUARD(cols >= 1 && cols <= 0x7f000000u, "TOPK_IDX: %zu values", cols);
+    const size_t want = (size_t)cdiv(cols, (size_t)256 * AM_E);
+    const unsigned nwg = (unsigned)(want < ARGMAX_KEYS / 4 ? want : ARGMAX_KEYS / 4);
     argmax_keys_kernel<<<nwg, 256, 0, st>>>(src, (int)cols, keys);
-    argmax_final_kernel<<<1, 1, 0, st>>>(src, keys, dst_f, dst_i);
+    argmax_final_kernel<<<1, 256, 0, st>>>(src, keys, (int)nwg * 4, dst_f, dst_i);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

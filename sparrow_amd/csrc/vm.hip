@@ -617,7 +617,7 @@ int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weig
         if ((e = hipMalloc((void **)pp, bytes + 64)) != hipSuccess) return bad(hip_fail(e, "arena"));
         if ((rc = launch_fill_zero(*pp, bytes + 64, vm->st))) return bad(rc);
     }
-    if ((e = hipMalloc((void **)&vm->keys, 64)) != hipSuccess) return bad(hip_fail(e, "vm keys"));
+    if ((e = hipMalloc((void **)&vm->keys, ARGMAX_KEYS * sizeof(unsigned long long))) != hipSuccess) return bad(hip_fail(e, "vm keys"));
     if ((e = hipStreamSynchronize(vm->st)) != hipSuccess) return bad(hip_fail(e, "vm load"));
     *out = vm;
     return VMLM_OK;
