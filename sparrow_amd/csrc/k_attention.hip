@@ -22,15 +22,22 @@
 namespace vmlm {
 
 // ---------------------------------------------------------------- f32 GEMM
-// C[m,n] (+)= A[m,k] . op(B), op(B) = B[n,k]^T (nt) or B[k,n].
-// 64x64 tiles, 256 threads of 4x4 outputs, 64-deep k-steps through LDS
-// (As[k][row], Bs[k][col]); the next step's tiles are loaded into registers
-// while the current one is consumed. With VEC the rows are read as float4
-// (k, or n for an NN B, a multiple of 4 and 16-byte aligned operands).
-// A narrow output is split over k (grid z): each slice writes its partial
-// tile to `part` [ks][m][n] and gemm_f32_reduce_kernel sums the slices in
-// order (deterministic).
-constexpr int GF_T = 64, GF_K = 64, GF_LD = 68;
+// C[m,n] (+)= A[m,k] . op(B), op(B) = B[n,k]^T (nt) or B[k,n], on the f32
+// matrix cores: v_mfma_f32_16x16x4f32 multiplies f32 operands exactly and
+// accumulates in f32 (only the summation order differs from the reference's
+// FMA chains, inside the 1e-4 * RMS contract of the attention composition).
+// 32 x 32 tiles, four waves of 16 x 16 (lane (g, r) = (lane / 16, lane % 16)
+// gives A[row r][k g] and op(B)[k g][col r] and holds rows 4g..4g+3 of column
+// r). 64-deep k-steps through LDS: A as [row][k], an NT B as [col][k], an NN
+// B as [k][col]; the next step's tiles are loaded into registers while the
+// current one is consumed. With VEC the rows are read as float4 (k, or n for
+// an NN B, a multiple of 4 and 16-byte aligned operands). A grid of few tiles
+// is split over k (grid z): each slice writes its partial tile to `part`
+// [ks][m][n] and gemm_f32_reduce_kernel sums the slices in order
+// (deterministic).
+constexpr int GF_T = 32, GF_K = 64;
+constexpr int GF_LDA = GF_K + 4;   // [row][k] pitch (floats)
+constexpr int GF_LDB = GF_T + 16;  // [k][col] pitch: lanes (g, r) two-way at most
 
 template <bool NT, bool VEC>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float *__restrict__ A,
@@ -38,111 +45,74 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float *__restrict__
                                                        float *__restrict__ C, int m, int n, int k,
                                                        int acc, int kslice,
                                                        float *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) float As[GF_K][GF_LD];
-    __shared__ __attribute__((aligned(16))) float Bs[GF_K][GF_LD];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    __shared__ __attribute__((aligned(16))) float As[GF_T][GF_LDA];
+    __shared__ __attribute__((aligned(16))) float Bs[NT ? GF_T : GF_K][NT ? GF_LDA : GF_LDB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 4, r = lane & 15;
     const int row0 = blockIdx.y * GF_T, col0 = blockIdx.x * GF_T;
     const int kb = blockIdx.z * kslice;
     const int ke = kb + kslice < k ? kb + kslice : k;
-    // loader roles: A (and an NT B) as 64 rows x 16 float4 of k; an NN B as
-    // 64 k-rows x 16 float4 of n; 4 pieces per thread
-    float4 ra[4], rb[4];
+    auto ld4 = [&](const float *p, bool ok, int left) {
+        if constexpr (VEC) {
+            return ok && left >= 4 ? *(const float4 *)p : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            return make_float4(ok && left > 0 ? p[0] : 0.f, ok && left > 1 ? p[1] : 0.f,
+                               ok && left > 2 ? p[2] : 0.f, ok && left > 3 ? p[3] : 0.f);
+        }
+    };
+    // loader roles (two float4 per thread and operand): A and an NT B as 32
+    // rows x 16 float4 of k; an NN B as 64 k-rows x 8 float4 of n
+    float4 ra[2], rb[2];
     auto load = [&](int k0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = tid + q * 256, r = e >> 4, c4 = (e & 15) * 4;
-            const int gk = k0 + c4;
-            {
-                const int gr = row0 + r;
-                const float *pa = A + (size_t)(gr < m ? gr : 0) * k + gk;
-                if constexpr (VEC) {
-                    ra[q] = gr < m && gk < ke ? *(const float4 *)pa : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    ra[q].x = gr < m && gk < ke ? pa[0] : 0.f;
-                    ra[q].y = gr < m && gk + 1 < ke ? pa[1] : 0.f;
-                    ra[q].z = gr < m && gk + 2 < ke ? pa[2] : 0.f;
-                    ra[q].w = gr < m && gk + 3 < ke ? pa[3] : 0.f;
-                }
-            }
+        for (int q = 0; q < 2; ++q) {
+            const int e = tid + q * 256, rr = e >> 4, c4 = (e & 15) * 4, gk = k0 + c4;
+            const int gr = row0 + rr;
+            ra[q] = ld4(A + (size_t)(gr < m ? gr : 0) * k + (gk < ke ? gk : kb), gr < m, ke - gk);
             if constexpr (NT) {
-                const int gc = col0 + r;
-                const float *pb = B + (size_t)(gc < n ? gc : 0) * k + gk;
-                if constexpr (VEC) {
-                    rb[q] = gc < n && gk < ke ? *(const float4 *)pb : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    rb[q].x = gc < n && gk < ke ? pb[0] : 0.f;
-                    rb[q].y = gc < n && gk + 1 < ke ? pb[1] : 0.f;
-                    rb[q].z = gc < n && gk + 2 < ke ? pb[2] : 0.f;
-                    rb[q].w = gc < n && gk + 3 < ke ? pb[3] : 0.f;
-                }
+                const int gc = col0 + rr;
+                rb[q] = ld4(B + (size_t)(gc < n ? gc : 0) * k + (gk < ke ? gk : kb), gc < n, ke - gk);
             } else {
-                const int gkr = k0 + r, gc = col0 + c4;
-                const float *pb = B + (size_t)(gkr < ke ? gkr : kb) * n + gc;
-                if constexpr (VEC) {
-                    rb[q] = gkr < ke && gc < n ? *(const float4 *)pb : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    rb[q].x = gkr < ke && gc < n ? pb[0] : 0.f;
-                    rb[q].y = gkr < ke && gc + 1 < n ? pb[1] : 0.f;
-                    rb[q].z = gkr < ke && gc + 2 < n ? pb[2] : 0.f;
-                    rb[q].w = gkr < ke && gc + 3 < n ? pb[3] : 0.f;
-                }
+                const int kr = e >> 3, n4 = (e & 7) * 4, gkr = k0 + kr, gc = col0 + n4;
+                rb[q] = ld4(B + (size_t)(gkr < ke ? gkr : kb) * n + (gc < n ? gc : 0), gkr < ke,
+                            n - gc);
             }
         }
     };
     auto store = [&]() {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = tid + q * 256, r = e >> 4, c4 = (e & 15) * 4;
-            As[c4][r] = ra[q].x;
-            As[c4 + 1][r] = ra[q].y;
-            As[c4 + 2][r] = ra[q].z;
-            As[c4 + 3][r] = ra[q].w;
-            if constexpr (NT) {
-                Bs[c4][r] = rb[q].x;
-                Bs[c4 + 1][r] = rb[q].y;
-                Bs[c4 + 2][r] = rb[q].z;
-                Bs[c4 + 3][r] = rb[q].w;
-            } else {
-                *(float4 *)&Bs[r][c4] = rb[q];
-            }
+        for (int q = 0; q < 2; ++q) {
+            const int e = tid + q * 256, rr = e >> 4, c4 = (e & 15) * 4;
+            *(float4 *)&As[rr][c4] = ra[q];
+            if constexpr (NT) *(float4 *)&Bs[rr][c4] = rb[q];
+            else *(float4 *)&Bs[e >> 3][(e & 7) * 4] = rb[q];
         }
     };
-    float c[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c[i][j] = 0.0f;
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
     load(kb);
     for (int k0 = kb; k0 < ke; k0 += GF_K) {
         __syncthreads();
         store();
         __syncthreads();
         if (k0 + GF_K < ke) load(k0 + GF_K);
-#pragma unroll 16
-        for (int kk = 0; kk < GF_K; ++kk) {
-            const float4 a = *(const float4 *)&As[kk][ty * 4];
-            const float4 b = *(const float4 *)&Bs[kk][tx * 4];
-            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) c[i][j] = __builtin_fmaf(av[i], bv[j], c[i][j]);
+        for (int kk = 0; kk < GF_K; kk += 4) {
+            const float a = As[wm * 16 + r][kk + g];
+            const float b = NT ? Bs[wn * 16 + r][kk + g] : Bs[kk + g][wn * 16 + r];
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, d, 0, 0, 0);
         }
     }
+    const int gc = col0 + wn * 16 + r;
+    if (gc >= n) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int gr = row0 + ty * 4 + i;
+    for (int q = 0; q < 4; ++q) {
+        const int gr = row0 + wm * 16 + 4 * g + q;
         if (gr >= m) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int gc = col0 + tx * 4 + j;
-            if (gc >= n) continue;
-            if (part) {
-                part[((size_t)blockIdx.z * m + gr) * n + gc] = c[i][j];
-            } else {
-                float *o = C + (size_t)gr * n + gc;
-                *o = acc ? *o + c[i][j] : c[i][j];
-            }
+        if (part) {
+            part[((size_t)blockIdx.z * m + gr) * n + gc] = d[q];
+        } else {
+            float *o = C + (size_t)gr * n + gc;
+            *o = acc ? *o + d[q] : d[q];
         }
     }
 }
