@@ -737,8 +737,9 @@ def main():
     if args.no_batch1:
         print(json.dumps({"probe": "decode", "batch": args.batch,
                           "tokens_per_s": round(args.batch * args.steps / wall, 2),
-                          "roofline_frac": roof["frac"], "decode_attention": attn,
-                          "prefill": prefill}))
+                          "roofline_frac": roof["frac"],
+                          "gemv_us": {k: v["us"] for k, v in roof["per_shape"].items()},
+                          "decode_attention": attn, "prefill": prefill}))
         return
 
     if args.batch == 1:

@@ -392,44 +392,45 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
         rowf = segf * (1.0f / sqrtf(ss + p.eps));
     }
 
-    i32x4 acc[TW][Q8_T];
+    // the B fragments of every block and term, then the tiles one at a time
+    // in load order: a tile's partial row is stored as soon as its weights
+    // have arrived and been multiplied, so the stores overlap the later
+    // tiles' loads instead of following the whole load stream
+    i32x4 b[KB][Q8_T];
 #pragma unroll
-    for (int t = 0; t < TW; ++t)
-#pragma unroll
-        for (int q = 0; q < Q8_T; ++q) acc[t][q] = i32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-        i32x4 b[Q8_T];
+    for (int i = 0; i < KB; ++i)
 #pragma unroll
         for (int q = 0; q < Q8_T; ++q) {
             const uint2 lo = *(const uint2 *)&as8[q][n][i * 64 + 8 * g];
             const uint2 hi = *(const uint2 *)&as8[q][n][i * 64 + 32 + 8 * g];
-            b[q] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            b[i][q] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
         }
+    float *yr = p.Y + ((size_t)blockIdx.y * p.M + n) * p.ldy;
 #pragma unroll
-        for (int t = 0; t < TW; ++t) {
+    for (int t = 0; t < TW; ++t) {
+        i32x4 acc[Q8_T];
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q) acc[q] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
             const i32x4 a = __builtin_bit_cast(i32x4, wr[t][i]);
 #pragma unroll
             for (int q = 0; q < Q8_T; ++q)
-                acc[t][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[q], acc[t][q], 0, 0, 0);
+                acc[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[i][q], acc[q], 0, 0, 0);
         }
-    }
-    if (n < p.M) {
-        float *yr = p.Y + ((size_t)blockIdx.y * p.M + n) * p.ldy;
-#pragma unroll
-        for (int t = 0; t < TW; ++t) {
-            const int tl = tile0 + t;
-            if (tl >= (p.N >> 4)) continue;
+        const int tl = tile0 + t;
+        if (n < p.M && tl < (p.N >> 4)) {
             f32x4 v;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float f = (float)acc[t][0][j];
+                float f = (float)acc[0][j];
 #pragma unroll
-                for (int u = 1; u < Q8_T; ++u) f = f + (float)acc[t][u][j] * q8_term_weight(u);
+                for (int u = 1; u < Q8_T; ++u) f = f + (float)acc[u][j] * q8_term_weight(u);
                 v[j] = f * rowf;
             }
             *(f32x4 *)(yr + tl * 16 + 4 * g) = v;
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
