@@ -269,8 +269,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
 // (q8_term_weight), times the row factor and the column scale. No int8 ->
 // bf16 conversion, and Q8_T MFMAs of 8 passes per k-step against six for
 // three bf16 terms.
-template <int BM, int BN, int NS, bool WB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_i8_kernel(GemmParams p) {
+template <int BM, int BN, int NS, bool WB, int OCC = 2>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_dma_i8_kernel(GemmParams p) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int ROW = 64;  // bytes of a row-major W row in LDS (64 k of int8)
@@ -495,7 +495,14 @@ static int launch_i8(const GemmParams &p, bool wb, int ksl, bool keep, hipStream
     constexpr int stage = Q8_T * BM * 64 + BN * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
     const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, ksl);
-    if (wb)
+    // two stages over blocked weights: registers for four workgroups per CU
+    // (128 VGPRs, the LDS holds four 40 KiB rings); 2 % faster than three at
+    // the prefill's q/k/v and gate/up shapes, where 128 x 256 tiles of eight
+    // waves (one workgroup per CU, two to four stages) measured 7 to 14 %
+    // slower than either
+    if (wb && NS == 2)
+        gemm_dma_i8_kernel<BM, BN, NS, true, 4><<<grid, 256, 0, st>>>(p);
+    else if (wb)
         gemm_dma_i8_kernel<BM, BN, NS, true><<<grid, 256, 0, st>>>(p);
     else
         gemm_dma_i8_kernel<BM, BN, NS, false><<<grid, 256, 0, st>>>(p);

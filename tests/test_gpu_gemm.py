@@ -133,3 +133,26 @@ def test_gemm_int8_row_split_paths_agree(dev):
     ok = np.isfinite(ref).all(axis=1)
     for r in np.flatnonzero(ok)[:40]:
         assert_close_rms(g257[r], ref[r])
+
+
+@pytest.mark.parametrize("m,n", [(2048, 4096),    # 32 x 32 tiles of 64 x 128
+                                 (2100, 4112)])   # ragged last tile row and column
+def test_gemm_int8_many_tiles_exact(dev, m, n):
+    """A large grid over blocked weights (M >= 256 swizzles the caller's
+    weights; two LDS stages, four workgroups per CU). Integer activations
+    give exact int8 terms and exact f32 sums, so the result is the float64
+    product bit for bit; the ragged case clamps the copies of column tiles
+    past the weights and stores only rows < M and columns < N. A NaN row goes
+    through the f32 recomputation."""
+    k = 256
+    rng = np.random.default_rng(m + n)
+    a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    a[m - 1, 7] = np.nan
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = np.ones(n, np.float32)
+    da, dq, ds, dc = dev.up(a), dev.up(q), dev.up(s), dev.empty(m * n * 4)
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, dc, m, n, k, None))
+    got = dev.down(dc, (m, n), np.float32)
+    ref = a[:m - 1].astype(np.float64) @ q.astype(np.float64).T
+    np.testing.assert_array_equal(got[:m - 1].astype(np.float64), ref)
+    assert np.isnan(got[m - 1]).all()
