@@ -499,13 +499,14 @@ static int launch_i8(const GemmParams &p, bool wb, int ksl, bool keep, hipStream
     // (128 VGPRs, the LDS holds four 40 KiB rings); 2 % faster than three at
     // the prefill's q/k/v and gate/up shapes, where 128 x 256 tiles of eight
     // waves (one workgroup per CU, two to four stages) measured 7 to 14 %
-    // slower than either
-    if (wb && NS == 2)
-        gemm_dma_i8_kernel<BM, BN, NS, true, 4><<<grid, 256, 0, st>>>(p);
-    else if (wb)
-        gemm_dma_i8_kernel<BM, BN, NS, true><<<grid, 256, 0, st>>>(p);
-    else
+    // slower than either; 64 x 64 tiles (five workgroups per CU) 20 to 60 %
+    // slower: below 64 x 128 the copy bytes per MFMA set the time
+    if (!wb)
         gemm_dma_i8_kernel<BM, BN, NS, false><<<grid, 256, 0, st>>>(p);
+    else if constexpr (NS == 2)
+        gemm_dma_i8_kernel<BM, BN, NS, true, 4><<<grid, 256, 0, st>>>(p);
+    else
+        gemm_dma_i8_kernel<BM, BN, NS, true><<<grid, 256, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     if (ksl == 1 || keep) return VMLM_OK;
     return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
