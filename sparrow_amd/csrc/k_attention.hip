@@ -847,15 +847,20 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
     float pv[PART ? PART_KS_MAX : 1];
     float wsc = 0.f;
     if constexpr (PART) {
-        // threads 0..191 each own one of the head's q/k/v columns and load
-        // every k-slice partial of it (index clamped) before the cache rows
-        const int c = tid < 192 ? tid : 191;
-        const int pcol = (c >> 6) * a.H * 64 + h * 64 + (c & 63);
-        const float *pp = a.part + (size_t)b * a.ldp + pcol;
-        wsc = a.wscale[pcol];
-        const size_t pst = (size_t)B * a.ldp;
+        // threads 0..191 (waves 0-2) each own one of the head's q/k/v
+        // columns and load every k-slice partial of it before the cache
+        // rows; the branches on the wave and the slice count are uniform
 #pragma unroll
-        for (int k = 0; k < PART_KS_MAX; ++k) pv[k] = pp[(k < a.ks ? k : a.ks - 1) * pst];
+        for (int k = 0; k < PART_KS_MAX; ++k) pv[k] = 0.0f;
+        if (tid < 192) {
+            const int pcol = (tid >> 6) * a.H * 64 + h * 64 + (tid & 63);
+            const float *pp = a.part + (size_t)b * a.ldp + pcol;
+            wsc = a.wscale[pcol];
+            const size_t pst = (size_t)B * a.ldp;
+#pragma unroll
+            for (int k = 0; k < PART_KS_MAX; ++k)
+                if (k < a.ks) pv[k] = pp[k * pst];
+        }
     } else {
         const float *qr = a.q + (size_t)b * a.ldq + h * 64;
         const float *kr = a.k_new + (size_t)b * a.ldq + h * 64;
