@@ -228,8 +228,7 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 // One wave per (segment, row): the residual add of a k-split projection and
 // the int8 input of the next k-slice GEMVs (see launch_resid_q8). Lane l
 // holds columns 4c..4c+3 of the segment, c = l + 64i (i < SI); all slices of
-// a column are loaded up front (index clamped) so the reads take one round
-// trip. The segment's power-of-two factor comes from its own max |x * g|.
+// a column are loaded up front so the reads take one round trip. The segment's power-of-two factor comes from its own max |x * g|.
 template <int SI, int KSN>
 __global__ __launch_bounds__(64) void resid_q8_kernel(
     const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
@@ -250,9 +249,9 @@ __global__ __launch_bounds__(64) void resid_q8_kernel(
         if (ks > 0) {
             float4 pv[KSN];
 #pragma unroll
-            for (int k = 0; k < KSN; ++k) {
-                const int kk = k < ks ? k : ks - 1;
-                pv[k] = *(const float4 *)(part + ((size_t)kk * rows + row) * ldp + col);
+            for (int k = 0; k < KSN; ++k) {  // the slices there are (a uniform branch)
+                pv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k < ks) pv[k] = *(const float4 *)(part + ((size_t)k * rows + row) * ldp + col);
             }
             const float4 sc = *(const float4 *)(scale + col);
             float4 acc = pv[0];
@@ -313,7 +312,7 @@ int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const
                "resid_q8: aligned rows and outputs");
     const dim3 grid((unsigned)(cols / seg), (unsigned)rows);
     // slice loads sized to the slice count of the decoder's projections (9
-    // for K = 2304, 15 for K = 5760), else 4 or 16 with the index clamped
+    // for K = 2304, 15 for K = 5760), else 4 or 16 (loads past ks skipped)
 #define RQ_LAUNCH(SI, KSN)                                                                      \
     resid_q8_kernel<SI, KSN><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g,        \
                                                   (int)cols, (int)rows, seg, q8, q8s, ssp)
@@ -354,10 +353,13 @@ __global__ __launch_bounds__(128) void silu_q8_kernel(const float *__restrict__ 
     const int jg = (jo >> 4) * 32 + (jo & 15), ju = jg + 16;  // gate/up tiles interleave by 16
     float4 gv[KSN], uv[KSN];
 #pragma unroll
-    for (int k = 0; k < KSN; ++k) {
-        const float *pr = part + ((size_t)(k < ks ? k : ks - 1) * rows + row) * ldp;
-        gv[k] = *(const float4 *)(pr + jg);
-        uv[k] = *(const float4 *)(pr + ju);
+    for (int k = 0; k < KSN; ++k) {  // the slices there are (a uniform branch)
+        gv[k] = uv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < ks) {
+            const float *pr = part + ((size_t)k * rows + row) * ldp;
+            gv[k] = *(const float4 *)(pr + jg);
+            uv[k] = *(const float4 *)(pr + ju);
+        }
     }
     const float4 sg = *(const float4 *)(sgu + jg), su = *(const float4 *)(sgu + ju);
     float4 ga = gv[0], ua = uv[0];
