@@ -806,7 +806,6 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
                                                               int gsub) {
     extern __shared__ float spart[];  // [nsub][AD_PART] when this workgroup merges
     __shared__ float qs[64], kn[64], vn[64];
-    __shared__ float qkv_s[PART ? 192 : 1];
     // the cache rows are streamed once per step: nontemporal loads
     constexpr int KV_POLICY = BUF_NT;
     const int h = blockIdx.x, b = blockIdx.y;
@@ -872,31 +871,37 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
     int s = s0 + wave;
     load(ka, va, live(s));
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (PART) {  // slices summed in order, then the row scale
-        float v = pv[0];
+    const float fpos = (float)pos;
+    if constexpr (PART) {
+        // slices summed in order, then the column scale; wave 0 holds q, wave
+        // 1 k, wave 2 v, one column per lane: each lane of waves 0 and 1
+        // takes its RoPE partner (column l ^ 32) by a lane swap and keeps its
+        // own half of the rotated pair (l32, l32 + 32)
+        if (tid < 192) {
+            float v = pv[0];
 #pragma unroll
-        for (int k = 1; k < PART_KS_MAX; ++k)
-            if (k < a.ks) v += pv[k];
-        if (tid < 192) qkv_s[tid] = v * wsc;
-        __syncthreads();
-        q1 = qkv_s[l32];
-        q2 = qkv_s[l32 + 32];
-        k1 = qkv_s[64 + l32];
-        k2 = qkv_s[96 + l32];
-        vnew = qkv_s[128 + lane];
-    }
-    if (wave == 0) {
-        if (lane < 32) {
-            const float fpos = (float)pos;
-            float y1, y2;
-            rope_pair(q1, q2, fpos, lane, a.step, &y1, &y2);
-            qs[lane] = y1;
-            qs[lane + 32] = y2;
-            rope_pair(k1, k2, fpos, lane, a.step, &y1, &y2);
-            kn[lane] = y1;
-            kn[lane + 32] = y2;
+            for (int k = 1; k < PART_KS_MAX; ++k)
+                if (k < a.ks) v += pv[k];
+            v = v * wsc;
+            if (wave < 2) {
+                const float o = lane_xor32(v);
+                const bool lo = lane < 32;
+                float y1, y2;
+                rope_pair(lo ? v : o, lo ? o : v, fpos, l32, a.step, &y1, &y2);
+                (wave == 0 ? qs : kn)[lane] = lo ? y1 : y2;
+            } else {
+                vn[lane] = v;
+            }
         }
-        vn[lane] = vnew;
+    } else {  // q rotated by wave 0, k by wave 1
+        if (wave < 2 && lane < 32) {
+            float y1, y2;
+            rope_pair(wave == 0 ? q1 : k1, wave == 0 ? q2 : k2, fpos, lane, a.step, &y1, &y2);
+            float *dst = wave == 0 ? qs : kn;
+            dst[lane] = y1;
+            dst[lane + 32] = y2;
+        }
+        if (wave == 0) vn[lane] = vnew;
     }
     __syncthreads();
     if (tid < 64 && blockIdx.z == 0) {  // append the new row (no wave reads row `pos` from the cache)
