@@ -94,8 +94,15 @@ struct FkArgs {
     int M = 1, N = 0, K = 0;
     int epi = FK_STORE;
     int kb = 0;  // 64-wide k-blocks per wave (2, 3, 4, 6, 8); 0 = chosen by shape
+    // optional (M = 1, K = heads x 64): the input row as the attention's
+    // FK_APART position-range partials per head [K/64][FK_APART][68]
+    // (DecodeArgs::frac), merged in order here instead of term planes
+    const float *apart = nullptr;
 };
+constexpr int FK_APART = 4;  // position ranges per head of the attention partials
 bool fk_gemv_ok(int M, int N, int K, int epi);
+// an o projection of input width K can take the attention's range partials
+bool fk_apart_ok(int K);
 int launch_fk_gemv(const FkArgs &a, hipStream_t st);
 // Rows h [M][ldh] entering the fused path: terms of h * g into [3][M][ldt]
 // and the partial sums of squares [N/16][M].
@@ -317,6 +324,13 @@ struct DecodeArgs {
     // workgroup per pair; -1: chosen by the launcher. The result is the same
     // bits for every choice.
     int split = -1;
+    // optional (one sequence, device or host position): the cached positions
+    // split into `frac` ranges of about equal size, one workgroup each, which
+    // merges its range in LDS and writes (max, sum, O[64]) as one partial
+    // [B][H][frac][68] to fpart instead of the output; the consumer merges
+    // the frac partials of a head in order (launch_fk_gemv's apart)
+    int frac = 0;
+    float *fpart = nullptr;
 };
 // `work` (attention_decode_work_floats() floats, 0 when the positions are
 // not split) holds the sub-chunk partials of a split launch.

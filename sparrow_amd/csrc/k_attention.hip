@@ -814,9 +814,20 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
     const int grp = lane >> 4, q = lane & 15;
     const int pos = a.posp ? *a.posp : a.pos;
     const int nsub = pos / AD_SUB + 1;
-    const int s0 = spp ? (int)blockIdx.z * spp : 0;
-    const int s1 = spp ? min(s0 + spp, nsub) : nsub;
-    if (s0 >= s1) return;  // a partition past the cached positions (never z = 0)
+    const int z = (int)blockIdx.z, nf = SPLIT ? 0 : a.frac;
+    // spp: fixed partitions of spp sub-chunks; nf: nf ranges of about equal
+    // size, [ceil(z nsub / nf), ceil((z + 1) nsub / nf)) -- range 0 is never
+    // empty, so its workgroup always appends the new row
+    const int s0 = nf ? (z * nsub + nf - 1) / nf : spp ? z * spp : 0;
+    const int s1 = nf ? ((z + 1) * nsub + nf - 1) / nf : spp ? min(s0 + spp, nsub) : nsub;
+    if (s0 >= s1) {  // a partition past the cached positions (never z = 0)
+        if (nf && tid < 64) {  // an empty range: max -inf, sum 0, O 0
+            float *fp = a.fpart + (((size_t)b * a.H + h) * nf + z) * AD_PART;
+            if (tid == 0) *(float2 *)fp = make_float2(-INFINITY, 0.0f);
+            fp[4 + tid] = 0.0f;
+        }
+        return;
+    }
     const size_t head = ((size_t)b * a.H + h) * (a.hs ? a.hs : a.cap) * 64;
 
     // Cache rows through buffer loads whose range ends at row `pos`: rows at
@@ -977,7 +988,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
             if (lane == 0) *(float2 *)pc = make_float2(mc, lc);
             if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
         } else {
-            float *pc = spart + sc_ * AD_PART;
+            float *pc = spart + (sc_ - s0) * AD_PART;
             if (lane == 0) *(float2 *)pc = make_float2(mc, lc);
             if (grp == 0) *(float4 *)&pc[4 + 4 * q] = o;
         }
@@ -993,12 +1004,19 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_kernel(DecodeArgs a, floa
     }
     if constexpr (SPLIT) return;  // merged by attn_decode_merge_kernel
     __syncthreads();
-    const float M = partial_max(spart, nsub);  // every wave, the same value
-    for (int c = tid; c < nsub; c += NW * 64) spart[c * AD_PART + 2] = exp_f(spart[c * AD_PART] - M);
+    const int nloc = s1 - s0;  // this workgroup's sub-chunks (all of them unless nf)
+    const float M = partial_max(spart, nloc);  // every wave, the same value
+    for (int c = tid; c < nloc; c += NW * 64) spart[c * AD_PART + 2] = exp_f(spart[c * AD_PART] - M);
     __syncthreads();
     if (tid >= 64) return;
     float L = 0.0f, O = 0.0f;
-    merge_partials(spart, nsub, tid, L, O);
+    merge_partials(spart, nloc, tid, L, O);
+    if (nf) {  // the range's partial, merged with the others by the consumer
+        float *fp = a.fpart + (((size_t)b * a.H + h) * nf + z) * AD_PART;
+        if (tid == 0) *(float2 *)fp = make_float2(M, L);
+        fp[4 + tid] = O;
+        return;
+    }
     decode_store(O / L, h * 64 + tid, b, out, ldo, terms, T, ldt, B);
 }
 
@@ -1080,7 +1098,17 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
     VMLM_GUARD(!a.part || (a.ks >= 1 && a.ks <= PART_KS_MAX && a.wscale && a.ldp >= 3 * a.H * 64),
                "attention decode: partial q/k/v need ks, ldp and scales");
     const int gsub = (a.cap + AD_SUB - 1) / AD_SUB;
-    const int spp = decode_spp(a, B);
+    const int spp = a.frac > 0 ? 0 : decode_spp(a, B);
+    if (a.frac > 0) {
+        VMLM_GUARD(a.fpart && !a.part && a.frac <= 64 && (size_t)gsub * AD_PART * sizeof(float) <= AD_LDS_MAX,
+                   "attention decode: position ranges need the partial buffer, rows (not slices) "
+                   "of q/k/v, at most 64 ranges and a capacity within one workgroup's LDS");
+        const dim3 grid(a.H, B, a.frac);
+        launch_decode_nw<4>(a, B, out, ldo, terms, T, ldt, st, grid,
+                            (size_t)gsub * AD_PART * sizeof(float), 0, nullptr, gsub);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     if (spp > 0) {
         VMLM_GUARD(work, "attention decode: split positions need a work buffer of %zu floats",
                    attention_decode_work_floats(a, B));

@@ -68,6 +68,7 @@ struct FkParams {
     float *ssp_out;     // FK_RESID: partial sums of squares of Y, [N / 16][M]
     int M, N, K;
     int epi;
+    const float *apart; // AP: the attention's position-range partials [K/64][FK_APART][68]
 };
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -102,7 +103,13 @@ __device__ __forceinline__ float row16_sum(float v) {
 // and takes its B fragments from there, instead of 2 KB fragment loads on
 // the live lanes (measured 0.3 - 0.9 us per launch faster at the MiniCPM-2B
 // shapes).
-template <int KB, int WPT, int TPW, bool BL>
+// AP (one input row, the o projection): the run's KB heads arrive as the
+// attention's FK_APART position-range partials (max m, sum l, O[64]) each;
+// every wave merges its heads in range order -- M = max m, f = exp_f(m - M),
+// L = sum l f, O = sum O f (FMAs in range order), y = O / L -- and writes the
+// three bf16 terms of y into its LDS slot, which the attention would
+// otherwise have written to the term planes.
+template <int KB, int WPT, int TPW, bool BL, bool AP = false>
 __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
     constexpr int NTH = WPT * 64;
     constexpr int RUN = KB * 64;              // bf16 of one term plane in a k-run
@@ -129,8 +136,21 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
     // the other columns of the MFMA hold whatever the registers held and are
     // never read: each output column depends on its own B column only.
     u32x4 av[KB][2];
-    u32x4 bq[BL ? PQ : 1];
-    if constexpr (BL) {  // piece e: plane e / (RUN / 8), bf16 8 (e % (RUN / 8)) of the run
+    u32x4 bq[BL && !AP ? PQ : 1];
+    float ap_o[AP ? KB : 1][FK_APART];
+    float2 ap_ml[AP ? KB : 1][FK_APART];
+    if constexpr (AP) {  // head j of the run: range z's O[lane], (m, l)
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const int hd = kb0 + j < nkb ? kb0 + j : nkb - 1;
+#pragma unroll
+            for (int z = 0; z < FK_APART; ++z) {
+                const float *pz = p.apart + ((size_t)hd * FK_APART + z) * 68;
+                ap_o[j][z] = pz[4 + lane];
+                ap_ml[j][z] = *(const float2 *)pz;
+            }
+        }
+    } else if constexpr (BL) {  // piece e: plane e / (RUN / 8), bf16 8 (e % (RUN / 8)) of the run
 #pragma unroll
         for (int q = 0; q < PQ; ++q) {
             int e = lane + 64 * q;
@@ -209,10 +229,45 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
     }
 
     if constexpr (BL) {  // the run into the wave's LDS slot, then the live lanes' fragments
+        if constexpr (AP) {
+            // the KB x FK_APART weights e^{m - M} in one exp_f: lane
+            // j * FK_APART + z takes (j, z), then each weight is read back
+            // as a wave-uniform value
+            float xm = 0.0f;
 #pragma unroll
-        for (int q = 0; q < PQ; ++q) {
-            const int e = lane + 64 * q;
-            if (e < PCS) *(u32x4 *)&bs[wave][e * 8] = bq[q];
+            for (int j = 0; j < KB; ++j) {
+                float M = ap_ml[j][0].x;
+#pragma unroll
+                for (int z = 1; z < FK_APART; ++z) M = fmaxf(M, ap_ml[j][z].x);
+#pragma unroll
+                for (int z = 0; z < FK_APART; ++z)
+                    if (lane == j * FK_APART + z) xm = ap_ml[j][z].x - M;
+            }
+            const float ex = exp_f(xm);
+#pragma unroll
+            for (int j = 0; j < KB; ++j) {
+                float L = 0.0f, O = 0.0f;
+#pragma unroll
+                for (int z = 0; z < FK_APART; ++z) {
+                    const float f = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j * FK_APART + z));
+                    L = __builtin_fmaf(ap_ml[j][z].y, f, L);
+                    O = __builtin_fmaf(ap_o[j][z], f, O);
+                }
+                float y = O / L;
+#pragma unroll
+                for (int t = 0; t < FK_T; ++t) {
+                    const uint32_t hb = bf16_rne_bits(y);
+                    y = term_rem(y, hb);
+                    bs[wave][t * RUN + j * 64 + lane] = (uint16_t)hb;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < PQ; ++q) {
+                const int e = lane + 64 * q;
+                if (e < PCS) *(u32x4 *)&bs[wave][e * 8] = bq[q];
+            }
         }
         if (live) {
 #pragma unroll
@@ -553,7 +608,13 @@ __global__ void swizzle_w_kernel(const uint8_t *__restrict__ src, uint8_t *__res
 template <int KB, int WPT, int TPW>
 int launch_fk_t(const FkParams &p, hipStream_t st) {
     const unsigned grid = (unsigned)(p.N / 16 / TPW);
-    if (p.M == 1)
+    if (p.apart) {
+        if constexpr ((KB == 2 || KB == 3) && TPW == 1)  // fk_apart_ok: the o projection
+            fk_gemv_kernel<KB, WPT, TPW, true, true><<<grid, WPT * 64, 0, st>>>(p);
+        else
+            return fail(VMLM_ERR_UNIMPL, "fused GEMV: attention partials need runs of 2 or 3 "
+                                         "blocks and one tile");
+    } else if (p.M == 1)
         fk_gemv_kernel<KB, WPT, TPW, true><<<grid, WPT * 64, 0, st>>>(p);
     else
         fk_gemv_kernel<KB, WPT, TPW, false><<<grid, WPT * 64, 0, st>>>(p);
@@ -573,6 +634,11 @@ static int fk_kb(int nkb) {
     return 0;
 }
 
+bool fk_apart_ok(int K) {
+    const int kb = K % 64 ? 0 : fk_kb(K / 64);
+    return kb == 2 || kb == 3;
+}
+
 bool fk_gemv_ok(int M, int N, int K, int epi) {
     const int tpw = epi == FK_SILU ? 2 : 1;
     return M >= 1 && M <= 5 && K >= 64 && K % 64 == 0 && N % (16 * tpw) == 0 &&
@@ -587,6 +653,8 @@ int launch_fk_gemv(const FkArgs &a, hipStream_t st) {
     VMLM_GUARD(!a.ssp || (a.nssp >= 1 && a.nssp * a.M <= FK_SSPF && ((uintptr_t)a.ssp & 15) == 0),
                "fused GEMV: %d norm partials x %d rows", a.nssp, a.M);
     VMLM_GUARD(a.epi == FK_SILU ? a.Y || a.Aout : !!a.Y, "fused GEMV: no output");
+    VMLM_GUARD(!a.apart || (a.M == 1 && a.epi != FK_SILU && !a.ssp && ((uintptr_t)a.apart & 7) == 0),
+               "fused GEMV: attention partials go with one row, no input norm, no SiLU pair");
     VMLM_GUARD(!a.ssp_out || (a.epi == FK_RESID && a.Aout && a.gout),
                "fused GEMV: the norm partials out need FK_RESID, terms and the gain");
     FkParams p;
@@ -608,6 +676,7 @@ int launch_fk_gemv(const FkArgs &a, hipStream_t st) {
     p.N = a.N;
     p.K = a.K;
     p.epi = a.epi;
+    p.apart = a.apart;
     const bool pair = a.epi == FK_SILU;
     const int nkb = a.K / 64;
     const int kb = a.kb ? a.kb : fk_kb(nkb), w = (nkb + kb - 1) / kb;

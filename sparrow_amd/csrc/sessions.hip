@@ -112,6 +112,9 @@ struct vmlm_decoder {
     int8_t *act8 = nullptr;
     float *act8s = nullptr;
     int seg_i = 0;
+    // fused program at batch 1: the attention's position-range partials per
+    // head [NH][FK_APART][68], merged by the o projection
+    float *apart = nullptr;
     int32_t *tok = nullptr, *tokens_out = nullptr;
     unsigned long long *keys = nullptr;  // [B][KEY_SLOTS] argmax slots
     float *part = nullptr;               // k-slice partial sums of the decode GEMVs
@@ -239,6 +242,10 @@ DecodeArgs attn_args(vmlm_decoder *d, size_t l) {
         a.q = d->qkv;
         a.k_new = d->qkv + H;
         a.v_new = d->qkv + 2 * H;
+        if (d->B == 1 && fk_apart_ok(H)) {  // FK_APART workgroups per head, merged by the o projection
+            a.frac = FK_APART;
+            a.fpart = d->apart;
+        }
     } else {
         a.part = d->part;
         a.ks = d->ks_h;
@@ -318,6 +325,7 @@ FkArgs fk_args(vmlm_decoder *d, size_t l, int which) {
     case 1:
         f.W = d->Wo(l), f.scale = d->So(l), f.N = H, f.K = H;
         f.A = d->t_att;
+        if (d->B == 1 && fk_apart_ok(H)) f.apart = d->apart;  // the attention's range partials (attn_args)
         f.Y = d->h2, f.ldy = H, f.epi = FK_RESID, f.R = d->h, f.ldr = H;
         f.Aout = d->t_x, f.gout = d->PostLn(l), f.ssp_out = d->ssp;
         break;
@@ -447,6 +455,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->x8ssp, d->H / d->seg * d->B)) ||
         (rc = dalloc(d, &d->act8, (size_t)Q8_T * d->B * d->I)) ||
         (rc = dalloc(d, &d->act8s, d->I / d->seg_i * d->B)) ||
+        (rc = dalloc(d, &d->apart, d->NH * FK_APART * 68)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
