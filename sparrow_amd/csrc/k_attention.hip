@@ -651,7 +651,12 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
 // partials in LDS) or, with the positions split over several workgroups, by
 // attn_decode_merge_kernel from partials in global memory. Both merges are
 // the same arithmetic over the same partials, so the result does not depend
-// on how the positions are split.
+// on how the positions are split. A third form (DecodeArgs::frac, the
+// batch-1 decoder) splits a head's positions into a few ranges of about
+// equal size, merges each range in its workgroup and leaves one (max, sum,
+// O) partial per range, which the o projection merges in range order: a
+// two-level merge, within 1e-4 of the output RMS of the one-level result
+// but not the same bits.
 // Lane (grp, q) of a wave holds dims 4q..4q+3 of rows 16 s + 4 it + grp
 // (it = 0..3): one load instruction covers 4 consecutive 256-byte rows. Dot
 // products are summed over the 16 lanes of a row group with DPP and over
