@@ -101,7 +101,9 @@ def gemv_roofline(dec, iters):
             "traffic": measured_traffic(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE),
             "traffic_source": os.path.relpath(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE,
                                               ROOT),
-            "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues)"
+            "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues; "
+                       "at batch 1 the o projection also merges the attention's four "
+                       "position-range partials per head)"
                        if dec.fused else
                        "ks_gemv_i8_kernel (q/k/v, gate+up; int8 rows) and ks_gemv_kernel "
                        "(o, down); k-slice partials"),
