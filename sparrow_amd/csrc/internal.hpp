@@ -100,6 +100,7 @@ struct FkArgs {
     const float *apart = nullptr;
 };
 constexpr int FK_APART = 4;  // position ranges per head of the attention partials
+constexpr int ATTN_PART = 68;  // floats per attention partial: max, sum, 2 unused, O[64]
 bool fk_gemv_ok(int M, int N, int K, int epi);
 // an o projection of input width K can take the attention's range partials
 bool fk_apart_ok(int K);

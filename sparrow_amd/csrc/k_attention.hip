@@ -706,6 +706,7 @@ __device__ __forceinline__ float rows_to_uniform_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 constexpr int AD_PART = 68;             // floats per sub-chunk partial: m, l, f, pad, o[64]
+static_assert(AD_PART == ATTN_PART, "the range partials the o projection reads");
 constexpr int AD_SUB = 16;              // cached positions per sub-chunk (16, 32 or 64)
 constexpr int AD_NV = AD_SUB / 4;       // rows of a sub-chunk per lane
 constexpr int AD_RSH = AD_NV == 4 ? 2 : AD_NV == 8 ? 1 : 0;  // lane q holds row q >> AD_RSH

@@ -111,6 +111,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // otherwise have written to the term planes.
 template <int KB, int WPT, int TPW, bool BL, bool AP = false>
 __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
+    static_assert(!AP || (BL && KB * FK_APART <= 64), "one lane per (head, range) weight");
     constexpr int NTH = WPT * 64;
     constexpr int RUN = KB * 64;              // bf16 of one term plane in a k-run
     constexpr int PCS = FK_T * RUN / 8;        // its 16-byte pieces over the planes
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
             const int hd = kb0 + j < nkb ? kb0 + j : nkb - 1;
 #pragma unroll
             for (int z = 0; z < FK_APART; ++z) {
-                const float *pz = p.apart + ((size_t)hd * FK_APART + z) * 68;
+                const float *pz = p.apart + ((size_t)hd * FK_APART + z) * ATTN_PART;
                 ap_o[j][z] = pz[4 + lane];
                 ap_ml[j][z] = *(const float2 *)pz;
             }

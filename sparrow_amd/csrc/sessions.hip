@@ -455,7 +455,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->x8ssp, d->H / d->seg * d->B)) ||
         (rc = dalloc(d, &d->act8, (size_t)Q8_T * d->B * d->I)) ||
         (rc = dalloc(d, &d->act8s, d->I / d->seg_i * d->B)) ||
-        (rc = dalloc(d, &d->apart, d->NH * FK_APART * 68)) ||
+        (rc = dalloc(d, &d->apart, d->NH * FK_APART * ATTN_PART)) ||
         (d->fused && (rc = dalloc(d, &d->ssp, d->H / 16 * d->B))) ||
         (rc = dalloc(d, &d->h, d->B * d->H)) || (rc = dalloc(d, &d->h2, d->B * d->H)) ||
         (rc = dalloc(d, &d->qkv, d->B * 3 * d->H)) || (rc = dalloc(d, &d->att, d->B * d->H)) ||
