@@ -217,13 +217,13 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
     // replay over 40 layers' weights): q/k/v 2 x 8 (5.40 us; 2 x 4 5.36,
     // 4 x 4 5.64), gate/up 4 x 4 (7.90; 2 x 8 8.19), down 3 x 4 (5.46; 2 x 8
     // 6.08, 4 x 4 5.86), o 2 x 4. Swept again with the tiles stored one at a
-    // time: q/k/v 2 x 8 5.20 (4 x 4 5.09, 2 x 4 5.20, 1 x 8 5.58), gate/up
-    // 4 x 4 7.79-7.99 (2 x 8 8.00, 3 x 4 8.47), down 3 x 4 4.72 (2 x 8 5.26,
-    // 4 x 4 5.25)
+    // time: q/k/v 4 x 4 5.07-5.09 (2 x 8 5.18-5.20, 2 x 4 5.20, 1 x 8 5.58),
+    // gate/up 4 x 4 7.79-7.99 (2 x 8 8.00, 3 x 4 8.47), down 3 x 4 4.72
+    // (2 x 8 5.26, 4 x 4 5.25)
     if (g.A8) {
         const bool wide = N >= 4 * K, deep = K > N;
-        g.tw = wide ? 4 : deep ? 3 : 2;
-        g.nwv = wide || deep ? 4 : 8;
+        g.tw = wide ? 4 : deep ? 3 : 4;
+        g.nwv = 4;
     } else {
         g.tw = 2;
         g.nwv = K > (int)d->H ? 8 : 4;
