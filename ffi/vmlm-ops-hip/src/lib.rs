@@ -36,7 +36,7 @@
 #![no_std]
 #![allow(clippy::missing_safety_doc, clippy::too_many_arguments)]
 
-use core::ffi::{c_char, c_int};
+use core::ffi::{c_char, c_int, c_void};
 
 /// vmlm_sparse_conn_w: the fields of ops/src/conn.rs:8-53 `SparseConnW` in
 /// order, laid out for C.
@@ -51,6 +51,13 @@ pub struct SparseConnWC {
     pub src: *mut f32,
     pub src_u32: *mut u32,
     pub act: *mut f32,
+}
+
+/// The library's device-resident VM (`vmlm_vm` in include/vmlm_hip.h); only
+/// ever handled by pointer.
+#[repr(C)]
+pub struct VmRaw {
+    _opaque: [u8; 0],
 }
 
 /// vmlm_backend_t: sys/src/lib.rs:29-38 `Backend`, field for field.
@@ -98,6 +105,17 @@ extern "C" {
     fn vmlm_backend_max256(x: *const f32, n: usize) -> f32;
     fn vmlm_backend_sum256(x: *const f32, n: usize) -> f32;
     fn vmlm_backend_scale_mul(dst: *mut f32, src: *const f32, a: f32, n: usize);
+    fn vmlm_vm_load(image: *const u8, len: usize, weights: *const u8, weights_len: usize,
+                    out: *mut *mut VmRaw) -> c_int;
+    fn vmlm_vm_destroy(vm: *mut VmRaw) -> c_int;
+    fn vmlm_vm_run(vm: *mut VmRaw) -> c_int;
+    fn vmlm_vm_find_slot(vm: *const VmRaw, name: *const c_char, slot: *mut u32) -> c_int;
+    fn vmlm_vm_slot_info(vm: *mut VmRaw, slot: u32, dptr: *mut *mut c_void, rows: *mut u32,
+                         cols: *mut u32, dtype: *mut u8) -> c_int;
+    fn vmlm_vm_write_slot(vm: *mut VmRaw, slot: u32, host: *const f32, count: usize) -> c_int;
+    fn vmlm_vm_read_slot(vm: *mut VmRaw, slot: u32, host: *mut f32, count: usize) -> c_int;
+    fn vmlm_vm_output(vm: *mut VmRaw, host: *mut f32, cap: usize, count: *mut usize) -> c_int;
+    fn vmlm_vm_clear_output(vm: *mut VmRaw) -> c_int;
 }
 
 /// The interpreter's error convention: print the library's message and exit
@@ -250,3 +268,102 @@ pub fn hip_backend() -> HipBackend {
 //         vmlm_ops_hip::SparseConnWC { e: sc.e, k0: sc.k0, layer: sc.layer,
 //             n_neurons: sc.n_neurons, w: sc.w, src: sc.src, src_u32: sc.src_u32, act: sc.act }
 //     }
+
+// ---------------------------------------------------------------- device VM
+/// A `.vmb` program loaded onto the GPU: the counterpart of `Vm::load` +
+/// `Vm::run` (core/src/interp.rs:108-396, 720-2370). The constant pool is
+/// uploaded once (shared by every VM loaded over the same weights), the
+/// activation / state / gradient arenas live in HBM, and every opcode runs
+/// as GPU kernels on the VM's stream with the interpreter's guards. Failures
+/// take the interpreter's exit path through `check` with its exit codes
+/// (9 guard, 5 unimplemented op, 6 training op, 3 bad magic, 7 slot not
+/// found, 8 EW shape mismatch, 2 device).
+pub struct DeviceVm {
+    raw: *mut VmRaw,
+}
+
+impl DeviceVm {
+    /// `Vm::load(buf)` (core/src/interp.rs:108): parses the image, runs
+    /// `audit_const_dtypes` and `bind_slots`, uploads the CONST region.
+    pub unsafe fn load(image: *const u8, len: usize) -> DeviceVm {
+        let mut raw = core::ptr::null_mut();
+        check(vmlm_vm_load(image, len, core::ptr::null(), 0, &mut raw));
+        DeviceVm { raw }
+    }
+    /// `load_weights_mapped` (core/src/interp.rs:108-236): the constants come
+    /// from a separately mapped weights region, uploaded once per (pointer,
+    /// length) and shared; the caller keeps it unchanged while VMs use it.
+    pub unsafe fn load_mapped(image: *const u8, len: usize, weights: *const u8,
+                              weights_len: usize) -> DeviceVm {
+        let mut raw = core::ptr::null_mut();
+        check(vmlm_vm_load(image, len, weights, weights_len, &mut raw));
+        DeviceVm { raw }
+    }
+    /// `Vm::run` (core/src/interp.rs:720): runs to HALT, then prints every
+    /// value the program's PRINT instructions produced, in order, in the
+    /// interpreter's format (`print_f32`), before a failing status exits.
+    pub unsafe fn run(&mut self) {
+        let rc = vmlm_vm_run(self.raw);
+        self.flush_prints();
+        check(rc);
+    }
+    unsafe fn flush_prints(&mut self) {
+        let mut n = 0usize;
+        check(vmlm_vm_output(self.raw, core::ptr::null_mut(), 0, &mut n));
+        if n == 0 {
+            return;
+        }
+        let buf = vmlm_sys::mem::alloc(n * 4) as *mut f32;
+        let mut got = 0usize;
+        check(vmlm_vm_output(self.raw, buf, n, &mut got));
+        vmlm_sys::io::print_f32(buf, if got < n { got } else { n });
+        vmlm_sys::mem::dealloc(buf as *mut u8, n * 4);
+        check(vmlm_vm_clear_output(self.raw));
+    }
+    /// The slot named `name` (NUL-terminated), or None when the program
+    /// declares no such slot: the runtime's `slot_index` probe
+    /// (runtime/src/main.rs:160-190), which must not exit on a miss.
+    pub unsafe fn slot_index(&self, name: &[u8]) -> Option<u32> {
+        let mut slot = 0u32;
+        match vmlm_vm_find_slot(self.raw, name.as_ptr() as *const c_char, &mut slot) {
+            0 => Some(slot),
+            7 => None,
+            rc => {
+                check(rc);
+                None
+            }
+        }
+    }
+    /// `Vm::slot_shape` (rows, cols).
+    pub unsafe fn slot_shape(&self, slot: u32) -> (usize, usize) {
+        let (mut r, mut c) = (0u32, 0u32);
+        check(vmlm_vm_slot_info(self.raw, slot, core::ptr::null_mut(), &mut r, &mut c,
+                                core::ptr::null_mut()));
+        (r as usize, c as usize)
+    }
+    /// Device address of a slot (layer base applied), for callers that run
+    /// their own kernels on the VM's arenas.
+    pub unsafe fn slot_device_ptr(&self, slot: u32) -> *mut c_void {
+        let mut p = core::ptr::null_mut();
+        check(vmlm_vm_slot_info(self.raw, slot, &mut p, core::ptr::null_mut(),
+                                core::ptr::null_mut(), core::ptr::null_mut()));
+        p
+    }
+    /// Host f32 values into an activation / state / gradient slot: what
+    /// `load_ids` does through `slot_mut` (runtime/src/main.rs:209-247).
+    pub unsafe fn write_slot(&mut self, slot: u32, host: *const f32, count: usize) {
+        check(vmlm_vm_write_slot(self.raw, slot, host, count))
+    }
+    /// A slot's first `count` f32 values back to the host.
+    pub unsafe fn read_slot(&self, slot: u32, host: *mut f32, count: usize) {
+        check(vmlm_vm_read_slot(self.raw, slot, host, count))
+    }
+}
+
+impl Drop for DeviceVm {
+    fn drop(&mut self) {
+        unsafe {
+            vmlm_vm_destroy(self.raw);
+        }
+    }
+}

@@ -18,7 +18,7 @@ namespace vmlm {
 
 // ------------------------------------------------------------------ status
 // Sets the thread's last-error message and returns `code`.
-int fail(int code, const char *fmt, ...);
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t e, const char *what);
 
 #define VMLM_HIP_CHECK(expr)                                   \

@@ -276,8 +276,10 @@ int launch_scale(float *dst, const float *src, size_t n, float s, hipStream_t st
 // head h at column h*hd of a row of stride ld.
 int launch_rope(float *dst, const float *src, size_t rows, size_t hd, size_t ld, float theta,
                 float pos0, int heads, hipStream_t st);
+// `guard` (null: the library's flag) is raised for a bad row index.
 int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
-                    const float *rowf, const int32_t *rowi, int n, hipStream_t st);
+                    const float *rowf, const int32_t *rowi, int n, hipStream_t st,
+                    int *guard = nullptr);
 // OP_TOPK_IDX over one row of cols values: index of the largest non-NaN value,
 // lowest index on ties, 0 when x[0] is NaN or every value is; keys:
 // ARGMAX_KEYS 64-bit device words of workspace.

@@ -898,10 +898,10 @@ __global__ void emb_bf16_kernel(float *__restrict__ dst, size_t ldd,
 }
 
 int launch_emb_bf16(float *dst, size_t ldd, const uint16_t *table, size_t rows, size_t cols,
-                    const float *rowf, const int32_t *rowi, int n, hipStream_t st) {
+                    const float *rowf, const int32_t *rowi, int n, hipStream_t st, int *guard) {
     if (n == 0) return VMLM_OK;
     emb_bf16_kernel<<<n, 256, 0, st>>>(dst, ldd, table, rows, (int)cols, rowf, rowi,
-                                       guard_flag_ptr());
+                                       guard ? guard : guard_flag_ptr());
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

@@ -82,6 +82,10 @@ __device__ __forceinline__ long dev_index(const float *p, long limit, int *guard
     return u;
 }
 
+// Device guard codes (bits of the VM's guard flag), reported by run() with
+// the interpreter's message for the first in this order.
+enum VmGuard : int { VG_INDEX = 1, VG_OFFSETS = 2, VG_SEL = 4, VG_SRC = 8 };
+
 // Rust's `f as usize` (saturating: NaN and negatives give 0), the cast the
 // reference applies to f32-held offsets and ids before checking them.
 __device__ __forceinline__ size_t as_usize(float f) {
@@ -172,22 +176,22 @@ __global__ __launch_bounds__(256) void vm_copy2d_kernel(float *d, size_t dld, si
 // first element, then strict `>`) and GEMV (:815-827, s += a * b).
 __global__ __launch_bounds__(256) void vm_rowwise_kernel(float *d, const float *a, const float *b,
                                                          size_t r, size_t c, int op) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= r) return;
-    const float *row = a + i * c;
-    float s;
-    if (op == VOP_MAX) {
-        s = row[0];
-        for (size_t j = 1; j < c; ++j)
-            if (row[j] > s) s = row[j];
-    } else if (op == VOP_GEMV) {
-        s = 0.0f;
-        for (size_t j = 0; j < c; ++j) s += row[j] * b[j];
-    } else {
-        s = 0.0f;
-        for (size_t j = 0; j < c; ++j) s += row[j];
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < r; i += (size_t)gridDim.x * 256) {
+        const float *row = a + i * c;
+        float s;
+        if (op == VOP_MAX) {
+            s = row[0];
+            for (size_t j = 1; j < c; ++j)
+                if (row[j] > s) s = row[j];
+        } else if (op == VOP_GEMV) {
+            s = 0.0f;
+            for (size_t j = 0; j < c; ++j) s += row[j] * b[j];
+        } else {
+            s = 0.0f;
+            for (size_t j = 0; j < c; ++j) s += row[j];
+        }
+        d[i] = s;
     }
-    d[i] = s;
 }
 
 // SCALE (:1225-1235): d = a * s, s from the device.
@@ -214,15 +218,16 @@ __global__ void vm_rope_kernel(float *dst, const float *src, int rows, int hd, f
     const long pos = dev_index(posp, 1L << 24, guard);
     if (pos < 0) return;
     const int half = hd / 2;
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)rows * half) return;
-    const int row = (int)(idx / half), i = (int)(idx % half);
-    const float *sr = src + (size_t)row * hd;
-    float *dr = dst + (size_t)row * hd;
-    float y1, y2;
-    rope_pair(sr[i], sr[i + half], (float)pos + (float)row, i, step, &y1, &y2);
-    dr[i] = y1;
-    dr[i + half] = y2;
+    const size_t n = (size_t)rows * half, stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += stride) {
+        const int row = (int)(idx / half), i = (int)(idx % half);
+        const float *sr = src + (size_t)row * hd;
+        float *dr = dst + (size_t)row * hd;
+        float y1, y2;
+        rope_pair(sr[i], sr[i + half], (float)pos + (float)row, i, step, &y1, &y2);
+        dr[i] = y1;
+        dr[i + half] = y2;
+    }
 }
 
 // SOFTMAX with the live width read from the device: columns [0, live) as
@@ -261,27 +266,27 @@ __global__ __launch_bounds__(256) void vm_softmax_live_kernel(float *p, int cols
 __global__ __launch_bounds__(64) void vm_topk_thresh_kernel(float *d, const float *a, size_t r,
                                                             size_t c, size_t k,
                                                             unsigned char *used) {
-    const size_t i = (size_t)blockIdx.x * 64 + threadIdx.x;
-    if (i >= r) return;
-    const float *x = a + i * c;
-    unsigned char *u = used + i * c;
-    for (size_t j = 0; j < c; ++j) u[j] = 0;
-    float best = -__builtin_inff();
-    size_t found = 0;
-    while (found < k && found < c) {
-        long bi = -1;
-        float bv = -__builtin_inff();
-        for (size_t j = 0; j < c; ++j)
-            if (!u[j] && x[j] > bv) {
-                bv = x[j];
-                bi = (long)j;
-            }
-        if (bi < 0) break;
-        u[bi] = 1;
-        best = bv;
-        ++found;
+    for (size_t i = (size_t)blockIdx.x * 64 + threadIdx.x; i < r; i += (size_t)gridDim.x * 64) {
+        const float *x = a + i * c;
+        unsigned char *u = used + i * c;
+        for (size_t j = 0; j < c; ++j) u[j] = 0;
+        float best = -__builtin_inff();
+        size_t found = 0;
+        while (found < k && found < c) {
+            long bi = -1;
+            float bv = -__builtin_inff();
+            for (size_t j = 0; j < c; ++j)
+                if (!u[j] && x[j] > bv) {
+                    bv = x[j];
+                    bi = (long)j;
+                }
+            if (bi < 0) break;
+            u[bi] = 1;
+            best = bv;
+            ++found;
+        }
+        d[i] = best;
     }
-    d[i] = best;
 }
 
 // TOPK_BY_STRENGTH (:1743-1955) per row of L values (one thread each; the
@@ -294,40 +299,40 @@ __global__ __launch_bounds__(64) void vm_topk_strength_kernel(float *d, size_t d
                                                               size_t L, const float *kp,
                                                               size_t kmax, size_t kseg,
                                                               unsigned char *taken, int *guard) {
-    const size_t r = (size_t)blockIdx.x * 64 + threadIdx.x;
-    if (r >= rows) return;
     const float kf = *kp;
     const size_t k = as_usize(kf);
     if (!(kf >= 0.0f) || k > kmax) {
-        atomicOr(guard, 1);
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(guard, 1);
         return;
     }
-    const float *row = s + r * L;
-    unsigned char *t = taken + r * L;
-    for (size_t i = 0; i < L; ++i) t[i] = 0;
-    for (size_t q = 0; q < k; ++q) {
-        long best = -1;
-        float bv = 0.0f;
-        for (size_t i = 0; i < L; ++i) {
-            if (t[i]) continue;
-            const float v = row[i];
-            if (best < 0 || v > bv) {
-                bv = v;
-                best = (long)i;
+    for (size_t r = (size_t)blockIdx.x * 64 + threadIdx.x; r < rows; r += (size_t)gridDim.x * 64) {
+        const float *row = s + r * L;
+        unsigned char *t = taken + r * L;
+        for (size_t i = 0; i < L; ++i) t[i] = 0;
+        for (size_t q = 0; q < k; ++q) {
+            long best = -1;
+            float bv = 0.0f;
+            for (size_t i = 0; i < L; ++i) {
+                if (t[i]) continue;
+                const float v = row[i];
+                if (best < 0 || v > bv) {
+                    bv = v;
+                    best = (long)i;
+                }
             }
+            if (best < 0) break;
+            t[best] = 1;
         }
-        if (best < 0) break;
-        t[best] = 1;
+        float *out = d + r * dld;
+        size_t o = 0;
+        for (size_t i = 0; i < L && o < kseg; ++i)
+            if (t[i]) {
+                out[2 * o] = (float)i;
+                out[2 * o + 1] = row[i];
+                ++o;
+            }
+        for (; o < kseg; ++o) out[2 * o] = out[2 * o + 1] = 0.0f;
     }
-    float *out = d + r * dld;
-    size_t o = 0;
-    for (size_t i = 0; i < L && o < kseg; ++i)
-        if (t[i]) {
-            out[2 * o] = (float)i;
-            out[2 * o + 1] = row[i];
-            ++o;
-        }
-    for (; o < kseg; ++o) out[2 * o] = out[2 * o + 1] = 0.0f;
 }
 
 // SPARSE_MATVEC (:2058-2346), one thread per neuron j over its CSR row
@@ -338,52 +343,57 @@ __global__ __launch_bounds__(64) void vm_topk_strength_kernel(float *d, size_t d
 __global__ __launch_bounds__(64) void vm_sparse_matvec_kernel(
     float *d, const float *off, const float *src, const float *w, const float *x, size_t n,
     size_t nnz, size_t nx, const float *sel, size_t seg, unsigned *cnt, int *guard) {
-    const size_t j = (size_t)blockIdx.x * 64 + threadIdx.x;
-    if (j >= n) return;
-    cnt[j] = 0;
-    const size_t o0 = as_usize(off[j]), o1 = as_usize(off[j + 1]);
-    if (o1 > nnz || o0 > o1) {
-        atomicOr(guard, 1);
-        return;
-    }
-    if (o0 == o1) {
-        d[j] = 0.0f;
-        return;
-    }
-    float acc = 0.0f;
-    unsigned done = 0;
-    if (sel) {
-        for (size_t q = 0; q < seg; ++q) {
-            const size_t rel = as_usize(sel[(j * seg + q) * 2]);
-            if (q > 0 && rel == 0) break;
-            const size_t idx = o0 + rel;
-            if (idx < o0 || idx >= o1) {
-                atomicOr(guard, 1);
-                return;
-            }
-            const size_t sid = as_usize(src[idx]);
-            if (sid >= nx) {
-                atomicOr(guard, 1);
-                return;
-            }
-            const float term = w[idx] * x[sid];
-            acc = done == 0 ? term : acc + term;
-            ++done;
+    for (size_t j = (size_t)blockIdx.x * 64 + threadIdx.x; j < n; j += (size_t)gridDim.x * 64) {
+        cnt[j] = 0;
+        const size_t o0 = as_usize(off[j]), o1 = as_usize(off[j + 1]);
+        if (o1 > nnz || o0 > o1) {
+            atomicOr(guard, VG_OFFSETS);
+            continue;
         }
-    } else {
-        for (size_t t = o0; t < o1; ++t) {
-            const size_t sid = as_usize(src[t]);
-            if (sid >= nx) {
-                atomicOr(guard, 1);
-                return;
-            }
-            const float term = w[t] * x[sid];
-            acc = t == o0 ? term : acc + term;
-            ++done;
+        if (o0 == o1) {
+            d[j] = 0.0f;
+            continue;
         }
+        float acc = 0.0f;
+        unsigned done = 0;
+        int bad = 0;
+        if (sel) {
+            for (size_t q = 0; q < seg; ++q) {
+                const size_t rel = as_usize(sel[(j * seg + q) * 2]);
+                if (q > 0 && rel == 0) break;
+                const size_t idx = o0 + rel;
+                if (idx < o0 || idx >= o1) {
+                    bad = VG_SEL;
+                    break;
+                }
+                const size_t sid = as_usize(src[idx]);
+                if (sid >= nx) {
+                    bad = VG_SRC;
+                    break;
+                }
+                const float term = w[idx] * x[sid];
+                acc = done == 0 ? term : acc + term;
+                ++done;
+            }
+        } else {
+            for (size_t t = o0; t < o1; ++t) {
+                const size_t sid = as_usize(src[t]);
+                if (sid >= nx) {
+                    bad = VG_SRC;
+                    break;
+                }
+                const float term = w[t] * x[sid];
+                acc = t == o0 ? term : acc + term;
+                ++done;
+            }
+        }
+        if (bad) {
+            atomicOr(guard, bad);
+            continue;
+        }
+        d[j] = acc;
+        cnt[j] = done;
     }
-    d[j] = acc;
-    cnt[j] = done;
 }
 
 // The count of terms performed (FL_NNZ): d[0] = sum of cnt, one thread.
@@ -455,6 +465,7 @@ struct vmlm_vm {
     void *ws = nullptr;                            // executor workspace
     size_t ws_bytes = 0;
     unsigned long long *keys = nullptr;            // TOPK_IDX reduction keys
+    int *guard = nullptr;  // this VM's device guard flag (index checks on device data)
 };
 
 static uint32_t rd32(const uint8_t *p, size_t off) {
@@ -467,7 +478,8 @@ static void vm_free(vmlm_vm *vm) {
     if (!vm) return;
     if (vm->st) (void)hipStreamSynchronize(vm->st);
     pool_release(vm->pool);
-    for (void *p : {(void *)vm->act, (void *)vm->state, (void *)vm->grad, vm->ws, (void *)vm->keys})
+    for (void *p : {(void *)vm->act, (void *)vm->state, (void *)vm->grad, vm->ws, (void *)vm->keys,
+                    (void *)vm->guard})
         if (p) (void)hipFree(p);
     if (vm->st) (void)hipStreamDestroy(vm->st);
     delete vm;
@@ -618,6 +630,8 @@ int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weig
         if ((rc = launch_fill_zero(*pp, bytes + 64, vm->st))) return bad(rc);
     }
     if ((e = hipMalloc((void **)&vm->keys, ARGMAX_KEYS * sizeof(unsigned long long))) != hipSuccess) return bad(hip_fail(e, "vm keys"));
+    if ((e = hipMalloc((void **)&vm->guard, 64)) != hipSuccess) return bad(hip_fail(e, "vm guard"));
+    if ((rc = launch_fill_zero(vm->guard, 64, vm->st))) return bad(rc);
     if ((e = hipStreamSynchronize(vm->st)) != hipSuccess) return bad(hip_fail(e, "vm load"));
     *out = vm;
     return VMLM_OK;
@@ -986,7 +1000,7 @@ int Exec::step(const VmIns &in, size_t *ip) {
         P_(ca, a);
         P_(rowp, b);
         if (dt(a) == VDT_BF16)
-            return launch_emb_bf16(cd, c, (const uint16_t *)ca, r, c, rowp, nullptr, 1, st);
+            return launch_emb_bf16(cd, c, (const uint16_t *)ca, r, c, rowp, nullptr, 1, st, guard);
         NEED(dt(a) == VDT_F32, "EMB table dtype unsupported");
         vm_emb_f32_kernel<<<1, 256, 0, st>>>(cd, ca, r, c, rowp, guard);
         VMLM_HIP_CHECK(hipGetLastError());
@@ -1157,25 +1171,68 @@ int Exec::step(const VmIns &in, size_t *ip) {
 
 extern "C" {
 
+// The slot an instruction writes: `dst`, or `a` for LOOP_CNT (its counter)
+// and STACK_INIT; UINT32_MAX for instructions that write no slot.
+static uint32_t written_slot(const VmIns &in) {
+    switch (in.op) {
+    case VOP_SHAPE: case VOP_JMP: case VOP_CMPLE: case VOP_LAYERB: case VOP_PRINT:
+    case VOP_HALT: case VOP_LN_EPS:
+        return UINT32_MAX;
+    case VOP_LOOP_CNT: case VOP_STACK_INIT:
+        return in.a;
+    default:
+        return in.dst;
+    }
+}
+
+// A program may write a constant slot (the interpreter's slot_mut does not
+// distinguish kinds, core/src/interp.rs:477). In a private pool the write
+// lands in this VM's own copy and the host's cache of constant scalars is
+// dropped, so later CMPLE / LOOP_CNT / SCALE operands read the new value. A
+// pool shared over mapped weights is read-only, as the interpreter's mapped
+// pool is (cpool_readonly, :87, 2357-2362): such a write is refused with 9.
+static int const_write_check(vmlm_vm *vm, const VmIns &in, size_t at) {
+    const uint32_t w = written_slot(in);
+    if (w >= vm->slots.size() || vm->slots[w].kind != VSLOT_CONST) return VMLM_OK;
+    VMLM_GUARD(!vm->pool || !vm->pool->host,
+               "weights are mapped read-only: instruction %zu (op %u) writes constant slot %u", at,
+               (unsigned)in.op, w);
+    vm->kcache.clear();
+    return VMLM_OK;
+}
+
 int vmlm_vm_run(vmlm_vm *vm) {
     VMLM_GUARD(vm, "vm_run: null vm");
     int rc = ensure_init();
     if (rc) return rc;
-    // a device guard raised before this run is not this run's
-    if ((rc = vmlm_hip_check_guards())) (void)rc;
-    Exec ex{vm, guard_flag_ptr()};
+    // this VM's own guard flag: a guard raised by another VM or session on
+    // another stream is neither lost nor reported here
+    if ((rc = launch_fill_zero(vm->guard, sizeof(int), vm->st))) return rc;
+    Exec ex{vm, vm->guard};
     size_t ip = 0;
     const size_t n = vm->text.size();
     while (ip < n) {
         const VmIns in = vm->text[ip++];
         if (in.op == VOP_HALT) break;
-        if ((rc = ex.step(in, &ip))) {
+        if ((rc = const_write_check(vm, in, ip - 1)) || (rc = ex.step(in, &ip))) {
             (void)hipStreamSynchronize(vm->st);
             return rc;
         }
     }
+    int tripped = 0;
+    VMLM_HIP_CHECK(hipMemcpyAsync(&tripped, vm->guard, sizeof(int), hipMemcpyDeviceToHost, vm->st));
     VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
-    return vmlm_hip_check_guards();
+    if (tripped & VG_OFFSETS)
+        return fail(VMLM_ERR_GUARD, "SPARSE_MATVEC: offsets out of range (device check)");
+    if (tripped & VG_SEL)
+        return fail(VMLM_ERR_GUARD, "SPARSE_MATVEC: sel index outside its CSR row (device check)");
+    if (tripped & VG_SRC)
+        return fail(VMLM_ERR_GUARD, "SPARSE_MATVEC: src_id out of range (device check)");
+    if (tripped)
+        return fail(VMLM_ERR_GUARD,
+                    "device guard tripped (code %d): row, position or column index out of range",
+                    tripped);
+    return VMLM_OK;
 }
 
 int vmlm_vm_find_slot(const vmlm_vm *vm, const char *name, uint32_t *slot) {
@@ -1193,7 +1250,7 @@ int vmlm_vm_find_slot(const vmlm_vm *vm, const char *name, uint32_t *slot) {
 int vmlm_vm_slot_info(vmlm_vm *vm, uint32_t slot, void **dptr, uint32_t *rows, uint32_t *cols,
                       uint8_t *dtype) {
     VMLM_GUARD(vm, "vm_slot_info: null vm");
-    Exec ex{vm, guard_flag_ptr()};
+    Exec ex{vm, vm->guard};
     float *p;
     int rc = ex.ptr(slot, &p);
     if (rc) return rc;
@@ -1206,7 +1263,7 @@ int vmlm_vm_slot_info(vmlm_vm *vm, uint32_t slot, void **dptr, uint32_t *rows, u
 
 static int vm_xfer(vmlm_vm *vm, uint32_t slot, void *host, size_t count, bool write) {
     VMLM_GUARD(vm && (host || count == 0), "vm slot transfer: null argument");
-    Exec ex{vm, guard_flag_ptr()};
+    Exec ex{vm, vm->guard};
     float *p;
     int rc = ex.ptr(slot, &p);
     if (rc) return rc;

@@ -65,6 +65,15 @@ FL_WRITECOL_SLOT = 1 << 6      # WRITECOL: column offset from slot `dt`
 FL_SOFTMAX_LIVE = 1 << 6       # SOFTMAX: live width from slot `b` (columns past it are 0)
 
 
+def sparse_matvec_fl(wslot: int, nnz: bool = False, selgate: bool = False) -> int:
+    """The `fl` byte of SPARSE_MATVEC: the weight slot in bits 0..5, FL_NNZ
+    and FL_SELGATE above it. A weight slot past 63 does not fit, and the
+    reference's assembler refuses such a program (no image is written)."""
+    if not 0 <= wslot <= SPARSE_WSLOT_MASK:
+        raise ValueError(f"SPARSE_MATVEC: weight slot {wslot} does not fit fl bits 0..5")
+    return wslot | (FL_NNZ if nnz else 0) | (FL_SELGATE if selgate else 0)
+
+
 def hash32(name: str) -> int:
     """FNV-1a 32-bit (core/src/format.rs hash32)."""
     h = 0x811C9DC5

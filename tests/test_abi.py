@@ -74,6 +74,15 @@ def test_ffi_crate_matches_header():
     block = block[:block.index("\n}\n")]
     decls = re.findall(r"fn\s+(vmlm_\w+)\s*\(([^)]*)\)", block, flags=re.S)
     assert len(decls) >= 30
+    # the device VM's entry points, which the runtime's load -> run path binds
+    # (runtime/src/main.rs:136-153, 209-260)
+    vm_needed = {"vmlm_vm_load", "vmlm_vm_destroy", "vmlm_vm_run", "vmlm_vm_find_slot",
+                 "vmlm_vm_slot_info", "vmlm_vm_write_slot", "vmlm_vm_read_slot",
+                 "vmlm_vm_output", "vmlm_vm_clear_output"}
+    assert vm_needed <= {name for name, _ in decls}, vm_needed - {name for name, _ in decls}
+    for fn in ("pub unsafe fn load(", "pub unsafe fn run(", "pub unsafe fn slot_index(",
+               "pub unsafe fn write_slot(", "impl Drop for DeviceVm"):
+        assert fn in src, fn
     header = _header_params()
     L = C.CDLL(str(sparrow_amd.LIB_PATH))
     for name, args in decls:

@@ -263,3 +263,126 @@ def test_vm_shared_const_pool(gvm, tiny):
             v.write("st_tok", prompt)
             v.run()
         assert np.array_equal(bits(a.output()), bits(b.output()))
+
+
+def _counter_program():
+    """LOOP_CNT over a constant counter (3 rounds of acc += 1), then a SCALE
+    by a constant factor before and after a COPY writes that factor."""
+    P = vmb.Program()
+    n = P.scalar("n", 3.0)
+    one = P.scalar("one", 1.0)
+    f = P.scalar("f", 2.0)
+    x = P.const("x", np.float32([[1, 2, 3, 4]]))
+    acc = P.act("acc", 1, 1)
+    src = P.act("src", 1, 1)
+    out = P.act("out", 1, 4)
+    top = P.label()
+    P.ins("EWADD", acc, acc, one)
+    P.ins("LOOP_CNT", top, n)
+    P.ins("SCALE", out, x, f)      # f read while it is 2
+    P.ins("EWADD", src, acc, one)  # 4
+    P.ins("COPY", f, src)          # the constant f becomes 4
+    P.ins("SCALE", out, x, f)      # reads 4
+    P.ins("PRINT", acc)
+    P.ins("PRINT", out)
+    P.ins("HALT")
+    return P
+
+
+def test_vm_constant_slot_writes(gvm, oracle):
+    """A program may write constant slots (slot_mut makes no distinction,
+    core/src/interp.rs:477): LOOP_CNT on a constant counter runs its body
+    the counter's number of times, and a SCALE after a COPY into its constant
+    factor uses the new value, as in the oracle. Over constants shared through
+    mapped weights the write is refused with 9: the mapped pool is read-only
+    (cpool_readonly, :87, 2357-2362)."""
+    P = _counter_program()
+    (g, _), (o, _) = both(gvm, P)
+    assert np.array_equal(g, np.float32([3, 4, 8, 12, 16])) and np.array_equal(g, o)
+    img = P.build()
+    d = vmb.parse(img)
+    weights = np.frombuffer(img[d["const_off"]:d["const_off"] + d["const_len"]], np.uint8).copy()
+    from sparrow_amd import VmlmError
+    with gvm.Vm(img, weights) as v:
+        with pytest.raises(VmlmError) as e:
+            v.run()
+    assert e.value.code == 9 and "read-only" in str(e.value)
+
+
+def test_vm_guard_flag_is_per_vm(gvm):
+    """Each VM reports only its own device guards: a VM whose EMB row is out
+    of range exits 9; another VM run afterwards, and one run while the
+    library's own flag is raised by a device-API call, both succeed, and that
+    flag is still there for its owner to read."""
+    import ctypes as C
+
+    from sparrow_amd import VmlmError, lib
+
+    def emb_program(row):
+        P = vmb.Program()
+        t = P.const("t", np.arange(12, dtype=np.float32).reshape(4, 3))
+        r = P.scalar("r", float(row))
+        y = P.act("y", 1, 3)
+        P.ins("EMB", y, t, r)
+        P.ins("PRINT", y)
+        P.ins("HALT")
+        return P.build()
+
+    with gvm.Vm(emb_program(99)) as bad, gvm.Vm(emb_program(2)) as good:
+        with pytest.raises(VmlmError) as e:
+            bad.run()
+        assert e.value.code == 9
+        good.run()
+        assert np.array_equal(good.output(), np.float32([6, 7, 8]))
+        L = lib()
+        buf = [C.c_void_p() for _ in range(3)]
+        for p, n in zip(buf, (8, 4, 12)):
+            assert L.vmlm_hip_malloc(C.byref(p), n) == 0
+        row = np.float32([7.0])  # a 2-row table
+        assert L.vmlm_hip_memcpy_h2d(buf[1], row.ctypes.data, 4) == 0
+        assert L.vmlm_hip_emb_bf16(buf[2], buf[0], 2, 2, buf[1], None) == 0
+        assert L.vmlm_hip_sync() == 0
+        good.clear_output()
+        good.run()
+        assert np.array_equal(good.output(), np.float32([6, 7, 8]))
+        assert L.vmlm_hip_check_guards() == 9
+        assert L.vmlm_hip_check_guards() == 0
+        for p in buf:
+            L.vmlm_hip_free(p)
+
+
+def test_vm_row_kernels_past_one_grid(gvm):
+    """Row-per-thread VM kernels cover every row when there are more rows
+    than one launch's 65535 workgroups hold: SUM over 65535 x 256 + 1000 rows
+    of one value (each row's sum is its value) and SPARSE_MATVEC over
+    65535 x 64 + 1000 neurons of one connection each (y_j = w_j * x_j)."""
+    rng = np.random.default_rng(9)
+    n = 65535 * 256 + 1000
+    P = vmb.Program()
+    a = P.act("a", n, 1)
+    s = P.act("s", n, 1)
+    P.ins("SUM", s, a)
+    P.ins("HALT")
+    v = rng.standard_normal(n).astype(np.float32)
+    with gvm.Vm(P.build()) as g:
+        g.write("a", v)
+        g.run()
+        assert np.array_equal(bits(g.read("s").ravel()), bits(v))
+    m = 65535 * 64 + 1000
+    P = vmb.Program()
+    off = P.act("off", m + 1, 1)
+    src = P.act("src", m, 1)
+    w = P.act("w", m, 1)
+    x = P.act("x", m, 1)
+    y = P.act("y", m, 1)
+    P.ins("SPARSE_MATVEC", y, off, src, dt=x, fl=w)
+    P.ins("HALT")
+    wv = rng.standard_normal(m).astype(np.float32)
+    xv = rng.standard_normal(m).astype(np.float32)
+    with gvm.Vm(P.build()) as g:
+        g.write("off", np.arange(m + 1, dtype=np.float32))
+        g.write("src", np.arange(m, dtype=np.float32))
+        g.write("w", wv)
+        g.write("x", xv)
+        g.run()
+        assert np.array_equal(bits(g.read("y").ravel()), bits(wv * xv))

@@ -1,10 +1,16 @@
 """The allocation-free int8 GEMM (vmlm_hip_gemm_nt_int8_noalloc), through the
-C ABI, against the entry point it mirrors (vmlm_hip_gemm_nt_int8): both run
-the same kernels, so the outputs must be bitwise equal; both also stay
+C ABI, against the entry point it mirrors (vmlm_hip_gemm_nt_int8). Up to
+M = 255 both run the same kernels. From M = 256 (N a multiple of 16) the
+allocating call first swizzles the weights into 1 KiB blocks in its
+workspace and runs the blocked int8-row GEMM, while the allocation-free call
+keeps its scratch for the rows and runs the row-major form of the same GEMM
+(its own tile shapes); both sum each term's int8 products exactly in int32
+over the whole K (one k-slice at these grids) and combine them with the same
+arithmetic, so the outputs are bitwise equal in every case. Both also stay
 within 1e-4 x RMS of the CPU oracle. Two calls in a row share the scratch
-array, the second with a smaller input, then the int8-row path (M > 16),
-then a shape whose temporaries exceed the scratch, which must return 9
-without touching the output."""
+array, the second with a smaller input, then the int8-row paths (M > 16,
+M >= 256), then a shape whose temporaries exceed the scratch, which must
+return 9 without touching the output."""
 import ctypes as C
 
 import numpy as np
@@ -76,6 +82,8 @@ def test_noalloc_matches_gemm_nt_int8(dev, oracle):
     run_both(dev, oracle, 3, 1000, 1024, 2)    # smaller, right after
     run_both(dev, oracle, 40, 512, 2304, 3)    # int8 rows + ordered k-slices
     run_both(dev, oracle, 2, 70, 100, 4)       # K % 128 != 0: padded copy in scratch
+    run_both(dev, oracle, 256, 512, 2304, 6)   # M >= 256: blocked (allocating) vs row-major
+    run_both(dev, oracle, 300, 2304, 2304, 7)  # the same with ragged M
 
 
 def test_noalloc_rejects_oversized(dev):
