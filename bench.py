@@ -105,8 +105,8 @@ def gemv_roofline(dec, iters):
                        "at batch 1 the o projection also merges the attention's four "
                        "position-range partials per head)"
                        if dec.fused else
-                       "ks_gemv_i8_kernel (q/k/v, gate+up; int8 rows) and ks_gemv_kernel "
-                       "(o, down); k-slice partials"),
+                       "ks_gemv_i8_kernel (q/k/v, gate+up, down; int8 rows) and "
+                       "ks_gemv_kernel (o; bf16 terms); k-slice partials"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
             "timing": "graph replay of back-to-back launches (launch gaps included)",
             "read_floor_frac": round(rd_b / rd_t / 1e3 / HBM_PEAK_GBS, 4),
@@ -125,33 +125,52 @@ def decode_attention(dec, iters):
 
 
 def cpu_baseline(cfg, W, steps, threads):
-    """The oracle (C restatement of the reference kernels) decoding at batch 1
-    on the host: `steps` decode steps at positions 128.. of a KV cache whose
-    first 128 positions hold synthetic values (the step cost does not depend
-    on them)."""
+    """The oracle (C restatement of the reference kernels) decoding on the
+    host, at positions 129.. of a KV cache whose first 128 positions hold
+    synthetic values (the step cost does not depend on them):
+      - 1 thread, batch 1: the reference engine's execution model (a single
+        thread, core/src/lib.rs:2); this is `value`;
+      - `threads` OpenMP threads (rows split like par_for), batch 1;
+      - `threads` threads, batch 16: 16 sequences, one step each per batch
+        step (the oracle, like the reference's program, steps one sequence
+        at a time; each step appends its row at the same position of one
+        cache, which costs what 16 caches would)."""
     from oracle import oracle
-    oracle.set_threads(threads)
-    ref = oracle.DecoderOracle(W, cfg, cap=128 + steps + 1)
+    n1 = max(2, steps // 2)
+    ref = oracle.DecoderOracle(W, cfg, cap=128 + max(steps, n1) + 2)
     rng = np.random.default_rng(0)
     ref.kcache[:, :, :128, :] = rng.standard_normal(ref.kcache[:, :, :128, :].shape,
                                                     dtype=np.float32)
     ref.vcache[:, :, :128, :] = rng.standard_normal(ref.vcache[:, :, :128, :].shape,
                                                     dtype=np.float32)
-    ref.step(1, 128)  # warm-up (page in weights)
-    t = time.perf_counter()
-    tok = 2
-    for s in range(steps):
-        logits, _ = ref.step(tok, 129 + s)
-        tok = int(np.argmax(logits))
-    dt = time.perf_counter() - t
+
+    def rate(nthreads, nsteps, batch):
+        oracle.set_threads(nthreads)
+        ref.step(1, 128)  # warm-up (page in weights)
+        t = time.perf_counter()
+        tok = 2
+        for s in range(nsteps):
+            for b in range(batch):
+                logits, _ = ref.step((tok + 7919 * b) % cfg["vocab"], 129 + s)
+            tok = int(np.argmax(logits))
+        return nsteps * batch / (time.perf_counter() - t)
+
+    one = rate(1, n1, 1)
+    many = rate(threads, steps, 1)
+    many16 = rate(threads, max(1, steps // 8), 16)
     model, physical, logical = host_cpu()
-    return {"value": round(steps / dt, 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port", "batch": 1,
+    src = "oracle/vmlm_oracle.c (AVX2 restatement of ops/src/kernels.rs)"
+    return {"value": round(one, 3), "unit": "tokens/s", "cores": 1, "kind": "port", "batch": 1,
             "cpu_model": model, "host_physical_cores": physical, "host_logical_cpus": logical,
-            "sample": f"{steps} greedy decode steps, batch 1 (the oracle decodes one sequence "
-                      f"at a time), all 40 layers + LM head at the MiniCPM-2B shape, positions "
-                      f"129..{128 + steps}; oracle/vmlm_oracle.c (AVX2 restatement of "
-                      f"ops/src/kernels.rs), {threads} OpenMP threads on {model}"}
+            "sample": f"{n1} greedy decode steps, batch 1, 1 thread (the reference engine is "
+                      f"single-threaded), all 40 layers + LM head at the MiniCPM-2B shape, "
+                      f"positions 129..{128 + n1}; {src} on {model}",
+            "threads": {
+                "batch1": {"value": round(many, 3), "unit": "tokens/s", "cores": threads,
+                           "sample": f"{steps} steps, batch 1, {threads} OpenMP threads"},
+                "batch16": {"value": round(many16, 3), "unit": "tokens/s", "cores": threads,
+                            "sample": f"{max(1, steps // 8)} steps of 16 sequences, one "
+                                      f"sequence at a time, {threads} OpenMP threads"}}}
 
 
 def host_cpu():
@@ -187,27 +206,49 @@ Q8_TERMS = 3                # int8 terms per f32 activation in the int8-row path
 _LAST = ["eager"]  # how the last _timed call measured the GPU time
 
 
+INFINITY_CACHE = 256 << 20  # MI355X last-level (Infinity) cache
+
+
+def n_sets(set_bytes, iters):
+    """Buffer sets an HBM-bound row cycles through: enough that one graph
+    replay of `iters` calls streams more than twice the Infinity Cache, so
+    each call reads memory the previous ones did not leave cached (capped at
+    one set per call)."""
+    return max(1, min(iters, -(-2 * INFINITY_CACHE // max(1, set_bytes))))
+
+
+def cache_note(set_bytes, sets):
+    """How an HBM row was timed: cold (its calls cycle through more bytes
+    than the Infinity Cache holds, so a set is gone before its next use) or
+    warm (what it reads fits that cache)."""
+    tot = set_bytes * sets
+    if tot > INFINITY_CACHE:
+        return f"cold: calls cycle through {sets} buffer sets ({tot / 2**20:.0f} MiB)"
+    return (f"warm: {sets} buffer set(s), {tot / 2**20:.1f} MiB in all, fit the 256 MiB "
+            f"Infinity Cache")
+
+
 def _timed(L, fn, iters):
-    """Mean GPU time per call and host wall time per call.
+    """Mean GPU time per call and host wall time per call. `fn(i)` issues
+    call i (HBM-bound rows pick their buffer set from i).
 
     GPU time: `iters` calls captured into one HIP graph (after 3 warm-up
     calls, so every workspace is in place), the graph replayed for about
     30 ms of warm-up, then 5 times between HIP events on the library stream;
-    consecutive kernels keep their
-    in-graph launch gap. When a call's work cannot be captured as kernels
-    only, the GPU time is the event time around `iters` eager calls instead
-    (then bounded below by the host issue rate). Host time: the wall time per
-    eager call."""
+    consecutive kernels keep their in-graph launch gap. When a call's work
+    cannot be captured as kernels only, the GPU time is the event time around
+    `iters` eager calls instead (then bounded below by the host issue rate).
+    Host time: the wall time per eager call."""
     import ctypes as C
     from sparrow_amd import check
-    for _ in range(3):
-        check(fn())
+    for i in range(3):
+        check(fn(i))
     check(L.vmlm_hip_sync())
     e0, e1 = C.c_int(), C.c_int()
     check(L.vmlm_hip_event_record(None, C.byref(e0)))
     t = time.perf_counter()
-    for _ in range(iters):
-        check(fn())
+    for i in range(iters):
+        check(fn(i))
     check(L.vmlm_hip_event_record(None, C.byref(e1)))
     check(L.vmlm_hip_sync())
     wall = (time.perf_counter() - t) / iters * 1e6
@@ -220,8 +261,8 @@ def _timed(L, fn, iters):
     if L.vmlm_hip_capture_begin(None) != 0:
         return eager, wall
     rc = 0
-    for _ in range(iters):
-        rc = rc or fn()
+    for i in range(iters):
+        rc = rc or fn(i)
     if L.vmlm_hip_capture_end(None, C.byref(graph)) != 0 or rc or not graph.value:
         return eager, wall
     try:
@@ -295,6 +336,18 @@ def run_suite(iters, cpu=True):
         u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
         return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
+    def copies(p, nbytes, n):
+        """p and n - 1 device copies of its nbytes (the buffer sets an HBM
+        row cycles through)."""
+        out = [p]
+        for _ in range(n - 1):
+            q = C.c_void_p()
+            check(L.vmlm_hip_malloc(C.byref(q), nbytes))
+            check(L.vmlm_hip_memcpy_d2d(q, p, nbytes))
+            ptrs.append(q)
+            out.append(q)
+        return out
+
     out = {}
     # config 0: q8 GEMM X f32[16,2304] . (W i8[2304,2304] * scale)^T (+ the M=1 GEMV)
     rng = np.random.default_rng(0)
@@ -302,13 +355,20 @@ def run_suite(iters, cpu=True):
     x = rng.standard_normal((16, k), dtype=np.float32)
     q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
     sc = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
-    dx, dq, ds, dy = up(x), up(q), up(sc), zeros(16 * n * 4)
     cfg0 = {}
+    set0 = x.nbytes + q.nbytes + sc.nbytes + 16 * n * 4
+    ns0 = n_sets(set0, 10**9)
+    dx, dq, ds = copies(up(x), x.nbytes, ns0), copies(up(q), q.nbytes, ns0), \
+        copies(up(sc), sc.nbytes, ns0)
+    dy = [zeros(16 * n * 4) for _ in range(ns0)]
     for m, nbytes in ((16, 5612544), (1, 5336064)):
-        us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt_int8(dx, dq, ds, dy, m, n, k, None), iters)
+        us, wall = _timed(L, lambda i: L.vmlm_hip_gemm_nt_int8(dx[i % ns0], dq[i % ns0],
+                                                               ds[i % ns0], dy[i % ns0], m, n, k,
+                                                               None), max(iters, ns0))
         gbs = nbytes / us / 1e3
         cfg0[f"M{m}"] = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0], "bytes": nbytes,
-                         "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                         "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                         "cache": cache_note(set0, ns0)}
     if orc:
         cfg0["cpu_us_M16"] = _cpu_us(lambda: orc.gemm_nt_int8(x, q, sc))
         cfg0["cpu_threads"] = orc.get_threads()
@@ -318,19 +378,24 @@ def run_suite(iters, cpu=True):
     a = bf16(rng.standard_normal((1024, 512), dtype=np.float32))
     bt = bf16((rng.standard_normal((512, 2048), dtype=np.float32) / np.sqrt(512)).T)
     da, db, dc = up(a), up(bt), zeros(1024 * 2048 * 4)
-    us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, 1024, 2048, 512, None),
+    us, wall = _timed(L, lambda i: L.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, 1024, 2048, 512, None),
                       iters)
     tf = 2147483648 / us / 1e6
     out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0],
                              "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
     # config 1's M = 1 variant (the GEMV path of the same entry point)
-    us1, wall1 = _timed(L, lambda: L.vmlm_hip_gemm_nt_bf16bf16(da, db, dc, 1, 2048, 512, None),
-                        iters)
     b1 = 2048 * 512 * 2 + 512 * 2 + 2048 * 4
+    ns1 = n_sets(b1, 10**9)
+    db1 = copies(db, bt.nbytes, ns1)
+    dc1 = [zeros(2048 * 4) for _ in range(ns1)]
+    us1, wall1 = _timed(L, lambda i: L.vmlm_hip_gemm_nt_bf16bf16(da, db1[i % ns1], dc1[i % ns1], 1,
+                                                                 2048, 512, None),
+                        max(iters, ns1))
     out["cfg1_bf16_gemm"]["M1"] = {"us": round(us1, 2), "host_us": round(wall1, 2),
                                    "timing": _LAST[0], "bytes": b1,
                                    "GBps": round(b1 / us1 / 1e3, 1),
-                                   "frac_hbm": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4)}
+                                   "frac_hbm": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4),
+                                   "cache": cache_note(b1, ns1)}
     # the decoder's prefill projections at batch 16 (M = 2048 rows of f32
     # activations) through the device API: rows_q8 (the int8 terms of the
     # rows), the int8 x int8 MFMA GEMM and the non-finite-row check, per call
@@ -341,7 +406,7 @@ def run_suite(iters, cpu=True):
         wq = up(rng.integers(-127, 128, (n, k), dtype=np.int8))
         sq = up(np.full(n, 1e-3, np.float32))
         yq = zeros(2048 * n * 4)
-        usp, wallp = _timed(L, lambda: L.vmlm_hip_gemm_nt_int8(xp, wq, sq, yq, 2048, n, k, None),
+        usp, wallp = _timed(L, lambda i: L.vmlm_hip_gemm_nt_int8(xp, wq, sq, yq, 2048, n, k, None),
                             max(8, iters // 10))
         useful = 2 * 2048 * n * k / usp / 1e6
         pre[name] = {"us": round(usp, 2), "host_us": round(wallp, 2), "timing": _LAST[0],
@@ -360,20 +425,24 @@ def run_suite(iters, cpu=True):
     qkv_h = [rng.standard_normal((S, H * 64), dtype=np.float32) for _ in range(3)]
     qkv = [up(t) for t in qkv_h]
     do = zeros(S * H * 64 * 4)
-    us, wall = _timed(L, lambda: L.vmlm_hip_attention_prefill(qkv[0], qkv[1], qkv[2], do, S, H, 64,
+    us, wall = _timed(L, lambda i: L.vmlm_hip_attention_prefill(qkv[0], qkv[1], qkv[2], do, S, H, 64,
                                                              C.c_float(10000.0), 0,
                                                              C.c_float(0.125), True, None),
                       max(8, iters // 4))
     tf = 1210318848 / us / 1e6
     tm_prefill = _LAST[0]
     cap = 1024
-    kc = up(rng.standard_normal((H, cap, 64), dtype=np.float32))
-    vc = up(rng.standard_normal((H, cap, 64), dtype=np.float32))
+    kvb = H * cap * 64 * 4
+    ns2 = n_sets(2 * kvb, 10**9)
+    kc = copies(up(rng.standard_normal((H, cap, 64), dtype=np.float32)), kvb, ns2)
+    vc = copies(up(rng.standard_normal((H, cap, 64), dtype=np.float32)), kvb, ns2)
     qd, kd, vd = (up(rng.standard_normal(H * 64, dtype=np.float32)) for _ in range(3))
     dod = zeros(H * 64 * 4)
-    usd, walld = _timed(L, lambda: L.vmlm_hip_attention_decode(qd, kd, vd, kc, vc, dod, H, 64, cap,
+    usd, walld = _timed(L, lambda i: L.vmlm_hip_attention_decode(qd, kd, vd, kc[i % ns2],
+                                                              vc[i % ns2], dod, H, 64, cap,
                                                               cap - 1, C.c_float(10000.0),
-                                                              C.c_float(0.125), None), iters)
+                                                              C.c_float(0.125), None),
+                        max(iters, ns2))
     gbs = (18874368 + 18432) / usd / 1e3
     out["cfg2_attention"] = {
         "prefill": {"us": round(us, 2), "host_us": round(wall, 2), "timing": tm_prefill,
@@ -381,7 +450,8 @@ def run_suite(iters, cpu=True):
                     "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)},
         "decode": {"us": round(usd, 2), "host_us": round(walld, 2), "timing": _LAST[0],
                    "GBps": round(gbs, 1),
-                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}}
+                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                   "cache": cache_note(2 * kvb, ns2)}}
     if orc:
         out["cfg2_attention"]["prefill"]["cpu_us"] = _cpu_us(
             lambda: orc.attention_prefill(qkv_h[0], qkv_h[1], qkv_h[2], H, 10000.0, 0, 0.125,
@@ -396,13 +466,13 @@ def run_suite(iters, cpu=True):
     xb = up(rng.standard_normal((T, d), dtype=np.float32))
     yb = zeros(T * d * 4)
     arr = (type(layers[0].struct) * 8)(*[l.struct for l in layers])
-    us_fwd, wall_fwd = _timed(L, lambda: L.vmlm_b1_stack_forward(arr, 8, xb, yb, T, 4, None),
+    us_fwd, wall_fwd = _timed(L, lambda i: L.vmlm_b1_stack_forward(arr, 8, xb, yb, T, 4, None),
                               max(8, iters // 4))
     tm_fwd = _LAST[0]
     # the plan built once (vmlm_b1_stack_create): one kernel per forward,
     # captured and replayed
     plan = conn.StackPlan(layers)
-    us, wall = _timed(L, lambda: L.vmlm_b1_stack_run(plan._h, xb, yb, T, 4, None),
+    us, wall = _timed(L, lambda i: L.vmlm_b1_stack_run(plan._h, xb, yb, T, 4, None),
                       max(8, iters // 4))
     plan.close()
     layer_bytes = 12976128
@@ -419,6 +489,9 @@ def run_suite(iters, cpu=True):
                             "frac_valu_mac": round(tmac / VALU_MAC_PEAK_T, 4),
                             "note": "one kernel for all 8 layers over a plan built once "
                                     "(vmlm_b1_stack_create), x and y [T][d]",
+                            "cache": "warm: one buffer set replayed (x, y, 8 layers of w and "
+                                     "src, the plan: about 27 MB, within the Infinity Cache); "
+                                     "frac_hbm is over the unique bytes",
                             "per_call_forward": {"us": round(us_fwd, 2),
                                                  "host_us": round(wall_fwd, 2),
                                                  "timing": tm_fwd,
@@ -430,7 +503,7 @@ def run_suite(iters, cpu=True):
                                 T)
         out["cfg4_b1_stack"]["cpu_us_per_layer"] = _cpu_us(
             lambda: orc.b1_forward_t8(w0, s0, xt_h, T))
-    out["ops"] = run_ops(L, up, zeros, iters, orc)
+    out["ops"] = run_ops(L, up, zeros, copies, iters, orc)
     for l in layers:
         l.free()
     for p in ptrs:
@@ -438,17 +511,18 @@ def run_suite(iters, cpu=True):
     return out
 
 
-def run_ops(L, up, zeros, iters, orc):
+def run_ops(L, up, zeros, copies, iters, orc):
     """The per-op kernels of the VM path (RMSNorm, softmax, RoPE, activation,
     elementwise, scale, EMB, TOPK_IDX, f32 GEMM NT / NN) through the device
     API at decoder-sized shapes: time per call, algorithmic bytes (or flops)
     and the fraction of the roofline that bounds each; the oracle on the same
-    inputs beside it."""
+    inputs beside it. The HBM rows cycle through buffer sets larger than the
+    Infinity Cache (`cache` says how each was timed)."""
     import ctypes as C
     rng = np.random.default_rng(7)
     ops = {}
 
-    def rec(name, us, wall, nbytes=None, flops=None, cpu=None):
+    def rec(name, us, wall, nbytes=None, flops=None, cpu=None, cache=None):
         e = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0]}
         if nbytes is not None:
             gbs = nbytes / us / 1e3
@@ -458,59 +532,83 @@ def run_ops(L, up, zeros, iters, orc):
             tf = flops / us / 1e6
             e.update({"flops": int(flops), "TFLOPs": round(tf, 2),
                       "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)})
+        if cache is not None:
+            e["cache"] = cache
         if cpu is not None:
             e["cpu_us"] = cpu
         ops[name] = e
+
+    def sets(*arrays_or_bytes):
+        """(buffer sets, bytes per set) of a row whose calls touch these."""
+        nb = sum(a if isinstance(a, int) else a.nbytes for a in arrays_or_bytes)
+        return n_sets(nb, 10**9), nb
 
     R, Hd = 2048, 2304  # prefill activations: 16 sequences x 128 tokens
     x = rng.standard_normal((R, Hd), dtype=np.float32)
     y = rng.standard_normal((R, Hd), dtype=np.float32)
     g = rng.standard_normal(Hd, dtype=np.float32)
-    dx, dy, dg, dd = up(x), up(y), up(g), zeros(x.nbytes)
-    us, wall = _timed(L, lambda: L.vmlm_hip_rmsnorm(dd, dx, dg, R, Hd, C.c_float(1e-5), None), iters)
+    dg = up(g)
+    n, sb = sets(x, x)
+    dx, dd = copies(up(x), x.nbytes, n), [zeros(x.nbytes) for _ in range(n)]
+    us, wall = _timed(L, lambda i: L.vmlm_hip_rmsnorm(dd[i % n], dx[i % n], dg, R, Hd,
+                                                      C.c_float(1e-5), None), max(iters, n))
     rec("rmsnorm_2048x2304", us, wall, nbytes=2 * x.nbytes + g.nbytes,
-        cpu=_cpu_us(lambda: orc.rmsnorm(x, g, 1e-5)) if orc else None)
+        cpu=_cpu_us(lambda: orc.rmsnorm(x, g, 1e-5)) if orc else None, cache=cache_note(sb, n))
     EWADD, SILU = 20, 2  # VMLM_OP_EWADD, VMLM_ACT_SILU
-    us, wall = _timed(L, lambda: L.vmlm_hip_ew_op(dd, dx, dy, R * Hd, EWADD, None), iters)
+    n3, sb3 = sets(x, y, x)
+    dx3 = copies(dx[0], x.nbytes, n3)
+    dy3 = copies(up(y), y.nbytes, n3)
+    dd3 = [zeros(x.nbytes) for _ in range(n3)]
+    us, wall = _timed(L, lambda i: L.vmlm_hip_ew_op(dd3[i % n3], dx3[i % n3], dy3[i % n3], R * Hd,
+                                                    EWADD, None), max(iters, n3))
     rec("ew_add_2048x2304", us, wall, nbytes=3 * x.nbytes,
-        cpu=_cpu_us(lambda: orc.ew_op(x, y, EWADD)) if orc else None)
-    us, wall = _timed(L, lambda: L.vmlm_hip_scale(dd, dx, R * Hd, C.c_float(0.125), None), iters)
+        cpu=_cpu_us(lambda: orc.ew_op(x, y, EWADD)) if orc else None, cache=cache_note(sb3, n3))
+    us, wall = _timed(L, lambda i: L.vmlm_hip_scale(dd[i % n], dx[i % n], R * Hd,
+                                                    C.c_float(0.125), None), max(iters, n))
     rec("scale_2048x2304", us, wall, nbytes=2 * x.nbytes,
-        cpu=_cpu_us(lambda: orc.scale(x, 0.125)) if orc else None)
+        cpu=_cpu_us(lambda: orc.scale(x, 0.125)) if orc else None, cache=cache_note(sb, n))
     a = rng.standard_normal((R, 5760), dtype=np.float32)
-    da = up(a)
-    us, wall = _timed(L, lambda: L.vmlm_hip_act(da, R * 5760, SILU, None), iters)
+    na, sba = sets(a)  # in place
+    da = copies(up(a), a.nbytes, na)
+    us, wall = _timed(L, lambda i: L.vmlm_hip_act(da[i % na], R * 5760, SILU, None),
+                      max(iters, na))
     rec("act_silu_2048x5760", us, wall, nbytes=2 * a.nbytes,
-        cpu=_cpu_us(lambda: orc.act(a, SILU)) if orc else None)
-    # softmax over the scores of 36 heads x 512 queries (rows of 512)
+        cpu=_cpu_us(lambda: orc.act(a, SILU)) if orc else None, cache=cache_note(sba, na))
+    # softmax over the scores of 36 heads x 512 queries (rows of 512), in place
     p = rng.standard_normal((36 * 512, 512), dtype=np.float32)
-    dp = up(p)
-    us, wall = _timed(L, lambda: L.vmlm_hip_softmax(dp, 36 * 512, 512, False, None), iters)
+    npp, sbp = sets(p)
+    dp = copies(up(p), p.nbytes, npp)
+    us, wall = _timed(L, lambda i: L.vmlm_hip_softmax(dp[i % npp], 36 * 512, 512, False, None),
+                      max(iters, npp))
     rec("softmax_18432x512", us, wall, nbytes=2 * p.nbytes,
-        cpu=_cpu_us(lambda: orc.softmax(p, False)) if orc else None)
+        cpu=_cpu_us(lambda: orc.softmax(p, False)) if orc else None, cache=cache_note(sbp, npp))
     # RoPE of 512 positions x 36 heads (rows of 64)
     r = rng.standard_normal((512 * 36, 64), dtype=np.float32)
-    dr, dro = up(r), zeros(r.nbytes)
-    us, wall = _timed(L, lambda: L.vmlm_hip_rope(dro, dr, 512 * 36, 64, C.c_float(10000.0), 0,
-                                                 None), iters)
+    nr, sbr = sets(r, r)
+    dr, dro = copies(up(r), r.nbytes, nr), [zeros(r.nbytes) for _ in range(nr)]
+    us, wall = _timed(L, lambda i: L.vmlm_hip_rope(dro[i % nr], dr[i % nr], 512 * 36, 64,
+                                                   C.c_float(10000.0), 0, None), max(iters, nr))
     rec("rope_18432x64", us, wall, nbytes=2 * r.nbytes,
-        cpu=_cpu_us(lambda: orc.rope(r, 10000.0, 0)) if orc else None)
+        cpu=_cpu_us(lambda: orc.rope(r, 10000.0, 0)) if orc else None, cache=cache_note(sbr, nr))
     # TOPK_IDX over one row of LM-head logits (the op scans the first row)
     lg = rng.standard_normal((1, 122753), dtype=np.float32)
-    dl, di = up(lg), zeros(4)
-    us, wall = _timed(L, lambda: L.vmlm_hip_topk_idx(dl, 1, 122753, di, None), iters)
+    nl, sbl = sets(lg)
+    nl = min(nl, 1024)
+    dl, di = copies(up(lg), lg.nbytes, nl), zeros(4)
+    us, wall = _timed(L, lambda i: L.vmlm_hip_topk_idx(dl[i % nl], 1, 122753, di, None),
+                      max(iters, nl))
     rec("topk_idx_122753", us, wall, nbytes=lg.nbytes,
-        cpu=_cpu_us(lambda: orc.topk_idx(lg)) if orc else None)
+        cpu=_cpu_us(lambda: orc.topk_idx(lg)) if orc else None, cache=cache_note(sbl, nl))
     # f32 GEMMs of the VM's attention composition (one head): scores Q K^T
     # 512x512x64 (NT) and P V 512x64x512 (NN)
     qh = rng.standard_normal((512, 64), dtype=np.float32)
     kh = rng.standard_normal((512, 64), dtype=np.float32)
     ph = rng.standard_normal((512, 512), dtype=np.float32)
     dq, dk, dph, ds_, do_ = up(qh), up(kh), up(ph), zeros(512 * 512 * 4), zeros(512 * 64 * 4)
-    us, wall = _timed(L, lambda: L.vmlm_hip_gemm_nt(dq, dk, ds_, 512, 512, 64, False, None), iters)
+    us, wall = _timed(L, lambda i: L.vmlm_hip_gemm_nt(dq, dk, ds_, 512, 512, 64, False, None), iters)
     rec("gemm_nt_f32_512x512x64", us, wall, flops=2 * 512 * 512 * 64,
         cpu=_cpu_us(lambda: orc.gemm_nt(qh, kh)) if orc else None)
-    us, wall = _timed(L, lambda: L.vmlm_hip_gemm(dph, dk, do_, 512, 64, 512, False, None), iters)
+    us, wall = _timed(L, lambda i: L.vmlm_hip_gemm(dph, dk, do_, 512, 64, 512, False, None), iters)
     rec("gemm_nn_f32_512x64x512", us, wall, flops=2 * 512 * 64 * 512,
         cpu=_cpu_us(lambda: orc.gemm(ph, kh)) if orc else None)
     return ops
@@ -764,7 +862,9 @@ def main():
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(cfg, W, args.cpu_steps, threads)
-        log(f"cpu oracle: {cpu['value']} tokens/s on {threads} threads")
+        log(f"cpu oracle: {cpu['value']} tokens/s on 1 thread, "
+            f"{cpu['threads']['batch1']['value']} on {threads} (batch 16: "
+            f"{cpu['threads']['batch16']['value']})")
 
     value = args.steps * args.batch / wall
     out = {
@@ -778,7 +878,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 weights x f32 activations (f32 accumulate)",
+        "dtype": ("int8 weights; batch 16: each f32 activation as three int8 terms with "
+                  "power-of-two factors per row segment (int32 sums, f32 combine); batch <= 5: "
+                  "three bf16 terms (f32 accumulate)"),
         "data": "synthetic (seeded random-init weights and prompts)",
         "config": {
             "workload": "config 3: MiniCPM-2B-shaped int8 decoder, greedy decode",
