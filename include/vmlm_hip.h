@@ -331,12 +331,27 @@ void *vmlm_decoder_stream(vmlm_decoder *dec);
  * reference counterpart: the reference runs one opcode per instruction.) */
 int vmlm_decoder_set_fused(vmlm_decoder *dec, int enable);
 int vmlm_decoder_fused(const vmlm_decoder *dec);
+/* The layer program by number: VMLM_DECODER_KSLICE (k-slice GEMVs, eight
+ * launches per layer), VMLM_DECODER_FUSED (batch <= 5, five launches) or
+ * VMLM_DECODER_FULLK (batch <= 16, hidden 768, 1536 or 2304: q/k/v and gate/up over the
+ * whole K in one launch each, SiLU * up in the gate/up epilogue, seven
+ * launches). A new session takes the fused program where it fits, else the
+ * full-K one, else the k-slice one. All give the same greedy tokens within
+ * the 1e-4 x RMS contract of their logits. (No reference counterpart.) */
+#define VMLM_DECODER_KSLICE 0
+#define VMLM_DECODER_FUSED 1
+#define VMLM_DECODER_FULLK 2
+int vmlm_decoder_set_program(vmlm_decoder *dec, int program);
+int vmlm_decoder_program(const vmlm_decoder *dec);
 /* Times `iters` launches of one decode-step GEMV of every layer in turn
- * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; on the k-slice
- * program also 5, 6, 7: the o, gate/up or down projection followed by the
- * kernel that reduces its k-slice partials; 8..11: a plain streaming read
- * of the q/k/v, o, gate/up or down weights, the single-launch floor of
- * those bytes; 12: the decode attention; 13: an empty kernel) captured into
+ * (which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; on the k-slice and
+ * full-K programs also 5, 6, 7: the o, gate/up or down projection followed
+ * by the kernel that reduces its k-slice partials (the full-K gate/up needs
+ * none); 8..11: a plain streaming read of the q/k/v, o, gate/up or down
+ * weights, the single-launch floor of those bytes; 12: the decode
+ * attention; 13: an empty kernel; 14, 15 (full-K program): the q/k/v
+ * projection at four tiles per workgroup, the gate/up projection at one
+ * tile pair per workgroup) captured into
  * one HIP graph on the session stream; writes the mean per-launch (or
  * per-pair) duration of a replay (HIP events, launch gaps included) and the
  * algorithmic HBM bytes (weights + scales + activations in + outputs; on the

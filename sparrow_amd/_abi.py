@@ -134,6 +134,8 @@ SIGNATURES = {
     "vmlm_decoder_stream": (P, [P]),
     "vmlm_decoder_set_fused": (I, [P, I]),
     "vmlm_decoder_fused": (I, [P]),
+    "vmlm_decoder_set_program": (I, [P, I]),
+    "vmlm_decoder_program": (I, [P]),
     "vmlm_decoder_time_gemv": (I, [P, I, U32, C.POINTER(F), C.POINTER(C.c_double)]),
     "vmlm_b1_stack_forward": (I, [C.POINTER(SparseConnW), U32, P, P, SZ, U16, P]),
     "vmlm_b1_stack_create": (I, [C.POINTER(SparseConnW), U32, P, C.POINTER(C.c_void_p)]),

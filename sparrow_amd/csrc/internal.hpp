@@ -129,10 +129,38 @@ struct KsArgs {
     int ldy = 0;
     int M = 1, N = 0, K = 0;
     int tw = 0, nwv = 0;  // tiles per wave, waves per workgroup; 0 = 2, 4
+    const float *X = nullptr;  // f32 rows [M][lda], quantized per slice while staged
 };
 int ks_gemv_slices(int K);
+// (with X instead of A / A8: f32 rows [M][lda], each slice's rows split into
+// int8 terms while staged, with the factor of the slice's own maximum.)
 inline int ks_gemv_window(int K) { return K / ks_gemv_slices(K); }
 int launch_ks_gemv(const KsArgs &a, hipStream_t st);
+// Full-K int8 GEMV for decode batches up to 16 rows (k_fullk.hip): one
+// launch per projection, no k-slice partials. Input: int8 rows in blocked
+// layout [Q8_T][K/64][1 KiB] (launch_resid_q8 with `blocked`), segment
+// factors a8s[K/64/seg_kb][M] and, for an RMSNorm input, segment sums of
+// squares ssp (same shape). FQ_STORE: Y[m][j] = acc * scale[j] * inv[m];
+// FQ_SILU over the gate/up tile pairs of the swizzled Wgu:
+// Y[m][16p + r] = silu(gate) * up.
+enum FqEpi { FQ_STORE = 0, FQ_SILU = 1 };
+struct FqArgs {
+    const int8_t *W = nullptr;
+    const float *scale = nullptr;
+    const int8_t *A8 = nullptr;
+    const float *a8s = nullptr;
+    const float *ssp = nullptr;
+    float eps = 0.0f;
+    int seg_kb = 4;
+    float *Y = nullptr;
+    int ldy = 0;
+    int M = 1, N = 0, K = 0;
+    int epi = FQ_STORE;
+    int tw = 1;  // 16-row tiles per workgroup (1, 2 or 4; FQ_SILU: 2 or 4)
+};
+bool fq_gemv_ok(int M, int N, int K, int epi, int tw);
+int launch_fq_gemv(const FqArgs &a, hipStream_t st);
+
 // int8 [N][K] row-major -> [N/16][K/64][64 lanes][16 B] MFMA-operand order.
 int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
 
@@ -242,10 +270,13 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 //   resid = x;  q8/q8s = int8 terms of x * g with each segment's power-of-two
 //   factor [cols/seg][rows];  ssp = each segment's sum of x^2 [cols/seg][rows].
 // The consumer applies 1/sqrt(sum(ssp)/cols + eps) (the RMSNorm) to its dot
-// products.
+// products. With `blocked` (rows <= 16) q8 takes the layout of the full-K
+// GEMV's input instead of row-major planes: [Q8_T][cols/64][1 KiB], lane
+// (g, n) of a block = row n, k 8g .. +7 and 32 + 8g .. +7 (rows past `rows`
+// are left as they are: zero from the owner's initialisation).
 int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
                     float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
-                    float *q8s, float *ssp, hipStream_t st);
+                    float *q8s, float *ssp, hipStream_t st, bool blocked = false);
 // Rows x [rows][ldx] (with g: RMSNorm(x) * g) as Q8_T int8 terms with
 // per-row power-of-two factors q8s [rows]: the input of launch_gemm's
 // int8-row path. Layout (q8_rows_bytes(rows, cols) bytes): Q8_T planes of

@@ -351,7 +351,8 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
 struct KsParams {
     const uint8_t *W;   // swizzled [N/16][K/64][64][16]
     const uint16_t *A;  // [3][M][lda] bf16 term planes, or
-    const int8_t *A8;   // [Q8_T][M][lda] int8 rows, slice factors a8s[ks][M]
+    const int8_t *A8;   // [Q8_T][M][lda] int8 rows, slice factors a8s[ks][M], or
+    const float *X;     // f32 rows [M][lda], split into int8 terms while staged
     const float *a8s;
     const float *ssp;   // [ks][M] segment sums of squares (RMSNorm), or null
     float eps;
@@ -374,13 +375,15 @@ constexpr int KS_SSP_MAX = 16;  // k-slices whose segment sums are read up front
 // The swizzled weight bytes of lane (g, r) are k = 8g .. +7 and 32 + 8g .. +7
 // of the block; the B fragment of lane (g, n) takes the same k of token n,
 // so each product pairs matching k whatever order the MFMA sums them in.
-template <int KB, int TW, int NWV>
+template <int KB, int TW, int NWV, bool XF>
 __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
     constexpr int NTH = NWV * 64;
     constexpr int KW = KB * 64;
     constexpr int ALD = KW + 16;     // padded LDS row (bytes)
+    static_assert(!XF || NTH == 256, "f32 staging: 16 threads per row");
     __shared__ __attribute__((aligned(16))) int8_t as8[Q8_T][16][ALD];
     __shared__ float ssp_s[KS_SSP_MAX][16];
+    __shared__ float xf_s[XF ? 16 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -390,21 +393,30 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
     const int tile0 = (blockIdx.x * NWV + wave) * TW;
 
     constexpr int PIECES = Q8_T * 16 * (KW / 16);
-    constexpr int PER = (PIECES + NTH - 1) / NTH;
+    constexpr int PER = XF ? 1 : (PIECES + NTH - 1) / NTH;
+    constexpr int XPER = KW / 64;  // XF: float4 pieces per thread (16 threads per row)
     u32x4 ap[PER];
+    float4 xv[XF ? XPER : 1];
+    const int xr = tid >> 4, xc = tid & 15;  // XF: row, and the thread's pieces xc + 16 i
+    if constexpr (XF) {
+        const float *xrow = p.X + (size_t)(xr < p.M ? xr : 0) * p.lda + (size_t)kb0 * 64;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        int e = tid + i * NTH;
-        e = e < PIECES ? e : PIECES - 1;
-        const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
-        const int rs = r < p.M ? r : 0;
-        ap[i] = *(const u32x4 *)(p.A8 + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c16 * 16);
+        for (int i = 0; i < XPER; ++i) xv[i] = *(const float4 *)(xrow + 4 * (xc + 16 * i));
+    } else {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int e = tid + i * NTH;
+            e = e < PIECES ? e : PIECES - 1;
+            const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
+            const int rs = r < p.M ? r : 0;
+            ap[i] = *(const u32x4 *)(p.A8 + ((size_t)t * p.M + rs) * p.lda + (size_t)kb0 * 64 + c16 * 16);
+        }
     }
     // the row factor: this slice's segment factor, times the RMSNorm's
     // 1 / sqrt(mean(x^2) + eps) from the segment sums (one load per thread
     // into LDS; summed per row in segment order after the barrier)
     const int nr = n < p.M ? n : 0;
-    const float segf = p.a8s[blockIdx.y * p.M + nr];
+    const float segf = XF ? 0.0f : p.a8s[blockIdx.y * p.M + nr];
     const int nsl = (int)gridDim.y;
     constexpr int SPER = (KS_SSP_MAX * 16 + NTH - 1) / NTH;
     float sspv[SPER];
@@ -426,12 +438,40 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
             wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XF) {
+        // the slice of row xr as int8 terms with the power-of-two factor of
+        // its own maximum (q8_row_k over the 16 threads of the row)
+        float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int e = tid + i * NTH;
-        if (e < PIECES) {
-            const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
-            *(u32x4 *)&as8[t][r][c16 * 16] = ap[i];
+        for (int i = 0; i < XPER; ++i)
+            mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(xv[i].x), q8_mag(xv[i].y)),
+                                 fmaxf(q8_mag(xv[i].z), q8_mag(xv[i].w))));
+        mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        const int k = q8_row_k(mx);
+        if (xc == 0) xf_s[xr] = q8_factor(k);
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) {
+            int a[4][Q8_T];
+            q8_split(xv[i].x, k, a[0]);
+            q8_split(xv[i].y, k, a[1]);
+            q8_split(xv[i].z, k, a[2]);
+            q8_split(xv[i].w, k, a[3]);
+#pragma unroll
+            for (int t = 0; t < Q8_T; ++t)
+                *(uint32_t *)&as8[t][xr][4 * (xc + 16 * i)] =
+                    pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = tid + i * NTH;
+            if (e < PIECES) {
+                const int t = e / (16 * (KW / 16)), r = (e / (KW / 16)) % 16, c16 = e % (KW / 16);
+                *(u32x4 *)&as8[t][r][c16 * 16] = ap[i];
+            }
         }
     }
 #pragma unroll
@@ -440,12 +480,12 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
         if (e < nsl * 16) ssp_s[e >> 4][e & 15] = sspv[i];
     }
     __syncthreads();
-    float rowf = segf;
+    float rowf = XF ? xf_s[n] : segf;
     if (p.ssp) {
         float ss = ssp_s[0][n];
         for (int s = 1; s < nsl; ++s) ss += ssp_s[s][n];
         ss = ss / (float)p.K;
-        rowf = segf * (1.0f / sqrtf(ss + p.eps));
+        rowf = rowf * (1.0f / sqrtf(ss + p.eps));
     }
 
     // the B fragments of every block and term, then the tiles one at a time
@@ -579,8 +619,13 @@ template <int KB, int TW, int NWV>
 int launch_ks_t(const KsParams &p, int ks, hipStream_t st) {
     const int rows = 16 * TW * NWV;
     const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ks);
-    if (p.A8)
-        ks_gemv_i8_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
+    if (p.X) {
+        if constexpr (NWV == 4)
+            ks_gemv_i8_kernel<KB, TW, NWV, true><<<grid, NWV * 64, 0, st>>>(p);
+        else
+            return fail(VMLM_ERR_UNIMPL, "k-slice GEMV: f32 rows need 4 waves per workgroup");
+    } else if (p.A8)
+        ks_gemv_i8_kernel<KB, TW, NWV, false><<<grid, NWV * 64, 0, st>>>(p);
     else
         ks_gemv_kernel<KB, TW, NWV><<<grid, NWV * 64, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
@@ -750,17 +795,22 @@ int ks_gemv_slices(int K) {
 int launch_ks_gemv(const KsArgs &a, hipStream_t st) {
     VMLM_GUARD(a.M >= 1 && a.M <= 16 && a.K % 64 == 0 && a.K >= 64 && a.N % 16 == 0 && a.N >= 16,
                "k-slice GEMV: shape M=%d N=%d K=%d unsupported", a.M, a.N, a.K);
-    VMLM_GUARD((a.A != nullptr) != (a.A8 != nullptr) && (!a.A8 || a.a8s),
-               "k-slice GEMV: bf16 term planes or int8 rows with their factors");
-    VMLM_GUARD(!a.ssp || (a.A8 && ks_gemv_slices(a.K) <= KS_SSP_MAX),
-               "k-slice GEMV: segment sums go with int8 rows of at most %d slices", KS_SSP_MAX);
-    VMLM_GUARD(a.lda % 16 == 0 && ((uintptr_t)(a.A ? (const void *)a.A : (const void *)a.A8) & 15) == 0 &&
+    VMLM_GUARD((a.A != nullptr) + (a.A8 != nullptr) + (a.X != nullptr) == 1 && (!a.A8 || a.a8s),
+               "k-slice GEMV: bf16 term planes, int8 rows with their factors, or f32 rows");
+    VMLM_GUARD(!a.ssp || ((a.A8 || a.X) && ks_gemv_slices(a.K) <= KS_SSP_MAX),
+               "k-slice GEMV: segment sums go with int8 or f32 rows of at most %d slices",
+               KS_SSP_MAX);
+    VMLM_GUARD(!a.X || (a.K / ks_gemv_slices(a.K)) % 64 == 0,
+               "k-slice GEMV: f32 rows need slices of whole 64-column blocks");
+    const void *ain = a.A ? (const void *)a.A : a.A8 ? (const void *)a.A8 : (const void *)a.X;
+    VMLM_GUARD(a.lda % 16 == 0 && ((uintptr_t)ain & 15) == 0 &&
                    a.Y && a.ldy % 4 == 0 && ((uintptr_t)a.Y & 15) == 0,
                "k-slice GEMV: input rows and partial rows must be 16-byte aligned");
     KsParams p;
     p.W = (const uint8_t *)a.W;
     p.A = a.A;
     p.A8 = a.A8;
+    p.X = a.X;
     p.a8s = a.a8s;
     p.ssp = a.ssp;
     p.eps = a.eps;

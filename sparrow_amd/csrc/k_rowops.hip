@@ -229,7 +229,7 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 // the int8 input of the next k-slice GEMVs (see launch_resid_q8). Lane l
 // holds columns 4c..4c+3 of the segment, c = l + 64i (i < SI); all slices of
 // a column are loaded up front so the reads take one round trip. The segment's power-of-two factor comes from its own max |x * g|.
-template <int SI, int KSN>
+template <int SI, int KSN, bool BLK>
 __global__ __launch_bounds__(64) void resid_q8_kernel(
     const float *__restrict__ base, const float *__restrict__ part, int ks, int ldp,
     const float *__restrict__ scale, float *__restrict__ resid, const float *__restrict__ g,
@@ -292,17 +292,28 @@ __global__ __launch_bounds__(64) void resid_q8_kernel(
         q8_split(xg[i].y, k, a[1]);
         q8_split(xg[i].z, k, a[2]);
         q8_split(xg[i].w, k, a[3]);
+        // blocked: column col of k-block col / 64 sits in lane (g, row), g =
+        // (col % 32) / 8, at byte 8 * (col % 64 >= 32) + col % 8
+        const int o = col & 63;
+        const size_t boff = ((size_t)(col >> 6) * 1024) + 16 * (16 * ((o & 31) >> 3) + row) +
+                            8 * (o >> 5) + (o & 7);
 #pragma unroll
-        for (int t = 0; t < Q8_T; ++t)
-            *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + col) =
-                pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+        for (int t = 0; t < Q8_T; ++t) {
+            const uint32_t v = pack_i8x4(a[0][t], a[1][t], a[2][t], a[3][t]);
+            if constexpr (BLK)
+                *(uint32_t *)(q8 + (size_t)t * (cols >> 6) * 1024 + boff) = v;
+            else
+                *(uint32_t *)(q8 + ((size_t)t * rows + row) * cols + col) = v;
+        }
     }
 }
 
 int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const float *scale,
                     float *resid, const float *g, size_t rows, size_t cols, int seg, int8_t *q8,
-                    float *q8s, float *ssp, hipStream_t st) {
+                    float *q8s, float *ssp, hipStream_t st, bool blocked) {
     if (rows == 0) return VMLM_OK;
+    VMLM_GUARD(!blocked || (rows <= 16 && cols % 64 == 0 && ((uintptr_t)q8 & 15) == 0),
+               "resid_q8: blocked rows need at most 16 rows, 64-column blocks, 16-byte alignment");
     VMLM_GUARD(seg >= 64 && seg <= 512 && seg % 64 == 0 && cols % seg == 0 && cols / seg <= 65535,
                "resid_q8: segments of 64..512 columns (multiple of 64) tiling the row");
     VMLM_GUARD(ks >= 0 && ks <= KS_MAX && (ks == 0 || (part && scale && resid && ldp % 4 == 0)),
@@ -314,8 +325,16 @@ int launch_resid_q8(const float *base, const float *part, int ks, int ldp, const
     // slice loads sized to the slice count of the decoder's projections (9
     // for K = 2304, 15 for K = 5760), else 4 or 16 (loads past ks skipped)
 #define RQ_LAUNCH(SI, KSN)                                                                      \
-    resid_q8_kernel<SI, KSN><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale, resid, g,        \
-                                                  (int)cols, (int)rows, seg, q8, q8s, ssp)
+    do {                                                                                        \
+        if (blocked)                                                                            \
+            resid_q8_kernel<SI, KSN, true><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale,    \
+                                                                resid, g, (int)cols, (int)rows, \
+                                                                seg, q8, q8s, ssp);             \
+        else                                                                                    \
+            resid_q8_kernel<SI, KSN, false><<<grid, 64, 0, st>>>(base, part, ks, ldp, scale,   \
+                                                                 resid, g, (int)cols,           \
+                                                                 (int)rows, seg, q8, q8s, ssp); \
+    } while (0)
 #define RQ_KS(SI)                                                                               \
     if (ks == 9) RQ_LAUNCH(SI, 9);                                                              \
     else if (ks == 15) RQ_LAUNCH(SI, 15);                                                       \

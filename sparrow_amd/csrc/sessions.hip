@@ -28,6 +28,8 @@
 
 namespace vmlm {
 
+enum { PROG_KSLICE = 0, PROG_FUSED = 1, PROG_FULLK = 2 };
+
 // Folds the LM head's argmax slots of each sequence into tok[b] (the
 // TOPK_IDX result fed to the next step's EMB), clears the slots for the next
 // step, and -- when `out` is given -- records tok into tokens_out[step] and
@@ -93,7 +95,16 @@ struct vmlm_decoder {
     int8_t *wstage = nullptr;  // one layer's row-major weights, swizzled into wsw at load
     int8_t *wsw = nullptr;     // the weights in MFMA-operand order (every projection)
     float *ssp = nullptr;   // fused path: RMSNorm partial sums of squares [H/16][B]
-    bool fused = false;     // five-launch layers of full-K fused GEMVs (batch <= 5)
+    // layer program of the decode step: PROG_KSLICE (k-slice GEMVs and
+    // reduction kernels, eight launches per layer), PROG_FUSED (batch <= 5:
+    // five launches of full-K fused GEMVs) or PROG_FULLK (batch <= 16: full-K
+    // int8 GEMVs for q/k/v and gate/up, seven launches)
+    int prog = PROG_KSLICE;
+    bool fused = false;     // prog == PROG_FUSED
+    // full-K program: the normed rows as blocked int8 terms [Q8_T][H/64][1 KiB]
+    int8_t *x8b = nullptr;
+    int fq_tw = 2;     // 16-row tiles per workgroup of the full-K q/k/v projection
+    int fq_tw_gu = 4;  // and of the gate/up projection (two gate/up tile pairs)
     float *s = nullptr, *norms = nullptr;
     uint16_t *embed = nullptr, *lm_head = nullptr;
     float *final_norm = nullptr;
@@ -233,16 +244,16 @@ KsArgs step_gemv(vmlm_decoder *d, const int8_t *W, const uint16_t *A, int N, int
 
 // Decode attention of layer l at the device position: q/k/v as the q/k/v
 // projection's k-slice partials (k-slice program) or as final rows (fused
-// program).
+// and full-K programs).
 DecodeArgs attn_args(vmlm_decoder *d, size_t l) {
     const int H = (int)d->H;
     DecodeArgs a;
     a.q = a.k_new = a.v_new = nullptr;
-    if (d->fused) {
+    if (d->prog != PROG_KSLICE) {
         a.q = d->qkv;
         a.k_new = d->qkv + H;
         a.v_new = d->qkv + 2 * H;
-        if (d->B == 1 && fk_apart_ok(H)) {  // FK_APART workgroups per head, merged by the o projection
+        if (d->fused && d->B == 1 && fk_apart_ok(H)) {  // FK_APART workgroups per head, merged by the o projection
             a.frac = FK_APART;
             a.fpart = d->apart;
         }
@@ -371,8 +382,86 @@ int enqueue_step_fused(vmlm_decoder *d) {
     return VMLM_OK;
 }
 
+// The full-K projections of layer l (which: 0 q/k/v rows, 2 gate/up with
+// SiLU * up) over the blocked int8 rows of the input norm.
+FqArgs fq_args(vmlm_decoder *d, size_t l, int which) {
+    const int H = (int)d->H, I = (int)d->I;
+    FqArgs f;
+    f.A8 = d->x8b;
+    f.a8s = d->x8s;
+    f.ssp = d->x8ssp;
+    f.eps = d->c.eps;
+    f.seg_kb = d->seg / 64;
+    f.M = (int)d->B;
+    f.K = H;
+    if (which == 0) {
+        f.W = d->Wqkv(l), f.scale = d->Sqkv(l), f.N = 3 * H;
+        f.Y = d->qkv, f.ldy = 3 * H, f.epi = FQ_STORE, f.tw = d->fq_tw;
+    } else {
+        f.W = d->Wgu(l), f.scale = d->Sgu(l), f.N = 2 * I;
+        f.Y = d->act, f.ldy = I, f.epi = FQ_SILU, f.tw = d->fq_tw_gu;
+    }
+    return f;
+}
+
+// The down projection of the full-K program: k-slice GEMV over the f32
+// SiLU * up rows, each slice split into int8 terms while staged.
+KsArgs fq_down(vmlm_decoder *d, size_t l) {
+    KsArgs g;
+    g.W = d->Wd(l);
+    g.X = d->act;
+    g.lda = (int)d->I;
+    g.M = (int)d->B;
+    g.N = (int)d->H;
+    g.K = (int)d->I;
+    g.Y = d->part;
+    g.ldy = (int)d->H;
+    g.tw = 3;
+    g.nwv = 4;
+    return g;
+}
+
+// Seven launches per layer (batch <= 16): the q/k/v and gate/up projections
+// over the whole K in one launch each (q/k/v rows for the attention; SiLU *
+// up in the gate/up epilogue), o and down as k-slice GEMVs whose partials the
+// residual kernels reduce; the residual kernels write the next projection's
+// input as blocked int8 rows.
+int enqueue_step_fullk(vmlm_decoder *d) {
+    hipStream_t st = d->st;
+    const int B = (int)d->B, H = (int)d->H;
+    int rc = launch_emb_bf16(d->h, H, d->embed, d->V, H, nullptr, d->tok, B, st);
+    if (rc) return rc;
+    if ((rc = launch_resid_q8(d->h, nullptr, 0, 0, nullptr, nullptr, d->InLn(0), B, H, d->seg,
+                              d->x8b, d->x8s, d->x8ssp, st, true)))
+        return rc;
+    for (size_t l = 0; l < d->L; ++l) {
+        if ((rc = launch_fq_gemv(fq_args(d, l, 0), st))) return rc;
+        if ((rc = launch_attention_decode(attn_args(d, l), B, d->att, H, d->t_att, 3, H, st)))
+            return rc;
+        if ((rc = launch_ks_gemv(step_gemv(d, d->Wo(l), d->t_att, H, H), st))) return rc;
+        if ((rc = launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
+                                  d->seg, d->x8b, d->x8s, d->x8ssp, st, true)))
+            return rc;
+        if ((rc = launch_fq_gemv(fq_args(d, l, 2), st))) return rc;
+        if ((rc = launch_ks_gemv(fq_down(d, l), st))) return rc;
+        if (l + 1 < d->L)
+            rc = launch_resid_q8(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, d->InLn(l + 1), B, H,
+                                 d->seg, d->x8b, d->x8s, d->x8ssp, st, true);
+        else
+            rc = launch_rmsnorm_resid(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, B, H,
+                                      d->final_norm, d->c.eps, d->t_x, 3, H, st);
+        if (rc) return rc;
+    }
+    if ((rc = enqueue_head(d, true))) return rc;
+    step_advance_kernel<<<1, 1, 0, st>>>(d->step, d->pos);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 int enqueue_any_step(vmlm_decoder *d) {
-    return d->fused ? enqueue_step_fused(d) : enqueue_step(d);
+    return d->prog == PROG_FUSED   ? enqueue_step_fused(d)
+           : d->prog == PROG_FULLK ? enqueue_step_fullk(d)
+                                   : enqueue_step(d);
 }
 
 int ensure_graph(vmlm_decoder *d) {
@@ -398,6 +487,28 @@ bool fused_ok(const vmlm_decoder *d) {
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     return H / 16 * B <= 768 && fk_gemv_ok(B, 3 * H, H, FK_STORE) && fk_gemv_ok(B, H, H, FK_RESID) &&
            fk_gemv_ok(B, 2 * I, H, FK_SILU) && fk_gemv_ok(B, H, I, FK_RESID);
+}
+
+// The full-K program: the q/k/v and gate/up shapes fit the full-K kernel,
+// the down projection's slices are whole 64-column blocks staged by 4 waves.
+bool fullk_ok(const vmlm_decoder *d) {
+    const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
+    return fq_gemv_ok(B, 3 * H, H, FQ_STORE, d->fq_tw) &&
+           fq_gemv_ok(B, 2 * I, H, FQ_SILU, d->fq_tw_gu) &&
+           d->seg % 64 == 0 && d->seg_i % 64 == 0 && d->seg_i / 64 <= 6;
+}
+
+// Sets the layer program (the graph of the old one is dropped).
+int set_program(vmlm_decoder *d, int prog) {
+    if (d->prog == prog) return VMLM_OK;
+    if (d->graph) {
+        VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
+        (void)hipGraphExecDestroy(d->graph);
+        d->graph = nullptr;
+    }
+    d->prog = prog;
+    d->fused = prog == PROG_FUSED;
+    return VMLM_OK;
 }
 
 }  // namespace
@@ -435,7 +546,8 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
                c.hidden, c.inter);
     d->seg = ks_gemv_window((int)d->H);  // 64 .. 384 columns
     d->seg_i = ks_gemv_window((int)d->I);
-    d->fused = fused_ok(d);
+    d->prog = fused_ok(d) ? PROG_FUSED : fullk_ok(d) ? PROG_FULLK : PROG_KSLICE;
+    d->fused = d->prog == PROG_FUSED;
     d->loaded.assign(d->L, false);
     auto cleanup = [&](int code) {
         vmlm_decoder_destroy(d);
@@ -451,6 +563,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (rc = dalloc(d, &d->kc, kvn)) || (rc = dalloc(d, &d->vc, kvn)) ||
         (rc = dalloc(d, &d->wsw, d->L * d->w_layer)) ||
         (rc = dalloc(d, &d->x8, (size_t)Q8_T * d->B * d->H)) ||
+        (rc = dalloc(d, &d->x8b, (size_t)Q8_T * d->H * 16)) ||
         (rc = dalloc(d, &d->x8s, d->H / d->seg * d->B)) ||
         (rc = dalloc(d, &d->x8ssp, d->H / d->seg * d->B)) ||
         (rc = dalloc(d, &d->act8, (size_t)Q8_T * d->B * d->I)) ||
@@ -474,6 +587,7 @@ int vmlm_decoder_create(const vmlm_decoder_cfg *cfg, vmlm_decoder **out) {
         (e = hipMemsetAsync(d->vc, 0, kvn * 4, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->pos, 0, 4, d->st)) != hipSuccess ||
         (e = hipMemsetAsync(d->step, 0, 4, d->st)) != hipSuccess ||
+        (e = hipMemsetAsync(d->x8b, 0, (size_t)Q8_T * d->H * 16, d->st)) != hipSuccess ||
         (e = hipStreamSynchronize(d->st)) != hipSuccess)
         return cleanup(hip_fail(e, "decoder init"));
     *out = d;
@@ -769,26 +883,34 @@ void *vmlm_decoder_stream(vmlm_decoder *d) { return d ? (void *)d->st : nullptr;
 int vmlm_decoder_set_fused(vmlm_decoder *d, int enable) {
     VMLM_GUARD(d, "decoder: null");
     VMLM_GUARD(!enable || fused_ok(d), "decoder: the fused layer needs a batch of at most 5");
-    if (d->fused != (enable != 0)) {
-        if (d->graph) {
-            VMLM_HIP_CHECK(hipStreamSynchronize(d->st));
-            (void)hipGraphExecDestroy(d->graph);
-            d->graph = nullptr;
-        }
-        d->fused = enable != 0;
-    }
-    return VMLM_OK;
+    return set_program(d, enable ? PROG_FUSED : PROG_KSLICE);
 }
 
 int vmlm_decoder_fused(const vmlm_decoder *d) { return d && d->fused ? 1 : 0; }
+
+int vmlm_decoder_set_program(vmlm_decoder *d, int program) {
+    VMLM_GUARD(d, "decoder: null");
+    VMLM_GUARD(program >= PROG_KSLICE && program <= PROG_FULLK, "decoder: program %d", program);
+    VMLM_GUARD(program != PROG_FUSED || fused_ok(d),
+               "decoder: the fused layer needs a batch of at most 5");
+    VMLM_GUARD(program != PROG_FULLK || fullk_ok(d),
+               "decoder: the full-K program needs hidden 768, 1536 or 2304 and a batch of at "
+               "most 16");
+    return set_program(d, program);
+}
+
+int vmlm_decoder_program(const vmlm_decoder *d) { return d ? d->prog : -1; }
 
 int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *avg_us,
                            double *bytes_per_launch) {
     int rc = check_loaded(d);
     if (rc) return rc;
-    VMLM_GUARD(which >= 0 && which <= 13 && iters >= 1, "time_gemv: which 0..13, iters >= 1");
+    VMLM_GUARD(which >= 0 && which <= 15 && iters >= 1, "time_gemv: which 0..15, iters >= 1");
     VMLM_GUARD(which <= 4 || which >= 8 || !d->fused,
-               "time_gemv: 5..7 time a k-slice projection with its reduction (k-slice program)");
+               "time_gemv: 5..7 time a projection with its reduction (k-slice and full-K programs)");
+    VMLM_GUARD(which < 14 || d->prog == PROG_FULLK,
+               "time_gemv: 14, 15 time the q/k/v and gate/up projections of the full-K program "
+               "at their other workgroup tilings");
     const int B = (int)d->B, H = (int)d->H, I = (int)d->I;
     // the launches of the decode step: the k-slice GEMVs, or the LM head (bf16)
     auto make_lm = [&]() {
@@ -811,7 +933,7 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     // 8..11: a plain read of the q/k/v, o, gate/up or down weights of the
     // layer (stream_read_kernel), the single-launch floor of that shape
     const bool rd = which >= 8 && which <= 11;
-    const int proj = which >= 12 ? 0 : rd ? which - 8 : which >= 5 ? which - 4 : which;
+    const int proj = which == 15 ? 2 : which >= 12 ? 0 : rd ? which - 8 : which >= 5 ? which - 4 : which;
     auto make = [&](size_t l) {
         switch (proj) {
         case 0: return step_gemv(d, d->Wqkv(l), d->t_x, 3 * H, H);
@@ -822,6 +944,19 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
     };
     // the fused program (batch <= 5) runs the full-K kernels with their row ops
     const bool fk = d->fused && which < 4;
+    // the full-K program: q/k/v and gate/up (with SiLU * up) over the whole
+    // K, down over f32 rows; 14: q/k/v at four tiles per workgroup, 15:
+    // gate/up at one tile pair per workgroup
+    const bool fq = d->prog == PROG_FULLK;
+    auto fq_launch = [&](size_t l, int pr) {
+        if (pr == 0 || pr == 2) {
+            FqArgs f = fq_args(d, l, pr);
+            if (which == 14) f.tw = 4;
+            if (which == 15) f.tw = 2;
+            return launch_fq_gemv(f, d->st);
+        }
+        return launch_ks_gemv(pr == 1 ? make(l) : fq_down(d, l), d->st);
+    };
     auto read = [&](size_t l) {
         const KsArgs g = make(l);
         const size_t n16 = (size_t)g.N * g.K / 16;
@@ -830,15 +965,17 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
         VMLM_HIP_CHECK(hipGetLastError());
         return (int)VMLM_OK;
     };
+    int8_t *x8 = fq ? d->x8b : d->x8;
     auto reduce = [&](size_t l) {
         if (which == 5)
             return launch_resid_q8(d->h, d->part, d->ks_h, H, d->So(l), d->h2, d->PostLn(l), B, H,
-                                   d->seg, d->x8, d->x8s, d->x8ssp, d->st);
-        if (which == 6)
-            return launch_silu_q8(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->seg_i, d->act8,
-                                  d->act8s, d->st);
+                                   d->seg, x8, d->x8s, d->x8ssp, d->st, fq);
+        if (which == 6)  // (full-K: SiLU * up is in the projection's epilogue)
+            return fq ? (int)VMLM_OK
+                      : launch_silu_q8(d->part, d->ks_h, 2 * I, d->Sgu(l), B, I, d->seg_i,
+                                       d->act8, d->act8s, d->st);
         return launch_resid_q8(d->h2, d->part, d->ks_i, H, d->Sd(l), d->h, d->InLn((l + 1) % d->L),
-                               B, H, d->seg, d->x8, d->x8s, d->x8ssp, d->st);
+                               B, H, d->seg, x8, d->x8s, d->x8ssp, d->st, fq);
     };
     auto launch = [&](size_t l) {
         if (rd) return read(l);
@@ -851,8 +988,9 @@ int vmlm_decoder_time_gemv(vmlm_decoder *d, int which, uint32_t iters, float *av
             return launch_attention_decode(attn_args(d, l), B, d->att, H, d->t_att, 3, H, d->st);
         if (which == 4) return launch_gemv(make_lm(), d->st);
         if (fk) return launch_fk_gemv(fk_args(d, l, which), d->st);
-        int r = launch_ks_gemv(make(l), d->st);
-        return r || which < 5 ? r : reduce(l);
+        int r = fq ? fq_launch(l, which == 14 ? 0 : which == 15 ? 2 : proj)
+                   : launch_ks_gemv(make(l), d->st);
+        return r || which < 5 || which >= 14 ? r : reduce(l);
     };
     // `iters` back-to-back launches captured into one HIP graph, as the
     // decode step runs; one event pair around a replay gives the mean launch

@@ -67,6 +67,18 @@ class Decoder:
     def fused(self) -> bool:
         return bool(lib().vmlm_decoder_fused(self._h))
 
+    KSLICE, FUSED, FULLK = 0, 1, 2
+
+    def set_program(self, program: int) -> None:
+        """The layer program: KSLICE (k-slice GEMVs, eight launches per
+        layer), FUSED (batch <= 5, five launches) or FULLK (batch <= 16, full-K
+        q/k/v and gate/up, seven launches)."""
+        check(lib().vmlm_decoder_set_program(self._h, int(program)))
+
+    @property
+    def program(self) -> int:
+        return int(lib().vmlm_decoder_program(self._h))
+
     def set_graph(self, enable: bool) -> None:
         check(lib().vmlm_decoder_set_graph(self._h, int(bool(enable))))
 
@@ -108,9 +120,11 @@ class Decoder:
         bytes. which: 0 qkv, 1 o, 2 gate/up, 3 down, 4 LM head; the kernels of
         the program the session runs (fused full-K or k-slice). On the k-slice
         program 5, 6, 7 time the o, gate/up or down projection together with
-        the kernel that reduces its partials. 8..11: a plain read of the
-        q/k/v, o, gate/up or down weights; 12: the decode attention; 13: an
-        empty kernel. Launches are replayed from one HIP graph."""
+        the kernel that reduces its partials (also on the full-K program).
+        8..11: a plain read of the q/k/v, o, gate/up or down weights; 12: the
+        decode attention; 13: an empty kernel; 14, 15: the full-K q/k/v
+        projection at four tiles per workgroup, the full-K gate/up at one tile
+        pair. Launches are replayed from one HIP graph."""
         us = C.c_float()
         nbytes = C.c_double()
         check(lib().vmlm_decoder_time_gemv(self._h, int(which), int(iters), C.byref(us),

@@ -103,6 +103,63 @@ def test_tiny_batch16_kslice_matches_oracle(hip, oracle, tiny):
         assert np.abs(last[b] - lr).max() <= 1e-4 * rms(lr)
 
 
+@pytest.fixture(scope="module")
+def small768():
+    cfg = M.tiny_config(n_layers=2, hidden=768, n_heads=12, inter=2048, vocab=3000)
+    return cfg, M.make_weights(cfg, seed=13)
+
+
+@pytest.mark.parametrize("batch", [16, 7])
+def test_fullk_matches_kslice_and_oracle(hip, oracle, small768, batch):
+    """The full-K program (the default from batch 6 at hidden 768..2304: q/k/v
+    and gate/up in one launch each, SiLU * up in the epilogue, down over
+    f32 rows quantized while staged) against the k-slice program and the
+    oracle: identical greedy chains, last-step logits within 1e-4 of their
+    RMS, at a full and a ragged batch."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = small768
+    prompts = M.make_prompts(cfg, batch, 11, seed=41)
+    out = {}
+    for prog in (Decoder.FULLK, Decoder.KSLICE):
+        with Decoder(cfg, batch=batch, cap=64) as dec:
+            assert dec.program == Decoder.FULLK
+            dec.load(W)
+            dec.set_program(prog)
+            assert dec.program == prog
+            t0, _ = dec.prefill(prompts)
+            toks, last = dec.decode(8, want_logits=True)
+        out[prog] = (np.concatenate([t0[None, :], toks], 0), last)
+    assert np.array_equal(out[Decoder.FULLK][0], out[Decoder.KSLICE][0])
+    for b in (0, batch // 2, batch - 1):
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        chain, _ = ref.generate(prompts[b], 8)
+        assert np.array_equal(out[Decoder.FULLK][0][:, b], chain)
+        ref = oracle.DecoderOracle(W, cfg, cap=64)
+        ref.prefill(prompts[b])
+        for i in range(8):
+            lr, _ = ref.step(chain[i], 11 + i)
+        for prog in out:
+            assert np.abs(out[prog][1][b] - lr).max() <= 1e-4 * rms(lr), (prog, b)
+
+
+def test_fullk_graph_equals_eager(hip, small768):
+    """The full-K step replayed from its HIP graph gives the eager launches'
+    logits bitwise."""
+    from sparrow_amd.decoder import Decoder
+    cfg, W = small768
+    prompts = M.make_prompts(cfg, 9, 6, seed=8)
+    out = []
+    for graph in (True, False):
+        with Decoder(cfg, batch=9, cap=32) as dec:
+            dec.load(W)
+            dec.set_graph(graph)
+            dec.prefill(prompts)
+            toks, logits = dec.decode(5, want_logits=True)
+            out.append((toks, logits))
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+
+
 def test_fused_guard(hip, tiny):
     from sparrow_amd import VmlmError
     from sparrow_amd.decoder import Decoder
@@ -173,13 +230,15 @@ def test_minicpm_batch1_64_greedy_tokens_identical(hip, oracle, minicpm):
     assert np.array_equal(got, chain), f"first divergence at {np.argmax(got != chain)}"
 
 
-def test_minicpm_batch16_64_greedy_tokens_identical(hip, oracle, minicpm, golden_dir):
+@pytest.mark.parametrize("program", [2, 0])
+def test_minicpm_batch16_64_greedy_tokens_identical(hip, oracle, minicpm, golden_dir, program):
     """BASELINE config 3 at batch 16: 16 prompts of 128 ids, 64 greedy steps
-    on the k-slice program. Every sequence's 65 tokens equal the CPU
-    oracle's chain (tests/golden/minicpm2b_b16_chains.npz, written by
-    make_decoder_chains.py from oracle.DecoderOracle.generate); for
-    sequences 0 and 15 the oracle runs here as well, fed the chain, and the
-    last step's logits are within 1e-4 of their RMS."""
+    on the full-K program (the default) and on the k-slice program. Every
+    sequence's 65 tokens equal the CPU oracle's chain
+    (tests/golden/minicpm2b_b16_chains.npz, written by make_decoder_chains.py
+    from oracle.DecoderOracle.generate); for sequences 0 and 15 the oracle
+    runs here as well, fed the chain, and the last step's logits are within
+    1e-4 of their RMS."""
     from sparrow_amd.decoder import Decoder
     cfg, W = minicpm
     gold = np.load(golden_dir / "minicpm2b_b16_chains.npz")
@@ -187,8 +246,9 @@ def test_minicpm_batch16_64_greedy_tokens_identical(hip, oracle, minicpm, golden
     assert np.array_equal(prompts, gold["prompts"])
     t = time.time()
     with Decoder(cfg, batch=16, cap=200) as dec:
-        assert not dec.fused
+        assert dec.program == Decoder.FULLK
         dec.load(W)
+        dec.set_program(program)
         t0, _ = dec.prefill(prompts)
         toks, last = dec.decode(64, want_logits=True)
     got = np.concatenate([t0[None, :], toks], 0).T
