@@ -30,7 +30,15 @@ def log(msg):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "ks_gemv_decode_minicpm2b_b16_traffic.md")
+TRAFFIC_PROFILE_FULLK = os.path.join(ROOT, "profiles", "fq_gemv_decode_minicpm2b_b16_traffic.md")
 TRAFFIC_PROFILE_FUSED = os.path.join(ROOT, "profiles", "fk_gemv_decode_minicpm2b_b1_traffic.md")
+
+
+def traffic_profile(dec):
+    """The committed counter summary of the program the session runs."""
+    if dec.fused:
+        return TRAFFIC_PROFILE_FUSED
+    return TRAFFIC_PROFILE_FULLK if dec.program == dec.FULLK else TRAFFIC_PROFILE
 
 
 def measured_traffic(path=TRAFFIC_PROFILE):
@@ -51,9 +59,11 @@ def gemv_roofline(dec, iters):
     """q8 GEMV (the int8 projections of a decode step): mean launch duration
     per shape from HIP events on the session stream, and the step-mix
     achieved bandwidth = sum(bytes) / sum(time) over one launch of each.
-    At batch 16 these are the k-slice kernels (ks_gemv_i8_kernel on int8
-    rows for q/k/v and gate/up, ks_gemv_kernel on bf16 terms for o and
-    down); at batch <= 5 the fused full-K kernels (fk_gemv_kernel, with
+    At batch 16 (the full-K program) q/k/v and gate/up are full-K kernels
+    (fq_gemv_kernel: rows out, SiLU * up in the gate/up epilogue) and o and
+    down k-slice kernels (ks_gemv_kernel on bf16 terms, ks_gemv_i8_kernel on
+    f32 rows quantized while staged) whose partials a residual kernel
+    reduces; at batch <= 5 the fused full-K kernels (fk_gemv_kernel, with
     their RMSNorm, residual and SiLU work)."""
     per = {}
     tot_b = tot_t = 0.0
@@ -79,32 +89,40 @@ def gemv_roofline(dec, iters):
     per["o"]["cache"] = "212 MB of o weights fit the 256 MB Infinity Cache: may read warm"
     with_red = None
     if not dec.fused:
-        # the k-slice projections followed by the kernel that reduces their
-        # partials (o: residual RMSNorm into int8 rows, gate/up: SiLU * up,
-        # down: residual RMSNorm); q/k/v's partials are reduced inside the
-        # attention kernel
+        # each projection with the kernel that reduces its partials (o:
+        # residual RMSNorm into int8 rows, down: residual RMSNorm; gate/up: on
+        # the full-K program none, SiLU * up is in its epilogue, on the k-slice
+        # program SiLU * up); q/k/v needs none on the full-K program (its
+        # k-slice form's partials are reduced inside the attention kernel)
         with_red = {}
         rb = rt = 0.0
-        for which, name in ((5, "o+resid_q8"), (6, "gate_up+silu_q8"), (7, "down+resid_q8")):
+        fullk = dec.program == dec.FULLK
+        pairs = ((0, "qkv"), (5, "o+resid_q8"), (6, "gate_up_silu"), (7, "down+resid_q8")) \
+            if fullk else ((5, "o+resid_q8"), (6, "gate_up+silu_q8"), (7, "down+resid_q8"))
+        for which, name in pairs:
             us, nbytes = dec.time_gemv(which, iters)
             with_red[name] = {"us": round(us, 3), "bytes": int(nbytes),
                               "GBps": round(nbytes / us / 1e3, 1)}
             rb += nbytes
             rt += us
         with_red["frac"] = round(rb / rt / 1e3 / HBM_PEAK_GBS, 4)
-        with_red["note"] = ("projection plus its partial reduction, per pair; frac = sum bytes / "
-                            "sum time over the three pairs")
+        with_red["note"] = ("each projection with the kernel that reduces its partials (none for "
+                            "the full-K ones); frac = sum bytes / sum time over them")
     achieved = tot_b / tot_t / 1e3  # GB/s
     gap_us, _ = dec.time_gemv(13, iters)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE),
-            "traffic_source": os.path.relpath(TRAFFIC_PROFILE_FUSED if dec.fused else TRAFFIC_PROFILE,
-                                              ROOT),
+            "traffic": measured_traffic(traffic_profile(dec)),
+            "traffic_source": os.path.relpath(traffic_profile(dec), ROOT),
             "kernel": ("fk_gemv_kernel (full-K, fused RMSNorm / residual / SiLU epilogues; "
                        "at batch 1 the o projection also merges the attention's four "
                        "position-range partials per head)"
                        if dec.fused else
+                       "fq_gemv_kernel (q/k/v and gate/up with SiLU * up; full-K over blocked "
+                       "int8 rows), ks_gemv_kernel (o; bf16 terms, k-slice partials) and "
+                       "ks_gemv_i8_kernel (down; f32 rows quantized while staged, k-slice "
+                       "partials)"
+                       if dec.program == dec.FULLK else
                        "ks_gemv_i8_kernel (q/k/v, gate+up, down; int8 rows) and "
                        "ks_gemv_kernel (o; bf16 terms); k-slice partials"),
             "bytes_per_launch_mean": int(tot_b / 4), "us_per_launch_mean": round(tot_t / 4, 3),
