@@ -418,6 +418,11 @@ int vmlm_vm_clear_output(vmlm_vm *vm);
 void *vmlm_vm_stream(vmlm_vm *vm);
 /* Constant pools uploaded by this process so far (shared pools count once). */
 int vmlm_vm_pool_uploads(size_t *n);
+/* int8 constants this VM also holds in the swizzled MFMA layout (made once
+ * per pool at load, read by OP_GEMM instead of the row-major bytes). No
+ * counterpart in the reference (a layout of this build); for diagnostics
+ * and tests. */
+int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n);
 
 /* ================================================================ tables */
 

@@ -270,10 +270,13 @@ static inline size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; 
 // the int8 MFMA GEMM; otherwise A split into 3 bf16 terms and the GEMV kernel
 // (m <= 16) or the tiled bf16 MFMA GEMM.
 // Temporaries come from `stg`: the stream's arena (Stage) or the fixed
-// scratch array of the allocation-free entry point (ScratchBump).
+// scratch array of the allocation-free entry point (ScratchBump). Wsw, when
+// given, is a swizzled copy of int8 W (launch_swizzle_w) that the caller
+// keeps: the small-row launch and the int8-row GEMM read it instead of W.
 template <class WS>
 static int q_matmul(const float *a, const void *W, bool wi8, const float *scale, float *c,
-                    size_t m, size_t n, size_t k, hipStream_t st, WS &stg) {
+                    size_t m, size_t n, size_t k, hipStream_t st, WS &stg,
+                    const void *Wsw = nullptr) {
     if (m == 0 || n == 0) return VMLM_OK;
     const size_t esz = wi8 ? 1 : 2;
     const size_t Kp = round_up(k == 0 ? 1 : k, 128);  // one 128-byte GEMV chunk covers 128 k
@@ -295,6 +298,24 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         Wd = wp;
     }
     const int T = 3;
+    // int8 weights, up to FX_ROWS rows: one full-K launch whose waves split
+    // their k-runs of the f32 rows into int8 terms themselves
+    if (wi8 && m <= FX_ROWS && Wd == W && ((uintptr_t)a & 15) == 0 && k <= (size_t)1 << 30 &&
+        fx_run_blocks((int)k)) {
+        FxArgs x;
+        x.W = Wsw ? Wsw : Wd;
+        x.swizzled = Wsw != nullptr;
+        x.ldw = (int)k;
+        x.scale = scale;
+        x.X = a;
+        x.ldx = (int)k;
+        x.C = c;
+        x.ldc = (int)n;
+        x.M = (int)m;
+        x.N = (int)n;
+        x.K = (int)k;
+        return launch_fx_gemv(x, st);
+    }
     // int8 weights, a few rows: the wide k-split GEMV splits the f32 rows
     // into terms while staging them, then the slices are reduced in order
     const size_t nch = Kp / 128;
@@ -339,14 +360,15 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
         // many rows: the weights swizzled into 1 KiB blocks first (one pass
         // over N x K bytes), so the GEMM's weight copies move whole blocks;
         // the allocation-free entry point keeps its scratch for the rows
-        const bool blk = std::is_same<WS, Stage>::value && m >= 256 && n % 16 == 0;
-        int8_t *wsw = blk ? stg.template alloc<int8_t>(n * k) : nullptr;
+        // (a swizzled copy the caller keeps is read as it is)
+        const bool blk = Wsw || (std::is_same<WS, Stage>::value && m >= 256 && n % 16 == 0);
+        int8_t *wsw = blk && !Wsw ? stg.template alloc<int8_t>(n * k) : nullptr;
         STAGE_OK(stg);
         int rc = launch_rows_q8(a, k, nullptr, 0.0f, m, k, a8, a8s, st);
         if (rc) return rc;
-        if (blk && (rc = launch_swizzle_w((const int8_t *)Wd, wsw, (int)n, (int)k, st))) return rc;
+        if (wsw && (rc = launch_swizzle_w((const int8_t *)Wd, wsw, (int)n, (int)k, st))) return rc;
         GemmArgs g;
-        g.W = blk ? (const void *)wsw : Wd;
+        g.W = Wsw ? Wsw : blk ? (const void *)wsw : Wd;
         g.w_blocked = blk;
         g.w_int8 = true;
         g.scale = scale;
@@ -399,6 +421,15 @@ static int q_matmul(const float *a, const void *W, bool wi8, const float *scale,
     return launch_gemv(g, st);
 }
 
+// The int8 GEMM of the device VM, which keeps swizzled copies of its int8
+// constants (wsw, or null where it has none).
+int q8_gemm_vm(const float *a, const int8_t *q, const int8_t *wsw, const float *scale, float *c,
+               size_t m, size_t n, size_t k, hipStream_t st) {
+    VMLM_GUARD(scale != nullptr, "int8 gemm: scale slot must be f32 (null)");
+    VMLM_GUARD(!wsw || n % 16 == 0, "int8 gemm: a swizzled copy needs N %% 16 == 0");
+    Stage stg(st);
+    return q_matmul(a, q, true, scale, c, m, n, k, st, stg, (const void *)wsw);
+}
 }  // namespace vmlm
 
 using namespace vmlm;

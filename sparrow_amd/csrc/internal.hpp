@@ -161,6 +161,31 @@ struct FqArgs {
 bool fq_gemv_ok(int M, int N, int K, int epi, int tw);
 int launch_fq_gemv(const FqArgs &a, hipStream_t st);
 
+// The standalone q8 GEMM at M <= FX_ROWS f32 rows in one launch
+// (k_q8gemv.hip): C[m][j] = (X[m] . W[j]) * scale[j], int8 weights
+// row-major [N][ldw] or swizzled (launch_swizzle_w's layout, N % 16 == 0).
+// fx_run_blocks(K) != 0 says a kernel exists for K.
+constexpr int FX_ROWS = 4;
+int fx_run_blocks(int K);
+struct FxArgs {
+    const void *W = nullptr;
+    bool swizzled = false;
+    int ldw = 0;
+    const float *scale = nullptr;
+    const float *X = nullptr;
+    int ldx = 0;
+    float *C = nullptr;
+    int ldc = 0;
+    int M = 0, N = 0, K = 0;
+    int kb = 0, tw = 0;  // blocks per wave run, 16-row tiles per workgroup (0: by shape)
+};
+int launch_fx_gemv(const FxArgs &a, hipStream_t st);
+// The int8 GEMM C[m][n] = (A[m] . Q[n]) * scale[n] (vmlm_hip_gemm_nt_int8) with
+// a swizzled copy wsw of Q (launch_swizzle_w, N % 16 == 0) that the caller
+// keeps, read instead of Q where a kernel takes that layout; wsw may be null.
+int q8_gemm_vm(const float *a, const int8_t *q, const int8_t *wsw, const float *scale, float *c,
+               size_t m, size_t n, size_t k, hipStream_t st);
+
 // int8 [N][K] row-major -> [N/16][K/64][64 lanes][16 B] MFMA-operand order.
 int launch_swizzle_w(const int8_t *src, int8_t *dst, int N, int K, hipStream_t st);
 

@@ -1,0 +1,314 @@
+// k_q8gemv.hip -- the standalone q8 GEMM at a few f32 rows (M <= 4) as one
+// launch: C[m][j] = (sum_k X[m][k] * (f32)W[j][k]) * scale[j]
+// (gemm_nt_int8, ops/src/kernels.rs:1256-1287) on rows and int8 weights the
+// caller owns -- the call of the FFI crate's gemm_nt_int8 and of the device
+// VM's OP_GEMM at decode rows.
+//
+// Design (gfx950):
+//  * A workgroup of NW waves owns TW 16-row tiles over the whole K; wave w
+//    takes the k-run of 64-wide blocks w*KB .. w*KB + KB - 1 (NW * KB = K/64)
+//    and issues all of its loads (the run of each input row, its weight
+//    blocks) before it waits on any.
+//  * The wave splits its run of each input row itself: every lane takes
+//    16-byte pieces of the row, the wave finds the row's maximum over the
+//    run and splits each value into Q8_T int8 terms with the power-of-two
+//    factor of that maximum (q8_row_k, q8_split) into a wave-private LDS
+//    slot; the live lanes read their B fragments from there. A row costs
+//    about 20 VALU operations per value and per workgroup, which is why
+//    this form stops at 4 rows.
+//  * Per block and tile Q8_T v_mfma_i32_16x16x64_i8 straight on the int8
+//    weights give exact int32 sums of each term over the run, combined once
+//    as (s0 + s1 / 2^7) + s2 / 2^14 times the row's run factor.
+//  * Weights row-major as passed (lane (g, r) reads bytes 16g .. 16g + 15 of
+//    the block on row r: one 16-byte load), or a swizzled copy (1 KiB MFMA
+//    blocks, lane (g, r) holding bytes 8g .. +7 and 32 + 8g .. +7). The B
+//    fragment of lane (g, n) takes the same k of row n, so each product
+//    pairs matching k.
+//  * The waves' partial tiles meet in LDS and are summed in wave order: the
+//    result does not depend on scheduling.
+//  * Non-finite rows: q8 gives a row holding NaN or +-inf a NaN factor, so
+//    its sums are NaN; the epilogue then classifies the row's products
+//    x * w in f32 (a NaN product, or both infinities: NaN; else the
+//    infinity that occurs), the reference's f32 value whatever its
+//    summation order.
+#include "internal.hpp"
+
+namespace vmlm {
+
+namespace {
+
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+
+struct FxParams {
+    const int8_t *W;     // row-major [N][ldw], or swizzled [N/16][K/64][1 KiB]
+    int ldw;
+    const float *scale;  // [N]
+    const float *X;      // [M][ldx]
+    int ldx;
+    float *C;            // [M][ldc]
+    int ldc;
+    int M, N, K;
+};
+
+// W[j][k] as f32 (the classification of non-finite rows)
+template <bool RM>
+__device__ __forceinline__ float fx_w(const FxParams &p, int j, int k) {
+    if constexpr (RM) return (float)p.W[(size_t)j * p.ldw + k];
+    const int o = k & 63, g = (o & 31) >> 3;
+    const size_t blk = (size_t)(j >> 4) * (p.K >> 6) + (k >> 6);
+    return (float)p.W[blk * 1024 + (size_t)(16 * g + (j & 15)) * 16 + (o >> 5) * 8 + (o & 7)];
+}
+
+// Row m . weight row j when row m holds a NaN or an infinity: NaN if a
+// product x * w is NaN or both infinities occur, else the infinity that
+// occurs; v (the q8 value) if no product is non-finite.
+template <bool RM>
+__device__ float fx_nonfinite(const FxParams &p, int m, int j, float v) {
+    const float *x = p.X + (size_t)m * p.ldx;
+    bool nan = false, pos = false, neg = false;
+    for (int k = 0; k < p.K; ++k) {
+        const float t = x[k] * fx_w<RM>(p, j, k);
+        nan = nan || t != t;
+        pos = pos || t == __builtin_inff();
+        neg = neg || t == -__builtin_inff();
+    }
+    if (nan || (pos && neg)) return __builtin_nanf("");
+    return pos ? __builtin_inff() : neg ? -__builtin_inff() : v;
+}
+
+// Maximum over the wave of a non-negative v (its bits order as int32), the
+// same in every lane: DPP steps inside each row of 16 lanes (quad swaps, then
+// row rotations by 4 and 8), then the four row maxima read as scalars.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    int x = __float_as_int(v);
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x124, 0xF, 0xF, false));  // row_ror:4
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false));  // row_ror:8
+    const int r = max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+                      max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+    return __int_as_float(r);
+}
+
+template <int KB, int NW, int TW, bool RM>
+__global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
+    constexpr int RUN = KB * 64;        // k of a wave's run
+    constexpr int PR = RUN / 4;         // 16-byte f32 pieces of a row's run
+    constexpr int XI = (PR + 63) / 64;  // pieces per lane and row
+    constexpr int SLD = RUN + 16;       // padded LDS row of the terms (bytes)
+    __shared__ __attribute__((aligned(16))) int8_t xs8[NW][Q8_T][FX_ROWS][SLD];
+    __shared__ float red[TW][NW][16][17];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int nkb = p.K >> 6;
+    const int kb0 = wave * KB;
+    const int ntile = (p.N + 15) >> 4;
+    const int tile0 = blockIdx.x * TW;
+    const int M = p.M;
+
+    // 1. every global read up front: the run of each input row (piece
+    // lane + 64 i), then the weight blocks of the run for each tile (rows
+    // past N read row N - 1)
+    float4 xv[FX_ROWS][XI];
+#pragma unroll
+    for (int m = 0; m < FX_ROWS; ++m) {
+        if (m < M) {  // uniform
+            const float *xrow = p.X + (size_t)m * p.ldx + (size_t)kb0 * 64;
+#pragma unroll
+            for (int i = 0; i < XI; ++i) {
+                const int e = lane + 64 * i < PR ? lane + 64 * i : PR - 1;
+                xv[m][i] = *(const float4 *)(xrow + 4 * e);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wr[TW][KB];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tl = tile0 + t < ntile ? tile0 + t : ntile - 1;
+        if constexpr (RM) {
+            const int row = tl * 16 + n < p.N ? tl * 16 + n : p.N - 1;
+            const int8_t *wt = p.W + (size_t)row * p.ldw + (size_t)kb0 * 64 + 16 * g;
+#pragma unroll
+            for (int i = 0; i < KB; ++i)
+                wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + 64 * i));
+        } else {
+            const int8_t *wt = p.W + ((size_t)tl * nkb + kb0) * 1024 + lane * 16;
+#pragma unroll
+            for (int i = 0; i < KB; ++i)
+                wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
+        }
+    }
+    // the scale of the thread's first epilogue output (row e0 % 16 of tile
+    // e0 / (16 M), e0 = tid)
+    const int e0 = tid < TW * 16 * M ? tid : 0;
+    const int row0 = (tile0 + e0 / (16 * M)) * 16 + (e0 & 15);
+    const float sc0 = p.scale[row0 < p.N ? row0 : p.N - 1];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. each row's run as int8 terms with the factor of its own maximum,
+    // into the wave's LDS slot (read back below by this wave only: its LDS
+    // operations complete in order)
+    float fac[FX_ROWS];
+#pragma unroll
+    for (int m = 0; m < FX_ROWS; ++m) {
+        fac[m] = 0.0f;
+        if (m < M) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < XI; ++i)
+                if (lane + 64 * i < PR)
+                    mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(xv[m][i].x), q8_mag(xv[m][i].y)),
+                                         fmaxf(q8_mag(xv[m][i].z), q8_mag(xv[m][i].w))));
+            const int k = q8_row_k(wave_max_nonneg(mx));
+            fac[m] = q8_factor(k);
+#pragma unroll
+            for (int i = 0; i < XI; ++i) {
+                const int e = lane + 64 * i;
+                if (e < PR) {
+                    int a[4][Q8_T];
+                    q8_split(xv[m][i].x, k, a[0]);
+                    q8_split(xv[m][i].y, k, a[1]);
+                    q8_split(xv[m][i].z, k, a[2]);
+                    q8_split(xv[m][i].w, k, a[3]);
+#pragma unroll
+                    for (int q = 0; q < Q8_T; ++q)
+                        *(uint32_t *)&xs8[wave][q][m][4 * e] =
+                            pack_i8x4(a[0][q], a[1][q], a[2][q], a[3][q]);
+                }
+            }
+        }
+    }
+    // the lanes of rows past M read row 0 (their columns are never stored)
+    const int nr = n < M ? n : 0;
+    i32x4 b[KB][Q8_T];
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q) {
+            if constexpr (RM) {
+                b[i][q] = *(const i32x4 *)&xs8[wave][q][nr][i * 64 + 16 * g];
+            } else {
+                const uint2 lo = *(const uint2 *)&xs8[wave][q][nr][i * 64 + 8 * g];
+                const uint2 hi = *(const uint2 *)&xs8[wave][q][nr][i * 64 + 32 + 8 * g];
+                b[i][q] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+        }
+    float rowf = fac[0];
+#pragma unroll
+    for (int m = 1; m < FX_ROWS; ++m)
+        if (n == m) rowf = fac[m];
+
+    // 3. per tile: Q8_T MFMAs per block, the run's exact int32 term sums
+    // combined once (the term weights and the factor are powers of two)
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        i32x4 s[Q8_T];
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q) s[q] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+            const i32x4 a = __builtin_bit_cast(i32x4, wr[t][i]);
+#pragma unroll
+            for (int q = 0; q < Q8_T; ++q)
+                s[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[i][q], s[q], 0, 0, 0);
+        }
+        // D[row 4g + j][column n]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float f = (float)s[0][j];
+#pragma unroll
+            for (int u = 1; u < Q8_T; ++u) f = __builtin_fmaf((float)s[u][j], q8_term_weight(u), f);
+            red[t][wave][4 * g + j][n] = f * rowf;
+        }
+    }
+    __syncthreads();
+
+    // 4. the waves' partial tiles summed in wave order, scaled and stored:
+    // consecutive threads take consecutive rows of one input row
+    for (int e = tid; e < TW * 16 * M; e += NW * 64) {
+        const int t = e / (16 * M), m = (e >> 4) % M, r = e & 15;
+        const int row = (tile0 + t) * 16 + r;
+        if (row < p.N) {
+            float s = red[t][0][r][m];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) s += red[t][w][r][m];
+            if (s != s) s = fx_nonfinite<RM>(p, m, row, s);
+            p.C[(size_t)m * p.ldc + row] = s * (e == tid ? sc0 : p.scale[row]);
+        }
+    }
+}
+
+template <int KB, int NW, int TW, bool RM>
+int launch_fx_t(const FxParams &p, hipStream_t st) {
+    const unsigned grid = (unsigned)((p.N + 16 * TW - 1) / (16 * TW));
+    fx_gemv_kernel<KB, NW, TW, RM><<<grid, NW * 64, 0, st>>>(p);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
+}  // namespace
+
+// (blocks per run, waves) pairs with a kernel: the decoder programs' K
+// (hidden 2304 or 768, inter 5760 or 2048) and small shapes
+#define FX_SHAPES(X) \
+    X(4, 9) X(6, 15) X(4, 3) X(4, 8) X(4, 6) X(4, 4) X(4, 2) X(4, 1) X(4, 16) X(2, 1) X(3, 1) X(6, 1)
+
+// The k-run per wave for K: K / 64 = waves * blocks with a kernel (4 blocks
+// preferred); 0 when there is none.
+int fx_run_blocks(int K) {
+    if (K < 128 || K % 64) return 0;
+    const int nkb = K / 64;
+    for (int kb : {4, 6, 3, 2}) {
+        if (nkb % kb) continue;
+        const int nw = nkb / kb;
+#define FX_HAS(KBV, NWV) \
+    if (kb == KBV && nw == NWV) return kb;
+        FX_SHAPES(FX_HAS)
+#undef FX_HAS
+    }
+    return 0;
+}
+
+int launch_fx_gemv(const FxArgs &a, hipStream_t st) {
+    const int kb = a.kb ? a.kb : fx_run_blocks(a.K);
+    const int nw = kb ? a.K / 64 / kb : 0;
+    // two tiles per workgroup for wide outputs (fewer, longer workgroups),
+    // one where the run is long (15 waves of 6 blocks: registers)
+    const int tw = a.tw ? a.tw : a.N >= 4096 && kb <= 4 ? 2 : 1;
+    VMLM_GUARD(a.M >= 1 && a.M <= FX_ROWS && a.N >= 1 && kb && a.K == 64 * kb * nw &&
+                   (tw == 1 || tw == 2),
+               "q8 GEMV: shape M=%d N=%d K=%d (M <= %d, K / 64 = waves x blocks), %d tiles", a.M,
+               a.N, a.K, FX_ROWS, tw);
+    VMLM_GUARD(a.W && a.scale && a.X && a.C && ((uintptr_t)a.X & 15) == 0 && a.ldx % 4 == 0 &&
+                   a.ldx >= a.K && a.ldc >= a.N && ((uintptr_t)a.W & 15) == 0 &&
+                   (a.swizzled ? a.N % 16 == 0 : a.ldw % 16 == 0 && a.ldw >= a.K),
+               "q8 GEMV: operands (16-byte aligned rows)");
+    FxParams p;
+    p.W = (const int8_t *)a.W;
+    p.ldw = a.ldw;
+    p.scale = a.scale;
+    p.X = a.X;
+    p.ldx = a.ldx;
+    p.C = a.C;
+    p.ldc = a.ldc;
+    p.M = a.M;
+    p.N = a.N;
+    p.K = a.K;
+#define FX_LAUNCH(KBV, NWV)                                                    \
+    if (kb == KBV && nw == NWV) {                                              \
+        if (a.swizzled)                                                        \
+            return tw == 2 ? launch_fx_t<KBV, NWV, 2, false>(p, st)            \
+                           : launch_fx_t<KBV, NWV, 1, false>(p, st);           \
+        return tw == 2 ? launch_fx_t<KBV, NWV, 2, true>(p, st)                 \
+                       : launch_fx_t<KBV, NWV, 1, true>(p, st);                \
+    }
+    FX_SHAPES(FX_LAUNCH)
+#undef FX_LAUNCH
+    return fail(VMLM_ERR_UNIMPL, "q8 GEMV: no kernel for K=%d (%d waves of %d blocks)", a.K, nw,
+                kb);
+}
+
+}  // namespace vmlm

@@ -27,6 +27,7 @@
 // runtime operand read from a slot (ROPE position from slot `dt`, WRITECOL
 // column from slot `dt`, SOFTMAX live width from slot `b`).
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -413,11 +414,18 @@ static unsigned vm_blocks(size_t n, unsigned per = 256) {
 // Constant pools on the device, shared by every VM loaded over the same
 // mapped host range (vmlm_vm_load with `weights`); an image's own CONST
 // region is uploaded privately.
+// A swizzled copy (launch_swizzle_w) of an int8 constant: the layout the
+// small-row GEMV and the int8-row GEMM read as whole 1 KiB MFMA blocks.
+struct SwzConst {
+    uint32_t rows, cols;
+    int8_t *dev;
+};
 struct ConstPool {
     const void *host;  // null: private
     size_t len;
     char *dev;
     int refs;
+    std::map<size_t, SwzConst> swz;  // by byte offset in the pool (int8 constants never change)
 };
 static std::mutex g_pool_mu;
 static std::vector<ConstPool *> g_pools;
@@ -429,6 +437,7 @@ static void pool_release(ConstPool *p) {
     if (--p->refs > 0) return;
     for (size_t i = 0; i < g_pools.size(); ++i)
         if (g_pools[i] == p) g_pools.erase(g_pools.begin() + i);
+    for (auto &kv : p->swz) (void)hipFree(kv.second.dev);
     (void)hipFree(p->dev);
     delete p;
 }
@@ -466,6 +475,7 @@ struct vmlm_vm {
     size_t ws_bytes = 0;
     unsigned long long *keys = nullptr;            // TOPK_IDX reduction keys
     int *guard = nullptr;  // this VM's device guard flag (index checks on device data)
+    std::map<size_t, SwzConst> swz;  // the pool's swizzled int8 constants (owned by the pool)
 };
 
 static uint32_t rd32(const uint8_t *p, size_t off) {
@@ -632,7 +642,40 @@ int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weig
     if ((e = hipMalloc((void **)&vm->keys, ARGMAX_KEYS * sizeof(unsigned long long))) != hipSuccess) return bad(hip_fail(e, "vm keys"));
     if ((e = hipMalloc((void **)&vm->guard, 64)) != hipSuccess) return bad(hip_fail(e, "vm guard"));
     if ((rc = launch_fill_zero(vm->guard, 64, vm->st))) return bad(rc);
-    if ((e = hipStreamSynchronize(vm->st)) != hipSuccess) return bad(hip_fail(e, "vm load"));
+    // every int8 constant (the audit admits them only as GEMM B) also in the
+    // swizzled layout, made once per pool; a constant whose copy does not fit
+    // in device memory stays row-major only
+    std::map<size_t, SwzConst> made;
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        for (const VmSlot &s : vm->slots) {
+            if (s.kind != VSLOT_CONST || s.dtype != VDT_I8 || !s.rows || s.rows % 16 ||
+                s.cols % 64 || (((uintptr_t)vm->pool->dev + s.off) & 15) ||
+                vm->pool->swz.count(s.off) || made.count(s.off))
+                continue;
+            int8_t *d = nullptr;
+            if (hipMalloc((void **)&d, (size_t)s.rows * s.cols) != hipSuccess) {
+                (void)hipGetLastError();
+                continue;
+            }
+            if ((rc = launch_swizzle_w((const int8_t *)(vm->pool->dev + s.off), d, (int)s.rows,
+                                       (int)s.cols, vm->st))) {
+                (void)hipFree(d);
+                for (auto &kv : made) (void)hipFree(kv.second.dev);
+                return bad(rc);
+            }
+            made[s.off] = SwzConst{s.rows, s.cols, d};
+        }
+    }
+    if ((e = hipStreamSynchronize(vm->st)) != hipSuccess) {
+        for (auto &kv : made) (void)hipFree(kv.second.dev);
+        return bad(hip_fail(e, "vm load"));
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        for (auto &kv : made) vm->pool->swz.insert(kv);
+        vm->swz = vm->pool->swz;
+    }
     *out = vm;
     return VMLM_OK;
 }
@@ -646,6 +689,12 @@ int vmlm_vm_pool_uploads(size_t *n) {
     VMLM_GUARD(n, "null argument");
     std::lock_guard<std::mutex> lk(g_pool_mu);
     *n = g_pool_uploads;
+    return VMLM_OK;
+}
+
+int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n) {
+    VMLM_GUARD(vm && n, "null argument");
+    *n = vm->swz.size();
     return VMLM_OK;
 }
 
@@ -776,7 +825,14 @@ int Exec::step(const VmIns &in, size_t *ip) {
             return vmlm_hip_gemm_nt_bf16(ca, (const uint16_t *)cb, cc, m, brows, k, st);
         if (bt == VDT_I8) {
             P_(cs, in.dt);
-            return vmlm_hip_gemm_nt_int8(ca, (const int8_t *)cb, cs, cc, m, brows, k, st);
+            // the swizzled copy made at load, when the read is one whole
+            // constant of this shape (through the layer base too)
+            const int8_t *wsw = nullptr;
+            const auto it = vm->swz.find((size_t)((char *)cb - vm->pool->dev));
+            if (it != vm->swz.end() && it->second.rows == brows && it->second.cols == bcols &&
+                bcols == k)
+                wsw = it->second.dev;
+            return q8_gemm_vm(ca, (const int8_t *)cb, wsw, cs, cc, m, brows, k, st);
         }
         NEED(bt == VDT_F32, "gemm operand dtype unsupported");
         return nt ? vmlm_hip_gemm_nt(ca, cb, cc, m, brows, k, acc, st)

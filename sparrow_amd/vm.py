@@ -77,6 +77,13 @@ class Vm:
     def clear_output(self) -> None:
         check(lib().vmlm_vm_clear_output(self._h))
 
+    def swizzled_consts(self) -> int:
+        """int8 constants also held in the swizzled MFMA layout, which
+        OP_GEMM reads instead of the row-major bytes."""
+        n = C.c_size_t()
+        check(lib().vmlm_vm_swizzled_consts(self._h, C.byref(n)))
+        return n.value
+
 
 def pool_uploads() -> int:
     n = C.c_size_t()

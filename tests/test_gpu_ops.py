@@ -47,7 +47,8 @@ def test_q8_kat(ops):
 
 @pytest.mark.parametrize("m,n,k", [(16, 2304, 2304), (1, 2304, 2304), (1, 5760, 2304),
                                    (4, 2304, 5760), (3, 17, 100), (40, 300, 256),
-                                   (128, 512, 2304)])
+                                   (128, 512, 2304), (1, 2304, 5760), (2, 100, 2304),
+                                   (4, 2304, 768), (1, 64, 128), (3, 48, 384), (2, 8192, 2304)])
 def test_gemm_nt_int8(ops, oracle, m, n, k):
     rng = np.random.default_rng(m * 7 + n + k)
     a, q, s = q8_case(rng, m, n, k)
@@ -117,6 +118,42 @@ def test_gemm_nt_int8_nonfinite(ops, oracle, m, k, path):
     clean = [i for i in range(m) if i not in (1, 2, m - 1, m - 2)]
     for i in clean:
         assert_close_rms(got[i], ref[i])
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemm_nt_int8_nonfinite_few_rows(ops, oracle, m):
+    """The one-launch form (M <= 4): a row holding NaN or +-inf gets the
+    reference's f32 pattern (its products classified after the q8 sums come
+    out NaN); the other rows are untouched."""
+    rng = np.random.default_rng(90 + m)
+    n, k = 256, 2304
+    a, q, s = q8_case(rng, m, n, k)
+    q[:40, 9] = 0                      # inf * 0 -> NaN in those columns
+    q[40:80, 5] = -q[40:80, 4]
+    a[0, 9] = -np.inf                  # -inf / +inf by the weight's sign, NaN at w = 0
+    if m == 4:
+        a[1, 7] = np.nan               # all NaN
+        a[3, 4] = np.inf               # +inf and -inf in one row: NaN where the two
+        a[3, 5] = -np.inf              # weights share a sign, +-inf elsewhere
+    got, ref = ops.gemm_nt_int8(a, q, s), oracle.gemm_nt_int8(a, q, s)
+    nonfinite_masks_equal(got, ref)
+    assert np.isnan(got[0, :40]).all() and np.isinf(got[0, 40:]).all()
+    assert np.isposinf(got[0]).any() and np.isneginf(got[0]).any()
+    if m == 4:
+        assert np.isnan(got[1]).all() and np.isfinite(got[3]).sum() == 0
+        assert_close_rms(got[2], ref[2])
+
+
+def test_gemm_nt_int8_exact_case_few_rows(ops):
+    """Integer activations at M <= 4 (the one-launch form): the int8 terms,
+    the int32 sums, the run factors and the wave-order sum are all exact."""
+    rng = np.random.default_rng(8)
+    for m, k in ((1, 2304), (3, 768), (4, 5760)):
+        a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+        q = rng.integers(-127, 128, size=(64, k), dtype=np.int8)
+        s = np.full(64, 1 / 64, np.float32)
+        ref = (a.astype(np.float64) @ q.astype(np.float64).T) / 64
+        assert np.array_equal(ops.gemm_nt_int8(a, q, s).astype(np.float64), ref), (m, k)
 
 
 def test_gemm_nt_bf16_nonfinite(ops, oracle):

@@ -200,6 +200,49 @@ def test_vm_op_zoo(gvm, oracle):
             assert np.abs(a - b).max() <= 1e-4 * rms, name
 
 
+@pytest.mark.parametrize("m", [1, 3, 5, 20])
+def test_vm_int8_gemm_swizzled_consts(gvm, oracle, m):
+    """OP_GEMM over int8 constants: the 96-row weight is also held in the
+    swizzled layout from load on (the small-row launch and the int8-row GEMM
+    read it), the 100-row one stays row-major only. Both against the oracle
+    VM within 1e-4 of each row's RMS, with the reference's non-finite
+    pattern for a NaN row and a row holding +inf."""
+    rng = np.random.default_rng(40 + m)
+    k = 768
+    P = vmb.Program()
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if m >= 3:
+        x[1, 5] = np.nan
+        x[2, 7] = np.inf
+    X = P.const("x", x)
+    outs = []
+    for name, n in (("ws", 96), ("wr", 100)):
+        w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        w[:8, 7] = 0
+        W = P.const(name, w, "i8")
+        sc = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
+        S = P.const(name + "_sc", sc, rows=n, cols=1)
+        Y = P.act("y" + name, m, n)
+        P.ins("GEMM", Y, X, W, dt=S)
+        outs.append("y" + name)
+    P.ins("HALT")
+    img = P.build()
+    with gvm.Vm(img) as g:
+        assert g.swizzled_consts() == 1
+        g.run()
+        got = [g.read(r) for r in outs]
+    with oracle.OracleVm(img) as o:
+        o.run()
+        ref = [o.read(r) for r in outs]
+    for a, b in zip(got, ref):
+        for f in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(f(a), f(b)), f.__name__
+        for i in range(m):
+            if np.isfinite(b[i]).all():
+                r = np.sqrt(np.mean(b[i].astype(np.float64) ** 2))
+                assert np.abs(a[i] - b[i]).max() <= 1e-4 * r, i
+
+
 @pytest.fixture(scope="module")
 def tiny():
     cfg = M.tiny_config(n_layers=3, hidden=256, n_heads=4, inter=512, vocab=1000)
