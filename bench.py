@@ -663,6 +663,64 @@ def run_decode(cfg, W, batch, steps, warmup, prompt_len=128, cap=1024):
     return dec, wall, ms.value / 1e3, t0, toks
 
 
+def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
+    """The step-looped decoder program (config 3 at batch 1) on the device
+    VM: one LOOP_CNT body per greedy step, run by the executor opcode by
+    opcode. Two programs of base and base + steps steps are loaded; each is
+    run once (first run: code objects, workspaces), then timed on a second
+    run, and the decode rate is steps / (t(base + steps) - t(base)). Its
+    greedy chain (st_gen, fed the session's first token) is compared with
+    the batch-1 session's over the same steps."""
+    from sparrow_amd import model as M
+    from sparrow_amd import programs, vmb
+    from sparrow_amd import vm as gvm
+    from sparrow_amd.decoder import Decoder
+    prompts = M.make_prompts(cfg, 1, prompt_len, seed=3)
+    dec = Decoder(cfg, batch=1, cap=1024)
+    dec.load(W)
+    chain = dec.generate(prompts, base + steps)[0]
+    dec.close()
+    times, gen, info = {}, None, {}
+    for G in (base, base + steps):
+        t = time.perf_counter()
+        P = programs.minicpm_program(cfg, W, prompt_len, G, step_loop=True, print_prefill=False)
+        loop = [i for i, ins in enumerate(P.text) if ins[0] == vmb.OP["LOOP_CNT"]][-1]
+        info["instructions_per_step"] = loop - P.text[loop][3] + 1  # LOOP_CNT jumps to dst
+        img = P.build()
+        del P
+        info["build_s"] = round(time.perf_counter() - t, 2)
+        t = time.perf_counter()
+        with gvm.Vm(img) as v:
+            del img
+            info["load_s"] = round(time.perf_counter() - t, 2)
+            info["swizzled_int8_consts"] = v.swizzled_consts()
+            v.write("st_tok", np.float32(prompts[0]))
+            v.write("st_gen", np.float32([chain[0]]))
+            v.run()
+            v.clear_output()
+            t = time.perf_counter()
+            v.run()
+            times[G] = time.perf_counter() - t
+            gen = v.read("st_gen")[0].astype(np.int64)
+    dt = times[base + steps] - times[base]
+    same = np.array_equal(gen, chain.astype(np.int64))
+    diff = np.nonzero(gen != chain)[0]
+    return {
+        "tokens_per_s": round(steps / dt, 2),
+        "ms_per_step": round(dt / steps * 1e3, 3),
+        "run_s": {str(k): round(v, 3) for k, v in times.items()},
+        "chain_equal_to_session": bool(same),
+        "first_difference": None if same else int(diff[0]),
+        "steps": steps,
+        "load": info,
+        "note": "step-looped program (programs.minicpm_program step_loop=True): prefill of the "
+                "128-token prompt, then a LOOP_CNT body per step (per layer: RMSNORM, q/k/v "
+                "GEMMs, per head SLICE/ROPE/TRANSPOSE/WRITECOL and GEMM/SCALE/SOFTMAX/GEMM, "
+                "then o, gate/up, down), one executor dispatch per opcode; the rate is the "
+                "difference of two programs' run times",
+    }
+
+
 def traffic_probe(iters, batches=(16, 1)):
     """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` runs: a plain device copy
     of 256 MiB (the calibration: its bytes are known) three times, then the
@@ -813,6 +871,9 @@ def main():
                          "and traffic counters of the batch-16 program")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
+    ap.add_argument("--no-vm", action="store_true",
+                    help="skip the device VM's step-looped decoder program")
+    ap.add_argument("--vm-steps", type=int, default=32)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -871,6 +932,13 @@ def main():
         dec1.close()
         log(f"batch 1: {args.steps} steps in {wall1 * 1e3:.1f} ms wall")
 
+    vm = None
+    if not args.no_vm:
+        vm = vm_step_loop(cfg, W, args.vm_steps)
+        log(f"device VM step loop: {vm['tokens_per_s']} tokens/s at batch 1 "
+            f"({vm['load']['instructions_per_step']} opcodes per step), chain equal to the "
+            f"session's: {vm['chain_equal_to_session']}")
+
     suite = None
     if not args.no_suite:
         suite = run_suite(args.suite_iters, cpu=not args.no_cpu)
@@ -910,6 +978,7 @@ def main():
         "batch1_tokens_per_s": round(args.steps / wall1, 2),
         "batch1_ms_per_step": round(wall1 / args.steps * 1e3, 4),
         "batch1_roofline": roof1,
+        "vm_step_loop_batch1": vm,
         "prefill": dict(prefill, prompt_len=128,
                         note="wall time of one prefill call (128 prompt tokens per sequence, "
                              "40 layers, LM head and first argmax): median of three "

@@ -156,13 +156,12 @@ class Program:
 
     # -------------------------------------------------------------- image
     def build(self) -> bytes:
-        cdata = bytearray()
-        offs = []
+        # constant offsets (each constant starts on a CONST_ALIGN boundary);
+        # the pool itself is written once into the final image below
+        offs, clen = [], 0
         for c in self.consts:
-            offs.append(len(cdata))
-            cdata += c.data
-            while len(cdata) % CONST_ALIGN:
-                cdata.append(0)
+            offs.append(clen)
+            clen += (len(c.data) + CONST_ALIGN - 1) // CONST_ALIGN * CONST_ALIGN
         cidx = {c.name: i for i, c in enumerate(self.consts)}
         region = {SLOT_ACT: 0, SLOT_STATE: 0, SLOT_GRAD: 0}
         idx = []
@@ -184,13 +183,24 @@ class Program:
             meta += struct.pack("<4I", s.kind, i, s.rows, s.cols)
         for s in self.slots:
             meta += struct.pack("<I", hash32(s.name))
-        text = b"".join(struct.pack("<BBHIII", *t) for t in self.text)
+        ins = struct.Struct("<BBHIII")
+        text = bytearray(ins.size * len(self.text))
+        for i, t in enumerate(self.text):
+            ins.pack_into(text, i * ins.size, *t)
         text_off = HEADER
         const_off = text_off + len(text)
-        meta_off = const_off + len(cdata)
+        meta_off = const_off + clen
         head = struct.pack("<IHHIIIIII", MAGIC, VERSION, 0, text_off, len(text), const_off,
-                           len(cdata), meta_off, len(meta))
-        return head + text + bytes(cdata) + bytes(meta)
+                           clen, meta_off, len(meta))
+        # one join: the image is allocated and written once
+        parts = [head, bytes(text)]
+        for c in self.consts:
+            parts.append(c.data)
+            pad = -len(c.data) % CONST_ALIGN
+            if pad:
+                parts.append(bytes(pad))
+        parts.append(bytes(meta))
+        return b"".join(parts)
 
 
 def parse(image: bytes) -> dict:
