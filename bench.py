@@ -430,9 +430,12 @@ def run_suite(iters, cpu=True):
         pre[name] = {"us": round(usp, 2), "host_us": round(wallp, 2), "timing": _LAST[0],
                      "useful_TOPs": round(useful, 1),
                      "frac_int8_peak_useful": round(useful / PEAK_INT8_TOPS, 4),
+                     "frac_bf16_peak_useful": round(useful / (PEAK_BF16_TFLOPS), 4),
                      "frac_int8_peak_issued": round(Q8_TERMS * useful / PEAK_INT8_TOPS, 4)}
     pre["note"] = (f"per call: rows_q8 + gemm_dma_i8_kernel + non-finite-row check; issued = "
-                   f"{Q8_TERMS} int8 MFMAs per product ({Q8_TERMS} int8 terms per activation)")
+                   f"{Q8_TERMS} int8 MFMAs per product ({Q8_TERMS} int8 terms per activation), so "
+                   f"useful work is at most 1/{Q8_TERMS} of the int8 peak "
+                   f"({PEAK_INT8_TOPS / Q8_TERMS / PEAK_BF16_TFLOPS:.3f} of the bf16 peak)")
     out["cfg3_prefill_gemm"] = pre
     if orc:
         af = orc.bf16_to_f32(a)
