@@ -330,6 +330,46 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// DPP forms of the wave reductions: no LDS round trip per step (each
+// __shfl_xor above is a ds_bpermute). Inside a row of 16 lanes: quad swaps
+// (quad_perm 1,0,3,2 and 2,3,0,1), then rotations of the row by 4 and 8.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL,
+                                                      0xF, 0xF, false));
+}
+// Maximum of a non-negative v over each row of 16 lanes, in every lane of
+// the row (exact in any order).
+__device__ __forceinline__ float row16_max_nonneg(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x124>(v));
+    return fmaxf(v, dpp_mov<0x128>(v));
+}
+// Maximum of a non-negative v over the wave, the same in every lane: the
+// four row maxima read as scalars.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = row16_max_nonneg(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48))));
+}
+// Sum over the wave in a fixed order, the same in every lane: lane 16r
+// holds row r's sum ((quad pairs), then the rotations), and the four row
+// sums are read as scalars and added as (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = v + dpp_mov<0xB1>(v);
+    v = v + dpp_mov<0x4E>(v);
+    v = v + dpp_mov<0x124>(v);
+    v = v + dpp_mov<0x128>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace vmlm

@@ -446,10 +446,7 @@ __global__ __launch_bounds__(NWV * 64) void ks_gemv_i8_kernel(KsParams p) {
         for (int i = 0; i < XPER; ++i)
             mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(xv[i].x), q8_mag(xv[i].y)),
                                  fmaxf(q8_mag(xv[i].z), q8_mag(xv[i].w))));
-        mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = row16_max_nonneg(mx);
         const int k = q8_row_k(mx);
         if (xc == 0) xf_s[xr] = q8_factor(k);
 #pragma unroll

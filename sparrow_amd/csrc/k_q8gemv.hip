@@ -76,20 +76,6 @@ __device__ float fx_nonfinite(const FxParams &p, int m, int j, float v) {
     return pos ? __builtin_inff() : neg ? -__builtin_inff() : v;
 }
 
-// Maximum over the wave of a non-negative v (its bits order as int32), the
-// same in every lane: DPP steps inside each row of 16 lanes (quad swaps, then
-// row rotations by 4 and 8), then the four row maxima read as scalars.
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    int x = __float_as_int(v);
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x124, 0xF, 0xF, false));  // row_ror:4
-    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false));  // row_ror:8
-    const int r = max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
-                      max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
-    return __int_as_float(r);
-}
-
 template <int KB, int NW, int TW, bool RM>
 __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     constexpr int RUN = KB * 64;        // k of a wave's run

@@ -275,8 +275,8 @@ __global__ __launch_bounds__(64) void resid_q8_kernel(
                                  fmaxf(q8_mag(xg[i].z), q8_mag(xg[i].w))));
         }
     }
-    ss = wave_sum(ss);
-    mg = wave_max(mg);
+    ss = wave_sum_dpp(ss);
+    mg = wave_max_nonneg(mg);
     const int k = q8_row_k(mg);
     if (lane == 0) {
         q8s[(size_t)sgi * rows + row] = q8_factor(k);
