@@ -93,6 +93,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void fq_gemv_kernel(FqParams p) {
     const int er = tid & 15;
     const float sspv = p.ssp && tid < 16 * nseg ? p.ssp[(tid >> 4) * p.M + (er < p.M ? er : 0)]
                                                 : 0.0f;
+    // the scales of the thread's first epilogue output (e = tid; one output
+    // per thread at the launch shapes), loaded with everything else
+    constexpr int NOUT = EPI == FQ_STORE ? TW * 256 : TW * 128;
+    const int e0 = tid < NOUT ? tid : 0;
+    const int row0 = EPI == FQ_STORE ? (tile0 + (e0 >> 8)) * 16 + (e0 & 15)
+                                     : (tile0 + 2 * (e0 >> 8)) * 16 + (e0 & 15);
+    const float sc0 = p.scale[row0];
+    const float sc1 = EPI == FQ_STORE ? 0.0f : p.scale[row0 + 16];
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. per tile: Q8_T MFMAs per block, exact int32 sums of each term over
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void fq_gemv_kernel(FqParams p) {
 #pragma unroll
             for (int w = 1; w < NW; ++w) s += red[t][w][r][m];
             const int row = (tile0 + t) * 16 + r;
-            if (m < p.M) p.Y[(size_t)m * p.ldy + row] = (s * p.scale[row]) * inv_of(m);
+            if (m < p.M) p.Y[(size_t)m * p.ldy + row] = (s * (e == tid ? sc0 : p.scale[row])) * inv_of(m);
         }
     } else {
         // pair pp: gate tile 2pp, up tile 2pp + 1, outputs 16 (pair index) + r
@@ -156,8 +164,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void fq_gemv_kernel(FqParams p) {
             }
             const float inv = inv_of(m);
             const int row = (tile0 + 2 * pp) * 16 + r;
-            const float gs = (sg * p.scale[row]) * inv;
-            const float us = (su * p.scale[row + 16]) * inv;
+            const float gs = (sg * (e == tid ? sc0 : p.scale[row])) * inv;
+            const float us = (su * (e == tid ? sc1 : p.scale[row + 16])) * inv;
             if (m < p.M)
                 p.Y[(size_t)m * p.ldy + (tile0 / 2 + pp) * 16 + r] = (gs / (1.0f + exp_f(-gs))) * us;
         }
