@@ -697,6 +697,7 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
             del img
             info["load_s"] = round(time.perf_counter() - t, 2)
             info["swizzled_int8_consts"] = v.swizzled_consts()
+            info["fused_runs"] = v.fused_runs()
             v.write("st_tok", np.float32(prompts[0]))
             v.write("st_gen", np.float32([chain[0]]))
             v.run()
@@ -719,8 +720,10 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
         "note": "step-looped program (programs.minicpm_program step_loop=True): prefill of the "
                 "128-token prompt, then a LOOP_CNT body per step (per layer: RMSNORM, q/k/v "
                 "GEMMs, per head SLICE/ROPE/TRANSPOSE/WRITECOL and GEMM/SCALE/SOFTMAX/GEMM, "
-                "then o, gate/up, down), one executor dispatch per opcode; the rate is the "
-                "difference of two programs' run times",
+                "then o, gate/up, down). The executor dispatches opcode by opcode, except the "
+                "per-head runs it matched at load (fused_runs: each layer's cache append and "
+                "attention over all heads, one launch each); the rate is the difference of two "
+                "programs' run times",
     }
 
 

@@ -423,6 +423,12 @@ int vmlm_vm_pool_uploads(size_t *n);
  * counterpart in the reference (a layout of this build); for diagnostics
  * and tests. */
 int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n);
+/* Per-head opcode runs of the decode loop (the cache append and the
+ * attention of all heads of a layer) that this VM executes as one launch
+ * each, found at load. No counterpart in the reference (an execution
+ * strategy of this build: the interpreter runs them opcode by opcode with
+ * the same results); for diagnostics and tests. */
+int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n);
 
 /* ================================================================ tables */
 

@@ -154,6 +154,7 @@ SIGNATURES = {
     "vmlm_vm_stream": (P, [P]),
     "vmlm_vm_pool_uploads": (I, [C.POINTER(SZ)]),
     "vmlm_vm_swizzled_consts": (I, [P, C.POINTER(SZ)]),
+    "vmlm_vm_fused_runs": (I, [P, C.POINTER(SZ)]),
     "vmlm_hip_backend": (P, []),
     "vmlm_backend_dot256": (F, [P, P, SZ]),
     "vmlm_backend_axpy256": (None, [P, P, F, SZ]),

@@ -26,6 +26,7 @@
 // would read neighbouring memory), and bit 6 of `fl` gives three opcodes a
 // runtime operand read from a slot (ROPE position from slot `dt`, WRITECOL
 // column from slot `dt`, SOFTMAX live width from slot `b`).
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -210,6 +211,155 @@ __global__ void vm_emb_f32_kernel(float *d, const float *table, size_t rows, siz
     const long row = dev_index(rowf, (long)rows, guard);
     if (row < 0) return;
     for (size_t i = threadIdx.x; i < cols; i += blockDim.x) d[i] = table[(size_t)row * cols + i];
+}
+
+// ---------------------------------------------------------------- fused blocks
+// The decode loop of the reference's step-looped program repeats two
+// opcode runs per head of every layer (tools/p14_gen_build.py:470-560): the
+// cache append SLICE k, SLICE v, ROPE, TRANSPOSE x2, WRITECOL x2, and the
+// attention SLICE q, ROPE, GEMM (scores), SCALE, SOFTMAX (live width), GEMM
+// (context), WRITECOL. The loader recognises such runs over all heads and
+// the executor runs each as one launch over the heads with the same results:
+// the same rotation (rope_pair, the ROPE step), the same guards on the
+// device position and live width, the softmax of vm_softmax_live_kernel
+// (block max, exp_f, block sum, times 1 / sum), and the scratch slots left
+// holding the last head's values as the opcode run leaves them. The score
+// and context dot products are f32 sums in k order (the GEMM kernel's
+// order differs; both are within the GEMM contract).
+struct VmKvAppend {
+    const float *k, *v;          // [1, nh * hd] rows of k and v
+    float *const *kc;            // [nh] caches [hd, cols] (K), then [nh] (V)
+    const float *posp;
+    float step;
+    int hd, cols;
+    float *kdh, *vdh, *kdrot, *kdT, *vdT;  // the last head's scratch
+};
+
+// One workgroup per head: rotates k at the device position, writes k and v
+// into column `pos` of the head's caches.
+__global__ __launch_bounds__(64) void vm_kv_append_kernel(VmKvAppend a, int nh, int *guard) {
+    const int h = blockIdx.x, half = a.hd / 2;
+    const long pos = dev_index(a.posp, 1L << 24, guard);  // ROPE's check
+    const long col = dev_index(a.posp, (long)a.cols + 1, guard);  // WRITECOL's
+    const bool wr = col >= 0 && col + 1 <= a.cols;
+    if (col >= 0 && !wr) atomicOr(guard, 1);
+    const float *kr = a.k + (size_t)h * a.hd, *vr = a.v + (size_t)h * a.hd;
+    float *kc = a.kc[h], *vc = a.kc[nh + h];
+    const bool last = h == nh - 1;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float x1 = kr[i], x2 = kr[i + half];
+        if (last) {
+            a.kdh[i] = x1;
+            a.kdh[i + half] = x2;
+        }
+        if (pos < 0) continue;
+        float y1, y2;
+        rope_pair(x1, x2, (float)pos, i, a.step, &y1, &y2);
+        if (last) {
+            a.kdrot[i] = y1;
+            a.kdrot[i + half] = y2;
+            a.kdT[i] = y1;
+            a.kdT[i + half] = y2;
+        }
+        if (wr) {
+            kc[(size_t)i * a.cols + col] = y1;
+            kc[(size_t)(i + half) * a.cols + col] = y2;
+        }
+    }
+    for (int i = threadIdx.x; i < a.hd; i += blockDim.x) {
+        const float x = vr[i];
+        if (last) {
+            a.vdh[i] = x;
+            a.vdT[i] = x;
+        }
+        if (wr) vc[(size_t)i * a.cols + col] = x;
+    }
+}
+
+struct VmHeadAttn {
+    const float *q;              // [1, nh * hd]
+    float *const *kc;            // [nh] K caches [hd, cols], then [nh] V caches
+    const float *posp, *livep, *scalep;
+    float step;
+    int hd, cols;
+    float *att;                  // [1, >= nh * hd]
+    float *qdh, *qdrot, *scd, *ctxd;  // the last head's scratch
+};
+constexpr int VM_ATTN_MAX_COLS = 8192;
+
+// One workgroup of 256 threads per head: q rotated into LDS, the scores of
+// every cached column (sum over k in order) times the scale, the softmax of
+// the first `live` columns (zeros past them), and the context over all
+// columns, as the GEMM-SCALE-SOFTMAX-GEMM run computes them.
+__global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh, int *guard) {
+    extern __shared__ float sm[];     // q[hd], p[cols]
+    __shared__ float red[4];
+    float *qs = sm, *pr = sm + a.hd;
+    const int h = blockIdx.x, half = a.hd / 2, tid = threadIdx.x;
+    const long pos = dev_index(a.posp, 1L << 24, guard);
+    const long live = dev_index(a.livep, (long)a.cols + 1, guard);
+    if (pos < 0 || live < 0) return;
+    const bool last = h == nh - 1;
+    const float *qr = a.q + (size_t)h * a.hd;
+    for (int i = tid; i < half; i += 256) {
+        const float x1 = qr[i], x2 = qr[i + half];
+        float y1, y2;
+        rope_pair(x1, x2, (float)pos, i, a.step, &y1, &y2);
+        qs[i] = y1;
+        qs[i + half] = y2;
+        if (last) {
+            a.qdh[i] = x1;
+            a.qdh[i + half] = x2;
+            a.qdrot[i] = y1;
+            a.qdrot[i + half] = y2;
+        }
+    }
+    __syncthreads();
+    const float *K = a.kc[h], *V = a.kc[nh + h];
+    const float sc = *a.scalep;
+    for (int c = tid; c < a.cols; c += 256) {
+        float s = 0.0f;
+        for (int k = 0; k < a.hd; ++k) s += qs[k] * K[(size_t)k * a.cols + c];
+        pr[c] = s * sc;
+    }
+    __syncthreads();
+    const int lim = (int)live;
+    float mx = -INFINITY;
+    for (int i = tid; i < lim; i += 256) mx = fmaxf(mx, pr[i]);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = tid; i < lim; i += 256) {
+        const float e = exp_f(pr[i] - mx);
+        pr[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    s = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / s;
+    for (int i = tid; i < lim; i += 256) pr[i] *= inv;
+    for (int i = lim + tid; i < a.cols; i += 256) pr[i] = 0.0f;
+    __syncthreads();
+    if (last)
+        for (int i = tid; i < a.cols; i += 256) a.scd[i] = pr[i];
+    // context: wave w takes rows w, w + 4, ...; its lanes sum columns in
+    // order per lane, then the wave sums its lanes
+    const int w = tid >> 6, lane = tid & 63;
+    for (int r = w; r < a.hd; r += 4) {
+        const float *vr = V + (size_t)r * a.cols;
+        float t = 0.0f;
+        for (int c = lane; c < a.cols; c += 64) t += pr[c] * vr[c];
+        t = wave_sum_dpp(t);
+        if (lane == 0) {
+            a.att[(size_t)h * a.hd + r] = t;
+            if (last) a.ctxd[r] = t;
+        }
+    }
 }
 
 // ROPE with the position read from the device (runtime position): the
@@ -458,6 +608,19 @@ struct VmSlot {
     uint8_t dtype;
 };
 
+// A run of the decode loop's per-head opcodes that the executor launches as
+// one kernel (vm_kv_append_kernel, vm_head_attn_kernel).
+enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2 };
+struct VmFused {
+    int kind = 0;
+    uint32_t len = 0;        // instructions replaced
+    uint32_t nh = 0, hd = 0, cols = 0;
+    uint32_t k = 0, v = 0;   // KV_APPEND: the k and v rows; HEAD_ATTN: q in k
+    uint32_t theta = 0, pos = 0, live = 0, scale = 0, att = 0;
+    uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;  // scratch slots, in opcode order
+    float **tab = nullptr;   // device: the nh K cache addresses, then the nh V
+};
+
 struct vmlm_vm {
     std::vector<VmIns> text;
     std::vector<VmSlot> slots;
@@ -476,6 +639,8 @@ struct vmlm_vm {
     unsigned long long *keys = nullptr;            // TOPK_IDX reduction keys
     int *guard = nullptr;  // this VM's device guard flag (index checks on device data)
     std::map<size_t, SwzConst> swz;  // the pool's swizzled int8 constants (owned by the pool)
+    std::vector<VmFused> fused;      // opcode runs executed as one launch each
+    std::vector<int32_t> fuse_at;    // per instruction: index into `fused`, or -1
 };
 
 static uint32_t rd32(const uint8_t *p, size_t off) {
@@ -491,6 +656,8 @@ static void vm_free(vmlm_vm *vm) {
     for (void *p : {(void *)vm->act, (void *)vm->state, (void *)vm->grad, vm->ws, (void *)vm->keys,
                     (void *)vm->guard})
         if (p) (void)hipFree(p);
+    for (VmFused &f : vm->fused)
+        if (f.tab) (void)hipFree(f.tab);
     if (vm->st) (void)hipStreamDestroy(vm->st);
     delete vm;
 }
@@ -523,6 +690,199 @@ static int vm_audit(const vmlm_vm *vm) {
                         "op %u uses %s const at slot %u (only a GEMM may read a non-f32 operand)",
                         in.op, d == VDT_BF16 ? "bf16" : d == VDT_I8 ? "i8" : "non-f32", s);
         }
+    }
+    return VMLM_OK;
+}
+
+// The loader's matcher for the decode loop's per-head runs (see
+// VmKvAppend, VmHeadAttn): every head's run must be the same opcodes over
+// the same scratch slots, with the row offsets of consecutive heads and a
+// cache pair of its own; the shapes must make each opcode's static guard
+// pass; the slots written must be f32 activation or state slots, distinct
+// from each other and from the slots read; and no jump may land inside the
+// run. Anything else runs opcode by opcode.
+static int vm_detect_fusions(vmlm_vm *vm) {
+    const std::vector<VmIns> &T = vm->text;
+    const size_t n = T.size(), ns = vm->slots.size();
+    vm->fuse_at.assign(n, -1);
+    std::vector<char> target(n + 1, 0);
+    for (const VmIns &in : T)
+        if ((in.op == VOP_JMP || in.op == VOP_CMPLE || in.op == VOP_TOPK_THRESH ||
+             in.op == VOP_LOOP_CNT) && in.dst <= n)
+            target[in.dst] = 1;
+    auto ok = [&](uint32_t i) { return i < ns; };
+    auto rows = [&](uint32_t i) { return (size_t)vm->slots[i].rows; };
+    auto cols = [&](uint32_t i) { return (size_t)vm->slots[i].cols; };
+    auto f32 = [&](uint32_t i) { return ok(i) && vm->slots[i].dtype == VDT_F32; };
+    auto data = [&](uint32_t i) {
+        return f32(i) && (vm->slots[i].kind == VSLOT_ACT || vm->slots[i].kind == VSLOT_STATE);
+    };
+    auto same = [](const VmIns &x, uint8_t op, uint8_t fl, uint32_t d, uint32_t a, uint32_t b,
+                   uint16_t dt) {
+        return x.op == op && x.fl == fl && x.dst == d && x.a == a && x.b == b && x.dt == dt;
+    };
+    // written slots pairwise distinct and never read by the run
+    auto disjoint = [](std::vector<uint32_t> w, const std::vector<uint32_t> &r) {
+        std::sort(w.begin(), w.end());
+        if (std::adjacent_find(w.begin(), w.end()) != w.end()) return false;
+        for (uint32_t x : r)
+            if (std::binary_search(w.begin(), w.end(), x)) return false;
+        return true;
+    };
+    constexpr uint8_t RT = VFL_RUNTIME;
+    std::vector<float *> tab;
+    for (size_t i = 0; i + 7 <= n;) {
+        const VmIns &h0 = T[i];
+        VmFused f;
+        std::vector<uint32_t> caches;
+        if (h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_SLICE &&
+            T[i + 2].op == VOP_ROPE) {  // cache append
+            const uint32_t kdh = h0.dst, kd = h0.a, vdh = T[i + 1].dst, vd = T[i + 1].a;
+            const uint32_t kdrot = T[i + 2].dst, th = T[i + 2].b, pos = T[i + 2].dt;
+            const uint32_t kdT = T[i + 3].dst, vdT = T[i + 4].dst;
+            if (ok(kdh) && ok(vdh) && ok(kdrot) && ok(kdT) && ok(vdT)) {
+                const size_t hd = cols(kdh);
+                size_t j = 0;
+                for (; i + 7 * (j + 1) <= n; ++j) {
+                    const VmIns *g = &T[i + 7 * j];
+                    const uint32_t off = (uint32_t)(j * hd);
+                    if (!(same(g[0], VOP_SLICE, 0, kdh, kd, off, g[0].dt) &&
+                          same(g[1], VOP_SLICE, 0, vdh, vd, off, g[1].dt) &&
+                          same(g[2], VOP_ROPE, RT, kdrot, kdh, th, (uint16_t)pos) &&
+                          same(g[3], VOP_TRANSPOSE, 0, kdT, kdrot, g[3].b, g[3].dt) &&
+                          same(g[4], VOP_TRANSPOSE, 0, vdT, vdh, g[4].b, g[4].dt) &&
+                          same(g[5], VOP_WRITECOL, RT, g[5].dst, kdT, 0, (uint16_t)pos) &&
+                          same(g[6], VOP_WRITECOL, RT, g[6].dst, vdT, 0, (uint16_t)pos)))
+                        break;
+                    bool inside = false;
+                    for (size_t t = 1; t <= 7; ++t) inside |= target[i + 7 * j + t] && t < 7;
+                    if (j > 0) inside |= target[i + 7 * j];
+                    if (inside) break;
+                    caches.push_back(g[5].dst);
+                    caches.push_back(g[6].dst);
+                }
+                const size_t nh = j;
+                bool good = nh >= 2 && hd >= 2 && hd % 2 == 0 && hd <= 4096 && pos == T[i + 2].dt;
+                good = good && data(kdh) && data(vdh) && data(kdrot) && data(kdT) && data(vdT) &&
+                       f32(kd) && f32(vd) && f32(th) && f32(pos) && rows(kdh) == 1 &&
+                       rows(vdh) == 1 && cols(vdh) == hd && rows(kdrot) == 1 &&
+                       cols(kdrot) == hd && rows(kdT) == hd && cols(kdT) == 1 && rows(vdT) == hd &&
+                       cols(vdT) == 1 && rows(kd) * cols(kd) >= nh * hd &&
+                       rows(vd) * cols(vd) >= nh * hd;
+                size_t cc = 0;
+                for (size_t c = 0; good && c < caches.size(); ++c) {
+                    const uint32_t x = caches[c];
+                    good = data(x) && rows(x) == hd && cols(x) >= 1 && (c == 0 || cols(x) == cc);
+                    cc = cols(x);
+                }
+                std::vector<uint32_t> w = {kdh, vdh, kdrot, kdT, vdT};
+                w.insert(w.end(), caches.begin(), caches.end());
+                good = good && disjoint(w, {kd, vd, th, pos});
+                if (good) {
+                    f.kind = VF_KV_APPEND;
+                    f.len = (uint32_t)(7 * nh);
+                    f.nh = (uint32_t)nh;
+                    f.hd = (uint32_t)hd;
+                    f.cols = (uint32_t)cc;
+                    f.k = kd;
+                    f.v = vd;
+                    f.theta = th;
+                    f.pos = pos;
+                    f.s0 = kdh;
+                    f.s1 = vdh;
+                    f.s2 = kdrot;
+                    f.s3 = kdT;
+                    f.s4 = vdT;
+                    // K caches (even entries), then V caches (odd)
+                    std::vector<uint32_t> kc, vc;
+                    for (size_t c = 0; c < caches.size(); c += 2) {
+                        kc.push_back(caches[c]);
+                        vc.push_back(caches[c + 1]);
+                    }
+                    caches = kc;
+                    caches.insert(caches.end(), vc.begin(), vc.end());
+                }
+            }
+        } else if (h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_ROPE &&
+                   T[i + 2].op == VOP_GEMM) {  // attention per head
+            const uint32_t qdh = h0.dst, qd = h0.a, qdrot = T[i + 1].dst, th = T[i + 1].b,
+                           pos = T[i + 1].dt, scd = T[i + 2].dst, sc = T[i + 3].b,
+                           live = T[i + 4].b, ctxd = T[i + 5].dst, att = T[i + 6].dst;
+            if (ok(qdh) && ok(qdrot) && ok(scd) && ok(ctxd) && ok(att)) {
+                const size_t hd = cols(qdh);
+                size_t j = 0;
+                std::vector<uint32_t> kc, vc;
+                for (; i + 7 * (j + 1) <= n; ++j) {
+                    const VmIns *g = &T[i + 7 * j];
+                    const uint32_t off = (uint32_t)(j * hd);
+                    if (!(same(g[0], VOP_SLICE, 0, qdh, qd, off, g[0].dt) &&
+                          same(g[1], VOP_ROPE, RT, qdrot, qdh, th, (uint16_t)pos) &&
+                          same(g[2], VOP_GEMM, VFL_TRANS_B, scd, qdrot, g[2].b, g[2].dt) &&
+                          same(g[3], VOP_SCALE, 0, scd, scd, sc, g[3].dt) &&
+                          same(g[4], VOP_SOFTMAX, RT, scd, scd, live, g[4].dt) &&
+                          same(g[5], VOP_GEMM, 0, ctxd, scd, g[5].b, g[5].dt) &&
+                          same(g[6], VOP_WRITECOL, 0, att, ctxd, off, g[6].dt)))
+                        break;
+                    bool inside = false;
+                    for (size_t t = 1; t < 7; ++t) inside |= target[i + 7 * j + t];
+                    if (j > 0) inside |= target[i + 7 * j];
+                    if (inside) break;
+                    kc.push_back(g[2].b);
+                    vc.push_back(g[5].b);
+                }
+                const size_t nh = j, C = ok(scd) ? cols(scd) : 0;
+                bool good = nh >= 2 && hd >= 2 && hd % 2 == 0 && hd <= 4096 && C >= 1 &&
+                            C <= (size_t)VM_ATTN_MAX_COLS && data(qdh) && data(qdrot) &&
+                            data(scd) && data(ctxd) && data(att) && f32(qd) && f32(th) &&
+                            f32(pos) && f32(sc) && f32(live) && rows(qdh) == 1 &&
+                            rows(qdrot) == 1 && cols(qdrot) == hd && rows(scd) == 1 &&
+                            rows(ctxd) == 1 && cols(ctxd) == hd && rows(att) == 1 &&
+                            cols(att) >= nh * hd && rows(qd) * cols(qd) >= nh * hd &&
+                            rows(sc) * cols(sc) >= 1;
+                for (size_t c = 0; good && c < nh; ++c)
+                    good = f32(kc[c]) && rows(kc[c]) == hd && cols(kc[c]) == C && f32(vc[c]) &&
+                           rows(vc[c]) == hd && cols(vc[c]) == C;
+                std::vector<uint32_t> r = {qd, th, pos, sc, live};
+                r.insert(r.end(), kc.begin(), kc.end());
+                r.insert(r.end(), vc.begin(), vc.end());
+                good = good && disjoint({qdh, qdrot, scd, ctxd, att}, r);
+                if (good) {
+                    f.kind = VF_HEAD_ATTN;
+                    f.len = (uint32_t)(7 * nh);
+                    f.nh = (uint32_t)nh;
+                    f.hd = (uint32_t)hd;
+                    f.cols = (uint32_t)C;
+                    f.k = qd;
+                    f.theta = th;
+                    f.pos = pos;
+                    f.live = live;
+                    f.scale = sc;
+                    f.att = att;
+                    f.s0 = qdh;
+                    f.s1 = qdrot;
+                    f.s2 = scd;
+                    f.s3 = ctxd;
+                    caches = kc;
+                    caches.insert(caches.end(), vc.begin(), vc.end());
+                }
+            }
+        }
+        if (!f.kind) {
+            ++i;
+            continue;
+        }
+        // the cache addresses (activation and state slots do not move)
+        std::vector<float *> addr;
+        for (uint32_t c : caches) {
+            const VmSlot &sl = vm->slots[c];
+            addr.push_back((float *)((sl.kind == VSLOT_STATE ? vm->state : vm->act) + sl.off));
+        }
+        VMLM_HIP_CHECK(hipMalloc((void **)&f.tab, addr.size() * sizeof(float *)));
+        vm->fused.push_back(f);  // freed with the VM from here on
+        VMLM_HIP_CHECK(hipMemcpy(f.tab, addr.data(), addr.size() * sizeof(float *),
+                                 hipMemcpyHostToDevice));
+        vm->fuse_at[i] = (int32_t)vm->fused.size() - 1;
+        i += f.len;
     }
     return VMLM_OK;
 }
@@ -642,6 +1002,7 @@ int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weig
     if ((e = hipMalloc((void **)&vm->keys, ARGMAX_KEYS * sizeof(unsigned long long))) != hipSuccess) return bad(hip_fail(e, "vm keys"));
     if ((e = hipMalloc((void **)&vm->guard, 64)) != hipSuccess) return bad(hip_fail(e, "vm guard"));
     if ((rc = launch_fill_zero(vm->guard, 64, vm->st))) return bad(rc);
+    if ((rc = vm_detect_fusions(vm))) return bad(rc);
     // every int8 constant (the audit admits them only as GEMM B) also in the
     // swizzled layout, made once per pool; a constant whose copy does not fit
     // in device memory stays row-major only
@@ -695,6 +1056,12 @@ int vmlm_vm_pool_uploads(size_t *n) {
 int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n) {
     VMLM_GUARD(vm && n, "null argument");
     *n = vm->swz.size();
+    return VMLM_OK;
+}
+
+int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n) {
+    VMLM_GUARD(vm && n, "null argument");
+    *n = vm->fused.size();
     return VMLM_OK;
 }
 
@@ -784,6 +1151,7 @@ struct Exec {
     }
 
     int step(const VmIns &in, size_t *ip);
+    int fused(const VmFused &f);
 };
 
 #define P_(name, slot)                 \
@@ -1229,6 +1597,62 @@ extern "C" {
 
 // The slot an instruction writes: `dst`, or `a` for LOOP_CNT (its counter)
 // and STACK_INIT; UINT32_MAX for instructions that write no slot.
+// A run found by vm_detect_fusions, in one launch: the host-side guards of
+// its opcodes (ROPE's theta), then the kernel with the device-side ones.
+int Exec::fused(const VmFused &f) {
+    int rc = VMLM_OK;
+    float theta;
+    if ((rc = scalar(f.theta, &theta))) return rc;
+    VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
+    const float step = -2.0f / (float)f.hd * host_ln_f(theta);
+    hipStream_t st = vm->st;
+    if (f.kind == VF_KV_APPEND) {
+        VmKvAppend a;
+        float *k, *v, *pp, *s0, *s1, *s2, *s3, *s4;
+        if ((rc = ptr(f.k, &k)) || (rc = ptr(f.v, &v)) || (rc = ptr(f.pos, &pp)) ||
+            (rc = ptr(f.s0, &s0)) || (rc = ptr(f.s1, &s1)) || (rc = ptr(f.s2, &s2)) ||
+            (rc = ptr(f.s3, &s3)) || (rc = ptr(f.s4, &s4)))
+            return rc;
+        a.k = k;
+        a.v = v;
+        a.kc = f.tab;
+        a.posp = pp;
+        a.step = step;
+        a.hd = (int)f.hd;
+        a.cols = (int)f.cols;
+        a.kdh = s0;
+        a.vdh = s1;
+        a.kdrot = s2;
+        a.kdT = s3;
+        a.vdT = s4;
+        vm_kv_append_kernel<<<f.nh, 64, 0, st>>>(a, (int)f.nh, guard);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
+    VmHeadAttn a;
+    float *q, *pp, *lp, *sp, *att, *s0, *s1, *s2, *s3;
+    if ((rc = ptr(f.k, &q)) || (rc = ptr(f.pos, &pp)) || (rc = ptr(f.live, &lp)) ||
+        (rc = ptr(f.scale, &sp)) || (rc = ptr(f.att, &att)) || (rc = ptr(f.s0, &s0)) ||
+        (rc = ptr(f.s1, &s1)) || (rc = ptr(f.s2, &s2)) || (rc = ptr(f.s3, &s3)))
+        return rc;
+    a.q = q;
+    a.kc = f.tab;
+    a.posp = pp;
+    a.livep = lp;
+    a.scalep = sp;
+    a.step = step;
+    a.hd = (int)f.hd;
+    a.cols = (int)f.cols;
+    a.att = att;
+    a.qdh = s0;
+    a.qdrot = s1;
+    a.scd = s2;
+    a.ctxd = s3;
+    vm_head_attn_kernel<<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
+}
+
 static uint32_t written_slot(const VmIns &in) {
     switch (in.op) {
     case VOP_SHAPE: case VOP_JMP: case VOP_CMPLE: case VOP_LAYERB: case VOP_PRINT:
@@ -1268,6 +1692,15 @@ int vmlm_vm_run(vmlm_vm *vm) {
     size_t ip = 0;
     const size_t n = vm->text.size();
     while (ip < n) {
+        if (vm->fuse_at[ip] >= 0) {  // a per-head run in one launch (no constant written)
+            const VmFused &f = vm->fused[vm->fuse_at[ip]];
+            if ((rc = ex.fused(f))) {
+                (void)hipStreamSynchronize(vm->st);
+                return rc;
+            }
+            ip += f.len;
+            continue;
+        }
         const VmIns in = vm->text[ip++];
         if (in.op == VOP_HALT) break;
         if ((rc = const_write_check(vm, in, ip - 1)) || (rc = ex.step(in, &ip))) {

@@ -77,6 +77,13 @@ class Vm:
     def clear_output(self) -> None:
         check(lib().vmlm_vm_clear_output(self._h))
 
+    def fused_runs(self) -> int:
+        """Per-head opcode runs of the decode loop executed as one launch
+        each (found at load)."""
+        n = C.c_size_t()
+        check(lib().vmlm_vm_fused_runs(self._h, C.byref(n)))
+        return n.value
+
     def swizzled_consts(self) -> int:
         """int8 constants also held in the swizzled MFMA layout, which
         OP_GEMM reads instead of the row-major bytes."""

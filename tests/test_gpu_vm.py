@@ -290,6 +290,111 @@ def test_vm_looped_and_step_loop(gvm, tiny):
     assert np.array_equal(toks[0], toks[1])
 
 
+def test_vm_fused_head_runs(gvm, oracle, tiny):
+    """The step-looped decode's per-head runs (cache append; attention) run
+    as one launch each per layer: the same greedy tokens as the oracle VM,
+    and the step logits, the last head's scratch slots, the K/V caches and
+    the attention rows within 1e-4 RMS (they follow the projections' GEMM
+    numerics; the runs' own rotation and copies are checked bitwise on exact
+    inputs below). The unrolled program (compile-time positions) runs opcode
+    by opcode."""
+    cfg, W = tiny
+    S, G = 6, 5
+    prompt = M.make_prompts(cfg, 1, S, seed=9)[0]
+    img = programs.minicpm_program(cfg, W, S, G, step_loop=True, print_prefill=False).build()
+    nl, nh = cfg["n_layers"], cfg["n_heads"]
+    exact = ["st_gen"]
+    approx = ["kdh", "vdh", "kdrot", "kdT", "vdT", "qdh", "qdrot", "scd", "ctxd", "attd"]
+    approx += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
+    approx += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
+    with gvm.Vm(img) as g:
+        assert g.fused_runs() == 2 * nl
+        g.write("st_tok", prompt)
+        g.write("st_gen", [11])
+        g.run()
+        gout, got = g.output(), {r: g.read(r) for r in exact + approx}
+    with oracle.OracleVm(img) as o:
+        o.write("st_tok", np.float32(prompt))
+        o.write("st_gen", np.float32([11]))
+        o.run()
+        oout, ref = o.output(), {r: o.read(r) for r in exact + approx}
+    for r in exact:
+        assert np.array_equal(bits(got[r]), bits(ref[r])), r
+    for r in approx:
+        rms = np.sqrt(np.mean(ref[r].astype(np.float64) ** 2))
+        assert np.abs(got[r] - ref[r]).max() <= 1e-4 * rms, r
+    gl, ol = gout.reshape(G, -1), oout.reshape(G, -1)
+    for s_ in range(G):
+        rms = np.sqrt(np.mean(ol[s_].astype(np.float64) ** 2))
+        assert np.abs(gl[s_] - ol[s_]).max() <= 1e-4 * rms, s_
+    with gvm.Vm(programs.minicpm_program(cfg, W, S, G).build()) as g:
+        assert g.fused_runs() == 0
+
+
+def test_vm_fused_runs_guard(gvm):
+    """Fused runs over exact inputs (constant rows): the rotated and copied
+    slots and the caches equal the oracle VM bitwise, the attention rows are
+    within 1e-4 RMS. A fused run keeps its opcodes' device guards: a
+    position past the cache (WRITECOL's runtime column) and a live width
+    past the scores (SOFTMAX) trip the VM's guard (status 9), as opcode by
+    opcode."""
+    rng = np.random.default_rng(2)
+    hd, nh, C = 8, 2, 6
+
+    def prog(pos, live):
+        P = vmb.Program()
+        x = P.const("x", rng.standard_normal((1, nh * hd)).astype(np.float32))
+        th = P.scalar("theta", 10000.0)
+        sc = P.scalar("sc", 0.5)
+        pp = P.scalar("pos", float(pos))
+        lv = P.scalar("live", float(live))
+        for name, r, c in (("kh", 1, hd), ("vh", 1, hd), ("kr", 1, hd), ("kT", hd, 1),
+                           ("vT", hd, 1), ("qh", 1, hd), ("qr", 1, hd), ("s", 1, C),
+                           ("ctx", 1, hd), ("att", 1, nh * hd)):
+            P.act(name, r, c)
+        for h in range(nh):
+            P.state(f"kc{h}", hd, C)
+            P.state(f"vc{h}", hd, C)
+        rt = vmb.FL_RUNTIME if hasattr(vmb, "FL_RUNTIME") else 64
+        for h in range(nh):
+            P.ins("SLICE", P["kh"], x, h * hd)
+            P.ins("SLICE", P["vh"], x, h * hd)
+            P.ins("ROPE", P["kr"], P["kh"], th, dt=pp, fl=rt)
+            P.ins("TRANSPOSE", P["kT"], P["kr"])
+            P.ins("TRANSPOSE", P["vT"], P["vh"])
+            P.ins("WRITECOL", P[f"kc{h}"], P["kT"], 0, dt=pp, fl=rt)
+            P.ins("WRITECOL", P[f"vc{h}"], P["vT"], 0, dt=pp, fl=rt)
+        for h in range(nh):
+            P.ins("SLICE", P["qh"], x, h * hd)
+            P.ins("ROPE", P["qr"], P["qh"], th, dt=pp, fl=rt)
+            P.ins("GEMM", P["s"], P["qr"], P[f"kc{h}"], fl=vmb.FL_TRANS_B)
+            P.ins("SCALE", P["s"], P["s"], sc)
+            P.ins("SOFTMAX", P["s"], P["s"], lv, fl=rt)
+            P.ins("GEMM", P["ctx"], P["s"], P[f"vc{h}"])
+            P.ins("WRITECOL", P["att"], P["ctx"], h * hd)
+        P.ins("HALT")
+        return P
+
+    from oracle import oracle as orc
+    img = prog(2, 3).build()
+    exact = ["kh", "vh", "kr", "kT", "vT", "qh", "qr", "kc0", "kc1", "vc0", "vc1"]
+    with gvm.Vm(img) as g:
+        assert g.fused_runs() == 2
+        g.run()
+        got = {r: g.read(r) for r in exact + ["att", "s", "ctx"]}
+    with orc.OracleVm(img) as o:
+        o.run()
+        ref = {r: o.read(r) for r in exact + ["att", "s", "ctx"]}
+    for r in exact:
+        assert np.array_equal(bits(got[r]), bits(ref[r])), r
+    for r in ("att", "s", "ctx"):
+        rms = np.sqrt(np.mean(ref[r].astype(np.float64) ** 2))
+        assert np.abs(got[r] - ref[r]).max() <= 1e-4 * rms, r
+    for pos, live in ((C, 3), (2, C + 1)):
+        c, m = codes(gvm, prog(pos, live))
+        assert c == 9 and "guard" in m, m
+
+
 def test_vm_shared_const_pool(gvm, tiny):
     """Two VMs over the same mapped weights region share one device pool
     (one upload); both run and agree bitwise."""
