@@ -41,6 +41,28 @@ def traffic_profile(dec):
     return TRAFFIC_PROFILE_FULLK if dec.program == dec.FULLK else TRAFFIC_PROFILE
 
 
+SUITE_KERNELS_PROFILE = os.path.join(ROOT, "profiles", "suite_device_api_kernels.md")
+
+
+def profiled_kernel_us(*names):
+    """Kernel-only mean and minimum duration (us) of the named kernels, summed,
+    from the rocprofv3 trace of the suite (profiles/suite_device_api_kernels.md),
+    or None when the file or a kernel is missing."""
+    try:
+        rows = {}
+        for line in open(SUITE_KERNELS_PROFILE):
+            parts = [x.strip() for x in line.strip().strip("|").split("|")]
+            if len(parts) == 4 and parts[0].startswith("`"):
+                rows[parts[0].strip("`")] = (float(parts[2]), float(parts[3]))
+        mean = sum(rows[n][0] for n in names)
+        mn = sum(rows[n][1] for n in names)
+    except (OSError, KeyError, ValueError):
+        return None
+    return {"mean_us": round(mean, 2), "min_us": round(mn, 2), "kernels": list(names),
+            "source": "profiles/suite_device_api_kernels.md (rocprofv3 per-dispatch durations, "
+                      "profiler overhead included)"}
+
+
 def measured_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per launch of the decode GEMV from the committed counter
     summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
@@ -246,6 +268,9 @@ def cache_note(set_bytes, sets):
             f"Infinity Cache")
 
 
+_EAGER = [False]  # --eager: no graph replay (kernel traces of the suite)
+
+
 def _timed(L, fn, iters):
     """Mean GPU time per call and host wall time per call. `fn(i)` issues
     call i (HBM-bound rows pick their buffer set from i).
@@ -276,7 +301,7 @@ def _timed(L, fn, iters):
     graph = C.c_void_p()
     _LAST[0] = "eager (host-issue bound)"
     L.vmlm_hip_event_release_all()
-    if L.vmlm_hip_capture_begin(None) != 0:
+    if _EAGER[0] or L.vmlm_hip_capture_begin(None) != 0:
         return eager, wall
     rc = 0
     for i in range(iters):
@@ -390,6 +415,9 @@ def run_suite(iters, cpu=True):
     if orc:
         cfg0["cpu_us_M16"] = _cpu_us(lambda: orc.gemm_nt_int8(x, q, sc))
         cfg0["cpu_threads"] = orc.get_threads()
+    cfg0["M16"]["kernel_only"] = profiled_kernel_us("gemv_wide_kernel<3, false, 2, 8, true>",
+                                                    "gemv_reduce_kernel")
+    cfg0["M1"]["kernel_only"] = profiled_kernel_us("fx_gemv_kernel<4, 9, 1, true>")
     out["cfg0_q8_gemm"] = cfg0
     # config 1: bf16 A[1024,512] . B[512,2048] (B passed as its [2048,512] transpose)
     rng = np.random.default_rng(1)
@@ -400,7 +428,8 @@ def run_suite(iters, cpu=True):
                       iters)
     tf = 2147483648 / us / 1e6
     out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0],
-                             "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+                             "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                             "kernel_only": profiled_kernel_us("gemm_dma_kernel<false, 1, 64, 128, 2>")}
     # config 1's M = 1 variant (the GEMV path of the same entry point)
     b1 = 2048 * 512 * 2 + 512 * 2 + 2048 * 4
     ns1 = n_sets(b1, 10**9)
@@ -877,6 +906,9 @@ def main():
                          "and traffic counters of the batch-16 program")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the copy + GEMV launches that the counter runs measure")
+    ap.add_argument("--eager", action="store_true",
+                    help="suite rows timed from eager launches only (no HIP graph replay): "
+                         "for rocprofv3 kernel traces of the suite's kernels")
     ap.add_argument("--no-vm", action="store_true",
                     help="skip the device VM's step-looped decoder program")
     ap.add_argument("--vm-steps", type=int, default=32)
@@ -891,6 +923,7 @@ def main():
     import sparrow_amd
     from sparrow_amd import model as M
     sparrow_amd.init(0)
+    _EAGER[0] = args.eager
     if args.traffic_probe:
         traffic_probe(20, (16,) if args.no_batch1 else (16, 1))
         return
