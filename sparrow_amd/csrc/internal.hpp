@@ -180,6 +180,27 @@ struct FxArgs {
     int kb = 0, tw = 0;  // blocks per wave run, 16-row tiles per workgroup (0: by shape)
 };
 int launch_fx_gemv(const FxArgs &a, hipStream_t st);
+// Up to three projections of the same rows in one launch (each output what
+// its own launch_fx_gemv gives), or, with `act`, a gate/up pair (two
+// segments of one width) that also writes act = silu(gate) * up.
+struct FxSegArgs {
+    const void *W = nullptr;
+    const float *scale = nullptr;
+    float *C = nullptr;
+    int N = 0, ldc = 0;
+};
+struct FxMultiArgs {
+    FxSegArgs seg[3];
+    int nseg = 0;
+    bool swizzled = false;
+    int ldw = 0;
+    const float *X = nullptr;
+    int ldx = 0;
+    int M = 0, K = 0;
+    float *act = nullptr;
+    int ldact = 0;
+};
+int launch_fx_multi(const FxMultiArgs &a, hipStream_t st);
 // The int8 GEMM C[m][n] = (A[m] . Q[n]) * scale[n] (vmlm_hip_gemm_nt_int8) with
 // a swizzled copy wsw of Q (launch_swizzle_w, N % 16 == 0) that the caller
 // keeps, read instead of Q where a kernel takes that layout; wsw may be null.

@@ -39,41 +39,68 @@ namespace {
 
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 
-struct FxParams {
+// Up to three output segments over one input (the q/k/v projections of a
+// decoder layer in one launch). Tiles 0 .. tstart[1] - 1 belong to segment
+// 0, and so on; with `pair`, workgroup i instead computes tile i of segment
+// 0 (gate) and tile i of segment 1 (up) and also writes act = silu(gate) *
+// up (the ACT and EWMUL after the gate/up projections). Every segment's
+// outputs are what its own launch would give: a tile's sums do not depend
+// on the tiles beside it.
+struct FxSeg {
     const int8_t *W;     // row-major [N][ldw], or swizzled [N/16][K/64][1 KiB]
-    int ldw;
     const float *scale;  // [N]
+    float *C;            // [M][ldc]
+    int N, ldc;
+};
+struct FxParams {
+    FxSeg seg[3];
+    int nseg;
+    int tstart[3];       // first tile of each segment
+    int pair;            // gate/up pair (TW == 2)
+    float *act;          // pair: [M][ldact]
+    int ldact;
+    int ldw;
     const float *X;      // [M][ldx]
     int ldx;
-    float *C;            // [M][ldc]
-    int ldc;
-    int M, N, K;
+    int M, K;
 };
 
-// W[j][k] as f32 (the classification of non-finite rows)
+// W[j][k] of weights W as f32 (the classification of non-finite rows)
 template <bool RM>
-__device__ __forceinline__ float fx_w(const FxParams &p, int j, int k) {
-    if constexpr (RM) return (float)p.W[(size_t)j * p.ldw + k];
+__device__ __forceinline__ float fx_w(const int8_t *W, int ldw, int K, int j, int k) {
+    if constexpr (RM) return (float)W[(size_t)j * ldw + k];
     const int o = k & 63, g = (o & 31) >> 3;
-    const size_t blk = (size_t)(j >> 4) * (p.K >> 6) + (k >> 6);
-    return (float)p.W[blk * 1024 + (size_t)(16 * g + (j & 15)) * 16 + (o >> 5) * 8 + (o & 7)];
+    const size_t blk = (size_t)(j >> 4) * (K >> 6) + (k >> 6);
+    return (float)W[blk * 1024 + (size_t)(16 * g + (j & 15)) * 16 + (o >> 5) * 8 + (o & 7)];
 }
 
 // Row m . weight row j when row m holds a NaN or an infinity: NaN if a
 // product x * w is NaN or both infinities occur, else the infinity that
 // occurs; v (the q8 value) if no product is non-finite.
 template <bool RM>
-__device__ float fx_nonfinite(const FxParams &p, int m, int j, float v) {
+__device__ float fx_nonfinite(const FxParams &p, const int8_t *W, int m, int j, float v) {
     const float *x = p.X + (size_t)m * p.ldx;
     bool nan = false, pos = false, neg = false;
     for (int k = 0; k < p.K; ++k) {
-        const float t = x[k] * fx_w<RM>(p, j, k);
+        const float t = x[k] * fx_w<RM>(W, p.ldw, p.K, j, k);
         nan = nan || t != t;
         pos = pos || t == __builtin_inff();
         neg = neg || t == -__builtin_inff();
     }
     if (nan || (pos && neg)) return __builtin_nanf("");
     return pos ? __builtin_inff() : neg ? -__builtin_inff() : v;
+}
+
+// The segment and the tile within it of this workgroup's tile t (uniform).
+__device__ __forceinline__ void fx_tile(const FxParams &p, int tw, int t, int &s, int &lt) {
+    if (p.pair) {
+        s = t;
+        lt = blockIdx.x;
+        return;
+    }
+    const int gt = blockIdx.x * tw + t;
+    s = p.nseg > 2 && gt >= p.tstart[2] ? 2 : p.nseg > 1 && gt >= p.tstart[1] ? 1 : 0;
+    lt = gt - p.tstart[s];
 }
 
 template <int KB, int NW, int TW, bool RM>
@@ -90,8 +117,6 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     const int g = lane >> 4, n = lane & 15;
     const int nkb = p.K >> 6;
     const int kb0 = wave * KB;
-    const int ntile = (p.N + 15) >> 4;
-    const int tile0 = blockIdx.x * TW;
     const int M = p.M;
 
     // 1. every global read up front: the run of each input row (piece
@@ -113,25 +138,33 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     u32x4 wr[TW][KB];
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
-        const int tl = tile0 + t < ntile ? tile0 + t : ntile - 1;
+        int sg, lt;
+        fx_tile(p, TW, t, sg, lt);
+        const FxSeg &S = p.seg[sg];
+        const int ntile = (S.N + 15) >> 4;
+        const int tl = lt < ntile ? lt : ntile - 1;
         if constexpr (RM) {
-            const int row = tl * 16 + n < p.N ? tl * 16 + n : p.N - 1;
-            const int8_t *wt = p.W + (size_t)row * p.ldw + (size_t)kb0 * 64 + 16 * g;
+            const int row = tl * 16 + n < S.N ? tl * 16 + n : S.N - 1;
+            const int8_t *wt = S.W + (size_t)row * p.ldw + (size_t)kb0 * 64 + 16 * g;
 #pragma unroll
             for (int i = 0; i < KB; ++i)
                 wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + 64 * i));
         } else {
-            const int8_t *wt = p.W + ((size_t)tl * nkb + kb0) * 1024 + lane * 16;
+            const int8_t *wt = S.W + ((size_t)tl * nkb + kb0) * 1024 + lane * 16;
 #pragma unroll
             for (int i = 0; i < KB; ++i)
                 wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
         }
     }
-    // the scale of the thread's first epilogue output (row e0 % 16 of tile
-    // e0 / (16 M), e0 = tid)
-    const int e0 = tid < TW * 16 * M ? tid : 0;
-    const int row0 = (tile0 + e0 / (16 * M)) * 16 + (e0 & 15);
-    const float sc0 = p.scale[row0 < p.N ? row0 : p.N - 1];
+    // the scales of the thread's first epilogue output (row e0 % 16 of tile
+    // e0 / (16 M), e0 = tid; with `pair`, of both tiles)
+    const int nout = (p.pair ? 16 : TW * 16) * M;
+    const int e0 = tid < nout ? tid : 0;
+    int sg0, lt0;
+    fx_tile(p, TW, e0 / (16 * M), sg0, lt0);
+    const int row0 = lt0 * 16 + (e0 & 15);
+    const float sc0 = p.seg[sg0].scale[row0 < p.seg[sg0].N ? row0 : p.seg[sg0].N - 1];
+    const float sc1 = p.pair ? p.seg[1].scale[row0 < p.seg[1].N ? row0 : p.seg[1].N - 1] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. each row's run as int8 terms with the factor of its own maximum,
@@ -214,22 +247,32 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
 
     // 4. the waves' partial tiles summed in wave order, scaled and stored:
     // consecutive threads take consecutive rows of one input row
-    for (int e = tid; e < TW * 16 * M; e += NW * 64) {
-        const int t = e / (16 * M), m = (e >> 4) % M, r = e & 15;
-        const int row = (tile0 + t) * 16 + r;
-        if (row < p.N) {
-            float s = red[t][0][r][m];
+    auto tile_out = [&](int t, int m, int r, int row, const FxSeg &S, float scl) {
+        float v = red[t][0][r][m];
 #pragma unroll
-            for (int w = 1; w < NW; ++w) s += red[t][w][r][m];
-            if (s != s) s = fx_nonfinite<RM>(p, m, row, s);
-            p.C[(size_t)m * p.ldc + row] = s * (e == tid ? sc0 : p.scale[row]);
+        for (int w = 1; w < NW; ++w) v += red[t][w][r][m];
+        if (v != v) v = fx_nonfinite<RM>(p, S.W, m, row, v);
+        v = v * scl;
+        S.C[(size_t)m * S.ldc + row] = v;
+        return v;
+    };
+    for (int e = tid; e < nout; e += NW * 64) {
+        const int t = e / (16 * M), m = (e >> 4) % M, r = e & 15;
+        int sg, lt;
+        fx_tile(p, TW, t, sg, lt);
+        const FxSeg &S = p.seg[sg];
+        const int row = lt * 16 + r;
+        if (row >= S.N) continue;
+        const float v = tile_out(t, m, r, row, S, e == tid ? sc0 : S.scale[row]);
+        if (p.pair) {  // t == 0: the gate; the up value of the same output
+            const float u = tile_out(1, m, r, row, p.seg[1], e == tid ? sc1 : p.seg[1].scale[row]);
+            p.act[(size_t)m * p.ldact + row] = act_scalar(v, VMLM_ACT_SILU) * u;
         }
     }
 }
 
 template <int KB, int NW, int TW, bool RM>
-int launch_fx_t(const FxParams &p, hipStream_t st) {
-    const unsigned grid = (unsigned)((p.N + 16 * TW - 1) / (16 * TW));
+int launch_fx_t(const FxParams &p, unsigned grid, hipStream_t st) {
     fx_gemv_kernel<KB, NW, TW, RM><<<grid, NW * 64, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
@@ -258,43 +301,88 @@ int fx_run_blocks(int K) {
     return 0;
 }
 
+// Checks shared by both entry points: the run split of K, the input rows.
+static int fx_check(int M, int K, int kb, int nw, const float *X, int ldx) {
+    VMLM_GUARD(M >= 1 && M <= FX_ROWS && kb && K == 64 * kb * nw,
+               "q8 GEMV: shape M=%d K=%d (M <= %d, K / 64 = waves x blocks)", M, K, FX_ROWS);
+    VMLM_GUARD(X && ((uintptr_t)X & 15) == 0 && ldx % 4 == 0 && ldx >= K,
+               "q8 GEMV: 16-byte aligned input rows");
+    return VMLM_OK;
+}
+static int fx_seg_check(const FxSeg &S, bool swizzled, int ldw, int K) {
+    VMLM_GUARD(S.W && S.scale && S.C && S.N >= 1 && S.ldc >= S.N && ((uintptr_t)S.W & 15) == 0 &&
+                   (swizzled ? S.N % 16 == 0 : ldw % 16 == 0 && ldw >= K),
+               "q8 GEMV: weights, scales and outputs (16-byte aligned rows)");
+    return VMLM_OK;
+}
+
+static int fx_dispatch(const FxParams &p, int kb, int nw, int tw, bool swizzled, unsigned grid,
+                       hipStream_t st) {
+#define FX_LAUNCH(KBV, NWV)                                                    \
+    if (kb == KBV && nw == NWV) {                                              \
+        if (swizzled)                                                          \
+            return tw == 2 ? launch_fx_t<KBV, NWV, 2, false>(p, grid, st)      \
+                           : launch_fx_t<KBV, NWV, 1, false>(p, grid, st);     \
+        return tw == 2 ? launch_fx_t<KBV, NWV, 2, true>(p, grid, st)           \
+                       : launch_fx_t<KBV, NWV, 1, true>(p, grid, st);          \
+    }
+    FX_SHAPES(FX_LAUNCH)
+#undef FX_LAUNCH
+    return fail(VMLM_ERR_UNIMPL, "q8 GEMV: no kernel for K=%d (%d waves of %d blocks)", p.K, nw,
+                kb);
+}
+
 int launch_fx_gemv(const FxArgs &a, hipStream_t st) {
     const int kb = a.kb ? a.kb : fx_run_blocks(a.K);
     const int nw = kb ? a.K / 64 / kb : 0;
     // two tiles per workgroup for wide outputs (fewer, longer workgroups),
     // one where the run is long (15 waves of 6 blocks: registers)
     const int tw = a.tw ? a.tw : a.N >= 4096 && kb <= 4 ? 2 : 1;
-    VMLM_GUARD(a.M >= 1 && a.M <= FX_ROWS && a.N >= 1 && kb && a.K == 64 * kb * nw &&
-                   (tw == 1 || tw == 2),
-               "q8 GEMV: shape M=%d N=%d K=%d (M <= %d, K / 64 = waves x blocks), %d tiles", a.M,
-               a.N, a.K, FX_ROWS, tw);
-    VMLM_GUARD(a.W && a.scale && a.X && a.C && ((uintptr_t)a.X & 15) == 0 && a.ldx % 4 == 0 &&
-                   a.ldx >= a.K && a.ldc >= a.N && ((uintptr_t)a.W & 15) == 0 &&
-                   (a.swizzled ? a.N % 16 == 0 : a.ldw % 16 == 0 && a.ldw >= a.K),
-               "q8 GEMV: operands (16-byte aligned rows)");
-    FxParams p;
-    p.W = (const int8_t *)a.W;
+    int rc = fx_check(a.M, a.K, kb, nw, a.X, a.ldx);
+    if (rc) return rc;
+    VMLM_GUARD(tw == 1 || tw == 2, "q8 GEMV: %d tiles per workgroup", tw);
+    FxParams p{};
+    p.seg[0] = FxSeg{(const int8_t *)a.W, a.scale, a.C, a.N, a.ldc};
+    if ((rc = fx_seg_check(p.seg[0], a.swizzled, a.ldw, a.K))) return rc;
+    p.nseg = 1;
     p.ldw = a.ldw;
-    p.scale = a.scale;
     p.X = a.X;
     p.ldx = a.ldx;
-    p.C = a.C;
-    p.ldc = a.ldc;
     p.M = a.M;
-    p.N = a.N;
     p.K = a.K;
-#define FX_LAUNCH(KBV, NWV)                                                    \
-    if (kb == KBV && nw == NWV) {                                              \
-        if (a.swizzled)                                                        \
-            return tw == 2 ? launch_fx_t<KBV, NWV, 2, false>(p, st)            \
-                           : launch_fx_t<KBV, NWV, 1, false>(p, st);           \
-        return tw == 2 ? launch_fx_t<KBV, NWV, 2, true>(p, st)                 \
-                       : launch_fx_t<KBV, NWV, 1, true>(p, st);                \
+    return fx_dispatch(p, kb, nw, tw, a.swizzled,
+                       (unsigned)((a.N + 16 * tw - 1) / (16 * tw)), st);
+}
+
+int launch_fx_multi(const FxMultiArgs &a, hipStream_t st) {
+    const int kb = fx_run_blocks(a.K);
+    const int nw = kb ? a.K / 64 / kb : 0;
+    int rc = fx_check(a.M, a.K, kb, nw, a.X, a.ldx);
+    if (rc) return rc;
+    const bool pair = a.act != nullptr;
+    VMLM_GUARD(a.nseg >= 1 && a.nseg <= 3 && (!pair || (a.nseg == 2 && a.seg[0].N == a.seg[1].N &&
+                                                        a.ldact >= a.seg[0].N)),
+               "q8 GEMV: 1..3 segments; a gate/up pair has two of one width");
+    FxParams p{};
+    int tiles = 0;
+    for (int i = 0; i < a.nseg; ++i) {
+        p.seg[i] = FxSeg{(const int8_t *)a.seg[i].W, a.seg[i].scale, a.seg[i].C, a.seg[i].N,
+                         a.seg[i].ldc};
+        if ((rc = fx_seg_check(p.seg[i], a.swizzled, a.ldw, a.K))) return rc;
+        p.tstart[i] = tiles;
+        tiles += (a.seg[i].N + 15) / 16;
     }
-    FX_SHAPES(FX_LAUNCH)
-#undef FX_LAUNCH
-    return fail(VMLM_ERR_UNIMPL, "q8 GEMV: no kernel for K=%d (%d waves of %d blocks)", a.K, nw,
-                kb);
+    p.nseg = a.nseg;
+    p.pair = pair;
+    p.act = a.act;
+    p.ldact = a.ldact;
+    p.ldw = a.ldw;
+    p.X = a.X;
+    p.ldx = a.ldx;
+    p.M = a.M;
+    p.K = a.K;
+    const unsigned grid = (unsigned)(pair ? (a.seg[0].N + 15) / 16 : tiles);
+    return fx_dispatch(p, kb, nw, pair ? 2 : 1, a.swizzled, grid, st);
 }
 
 }  // namespace vmlm

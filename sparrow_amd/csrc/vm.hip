@@ -610,9 +610,10 @@ struct VmSlot {
 
 // A run of the decode loop's per-head opcodes that the executor launches as
 // one kernel (vm_kv_append_kernel, vm_head_attn_kernel).
-enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2 };
+enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4 };
 struct VmFused {
     int kind = 0;
+    uint32_t start = 0;      // first instruction of the run
     uint32_t len = 0;        // instructions replaced
     uint32_t nh = 0, hd = 0, cols = 0;
     uint32_t k = 0, v = 0;   // KV_APPEND: the k and v rows; HEAD_ATTN: q in k
@@ -731,11 +732,12 @@ static int vm_detect_fusions(vmlm_vm *vm) {
     };
     constexpr uint8_t RT = VFL_RUNTIME;
     std::vector<float *> tab;
-    for (size_t i = 0; i + 7 <= n;) {
+    for (size_t i = 0; i < n;) {
         const VmIns &h0 = T[i];
         VmFused f;
         std::vector<uint32_t> caches;
-        if (h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_SLICE &&
+        const bool seven = i + 7 <= n;  // room for one head's run
+        if (seven && h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_SLICE &&
             T[i + 2].op == VOP_ROPE) {  // cache append
             const uint32_t kdh = h0.dst, kd = h0.a, vdh = T[i + 1].dst, vd = T[i + 1].a;
             const uint32_t kdrot = T[i + 2].dst, th = T[i + 2].b, pos = T[i + 2].dt;
@@ -803,7 +805,7 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                     caches.insert(caches.end(), vc.begin(), vc.end());
                 }
             }
-        } else if (h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_ROPE &&
+        } else if (seven && h0.op == VOP_SLICE && h0.fl == 0 && h0.b == 0 && T[i + 1].op == VOP_ROPE &&
                    T[i + 2].op == VOP_GEMM) {  // attention per head
             const uint32_t qdh = h0.dst, qd = h0.a, qdrot = T[i + 1].dst, th = T[i + 1].b,
                            pos = T[i + 1].dt, scd = T[i + 2].dst, sc = T[i + 3].b,
@@ -867,10 +869,69 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                 }
             }
         }
+        // int8 GEMMs of one input at decode rows: two or three in a row (q/k/v),
+        // or gate, up, ACT silu of gate, EWMUL by up
+        auto q8_gemm = [&](const VmIns &x, uint32_t A) {
+            if (!(x.op == VOP_GEMM && x.fl == 0 && x.a == A && ok(x.b) && ok(x.dst) && ok(x.dt)))
+                return false;
+            const VmSlot &B = vm->slots[x.b];
+            const size_t m = rows(A), k = cols(A), nn = B.rows;
+            return B.dtype == VDT_I8 && B.cols == k && nn >= 1 && f32(x.dt) &&
+                   rows(x.dt) * cols(x.dt) >= nn && data(x.dst) &&
+                   rows(x.dst) * cols(x.dst) >= m * nn;
+        };
+        if (!f.kind && h0.op == VOP_GEMM && h0.fl == 0 && f32(h0.a) && rows(h0.a) >= 1 &&
+            rows(h0.a) <= (size_t)FX_ROWS && cols(h0.a) % 128 == 0 &&
+            fx_run_blocks((int)cols(h0.a)) && q8_gemm(h0, h0.a)) {
+            const uint32_t A = h0.a;
+            const size_t M = rows(A);
+            size_t j = 1;
+            while (j < 3 && i + j < n && !target[i + j] && q8_gemm(T[i + j], A)) ++j;
+            std::vector<uint32_t> dsts;
+            for (size_t t = 0; t < j; ++t) dsts.push_back(T[i + t].dst);
+            std::vector<uint32_t> reads = {A};
+            for (size_t t = 0; t < j; ++t) {
+                reads.push_back(T[i + t].b);
+                reads.push_back(T[i + t].dt);
+            }
+            const VmIns *g = &T[i];
+            const uint32_t gd = g[0].dst, ud = j >= 2 ? g[1].dst : 0;
+            const size_t N = vm->slots[g[0].b].rows;
+            const bool gate_up =
+                j >= 2 && i + 4 <= n && !target[i + 2] && !target[i + 3] &&
+                vm->slots[g[1].b].rows == N && g[2].op == VOP_ACT && g[2].fl == VMLM_ACT_SILU &&
+                g[2].a == gd && g[3].op == VOP_EWMUL && g[3].a == g[2].dst && g[3].b == ud &&
+                g[3].dst == g[2].dst && data(g[2].dst) && rows(g[2].dst) == M &&
+                cols(g[2].dst) == N && rows(gd) == M && cols(gd) == N && rows(ud) == M &&
+                cols(ud) == N;
+            if (gate_up) {
+                std::vector<uint32_t> w = {gd, ud, g[2].dst};
+                std::vector<uint32_t> r2 = {A, g[0].b, g[0].dt, g[1].b, g[1].dt};
+                if (disjoint(w, r2)) {
+                    f.kind = VF_GATE_UP;
+                    f.len = 4;
+                    f.nh = 2;
+                    f.att = g[2].dst;  // act
+                }
+            }
+            if (!f.kind && j >= 2 && disjoint(dsts, reads)) {
+                f.kind = VF_GEMMS;
+                f.len = (uint32_t)j;
+                f.nh = (uint32_t)j;
+            }
+        }
+        if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP) {  // no cache table
+            f.start = (uint32_t)i;
+            vm->fused.push_back(f);
+            vm->fuse_at[i] = (int32_t)vm->fused.size() - 1;
+            i += f.len;
+            continue;
+        }
         if (!f.kind) {
             ++i;
             continue;
         }
+        f.start = (uint32_t)i;
         // the cache addresses (activation and state slots do not move)
         std::vector<float *> addr;
         for (uint32_t c : caches) {
@@ -1152,6 +1213,7 @@ struct Exec {
 
     int step(const VmIns &in, size_t *ip);
     int fused(const VmFused &f);
+    int fused_gemms(const VmFused &f);
 };
 
 #define P_(name, slot)                 \
@@ -1597,10 +1659,65 @@ extern "C" {
 
 // The slot an instruction writes: `dst`, or `a` for LOOP_CNT (its counter)
 // and STACK_INIT; UINT32_MAX for instructions that write no slot.
+// A run of int8 GEMMs over one input at decode rows in one launch
+// (launch_fx_multi); each GEMM as OP_GEMM gives it, and with the gate/up
+// pair the ACT silu and EWMUL after it. The swizzled copies are looked up as
+// OP_GEMM does (through the layer base); a run whose GEMMs are not all
+// swizzled or all row-major runs opcode by opcode.
+int Exec::fused_gemms(const VmFused &f) {
+    int rc = VMLM_OK;
+    const VmIns *g = &vm->text[f.start];
+    const uint32_t A = g[0].a;
+    FxMultiArgs x;
+    x.nseg = (int)f.nh;
+    x.M = (int)rows(A);
+    x.K = (int)cols(A);
+    x.ldx = x.K;
+    x.ldw = x.K;
+    float *ca;
+    if ((rc = ptr(A, &ca))) return rc;
+    x.X = ca;
+    int nsw = 0;
+    for (int t = 0; t < x.nseg; ++t) {
+        float *cb, *cs, *cc;
+        if ((rc = ptr(g[t].b, &cb)) || (rc = ptr(g[t].dt, &cs)) || (rc = ptr(g[t].dst, &cc)))
+            return rc;
+        const size_t N = rows(g[t].b);
+        const auto it = vm->swz.find((size_t)((char *)cb - vm->pool->dev));
+        const bool sw = it != vm->swz.end() && it->second.rows == N && it->second.cols == cols(g[t].b);
+        nsw += sw;
+        x.seg[t].W = sw ? (const void *)it->second.dev : (const void *)cb;
+        x.seg[t].scale = cs;
+        x.seg[t].C = cc;
+        x.seg[t].N = (int)N;
+        x.seg[t].ldc = (int)N;
+    }
+    x.swizzled = nsw == x.nseg;
+    if (f.kind == VF_GATE_UP) {
+        float *act;
+        if ((rc = ptr(f.att, &act))) return rc;
+        x.act = act;
+        x.ldact = x.seg[0].N;
+    }
+    bool aligned = ((uintptr_t)ca & 15) == 0;
+    for (int t = 0; t < x.nseg; ++t) aligned = aligned && ((uintptr_t)x.seg[t].W & 15) == 0;
+    // mixed layouts, or operands OP_GEMM would not give this kernel: opcode
+    // by opcode
+    if ((nsw != 0 && nsw != x.nseg) || !aligned) {
+        for (uint32_t t = 0; t < f.len; ++t) {
+            size_t ip = f.start + t + 1;
+            if ((rc = step(g[t], &ip))) return rc;
+        }
+        return VMLM_OK;
+    }
+    return launch_fx_multi(x, vm->st);
+}
+
 // A run found by vm_detect_fusions, in one launch: the host-side guards of
 // its opcodes (ROPE's theta), then the kernel with the device-side ones.
 int Exec::fused(const VmFused &f) {
     int rc = VMLM_OK;
+    if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP) return fused_gemms(f);
     float theta;
     if ((rc = scalar(f.theta, &theta))) return rc;
     VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");

@@ -308,7 +308,8 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
     approx += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     approx += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     with gvm.Vm(img) as g:
-        assert g.fused_runs() == 2 * nl
+        # per layer: the cache append, the attention, q/k/v, gate/up
+        assert g.fused_runs() == 4 * nl
         g.write("st_tok", prompt)
         g.write("st_gen", [11])
         g.run()
@@ -328,7 +329,68 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
         rms = np.sqrt(np.mean(ol[s_].astype(np.float64) ** 2))
         assert np.abs(gl[s_] - ol[s_]).max() <= 1e-4 * rms, s_
     with gvm.Vm(programs.minicpm_program(cfg, W, S, G).build()) as g:
-        assert g.fused_runs() == 0
+        assert g.fused_runs() == 2 * nl * G  # q/k/v and gate/up of every step
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_vm_fused_gemm_runs(gvm, oracle, m):
+    """q/k/v-like GEMMs of one input, and gate, up, ACT silu, EWMUL, at
+    decode rows: one launch per run, the same bits as the same opcodes run
+    one by one (a SHAPE between them breaks the runs) and within 1e-4 RMS of
+    the oracle VM; a 100-row weight (row-major only) beside swizzled ones
+    runs opcode by opcode."""
+    rng = np.random.default_rng(70 + m)
+    k = 768
+
+    def prog(split, nq=96):
+        P = vmb.Program()
+        X = P.const("x", rng_x)
+        outs = []
+        for name, nrows in (("q", nq), ("k", 64), ("v", 64), ("gate", 128), ("up", 128)):
+            W = P.const(name, ws[name][:nrows], "i8")
+            S = P.const(name + "_sc", scs[name][:nrows], rows=nrows, cols=1)
+            P.act("y" + name, m, nrows)
+            outs.append(("y" + name, W, S))
+        P.act("a", m, 128)
+        for i, (y, W, S) in enumerate(outs):
+            P.ins("GEMM", P[y], X, W, dt=S)
+            if split:
+                P.ins("SHAPE", 0, 0, 0)
+        P.ins("ACT", P["a"], P["ygate"], fl=vmb.ACT["silu"])
+        if split:
+            P.ins("SHAPE", 0, 0, 0)
+        P.ins("EWMUL", P["a"], P["a"], P["yup"])
+        P.ins("HALT")
+        return P
+
+    rng_x = rng.standard_normal((m, k)).astype(np.float32)
+    ws = {n: rng.integers(-127, 128, size=(128, k), dtype=np.int8)
+          for n in ("q", "k", "v", "gate", "up")}
+    scs = {n: (np.abs(rng.normal(0, 0.02, 128)) / 127 + 1e-6).astype(np.float32) for n in ws}
+    names = ["yq", "yk", "yv", "ygate", "yup", "a"]
+    res = {}
+    for split in (False, True):
+        img = prog(split).build()
+        with gvm.Vm(img) as g:
+            assert g.fused_runs() == (0 if split else 2)
+            g.run()
+            res[split] = {r: g.read(r) for r in names}
+    with oracle.OracleVm(prog(False).build()) as o:
+        o.run()
+        ref = {r: o.read(r) for r in names}
+    for r in names:
+        assert np.array_equal(bits(res[False][r]), bits(res[True][r])), r
+        rms = np.sqrt(np.mean(ref[r].astype(np.float64) ** 2))
+        assert np.abs(res[False][r] - ref[r]).max() <= 1e-4 * rms, r
+    img = prog(False, nq=100).build()
+    with gvm.Vm(img) as g:
+        g.run()
+        y100 = g.read("yq")
+    with oracle.OracleVm(img) as o:
+        o.run()
+        r100 = o.read("yq")
+    rms = np.sqrt(np.mean(r100.astype(np.float64) ** 2))
+    assert np.abs(y100 - r100).max() <= 1e-4 * rms
 
 
 def test_vm_fused_runs_guard(gvm):
