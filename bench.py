@@ -755,7 +755,8 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
                 "then o, gate/up, ACT, EWMUL, down). The executor dispatches opcode by opcode, "
                 "except the runs it matched at load (fused_runs: per layer the cache append and "
                 "the attention over all heads, q/k/v, and gate/up with ACT and EWMUL, one launch "
-                "each); the rate is the difference of two programs' run times",
+                "each; per layer and head the prompt's column-by-column K/V cache writes, two "
+                "strided copies); the rate is the difference of two programs' run times",
     }
 
 

@@ -608,9 +608,14 @@ struct VmSlot {
     uint8_t dtype;
 };
 
-// A run of the decode loop's per-head opcodes that the executor launches as
-// one kernel (vm_kv_append_kernel, vm_head_attn_kernel).
-enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4 };
+// A run of opcodes that the executor launches as one kernel (per-head decode
+// runs: vm_kv_append_kernel, vm_head_attn_kernel; GEMMs of one input), or as
+// one strided copy per stream (VF_COL_RUN: column-by-column cache writes).
+enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4, VF_COL_RUN = 5 };
+struct VmColStream {
+    uint32_t c, x, y;   // the column slot, the slot sliced, the slot written
+    uint32_t xo, yo;    // first column read from x, first column written to y
+};
 struct VmFused {
     int kind = 0;
     uint32_t start = 0;      // first instruction of the run
@@ -620,6 +625,7 @@ struct VmFused {
     uint32_t theta = 0, pos = 0, live = 0, scale = 0, att = 0;
     uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;  // scratch slots, in opcode order
     float **tab = nullptr;   // device: the nh K cache addresses, then the nh V
+    VmColStream col[2];      // VF_COL_RUN: nh streams of `cols` steps
 };
 
 struct vmlm_vm {
@@ -722,12 +728,26 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                    uint16_t dt) {
         return x.op == op && x.fl == fl && x.dst == d && x.a == a && x.b == b && x.dt == dt;
     };
-    // written slots pairwise distinct and never read by the run
-    auto disjoint = [](std::vector<uint32_t> w, const std::vector<uint32_t> &r) {
-        std::sort(w.begin(), w.end());
-        if (std::adjacent_find(w.begin(), w.end()) != w.end()) return false;
-        for (uint32_t x : r)
-            if (std::binary_search(w.begin(), w.end(), x)) return false;
+    // written slots pairwise apart in memory and apart from every slot read
+    // by the run (byte ranges in their regions: an image may place two slots
+    // over the same arena bytes)
+    auto overlap = [&](uint32_t a, uint32_t b) {
+        if (a == b) return true;
+        const VmSlot &x = vm->slots[a], &y = vm->slots[b];
+        const bool cx = x.kind == VSLOT_CONST || x.kind == VSLOT_PARAM;
+        const bool cy = y.kind == VSLOT_CONST || y.kind == VSLOT_PARAM;
+        if (cx != cy || (!cx && x.kind != y.kind)) return false;
+        const size_t xe = x.off + (size_t)x.rows * x.cols * vdtype_size(x.dtype);
+        const size_t ye = y.off + (size_t)y.rows * y.cols * vdtype_size(y.dtype);
+        return x.off < ye && y.off < xe;
+    };
+    auto disjoint = [&](const std::vector<uint32_t> &w, const std::vector<uint32_t> &r) {
+        for (size_t a = 0; a < w.size(); ++a) {
+            for (size_t b = a + 1; b < w.size(); ++b)
+                if (overlap(w[a], w[b])) return false;
+            for (uint32_t x : r)
+                if (overlap(w[a], x)) return false;
+        }
         return true;
     };
     constexpr uint8_t RT = VFL_RUNTIME;
@@ -920,7 +940,57 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                 f.nh = (uint32_t)j;
             }
         }
-        if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP) {  // no cache table
+        // cache writes of a prompt, column by column (p12_build_minicpm.py:
+        // 794-840): P steps of SLICE c <- x at column xo + p, then WRITECOL
+        // y <- c at column yo + p, for one stream or two interleaved. The run
+        // writes columns yo .. yo + P - 1 of y from xo .. xo + P - 1 of x and
+        // leaves c holding column xo + P - 1, which two strided copies per
+        // stream reproduce.
+        auto col_pair = [&](size_t at) {
+            return at + 2 <= n && T[at].op == VOP_SLICE && T[at].fl == 0 &&
+                   T[at + 1].op == VOP_WRITECOL && T[at + 1].fl == 0 && T[at + 1].a == T[at].dst;
+        };
+        if (!f.kind && col_pair(i)) {
+            const int Q = col_pair(i + 2) && T[i + 2].dst != h0.dst ? 2 : 1;
+            size_t P = 0;
+            for (;; ++P) {
+                const size_t at = i + 2 * Q * P;
+                bool okp = at + 2 * Q <= n;
+                for (int q = 0; okp && q < Q; ++q) {
+                    const VmIns &s0 = T[i + 2 * q], &w0 = T[i + 2 * q + 1];
+                    const VmIns &sp = T[at + 2 * q], &wp = T[at + 2 * q + 1];
+                    okp = col_pair(at + 2 * q) && sp.dst == s0.dst && sp.a == s0.a &&
+                          (uint64_t)sp.b == (uint64_t)s0.b + P && wp.dst == w0.dst &&
+                          (uint64_t)wp.b == (uint64_t)w0.b + P;
+                }
+                for (size_t t = 0; okp && t < (size_t)(2 * Q); ++t)
+                    okp = (P == 0 && t == 0) || !target[at + t];  // no jump into the run
+                if (!okp) break;
+            }
+            bool good = P >= 2;
+            std::vector<uint32_t> w, r;
+            for (int q = 0; good && q < Q; ++q) {
+                const VmIns &s0 = T[i + 2 * q], &w0 = T[i + 2 * q + 1];
+                const uint32_t c = s0.dst, x = s0.a, y = w0.dst;
+                // the guards of SLICE and WRITECOL, at the run's last column
+                good = ok(c) && ok(x) && ok(y) && data(c) && data(y) && f32(x) && cols(c) == 1 &&
+                       rows(c) >= 1 && rows(c) >= rows(y) &&
+                       (rows(c) - 1) * cols(x) + s0.b + P <= rows(x) * cols(x) &&
+                       (size_t)w0.b + P <= cols(y);
+                if (!good) break;
+                f.col[q] = VmColStream{c, x, y, s0.b, w0.b};
+                w.push_back(c);
+                w.push_back(y);
+                r.push_back(x);
+            }
+            if (good && disjoint(w, r)) {
+                f.kind = VF_COL_RUN;
+                f.len = (uint32_t)(2 * Q * P);
+                f.nh = (uint32_t)Q;
+                f.cols = (uint32_t)P;
+            }
+        }
+        if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP || f.kind == VF_COL_RUN) {  // no cache table
             f.start = (uint32_t)i;
             vm->fused.push_back(f);
             vm->fuse_at[i] = (int32_t)vm->fused.size() - 1;
@@ -1718,6 +1788,18 @@ int Exec::fused_gemms(const VmFused &f) {
 int Exec::fused(const VmFused &f) {
     int rc = VMLM_OK;
     if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP) return fused_gemms(f);
+    if (f.kind == VF_COL_RUN) {
+        for (uint32_t q = 0; q < f.nh; ++q) {
+            const VmColStream &c = f.col[q];
+            float *pc, *px, *py;
+            if ((rc = ptr(c.c, &pc)) || (rc = ptr(c.x, &px)) || (rc = ptr(c.y, &py))) return rc;
+            const size_t xc = cols(c.x);
+            if ((rc = copy2d(py, cols(c.y), c.yo, px, xc, c.xo, rows(c.y), f.cols)) ||
+                (rc = copy2d(pc, 1, 0, px, xc, (size_t)c.xo + f.cols - 1, rows(c.c), 1)))
+                return rc;
+        }
+        return VMLM_OK;
+    }
     float theta;
     if ((rc = scalar(f.theta, &theta))) return rc;
     VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");

@@ -308,8 +308,9 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
     approx += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     approx += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     with gvm.Vm(img) as g:
-        # per layer: the cache append, the attention, q/k/v, gate/up
-        assert g.fused_runs() == 4 * nl
+        # per layer: the cache append, the attention, q/k/v, gate/up, and
+        # the prompt's column-by-column cache writes of every head
+        assert g.fused_runs() == 4 * nl + nl * nh
         g.write("st_tok", prompt)
         g.write("st_gen", [11])
         g.run()
@@ -329,7 +330,8 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
         rms = np.sqrt(np.mean(ol[s_].astype(np.float64) ** 2))
         assert np.abs(gl[s_] - ol[s_]).max() <= 1e-4 * rms, s_
     with gvm.Vm(programs.minicpm_program(cfg, W, S, G).build()) as g:
-        assert g.fused_runs() == 2 * nl * G  # q/k/v and gate/up of every step
+        # q/k/v and gate/up of every step, the prompt's cache writes per head
+        assert g.fused_runs() == 2 * nl * G + nl * nh
 
 
 @pytest.mark.parametrize("m", [1, 3])
@@ -455,6 +457,51 @@ def test_vm_fused_runs_guard(gvm):
     for pos, live in ((C, 3), (2, C + 1)):
         c, m = codes(gvm, prog(pos, live))
         assert c == 9 and "guard" in m, m
+
+
+@pytest.mark.parametrize("Q", [1, 2])
+def test_vm_col_runs(gvm, oracle, Q):
+    """Column-by-column writes (SLICE a column of x, WRITECOL it into y; one
+    stream or two interleaved, as the decoder program caches its prompt's K
+    and V) run as two strided copies per stream: y and the column slot equal
+    the oracle VM bitwise. With a jump into the run, the part before the jump
+    target runs opcode by opcode and the rest as a run, with the same result.
+    A run whose last WRITECOL would pass y's width runs opcode by opcode and
+    trips the same guard (status 9)."""
+    rng = np.random.default_rng(4 + Q)
+    R, S, Wd = 5, 7, 9
+
+    def prog(yo=1, jump=False):
+        P = vmb.Program()
+        xs = [P.const(f"x{q}", rng.standard_normal((R, S)).astype(np.float32)) for q in range(Q)]
+        for q in range(Q):
+            P.act(f"c{q}", R, 1)
+            P.state(f"y{q}", R, Wd)
+        if jump:
+            P.ins("JMP", 1 + 2 * Q)  # into the second column's pairs
+        for p in range(S):
+            for q in range(Q):
+                P.ins("SLICE", P[f"c{q}"], xs[q], p)
+                P.ins("WRITECOL", P[f"y{q}"], P[f"c{q}"], yo + p)
+        P.ins("HALT")
+        return P
+
+    names = [f"{k}{q}" for q in range(Q) for k in ("c", "y")]
+    for jump, runs in ((False, 1), (True, 1)):
+        img = prog(jump=jump).build()
+        with gvm.Vm(img) as g:
+            assert g.fused_runs() == runs
+            g.run()
+            got = {r: g.read(r) for r in names}
+        with oracle.OracleVm(img) as o:
+            o.run()
+            ref = {r: o.read(r) for r in names}
+        for r in names:
+            assert np.array_equal(bits(got[r]), bits(ref[r])), (jump, r)
+    with gvm.Vm(prog(yo=Wd - S + 1).build()) as g:
+        assert g.fused_runs() == 0
+    c, m = codes(gvm, prog(yo=Wd - S + 1))
+    assert c == 9 and "WRITECOL" in m, m
 
 
 def test_vm_shared_const_pool(gvm, tiny):
