@@ -73,6 +73,16 @@ __device__ __forceinline__ void dma16(const void *gptr, uint32_t lds_base) {
                  : "v"(gptr), "s"(lds_base)
                  : "memory", "m0");
 }
+
+// The same copy with a wave-uniform base held in SGPRs (sbase) and a 32-bit
+// per-lane byte offset: one VGPR per distinct offset instead of a 64-bit
+// address per copy.
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -269,9 +279,11 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmParams p) {
 // (q8_term_weight), times the row factor and the column scale. No int8 ->
 // bf16 conversion, and Q8_T MFMAs of 8 passes per k-step against six for
 // three bf16 terms.
-template <int BM, int BN, int NS, bool WB, int OCC = 2>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_dma_i8_kernel(GemmParams p) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, int NS, bool WB, int OCC = 2, int WMW = 2, int WNW = 2>
+__global__ __launch_bounds__(64 * WMW * WNW) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_dma_i8_kernel(GemmParams p) {
+    // WMW x WNW waves, each owning a WM x WN sub-tile
+    constexpr int NW = WMW * WNW;
+    constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int ROW = 64;  // bytes of a row-major W row in LDS (64 k of int8)
     constexpr int ABLK = Q8_T * BM / 16;  // 1 KiB blocks of A per k-step
@@ -279,19 +291,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     constexpr int A_BYTES = ABLK * 1024, B_BYTES = BN * ROW;
     constexpr int STAGE = A_BYTES + B_BYTES;
     constexpr int C_LD = WN + 4;
-    constexpr int C_BYTES = 4 * 16 * C_LD * 4;
+    constexpr int C_BYTES = NW * 16 * C_LD * 4;
     constexpr int SMEM = NS * STAGE > C_BYTES ? NS * STAGE : C_BYTES;
-    // copy instructions per wave and step: W blocks q * 4 + wave < BBLK (with
-    // BN = 96 waves 0-1 copy two, waves 2-3 one, which the vmcnt wait of two
-    // stages (wait for all) allows)
-    constexpr int A_INS = ABLK / 4, B_INS = (BBLK + 3) / 4;
-    static_assert(ABLK % 4 == 0 && BN % 16 == 0, "copy instructions per wave");
-    static_assert(BBLK % 4 == 0 || NS == 2, "uneven W copies need the two-stage wait");
+    // copy instructions per wave and step: the step's ABLK + BBLK blocks
+    // (A first, then W; block b at stage byte 1024 b) dealt round-robin to
+    // the waves, block q * NW + wave to this wave. An uneven deal (64 x 96:
+    // 5, 5, 4, 4) needs the two-stage wait (wait for all).
+    constexpr int NBLK = ABLK + BBLK, INS = (NBLK + NW - 1) / NW;
+    static_assert(WM % 16 == 0 && WN % 16 == 0 && BN % 16 == 0, "16 x 16 MFMA tiles");
+    static_assert(NBLK % NW == 0 || NS == 2, "uneven copies need the two-stage wait");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
     const int g = lane >> 4, r = lane & 15;
     int tbx, tby;
     gemm_tile(p.group, tbx, tby);
@@ -305,27 +318,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     // of this tile (the planes are p.tstride bytes apart, row tiles nkt KiB);
     // W blocks of the swizzled copy, or 16 rows x 64 B of row-major W per
     // instruction with lane i bringing piece (i & 3) ^ ((R >> 1) & 3) of row
-    // R = 16 * instr + i / 4
-    const uint8_t *a_src[A_INS];
-    const uint8_t *b_src[B_INS];
+    // R = 16 * instr + i / 4. Copy q reads base[q] (wave-uniform, advancing
+    // kstr[q] bytes per k-step) plus the lane's offset voff[q]: 16 * lane for
+    // whole blocks, the row and piece within the tile for row-major W.
+    const uint8_t *base[INS];
+    uint32_t voff[INS];
+    int kstr[INS];
 #pragma unroll
-    for (int q = 0; q < A_INS; ++q) {
-        const int blk = q * 4 + wave, t = blk / (BM / 16), i = blk % (BM / 16);
-        a_src[q] = (const uint8_t *)p.A8 + t * p.tstride +
-                   ((size_t)(m0 / 16 + i) * nkt) * 1024 + lane * 16;
-    }
-#pragma unroll
-    for (int q = 0; q < B_INS; ++q) {
-        if constexpr (WB) {
-            int tn = n0 / 16 + (q * 4 + wave < BBLK ? q * 4 + wave : BBLK - 1);
+    for (int q = 0; q < INS; ++q) {
+        const int blk0 = q * NW + wave, blk = blk0 < NBLK ? blk0 : NBLK - 1;
+        voff[q] = (uint32_t)lane * 16;
+        kstr[q] = 1024;
+        if (blk < ABLK) {
+            const int t = blk / (BM / 16), i = blk % (BM / 16);
+            base[q] = (const uint8_t *)p.A8 + t * p.tstride + ((size_t)(m0 / 16 + i) * nkt) * 1024;
+        } else if constexpr (WB) {
+            int tn = n0 / 16 + (blk - ABLK);
             tn = tn < p.N / 16 ? tn : p.N / 16 - 1;
-            b_src[q] = p.W + ((size_t)tn * nkt) * 1024 + lane * 16;
+            base[q] = p.W + ((size_t)tn * nkt) * 1024;
         } else {
-            const int R = (q * 4 + wave < BBLK ? q * 4 + wave : BBLK - 1) * 16 + (lane >> 2);
+            const int R = (blk - ABLK) * 16 + (lane >> 2);
             const int c = (lane & 3) ^ ((R >> 1) & 3);
             int gn = n0 + R;
             gn = gn < p.N ? gn : p.N - 1;
-            b_src[q] = p.W + (size_t)gn * p.K + c * 16;
+            base[q] = p.W + (size_t)n0 * p.K;
+            voff[q] = (uint32_t)((gn - n0) * p.K + c * 16);  // < BN * K (launch_gemm bounds K)
+            kstr[q] = ROW;
         }
     }
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
@@ -333,12 +351,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         const int kc = kb0 + (kt < nk ? kt : nk - 1);
         const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
 #pragma unroll
-        for (int q = 0; q < A_INS; ++q)
-            dma16(a_src[q] + (size_t)kc * 1024, sb + (q * 4 + wave) * 1024);
-#pragma unroll
-        for (int q = 0; q < B_INS; ++q)
-            if (BBLK % 4 == 0 || q * 4 + wave < BBLK)  // wave-uniform
-                dma16(b_src[q] + (size_t)kc * (WB ? 1024 : ROW), sb + A_BYTES + (q * 4 + wave) * 1024);
+        for (int q = 0; q < INS; ++q)
+            if (NBLK % NW == 0 || q * NW + wave < NBLK)  // wave-uniform
+                dma16s(base[q] + (size_t)kc * kstr[q], voff[q], sb + (q * NW + wave) * 1024);
     };
 
     gi32x4 acc[Q8_T][TM][TN];
@@ -379,7 +394,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s);
     for (int kt = 0; kt < nk; ++kt) {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * (A_INS + B_INS)));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * INS));
         __syncthreads();
         issue(kt + NS - 1);
         compute(smem + (kt % NS) * STAGE);
@@ -490,7 +505,7 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
     return bm == 128 ? launch_dma<WI8, T, 128, 128>(p, ns, st) : launch_dma<WI8, T, 64, 128>(p, ns, st);
 }
 
-template <int BM, int BN, int NS>
+template <int BM, int BN, int NS, int WMW = 2, int WNW = 2>
 static int launch_i8(const GemmParams &p, bool wb, int ksl, bool keep, hipStream_t st) {
     constexpr int stage = Q8_T * BM * 64 + BN * 64;
     static_assert(NS * stage <= DMA_LDS_MAX, "int8 gemm stages exceed the LDS");
@@ -499,14 +514,16 @@ static int launch_i8(const GemmParams &p, bool wb, int ksl, bool keep, hipStream
     // (128 VGPRs, the LDS holds four 40 KiB rings); 2 % faster than three at
     // the prefill's q/k/v and gate/up shapes, where 128 x 256 tiles of eight
     // waves (one workgroup per CU, two to four stages) measured 7 to 14 %
-    // slower than either; 64 x 64 tiles (five workgroups per CU) 20 to 60 %
-    // slower: below 64 x 128 the copy bytes per MFMA set the time
+    // slower than either, and 128 x 128 or 64 x 256 tiles of eight waves (two
+    // workgroups per CU, a quarter to a third fewer copy bytes per MFMA) 6 to
+    // 7 % slower over the whole batch-16 prefill; 64 x 64 tiles (five
+    // workgroups per CU) 20 to 60 % slower
     if (!wb)
-        gemm_dma_i8_kernel<BM, BN, NS, false><<<grid, 256, 0, st>>>(p);
+        gemm_dma_i8_kernel<BM, BN, NS, false, 2, WMW, WNW><<<grid, 64 * WMW * WNW, 0, st>>>(p);
     else if constexpr (NS == 2)
-        gemm_dma_i8_kernel<BM, BN, NS, true, 4><<<grid, 256, 0, st>>>(p);
+        gemm_dma_i8_kernel<BM, BN, NS, true, 4, WMW, WNW><<<grid, 64 * WMW * WNW, 0, st>>>(p);
     else
-        gemm_dma_i8_kernel<BM, BN, NS, true><<<grid, 256, 0, st>>>(p);
+        gemm_dma_i8_kernel<BM, BN, NS, true, 2, WMW, WNW><<<grid, 64 * WMW * WNW, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     if (ksl == 1 || keep) return VMLM_OK;
     return launch_gemv_reduce(p.part, ksl, p.M, p.N, p.scale, p.C, p.ldc, st);
@@ -581,6 +598,9 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
                        ((uintptr_t)a.A8 & 15) == 0 && (!a.w_blocked || a.N % 16 == 0),
                    "gemm (int8 rows): int8 weights, row factors, K %% 64 == 0, 16-byte aligned "
                    "operands, whole 16-row weight blocks");
+        // row-major weights: a lane's offset within a tile's rows is 32-bit
+        VMLM_GUARD(a.w_blocked || a.K <= (1 << 22), "gemm (int8 rows): K=%d above 2^22 needs "
+                   "blocked weights", a.K);
         VMLM_GUARD(!a.silu_pairs || (a.N % 32 == 0 && a.scale && a.ldc % 4 == 0 &&
                                      a.ldc >= a.N / 2 && ((uintptr_t)a.C & 15) == 0),
                    "gemm (int8 rows, SiLU pairs): N %% 32 == 0, column scales, 16-byte aligned "
