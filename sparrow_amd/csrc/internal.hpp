@@ -378,13 +378,19 @@ int launch_argmax(const float *src, size_t cols, float *dst_f, int32_t *dst_i,
 // v point into slice 0 of k-slices (qs.ks slices qs.pst floats apart) and
 // qs.scale holds the column scales of q's columns (k's and v's follow at
 // k - q and v - q).
+// Prompts of up to four 64-row blocks over a grid that fills the CUs
+// (attention_prefill_one_launch) run as one launch from the f32 rows; `rope_tab`, if given, holds the rotation's
+// (sin, cos) for positions pos0 + 0 .. S-1 and pair indices 0..31
+// (launch_rope_table), read instead of evaluating the angles.
 size_t attention_prefill_work_bytes(int S, int H, int nseq);
+bool attention_prefill_one_launch(int S, int H, int nseq);
+int launch_rope_table(float2 *tab, int S, float pos0, float rope_step, hipStream_t st);
 int launch_attention_prefill(const float *q, const float *k, const float *v, float *out, int S,
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope = false, float rope_step = 0.0f,
                              float pos0 = 0.0f, int nseq = 1, size_t sin = 0, size_t sout = 0,
                              float *kc = nullptr, float *vc = nullptr, int hs = 0,
-                             const Slices &qs = Slices{});
+                             const Slices &qs = Slices{}, const float2 *rope_tab = nullptr);
 struct DecodeArgs {
     const float *q, *k_new, *v_new;  // raw (unrotated) rows [B][ldq]
     int ldq;

@@ -398,6 +398,125 @@ __global__ __launch_bounds__(1024) void attn_qkv_prep_kernel(QKVPrepParams p) {
     }
 }
 
+// One key block of the prefill attention for the wave's 16 queries: S^T =
+// K Q^T over the block's 64 keys (two bf16 terms of K and of Q), the online
+// softmax update of (m, l, o), then O^T += V^T P^T (three terms of V, two of
+// P). Ks / Vt hold the block's terms in LDS; lane (g, r) owns query qa.
+__device__ __forceinline__ void prefill_block(const uint16_t (*Ks)[AT_B][AT_LD],
+                                              const uint16_t (*Vt)[64][AT_LD],
+                                              const u32x4 (&aq)[2][2], int k0, int qa, int S,
+                                              int causal, float scale, float &m, float &l,
+                                              f32x4 (&o)[4]) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+    // S^T: block j = keys 16j..16j+15; lane (g, r): keys 16j + 4g + i of
+    // query q0 + r. The four blocks' MFMA chains are interleaved.
+    f32x4 sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+        u32x4 b0[4], b1[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            b0[j] = *(const u32x4 *)&Ks[0][16 * j + r][sl * 32 + g * 8];
+            b1[j] = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][0], sc[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][0], sc[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][1], sc[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][1], sc[j]);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ka = k0 + 16 * j + 4 * g + i;
+            const bool valid = ka < S && (!causal || ka <= qa);
+            sc[j][i] = valid ? sc[j][i] * scale : -INFINITY;
+            mx = fmaxf(mx, sc[j][i]);
+        }
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
+    const float mn = fmaxf(m, mx);
+    const float alpha = m == -INFINITY ? 0.0f : __expf(m - mn);
+    float pv[4][4], rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pv[j][i] = sc[j][i] == -INFINITY ? 0.0f : __expf(sc[j][i] - mn);
+            rs += pv[j][i];
+        }
+    rs += lane_xor16(rs);
+    rs += lane_xor32(rs);
+    l = l * alpha + rs;
+    m = mn;
+#pragma unroll
+    for (int jd = 0; jd < 4; ++jd)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[jd][i] *= alpha;
+    // P^T fragments of the two 32-key steps: slots 8g..8g+7 hold keys
+    // 32 st + 4g + i and 32 st + 16 + 4g + i
+    u32x4 pb[2][2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        const float x[8] = {pv[2 * st][0],     pv[2 * st][1],     pv[2 * st][2],
+                            pv[2 * st][3],     pv[2 * st + 1][0], pv[2 * st + 1][1],
+                            pv[2 * st + 1][2], pv[2 * st + 1][3]};
+        split8(x, pb[st][0], pb[st][1]);
+    }
+    // O^T[d][q] += V^T[d][key] P^T[key][q]: A = V^T rows (dim 16 jd + r)
+    // at the same key slots; the four dim blocks' chains interleaved
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        u32x4 va[3][4];
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+            for (int jd = 0; jd < 4; ++jd) {
+                const uint16_t *row = &Vt[t][16 * jd + r][32 * st + 4 * g];
+                const uint2 lo = *(const uint2 *)row, hi = *(const uint2 *)(row + 16);
+                va[t][jd] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            }
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][0], o[jd]);
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][0], o[jd]);
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[2][jd], pb[st][0], o[jd]);
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][1], o[jd]);
+#pragma unroll
+        for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][1], o[jd]);
+    }
+}
+
+// lane (g, r): query qa, dims 16 jd + 4g .. +3
+__device__ __forceinline__ void prefill_store(const f32x4 (&o)[4], float l, int qa, int S,
+                                              float *O, size_t sout, int ldo, int o_vec, int h) {
+    const int g = (threadIdx.x & 63) >> 4;
+    if (qa >= S) return;
+    const float inv = 1.0f / l;
+    float *orow = O + blockIdx.z * sout + (size_t)qa * ldo + h * 64 + 4 * g;
+#pragma unroll
+    for (int jd = 0; jd < 4; ++jd) {
+        const float4 v = make_float4(o[jd][0] * inv, o[jd][1] * inv, o[jd][2] * inv, o[jd][3] * inv);
+        if (o_vec) {
+            *(float4 *)(orow + 16 * jd) = v;
+        } else {
+            orow[16 * jd] = v.x;
+            orow[16 * jd + 1] = v.y;
+            orow[16 * jd + 2] = v.z;
+            orow[16 * jd + 3] = v.w;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
@@ -448,7 +567,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
     const int qa = q0 + r;
     load_kv(kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
-        const int k0 = kb * AT_B;
         __syncthreads();  // the previous block's K / V are no longer read
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -463,112 +581,192 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillParams P) {
         __syncthreads();
         load_kv(kb + 1 < kb1 ? kb + 1 : kb);
         __builtin_amdgcn_sched_barrier(0);
+        prefill_block(Ks, Vt, aq, kb * AT_B, qa, S, causal, P.scale, m, l, o);
+    }
+    prefill_store(o, l, qa, S, P.O, P.sout, P.ldo, P.o_vec, h);
+}
 
-        // S^T: block j = keys 16j..16j+15; lane (g, r): keys 16j + 4g + i of
-        // query q0 + r. The four blocks' MFMA chains are interleaved.
-        f32x4 sc[4];
+// The same attention straight from the f32 Q, K and V rows (no term planes
+// in HBM and no second launch): each workgroup forms its queries' fragments
+// and, per key block, the block's K and V^T terms in LDS with the operations
+// of attn_qkv_prep_kernel (rotation, bf16 splits), so the scores, weights
+// and output are the two-kernel path's bits. The workgroup whose query block
+// is the key block (every key block has one) writes the block's rotated K
+// rows and raw V rows to the KV cache. K blocks are rotated by every query
+// block that reads them, so the launcher takes this form for up to four
+// query blocks (S <= 256).
+struct QKVPrefillParams {
+    const float *Q, *K, *V;  // rows of `ld` floats; sequence z at z * sin
+    float *O;
+    float *kc, *vc;          // KV cache [sequence][head][hs][64], or null
+    size_t sin, sout;
+    int S, ld, ldo, causal, nqb, H, hs, rope, o_vec;
+    float scale, rope_step, pos0;
+    const float2 *tab;       // (sin, cos) of [row][pair index], or null
+};
+
+// tab[row][i] = the (sin, cos) that rope_angle gives at position pos0 + row
+__global__ __launch_bounds__(256) void rope_table_kernel(float2 *tab, int S, float pos0, float step) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= S * 32) return;
+    float si, co;
+    rope_angle(pos0 + (float)(e >> 5), e & 31, step, &si, &co);
+    tab[e] = make_float2(si, co);
+}
+
+__global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillParams P) {
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
+    __shared__ float vs[AT_B][AT_B + 1];                                    // f32 V block
+    const int S = P.S, causal = P.causal;
+    const int h = blockIdx.y, z = blockIdx.z;
+    const int qb = causal ? P.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int kb1 = causal ? qb + 1 : P.nqb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r = lane & 15;
+    const int q0 = qb * AT_B + wave * 16;
+    const size_t base = (size_t)z * P.sin + h * 64;
+    // 4 values of row `row` from dim d
+    auto ld4 = [&](const float *b, int row, int d) {
+        return *(const float4 *)(b + base + (size_t)row * P.ld + d);
+    };
+    // RoPE of a row's dims d0 .. d0 + 7 (x1) with their partners d0 + 32 ..
+    // (x2) at position pos0 + row, the prep kernel's arithmetic
+    auto rotate = [&](float (&x1)[8], float (&x2)[8], int row, int d0) {
+        if (!P.rope) return;
+        const float fpos = P.pos0 + (float)row;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-            u32x4 b0[4], b1[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                b0[j] = *(const u32x4 *)&Ks[0][16 * j + r][sl * 32 + g * 8];
-                b1[j] = *(const u32x4 *)&Ks[1][16 * j + r][sl * 32 + g * 8];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][0], sc[j]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][0], sc[j]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b0[j], aq[sl][1], sc[j]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = mfma_b(b1[j], aq[sl][1], sc[j]);
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ka = k0 + 16 * j + 4 * g + i;
-                const bool valid = ka < S && (!causal || ka <= qa);
-                sc[j][i] = valid ? sc[j][i] * P.scale : -INFINITY;
-                mx = fmaxf(mx, sc[j][i]);
-            }
-        mx = fmaxf(mx, lane_xor16(mx));
-        mx = fmaxf(mx, lane_xor32(mx));
-        const float mn = fmaxf(m, mx);
-        const float alpha = m == -INFINITY ? 0.0f : __expf(m - mn);
-        float pv[4][4], rs = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pv[j][i] = sc[j][i] == -INFINITY ? 0.0f : __expf(sc[j][i] - mn);
-                rs += pv[j][i];
-            }
-        rs += lane_xor16(rs);
-        rs += lane_xor32(rs);
-        l = l * alpha + rs;
-        m = mn;
-#pragma unroll
-        for (int jd = 0; jd < 4; ++jd)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[jd][i] *= alpha;
-        // P^T fragments of the two 32-key steps: slots 8g..8g+7 hold keys
-        // 32 st + 4g + i and 32 st + 16 + 4g + i
-        u32x4 pb[2][2];
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const float x[8] = {pv[2 * st][0],     pv[2 * st][1],     pv[2 * st][2],
-                                pv[2 * st][3],     pv[2 * st + 1][0], pv[2 * st + 1][1],
-                                pv[2 * st + 1][2], pv[2 * st + 1][3]};
-            split8(x, pb[st][0], pb[st][1]);
-        }
-        // O^T[d][q] += V^T[d][key] P^T[key][q]: A = V^T rows (dim 16 jd + r)
-        // at the same key slots; the four dim blocks' chains interleaved
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            u32x4 va[3][4];
-#pragma unroll
-            for (int t = 0; t < 3; ++t)
-#pragma unroll
-                for (int jd = 0; jd < 4; ++jd) {
-                    const uint16_t *row = &Vt[t][16 * jd + r][32 * st + 4 * g];
-                    const uint2 lo = *(const uint2 *)row, hi = *(const uint2 *)(row + 16);
-                    va[t][jd] = u32x4{lo.x, lo.y, hi.x, hi.y};
-                }
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][0], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][0], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[2][jd], pb[st][0], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[0][jd], pb[st][1], o[jd]);
-#pragma unroll
-            for (int jd = 0; jd < 4; ++jd) o[jd] = mfma_b(va[1][jd], pb[st][1], o[jd]);
-        }
-    }
-    // lane (g, r): query q0 + r, dims 16 jd + 4g .. +3
-    if (qa < S) {
-        const float inv = 1.0f / l;
-        float *orow = P.O + z * P.sout + (size_t)qa * P.ldo + h * 64 + 4 * g;
-#pragma unroll
-        for (int jd = 0; jd < 4; ++jd) {
-            const float4 v =
-                make_float4(o[jd][0] * inv, o[jd][1] * inv, o[jd][2] * inv, o[jd][3] * inv);
-            if (P.o_vec) {
-                *(float4 *)(orow + 16 * jd) = v;
+        for (int i = 0; i < 8; ++i) {
+            float si, co;
+            if (P.tab) {
+                const float2 t = P.tab[row * 32 + d0 + i];
+                si = t.x;
+                co = t.y;
             } else {
-                orow[16 * jd] = v.x;
-                orow[16 * jd + 1] = v.y;
-                orow[16 * jd + 2] = v.z;
-                orow[16 * jd + 3] = v.w;
+                rope_angle(fpos, d0 + i, P.rope_step, &si, &co);
+            }
+            const float a = x1[i] * co - x2[i] * si, b = x1[i] * si + x2[i] * co;
+            x1[i] = a;
+            x2[i] = b;
+        }
+    };
+    auto unpack8 = [](float4 a, float4 b, float (&x)[8]) {
+        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
+        x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    };
+
+    // the block's raw rows in registers: thread (key kt, quarter kq) holds K
+    // dims 8 kq .. +7 and 32 + 8 kq .. +7, and V dims 16 kq .. +15
+    const int kt = tid >> 2, kq = tid & 3;
+    float4 kr[4], vr[4];
+    auto load_kv = [&](int kb) {
+        const int row = min(kb * AT_B + kt, S - 1);
+        kr[0] = ld4(P.K, row, 8 * kq);
+        kr[1] = ld4(P.K, row, 8 * kq + 4);
+        kr[2] = ld4(P.K, row, 32 + 8 * kq);
+        kr[3] = ld4(P.K, row, 32 + 8 * kq + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[i] = ld4(P.V, row, 16 * kq + 4 * i);
+    };
+    load_kv(0);
+
+    // this lane's query fragments: row q0 + r, dims 8g .. +7 and 32 + 8g ..
+    // (a RoPE pair per dim), two terms each; zero past the last row
+    const int qa = q0 + r;
+    u32x4 aq[2][2];  // [slice][term]
+    {
+        const int row = min(qa, S - 1);
+        float x1[8], x2[8];
+        unpack8(ld4(P.Q, row, 8 * g), ld4(P.Q, row, 8 * g + 4), x1);
+        unpack8(ld4(P.Q, row, 32 + 8 * g), ld4(P.Q, row, 32 + 8 * g + 4), x2);
+        rotate(x1, x2, row, 8 * g);
+        if (qa >= S)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.0f;
+        split8(x1, aq[0][0], aq[0][1]);
+        split8(x2, aq[1][0], aq[1][1]);
+    }
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < kb1; ++kb) {
+        const int key = kb * AT_B + kt, row = min(key, S - 1);
+        const bool ok = key < S, diag = kb == qb && ok;
+        __syncthreads();  // the previous block's Ks, Vt and vs are no longer read
+        {
+            float x1[8], x2[8];
+            unpack8(kr[0], kr[1], x1);
+            unpack8(kr[2], kr[3], x2);
+            rotate(x1, x2, row, 8 * kq);
+            if (!ok)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.0f;
+            if (diag && P.kc) {
+                float *kcr = P.kc + (((size_t)z * P.H + h) * P.hs + key) * 64;
+                *(float4 *)(kcr + 8 * kq) = make_float4(x1[0], x1[1], x1[2], x1[3]);
+                *(float4 *)(kcr + 8 * kq + 4) = make_float4(x1[4], x1[5], x1[6], x1[7]);
+                *(float4 *)(kcr + 32 + 8 * kq) = make_float4(x2[0], x2[1], x2[2], x2[3]);
+                *(float4 *)(kcr + 32 + 8 * kq + 4) = make_float4(x2[4], x2[5], x2[6], x2[7]);
+            }
+            u32x4 t0, t1;
+            split8(x1, t0, t1);
+            *(u32x4 *)&Ks[0][kt][8 * kq] = t0;
+            *(u32x4 *)&Ks[1][kt][8 * kq] = t1;
+            split8(x2, t0, t1);
+            *(u32x4 *)&Ks[0][kt][32 + 8 * kq] = t0;
+            *(u32x4 *)&Ks[1][kt][32 + 8 * kq] = t1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 x = vr[i];
+                if (diag && P.vc)
+                    *(float4 *)(P.vc + (((size_t)z * P.H + h) * P.hs + key) * 64 + 16 * kq + 4 * i) = x;
+                const int d = 16 * kq + 4 * i;
+                vs[kt][d] = ok ? x.x : 0.0f;
+                vs[kt][d + 1] = ok ? x.y : 0.0f;
+                vs[kt][d + 2] = ok ? x.z : 0.0f;
+                vs[kt][d + 3] = ok ? x.w : 0.0f;
             }
         }
+        __syncthreads();
+        // V^T terms: item (dim, key octet) splits 8 consecutive keys
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int item = tid + 256 * j, dim = item >> 3, kg = item & 7;
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = vs[8 * kg + i][dim];
+            u32x4 t0, t1, t2;
+            split8x3(x, t0, t1, t2);
+            *(u32x4 *)&Vt[0][dim][8 * kg] = t0;
+            *(u32x4 *)&Vt[1][dim][8 * kg] = t1;
+            *(u32x4 *)&Vt[2][dim][8 * kg] = t2;
+        }
+        __syncthreads();
+        if (kb + 1 < kb1) load_kv(kb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        prefill_block(Ks, Vt, aq, kb * AT_B, qa, S, causal, P.scale, m, l, o);
     }
+    prefill_store(o, l, qa, S, P.O, P.sout, P.ldo, P.o_vec, h);
+}
+
+// One launch when the K blocks are rotated by few query blocks and the grid
+// fills the CUs: with fewer workgroups (one 128-token sequence: 72) the
+// separate prep launch spreads the rotation and splitting over 4x the
+// threads, 5 % faster over the batch-1 prefill; at 16 sequences the one
+// launch is 2.4 % faster over the batch-16 prefill.
+bool attention_prefill_one_launch(int S, int H, int nseq) {
+    const int nqb = (S + AT_B - 1) / AT_B;
+    return S >= 1 && nqb <= 4 && (size_t)nqb * H * nseq >= 256;
+}
+
+int launch_rope_table(float2 *tab, int S, float pos0, float rope_step, hipStream_t st) {
+    if (S <= 0) return VMLM_OK;
+    rope_table_kernel<<<(S * 32 + 255) / 256, 256, 0, st>>>(tab, S, pos0, rope_step);
+    VMLM_HIP_CHECK(hipGetLastError());
+    return VMLM_OK;
 }
 
 size_t attention_prefill_work_bytes(int S, int H, int nseq) {
@@ -580,7 +778,7 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
                              int H, int ld, int ldo, float scale, bool causal, void *work,
                              hipStream_t st, bool rope, float rope_step, float pos0, int nseq,
                              size_t sin, size_t sout, float *kc, float *vc, int hs,
-                             const Slices &qs) {
+                             const Slices &qs, const float2 *rope_tab) {
     VMLM_GUARD(ld % 4 == 0 && ((uintptr_t)q & 7) == 0 && ((uintptr_t)k & 7) == 0 &&
                    ((uintptr_t)v & 15) == 0 && (nseq == 1 || sin % 4 == 0),
                "attention prefill: 16-byte aligned V rows and 8-byte aligned Q / K rows "
@@ -596,6 +794,36 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
     VMLM_GUARD(nseq >= 1 && nseq <= 65535 && H <= 65535, "attention prefill: grid too large");
     if (S <= 0) return VMLM_OK;
     const int Sp = (S + AT_B - 1) / AT_B * AT_B;
+    // up to four query blocks over a full grid: one launch from the f32 rows
+    // (16-byte rows, no k-slices)
+    if (attention_prefill_one_launch(S, H, nseq) && !qs.part && ((uintptr_t)q & 15) == 0 &&
+        ((uintptr_t)k & 15) == 0 && (nseq == 1 || sin % 4 == 0)) {
+        QKVPrefillParams F;
+        F.Q = q;
+        F.K = k;
+        F.V = v;
+        F.O = out;
+        F.kc = kc;
+        F.vc = vc;
+        F.sin = sin;
+        F.sout = sout;
+        F.S = S;
+        F.ld = ld;
+        F.ldo = ldo;
+        F.causal = causal ? 1 : 0;
+        F.nqb = Sp / AT_B;
+        F.H = H;
+        F.hs = hs;
+        F.rope = rope ? 1 : 0;
+        F.o_vec = ((uintptr_t)out & 15) == 0 && ldo % 4 == 0 && (nseq == 1 || sout % 4 == 0);
+        F.scale = scale;
+        F.rope_step = rope_step;
+        F.pos0 = pos0;
+        F.tab = rope ? rope_tab : nullptr;
+        attn_prefill_qkv_kernel<<<dim3(F.nqb, H, nseq), 256, 0, st>>>(F);
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     const size_t plane = (size_t)nseq * 2 * H * Sp * 64;
     QKVPrepParams kp;
     kp.Q = q;
@@ -1133,10 +1361,13 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
     VMLM_GUARD(lds <= AD_LDS_MAX, "attention decode: cache capacity %d needs split positions",
                a.cap);
     const dim3 grid(a.H, B);
+#ifndef VMLM_AD_NW
+#define VMLM_AD_NW 4
+#endif
     if (a.H * B < 256)
         launch_decode_nw<8>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
     else
-        launch_decode_nw<4>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
+        launch_decode_nw<VMLM_AD_NW>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }

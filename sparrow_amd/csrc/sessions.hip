@@ -698,6 +698,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
     int8_t *a8;
     int32_t *toks;
     char *kvw;
+    float2 *rtab;  // RoPE (sin, cos) of positions 0 .. S-1 (one-launch attention)
     // k-slice work of the int8-row GEMMs whose grids would leave CUs idle
     // (gate/up runs as one slice: its epilogue forms SiLU(gate) * up)
     const size_t gw = std::max(std::max(gemm_i8_work_floats((int)M, (int)(3 * H), (int)H),
@@ -705,7 +706,8 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
                                gemm_i8_work_floats((int)M, (int)H, (int)I));
     const size_t parts[] = {M * H * 4, M * H * 4, M * 3 * H * 4, M * H * 4, M * H * 4, M * I * 4,
                             q8_rows_bytes(M, std::max(H, I)), M * 4, M * 4,
-                            attention_prefill_work_bytes((int)S, (int)NH, (int)B), gw * 4};
+                            attention_prefill_work_bytes((int)S, (int)NH, (int)B), gw * 4,
+                            S * 32 * sizeof(float2)};
     size_t need = 0;
     for (size_t b : parts) need += (b + 255) / 256 * 256;
     if (d->pf_bytes < need) {
@@ -725,7 +727,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             c += (parts[i++] + 255) / 256 * 256;
         };
         carve(&h), carve(&h2), carve(&qkv), carve(&att), carve(&o), carve(&act), carve(&a8);
-        carve(&a8s), carve(&toks), carve(&kvw), carve(&gwork);
+        carve(&a8s), carve(&toks), carve(&kvw), carve(&gwork), carve(&rtab);
         if (!gw) gwork = nullptr;
     }
     auto run = [&]() -> int {
@@ -740,6 +742,12 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
         const int ks_qkv = gemm_i8_kslices((int)M, (int)(3 * H), (int)H);
         const int ks_o = gemm_i8_kslices((int)M, (int)H, (int)H);
         const int ks_d = gemm_i8_kslices((int)M, (int)H, (int)I);
+        // the rotation angles of the prompt positions, once for every layer
+        const float2 *tab = nullptr;
+        if (attention_prefill_one_launch((int)S, (int)NH, (int)B) && ks_qkv == 1) {
+            if ((r = launch_rope_table(rtab, (int)S, 0.0f, d->rope_step, st))) return r;
+            tab = rtab;
+        }
         for (size_t l = 0; l < d->L; ++l) {
             // the input norm; from layer 1 on it first adds the previous
             // layer's down projection to its residual h2: h = h2 + down
@@ -773,7 +781,7 @@ int vmlm_decoder_prefill(vmlm_decoder *d, const int32_t *tokens, uint32_t S,
             if ((r = launch_attention_prefill(qb, qb + H, qb + 2 * H, att, (int)S, (int)NH,
                                               (int)(3 * H), (int)H, d->c.attn_scale, true, kvw,
                                               st, true, d->rope_step, 0.0f, (int)B, S * 3 * H,
-                                              S * H, d->Kc(l), d->Vc(l), (int)d->hs, qs)))
+                                              S * H, d->Kc(l), d->Vc(l), (int)d->hs, qs, tab)))
                 return r;
             if ((r = launch_rows_q8(att, H, nullptr, 0.0f, M, H, a8, a8s, st))) return r;
             GemmArgs go = g;

@@ -454,6 +454,25 @@ def test_attention_prefill(ops, oracle, S, H):
     assert np.array_equal(got[0], v[0]) or np.abs(got[0] - v[0]).max() <= 1e-6
 
 
+def test_attention_prefill_one_launch_same_bits(ops, oracle):
+    """Up to four 64-query blocks (S <= 256) over at least 256 workgroups
+    (query blocks x heads) run as one launch from the f32 rows; longer
+    prompts prepare bf16 term planes in a first launch. Causal rows see only
+    earlier keys, so the first 256 output rows of a 300-token prompt (two
+    launches) equal those of its 256-token prefix (one launch, 64 heads) bit
+    for bit. Non-causal rows from the one launch match the oracle."""
+    rng = np.random.default_rng(31)
+    H = 64
+    q, k, v = (rng.standard_normal((300, H * 64), dtype=np.float32) for _ in range(3))
+    long_ = ops.attention_prefill(q, k, v, H, pos0=5)
+    short = ops.attention_prefill(q[:256].copy(), k[:256].copy(), v[:256].copy(), H, pos0=5)
+    assert np.array_equal(long_[:256].view(np.uint32), short.view(np.uint32))
+    for S in (200, 256):
+        got = ops.attention_prefill(q[:S].copy(), k[:S].copy(), v[:S].copy(), H, causal=False)
+        ref = oracle.attention_prefill(q[:S], k[:S], v[:S], H, causal=False)
+        assert_close_rms(got, ref)
+
+
 @pytest.mark.parametrize("H,pos", [(36, 1023), (36, 700), (4, 511), (36, 300)])
 def test_attention_decode_cfg2(ops, oracle, H, pos):
     """Config 2 decode: 1 query against a KV cache of length 1024 (pos 1023),
