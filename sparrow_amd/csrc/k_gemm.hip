@@ -615,9 +615,11 @@ int launch_gemm(const GemmArgs &a, hipStream_t st) {
         p.N = a.N;
         p.K = a.K;
         p.ldc = a.ldc;
-        // XCD-grouped tile order, 4 M-blocks per group (the prefill shapes,
-        // M = 2048: 7 to 12 % faster than the dispatch order)
-        p.group = a.group >= 0 ? a.group : 4;
+        // XCD-grouped tile order, 5 M-blocks per group (the prefill shapes,
+        // M = 2048: 7 to 12 % faster than the dispatch order; over the whole
+        // batch-16 prefill, groups of 3, 5 or 6 M-blocks measured 3.5 to 4 %
+        // faster than groups of 4 or 8, and 2 % faster than groups of 2)
+        p.group = a.group >= 0 ? a.group : 5;
         p.A8 = a.A8;
         p.a8s = a.a8s;
         // skinny grids: ordered k-slices through `work`, then the in-order
