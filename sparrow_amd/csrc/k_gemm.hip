@@ -497,6 +497,13 @@ static int launch_g(const GemmParams &p, int bm, int ns, hipStream_t st) {
     // gives two workgroups per CU (512 on this device), else 64 x 128 (and
     // always with three terms, whose 128-row stage would leave one workgroup
     // per CU). Two LDS stages keep two workgroups resident per CU.
+    // Single-term grids of at most one 64 x 128 tile per CU (config 1: 1024
+    // x 2048 x 512 gives 256, each CU streaming one tile's K and then writing
+    // 32 KB of results while nothing else runs): 64 x 64 tiles, two per CU,
+    // 6.6 -> 5.75 us; 32 x 64 and 32 x 128 tiles, three or four stages, or
+    // the XCD-grouped order were slower.
+    if (bm == 0 && T == 1 && (size_t)((p.M + 63) / 64) * ((p.N + 127) / 128) <= 256)
+        return launch_dma<WI8, T, 64, 64>(p, ns ? ns : 2, st);
     if (bm == 0) bm = T == 1 && ((p.M + 127) / 128) * ((p.N + 127) / 128) >= 512 ? 128 : 64;
     VMLM_GUARD(bm == 64 || bm == 128, "gemm: tile rows %d (64 or 128)", bm);
     if (ns == 0) ns = 2;
