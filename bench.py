@@ -429,7 +429,7 @@ def run_suite(iters, cpu=True):
     tf = 2147483648 / us / 1e6
     out["cfg1_bf16_gemm"] = {"us": round(us, 2), "host_us": round(wall, 2), "timing": _LAST[0],
                              "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                             "kernel_only": profiled_kernel_us("gemm_dma_kernel<false, 1, 64, 128, 2>")}
+                             "kernel_only": profiled_kernel_us("gemm_dma_kernel<false, 1, 64, 64, 2>")}
     # config 1's M = 1 variant (the GEMV path of the same entry point)
     b1 = 2048 * 512 * 2 + 512 * 2 + 2048 * 4
     ns1 = n_sets(b1, 10**9)
