@@ -1361,8 +1361,9 @@ int launch_attention_decode(const DecodeArgs &a, int B, float *out, int ldo, uin
     VMLM_GUARD(lds <= AD_LDS_MAX, "attention decode: cache capacity %d needs split positions",
                a.cap);
     const dim3 grid(a.H, B);
-    // (at 36 heads x 16 sequences, 8 and 16 waves per workgroup, 2 waves, or
-    // 32-position sub-chunks measured 1 to 34 % slower than 4 waves)
+    // (at 36 heads x 16 sequences, 8 and 16 waves per workgroup, 2 waves,
+    // 32-position sub-chunks, or two and three sub-chunks in flight per wave
+    // while one is consumed (one now) measured 1 to 34 % slower than 4 waves)
     if (a.H * B < 256)
         launch_decode_nw<8>(a, B, out, ldo, terms, T, ldt, st, grid, lds, 0, nullptr, gsub);
     else
