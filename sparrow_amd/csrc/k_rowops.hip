@@ -442,14 +442,18 @@ int launch_silu_q8(const float *part, int ks, int ldp, const float *sgu, int row
 // load. Lane piece p of a row: k-block p / 4, lane group g = p % 4, values
 // k = 64 (p / 4) + 8 g + 0..7 and 64 (p / 4) + 32 + 8 g + 0..7; rows past
 // the last (to the tile count) hold zero terms.
-// Many rows: two launches. rows_q8_stats_kernel (one workgroup per row) finds
+// At least 2048 rows: rows_q8_wave_kernel (below), one launch. Between 256
+// and 2048 rows: two launches. rows_q8_stats_kernel (one workgroup per row) finds
 // inv and the factor, rows_q8_terms_kernel (one workgroup per 16 rows x 32
 // lane pieces) forms y again with the same operations and writes the terms,
 // the 16 threads of a piece index writing 256 contiguous bytes of a block.
 // Few rows (RQ_ONE_MAX or fewer): rows_q8_stats_kernel<true> alone, one
 // workgroup per row that also writes its row's terms (4 bytes of a lane
 // piece per store), which saves the second launch where the grid is small.
-// Both give the same bits: the same sums in the same order.
+// These two give the same bits: the same sums in the same order. The wave
+// kernel sums x^2 in another order (a lane's pieces, then across the wave),
+// so with a norm its rows can differ from theirs in the last bit of inv;
+// without one (the maximum alone) all three give the same bits.
 // With ra / rb the rows are first formed as x = ra + rb (a residual add, the
 // f32 add of EWADD) and written to x; the terms kernel then reads them there.
 // rb may instead be k-slices (rbs.part, row stride cols): each element of rb
@@ -610,6 +614,125 @@ __global__ __launch_bounds__(16 * RQ_J) void rows_q8_terms_kernel(
         *(u32x4 *)(q8 + tt * plane + off) = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
 }
 
+// One launch for any row count: one wave per row, RW_ROWS rows per
+// workgroup. Lane l takes lane pieces l, l + 64, ... of its row (16 values
+// each: k-block p / 4, values 64 (p / 4) + 8 (p % 4) + 0..7 and + 32 ..), so
+// four adjacent lanes read one 64-column block with 16-byte loads, the row's
+// sum of squares and maximum reduce across the wave with DPP (no barrier),
+// and each term store is a whole 16-byte piece. The eight rows' pieces of a
+// 128-byte line of a block come from one workgroup, so the line is whole in
+// one L2 before it is written back (pieces of one line from different
+// workgroups, possibly on different XCDs, measured 5 % slower over the
+// batch-16 prefill than a second launch that re-reads the rows).
+constexpr int RW_ROWS = 8;
+template <int P>  // lane pieces per lane: cols <= 1024 * P
+__global__ __launch_bounds__(64 * RW_ROWS) void rows_q8_wave_kernel(
+    float *x, int ldx, const float *__restrict__ ra, const float *__restrict__ rb, Slices rbs,
+    const float *__restrict__ g, float eps, int cols, int rows, int row_tiles,
+    float *__restrict__ q8s, int8_t *__restrict__ q8) {
+    const int lane = threadIdx.x & 63;
+    const int row = (int)blockIdx.x * RW_ROWS + (int)(threadIdx.x >> 6);
+    const int npc = cols >> 4, nkb = cols >> 6;
+    const size_t plane = (size_t)row_tiles * cols * 16;
+    auto piece_off = [&](int pc) {
+        return ((size_t)(row >> 4) * nkb + (pc >> 2)) * 1024 +
+               (size_t)((pc & 3) * 16 + (row & 15)) * 16;
+    };
+    if (row >= rows) {  // a row past the last (to the tile count): zero terms
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int pc = lane + 64 * i;
+            if (pc >= npc) continue;
+#pragma unroll
+            for (int tt = 0; tt < Q8_T; ++tt) *(u32x4 *)(q8 + tt * plane + piece_off(pc)) = u32x4{0, 0, 0, 0};
+        }
+        return;
+    }
+    float *xr = x + (size_t)row * ldx;
+    const float *ar = ra ? ra + (size_t)row * ldx : nullptr;
+    const float *br = rbs.part ? rbs.part + (size_t)row * cols : rb ? rb + (size_t)row * ldx : nullptr;
+    // piece i: values k0 .. k0 + 7 in v[i][0..1], k0 + 32 .. in v[i][2..3]
+    auto kof = [&](int pc, int j) { return (pc >> 2) * 64 + 8 * (pc & 3) + 32 * (j >> 1) + 4 * (j & 1); };
+    float4 v[P][4];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int pc = lane + 64 * i;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (pc >= npc) continue;
+            const int kk = kof(pc, j);
+            if (ar) {
+                const float4 a = *(const float4 *)(ar + kk);
+                float4 b = *(const float4 *)(br + kk);
+                if (rbs.part) {  // slices in order, then the column scale
+                    for (int sl = 1; sl < rbs.ks; ++sl) {
+                        const float4 t = *(const float4 *)(br + (size_t)sl * rbs.pst + kk);
+                        b = make_float4(b.x + t.x, b.y + t.y, b.z + t.z, b.w + t.w);
+                    }
+                    const float4 sc = *(const float4 *)(rbs.scale + kk);
+                    b = make_float4(b.x * sc.x, b.y * sc.y, b.z * sc.z, b.w * sc.w);
+                }
+                v[i][j] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                *(float4 *)(xr + kk) = v[i][j];
+            } else {
+                v[i][j] = *(const float4 *)(xr + kk);
+            }
+        }
+    }
+    if (g) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ss += v[i][j].x * v[i][j].x + v[i][j].y * v[i][j].y + v[i][j].z * v[i][j].z +
+                      v[i][j].w * v[i][j].w;
+        ss = wave_sum_dpp(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int pc = lane + 64 * i;
+            if (pc >= npc) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 gg = *(const float4 *)(g + kof(pc, j));
+                v[i][j] = make_float4(v[i][j].x * inv * gg.x, v[i][j].y * inv * gg.y,
+                                      v[i][j].z * inv * gg.z, v[i][j].w * inv * gg.w);
+            }
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            mx = fmaxf(mx, fmaxf(fmaxf(q8_mag(v[i][j].x), q8_mag(v[i][j].y)),
+                                 fmaxf(q8_mag(v[i][j].z), q8_mag(v[i][j].w))));
+    const int k = q8_row_k(wave_max_nonneg(mx));
+    if (lane == 0) q8s[row] = q8_factor(k);
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int pc = lane + 64 * i;
+        if (pc >= npc) continue;
+        uint32_t w[Q8_T][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int a[4][Q8_T];
+            q8_split(v[i][j].x, k, a[0]);
+            q8_split(v[i][j].y, k, a[1]);
+            q8_split(v[i][j].z, k, a[2]);
+            q8_split(v[i][j].w, k, a[3]);
+#pragma unroll
+            for (int tt = 0; tt < Q8_T; ++tt) w[tt][j] = pack_i8x4(a[0][tt], a[1][tt], a[2][tt], a[3][tt]);
+        }
+        const size_t off = piece_off(pc);
+#pragma unroll
+        for (int tt = 0; tt < Q8_T; ++tt)
+            *(u32x4 *)(q8 + tt * plane + off) = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
+    }
+}
+
 size_t q8_rows_tiles(size_t rows) { return (rows + 63) / 64 * 4; }
 // the term planes, then one float per row (inv of the RMSNorm, kept between
 // the two launches)
@@ -633,6 +756,22 @@ int launch_rows_q8(const float *x, size_t ldx, const float *g, float eps, size_t
                    ((uintptr_t)q8 & 15) == 0 && q8s && rows <= 0x7fffffff,
                "rows_q8: cols %% 64 == 0, 64 <= cols <= %d, 16-byte aligned rows", 4 * 256 * RQ_U);
     const size_t tiles = q8_rows_tiles(rows);
+    // a grid of at least 256 workgroups of eight rows (M >= 2048: the batch-16
+    // prefill, 19.73 -> 19.35 ms); with fewer rows a wave per row leaves
+    // the CUs idle (the batch-1 prefill, 128 rows: 4.62 -> 5.87 ms)
+    if (rows >= (size_t)256 * RW_ROWS) {
+        const unsigned grid = (unsigned)(tiles * 16 / RW_ROWS);
+#define RW_LAUNCH(PV)                                                                            \
+    rows_q8_wave_kernel<PV><<<grid, 64 * RW_ROWS, 0, st>>>((float *)x, (int)ldx, ra, rb, rbs, g,  \
+                                                         eps, (int)cols, (int)rows, (int)tiles, \
+                                                         q8s, q8)
+        if (cols <= 1024 * 3) RW_LAUNCH(3);
+        else if (cols <= 1024 * 6) RW_LAUNCH(6);
+        else RW_LAUNCH(8);
+#undef RW_LAUNCH
+        VMLM_HIP_CHECK(hipGetLastError());
+        return VMLM_OK;
+    }
     if (rows <= RQ_ONE_MAX) {
         rows_q8_stats_kernel<true><<<(unsigned)(tiles * 16), 256, 0, st>>>(
             (float *)x, (int)ldx, ra, rb, rbs, g, eps, (int)cols, (int)rows, (int)tiles, nullptr,

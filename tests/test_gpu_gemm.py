@@ -135,6 +135,34 @@ def test_gemm_int8_row_split_paths_agree(dev):
         assert_close_rms(g257[r], ref[r])
 
 
+def test_gemm_int8_row_split_wave_path_agrees(dev):
+    """From 2048 rows one launch splits every row with one wave (eight rows
+    per workgroup, the row's maximum across the wave); below, the stats and
+    terms launches do. Without a norm the split depends only on each row's
+    maximum, so rows 0..2046 of a 2047-row and a 2048-row call give the same
+    bits. Rows of mixed magnitude, a zero row and a NaN row are among them."""
+    m, n, k = 2048, 8192, 512
+    rng = np.random.default_rng(2048)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    a *= np.float32(10.0) ** rng.integers(-6, 7, size=(m, 1)).astype(np.float32)
+    a[5] = 0.0
+    a[1700, 3] = np.nan
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, n)) / 127 + 1e-6).astype(np.float32)
+    da, dq, ds = dev.up(a), dev.up(q), dev.up(s)
+    c_lo, c_hi = dev.empty((m - 1) * n * 4), dev.empty(m * n * 4)
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, c_lo, m - 1, n, k, None))
+    dev.check(dev.lib.vmlm_hip_gemm_nt_int8(da, dq, ds, c_hi, m, n, k, None))
+    g_lo = dev.down(c_lo, (m - 1, n), np.float32)
+    g_hi = dev.down(c_hi, (m, n), np.float32)
+    assert np.isnan(g_hi[1700]).all() and (g_hi[5] == 0).all()
+    np.testing.assert_array_equal(g_lo.view(np.uint32), g_hi[:m - 1].view(np.uint32))
+    ref = (a[:64].astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    for r in range(0, 64, 7):
+        if r != 5:
+            assert_close_rms(g_hi[r], ref[r])
+
+
 @pytest.mark.parametrize("m,n", [(2048, 4096),    # 32 x 32 tiles of 64 x 128
                                  (2100, 4112)])   # ragged last tile row and column
 def test_gemm_int8_many_tiles_exact(dev, m, n):
