@@ -429,6 +429,15 @@ int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n);
  * strategy of this build: the interpreter runs them opcode by opcode with
  * the same results); for diagnostics and tests. */
 int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n);
+/* LOOP_CNT bodies, from the jump target up to the first opcode that needs
+ * the host between steps (PRINT, the counter, jumps, LAYERB, LN_EPS), run
+ * opcode by opcode on their first visit, are captured into a HIP graph on
+ * the second and replayed after (at the layer base they were captured at).
+ * on = 0 runs every body opcode by opcode; the results are the same bits.
+ * graph_segments counts the bodies replayed as graphs. No counterpart in the
+ * reference (an execution strategy of this build). */
+int vmlm_vm_set_graphs(vmlm_vm *vm, int on);
+int vmlm_vm_graph_segments(const vmlm_vm *vm, size_t *n);
 
 /* ================================================================ tables */
 

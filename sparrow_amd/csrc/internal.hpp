@@ -199,6 +199,10 @@ struct FxMultiArgs {
     int M = 0, K = 0;
     float *act = nullptr;
     int ldact = 0;
+    // one segment: also zadd = radd + C elementwise ([M][ldc], the EWADD
+    // after the GEMM; f32 addition, as the separate opcode)
+    const float *radd = nullptr;
+    float *zadd = nullptr;
 };
 int launch_fx_multi(const FxMultiArgs &a, hipStream_t st);
 // The int8 GEMM C[m][n] = (A[m] . Q[n]) * scale[n] (vmlm_hip_gemm_nt_int8) with

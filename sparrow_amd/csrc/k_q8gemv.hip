@@ -59,6 +59,8 @@ struct FxParams {
     int pair;            // gate/up pair (TW == 2)
     float *act;          // pair: [M][ldact]
     int ldact;
+    const float *radd;   // one segment: also z = radd + C (the EWADD after the
+    float *zadd;         // GEMM), both [M][ldc] of segment 0
     int ldw;
     const float *X;      // [M][ldx]
     int ldx;
@@ -264,6 +266,7 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
         const int row = lt * 16 + r;
         if (row >= S.N) continue;
         const float v = tile_out(t, m, r, row, S, e == tid ? sc0 : S.scale[row]);
+        if (p.zadd) p.zadd[(size_t)m * S.ldc + row] = p.radd[(size_t)m * S.ldc + row] + v;
         if (p.pair) {  // t == 0: the gate; the up value of the same output
             const float u = tile_out(1, m, r, row, p.seg[1], e == tid ? sc1 : p.seg[1].scale[row]);
             p.act[(size_t)m * p.ldact + row] = act_scalar(v, VMLM_ACT_SILU) * u;
@@ -363,6 +366,8 @@ int launch_fx_multi(const FxMultiArgs &a, hipStream_t st) {
     VMLM_GUARD(a.nseg >= 1 && a.nseg <= 3 && (!pair || (a.nseg == 2 && a.seg[0].N == a.seg[1].N &&
                                                         a.ldact >= a.seg[0].N)),
                "q8 GEMV: 1..3 segments; a gate/up pair has two of one width");
+    VMLM_GUARD(!a.zadd || (a.nseg == 1 && !pair && a.radd),
+               "q8 GEMV: the residual add takes one segment and its addend");
     FxParams p{};
     int tiles = 0;
     for (int i = 0; i < a.nseg; ++i) {
@@ -376,6 +381,8 @@ int launch_fx_multi(const FxMultiArgs &a, hipStream_t st) {
     p.pair = pair;
     p.act = a.act;
     p.ldact = a.ldact;
+    p.radd = a.radd;
+    p.zadd = a.zadd;
     p.ldw = a.ldw;
     p.X = a.X;
     p.ldx = a.ldx;

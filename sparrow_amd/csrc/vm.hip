@@ -291,11 +291,31 @@ constexpr int VM_ATTN_MAX_COLS = 8192;
 // every cached column (sum over k in order) times the scale, the softmax of
 // the first `live` columns (zeros past them), and the context over all
 // columns, as the GEMM-SCALE-SOFTMAX-GEMM run computes them.
+// FAST (hd = 64, at most 256 columns): every K and V value the thread uses
+// is loaded before the query is rotated (none depends on it), so the
+// workgroup waits for memory once instead of once per phase; the sums run in
+// the same order, so the results are the same bits.
+template <bool FAST>
 __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh, int *guard) {
     extern __shared__ float sm[];     // q[hd], p[cols]
     __shared__ float red[4];
     float *qs = sm, *pr = sm + a.hd;
     const int h = blockIdx.x, half = a.hd / 2, tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63;
+    const float *K = a.kc[h], *V = a.kc[nh + h];
+    float kv[FAST ? 64 : 1], vv[FAST ? 16 : 1][FAST ? 4 : 1];
+    if constexpr (FAST) {
+        // column tid of every K row; columns lane + 64 i of V rows w + 4 j
+#pragma unroll
+        for (int k = 0; k < 64; ++k) kv[k] = tid < a.cols ? K[(size_t)k * a.cols + tid] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = lane + 64 * i;
+                vv[j][i] = c < a.cols ? V[(size_t)(w + 4 * j) * a.cols + c] : 0.0f;
+            }
+    }
     const long pos = dev_index(a.posp, 1L << 24, guard);
     const long live = dev_index(a.livep, (long)a.cols + 1, guard);
     if (pos < 0 || live < 0) return;
@@ -315,12 +335,20 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         }
     }
     __syncthreads();
-    const float *K = a.kc[h], *V = a.kc[nh + h];
     const float sc = *a.scalep;
-    for (int c = tid; c < a.cols; c += 256) {
-        float s = 0.0f;
-        for (int k = 0; k < a.hd; ++k) s += qs[k] * K[(size_t)k * a.cols + c];
-        pr[c] = s * sc;
+    if constexpr (FAST) {
+        if (tid < a.cols) {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 64; ++k) s += qs[k] * kv[k];
+            pr[tid] = s * sc;
+        }
+    } else {
+        for (int c = tid; c < a.cols; c += 256) {
+            float s = 0.0f;
+            for (int k = 0; k < a.hd; ++k) s += qs[k] * K[(size_t)k * a.cols + c];
+            pr[c] = s * sc;
+        }
     }
     __syncthreads();
     const int lim = (int)live;
@@ -349,15 +377,28 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         for (int i = tid; i < a.cols; i += 256) a.scd[i] = pr[i];
     // context: wave w takes rows w, w + 4, ...; its lanes sum columns in
     // order per lane, then the wave sums its lanes
-    const int w = tid >> 6, lane = tid & 63;
-    for (int r = w; r < a.hd; r += 4) {
-        const float *vr = V + (size_t)r * a.cols;
-        float t = 0.0f;
-        for (int c = lane; c < a.cols; c += 64) t += pr[c] * vr[c];
+    auto store = [&](int r, float t) {
         t = wave_sum_dpp(t);
         if (lane == 0) {
             a.att[(size_t)h * a.hd + r] = t;
             if (last) a.ctxd[r] = t;
+        }
+    };
+    if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lane + 64 * i < a.cols) t += pr[lane + 64 * i] * vv[j][i];
+            store(w + 4 * j, t);
+        }
+    } else {
+        for (int r = w; r < a.hd; r += 4) {
+            const float *vr = V + (size_t)r * a.cols;
+            float t = 0.0f;
+            for (int c = lane; c < a.cols; c += 64) t += pr[c] * vr[c];
+            store(r, t);
         }
     }
 }
@@ -611,7 +652,9 @@ struct VmSlot {
 // A run of opcodes that the executor launches as one kernel (per-head decode
 // runs: vm_kv_append_kernel, vm_head_attn_kernel; GEMMs of one input), or as
 // one strided copy per stream (VF_COL_RUN: column-by-column cache writes).
-enum VmFuseKind { VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4, VF_COL_RUN = 5 };
+enum VmFuseKind {
+    VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4, VF_COL_RUN = 5, VF_GEMM_ADD = 6
+};
 struct VmColStream {
     uint32_t c, x, y;   // the column slot, the slot sliced, the slot written
     uint32_t xo, yo;    // first column read from x, first column written to y
@@ -626,6 +669,18 @@ struct VmFused {
     uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;  // scratch slots, in opcode order
     float **tab = nullptr;   // device: the nh K cache addresses, then the nh V
     VmColStream col[2];      // VF_COL_RUN: nh streams of `cols` steps
+};
+
+// The part of a LOOP_CNT body from its first instruction up to the first
+// opcode that needs the host between steps (PRINT, the loop counter, jumps,
+// LAYERB, LN_EPS): run eagerly on its first visit, captured into a HIP graph
+// on the second and replayed from then on (see vmlm_vm_run).
+enum VmSegState { VS_NEW = 0, VS_SEEN = 1, VS_GRAPH = 2, VS_EAGER = 3 };
+struct VmSeg {
+    uint32_t start = 0, end = 0;  // instructions [start, end)
+    int state = VS_NEW;
+    size_t base = 0;              // the layer base the graph was captured at
+    hipGraphExec_t exec = nullptr;
 };
 
 struct vmlm_vm {
@@ -648,6 +703,9 @@ struct vmlm_vm {
     std::map<size_t, SwzConst> swz;  // the pool's swizzled int8 constants (owned by the pool)
     std::vector<VmFused> fused;      // opcode runs executed as one launch each
     std::vector<int32_t> fuse_at;    // per instruction: index into `fused`, or -1
+    std::vector<VmSeg> segs;         // loop bodies replayed as HIP graphs
+    std::vector<int32_t> seg_at;     // per instruction: index into `segs`, or -1
+    bool graphs = true;              // vmlm_vm_set_graphs
 };
 
 static uint32_t rd32(const uint8_t *p, size_t off) {
@@ -665,6 +723,8 @@ static void vm_free(vmlm_vm *vm) {
         if (p) (void)hipFree(p);
     for (VmFused &f : vm->fused)
         if (f.tab) (void)hipFree(f.tab);
+    for (VmSeg &g : vm->segs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
     if (vm->st) (void)hipStreamDestroy(vm->st);
     delete vm;
 }
@@ -939,6 +999,23 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                 f.len = (uint32_t)j;
                 f.nh = (uint32_t)j;
             }
+            // one GEMM, then the residual EWADD of its output (z = r + y, the
+            // same shape, no broadcast): the GEMM's epilogue writes z too
+            const VmIns &e = T[i + 1];
+            if (!f.kind && j == 1 && i + 2 <= n && !target[i + 1] && e.op == VOP_EWADD &&
+                e.fl == 0 && ok(e.a) && ok(e.b) && ok(e.dst) && (e.a == gd) != (e.b == gd)) {
+                const uint32_t r = e.a == gd ? e.b : e.a, z = e.dst;
+                const bool shp = rows(gd) == M && cols(gd) == N && rows(e.a) == M &&
+                                 cols(e.a) == N && rows(e.b) == M && cols(e.b) == N;
+                if (shp && data(z) && f32(r) && rows(z) * cols(z) >= M * N &&
+                    disjoint({gd, z}, {A, g[0].b, g[0].dt, r})) {
+                    f.kind = VF_GEMM_ADD;
+                    f.len = 2;
+                    f.nh = 1;
+                    f.k = r;
+                    f.att = z;
+                }
+            }
         }
         // cache writes of a prompt, column by column (p12_build_minicpm.py:
         // 794-840): P steps of SLICE c <- x at column xo + p, then WRITECOL
@@ -990,7 +1067,8 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                 f.cols = (uint32_t)P;
             }
         }
-        if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP || f.kind == VF_COL_RUN) {  // no cache table
+        if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP || f.kind == VF_COL_RUN ||
+            f.kind == VF_GEMM_ADD) {  // no cache table
             f.start = (uint32_t)i;
             vm->fused.push_back(f);
             vm->fuse_at[i] = (int32_t)vm->fused.size() - 1;
@@ -1016,6 +1094,28 @@ static int vm_detect_fusions(vmlm_vm *vm) {
         i += f.len;
     }
     return VMLM_OK;
+}
+
+// The graph segments (VmSeg): for every LOOP_CNT, its body from the jump
+// target up to the first opcode that needs the host between steps.
+static void vm_detect_segments(vmlm_vm *vm) {
+    const std::vector<VmIns> &T = vm->text;
+    const size_t n = T.size();
+    vm->seg_at.assign(n, -1);
+    auto host_op = [](uint8_t op) {
+        return op == VOP_PRINT || op == VOP_LOOP_CNT || op == VOP_JMP || op == VOP_CMPLE ||
+               op == VOP_TOPK_THRESH || op == VOP_LAYERB || op == VOP_LN_EPS || op == VOP_HALT;
+    };
+    for (size_t i = 0; i < n; ++i) {
+        if (T[i].op != VOP_LOOP_CNT || T[i].dst >= i || vm->seg_at[T[i].dst] >= 0) continue;
+        VmSeg g;
+        g.start = T[i].dst;
+        g.end = g.start;
+        while (g.end < i && !host_op(T[g.end].op)) ++g.end;
+        if (g.end - g.start < 16) continue;  // too short to pay for a graph
+        vm->seg_at[g.start] = (int32_t)vm->segs.size();
+        vm->segs.push_back(g);
+    }
 }
 
 extern "C" {
@@ -1134,6 +1234,7 @@ int vmlm_vm_load(const void *image, size_t len, const void *weights, size_t weig
     if ((e = hipMalloc((void **)&vm->guard, 64)) != hipSuccess) return bad(hip_fail(e, "vm guard"));
     if ((rc = launch_fill_zero(vm->guard, 64, vm->st))) return bad(rc);
     if ((rc = vm_detect_fusions(vm))) return bad(rc);
+    vm_detect_segments(vm);
     // every int8 constant (the audit admits them only as GEMM B) also in the
     // swizzled layout, made once per pool; a constant whose copy does not fit
     // in device memory stays row-major only
@@ -1196,6 +1297,20 @@ int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n) {
     return VMLM_OK;
 }
 
+int vmlm_vm_set_graphs(vmlm_vm *vm, int on) {
+    VMLM_GUARD(vm, "null vm");
+    vm->graphs = on != 0;
+    return VMLM_OK;
+}
+
+int vmlm_vm_graph_segments(const vmlm_vm *vm, size_t *n) {
+    VMLM_GUARD(vm && n, "null argument");
+    size_t c = 0;
+    for (const VmSeg &g : vm->segs) c += g.state == VS_GRAPH;
+    *n = c;
+    return VMLM_OK;
+}
+
 void *vmlm_vm_stream(vmlm_vm *vm) { return vm ? (void *)vm->st : nullptr; }
 
 }  // extern "C"
@@ -1206,6 +1321,7 @@ namespace {
 struct Exec {
     vmlm_vm *vm;
     int *guard;
+    bool capturing = false;  // inside a graph capture: nothing may read the device or allocate
 
     size_t nel(uint32_t s) const {
         return s < vm->slots.size() ? (size_t)vm->slots[s].rows * vm->slots[s].cols : 0;
@@ -1250,6 +1366,7 @@ struct Exec {
                 return VMLM_OK;
             }
         }
+        VMLM_GUARD(!capturing, "graph capture: a device value read on the host");
         VMLM_HIP_CHECK(hipMemcpyAsync(v, p, 4, hipMemcpyDeviceToHost, vm->st));
         VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
         if (is_const) vm->kcache[(uintptr_t)p] = *v;
@@ -1257,6 +1374,7 @@ struct Exec {
     }
     int ws(size_t bytes, void **p) {
         if (bytes > vm->ws_bytes) {
+            VMLM_GUARD(!capturing, "graph capture: workspace growth");
             VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
             if (vm->ws) VMLM_HIP_CHECK(hipFree(vm->ws));
             vm->ws = nullptr;
@@ -1769,6 +1887,12 @@ int Exec::fused_gemms(const VmFused &f) {
         x.act = act;
         x.ldact = x.seg[0].N;
     }
+    if (f.kind == VF_GEMM_ADD) {
+        float *r, *z;
+        if ((rc = ptr(f.k, &r)) || (rc = ptr(f.att, &z))) return rc;
+        x.radd = r;
+        x.zadd = z;
+    }
     bool aligned = ((uintptr_t)ca & 15) == 0;
     for (int t = 0; t < x.nseg; ++t) aligned = aligned && ((uintptr_t)x.seg[t].W & 15) == 0;
     // mixed layouts, or operands OP_GEMM would not give this kernel: opcode
@@ -1787,7 +1911,7 @@ int Exec::fused_gemms(const VmFused &f) {
 // its opcodes (ROPE's theta), then the kernel with the device-side ones.
 int Exec::fused(const VmFused &f) {
     int rc = VMLM_OK;
-    if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP) return fused_gemms(f);
+    if (f.kind == VF_GEMMS || f.kind == VF_GATE_UP || f.kind == VF_GEMM_ADD) return fused_gemms(f);
     if (f.kind == VF_COL_RUN) {
         for (uint32_t q = 0; q < f.nh; ++q) {
             const VmColStream &c = f.col[q];
@@ -1847,7 +1971,10 @@ int Exec::fused(const VmFused &f) {
     a.qdrot = s1;
     a.scd = s2;
     a.ctxd = s3;
-    vm_head_attn_kernel<<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
+    if (f.hd == 64 && f.cols <= 256)
+        vm_head_attn_kernel<true><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
+    else
+        vm_head_attn_kernel<false><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -1880,6 +2007,61 @@ static int const_write_check(vmlm_vm *vm, const VmIns &in, size_t at) {
     return VMLM_OK;
 }
 
+// One instruction, or one fused run, at ip (advanced past it).
+static int vm_exec_one(Exec &ex, size_t &ip, bool &halt) {
+    vmlm_vm *vm = ex.vm;
+    if (vm->fuse_at[ip] >= 0) {  // a matched run in one launch (no constant written)
+        const VmFused &f = vm->fused[vm->fuse_at[ip]];
+        const int rc = ex.fused(f);
+        if (!rc) ip += f.len;
+        return rc;
+    }
+    const VmIns in = vm->text[ip++];
+    if (in.op == VOP_HALT) {
+        halt = true;
+        return VMLM_OK;
+    }
+    int rc = const_write_check(vm, in, ip - 1);
+    return rc ? rc : ex.step(in, &ip);
+}
+
+// Captures segment g into a HIP graph and launches it once (this visit's
+// work: capture itself runs nothing). Anything in the segment that would
+// read the device on the host, allocate, or fail ends the capture; the
+// caller then runs the segment opcode by opcode, which reports a real error
+// where it occurs.
+static int vm_capture(Exec &ex, VmSeg &g) {
+    vmlm_vm *vm = ex.vm;
+    if (hipStreamBeginCapture(vm->st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        (void)hipGetLastError();
+        return VMLM_ERR_UNIMPL;
+    }
+    ex.capturing = true;
+    size_t ip = g.start;
+    bool halt = false;
+    int rc = VMLM_OK;
+    while (rc == VMLM_OK && ip < g.end && !halt) rc = vm_exec_one(ex, ip, halt);
+    ex.capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(vm->st, &graph);
+    hipGraphExec_t x = nullptr;
+    if (rc == VMLM_OK && e == hipSuccess && graph && ip == g.end && !halt)
+        e = hipGraphInstantiate(&x, graph, nullptr, nullptr, 0);
+    else if (e == hipSuccess)
+        e = hipErrorUnknown;
+    if (graph) (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+        if (x) (void)hipGraphExecDestroy(x);
+        (void)hipGetLastError();
+        return VMLM_ERR_UNIMPL;
+    }
+    g.exec = x;
+    g.state = VS_GRAPH;
+    g.base = vm->layer_base;
+    VMLM_HIP_CHECK(hipGraphLaunch(x, vm->st));
+    return VMLM_OK;
+}
+
 int vmlm_vm_run(vmlm_vm *vm) {
     VMLM_GUARD(vm, "vm_run: null vm");
     int rc = ensure_init();
@@ -1890,19 +2072,26 @@ int vmlm_vm_run(vmlm_vm *vm) {
     Exec ex{vm, vm->guard};
     size_t ip = 0;
     const size_t n = vm->text.size();
-    while (ip < n) {
-        if (vm->fuse_at[ip] >= 0) {  // a per-head run in one launch (no constant written)
-            const VmFused &f = vm->fused[vm->fuse_at[ip]];
-            if ((rc = ex.fused(f))) {
-                (void)hipStreamSynchronize(vm->st);
-                return rc;
+    bool halt = false;
+    while (ip < n && !halt) {
+        if (vm->graphs && vm->seg_at[ip] >= 0) {
+            VmSeg &g = vm->segs[vm->seg_at[ip]];
+            if (g.state == VS_GRAPH && g.base == vm->layer_base) {
+                VMLM_HIP_CHECK(hipGraphLaunch(g.exec, vm->st));
+                ip = g.end;
+                continue;
             }
-            ip += f.len;
-            continue;
+            if (g.state == VS_SEEN) {
+                if (vm_capture(ex, g) == VMLM_OK) {  // captured and launched
+                    ip = g.end;
+                    continue;
+                }
+                g.state = VS_EAGER;  // opcode by opcode from now on
+            } else if (g.state == VS_NEW) {
+                g.state = VS_SEEN;  // the first visit runs eagerly (workspaces, scalars)
+            }
         }
-        const VmIns in = vm->text[ip++];
-        if (in.op == VOP_HALT) break;
-        if ((rc = const_write_check(vm, in, ip - 1)) || (rc = ex.step(in, &ip))) {
+        if ((rc = vm_exec_one(ex, ip, halt))) {
             (void)hipStreamSynchronize(vm->st);
             return rc;
         }

@@ -78,10 +78,20 @@ class Vm:
         check(lib().vmlm_vm_clear_output(self._h))
 
     def fused_runs(self) -> int:
-        """Per-head opcode runs of the decode loop executed as one launch
-        each (found at load)."""
+        """Opcode runs executed as one launch each (found at load)."""
         n = C.c_size_t()
         check(lib().vmlm_vm_fused_runs(self._h, C.byref(n)))
+        return n.value
+
+    def set_graphs(self, on: bool) -> None:
+        """Replay loop bodies as HIP graphs (the default), or run every
+        opcode one by one; the results are the same bits."""
+        check(lib().vmlm_vm_set_graphs(self._h, 1 if on else 0))
+
+    def graph_segments(self) -> int:
+        """Loop bodies replayed as HIP graphs so far."""
+        n = C.c_size_t()
+        check(lib().vmlm_vm_graph_segments(self._h, C.byref(n)))
         return n.value
 
     def swizzled_consts(self) -> int:

@@ -290,6 +290,53 @@ def test_vm_looped_and_step_loop(gvm, tiny):
     assert np.array_equal(toks[0], toks[1])
 
 
+def test_vm_graph_segments_same_bits(gvm, tiny):
+    """Loop bodies up to their first host opcode run eagerly on the first
+    visit, are captured into a HIP graph on the second and replayed after.
+    The step-looped decode (its body up to the PRINT of the logits) gives the
+    same bits with graphs as without: every PRINTed value, the greedy chain,
+    the caches and the scratch slots, over two runs of the same VM (the
+    second replays from its first step, with the eager opcodes and
+    synchronisations between replays). The LAYERB-looped prefill's layer body
+    reads each layer's own scalars (eps, theta) on the host at a new layer
+    base, which ends its capture: it runs opcode by opcode, with the same
+    bits."""
+    cfg, W = tiny
+    nl, nh = cfg["n_layers"], cfg["n_heads"]
+    prompt = M.make_prompts(cfg, 1, 6, seed=8)[0]
+    slots = ["st_gen", "hdec", "xnd", "attd", "actsd"]
+    slots += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
+    slots += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
+    img = programs.minicpm_program(cfg, W, 6, 7, step_loop=True, print_prefill=False).build()
+    res = {}
+    for on in (False, True):
+        with gvm.Vm(img) as g:
+            g.set_graphs(on)
+            runs = []
+            for _ in range(2):
+                g.clear_output()
+                g.write("st_tok", prompt)
+                g.write("st_gen", [11])
+                g.run()
+                runs.append((g.output(), {r: g.read(r) for r in slots}))
+            assert g.graph_segments() == (1 if on else 0)
+        res[on] = runs
+    for k in range(2):
+        assert np.array_equal(bits(res[False][k][0]), bits(res[True][k][0])), k
+        for r in slots:
+            assert np.array_equal(bits(res[False][k][1][r]), bits(res[True][k][1][r])), (k, r)
+    img = programs.minicpm_program(cfg, W, 6, looped=True).build()
+    outs = {}
+    for on in (False, True):
+        with gvm.Vm(img) as g:
+            g.set_graphs(on)
+            g.write("st_tok", prompt)
+            g.run()
+            outs[on] = g.output()
+            assert g.graph_segments() == 0
+    assert np.array_equal(bits(outs[False]), bits(outs[True]))
+
+
 def test_vm_fused_head_runs(gvm, oracle, tiny):
     """The step-looped decode's per-head runs (cache append; attention) run
     as one launch each per layer: the same greedy tokens as the oracle VM,
@@ -308,9 +355,10 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
     approx += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     approx += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     with gvm.Vm(img) as g:
-        # per layer: the cache append, the attention, q/k/v, gate/up, and
-        # the prompt's column-by-column cache writes of every head
-        assert g.fused_runs() == 4 * nl + nl * nh
+        # per layer: the cache append, the attention, q/k/v, gate/up, o and
+        # down each with its residual add, and the prompt's column-by-column
+        # cache writes of every head
+        assert g.fused_runs() == 6 * nl + nl * nh
         g.write("st_tok", prompt)
         g.write("st_gen", [11])
         g.run()
@@ -330,8 +378,9 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
         rms = np.sqrt(np.mean(ol[s_].astype(np.float64) ** 2))
         assert np.abs(gl[s_] - ol[s_]).max() <= 1e-4 * rms, s_
     with gvm.Vm(programs.minicpm_program(cfg, W, S, G).build()) as g:
-        # q/k/v and gate/up of every step, the prompt's cache writes per head
-        assert g.fused_runs() == 2 * nl * G + nl * nh
+        # q/k/v, gate/up, o + add and down + add of every step, the prompt's
+        # cache writes per head
+        assert g.fused_runs() == 4 * nl * G + nl * nh
 
 
 @pytest.mark.parametrize("m", [1, 3])
@@ -457,6 +506,57 @@ def test_vm_fused_runs_guard(gvm):
     for pos, live in ((C, 3), (2, C + 1)):
         c, m = codes(gvm, prog(pos, live))
         assert c == 9 and "guard" in m, m
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_vm_fused_gemm_add_runs(gvm, oracle, m):
+    """An int8 GEMM at decode rows followed by the EWADD of its output and a
+    residual (either operand order) runs as one launch whose epilogue also
+    writes the sum: the GEMM output and the sum are the bits of the two
+    opcodes run one by one (a SHAPE between them breaks the run), and match
+    the oracle VM (GEMM within 1e-4 RMS)."""
+    rng = np.random.default_rng(90 + m)
+    k, nrows = 768, 128
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.integers(-127, 128, size=(nrows, k), dtype=np.int8)
+    sc = (np.abs(rng.normal(0, 0.02, nrows)) / 127 + 1e-6).astype(np.float32)
+    rv = rng.standard_normal((m, nrows)).astype(np.float32)
+
+    def prog(split, swap):
+        P = vmb.Program()
+        X = P.const("x", x)
+        W = P.const("w", w, "i8")
+        S = P.const("w_sc", sc, rows=nrows, cols=1)
+        R0 = P.const("r0", rv)
+        for name in ("r", "y", "z"):
+            P.act(name, m, nrows)
+        P.ins("COPY", P["r"], R0)
+        P.ins("GEMM", P["y"], X, W, dt=S)
+        if split:
+            P.ins("SHAPE", 0, 0, 0)
+        if swap:
+            P.ins("EWADD", P["z"], P["y"], P["r"])
+        else:
+            P.ins("EWADD", P["z"], P["r"], P["y"])
+        P.ins("HALT")
+        return P
+
+    for swap in (False, True):
+        res = {}
+        for split in (False, True):
+            with gvm.Vm(prog(split, swap).build()) as g:
+                assert g.fused_runs() == (0 if split else 1)
+                g.run()
+                res[split] = {r: g.read(r) for r in ("y", "z")}
+        for r in ("y", "z"):
+            assert np.array_equal(bits(res[False][r]), bits(res[True][r])), (swap, r)
+        with oracle.OracleVm(prog(False, swap).build()) as o:
+            o.run()
+            ref = {r: o.read(r) for r in ("y", "z")}
+        for r in ("y", "z"):
+            rms = np.sqrt(np.mean(ref[r].astype(np.float64) ** 2))
+            assert np.abs(res[False][r] - ref[r]).max() <= 1e-4 * rms, (swap, r)
+        assert np.array_equal(bits(res[False]["z"]), bits(rv + res[False]["y"]))
 
 
 @pytest.mark.parametrize("Q", [1, 2])
