@@ -226,7 +226,11 @@ int launch_rmsnorm_resid(const float *base, const float *part, int ks, int ldp,
 }
 
 // One wave per (segment, row): the residual add of a k-split projection and
-// the int8 input of the next k-slice GEMVs (see launch_resid_q8). Lane l
+// the int8 input of the next k-slice GEMVs (see launch_resid_q8). One wave
+// per workgroup: grouping 4, 8 or 16 rows of a segment in one workgroup
+// (whole 128-byte lines of the blocked output from one CU) measured 0.5 to
+// 7 % slower over the batch-16 decode step; the latency of the partial
+// reads, not the write-back, sets this kernel's time. Lane l
 // holds columns 4c..4c+3 of the segment, c = l + 64i (i < SI); all slices of
 // a column are loaded up front so the reads take one round trip. The segment's power-of-two factor comes from its own max |x * g|.
 template <int SI, int KSN, bool BLK>
