@@ -729,6 +729,20 @@ static void vm_free(vmlm_vm *vm) {
     delete vm;
 }
 
+// Drops every captured loop-body graph (they bake in device addresses and
+// host-side values: the workspace, constant scalars, the LN epsilon); the
+// bodies are captured again on their next visits.
+static void vm_drop_graphs(vmlm_vm *vm) {
+    for (VmSeg &g : vm->segs) {
+        if (g.exec) {
+            (void)hipStreamSynchronize(vm->st);
+            (void)hipGraphExecDestroy(g.exec);
+            g.exec = nullptr;
+        }
+        if (g.state == VS_GRAPH || g.state == VS_SEEN) g.state = VS_NEW;
+    }
+}
+
 // core/src/interp.rs:241-348 audit_const_dtypes.
 static int vm_audit(const vmlm_vm *vm) {
     const size_t ns = vm->slots.size();
@@ -1096,22 +1110,31 @@ static int vm_detect_fusions(vmlm_vm *vm) {
     return VMLM_OK;
 }
 
+static uint32_t written_slot(const VmIns &in);
+
 // The graph segments (VmSeg): for every LOOP_CNT, its body from the jump
 // target up to the first opcode that needs the host between steps.
 static void vm_detect_segments(vmlm_vm *vm) {
     const std::vector<VmIns> &T = vm->text;
     const size_t n = T.size();
     vm->seg_at.assign(n, -1);
-    auto host_op = [](uint8_t op) {
-        return op == VOP_PRINT || op == VOP_LOOP_CNT || op == VOP_JMP || op == VOP_CMPLE ||
-               op == VOP_TOPK_THRESH || op == VOP_LAYERB || op == VOP_LN_EPS || op == VOP_HALT;
+    // opcodes that need the host between steps, and writes of a constant
+    // slot (the host drops its cached constant scalars there)
+    auto host_op = [&](const VmIns &in) {
+        const uint8_t op = in.op;
+        if (op == VOP_PRINT || op == VOP_LOOP_CNT || op == VOP_JMP || op == VOP_CMPLE ||
+            op == VOP_TOPK_THRESH || op == VOP_LAYERB || op == VOP_LN_EPS || op == VOP_HALT)
+            return true;
+        const uint32_t w = written_slot(in);
+        return w < vm->slots.size() &&
+               (vm->slots[w].kind == VSLOT_CONST || vm->slots[w].kind == VSLOT_PARAM);
     };
     for (size_t i = 0; i < n; ++i) {
         if (T[i].op != VOP_LOOP_CNT || T[i].dst >= i || vm->seg_at[T[i].dst] >= 0) continue;
         VmSeg g;
         g.start = T[i].dst;
         g.end = g.start;
-        while (g.end < i && !host_op(T[g.end].op)) ++g.end;
+        while (g.end < i && !host_op(T[g.end])) ++g.end;
         if (g.end - g.start < 16) continue;  // too short to pay for a graph
         vm->seg_at[g.start] = (int32_t)vm->segs.size();
         vm->segs.push_back(g);
@@ -1375,6 +1398,7 @@ struct Exec {
     int ws(size_t bytes, void **p) {
         if (bytes > vm->ws_bytes) {
             VMLM_GUARD(!capturing, "graph capture: workspace growth");
+            vm_drop_graphs(vm);  // the old workspace is freed below
             VMLM_HIP_CHECK(hipStreamSynchronize(vm->st));
             if (vm->ws) VMLM_HIP_CHECK(hipFree(vm->ws));
             vm->ws = nullptr;
@@ -1499,7 +1523,12 @@ int Exec::step(const VmIns &in, size_t *ip) {
         if ((rc = copy(cd, ca, r * c))) return rc;
         return launch_layernorm(cd, g, bias, r, c, vm->ln_eps, st);
     }
-    case VOP_LN_EPS: return scalar(d, &vm->ln_eps);
+    case VOP_LN_EPS: {
+        const float old = vm->ln_eps;
+        if ((rc = scalar(d, &vm->ln_eps))) return rc;
+        if (vm->ln_eps != old) vm_drop_graphs(vm);  // LN opcodes baked the old value
+        return VMLM_OK;
+    }
     case VOP_RMSNORM: {
         const size_t r = rows(a), c = cols(a);
         NEED(nel(d) >= r * c && nel(b) >= c, "RMSNORM: operand extents");
@@ -2004,6 +2033,7 @@ static int const_write_check(vmlm_vm *vm, const VmIns &in, size_t at) {
                "weights are mapped read-only: instruction %zu (op %u) writes constant slot %u", at,
                (unsigned)in.op, w);
     vm->kcache.clear();
+    vm_drop_graphs(vm);  // captured bodies may have baked the constant's old value
     return VMLM_OK;
 }
 

@@ -337,6 +337,52 @@ def test_vm_graph_segments_same_bits(gvm, tiny):
     assert np.array_equal(bits(outs[False]), bits(outs[True]))
 
 
+@pytest.mark.parametrize("rewrite", [False, True])
+def test_vm_graph_segment_constant_writes(gvm, oracle, rewrite):
+    """A loop body whose ROPE angle comes from a constant scalar: captured
+    after its first visit and replayed (one graph segment) when nothing
+    writes the constant; when the body rewrites the constant (a COPY into
+    it, which ends the segment before it and drops captured graphs), the
+    body keeps running opcode by opcode. Either way the results equal the
+    same VM without graphs and the oracle VM, bit for bit."""
+    rng = np.random.default_rng(11)
+    hd = 16
+
+    def prog():
+        P = vmb.Program()
+        x0 = P.const("x0", rng_x)
+        th = P.scalar("th", 10000.0)
+        th2 = P.scalar("th2", 500.0)
+        P.scalar("steps", 5.0)
+        for name in ("x", "y", "acc", "cnt"):
+            P.act(name, 1, hd if name != "cnt" else 1)
+        P.ins("COPY", P["x"], x0)
+        P.ins("COPY", P["cnt"], P["steps"])
+        top = P.label()
+        for i in range(10):
+            P.ins("ROPE", P["y"], P["x"], th, dt=i)
+            P.ins("EWADD", P["acc"], P["acc"], P["y"])
+        if rewrite:
+            P.ins("COPY", th, th2)
+        P.ins("LOOP_CNT", top, P["cnt"])
+        P.ins("HALT")
+        return P
+
+    rng_x = rng.standard_normal((1, hd)).astype(np.float32)
+    img = prog().build()
+    res = {}
+    for on in (False, True):
+        with gvm.Vm(img) as g:
+            g.set_graphs(on)
+            g.run()
+            res[on] = g.read("acc")
+            assert g.graph_segments() == (1 if on and not rewrite else 0)
+    assert np.array_equal(bits(res[False]), bits(res[True]))
+    with oracle.OracleVm(img) as o:
+        o.run()
+        assert np.array_equal(bits(o.read("acc")), bits(res[True]))
+
+
 def test_vm_fused_head_runs(gvm, oracle, tiny):
     """The step-looped decode's per-head runs (cache append; attention) run
     as one launch each per layer: the same greedy tokens as the oracle VM,
