@@ -737,6 +737,7 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
                 v.run()
                 ts.append(time.perf_counter() - t)
             times[G] = min(ts)
+            info["graph_segments"] = v.graph_segments()
             gen = v.read("st_gen")[0].astype(np.int64)
     dt = times[base + steps] - times[base]
     same = np.array_equal(gen, chain.astype(np.int64))
@@ -756,7 +757,10 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
                 "except the runs it matched at load (fused_runs: per layer the cache append and "
                 "the attention over all heads, q/k/v, and gate/up with ACT and EWMUL, one launch "
                 "each; per layer and head the prompt's column-by-column K/V cache writes, two "
-                "strided copies); the rate is the difference of two programs' run times",
+                "strided copies; o and down with their residual EWADD, one launch each). The "
+                "loop body up to its PRINT is captured into a HIP graph on its second step and "
+                "replayed after (graph_segments). The rate is the difference of two programs' "
+                "run times",
     }
 
 
