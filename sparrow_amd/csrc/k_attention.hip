@@ -617,7 +617,6 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2 *tab, int S, flo
 __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AT_B][AT_LD];   // [term][key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t Vt[3][64][AT_LD];     // [term][dim][key]
-    __shared__ float vs[AT_B][AT_B + 1];                                    // f32 V block
     const int S = P.S, causal = P.causal;
     const int h = blockIdx.y, z = blockIdx.z;
     const int qb = causal ? P.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
@@ -633,16 +632,27 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillPara
     };
     // RoPE of a row's dims d0 .. d0 + 7 (x1) with their partners d0 + 32 ..
     // (x2) at position pos0 + row, the prep kernel's arithmetic
-    auto rotate = [&](float (&x1)[8], float (&x2)[8], int row, int d0) {
+    // (sin, cos) of a row's pairs d0 .. d0 + 7 from the table (P.tab), or
+    // from rope_angle when there is none
+    auto load_tab = [&](float2 (&t)[8], int row, int d0) {
+        if (!P.rope || !P.tab) return;
+        const float4 *tp = (const float4 *)(P.tab + (size_t)row * 32 + d0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 u = tp[i];
+            t[2 * i] = make_float2(u.x, u.y);
+            t[2 * i + 1] = make_float2(u.z, u.w);
+        }
+    };
+    auto rotate = [&](float (&x1)[8], float (&x2)[8], int row, int d0, const float2 (&t)[8]) {
         if (!P.rope) return;
         const float fpos = P.pos0 + (float)row;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             float si, co;
             if (P.tab) {
-                const float2 t = P.tab[row * 32 + d0 + i];
-                si = t.x;
-                co = t.y;
+                si = t[i].x;
+                co = t[i].y;
             } else {
                 rope_angle(fpos, d0 + i, P.rope_step, &si, &co);
             }
@@ -656,18 +666,29 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillPara
         x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
     };
 
-    // the block's raw rows in registers: thread (key kt, quarter kq) holds K
-    // dims 8 kq .. +7 and 32 + 8 kq .. +7, and V dims 16 kq .. +15
-    const int kt = tid >> 2, kq = tid & 3;
-    float4 kr[4], vr[4];
+    // the block's raw rows in registers, loaded one block ahead: thread (key
+    // kt, quarter kq) holds K dims 8 kq .. +7 and 32 + 8 kq .. +7 with their
+    // rotation angles, and for the V^T items tid and tid + 256 (dim vd, keys
+    // 8 kg .. 8 kg + 7 with kg = tid / 64 + 4 j) the eight V values (each
+    // load instruction reads 64 consecutive dims of one row)
+    const int kt = tid >> 2, kq = tid & 3, vd = tid & 63;
+    float4 kr[4];
+    float2 ktab[8];
+    float vv[2][8];
     auto load_kv = [&](int kb) {
         const int row = min(kb * AT_B + kt, S - 1);
         kr[0] = ld4(P.K, row, 8 * kq);
         kr[1] = ld4(P.K, row, 8 * kq + 4);
         kr[2] = ld4(P.K, row, 32 + 8 * kq);
         kr[3] = ld4(P.K, row, 32 + 8 * kq + 4);
+        load_tab(ktab, row, 8 * kq);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[i] = ld4(P.V, row, 16 * kq + 4 * i);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int vrow = min(kb * AT_B + 8 * ((tid >> 6) + 4 * j) + i, S - 1);
+                vv[j][i] = P.V[base + (size_t)vrow * P.ld + vd];
+            }
     };
     load_kv(0);
 
@@ -678,9 +699,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillPara
     {
         const int row = min(qa, S - 1);
         float x1[8], x2[8];
+        float2 qtab[8];
         unpack8(ld4(P.Q, row, 8 * g), ld4(P.Q, row, 8 * g + 4), x1);
         unpack8(ld4(P.Q, row, 32 + 8 * g), ld4(P.Q, row, 32 + 8 * g + 4), x2);
-        rotate(x1, x2, row, 8 * g);
+        load_tab(qtab, row, 8 * g);
+        rotate(x1, x2, row, 8 * g, qtab);
         if (qa >= S)
 #pragma unroll
             for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.0f;
@@ -695,12 +718,12 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillPara
     for (int kb = 0; kb < kb1; ++kb) {
         const int key = kb * AT_B + kt, row = min(key, S - 1);
         const bool ok = key < S, diag = kb == qb && ok;
-        __syncthreads();  // the previous block's Ks, Vt and vs are no longer read
+        __syncthreads();  // the previous block's Ks and Vt are no longer read
         {
             float x1[8], x2[8];
             unpack8(kr[0], kr[1], x1);
             unpack8(kr[2], kr[3], x2);
-            rotate(x1, x2, row, 8 * kq);
+            rotate(x1, x2, row, 8 * kq, ktab);
             if (!ok)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.0f;
@@ -718,31 +741,26 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_qkv_kernel(QKVPrefillPara
             split8(x2, t0, t1);
             *(u32x4 *)&Ks[0][kt][32 + 8 * kq] = t0;
             *(u32x4 *)&Ks[1][kt][32 + 8 * kq] = t1;
+            // V^T terms: item (dim vd, key octet kg) splits 8 consecutive keys
+            // (zero past the last row); the diagonal block's raw rows go to
+            // the cache, 64 consecutive dims per store instruction
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 x = vr[i];
-                if (diag && P.vc)
-                    *(float4 *)(P.vc + (((size_t)z * P.H + h) * P.hs + key) * 64 + 16 * kq + 4 * i) = x;
-                const int d = 16 * kq + 4 * i;
-                vs[kt][d] = ok ? x.x : 0.0f;
-                vs[kt][d + 1] = ok ? x.y : 0.0f;
-                vs[kt][d + 2] = ok ? x.z : 0.0f;
-                vs[kt][d + 3] = ok ? x.w : 0.0f;
+            for (int j = 0; j < 2; ++j) {
+                const int kg = (tid >> 6) + 4 * j;
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int vkey = kb * AT_B + 8 * kg + i;
+                    x[i] = vkey < S ? vv[j][i] : 0.0f;
+                    if (kb == qb && vkey < S && P.vc)
+                        P.vc[(((size_t)z * P.H + h) * P.hs + vkey) * 64 + vd] = vv[j][i];
+                }
+                u32x4 t0, t1, t2;
+                split8x3(x, t0, t1, t2);
+                *(u32x4 *)&Vt[0][vd][8 * kg] = t0;
+                *(u32x4 *)&Vt[1][vd][8 * kg] = t1;
+                *(u32x4 *)&Vt[2][vd][8 * kg] = t2;
             }
-        }
-        __syncthreads();
-        // V^T terms: item (dim, key octet) splits 8 consecutive keys
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int item = tid + 256 * j, dim = item >> 3, kg = item & 7;
-            float x[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = vs[8 * kg + i][dim];
-            u32x4 t0, t1, t2;
-            split8x3(x, t0, t1, t2);
-            *(u32x4 *)&Vt[0][dim][8 * kg] = t0;
-            *(u32x4 *)&Vt[1][dim][8 * kg] = t1;
-            *(u32x4 *)&Vt[2][dim][8 * kg] = t2;
         }
         __syncthreads();
         if (kb + 1 < kb1) load_kv(kb + 1);
@@ -819,7 +837,7 @@ int launch_attention_prefill(const float *q, const float *k, const float *v, flo
         F.scale = scale;
         F.rope_step = rope_step;
         F.pos0 = pos0;
-        F.tab = rope ? rope_tab : nullptr;
+        F.tab = rope && ((uintptr_t)rope_tab & 15) == 0 ? rope_tab : nullptr;  // 16-byte table loads
         attn_prefill_qkv_kernel<<<dim3(F.nqb, H, nseq), 256, 0, st>>>(F);
         VMLM_HIP_CHECK(hipGetLastError());
         return VMLM_OK;
