@@ -423,12 +423,18 @@ int vmlm_vm_pool_uploads(size_t *n);
  * counterpart in the reference (a layout of this build); for diagnostics
  * and tests. */
 int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n);
-/* Per-head opcode runs of the decode loop (the cache append and the
- * attention of all heads of a layer) that this VM executes as one launch
- * each, found at load. No counterpart in the reference (an execution
- * strategy of this build: the interpreter runs them opcode by opcode with
- * the same results); for diagnostics and tests. */
+/* Opcode runs that this VM executes as one launch each (or, for a
+ * prompt's column-by-column cache writes, two strided copies per stream),
+ * found at load: the decode loop's per-head cache append and attention of
+ * all heads of a layer, int8 GEMMs of one input at decode rows (with the
+ * RMSNORM before them, the ACT and EWMUL of a gate/up pair, or the residual
+ * EWADD after one GEMM), and column-by-column cache writes. No counterpart
+ * in the reference (an execution strategy of this build: the interpreter
+ * runs them opcode by opcode with the same results); for diagnostics and
+ * tests. vmlm_vm_fused_opcodes gives the number of opcodes those runs
+ * cover. */
 int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n);
+int vmlm_vm_fused_opcodes(const vmlm_vm *vm, size_t *n);
 /* LOOP_CNT bodies, from the jump target up to the first opcode that needs
  * the host between steps (PRINT, the counter, jumps, LAYERB, LN_EPS), run
  * opcode by opcode on their first visit, are captured into a HIP graph on

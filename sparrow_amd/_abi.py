@@ -155,6 +155,7 @@ SIGNATURES = {
     "vmlm_vm_pool_uploads": (I, [C.POINTER(SZ)]),
     "vmlm_vm_swizzled_consts": (I, [P, C.POINTER(SZ)]),
     "vmlm_vm_fused_runs": (I, [P, C.POINTER(SZ)]),
+    "vmlm_vm_fused_opcodes": (I, [P, C.POINTER(SZ)]),
     "vmlm_vm_set_graphs": (I, [P, I]),
     "vmlm_vm_graph_segments": (I, [P, C.POINTER(SZ)]),
     "vmlm_hip_backend": (P, []),

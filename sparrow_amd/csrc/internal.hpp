@@ -203,8 +203,17 @@ struct FxMultiArgs {
     // after the GEMM; f32 addition, as the separate opcode)
     const float *radd = nullptr;
     float *zadd = nullptr;
+    // with norm_g: the GEMMs read the RMSNorm of the row X (M = 1), y = (x *
+    // inv) * g with inv = 1 / sqrt(mean(x^2) + eps) summed as launch_rmsnorm's
+    // one-pass kernel sums it (the same bits as that launch), and y is also
+    // written to norm_out [K] (swizzled weights, K % 4 == 0, K <= 4096)
+    const float *norm_g = nullptr;
+    float *norm_out = nullptr;
+    float norm_eps = 0.0f;
 };
 int launch_fx_multi(const FxMultiArgs &a, hipStream_t st);
+// a normalizing launch_fx_multi kernel exists for rows of K values
+bool fx_norm_ok(int K);
 // The int8 GEMM C[m][n] = (A[m] . Q[n]) * scale[n] (vmlm_hip_gemm_nt_int8) with
 // a swizzled copy wsw of Q (launch_swizzle_w, N % 16 == 0) that the caller
 // keeps, read instead of Q where a kernel takes that layout; wsw may be null.

@@ -61,6 +61,9 @@ struct FxParams {
     int ldact;
     const float *radd;   // one segment: also z = radd + C (the EWADD after the
     float *zadd;         // GEMM), both [M][ldc] of segment 0
+    const float *norm_g; // NORM: the gain of the RMSNorm of the input rows,
+    float *norm_out;     // the normalized rows [M][K] (written by workgroup 0)
+    float norm_eps;
     int ldw;
     const float *X;      // [M][ldx]
     int ldx;
@@ -78,13 +81,16 @@ __device__ __forceinline__ float fx_w(const int8_t *W, int ldw, int K, int j, in
 
 // Row m . weight row j when row m holds a NaN or an infinity: NaN if a
 // product x * w is NaN or both infinities occur, else the infinity that
-// occurs; v (the q8 value) if no product is non-finite.
+// occurs; v (the q8 value) if no product is non-finite. With a gain gn the
+// row is the normalized one, (x * inv) * gn.
 template <bool RM>
-__device__ float fx_nonfinite(const FxParams &p, const int8_t *W, int m, int j, float v) {
+__device__ float fx_nonfinite(const FxParams &p, const int8_t *W, int m, int j, float v,
+                              float inv, const float *gn) {
     const float *x = p.X + (size_t)m * p.ldx;
     bool nan = false, pos = false, neg = false;
     for (int k = 0; k < p.K; ++k) {
-        const float t = x[k] * fx_w<RM>(W, p.ldw, p.K, j, k);
+        const float xk = gn ? x[k] * inv * gn[k] : x[k];
+        const float t = xk * fx_w<RM>(W, p.ldw, p.K, j, k);
         nan = nan || t != t;
         pos = pos || t == __builtin_inff();
         neg = neg || t == -__builtin_inff();
@@ -105,7 +111,13 @@ __device__ __forceinline__ void fx_tile(const FxParams &p, int tw, int t, int &s
     lt = gt - p.tstart[s];
 }
 
-template <int KB, int NW, int TW, bool RM>
+// With NORM the input row (M = 1) is first normalized (the RMSNORM opcode
+// before the GEMMs): its sum of squares is formed exactly as
+// rmsnorm_v4_kernel's 256 threads form it (thread t: float4 pieces t + 256 u;
+// the wave sums of its four waves, then (w0 + w1) + (w2 + w3)), wave w taking
+// that kernel's waves w, w + NW, ..., so inv and every y = (x * inv) * g are
+// that kernel's bits.
+template <int KB, int NW, int TW, bool RM, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     constexpr int RUN = KB * 64;        // k of a wave's run
     constexpr int PR = RUN / 4;         // 16-byte f32 pieces of a row's run
@@ -113,6 +125,7 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     constexpr int SLD = RUN + 16;       // padded LDS row of the terms (bytes)
     __shared__ __attribute__((aligned(16))) int8_t xs8[NW][Q8_T][FX_ROWS][SLD];
     __shared__ float red[TW][NW][16][17];
+    __shared__ float nsh[4];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -135,6 +148,29 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
                 xv[m][i] = *(const float4 *)(xrow + 4 * e);
             }
         }
+    }
+    // NORM: the gain at the run's pieces, and the whole row for the sum
+    // (four float4 pieces at most per thread of the 256-thread kernel: K <=
+    // 4096), for its waves wave + NW v
+    constexpr int VW = NORM ? (4 + NW - 1) / NW : 1;
+    float4 gv[NORM ? XI : 1];
+    float4 xn[VW][4];
+    const int n4 = p.K >> 2, nu = (n4 + 255) >> 8;
+    if constexpr (NORM) {
+        const float *grun = p.norm_g + (size_t)kb0 * 64;
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int e = lane + 64 * i < PR ? lane + 64 * i : PR - 1;
+            gv[i] = *(const float4 *)(grun + 4 * e);
+        }
+#pragma unroll
+        for (int v = 0; v < VW; ++v)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int vw = wave + NW * v, c = vw * 64 + lane + 256 * u;
+                xn[v][u] = vw < 4 && u < nu && c < n4 ? ((const float4 *)p.X)[c]
+                                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
     }
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wr[TW][KB];
@@ -168,6 +204,41 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     const float sc0 = p.seg[sg0].scale[row0 < p.seg[sg0].N ? row0 : p.seg[sg0].N - 1];
     const float sc1 = p.pair ? p.seg[1].scale[row0 < p.seg[1].N ? row0 : p.seg[1].N - 1] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
+
+    // NORM: the row's inv, the run normalized in place; workgroup 0 also
+    // writes the normalized row
+    float ninv = 0.0f;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int v = 0; v < VW; ++v) {
+            const int vw = wave + NW * v;
+            if (vw >= 4) continue;  // uniform
+            float ss = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (u >= nu) continue;
+                ss += xn[v][u].x * xn[v][u].x;
+                ss += xn[v][u].y * xn[v][u].y;
+                ss += xn[v][u].z * xn[v][u].z;
+                ss += xn[v][u].w * xn[v][u].w;
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) nsh[vw] = ss;
+        }
+        __syncthreads();
+        const float ss = ((nsh[0] + nsh[1]) + (nsh[2] + nsh[3])) / (float)p.K;
+        const float inv = 1.0f / sqrtf(ss + p.norm_eps);
+        ninv = inv;
+        float *orow = p.norm_out + (size_t)kb0 * 64;
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const float4 x = xv[0][i], gg = gv[i];
+            xv[0][i] = make_float4(x.x * inv * gg.x, x.y * inv * gg.y, x.z * inv * gg.z,
+                                   x.w * inv * gg.w);
+            if (blockIdx.x == 0 && lane + 64 * i < PR)
+                *(float4 *)(orow + 4 * (lane + 64 * i)) = xv[0][i];
+        }
+    }
 
     // 2. each row's run as int8 terms with the factor of its own maximum,
     // into the wave's LDS slot (read back below by this wave only: its LDS
@@ -253,7 +324,7 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
         float v = red[t][0][r][m];
 #pragma unroll
         for (int w = 1; w < NW; ++w) v += red[t][w][r][m];
-        if (v != v) v = fx_nonfinite<RM>(p, S.W, m, row, v);
+        if (v != v) v = fx_nonfinite<RM>(p, S.W, m, row, v, ninv, NORM ? p.norm_g : nullptr);
         v = v * scl;
         S.C[(size_t)m * S.ldc + row] = v;
         return v;
@@ -274,9 +345,9 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     }
 }
 
-template <int KB, int NW, int TW, bool RM>
+template <int KB, int NW, int TW, bool RM, bool NORM = false>
 int launch_fx_t(const FxParams &p, unsigned grid, hipStream_t st) {
-    fx_gemv_kernel<KB, NW, TW, RM><<<grid, NW * 64, 0, st>>>(p);
+    fx_gemv_kernel<KB, NW, TW, RM, NORM><<<grid, NW * 64, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
@@ -319,8 +390,32 @@ static int fx_seg_check(const FxSeg &S, bool swizzled, int ldw, int K) {
     return VMLM_OK;
 }
 
+// (blocks per run, waves) pairs with a normalizing kernel (swizzled weights):
+// the decoder programs' hidden sizes 2304 and 768
+#define FX_NORM_SHAPES(X) X(4, 9) X(4, 3)
+
+bool fx_norm_ok(int K) {
+    const int kb = fx_run_blocks(K), nw = kb ? K / 64 / kb : 0;
+#define FX_NHAS(KBV, NWV) \
+    if (kb == KBV && nw == NWV) return K % 4 == 0 && K <= 4096;
+    FX_NORM_SHAPES(FX_NHAS)
+#undef FX_NHAS
+    return false;
+}
+
 static int fx_dispatch(const FxParams &p, int kb, int nw, int tw, bool swizzled, unsigned grid,
                        hipStream_t st) {
+    if (p.norm_g) {
+#define FX_NLAUNCH(KBV, NWV)                                                   \
+    if (kb == KBV && nw == NWV && swizzled)                                    \
+        return tw == 2 ? launch_fx_t<KBV, NWV, 2, false, true>(p, grid, st)    \
+                       : launch_fx_t<KBV, NWV, 1, false, true>(p, grid, st);
+        FX_NORM_SHAPES(FX_NLAUNCH)
+#undef FX_NLAUNCH
+        return fail(VMLM_ERR_UNIMPL, "q8 GEMV: no normalizing kernel for K=%d (%d waves of %d "
+                                     "blocks, %s weights)", p.K, nw, kb,
+                    swizzled ? "swizzled" : "row-major");
+    }
 #define FX_LAUNCH(KBV, NWV)                                                    \
     if (kb == KBV && nw == NWV) {                                              \
         if (swizzled)                                                          \
@@ -368,6 +463,10 @@ int launch_fx_multi(const FxMultiArgs &a, hipStream_t st) {
                "q8 GEMV: 1..3 segments; a gate/up pair has two of one width");
     VMLM_GUARD(!a.zadd || (a.nseg == 1 && !pair && a.radd),
                "q8 GEMV: the residual add takes one segment and its addend");
+    VMLM_GUARD(!a.norm_g || (a.norm_out && a.M == 1 && a.K % 4 == 0 && a.K <= 4096 &&
+                             ((uintptr_t)a.norm_g & 15) == 0 && ((uintptr_t)a.norm_out & 15) == 0),
+               "q8 GEMV: the RMSNorm of the input takes one row of K <= 4096 (K %% 4 == 0), "
+               "a 16-byte aligned gain and output");
     FxParams p{};
     int tiles = 0;
     for (int i = 0; i < a.nseg; ++i) {
@@ -383,6 +482,9 @@ int launch_fx_multi(const FxMultiArgs &a, hipStream_t st) {
     p.ldact = a.ldact;
     p.radd = a.radd;
     p.zadd = a.zadd;
+    p.norm_g = a.norm_g;
+    p.norm_out = a.norm_out;
+    p.norm_eps = a.norm_eps;
     p.ldw = a.ldw;
     p.X = a.X;
     p.ldx = a.ldx;

@@ -669,6 +669,10 @@ struct VmFused {
     uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;  // scratch slots, in opcode order
     float **tab = nullptr;   // device: the nh K cache addresses, then the nh V
     VmColStream col[2];      // VF_COL_RUN: nh streams of `cols` steps
+    // VF_GEMMS / VF_GATE_UP after an RMSNORM of their input (start: the
+    // RMSNORM): its source rows, gain, epsilon scalar and normalized rows
+    bool norm = false;
+    uint32_t nx = 0, ng = 0, ne = 0, ny = 0;
 };
 
 // The part of a LOOP_CNT body from its first instruction up to the first
@@ -774,6 +778,8 @@ static int vm_audit(const vmlm_vm *vm) {
     }
     return VMLM_OK;
 }
+
+static uint32_t written_slot(const VmIns &in);
 
 // The loader's matcher for the decode loop's per-head runs (see
 // VmKvAppend, VmHeadAttn): every head's run must be the same opcodes over
@@ -964,7 +970,7 @@ static int vm_detect_fusions(vmlm_vm *vm) {
             }
         }
         // int8 GEMMs of one input at decode rows: two or three in a row (q/k/v),
-        // or gate, up, ACT silu of gate, EWMUL by up
+        // or gate, up, ACT silu of gate, EWMUL by up (the run at `at`)
         auto q8_gemm = [&](const VmIns &x, uint32_t A) {
             if (!(x.op == VOP_GEMM && x.fl == 0 && x.a == A && ok(x.b) && ok(x.dst) && ok(x.dt)))
                 return false;
@@ -974,63 +980,98 @@ static int vm_detect_fusions(vmlm_vm *vm) {
                    rows(x.dt) * cols(x.dt) >= nn && data(x.dst) &&
                    rows(x.dst) * cols(x.dst) >= m * nn;
         };
-        if (!f.kind && h0.op == VOP_GEMM && h0.fl == 0 && f32(h0.a) && rows(h0.a) >= 1 &&
-            rows(h0.a) <= (size_t)FX_ROWS && cols(h0.a) % 128 == 0 &&
-            fx_run_blocks((int)cols(h0.a)) && q8_gemm(h0, h0.a)) {
-            const uint32_t A = h0.a;
-            const size_t M = rows(A);
-            size_t j = 1;
-            while (j < 3 && i + j < n && !target[i + j] && q8_gemm(T[i + j], A)) ++j;
-            std::vector<uint32_t> dsts;
-            for (size_t t = 0; t < j; ++t) dsts.push_back(T[i + t].dst);
-            std::vector<uint32_t> reads = {A};
-            for (size_t t = 0; t < j; ++t) {
-                reads.push_back(T[i + t].b);
-                reads.push_back(T[i + t].dt);
-            }
-            const VmIns *g = &T[i];
-            const uint32_t gd = g[0].dst, ud = j >= 2 ? g[1].dst : 0;
-            const size_t N = vm->slots[g[0].b].rows;
-            const bool gate_up =
-                j >= 2 && i + 4 <= n && !target[i + 2] && !target[i + 3] &&
-                vm->slots[g[1].b].rows == N && g[2].op == VOP_ACT && g[2].fl == VMLM_ACT_SILU &&
-                g[2].a == gd && g[3].op == VOP_EWMUL && g[3].a == g[2].dst && g[3].b == ud &&
-                g[3].dst == g[2].dst && data(g[2].dst) && rows(g[2].dst) == M &&
-                cols(g[2].dst) == N && rows(gd) == M && cols(gd) == N && rows(ud) == M &&
-                cols(ud) == N;
-            if (gate_up) {
-                std::vector<uint32_t> w = {gd, ud, g[2].dst};
-                std::vector<uint32_t> r2 = {A, g[0].b, g[0].dt, g[1].b, g[1].dt};
-                if (disjoint(w, r2)) {
-                    f.kind = VF_GATE_UP;
-                    f.len = 4;
-                    f.nh = 2;
-                    f.att = g[2].dst;  // act
+        auto match_gemms = [&](size_t at, VmFused &f) {
+            const VmIns &h0 = T[at];
+            const size_t i = at;
+            if (!f.kind && h0.op == VOP_GEMM && h0.fl == 0 && f32(h0.a) && rows(h0.a) >= 1 &&
+                rows(h0.a) <= (size_t)FX_ROWS && cols(h0.a) % 128 == 0 &&
+                fx_run_blocks((int)cols(h0.a)) && q8_gemm(h0, h0.a)) {
+                const uint32_t A = h0.a;
+                const size_t M = rows(A);
+                size_t j = 1;
+                while (j < 3 && i + j < n && !target[i + j] && q8_gemm(T[i + j], A)) ++j;
+                std::vector<uint32_t> dsts;
+                for (size_t t = 0; t < j; ++t) dsts.push_back(T[i + t].dst);
+                std::vector<uint32_t> reads = {A};
+                for (size_t t = 0; t < j; ++t) {
+                    reads.push_back(T[i + t].b);
+                    reads.push_back(T[i + t].dt);
+                }
+                const VmIns *g = &T[i];
+                const uint32_t gd = g[0].dst, ud = j >= 2 ? g[1].dst : 0;
+                const size_t N = vm->slots[g[0].b].rows;
+                const bool gate_up =
+                    j >= 2 && i + 4 <= n && !target[i + 2] && !target[i + 3] &&
+                    vm->slots[g[1].b].rows == N && g[2].op == VOP_ACT && g[2].fl == VMLM_ACT_SILU &&
+                    g[2].a == gd && g[3].op == VOP_EWMUL && g[3].a == g[2].dst && g[3].b == ud &&
+                    g[3].dst == g[2].dst && data(g[2].dst) && rows(g[2].dst) == M &&
+                    cols(g[2].dst) == N && rows(gd) == M && cols(gd) == N && rows(ud) == M &&
+                    cols(ud) == N;
+                if (gate_up) {
+                    std::vector<uint32_t> w = {gd, ud, g[2].dst};
+                    std::vector<uint32_t> r2 = {A, g[0].b, g[0].dt, g[1].b, g[1].dt};
+                    if (disjoint(w, r2)) {
+                        f.kind = VF_GATE_UP;
+                        f.len = 4;
+                        f.nh = 2;
+                        f.att = g[2].dst;  // act
+                    }
+                }
+                if (!f.kind && j >= 2 && disjoint(dsts, reads)) {
+                    f.kind = VF_GEMMS;
+                    f.len = (uint32_t)j;
+                    f.nh = (uint32_t)j;
+                }
+                // one GEMM, then the residual EWADD of its output (z = r + y, the
+                // same shape, no broadcast): the GEMM's epilogue writes z too
+                const VmIns &e = T[i + 1];
+                if (!f.kind && j == 1 && i + 2 <= n && !target[i + 1] && e.op == VOP_EWADD &&
+                    e.fl == 0 && ok(e.a) && ok(e.b) && ok(e.dst) && (e.a == gd) != (e.b == gd)) {
+                    const uint32_t r = e.a == gd ? e.b : e.a, z = e.dst;
+                    const bool shp = rows(gd) == M && cols(gd) == N && rows(e.a) == M &&
+                                     cols(e.a) == N && rows(e.b) == M && cols(e.b) == N;
+                    if (shp && data(z) && f32(r) && rows(z) * cols(z) >= M * N &&
+                        disjoint({gd, z}, {A, g[0].b, g[0].dt, r})) {
+                        f.kind = VF_GEMM_ADD;
+                        f.len = 2;
+                        f.nh = 1;
+                        f.k = r;
+                        f.att = z;
+                    }
                 }
             }
-            if (!f.kind && j >= 2 && disjoint(dsts, reads)) {
-                f.kind = VF_GEMMS;
-                f.len = (uint32_t)j;
-                f.nh = (uint32_t)j;
+            return f.kind != 0;
+        };
+        // RMSNORM y <- x (gain g, epsilon e) of one row that feeds the GEMM
+        // run after it (the decoder's input and post-attention norms at
+        // decode): one launch that normalizes as the RMSNORM kernel does and
+        // also writes y. The RMSNORM's extents hold statically; y has x's
+        // shape, apart from x, g, e and the run's outputs.
+        if (!f.kind && h0.op == VOP_RMSNORM && i + 2 <= n && !target[i + 1] && ok(h0.dst) &&
+            ok(h0.a) && ok(h0.b) && ok(h0.dt)) {
+            const uint32_t x = h0.a, y = h0.dst, gn = h0.b, e = h0.dt;
+            VmFused fg;
+            const bool good =
+                match_gemms(i + 1, fg) && (fg.kind == VF_GEMMS || fg.kind == VF_GATE_UP) &&
+                T[i + 1].a == y && data(y) && f32(x) && f32(gn) && f32(e) &&
+                rows(e) * cols(e) >= 1 && rows(x) == 1 && rows(y) == 1 && cols(x) == cols(y) &&
+                rows(gn) * cols(gn) >= cols(x) && fx_norm_ok((int)cols(x));
+            std::vector<uint32_t> w = {y};  // each written slot once (ACT and EWMUL share one)
+            for (uint32_t t = 0; good && t < fg.len; ++t) {
+                const uint32_t ws_ = written_slot(T[i + 1 + t]);
+                if (std::find(w.begin(), w.end(), ws_) == w.end()) w.push_back(ws_);
             }
-            // one GEMM, then the residual EWADD of its output (z = r + y, the
-            // same shape, no broadcast): the GEMM's epilogue writes z too
-            const VmIns &e = T[i + 1];
-            if (!f.kind && j == 1 && i + 2 <= n && !target[i + 1] && e.op == VOP_EWADD &&
-                e.fl == 0 && ok(e.a) && ok(e.b) && ok(e.dst) && (e.a == gd) != (e.b == gd)) {
-                const uint32_t r = e.a == gd ? e.b : e.a, z = e.dst;
-                const bool shp = rows(gd) == M && cols(gd) == N && rows(e.a) == M &&
-                                 cols(e.a) == N && rows(e.b) == M && cols(e.b) == N;
-                if (shp && data(z) && f32(r) && rows(z) * cols(z) >= M * N &&
-                    disjoint({gd, z}, {A, g[0].b, g[0].dt, r})) {
-                    f.kind = VF_GEMM_ADD;
-                    f.len = 2;
-                    f.nh = 1;
-                    f.k = r;
-                    f.att = z;
-                }
+            if (good && disjoint(w, {x, gn, e})) {
+                f = fg;
+                f.norm = true;
+                f.len += 1;
+                f.nx = x;
+                f.ng = gn;
+                f.ne = e;
+                f.ny = y;
             }
         }
+        if (!f.kind) match_gemms(i, f);
         // cache writes of a prompt, column by column (p12_build_minicpm.py:
         // 794-840): P steps of SLICE c <- x at column xo + p, then WRITECOL
         // y <- c at column yo + p, for one stream or two interleaved. The run
@@ -1109,8 +1150,6 @@ static int vm_detect_fusions(vmlm_vm *vm) {
     }
     return VMLM_OK;
 }
-
-static uint32_t written_slot(const VmIns &in);
 
 // The graph segments (VmSeg): for every LOOP_CNT, its body from the jump
 // target up to the first opcode that needs the host between steps.
@@ -1317,6 +1356,14 @@ int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n) {
 int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n) {
     VMLM_GUARD(vm && n, "null argument");
     *n = vm->fused.size();
+    return VMLM_OK;
+}
+
+int vmlm_vm_fused_opcodes(const vmlm_vm *vm, size_t *n) {
+    VMLM_GUARD(vm && n, "null argument");
+    size_t c = 0;
+    for (const VmFused &f : vm->fused) c += f.len;
+    *n = c;
     return VMLM_OK;
 }
 
@@ -1874,17 +1921,18 @@ int Exec::step(const VmIns &in, size_t *ip) {
 
 extern "C" {
 
-// The slot an instruction writes: `dst`, or `a` for LOOP_CNT (its counter)
-// and STACK_INIT; UINT32_MAX for instructions that write no slot.
 // A run of int8 GEMMs over one input at decode rows in one launch
 // (launch_fx_multi); each GEMM as OP_GEMM gives it, and with the gate/up
-// pair the ACT silu and EWMUL after it. The swizzled copies are looked up as
-// OP_GEMM does (through the layer base); a run whose GEMMs are not all
-// swizzled or all row-major runs opcode by opcode.
+// pair the ACT silu and EWMUL after it; after an RMSNORM of the input, the
+// normalized rows (written to the RMSNORM's output too) as its kernel gives
+// them. The swizzled copies are looked up as OP_GEMM does (through the layer
+// base); a run whose GEMMs are not all swizzled or all row-major, or a
+// normalizing run over row-major weights, runs opcode by opcode.
 int Exec::fused_gemms(const VmFused &f) {
     int rc = VMLM_OK;
-    const VmIns *g = &vm->text[f.start];
-    const uint32_t A = g[0].a;
+    const VmIns *t0 = &vm->text[f.start];
+    const VmIns *g = t0 + (f.norm ? 1 : 0);  // the GEMMs (after the RMSNORM)
+    const uint32_t A = f.norm ? f.nx : g[0].a;  // the rows the kernel reads
     FxMultiArgs x;
     x.nseg = (int)f.nh;
     x.M = (int)rows(A);
@@ -1924,12 +1972,20 @@ int Exec::fused_gemms(const VmFused &f) {
     }
     bool aligned = ((uintptr_t)ca & 15) == 0;
     for (int t = 0; t < x.nseg; ++t) aligned = aligned && ((uintptr_t)x.seg[t].W & 15) == 0;
-    // mixed layouts, or operands OP_GEMM would not give this kernel: opcode
-    // by opcode
-    if ((nsw != 0 && nsw != x.nseg) || !aligned) {
+    if (f.norm) {  // the RMSNORM opcode's operands (its epsilon read as it reads it)
+        float *gp, *yp;
+        if ((rc = ptr(f.ng, &gp)) || (rc = ptr(f.ny, &yp)) || (rc = scalar(f.ne, &x.norm_eps)))
+            return rc;
+        x.norm_g = gp;
+        x.norm_out = yp;
+        aligned = aligned && ((uintptr_t)gp & 15) == 0 && ((uintptr_t)yp & 15) == 0;
+    }
+    // mixed layouts, operands OP_GEMM would not give this kernel, or a norm
+    // over row-major weights: opcode by opcode
+    if ((nsw != 0 && nsw != x.nseg) || !aligned || (f.norm && !x.swizzled)) {
         for (uint32_t t = 0; t < f.len; ++t) {
             size_t ip = f.start + t + 1;
-            if ((rc = step(g[t], &ip))) return rc;
+            if ((rc = step(t0[t], &ip))) return rc;
         }
         return VMLM_OK;
     }
@@ -2008,6 +2064,8 @@ int Exec::fused(const VmFused &f) {
     return VMLM_OK;
 }
 
+// The slot an instruction writes: `dst`, or `a` for LOOP_CNT (its counter)
+// and STACK_INIT; UINT32_MAX for instructions that write no slot.
 static uint32_t written_slot(const VmIns &in) {
     switch (in.op) {
     case VOP_SHAPE: case VOP_JMP: case VOP_CMPLE: case VOP_LAYERB: case VOP_PRINT:

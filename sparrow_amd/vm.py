@@ -83,6 +83,12 @@ class Vm:
         check(lib().vmlm_vm_fused_runs(self._h, C.byref(n)))
         return n.value
 
+    def fused_opcodes(self) -> int:
+        """Opcodes those runs cover."""
+        n = C.c_size_t()
+        check(lib().vmlm_vm_fused_opcodes(self._h, C.byref(n)))
+        return n.value
+
     def set_graphs(self, on: bool) -> None:
         """Replay loop bodies as HIP graphs (the default), or run every
         opcode one by one; the results are the same bits."""

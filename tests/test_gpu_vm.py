@@ -605,6 +605,77 @@ def test_vm_fused_gemm_add_runs(gvm, oracle, m):
         assert np.array_equal(bits(res[False]["z"]), bits(rv + res[False]["y"]))
 
 
+@pytest.mark.parametrize("k,inf", [(768, False), (2304, False), (2304, True)])
+def test_vm_fused_norm_gemm_runs(gvm, oracle, k, inf):
+    """An RMSNORM of one row followed by the GEMM run that reads it (q/k/v
+    GEMMs; gate, up, ACT silu, EWMUL) runs as that run's one launch, which
+    normalizes the row itself and also writes the RMSNORM's output: the
+    normalized row and every output are the bits of the opcodes run one by
+    one (a SHAPE after the RMSNORM keeps it out of the run), within 1e-4 RMS of the
+    oracle VM. With an infinite input value the normalized row is NaN there
+    and zero elsewhere, and every output NaN, as opcode by opcode."""
+    rng = np.random.default_rng(110 + k)
+    x = rng.standard_normal((1, k)).astype(np.float32) * 3
+    if inf:
+        x[0, 5] = np.inf
+    gain = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    ws = {n: rng.integers(-127, 128, size=(128, k), dtype=np.int8)
+          for n in ("q", "k", "v", "gate", "up")}
+    scs = {n: (np.abs(rng.normal(0, 0.02, 128)) / 127 + 1e-6).astype(np.float32) for n in ws}
+
+    def prog(split):
+        P = vmb.Program()
+        X = P.const("x", x)
+        G = P.const("g", gain)
+        E = P.scalar("eps", 1e-5)
+        P.act("y", 1, k)
+        P.act("y2", 1, k)
+        outs = {}
+        for name in ws:
+            outs[name] = (P.const(name, ws[name], "i8"),
+                          P.const(name + "_sc", scs[name], rows=128, cols=1))
+            P.act("o" + name, 1, 128)
+        P.act("a", 1, 128)
+        P.ins("RMSNORM", P["y"], X, G, dt=E)
+        if split:
+            P.ins("SHAPE", 0, 0, 0)
+        for name in ("q", "k", "v"):
+            P.ins("GEMM", P["o" + name], P["y"], outs[name][0], dt=outs[name][1])
+        P.ins("RMSNORM", P["y2"], X, G, dt=E)
+        if split:
+            P.ins("SHAPE", 0, 0, 0)
+        for name in ("gate", "up"):
+            P.ins("GEMM", P["o" + name], P["y2"], outs[name][0], dt=outs[name][1])
+        P.ins("ACT", P["a"], P["ogate"], fl=vmb.ACT["silu"])
+        P.ins("EWMUL", P["a"], P["a"], P["oup"])
+        P.ins("HALT")
+        return P
+
+    names = ["y", "y2", "oq", "ok", "ov", "ogate", "oup", "a"]
+    res = {}
+    for split in (False, True):
+        with gvm.Vm(prog(split).build()) as g:
+            # the q/k/v and gate/up runs either way, with the RMSNORMs unsplit
+            assert g.fused_runs() == 2
+            assert g.fused_opcodes() == (7 if split else 9)
+            g.run()
+            res[split] = {r: g.read(r) for r in names}
+    for r in names:
+        assert np.array_equal(bits(res[False][r]), bits(res[True][r])), r
+    if inf:  # inv = 1 / sqrt(inf) = 0: y is NaN at the infinity, +-0 elsewhere
+        for r in ("y", "y2"):
+            assert np.isnan(res[False][r][0, 5]) and np.all(res[False][r][0, 6:] == 0), r
+        for r in names[2:]:
+            assert np.all(np.isnan(res[False][r])), r
+        return
+    with oracle.OracleVm(prog(False).build()) as o:
+        o.run()
+        ref = {r: o.read(r) for r in names}
+    for r in names:
+        rms = np.sqrt(np.mean(ref[r].astype(np.float64) ** 2))
+        assert np.abs(res[False][r] - ref[r]).max() <= 1e-4 * rms, r
+
+
 @pytest.mark.parametrize("Q", [1, 2])
 def test_vm_col_runs(gvm, oracle, Q):
     """Column-by-column writes (SLICE a column of x, WRITECOL it into y; one
