@@ -755,9 +755,10 @@ def vm_step_loop(cfg, W, steps, base=2, prompt_len=128):
                 "GEMMs, per head SLICE/ROPE/TRANSPOSE/WRITECOL and GEMM/SCALE/SOFTMAX/GEMM, "
                 "then o, gate/up, ACT, EWMUL, down). The executor dispatches opcode by opcode, "
                 "except the runs it matched at load (fused_runs: per layer the cache append and "
-                "the attention over all heads, q/k/v, and gate/up with ACT and EWMUL, one launch "
-                "each; per layer and head the prompt's column-by-column K/V cache writes, two "
-                "strided copies; o and down with their residual EWADD, one launch each). The "
+                "the attention over all heads in one launch; q/k/v, and gate/up with ACT and "
+                "EWMUL, one launch each with the RMSNORM before them; per layer and head the "
+                "prompt's column-by-column K/V cache writes, two strided copies; o and down with "
+                "their residual EWADD, one launch each). The "
                 "loop body up to its PRINT is captured into a HIP graph on its second step and "
                 "replayed after (graph_segments). The rate is the difference of two programs' "
                 "run times",

@@ -295,15 +295,36 @@ constexpr int VM_ATTN_MAX_COLS = 8192;
 // is loaded before the query is rotated (none depends on it), so the
 // workgroup waits for memory once instead of once per phase; the sums run in
 // the same order, so the results are the same bits.
-template <bool FAST>
-__global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh, int *guard) {
+// APPEND (with FAST): the cache append of the same heads first (the append
+// run just before the attention run, over the same caches): the workgroup
+// writes its head's new K / V column as vm_kv_append_kernel does and uses
+// the values it wrote in place of the ones it loaded from that column.
+template <bool FAST, bool APPEND = false>
+__global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh, int *guard,
+                                                           VmKvAppend ap = {}) {
     extern __shared__ float sm[];     // q[hd], p[cols]
     __shared__ float red[4];
+    __shared__ float knew[APPEND ? 64 : 1], vnew[APPEND ? 64 : 1];
     float *qs = sm, *pr = sm + a.hd;
     const int h = blockIdx.x, half = a.hd / 2, tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63;
     const float *K = a.kc[h], *V = a.kc[nh + h];
     float kv[FAST ? 64 : 1], vv[FAST ? 16 : 1][FAST ? 4 : 1];
+    static_assert(FAST || !APPEND, "the append joins the FAST form");
+    // APPEND: the position and the new k / v values are read before the
+    // cache rows, so they arrive first
+    long apos = -1, col = -1;
+    float ax1 = 0.0f, ax2 = 0.0f, avx = 0.0f;
+    if constexpr (APPEND) {
+        apos = dev_index(ap.posp, 1L << 24, guard);
+        col = dev_index(ap.posp, (long)ap.cols + 1, guard);
+        if (tid < 32) {
+            ax1 = ap.k[(size_t)h * 64 + tid];
+            ax2 = ap.k[(size_t)h * 64 + tid + 32];
+        } else if (tid >= 64 && tid < 128) {
+            avx = ap.v[(size_t)h * 64 + tid - 64];
+        }
+    }
     if constexpr (FAST) {
         // column tid of every K row; columns lane + 64 i of V rows w + 4 j
 #pragma unroll
@@ -315,6 +336,58 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
                 const int c = lane + 64 * i;
                 vv[j][i] = c < a.cols ? V[(size_t)(w + 4 * j) * a.cols + c] : 0.0f;
             }
+    }
+    if constexpr (APPEND) {
+        // vm_kv_append_kernel's work for this head (hd = 64), the new column
+        // also kept in LDS
+        const bool wr = col >= 0 && col + 1 <= ap.cols;
+        if (col >= 0 && !wr && tid == 0) atomicOr(guard, 1);
+        const bool lastk = h == nh - 1;
+        float *kc = ap.kc[h], *vc = ap.kc[nh + h];
+        if (tid < 32) {
+            const float x1 = ax1, x2 = ax2;
+            if (lastk) {
+                ap.kdh[tid] = x1;
+                ap.kdh[tid + 32] = x2;
+            }
+            if (apos >= 0) {
+                float y1, y2;
+                rope_pair(x1, x2, (float)apos, tid, ap.step, &y1, &y2);
+                if (lastk) {
+                    ap.kdrot[tid] = y1;
+                    ap.kdrot[tid + 32] = y2;
+                    ap.kdT[tid] = y1;
+                    ap.kdT[tid + 32] = y2;
+                }
+                if (wr) {
+                    kc[(size_t)tid * ap.cols + col] = y1;
+                    kc[(size_t)(tid + 32) * ap.cols + col] = y2;
+                }
+                knew[tid] = y1;
+                knew[tid + 32] = y2;
+            }
+        } else if (tid >= 64 && tid < 128) {
+            const int i = tid - 64;
+            const float x = avx;
+            if (lastk) {
+                ap.vdh[i] = x;
+                ap.vdT[i] = x;
+            }
+            if (apos >= 0 && wr) vc[(size_t)i * ap.cols + col] = x;
+            vnew[i] = x;
+        }
+        __syncthreads();
+        if (apos >= 0 && wr) {  // the column as the append wrote it
+            if (tid == col) {
+#pragma unroll
+                for (int k = 0; k < 64; ++k) kv[k] = knew[k];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (lane + 64 * i == col) vv[j][i] = vnew[w + 4 * j];
+        }
     }
     const long pos = dev_index(a.posp, 1L << 24, guard);
     const long live = dev_index(a.livep, (long)a.cols + 1, guard);
@@ -653,7 +726,8 @@ struct VmSlot {
 // runs: vm_kv_append_kernel, vm_head_attn_kernel; GEMMs of one input), or as
 // one strided copy per stream (VF_COL_RUN: column-by-column cache writes).
 enum VmFuseKind {
-    VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4, VF_COL_RUN = 5, VF_GEMM_ADD = 6
+    VF_KV_APPEND = 1, VF_HEAD_ATTN = 2, VF_GEMMS = 3, VF_GATE_UP = 4, VF_COL_RUN = 5, VF_GEMM_ADD = 6,
+    VF_KV_ATTN = 7  // a cache append run and the attention run after it
 };
 struct VmColStream {
     uint32_t c, x, y;   // the column slot, the slot sliced, the slot written
@@ -673,6 +747,10 @@ struct VmFused {
     // RMSNORM): its source rows, gain, epsilon scalar and normalized rows
     bool norm = false;
     uint32_t nx = 0, ng = 0, ne = 0, ny = 0;
+    std::vector<uint32_t> cslots;  // per-head runs: the cache slots in `tab`
+    // VF_KV_ATTN: the attention run's q, live width, scale, output rows and
+    // scratch slots (the append run's operands in the fields above)
+    uint32_t aq = 0, alive = 0, ascale = 0, aatt = 0, a0 = 0, a1 = 0, a2 = 0, a3 = 0;
 };
 
 // The part of a LOOP_CNT body from its first instruction up to the first
@@ -1141,12 +1219,40 @@ static int vm_detect_fusions(vmlm_vm *vm) {
             const VmSlot &sl = vm->slots[c];
             addr.push_back((float *)((sl.kind == VSLOT_STATE ? vm->state : vm->act) + sl.off));
         }
+        f.cslots = caches;
         VMLM_HIP_CHECK(hipMalloc((void **)&f.tab, addr.size() * sizeof(float *)));
         vm->fused.push_back(f);  // freed with the VM from here on
         VMLM_HIP_CHECK(hipMemcpy(f.tab, addr.data(), addr.size() * sizeof(float *),
                                  hipMemcpyHostToDevice));
         vm->fuse_at[i] = (int32_t)vm->fused.size() - 1;
         i += f.len;
+    }
+    // A layer's cache append run and the attention run right after it, over
+    // the same caches, position and theta (hd = 64, at most 256 columns): one
+    // launch, each head's workgroup appending before it attends. The slots
+    // either run writes stay apart from those the other reads (the caches
+    // aside: the attention uses the column the append wrote).
+    for (size_t r = 0; r + 1 < vm->fused.size(); ++r) {
+        VmFused &a = vm->fused[r], &b = vm->fused[r + 1];
+        if (a.kind != VF_KV_APPEND || b.kind != VF_HEAD_ATTN || b.start != a.start + a.len ||
+            target[b.start] || a.nh != b.nh || a.hd != 64 || b.hd != 64 || a.cols != b.cols ||
+            b.cols > 256 || a.pos != b.pos || a.theta != b.theta || a.cslots != b.cslots)
+            continue;
+        if (!disjoint({a.s0, a.s1, a.s2, a.s3, a.s4, b.s0, b.s1, b.s2, b.s3, b.att},
+                      {a.k, a.v, a.theta, a.pos, b.k, b.scale, b.live}))
+            continue;
+        a.kind = VF_KV_ATTN;
+        a.len += b.len;
+        a.aq = b.k;
+        a.alive = b.live;
+        a.ascale = b.scale;
+        a.aatt = b.att;
+        a.a0 = b.s0;
+        a.a1 = b.s1;
+        a.a2 = b.s2;
+        a.a3 = b.s3;
+        vm->fuse_at[b.start] = -1;
+        b.kind = 0;  // no longer run (its table is freed with the VM)
     }
     return VMLM_OK;
 }
@@ -1355,14 +1461,16 @@ int vmlm_vm_swizzled_consts(const vmlm_vm *vm, size_t *n) {
 
 int vmlm_vm_fused_runs(const vmlm_vm *vm, size_t *n) {
     VMLM_GUARD(vm && n, "null argument");
-    *n = vm->fused.size();
+    size_t c = 0;
+    for (const VmFused &f : vm->fused) c += f.kind != 0;
+    *n = c;
     return VMLM_OK;
 }
 
 int vmlm_vm_fused_opcodes(const vmlm_vm *vm, size_t *n) {
     VMLM_GUARD(vm && n, "null argument");
     size_t c = 0;
-    for (const VmFused &f : vm->fused) c += f.len;
+    for (const VmFused &f : vm->fused) c += f.kind ? f.len : 0;
     *n = c;
     return VMLM_OK;
 }
@@ -2014,34 +2122,39 @@ int Exec::fused(const VmFused &f) {
     VMLM_GUARD(theta > 0.0f, "ROPE: theta must be > 0");
     const float step = -2.0f / (float)f.hd * host_ln_f(theta);
     hipStream_t st = vm->st;
-    if (f.kind == VF_KV_APPEND) {
-        VmKvAppend a;
+    VmKvAppend ap{};
+    if (f.kind == VF_KV_APPEND || f.kind == VF_KV_ATTN) {
         float *k, *v, *pp, *s0, *s1, *s2, *s3, *s4;
         if ((rc = ptr(f.k, &k)) || (rc = ptr(f.v, &v)) || (rc = ptr(f.pos, &pp)) ||
             (rc = ptr(f.s0, &s0)) || (rc = ptr(f.s1, &s1)) || (rc = ptr(f.s2, &s2)) ||
             (rc = ptr(f.s3, &s3)) || (rc = ptr(f.s4, &s4)))
             return rc;
-        a.k = k;
-        a.v = v;
-        a.kc = f.tab;
-        a.posp = pp;
-        a.step = step;
-        a.hd = (int)f.hd;
-        a.cols = (int)f.cols;
-        a.kdh = s0;
-        a.vdh = s1;
-        a.kdrot = s2;
-        a.kdT = s3;
-        a.vdT = s4;
-        vm_kv_append_kernel<<<f.nh, 64, 0, st>>>(a, (int)f.nh, guard);
+        ap.k = k;
+        ap.v = v;
+        ap.kc = f.tab;
+        ap.posp = pp;
+        ap.step = step;
+        ap.hd = (int)f.hd;
+        ap.cols = (int)f.cols;
+        ap.kdh = s0;
+        ap.vdh = s1;
+        ap.kdrot = s2;
+        ap.kdT = s3;
+        ap.vdT = s4;
+    }
+    if (f.kind == VF_KV_APPEND) {
+        vm_kv_append_kernel<<<f.nh, 64, 0, st>>>(ap, (int)f.nh, guard);
         VMLM_HIP_CHECK(hipGetLastError());
         return VMLM_OK;
     }
+    const bool joined = f.kind == VF_KV_ATTN;
     VmHeadAttn a;
     float *q, *pp, *lp, *sp, *att, *s0, *s1, *s2, *s3;
-    if ((rc = ptr(f.k, &q)) || (rc = ptr(f.pos, &pp)) || (rc = ptr(f.live, &lp)) ||
-        (rc = ptr(f.scale, &sp)) || (rc = ptr(f.att, &att)) || (rc = ptr(f.s0, &s0)) ||
-        (rc = ptr(f.s1, &s1)) || (rc = ptr(f.s2, &s2)) || (rc = ptr(f.s3, &s3)))
+    if ((rc = ptr(joined ? f.aq : f.k, &q)) || (rc = ptr(f.pos, &pp)) ||
+        (rc = ptr(joined ? f.alive : f.live, &lp)) || (rc = ptr(joined ? f.ascale : f.scale, &sp)) ||
+        (rc = ptr(joined ? f.aatt : f.att, &att)) || (rc = ptr(joined ? f.a0 : f.s0, &s0)) ||
+        (rc = ptr(joined ? f.a1 : f.s1, &s1)) || (rc = ptr(joined ? f.a2 : f.s2, &s2)) ||
+        (rc = ptr(joined ? f.a3 : f.s3, &s3)))
         return rc;
     a.q = q;
     a.kc = f.tab;
@@ -2056,7 +2169,10 @@ int Exec::fused(const VmFused &f) {
     a.qdrot = s1;
     a.scd = s2;
     a.ctxd = s3;
-    if (f.hd == 64 && f.cols <= 256)
+    if (joined)
+        vm_head_attn_kernel<true, true><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(
+            a, (int)f.nh, guard, ap);
+    else if (f.hd == 64 && f.cols <= 256)
         vm_head_attn_kernel<true><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
     else
         vm_head_attn_kernel<false><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);

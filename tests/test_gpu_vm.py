@@ -401,10 +401,10 @@ def test_vm_fused_head_runs(gvm, oracle, tiny):
     approx += [f"st_kc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     approx += [f"st_vc{l}_{h}" for l in (0, nl - 1) for h in (0, nh - 1)]
     with gvm.Vm(img) as g:
-        # per layer: the cache append, the attention, q/k/v, gate/up, o and
-        # down each with its residual add, and the prompt's column-by-column
-        # cache writes of every head
-        assert g.fused_runs() == 6 * nl + nl * nh
+        # per layer: the cache append with the attention, q/k/v, gate/up,
+        # o and down each with its residual add, and the prompt's
+        # column-by-column cache writes of every head
+        assert g.fused_runs() == 5 * nl + nl * nh
         g.write("st_tok", prompt)
         g.write("st_gen", [11])
         g.run()
@@ -490,19 +490,21 @@ def test_vm_fused_gemm_runs(gvm, oracle, m):
     assert np.abs(y100 - r100).max() <= 1e-4 * rms
 
 
-def test_vm_fused_runs_guard(gvm):
+@pytest.mark.parametrize("hd,nh,C", [(8, 2, 6), (64, 3, 40)])
+def test_vm_fused_runs_guard(gvm, hd, nh, C):
     """Fused runs over exact inputs (constant rows): the rotated and copied
     slots and the caches equal the oracle VM bitwise, the attention rows are
     within 1e-4 RMS. A fused run keeps its opcodes' device guards: a
     position past the cache (WRITECOL's runtime column) and a live width
     past the scores (SOFTMAX) trip the VM's guard (status 9), as opcode by
-    opcode."""
+    opcode. At hd = 64 the append and the attention run as one launch, with
+    the bits of the two runs launched apart (a SHAPE between them)."""
     rng = np.random.default_rng(2)
-    hd, nh, C = 8, 2, 6
+    xv = rng.standard_normal((1, nh * hd)).astype(np.float32)
 
-    def prog(pos, live):
+    def prog(pos, live, split=False):
         P = vmb.Program()
-        x = P.const("x", rng.standard_normal((1, nh * hd)).astype(np.float32))
+        x = P.const("x", xv)
         th = P.scalar("theta", 10000.0)
         sc = P.scalar("sc", 0.5)
         pp = P.scalar("pos", float(pos))
@@ -523,6 +525,8 @@ def test_vm_fused_runs_guard(gvm):
             P.ins("TRANSPOSE", P["vT"], P["vh"])
             P.ins("WRITECOL", P[f"kc{h}"], P["kT"], 0, dt=pp, fl=rt)
             P.ins("WRITECOL", P[f"vc{h}"], P["vT"], 0, dt=pp, fl=rt)
+        if split:
+            P.ins("SHAPE", 0, 0, 0)
         for h in range(nh):
             P.ins("SLICE", P["qh"], x, h * hd)
             P.ins("ROPE", P["qr"], P["qh"], th, dt=pp, fl=rt)
@@ -538,9 +542,15 @@ def test_vm_fused_runs_guard(gvm):
     img = prog(2, 3).build()
     exact = ["kh", "vh", "kr", "kT", "vT", "qh", "qr", "kc0", "kc1", "vc0", "vc1"]
     with gvm.Vm(img) as g:
-        assert g.fused_runs() == 2
+        assert g.fused_runs() == (1 if hd == 64 else 2)
         g.run()
         got = {r: g.read(r) for r in exact + ["att", "s", "ctx"]}
+    if hd == 64:
+        with gvm.Vm(prog(2, 3, split=True).build()) as g:
+            assert g.fused_runs() == 2
+            g.run()
+            for r in exact + ["att", "s", "ctx"]:
+                assert np.array_equal(bits(got[r]), bits(g.read(r))), r
     with orc.OracleVm(img) as o:
         o.run()
         ref = {r: o.read(r) for r in exact + ["att", "s", "ctx"]}
