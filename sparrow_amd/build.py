@@ -27,9 +27,15 @@ COMMON = [
 ]
 
 
+# Per-file flags. k_gemm.hip: MFMA accumulators in arch VGPRs rather than
+# AGPRs (the 16 x 16 products issue at about half rate with AGPR
+# accumulators on gfx950; config 1's bf16 GEMM 5.73 -> 5.42 us)
+EXTRA = {"k_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                     if "packed-fp32-ops" not in l)
