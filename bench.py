@@ -417,7 +417,7 @@ def run_suite(iters, cpu=True):
         cfg0["cpu_threads"] = orc.get_threads()
     cfg0["M16"]["kernel_only"] = profiled_kernel_us("gemv_wide_kernel<3, false, 2, 8, true>",
                                                     "gemv_reduce_kernel")
-    cfg0["M1"]["kernel_only"] = profiled_kernel_us("fx_gemv_kernel<4, 9, 1, true>")
+    cfg0["M1"]["kernel_only"] = profiled_kernel_us("fx_gemv_kernel<4, 9, 1, true, false>")
     out["cfg0_q8_gemm"] = cfg0
     # config 1: bf16 A[1024,512] . B[512,2048] (B passed as its [2048,512] transpose)
     rng = np.random.default_rng(1)
