@@ -299,17 +299,29 @@ constexpr int VM_ATTN_MAX_COLS = 8192;
 // run just before the attention run, over the same caches): the workgroup
 // writes its head's new K / V column as vm_kv_append_kernel does and uses
 // the values it wrote in place of the ones it loaded from that column.
-template <bool FAST, bool APPEND = false>
+// NP > 1 (with FAST): NP workgroups per head, each forming the head's
+// scores and softmax (the same bits in each) and the context rows of its
+// part, 64 / NP of them; workgroup b takes head 8 (b / 32) + b % 8, part
+// (b / 8) % 4, so a head's workgroups share an XCD (and its L2). Part 0
+// writes the scratch slots and the appended column.
+template <bool FAST, bool APPEND = false, int NP = 1>
 __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh, int *guard,
                                                            VmKvAppend ap = {}) {
     extern __shared__ float sm[];     // q[hd], p[cols]
     __shared__ float red[4];
     __shared__ float knew[APPEND ? 64 : 1], vnew[APPEND ? 64 : 1];
+    static_assert(NP == 1 || (FAST && NP == 4), "parts of the FAST form: 4");
+    constexpr int VR = FAST ? 16 / NP : 1;  // V rows per wave
     float *qs = sm, *pr = sm + a.hd;
-    const int h = blockIdx.x, half = a.hd / 2, tid = threadIdx.x;
+    const int bx = (int)blockIdx.x;
+    const int h = NP > 1 ? ((bx >> 5) << 3) | (bx & 7) : bx, part = NP > 1 ? (bx >> 3) & 3 : 0;
+    if (h >= nh) return;  // the grid's last group of 8 heads may be partial
+    const int half = a.hd / 2, tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63;
+    const int rbase = part * (64 / NP);     // this workgroup's first context row
+    const bool p0 = part == 0;
     const float *K = a.kc[h], *V = a.kc[nh + h];
-    float kv[FAST ? 64 : 1], vv[FAST ? 16 : 1][FAST ? 4 : 1];
+    float kv[FAST ? 64 : 1], vv[VR][FAST ? 4 : 1];
     static_assert(FAST || !APPEND, "the append joins the FAST form");
     // APPEND: the position and the new k / v values are read before the
     // cache rows, so they arrive first
@@ -330,11 +342,11 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
 #pragma unroll
         for (int k = 0; k < 64; ++k) kv[k] = tid < a.cols ? K[(size_t)k * a.cols + tid] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
+        for (int j = 0; j < VR; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int c = lane + 64 * i;
-                vv[j][i] = c < a.cols ? V[(size_t)(w + 4 * j) * a.cols + c] : 0.0f;
+                vv[j][i] = c < a.cols ? V[(size_t)(rbase + w + 4 * j) * a.cols + c] : 0.0f;
             }
     }
     if constexpr (APPEND) {
@@ -342,7 +354,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         // also kept in LDS
         const bool wr = col >= 0 && col + 1 <= ap.cols;
         if (col >= 0 && !wr && tid == 0) atomicOr(guard, 1);
-        const bool lastk = h == nh - 1;
+        const bool lastk = h == nh - 1 && p0;
         float *kc = ap.kc[h], *vc = ap.kc[nh + h];
         if (tid < 32) {
             const float x1 = ax1, x2 = ax2;
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
                     ap.kdT[tid] = y1;
                     ap.kdT[tid + 32] = y2;
                 }
-                if (wr) {
+                if (wr && p0) {
                     kc[(size_t)tid * ap.cols + col] = y1;
                     kc[(size_t)(tid + 32) * ap.cols + col] = y2;
                 }
@@ -373,7 +385,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
                 ap.vdh[i] = x;
                 ap.vdT[i] = x;
             }
-            if (apos >= 0 && wr) vc[(size_t)i * ap.cols + col] = x;
+            if (apos >= 0 && wr && p0) vc[(size_t)i * ap.cols + col] = x;
             vnew[i] = x;
         }
         __syncthreads();
@@ -383,16 +395,17 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
                 for (int k = 0; k < 64; ++k) kv[k] = knew[k];
             }
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
+            for (int j = 0; j < VR; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (lane + 64 * i == col) vv[j][i] = vnew[w + 4 * j];
+                    if (lane + 64 * i == col) vv[j][i] = vnew[rbase + w + 4 * j];
         }
     }
     const long pos = dev_index(a.posp, 1L << 24, guard);
     const long live = dev_index(a.livep, (long)a.cols + 1, guard);
     if (pos < 0 || live < 0) return;
     const bool last = h == nh - 1;
+    const bool lastp0 = last && p0;  // the scratch slots, from part 0
     const float *qr = a.q + (size_t)h * a.hd;
     for (int i = tid; i < half; i += 256) {
         const float x1 = qr[i], x2 = qr[i + half];
@@ -400,7 +413,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         rope_pair(x1, x2, (float)pos, i, a.step, &y1, &y2);
         qs[i] = y1;
         qs[i + half] = y2;
-        if (last) {
+        if (lastp0) {
             a.qdh[i] = x1;
             a.qdh[i + half] = x2;
             a.qdrot[i] = y1;
@@ -446,7 +459,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
     for (int i = tid; i < lim; i += 256) pr[i] *= inv;
     for (int i = lim + tid; i < a.cols; i += 256) pr[i] = 0.0f;
     __syncthreads();
-    if (last)
+    if (lastp0)
         for (int i = tid; i < a.cols; i += 256) a.scd[i] = pr[i];
     // context: wave w takes rows w, w + 4, ...; its lanes sum columns in
     // order per lane, then the wave sums its lanes
@@ -459,12 +472,12 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
     };
     if constexpr (FAST) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < VR; ++j) {
             float t = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (lane + 64 * i < a.cols) t += pr[lane + 64 * i] * vv[j][i];
-            store(w + 4 * j, t);
+            store(rbase + w + 4 * j, t);
         }
     } else {
         for (int r = w; r < a.hd; r += 4) {
@@ -2169,11 +2182,14 @@ int Exec::fused(const VmFused &f) {
     a.qdrot = s1;
     a.scd = s2;
     a.ctxd = s3;
+    // the FAST form over four workgroups per head (groups of 8 heads)
+    const unsigned g4 = (f.nh + 7) / 8 * 32;
     if (joined)
-        vm_head_attn_kernel<true, true><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(
+        vm_head_attn_kernel<true, true, 4><<<g4, 256, (f.hd + f.cols) * sizeof(float), st>>>(
             a, (int)f.nh, guard, ap);
     else if (f.hd == 64 && f.cols <= 256)
-        vm_head_attn_kernel<true><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
+        vm_head_attn_kernel<true, false, 4><<<g4, 256, (f.hd + f.cols) * sizeof(float), st>>>(
+            a, (int)f.nh, guard);
     else
         vm_head_attn_kernel<false><<<f.nh, 256, (f.hd + f.cols) * sizeof(float), st>>>(a, (int)f.nh, guard);
     VMLM_HIP_CHECK(hipGetLastError());
