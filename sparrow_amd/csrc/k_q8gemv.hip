@@ -99,6 +99,48 @@ __device__ float fx_nonfinite(const FxParams &p, const int8_t *W, int m, int j, 
     return pos ? __builtin_inff() : neg ? -__builtin_inff() : v;
 }
 
+// Segment s, where s may differ between lanes: every field is selected from
+// the three segments' scalar copies, so the kernel arguments are never read
+// with a vector load (whose wait would also wait for every weight load
+// issued before it).
+// a load and a store through global pointers the compiler can no longer
+// prove global (after in_sgpr): global, not flat, instructions, so the
+// memory-counter waits before them stay exact
+__device__ __forceinline__ float ld_g(const float *q) {
+    return *(const __attribute__((address_space(1))) float *)q;
+}
+__device__ __forceinline__ void st_g(float *q, float v) {
+    *(__attribute__((address_space(1))) float *)q = v;
+}
+template <class T>
+__device__ __forceinline__ T in_sgpr(T v) {  // an opaque scalar: selects stay selects of values
+    asm volatile("" : "+s"(v));
+    return v;
+}
+__device__ __forceinline__ FxSeg fx_seg(const FxParams &p, int s) {
+    FxSeg r;
+    r.W = in_sgpr(p.seg[0].W);
+    r.scale = in_sgpr(p.seg[0].scale);
+    r.C = in_sgpr(p.seg[0].C);
+    r.N = in_sgpr(p.seg[0].N);
+    r.ldc = in_sgpr(p.seg[0].ldc);
+#pragma unroll
+    for (int i = 1; i < 3; ++i) {
+        const int8_t *w = in_sgpr(p.seg[i].W);
+        const float *sc = in_sgpr(p.seg[i].scale);
+        float *c = in_sgpr(p.seg[i].C);
+        const int n = in_sgpr(p.seg[i].N), ld = in_sgpr(p.seg[i].ldc);
+        if (s == i) {
+            r.W = w;
+            r.scale = sc;
+            r.C = c;
+            r.N = n;
+            r.ldc = ld;
+        }
+    }
+    return r;
+}
+
 // The segment and the tile within it of this workgroup's tile t (uniform).
 __device__ __forceinline__ void fx_tile(const FxParams &p, int tw, int t, int &s, int &lt) {
     if (p.pair) {
@@ -108,7 +150,8 @@ __device__ __forceinline__ void fx_tile(const FxParams &p, int tw, int t, int &s
     }
     const int gt = blockIdx.x * tw + t;
     s = p.nseg > 2 && gt >= p.tstart[2] ? 2 : p.nseg > 1 && gt >= p.tstart[1] ? 1 : 0;
-    lt = gt - p.tstart[s];
+    const int t0 = in_sgpr(p.tstart[0]), t1 = in_sgpr(p.tstart[1]), t2 = in_sgpr(p.tstart[2]);
+    lt = gt - (s == 2 ? t2 : s == 1 ? t1 : t0);  // selects of scalar copies
 }
 
 // With NORM the input row (M = 1) is first normalized (the RMSNORM opcode
@@ -201,7 +244,8 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
     int sg0, lt0;
     fx_tile(p, TW, e0 / (16 * M), sg0, lt0);
     const int row0 = lt0 * 16 + (e0 & 15);
-    const float sc0 = p.seg[sg0].scale[row0 < p.seg[sg0].N ? row0 : p.seg[sg0].N - 1];
+    const FxSeg S0 = fx_seg(p, sg0);
+    const float sc0 = ld_g(S0.scale + (row0 < S0.N ? row0 : S0.N - 1));
     const float sc1 = p.pair ? p.seg[1].scale[row0 < p.seg[1].N ? row0 : p.seg[1].N - 1] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
 
@@ -326,17 +370,17 @@ __global__ __launch_bounds__(NW * 64) void fx_gemv_kernel(FxParams p) {
         for (int w = 1; w < NW; ++w) v += red[t][w][r][m];
         if (v != v) v = fx_nonfinite<RM>(p, S.W, m, row, v, ninv, NORM ? p.norm_g : nullptr);
         v = v * scl;
-        S.C[(size_t)m * S.ldc + row] = v;
+        st_g(S.C + (size_t)m * S.ldc + row, v);
         return v;
     };
     for (int e = tid; e < nout; e += NW * 64) {
         const int t = e / (16 * M), m = (e >> 4) % M, r = e & 15;
         int sg, lt;
         fx_tile(p, TW, t, sg, lt);
-        const FxSeg &S = p.seg[sg];
+        const FxSeg S = fx_seg(p, sg);
         const int row = lt * 16 + r;
         if (row >= S.N) continue;
-        const float v = tile_out(t, m, r, row, S, e == tid ? sc0 : S.scale[row]);
+        const float v = tile_out(t, m, r, row, S, e == tid ? sc0 : ld_g(S.scale + row));
         if (p.zadd) p.zadd[(size_t)m * S.ldc + row] = p.radd[(size_t)m * S.ldc + row] + v;
         if (p.pair) {  // t == 0: the gate; the up value of the same output
             const float u = tile_out(1, m, r, row, p.seg[1], e == tid ? sc1 : p.seg[1].scale[row]);
