@@ -226,6 +226,8 @@ __global__ void vm_emb_f32_kernel(float *d, const float *table, size_t rows, siz
 // holding the last head's values as the opcode run leaves them. The score
 // and context dot products are f32 sums in k order (the GEMM kernel's
 // order differs; both are within the GEMM contract).
+typedef __attribute__((address_space(1))) float gfloat;  // a float in global memory
+
 struct VmKvAppend {
     const float *k, *v;          // [1, nh * hd] rows of k and v
     float *const *kc;            // [nh] caches [hd, cols] (K), then [nh] (V)
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(64) void vm_kv_append_kernel(VmKvAppend a, int nh, 
     const bool wr = col >= 0 && col + 1 <= a.cols;
     if (col >= 0 && !wr) atomicOr(guard, 1);
     const float *kr = a.k + (size_t)h * a.hd, *vr = a.v + (size_t)h * a.hd;
-    float *kc = a.kc[h], *vc = a.kc[nh + h];
+    gfloat *kc = (gfloat *)a.kc[h], *vc = (gfloat *)a.kc[nh + h];  // global (from a device table)
     const bool last = h == nh - 1;
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const float x1 = kr[i], x2 = kr[i + half];
@@ -320,7 +322,10 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
     const int w = tid >> 6, lane = tid & 63;
     const int rbase = part * (64 / NP);     // this workgroup's first context row
     const bool p0 = part == 0;
-    const float *K = a.kc[h], *V = a.kc[nh + h];
+    // the cache addresses come from a device table, so the compiler cannot
+    // tell they are global: global pointers keep the loads global (flat
+    // loads would make every counter wait drain the LDS traffic too)
+    const gfloat *K = (const gfloat *)a.kc[h], *V = (const gfloat *)a.kc[nh + h];
     float kv[FAST ? 64 : 1], vv[VR][FAST ? 4 : 1];
     static_assert(FAST || !APPEND, "the append joins the FAST form");
     // APPEND: the position and the new k / v values are read before the
@@ -355,7 +360,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         const bool wr = col >= 0 && col + 1 <= ap.cols;
         if (col >= 0 && !wr && tid == 0) atomicOr(guard, 1);
         const bool lastk = h == nh - 1 && p0;
-        float *kc = ap.kc[h], *vc = ap.kc[nh + h];
+        gfloat *kc = (gfloat *)ap.kc[h], *vc = (gfloat *)ap.kc[nh + h];
         if (tid < 32) {
             const float x1 = ax1, x2 = ax2;
             if (lastk) {
@@ -481,7 +486,7 @@ __global__ __launch_bounds__(256) void vm_head_attn_kernel(VmHeadAttn a, int nh,
         }
     } else {
         for (int r = w; r < a.hd; r += 4) {
-            const float *vr = V + (size_t)r * a.cols;
+            const gfloat *vr = V + (size_t)r * a.cols;
             float t = 0.0f;
             for (int c = lane; c < a.cols; c += 64) t += pr[c] * vr[c];
             store(r, t);
