@@ -298,9 +298,11 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
     const int tile = blockIdx.x * NWV + wave;
     const int k0 = blockIdx.y * KW;
 
-    // this wave's weight rows, every chunk of the slice (rows clamped)
+    // this wave's weight rows, every chunk of the slice (rows clamped),
+    // issued after the activation loads below: those return first, so the
+    // activation is split and staged while the weights are in flight
     u32x4 wv[NC][2];
-    {
+    auto load_w = [&]() {
         int j0 = tile * 16 + lrow, j1 = j0 + 8;
         j0 = j0 < p.N ? j0 : p.N - 1;
         j1 = j1 < p.N ? j1 : p.N - 1;
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
             wv[c][0] = ldg16(w0 + c * CH_BYTES);
             wv[c][1] = ldg16(w1 + c * CH_BYTES);
         }
-    }
+    };
     // the activation slice [TA][16 rows][KW] -> LDS in 16-byte pieces; rows
     // past the live ones repeat row 0 (their outputs are never read). From
     // f32 rows (p.X) each thread splits 8 values into the T terms.
@@ -329,6 +331,9 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
             xv[i][0] = *(const float4 *)xr;
             xv[i][1] = *(const float4 *)(xr + 4);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < UPER; ++i) {
             const int e = tid + i * NTH;
@@ -361,6 +366,9 @@ __global__ __launch_bounds__(NWV * 64) void gemv_wide_kernel(GemvParams p) {
             const int rs = r < arows ? r : 0;
             ap[i] = ldg16_cached(p.A + (BT ? 0 : tt * p.tstride) + (size_t)rs * p.lda + k0 + c8 * 8);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             int e = tid + i * NTH;
