@@ -658,33 +658,77 @@ __global__ __launch_bounds__(64 * RW_ROWS) void rows_q8_wave_kernel(
     // piece i: values k0 .. k0 + 7 in v[i][0..1], k0 + 32 .. in v[i][2..3]
     auto kof = [&](int pc, int j) { return (pc >> 2) * 64 + 8 * (pc & 3) + 32 * (j >> 1) + 4 * (j & 1); };
     float4 v[P][4];
+    constexpr bool RA = P <= 6;  // registers for both rows
+    if (RA && ar && !rbs.part) {
+        // the residual add: every load of the row first, then the sums and
+        // their stores (a store to x between the loads would make each wait
+        // for it: one piece in flight per wave)
+        float4 bv[RA ? P : 1][4];
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
-        const int pc = lane + 64 * i;
+        for (int i = 0; i < P; ++i) {
+            const int pc = lane + 64 * i;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (pc >= npc) continue;
-            const int kk = kof(pc, j);
-            if (ar) {
-                const float4 a = *(const float4 *)(ar + kk);
-                float4 b = *(const float4 *)(br + kk);
-                if (rbs.part) {  // slices in order, then the column scale
+            for (int j = 0; j < 4; ++j) {
+                v[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                bv[RA ? i : 0][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (pc >= npc) continue;
+                const int kk = kof(pc, j);
+                v[i][j] = *(const float4 *)(ar + kk);
+                bv[RA ? i : 0][j] = *(const float4 *)(br + kk);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int pc = lane + 64 * i;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (pc >= npc) continue;
+                const float4 a = v[i][j], b = bv[RA ? i : 0][j];
+                v[i][j] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                *(float4 *)(xr + kof(pc, j)) = v[i][j];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int pc = lane + 64 * i;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[i][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (pc >= npc) continue;
+                const int kk = kof(pc, j);
+                if (ar) {
+                    const float4 a = *(const float4 *)(ar + kk);
+                    float4 b = *(const float4 *)(br + kk);
+                    // slices in order, then the column scale
                     for (int sl = 1; sl < rbs.ks; ++sl) {
                         const float4 t = *(const float4 *)(br + (size_t)sl * rbs.pst + kk);
                         b = make_float4(b.x + t.x, b.y + t.y, b.z + t.z, b.w + t.w);
                     }
                     const float4 sc = *(const float4 *)(rbs.scale + kk);
                     b = make_float4(b.x * sc.x, b.y * sc.y, b.z * sc.z, b.w * sc.w);
+                    v[i][j] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                    *(float4 *)(xr + kk) = v[i][j];
+                } else {
+                    v[i][j] = *(const float4 *)(xr + kk);
                 }
-                v[i][j] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-                *(float4 *)(xr + kk) = v[i][j];
-            } else {
-                v[i][j] = *(const float4 *)(xr + kk);
             }
         }
     }
     if (g) {
+        // the gains issued before the sum is reduced (up to 4 pieces per
+        // lane: registers), so they are in by the time they are needed
+        constexpr bool HG = P <= 4;
+        float4 gv[HG ? P : 1][4];
+        if constexpr (HG) {
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int pc = lane + 64 * i;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    gv[i][j] = pc < npc ? *(const float4 *)(g + kof(pc, j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < P; ++i)
@@ -700,7 +744,9 @@ __global__ __launch_bounds__(64 * RW_ROWS) void rows_q8_wave_kernel(
             if (pc >= npc) continue;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float4 gg = *(const float4 *)(g + kof(pc, j));
+                float4 gg;
+                if constexpr (HG) gg = gv[i][j];
+                else gg = *(const float4 *)(g + kof(pc, j));
                 v[i][j] = make_float4(v[i][j].x * inv * gg.x, v[i][j].y * inv * gg.y,
                                       v[i][j].z * inv * gg.z, v[i][j].w * inv * gg.w);
             }
