@@ -69,8 +69,17 @@ __global__ __launch_bounds__(NW * 64, WPE) void fq_gemv_kernel(FqParams p) {
     const int tile0 = blockIdx.x * TW;
     const int nr = n < p.M ? n : 0;
 
-    // 1. every global read up front: weights, B fragments, segment factors,
-    // and (threads 0..15) the row's segment sums of squares
+    // 1. every global read up front: B fragments, weights, segment factors,
+    // and (threads 0..15) the row's segment sums of squares. The fragments
+    // go first: loads return in order, so block i's products wait only for
+    // the weights up to block i, not for the whole run
+    i32x4 b[KB][Q8_T];
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+        for (int q = 0; q < Q8_T; ++q)
+            b[i][q] = *(const i32x4 *)(p.A8 + ((size_t)q * nkb + kb0 + i) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 wr[TW][KB];
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
@@ -79,13 +88,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void fq_gemv_kernel(FqParams p) {
         for (int i = 0; i < KB; ++i)
             wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)i * 1024));
     }
-    __builtin_amdgcn_sched_barrier(0);
-    i32x4 b[KB][Q8_T];
-#pragma unroll
-    for (int i = 0; i < KB; ++i)
-#pragma unroll
-        for (int q = 0; q < Q8_T; ++q)
-            b[i][q] = *(const i32x4 *)(p.A8 + ((size_t)q * nkb + kb0 + i) * 1024 + lane * 16);
     // the wave's run is one segment (KB == seg_kb, checked at launch)
     const float segf = p.a8s[wave * p.M + nr];
     const int nseg = nkb / KB;
