@@ -182,13 +182,15 @@ __global__ __launch_bounds__(WPT * 64) void fk_gemv_kernel(FkParams p) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // block-major, the order the k-run below consumes them in (loads return
+    // in order: block i's products then wait only for blocks 0 .. i)
     u32x4 wr[TPW][KB];
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        const uint8_t *wt = p.W + ((size_t)(blockIdx.x * TPW + t) * nkb) * 1024 + lane * 16;
+    for (int i = 0; i < KB; ++i) {
+        const int kb = kb0 + i < nkb ? kb0 + i : nkb - 1;
 #pragma unroll
-        for (int i = 0; i < KB; ++i) {
-            const int kb = kb0 + i < nkb ? kb0 + i : nkb - 1;
+        for (int t = 0; t < TPW; ++t) {
+            const uint8_t *wt = p.W + ((size_t)(blockIdx.x * TPW + t) * nkb) * 1024 + lane * 16;
             wr[t][i] = __builtin_nontemporal_load((const u32x4 *)(wt + (size_t)kb * 1024));
         }
     }
