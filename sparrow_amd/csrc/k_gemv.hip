@@ -627,7 +627,7 @@ __global__ __launch_bounds__(512) void gemv_wloop_kernel(GemvParams p) {
 template <bool WI8, int T, bool BT>
 static int launch_wloop_t(const GemvParams &p, hipStream_t st) {
     const dim3 grid((p.N + 127) / 128, p.ks);
-    gemv_wloop_kernel<WI8, T, BT, WI8 ? 1 : 2><<<grid, 512, 0, st>>>(p);
+    gemv_wloop_kernel<WI8, T, BT, 1><<<grid, 512, 0, st>>>(p);
     VMLM_HIP_CHECK(hipGetLastError());
     return VMLM_OK;
 }
